@@ -1,0 +1,87 @@
+"""Compile the native library libelastic_vmm.so for gfx950 with hipcc.
+
+The library holds the HIP VMM backing (ev_* ABI) and the hot-path kernels
+(ekv_* ABI). It is built in-tree so that it travels with the source tree:
+    python elastic-kv-vmm_amd/build_native.py
+This mirrors the reference's "compile the packaged native source" step
+(elastic_kv/build_vmm.py:20-41), with hipcc in place of g++ + libcuda.
+"""
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PACKAGE_ROOT = Path(__file__).resolve().parent
+SOURCE_DIR = PACKAGE_ROOT / "csrc"
+BUILD_DIR = PACKAGE_ROOT / "_build"
+LIBRARY = PACKAGE_ROOT / "lib" / "libelastic_vmm.so"
+SOURCES = ("vmm_backing.hip", "lookup.hip", "gather.hip")
+OFFLOAD_ARCH = "gfx950"
+
+COMMON_FLAGS = [
+    f"--offload-arch={OFFLOAD_ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-result",
+    # Code-object v5 is loadable by the HIP runtime bundled with PyTorch as
+    # well as by the system ROCm runtime.
+    "-mcode-object-version=5",
+    # Keep the compiler from forming packed-FP32 VALU ops.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def hipcc():
+    found = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(found).exists():
+        raise RuntimeError("hipcc not found; a ROCm toolchain is required to build libelastic_vmm.so")
+    return found
+
+
+def _compile(compiler, source, obj, verbose):
+    command = [compiler, *COMMON_FLAGS, "-c", str(source), "-o", str(obj)]
+    if verbose:
+        print(" ".join(command), flush=True)
+    result = subprocess.run(command, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {source.name}:\n{result.stdout}\n{result.stderr}")
+    return result.stderr
+
+
+def build(verbose=False):
+    """Compile every source and link lib/libelastic_vmm.so; returns its path."""
+    compiler = hipcc()
+    BUILD_DIR.mkdir(exist_ok=True)
+    LIBRARY.parent.mkdir(exist_ok=True)
+    jobs = min(len(SOURCES), max(1, (os.cpu_count() or 1)))
+    objects = []
+    with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
+        futures = []
+        for name in SOURCES:
+            source = SOURCE_DIR / name
+            obj = BUILD_DIR / (Path(name).stem + ".o")
+            objects.append(obj)
+            futures.append(pool.submit(_compile, compiler, source, obj, verbose))
+        for future in futures:
+            warnings = future.result()
+            if verbose and warnings.strip():
+                print(warnings, file=sys.stderr)
+    temporary = LIBRARY.with_suffix(".so.tmp")
+    command = [compiler, f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC",
+               *map(str, objects), "-o", str(temporary)]
+    if verbose:
+        print(" ".join(command), flush=True)
+    result = subprocess.run(command, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"link failed:\n{result.stdout}\n{result.stderr}")
+    os.replace(temporary, LIBRARY)
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

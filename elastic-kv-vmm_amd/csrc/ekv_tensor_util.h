@@ -1,0 +1,98 @@
+// Host-side validation of ekv_tensor descriptors and small device helpers for
+// reading int32/int64 index tensors whose dtype is known only at run time.
+#pragma once
+
+#include "../../include/ekv_kernels.h"
+#include "ekv_common.h"
+
+#include <string>
+
+namespace ekv {
+
+inline int64_t itemsize(int32_t dtype) {
+    switch (dtype) {
+        case EKV_INT32: return 4;
+        case EKV_INT64: return 8;
+        case EKV_UINT8: return 1;
+        case EKV_INT8: return 1;
+        case EKV_INT16: return 2;
+        case EKV_BFLOAT16: return 2;
+        case EKV_FLOAT16: return 2;
+        case EKV_FLOAT32: return 4;
+        default: throw std::invalid_argument("unknown dtype code " + std::to_string(dtype));
+    }
+}
+
+inline const ekv_tensor& need(const ekv_tensor* t, const char* name) {
+    if (t == nullptr) {
+        throw std::invalid_argument(std::string(name) + " is required");
+    }
+    if (t->ndim < 0 || t->ndim > 4) {
+        throw std::invalid_argument(std::string(name) + " must have 0..4 dimensions");
+    }
+    for (int i = 0; i < t->ndim; ++i) {
+        if (t->shape[i] < 0) {
+            throw std::invalid_argument(std::string(name) + " has a negative extent");
+        }
+    }
+    (void)itemsize(t->dtype);
+    return *t;
+}
+
+inline int64_t numel(const ekv_tensor& t) {
+    int64_t n = 1;
+    for (int i = 0; i < t.ndim; ++i) {
+        n *= t.shape[i];
+    }
+    return n;
+}
+
+inline void need_ndim(const ekv_tensor& t, int ndim, const char* name) {
+    if (t.ndim != ndim) {
+        throw std::invalid_argument(std::string(name) + " must have " + std::to_string(ndim) +
+                                    " dimensions, got " + std::to_string(t.ndim));
+    }
+}
+
+inline void need_index(const ekv_tensor& t, const char* name) {
+    if (t.dtype != EKV_INT32 && t.dtype != EKV_INT64) {
+        throw std::invalid_argument(std::string(name) + " must be int32 or int64");
+    }
+}
+
+inline void need_dim(const ekv_tensor& t, int dim, int64_t extent, const char* name) {
+    if (t.shape[dim] != extent) {
+        throw std::invalid_argument(std::string(name) + " dimension " + std::to_string(dim) + " is " +
+                                    std::to_string(t.shape[dim]) + ", expected " + std::to_string(extent));
+    }
+}
+
+inline void need_data(const ekv_tensor& t, const char* name) {
+    if (numel(t) > 0 && t.data == nullptr) {
+        throw std::invalid_argument(std::string(name) + " has a null data pointer");
+    }
+}
+
+// An int32/int64 index array read through one stride, dtype chosen at run time.
+struct IndexRef {
+    const void* data = nullptr;
+    int64_t stride = 0;
+    int32_t is64 = 0;
+
+#if defined(__HIPCC__)
+    __device__ __forceinline__ int64_t operator[](int64_t i) const {
+        return is64 ? static_cast<const int64_t*>(data)[i * stride]
+                    : static_cast<int64_t>(static_cast<const int32_t*>(data)[i * stride]);
+    }
+#endif
+};
+
+inline IndexRef index_ref(const ekv_tensor& t, int dim) {
+    IndexRef r;
+    r.data = t.data;
+    r.stride = t.ndim > dim ? t.stride[dim] : 0;
+    r.is64 = t.dtype == EKV_INT64;
+    return r;
+}
+
+}  // namespace ekv

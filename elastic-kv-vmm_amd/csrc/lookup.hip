@@ -1,0 +1,351 @@
+// Resident lookup with wave64 miss compaction (gfx950).
+//
+// Semantics: adaptive_sparse/resident_lookup.py:6-26 (Triton _resolve) and the
+// torch resolver adaptive_sparse/request_residency.py:819-825, extended with a
+// leading layer dimension, an optional second indirection level and an
+// ordered miss list (lanes whose slot is 0 = not resident).
+//
+// Launch shape: one 256-thread workgroup (4 waves) per (selected row, layer).
+// A row of `width` lanes is walked in chunks of 2048 lanes; wave w owns lanes
+// [512w, 512w + 512) of a chunk and processes them as 8 iterations of 64
+// consecutive lanes, so a wave's lane order is the row's lane order. All 8
+// Top-K loads of a lane are issued before its 8 table loads, which are issued
+// before any dependent mapping load, to keep many independent loads in flight.
+// Miss compaction: each iteration's misses form a 64-bit ballot; a lane's rank
+// in the miss list is (misses of lower waves in this chunk) + (misses of
+// earlier iterations of its wave) + mbcnt(ballot). One LDS exchange of the 4
+// wave totals per chunk; no atomics, so the list order is deterministic.
+#include "../../include/ekv_kernels.h"
+#include "ekv_common.h"
+#include "ekv_fastdiv.h"
+#include "ekv_tensor_util.h"
+
+namespace ekv {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kIters = 8;                      // 64-lane iterations per wave per chunk
+constexpr int kWaveSpan = 64 * kIters;         // 512 lanes per wave per chunk
+constexpr int kChunkLanes = kThreads * kIters; // 2048 lanes per chunk
+
+struct NoMap {};
+
+struct LookupArgs {
+    const void* topk;
+    int64_t topk_sl, topk_sb, topk_sk;
+    const void* table;
+    int64_t table_sl, table_sr, table_sc, table_rows, table_cols;
+    const void* mapping;
+    int64_t map_sl, map_s, map_len;
+    IndexRef rows, lengths, selected;
+    int32_t* out;
+    int64_t out_sl, out_sb, out_so;
+    int32_t* misses;
+    int64_t miss_sl, miss_sb, miss_so;
+    int32_t* counts;
+    int64_t count_sl, count_sb;
+    int64_t batch;
+    uint32_t width;
+    uint32_t block_size;
+    FastDiv block_div;
+};
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
+
+template <typename TopkT, typename TableT, typename MapT, bool kCompact>
+__global__ __launch_bounds__(kThreads) void resolve_kernel(const LookupArgs a) {
+    __shared__ int32_t wave_totals[kThreads / 64];
+    const int64_t row = a.selected[blockIdx.x];
+    if (row < 0 || row >= a.batch) {
+        return;  // uniform over the workgroup
+    }
+    const int64_t layer = blockIdx.y;
+    const int64_t req = a.rows[row];
+    const int64_t length = a.lengths[row];
+    const bool req_ok = req >= 0 && req < a.table_rows;
+    const TopkT* topk = static_cast<const TopkT*>(a.topk) + layer * a.topk_sl + row * a.topk_sb;
+    const TableT* table = static_cast<const TableT*>(a.table) + layer * a.table_sl + (req_ok ? req : 0) * a.table_sr;
+    int32_t* out = a.out + layer * a.out_sl + row * a.out_sb;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const bool unit_blocks = a.block_size == 1;
+    int32_t running = 0;
+
+    for (uint32_t chunk = 0; chunk < a.width; chunk += kChunkLanes) {
+        const uint32_t first = chunk + wave * kWaveSpan + lane;
+        int64_t block[kIters];
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+            const uint32_t o = first + i * 64;
+            block[i] = -1;
+            if (o < a.width) {
+                const uint32_t b = unit_blocks ? o : a.block_div.div(o);
+                block[i] = static_cast<int64_t>(topk[b * a.topk_sk]);
+            }
+        }
+        int64_t value[kIters];
+        bool hit_path[kIters];  // valid and every index in bounds
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+            const uint32_t o = first + i * 64;
+            const uint32_t offset = unit_blocks ? 0u : o - a.block_div.div(o) * a.block_size;
+            const int64_t pos = block[i] * a.block_size + offset;
+            const bool valid = o < a.width && block[i] >= 0 && pos < length;
+            hit_path[i] = valid && req_ok && pos < a.table_cols;
+            value[i] = hit_path[i] ? static_cast<int64_t>(table[pos * a.table_sc]) : -1;
+        }
+        if constexpr (!std::is_same<MapT, NoMap>::value) {
+            const MapT* mapping = static_cast<const MapT*>(a.mapping) + layer * a.map_sl;
+#pragma unroll
+            for (int i = 0; i < kIters; ++i) {
+                if (hit_path[i]) {
+                    const int64_t logical = value[i];
+                    if (logical >= 0 && logical < a.map_len) {
+                        value[i] = static_cast<int64_t>(mapping[logical * a.map_s]);
+                    } else {
+                        value[i] = -1;
+                        hit_path[i] = false;
+                    }
+                }
+            }
+        }
+        uint64_t miss_mask[kIters];
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+            const uint32_t o = first + i * 64;
+            const int32_t slot = static_cast<int32_t>(value[i]);
+            if (o < a.width) {
+                out[static_cast<int64_t>(o) * a.out_so] = slot;
+            }
+            if constexpr (kCompact) {
+                miss_mask[i] = __ballot(hit_path[i] && slot == 0);
+            }
+        }
+        if constexpr (kCompact) {
+            int32_t wave_total = 0;
+#pragma unroll
+            for (int i = 0; i < kIters; ++i) {
+                wave_total += __popcll(miss_mask[i]);
+            }
+            if (lane == 0) {
+                wave_totals[wave] = wave_total;
+            }
+            __syncthreads();
+            int32_t rank = running;
+            int32_t chunk_total = 0;
+#pragma unroll
+            for (int w = 0; w < kThreads / 64; ++w) {
+                rank += w < wave ? wave_totals[w] : 0;
+                chunk_total += wave_totals[w];
+            }
+            int32_t* misses = a.misses + layer * a.miss_sl + row * a.miss_sb;
+#pragma unroll
+            for (int i = 0; i < kIters; ++i) {
+                if ((miss_mask[i] >> lane) & 1u) {
+                    const int64_t at = rank + static_cast<int32_t>(lanes_below(miss_mask[i]));
+                    misses[at * a.miss_so] = static_cast<int32_t>(first + i * 64);
+                }
+                rank += __popcll(miss_mask[i]);
+            }
+            running += chunk_total;
+            __syncthreads();  // wave_totals is rewritten by the next chunk
+        }
+    }
+    if constexpr (kCompact) {
+        if (threadIdx.x == 0) {
+            a.counts[layer * a.count_sl + row * a.count_sb] = running;
+        }
+    }
+}
+
+template <typename TopkT, typename TableT, typename MapT>
+void launch_typed(const LookupArgs& a, bool compact, dim3 grid, hipStream_t stream) {
+    if (compact) {
+        resolve_kernel<TopkT, TableT, MapT, true><<<grid, dim3(kThreads), 0, stream>>>(a);
+    } else {
+        resolve_kernel<TopkT, TableT, MapT, false><<<grid, dim3(kThreads), 0, stream>>>(a);
+    }
+}
+
+template <typename TopkT, typename TableT>
+void launch_map(const LookupArgs& a, int32_t map_dtype, bool compact, dim3 grid, hipStream_t stream) {
+    if (a.mapping == nullptr) {
+        launch_typed<TopkT, TableT, NoMap>(a, compact, grid, stream);
+    } else if (map_dtype == EKV_INT64) {
+        launch_typed<TopkT, TableT, int64_t>(a, compact, grid, stream);
+    } else {
+        launch_typed<TopkT, TableT, int32_t>(a, compact, grid, stream);
+    }
+}
+
+template <typename TopkT>
+void launch_table(const LookupArgs& a, int32_t table_dtype, int32_t map_dtype, bool compact, dim3 grid,
+                  hipStream_t stream) {
+    if (table_dtype == EKV_INT64) {
+        launch_map<TopkT, int64_t>(a, map_dtype, compact, grid, stream);
+    } else {
+        launch_map<TopkT, int32_t>(a, map_dtype, compact, grid, stream);
+    }
+}
+
+int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const ekv_tensor* mapping_p,
+                     const ekv_tensor* rows_p, const ekv_tensor* lengths_p, const ekv_tensor* selected_p,
+                     const ekv_tensor* output_p, const ekv_tensor* misses_p, const ekv_tensor* counts_p,
+                     int64_t block_size, void* stream) {
+    const ekv_tensor& topk = need(topk_p, "topk");
+    const ekv_tensor& table = need(table_p, "table");
+    const ekv_tensor& rows = need(rows_p, "rows");
+    const ekv_tensor& lengths = need(lengths_p, "lengths");
+    const ekv_tensor& selected = need(selected_p, "selected");
+    const ekv_tensor& output = need(output_p, "output");
+    need_ndim(topk, 3, "topk");
+    need_index(topk, "topk");
+    const int64_t layers = topk.shape[0];
+    const int64_t batch = topk.shape[1];
+    const int64_t k = topk.shape[2];
+    if (block_size < 1) {
+        throw std::invalid_argument("block_size must be positive");
+    }
+    const int64_t width = k * block_size;
+    need_ndim(output, 3, "output");
+    if (output.dtype != EKV_INT32) {
+        throw std::invalid_argument("output must be int32");
+    }
+    need_dim(output, 0, layers, "output");
+    need_dim(output, 1, batch, "output");
+    need_dim(output, 2, width, "output");
+    if (table.ndim != 2 && table.ndim != 3) {
+        throw std::invalid_argument("table must be [R, T] or [L, R, T]");
+    }
+    need_index(table, "table");
+    const bool layered_table = table.ndim == 3;
+    if (layered_table) {
+        need_dim(table, 0, layers, "table");
+    }
+    for (const auto* one : {&rows, &lengths, &selected}) {
+        need_ndim(*one, 1, "rows/lengths/selected");
+        need_index(*one, "rows/lengths/selected");
+    }
+    need_dim(rows, 0, batch, "rows");
+    need_dim(lengths, 0, batch, "lengths");
+    const ekv_tensor* mapping = nullptr;
+    if (mapping_p != nullptr) {
+        mapping = &need(mapping_p, "mapping");
+        need_index(*mapping, "mapping");
+        if (mapping->ndim == 2) {
+            need_dim(*mapping, 0, layers, "mapping");
+        } else if (mapping->ndim != 1) {
+            throw std::invalid_argument("mapping must be [N] or [L, N]");
+        }
+    }
+    if ((misses_p == nullptr) != (counts_p == nullptr)) {
+        throw std::invalid_argument("misses and miss_count must be given together");
+    }
+    const bool compact = misses_p != nullptr;
+    if (compact) {
+        const ekv_tensor& misses = need(misses_p, "misses");
+        const ekv_tensor& counts = need(counts_p, "miss_count");
+        need_ndim(misses, 3, "misses");
+        need_ndim(counts, 2, "miss_count");
+        if (misses.dtype != EKV_INT32 || counts.dtype != EKV_INT32) {
+            throw std::invalid_argument("misses and miss_count must be int32");
+        }
+        need_dim(misses, 0, layers, "misses");
+        need_dim(misses, 1, batch, "misses");
+        need_dim(misses, 2, width, "misses");
+        need_dim(counts, 0, layers, "miss_count");
+        need_dim(counts, 1, batch, "miss_count");
+    }
+    const int64_t count = selected.shape[0];
+    if (count == 0 || width == 0 || layers == 0) {
+        return 0;  // the reference returns without launching
+    }
+    if (width >= (int64_t{1} << 31) - kChunkLanes) {
+        throw std::invalid_argument("K * block_size must be below 2^31");
+    }
+    if (layers > 65535) {
+        throw std::invalid_argument("at most 65535 layers per launch");
+    }
+    if (count > 0x7fffffff) {
+        throw std::invalid_argument("too many selected rows");
+    }
+    for (const auto* one : {&topk, &table, &rows, &lengths, &selected, &output}) {
+        need_data(*one, "tensor");
+    }
+
+    LookupArgs a{};
+    a.topk = topk.data;
+    a.topk_sl = topk.stride[0];
+    a.topk_sb = topk.stride[1];
+    a.topk_sk = topk.stride[2];
+    a.table = table.data;
+    const int d = layered_table ? 1 : 0;
+    a.table_sl = layered_table ? table.stride[0] : 0;
+    a.table_sr = table.stride[d];
+    a.table_sc = table.stride[d + 1];
+    a.table_rows = table.shape[d];
+    a.table_cols = table.shape[d + 1];
+    if (mapping != nullptr) {
+        need_data(*mapping, "mapping");
+        a.mapping = mapping->data;
+        a.map_sl = mapping->ndim == 2 ? mapping->stride[0] : 0;
+        a.map_s = mapping->stride[mapping->ndim - 1];
+        a.map_len = mapping->shape[mapping->ndim - 1];
+    }
+    a.rows = index_ref(rows, 0);
+    a.lengths = index_ref(lengths, 0);
+    a.selected = index_ref(selected, 0);
+    a.out = static_cast<int32_t*>(output.data);
+    a.out_sl = output.stride[0];
+    a.out_sb = output.stride[1];
+    a.out_so = output.stride[2];
+    if (compact) {
+        a.misses = static_cast<int32_t*>(misses_p->data);
+        a.miss_sl = misses_p->stride[0];
+        a.miss_sb = misses_p->stride[1];
+        a.miss_so = misses_p->stride[2];
+        a.counts = static_cast<int32_t*>(counts_p->data);
+        a.count_sl = counts_p->stride[0];
+        a.count_sb = counts_p->stride[1];
+        if (a.misses == nullptr || a.counts == nullptr) {
+            throw std::invalid_argument("misses / miss_count have null data pointers");
+        }
+    }
+    a.batch = batch;
+    a.width = static_cast<uint32_t>(width);
+    a.block_size = static_cast<uint32_t>(block_size);
+    if (block_size >= (int64_t{1} << 31)) {
+        throw std::invalid_argument("block_size must be below 2^31");
+    }
+    a.block_div = FastDiv(static_cast<uint32_t>(block_size));
+
+    const dim3 grid(static_cast<uint32_t>(count), static_cast<uint32_t>(layers));
+    const auto s = static_cast<hipStream_t>(stream);
+    const int32_t map_dtype = mapping ? mapping->dtype : 0;
+    if (topk.dtype == EKV_INT64) {
+        launch_table<int64_t>(a, table.dtype, map_dtype, compact, grid, s);
+    } else {
+        launch_table<int32_t>(a, table.dtype, map_dtype, compact, grid, s);
+    }
+    check_hip(hipGetLastError(), "launch resident lookup");
+    return 0;
+}
+
+}  // namespace
+}  // namespace ekv
+
+extern "C" int ekv_resolve_resident(const ekv_tensor* topk, const ekv_tensor* table, const ekv_tensor* mapping,
+                                    const ekv_tensor* rows, const ekv_tensor* lengths,
+                                    const ekv_tensor* selected, const ekv_tensor* output,
+                                    const ekv_tensor* misses, const ekv_tensor* miss_count,
+                                    int64_t block_size, void* stream) {
+    return ekv::guarded(-1, [&] {
+        return ekv::resolve_resident(topk, table, mapping, rows, lengths, selected, output, misses, miss_count,
+                                     block_size, stream);
+    });
+}
+
+extern "C" int ekv_abi_version(void) { return EKV_ABI_VERSION; }

@@ -1,0 +1,130 @@
+"""ctypes binding of the ekv_* kernel entry points of libelastic_vmm.so.
+
+torch tensors are described to the C ABI as (pointer, dtype code, shape,
+element strides); nothing but plain values crosses the boundary. There is no
+fallback: if the library cannot be loaded, every kernel call raises.
+"""
+
+import ctypes as ct
+
+import torch
+
+from .backing import _load_library, library_path
+
+EKV_ABI_VERSION = 1
+
+_DTYPE_CODES = {
+    torch.int32: 1,
+    torch.int64: 2,
+    torch.uint8: 3,
+    torch.int8: 4,
+    torch.int16: 5,
+    torch.bfloat16: 6,
+    torch.float16: 7,
+    torch.float32: 8,
+}
+
+
+class EkvTensor(ct.Structure):
+    _fields_ = [
+        ("data", ct.c_void_p),
+        ("dtype", ct.c_int32),
+        ("ndim", ct.c_int32),
+        ("shape", ct.c_int64 * 4),
+        ("stride", ct.c_int64 * 4),
+    ]
+
+
+class EkvPlanes(ct.Structure):
+    _fields_ = [
+        ("base", ct.c_void_p),
+        ("layers", ct.c_int64),
+        ("kv", ct.c_int64),
+        ("layer_stride", ct.c_int64),
+        ("kv_stride", ct.c_int64),
+        ("row_stride", ct.c_int64),
+        ("row_bytes", ct.c_int64),
+        ("rows", ct.c_int64),
+    ]
+
+
+class EkvKvRows(ct.Structure):
+    _fields_ = [
+        ("data", ct.c_void_p),
+        ("layer_stride", ct.c_int64),
+        ("batch_stride", ct.c_int64),
+        ("kv_stride", ct.c_int64),
+        ("lane_stride", ct.c_int64),
+    ]
+
+
+_P_TENSOR = ct.POINTER(EkvTensor)
+_SIGNATURES = {
+    "ekv_abi_version": ([], ct.c_int),
+    "ekv_resolve_resident": ([_P_TENSOR] * 9 + [ct.c_int64, ct.c_void_p], ct.c_int),
+    "ekv_gather_rows": ([_P_TENSOR] * 7 + [ct.c_int64, ct.c_int64, ct.c_int, ct.c_void_p], ct.c_int),
+    "ekv_gather_kv": ([ct.POINTER(EkvPlanes), _P_TENSOR, ct.POINTER(EkvKvRows), ct.c_int64, ct.c_void_p],
+                      ct.c_int),
+    "ekv_scatter_kv": ([ct.POINTER(EkvPlanes), _P_TENSOR, ct.POINTER(EkvKvRows), ct.c_int64, ct.c_void_p],
+                       ct.c_int),
+}
+KERNEL_SYMBOLS = tuple(_SIGNATURES)
+
+
+def kernel_library(library=None):
+    """The native library with ekv_* signatures declared (cached per path)."""
+    lib = _load_library(library_path(library))
+    if not getattr(lib, "_ekv_typed", False):
+        for name, (argtypes, restype) in _SIGNATURES.items():
+            try:
+                fn = getattr(lib, name)
+            except AttributeError as exc:
+                raise RuntimeError(
+                    f"libelastic_vmm.so lacks {name}; rebuild it with "
+                    "`python elastic-kv-vmm_amd/build_native.py`"
+                ) from exc
+            fn.argtypes = argtypes
+            fn.restype = restype
+        version = lib.ekv_abi_version()
+        if version != EKV_ABI_VERSION:
+            raise RuntimeError(f"libelastic_vmm.so kernel ABI {version} != {EKV_ABI_VERSION}; rebuild it")
+        lib._ekv_typed = True
+    return lib
+
+
+def describe(tensor, name="tensor"):
+    """EkvTensor for a torch tensor (any strides, at most 4 dimensions)."""
+    if tensor.dim() > 4:
+        raise ValueError(f"{name} has more than 4 dimensions")
+    code = _DTYPE_CODES.get(tensor.dtype)
+    if code is None:
+        raise TypeError(f"{name} has unsupported dtype {tensor.dtype}")
+    view = EkvTensor()
+    view.data = tensor.data_ptr() if tensor.numel() else None
+    view.dtype = code
+    view.ndim = tensor.dim()
+    for i, (extent, stride) in enumerate(zip(tensor.shape, tensor.stride())):
+        view.shape[i] = extent
+        view.stride[i] = stride
+    return view
+
+
+def device_of(*tensors):
+    """The single GPU device shared by every given tensor."""
+    devices = {t.device for t in tensors if t is not None}
+    if len(devices) != 1:
+        raise ValueError(f"tensors must share one device, got {sorted(map(str, devices))}")
+    device = devices.pop()
+    if device.type != "cuda":
+        raise ValueError("hot-path kernels need GPU tensors (no CPU fallback exists)")
+    return device
+
+
+def stream_handle(device):
+    return ct.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def check(lib, status, what):
+    if status:
+        message = lib.ev_error().decode("utf-8", errors="replace")
+        raise RuntimeError(f"{what}: {message}")

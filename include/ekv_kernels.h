@@ -1,0 +1,148 @@
+/*
+ * ekv_kernels.h - hot-path HIP kernels of the sparse-KV residency path (gfx950).
+ *
+ * Every entry point validates shapes on the host, launches asynchronously on
+ * the HIP stream passed by the caller (NULL = the legacy default stream), and
+ * returns 0, or -1 with a message for ev_error() (declared in elastic_vmm.h).
+ * No entry point allocates device memory or synchronizes the stream.
+ * Tensors are described by plain pointers, dtype codes, shapes and element
+ * strides; nothing here depends on PyTorch.
+ */
+#ifndef EKV_KERNELS_H
+#define EKV_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types understood by ekv_tensor. Index tensors must be INT32/INT64. */
+enum ekv_dtype {
+    EKV_INT32 = 1,
+    EKV_INT64 = 2,
+    EKV_UINT8 = 3,
+    EKV_INT8 = 4,
+    EKV_INT16 = 5,
+    EKV_BFLOAT16 = 6,
+    EKV_FLOAT16 = 7,
+    EKV_FLOAT32 = 8,
+};
+
+/* A strided device tensor of up to 4 dimensions; strides are in elements. */
+typedef struct ekv_tensor {
+    void* data;
+    int32_t dtype;      /* enum ekv_dtype */
+    int32_t ndim;
+    int64_t shape[4];
+    int64_t stride[4];
+} ekv_tensor;
+
+/* A KV pool seen as planes of fixed-size rows: plane (layer l, kv) starts at
+ * base + l*layer_stride + kv*kv_stride and slot s of it at + s*row_stride. */
+typedef struct ekv_planes {
+    void* base;
+    int64_t layers;       /* layers in the pool */
+    int64_t kv;           /* planes per layer: 1, or 2 for separate K and V */
+    int64_t layer_stride; /* bytes */
+    int64_t kv_stride;    /* bytes */
+    int64_t row_stride;   /* bytes between slot s and slot s+1 */
+    int64_t row_bytes;    /* payload bytes per slot row */
+    int64_t rows;         /* slots per plane: a slot >= rows is out of range */
+} ekv_planes;
+
+/* Dense destination (or source) rows addressed by (layer, batch, kv, lane). */
+typedef struct ekv_kv_rows {
+    void* data;
+    int64_t layer_stride; /* bytes */
+    int64_t batch_stride; /* bytes */
+    int64_t kv_stride;    /* bytes */
+    int64_t lane_stride;  /* bytes */
+} ekv_kv_rows;
+
+/* ABI revision of this header; bumped on any incompatible change. */
+#define EKV_ABI_VERSION 1
+int ekv_abi_version(void);
+
+/*
+ * Resident lookup with optional miss compaction.
+ * Replaces: adaptive_sparse/resident_lookup.py:29-40 (resolve_resident) and
+ * its kernel :6-26; torch twin adaptive_sparse/request_residency.py:819-825.
+ *
+ * Shapes (L = topk.shape[0]; the reference always has L = 1):
+ *   topk      [L, B, K]           int32/int64 block ids, -1 = padding
+ *   table     [R, T] or [L, R, T] int32/int64
+ *   mapping   NULL, [N] or [L, N] int32/int64; NULL = single level (the table
+ *                                 value is the slot)
+ *   rows      [B], lengths [B], selected [S]   int32/int64
+ *   output    [L, B, K*block_size] int32, any strides
+ *   misses    NULL or [L, B, K*block_size] int32
+ *   miss_count NULL or [L, B] int32 (both NULL or both given)
+ * For each selected row r = selected[i], each layer l and lane o:
+ *   block = topk[l, r, o / bs], pos = block*bs + o % bs,
+ *   valid = block >= 0 && pos < lengths[r],
+ *   output[l, r, o] = valid ? int32(mapping[l?, table[l?, rows[r], pos]]) : -1.
+ * Unselected rows are left untouched. With compaction, misses[l, r, 0:c] gets
+ * the lanes o with valid && output == 0 (slot 0 = not resident) in ascending
+ * order and miss_count[l, r] = c; misses[l, r, c:] is left untouched.
+ * Where the reference would read out of bounds (rows[r] >= R, pos >= T, a
+ * mapping index outside [0, N), a selected row outside [0, B)) the lane
+ * returns -1 and is not a miss, or the row is skipped.
+ */
+int ekv_resolve_resident(const ekv_tensor* topk, const ekv_tensor* table,
+                         const ekv_tensor* mapping, const ekv_tensor* rows,
+                         const ekv_tensor* lengths, const ekv_tensor* selected,
+                         const ekv_tensor* output, const ekv_tensor* misses,
+                         const ekv_tensor* miss_count, int64_t block_size,
+                         void* stream);
+
+/*
+ * Row gather over a fixed-position virtual layout.
+ * Replaces: experimental/sparse_read.py:33-51 (gather_rows) and its kernel
+ * :11-30.
+ *   raw [E] payload (any dtype), positions [B, S], request_ids [B],
+ *   lengths [B], request_table [Q, W] (indirect only), slot_offsets [N]
+ *   (indirect only), output [B, S, width] of raw's dtype.
+ * valid = 0 <= pos < lengths[b]; the source element offset is
+ *   direct:   sink_elements + request_ids[b]*request_stride + pos*width
+ *   indirect: slot_offsets[request_table[request_ids[b], pos]]
+ * and output[b, s, :] = raw[offset : offset + width], or zeros when invalid
+ * (or, unlike the reference, when the row would fall outside raw).
+ */
+int ekv_gather_rows(const ekv_tensor* raw, const ekv_tensor* positions,
+                    const ekv_tensor* request_ids, const ekv_tensor* lengths,
+                    const ekv_tensor* request_table,
+                    const ekv_tensor* slot_offsets, const ekv_tensor* output,
+                    int64_t request_stride, int64_t sink_elements, int indirect,
+                    void* stream);
+
+/*
+ * Top-K sparse KV gather from a (chunked, VMM-backed) pool of planes.
+ * No reference kernel: the reference's gather is the indirect mode of
+ * experimental/sparse_read.py:11-30 over one plane; this is its multi-plane
+ * form for the per-layer slot lists produced by ekv_resolve_resident.
+ *   slots [L, B, K] int32/int64 (stride 0 on dim 0 shares one list over layers)
+ * For l < L, b < B, kv < planes->kv, k < K:
+ *   out(l, b, kv, k) = plane(l, kv)[slot] if zero_below <= slot < rows,
+ *                      else planes->row_bytes zero bytes.
+ * zero_below = 1 makes slot 0 (the sink, "not resident") and -1 zero rows.
+ */
+int ekv_gather_kv(const ekv_planes* planes, const ekv_tensor* slots,
+                  const ekv_kv_rows* out, int64_t zero_below, void* stream);
+
+/*
+ * Inverse of ekv_gather_kv: plane(l, kv)[slot] = src(l, b, kv, k) for every
+ * slot with zero_below <= slot < rows; other lanes write nothing. Two lanes
+ * naming the same slot race (the caller must pass distinct slots).
+ * Replaces the byte movement of the third-party host-copy kernels used by
+ * adaptive_sparse/migration.py:109-111,232-237 (unpack side).
+ */
+int ekv_scatter_kv(const ekv_planes* planes, const ekv_tensor* slots,
+                   const ekv_kv_rows* src, int64_t zero_below, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EKV_KERNELS_H */

@@ -1,0 +1,272 @@
+"""CPU oracle of the sparse-KV residency hot path.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+CPU-baseline leg of bench.py, as the checker of the HIP kernels. Product code
+never imports it.
+
+Two independent restatements of the reference semantics live here:
+  * numpy functions (vectorized, following the torch indexing sequence of
+    adaptive_sparse/request_residency.py:819-825 and the Triton gather of
+    experimental/sparse_read.py:11-30), and
+  * COracle, a ctypes binding of ekv_oracle.c (scalar C, following the
+    Triton lookup adaptive_sparse/resident_lookup.py:14-26 lane by lane),
+plus restatements of the reference's hit semantics
+(adaptive_sparse/hisparse_access_trace.py:59-71) and batch-token LRU replay
+(benchmarks/hisparse_locality_replay.py:90-99). tests/test_oracle.py pins all
+of them against the reference's known-answer vectors, closed forms and
+brute-force loops.
+"""
+
+import ctypes as ct
+import subprocess
+from collections import OrderedDict
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+LIBRARY = ORACLE_DIR / "libekv_oracle.so"
+
+
+def build(force=True):
+    """Compile ekv_oracle.c into libekv_oracle.so with the oracle Makefile."""
+    command = ["make", "-s", "-C", str(ORACLE_DIR)] + (["-B"] if force else [])
+    subprocess.run(command, check=True)
+    return LIBRARY
+
+
+# ---------------------------------------------------------------- lookup (numpy)
+
+def resolve_resident(topk, table, mapping, rows, lengths, selected, block_size, output,
+                     with_misses=False):
+    """Return (output, misses, counts) after the lookup; inputs are not modified.
+
+    topk [L, B, K]; table [R, T] or [L, R, T]; mapping None, [N] or [L, N];
+    output [L, B, K * bs] int32 initial contents (unselected rows survive).
+    misses is a list over (l, row) of int32 lane arrays (None if not asked).
+    """
+    topk = np.asarray(topk, dtype=np.int64)
+    table = np.asarray(table, dtype=np.int64)
+    rows = np.asarray(rows, dtype=np.int64)
+    lengths = np.asarray(lengths, dtype=np.int64)
+    selected = np.asarray(selected, dtype=np.int64)
+    out = np.array(output, dtype=np.int32, copy=True)
+    L, B, K = topk.shape
+    width = K * block_size
+    misses = {} if with_misses else None
+    counts = np.zeros((L, B), dtype=np.int32) if with_misses else None
+    sel = selected[(selected >= 0) & (selected < B)]
+    for layer in range(L):
+        layer_table = table[layer] if table.ndim == 3 else table
+        R, T = layer_table.shape
+        blocks = topk[layer, sel]                                            # [S, K]
+        positions = (blocks[:, :, None] * block_size + np.arange(block_size)).reshape(len(sel), width)
+        valid = (positions >= 0) & (positions < lengths[sel, None])
+        req = rows[sel]
+        req_ok = (req >= 0) & (req < R)
+        in_bounds = valid & req_ok[:, None] & (positions < T)
+        logical = layer_table[np.where(req_ok, req, 0)[:, None], np.where(in_bounds, positions, 0)]
+        if mapping is None:
+            physical = logical
+        else:
+            layer_map = np.asarray(mapping, dtype=np.int64)
+            layer_map = layer_map[layer] if layer_map.ndim == 2 else layer_map
+            in_bounds &= (logical >= 0) & (logical < layer_map.shape[0])
+            physical = layer_map[np.where(in_bounds, logical, 0)]
+        result = np.where(in_bounds, physical, -1).astype(np.int32)
+        out[layer, sel] = result
+        if with_misses:
+            for i, row in enumerate(sel):
+                lanes = np.nonzero(in_bounds[i] & (result[i] == 0))[0].astype(np.int32)
+                misses[(layer, int(row))] = lanes
+                counts[layer, row] = lanes.size
+    return out, misses, counts
+
+
+def access_tokens(blocks, block_size, seq_len, hot_capacity, prestate):
+    """Selected tokens and sorted hit tokens of one HiSparse swap-in.
+
+    Restates adaptive_sparse/hisparse_access_trace.py:59-71: every token of a
+    non-negative block below seq_len is selected; when seq_len fits the hot
+    capacity everything hits, otherwise hits are selected tokens that were
+    resident before the swap or are the newest token seq_len - 1.
+    """
+    selected = []
+    for block in blocks:
+        if block < 0:
+            continue
+        stop = min((block + 1) * block_size, seq_len)
+        selected.extend(range(block * block_size, stop))
+    if seq_len <= hot_capacity:
+        return selected, sorted(set(selected))
+    resident = set(prestate) | {seq_len - 1}
+    return selected, sorted(resident & set(selected))
+
+
+def lru_misses(steps, capacity):
+    """Misses per step of the batch-token LRU of one (request, layer) stream.
+
+    Restates benchmarks/hisparse_locality_replay.py:90-99: misses are counted
+    on entry, hits are touched (moved to most recent) before eviction, least
+    recent entries are evicted until the misses fit, then misses are inserted
+    in selection order.
+    """
+    cache = OrderedDict()
+    result = []
+    for selected in steps:
+        missing = [token for token in selected if token not in cache]
+        for token in selected:
+            if token in cache:
+                cache.move_to_end(token)
+        while len(cache) + len(missing) > capacity:
+            cache.popitem(last=False)
+        for token in missing:
+            cache[token] = None
+        result.append(len(missing))
+    return result
+
+
+# ---------------------------------------------------------------- gathers (numpy)
+
+def gather_rows(raw, positions, request_ids, lengths, request_table, slot_offsets, width,
+                request_stride, sink, indirect):
+    """Restates experimental/sparse_read.py:18-30 on a 1-D numpy payload."""
+    raw = np.asarray(raw)
+    positions = np.asarray(positions, dtype=np.int64)
+    B, S = positions.shape
+    out = np.zeros((B, S, width), dtype=raw.dtype)
+    for b in range(B):
+        req = int(request_ids[b])
+        for s in range(S):
+            pos = int(positions[b, s])
+            if not 0 <= pos < int(lengths[b]):
+                continue
+            if indirect:
+                table = np.asarray(request_table)
+                if not (0 <= req < table.shape[0] and pos < table.shape[1]):
+                    continue
+                logical = int(table[req, pos])
+                if not 0 <= logical < len(slot_offsets):
+                    continue
+                element = int(slot_offsets[logical])
+            else:
+                element = sink + req * request_stride + pos * width
+            if 0 <= element and element + width <= raw.shape[0]:
+                out[b, s] = raw[element:element + width]
+    return out
+
+
+def gather_kv(pool, layer_stride, kv_stride, row_stride, row_bytes, rows, slots, kv, zero_below=1):
+    """Dense [B, L, KV, K, row_bytes] uint8 gather from a byte pool.
+
+    pool is a 1-D uint8 array; slots [L, B, K]. Rows with a slot outside
+    [zero_below, rows) are zero.
+    """
+    pool = np.asarray(pool, dtype=np.uint8)
+    slots = np.asarray(slots, dtype=np.int64)
+    L, B, K = slots.shape
+    out = np.zeros((B, L, kv, K, row_bytes), dtype=np.uint8)
+    cols = np.arange(row_bytes)
+    for layer in range(L):
+        for plane in range(kv):
+            valid = (slots[layer] >= zero_below) & (slots[layer] < rows)            # [B, K]
+            starts = layer * layer_stride + plane * kv_stride + np.where(valid, slots[layer], 0) * row_stride
+            values = pool[starts[..., None] + cols]                                  # [B, K, row_bytes]
+            out[:, layer, plane] = np.where(valid[..., None], values, 0)
+    return out
+
+
+# ---------------------------------------------------------------- C oracle
+
+_I64P = ct.POINTER(ct.c_int64)
+_I32P = ct.POINTER(ct.c_int32)
+_U8P = ct.POINTER(ct.c_uint8)
+
+
+def _i64(array):
+    return np.ascontiguousarray(array, dtype=np.int64)
+
+
+def _ptr(array, kind):
+    return array.ctypes.data_as(kind) if array is not None else None
+
+
+class COracle:
+    """ctypes binding of ekv_oracle.c (built by build())."""
+
+    def __init__(self, path=LIBRARY):
+        if not Path(path).exists():
+            build()
+        self.lib = ct.CDLL(str(path))
+        self.lib.oracle_resolve_resident.restype = None
+        self.lib.oracle_gather_rows.restype = None
+        self.lib.oracle_gather_kv.restype = None
+        self.lib.oracle_scatter_kv.restype = None
+
+    def resolve_resident(self, topk, table, mapping, rows, lengths, selected, block_size, output,
+                         with_misses=False):
+        topk, table, rows, lengths, selected = map(_i64, (topk, table, rows, lengths, selected))
+        L, B, K = topk.shape
+        width = K * block_size
+        out = np.array(output, dtype=np.int32, copy=True, order="C")
+        misses = np.full((L, B, width), -1, dtype=np.int32) if with_misses else None
+        counts = np.zeros((L, B), dtype=np.int32) if with_misses else None
+        layered = table.ndim == 3
+        R, T = table.shape[-2:]
+        map_arr = _i64(mapping) if mapping is not None else None
+        N = map_arr.shape[-1] if map_arr is not None else 0
+        self.lib.oracle_resolve_resident(
+            ct.c_int64(L), ct.c_int64(B), ct.c_int64(K), ct.c_int64(block_size), _ptr(topk, _I64P),
+            _ptr(table, _I64P), ct.c_int(int(layered)), ct.c_int64(R), ct.c_int64(T),
+            _ptr(map_arr, _I64P), ct.c_int(int(map_arr is not None and map_arr.ndim == 2)), ct.c_int64(N),
+            _ptr(rows, _I64P), _ptr(lengths, _I64P), _ptr(selected, _I64P), ct.c_int64(selected.shape[0]),
+            _ptr(out, _I32P), _ptr(misses, _I32P), _ptr(counts, _I32P))
+        return out, misses, counts
+
+    def gather_rows(self, raw, positions, request_ids, lengths, request_table, slot_offsets, width,
+                    request_stride, sink, indirect):
+        raw = np.ascontiguousarray(raw)
+        positions, request_ids, lengths = map(_i64, (positions, request_ids, lengths))
+        B, S = positions.shape
+        table = _i64(request_table) if indirect else np.zeros((0, 0), np.int64)
+        offsets = _i64(slot_offsets) if indirect else np.zeros(0, np.int64)
+        out = np.empty((B, S, width), dtype=raw.dtype)
+        self.lib.oracle_gather_rows(
+            raw.ctypes.data_as(_U8P), ct.c_int64(raw.shape[0]), ct.c_int64(raw.itemsize),
+            _ptr(positions, _I64P), ct.c_int64(B), ct.c_int64(S), _ptr(request_ids, _I64P),
+            _ptr(lengths, _I64P), _ptr(table, _I64P), ct.c_int64(table.shape[0]),
+            ct.c_int64(table.shape[1]), _ptr(offsets, _I64P), ct.c_int64(offsets.shape[0]),
+            ct.c_int(int(bool(indirect))), ct.c_int64(width), ct.c_int64(request_stride), ct.c_int64(sink),
+            out.ctypes.data_as(_U8P))
+        return out
+
+    def gather_kv(self, pool, layer_stride, kv_stride, row_stride, row_bytes, rows, slots, kv,
+                  zero_below=1, shared_layers=None):
+        """Dense [B, L, KV, K, row_bytes] gather. shared_layers=L uses one [B, K] slot list."""
+        pool = np.ascontiguousarray(pool, dtype=np.uint8)
+        slots = _i64(slots)
+        if shared_layers is not None:
+            B, K = slots.shape
+            L, layer_step = shared_layers, 0
+        else:
+            L, B, K = slots.shape
+            layer_step = B * K
+        out = np.empty((B, L, kv, K, row_bytes), dtype=np.uint8)
+        self.lib.oracle_gather_kv(
+            pool.ctypes.data_as(_U8P), ct.c_int64(layer_stride), ct.c_int64(kv_stride), ct.c_int64(row_stride),
+            ct.c_int64(row_bytes), ct.c_int64(rows), ct.c_int64(L), ct.c_int64(B), ct.c_int64(kv), ct.c_int64(K),
+            _ptr(slots, _I64P), ct.c_int64(layer_step), ct.c_int64(zero_below), out.ctypes.data_as(_U8P))
+        return out
+
+    def scatter_kv(self, pool, layer_stride, kv_stride, row_stride, row_bytes, rows, slots, kv, source,
+                   zero_below=1):
+        """Return a copy of the byte pool after scattering dense [B, L, KV, K, row_bytes] rows."""
+        pool = np.array(pool, dtype=np.uint8, copy=True)
+        slots = _i64(slots)
+        L, B, K = slots.shape
+        source = np.ascontiguousarray(source, dtype=np.uint8)
+        self.lib.oracle_scatter_kv(
+            pool.ctypes.data_as(_U8P), ct.c_int64(layer_stride), ct.c_int64(kv_stride), ct.c_int64(row_stride),
+            ct.c_int64(row_bytes), ct.c_int64(rows), ct.c_int64(L), ct.c_int64(B), ct.c_int64(kv), ct.c_int64(K),
+            _ptr(slots, _I64P), ct.c_int64(B * K), ct.c_int64(zero_below), source.ctypes.data_as(_U8P))
+        return pool

@@ -1,0 +1,137 @@
+"""GPU parity of the HIP resident lookup + miss compaction against the oracle.
+
+Bar: bit-exact output, miss list and miss counts. Inputs are seeded and
+identical for both sides; the oracle runs on the same host arrays.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from adaptive_sparse.resident_lookup import resolve_resident
+
+pytestmark = pytest.mark.gpu
+
+
+def strided(values, dtype, device):
+    """A non-contiguous view holding `values` (tests/smoke_resident_lookup.py:28-33)."""
+    source = torch.tensor(values, dtype=dtype, device=device)
+    backing = torch.empty((*source.shape, 2), dtype=dtype, device=device)
+    view = backing[..., 1]
+    view.copy_(source)
+    return view
+
+
+def test_reference_smoke_on_strided_inputs(gpu, coracle):
+    topk = [[[1, -1, 2] + [-1] * 13, [0] * 16, [0, 2, -1] + [-1] * 13]]
+    rows, lengths, selected = [3, 0, 1], [130, 0, 0], [2, 0]
+    table = [[i * 300 + j for j in range(300)] for i in range(4)]
+    mapping = [i * 3 + 5 for i in range(1200)]
+    output = torch.full((1, 3, 4096), -77, device=gpu, dtype=torch.int32)[..., ::2]
+    resolve_resident(strided(topk, torch.int32, gpu), strided(table, torch.long, gpu),
+                     strided(mapping, torch.long, gpu), strided(rows, torch.long, gpu),
+                     strided(lengths, torch.int32, gpu), strided(selected, torch.long, gpu),
+                     output, 128)
+    got = output.cpu().numpy()
+    assert got[0, 0, :3].tolist() == [3089, 3092, -1]
+    assert (got[0, 2] == -1).all() and (got[0, 1] == -77).all()
+    want, _, _ = coracle.resolve_resident(topk, table, mapping, rows, lengths, selected, 128,
+                                          np.full((1, 3, 2048), -77, np.int32))
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("batch", [1, 2, 4])
+def test_reference_closed_form(gpu, batch):
+    device = gpu
+    selected = torch.arange(batch, device=device)
+    rows = selected.flip(0)
+    lengths = torch.full((batch,), 8192, dtype=torch.int32, device=device)
+    table = torch.arange(batch * 8192, device=device).reshape(batch, 8192) + 1
+    mapping = torch.arange(batch * 8192 + 1, device=device) * 3 + 5
+    topk = (torch.arange(16, device=device) * 4).int().expand(1, batch, 16).contiguous()
+    result = torch.empty((1, batch, 2048), device=device, dtype=torch.int32)
+    resolve_resident(topk, table, mapping, rows, lengths, selected, result, 128)
+    closed = torch.tensor([[((batch - 1 - row) * 8192 + block * 512 + offset + 1) * 3 + 5
+                            for block in range(16) for offset in range(128)] for row in range(batch)],
+                          dtype=torch.int32).unsqueeze(0)
+    assert torch.equal(result.cpu(), closed)
+
+
+CASES = [
+    # layers, batch, k, block_size, table_rows, table_cols, layered, map dtype, topk/table dtypes
+    (1, 3, 16, 128, 4, 2100, False, torch.int64, torch.int32, torch.int64),
+    (2, 5, 37, 3, 6, 130, True, torch.int32, torch.int64, torch.int32),
+    (3, 4, 2053, 1, 4, 4100, True, None, torch.int32, torch.int32),
+    (1, 7, 64, 1, 9, 70, False, None, torch.int64, torch.int64),
+    (2, 2, 5, 7, 3, 40, False, torch.int64, torch.int32, torch.int32),
+    (1, 1, 4096, 2, 2, 9000, False, torch.int32, torch.int32, torch.int64),
+]
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+@pytest.mark.parametrize("compact", [True, False])
+def test_random_parity_with_oracle(gpu, coracle, case, compact):
+    layers, batch, k, bs, rrows, cols, layered, map_dtype, topk_dtype, table_dtype = CASES[case]
+    rng = np.random.default_rng(1000 + case)
+    topk = rng.integers(-1, cols // bs + 2, size=(layers, batch, k))
+    rows = rng.integers(0, rrows, size=batch)
+    lengths = rng.integers(0, cols + 3, size=batch)
+    n = 5000
+    table = rng.integers(0, n, size=(layers, rrows, cols) if layered else (rrows, cols))
+    mapping = None
+    if map_dtype is not None:
+        mapping = rng.integers(1, 1 << 20, size=n)
+        mapping[rng.random(n) < 0.3] = 0
+    else:
+        table[rng.random(table.shape) < 0.3] = 0
+    selected = rng.permutation(batch)[: max(1, batch - 1)]
+    width = k * bs
+    initial = np.full((layers, batch, width), -77, np.int32)
+    want, want_misses, want_counts = coracle.resolve_resident(topk, table, mapping, rows, lengths, selected,
+                                                              bs, initial, with_misses=True)
+    t = lambda a, dt: torch.tensor(a, dtype=dt, device=gpu)  # noqa: E731
+    output = t(initial, torch.int32)
+    misses = torch.full((layers, batch, width), -5, dtype=torch.int32, device=gpu) if compact else None
+    counts = torch.full((layers, batch), -5, dtype=torch.int32, device=gpu) if compact else None
+    resolve_resident(t(topk, topk_dtype), t(table, table_dtype),
+                     None if mapping is None else t(mapping, map_dtype), t(rows, torch.int64),
+                     t(lengths, torch.int32), t(selected, torch.int64), output, bs,
+                     misses=misses, miss_count=counts)
+    assert np.array_equal(output.cpu().numpy(), want)
+    if compact:
+        got_counts = counts.cpu().numpy()
+        got_misses = misses.cpu().numpy()
+        for layer in range(layers):
+            for row in range(batch):
+                if row in selected:
+                    c = want_counts[layer, row]
+                    assert got_counts[layer, row] == c
+                    assert np.array_equal(got_misses[layer, row, :c], want_misses[layer, row, :c])
+                    assert (got_misses[layer, row, c:] == -5).all()
+                else:
+                    assert got_counts[layer, row] == -5
+
+
+def test_empty_selection_and_zero_width_do_nothing(gpu):
+    output = torch.full((1, 2, 8), 9, dtype=torch.int32, device=gpu)
+    topk = torch.zeros((1, 2, 4), dtype=torch.int32, device=gpu)
+    table = torch.ones((2, 8), dtype=torch.int64, device=gpu)
+    rows = torch.arange(2, device=gpu)
+    lengths = torch.full((2,), 8, dtype=torch.int32, device=gpu)
+    resolve_resident(topk, table, None, rows, lengths, torch.empty(0, dtype=torch.long, device=gpu), output, 2)
+    resolve_resident(topk[:, :, :0], table, None, rows, lengths, rows, output[:, :, :0], 2)
+    torch.cuda.synchronize()
+    assert (output == 9).all()
+
+
+def test_shape_errors_raise(gpu):
+    topk = torch.zeros((1, 2, 4), dtype=torch.int32, device=gpu)
+    table = torch.ones((2, 8), dtype=torch.int64, device=gpu)
+    rows = torch.arange(2, device=gpu)
+    lengths = torch.full((2,), 8, dtype=torch.int32, device=gpu)
+    with pytest.raises(RuntimeError, match="output"):
+        resolve_resident(topk, table, None, rows, lengths, rows,
+                         torch.zeros((1, 2, 7), dtype=torch.int32, device=gpu), 2)
+    with pytest.raises(RuntimeError, match="int32"):
+        resolve_resident(topk, table, None, rows, lengths, rows,
+                         torch.zeros((1, 2, 8), dtype=torch.int64, device=gpu), 2)

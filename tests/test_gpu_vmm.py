@@ -1,0 +1,182 @@
+"""GPU tests of the HIP VMM backing and the gathers that read through it.
+
+Mirror the reference's GPU tests: tests/test_backing.py:370-413 (map, hole,
+reclaim, precommit, zero on commit, stable VA) and tests/test_graph_backing.py
+(graph replay across reclaim and recommit at a stable VA), plus the gather
+micro-benchmark's exact payload checks (scripts/bench_virtual_addressing.py:
+43-88) run through a real VMM arena.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from elastic_kv.backing import DEFAULT_CHUNK_BYTES, Backing
+from experimental.resident_arena import VmmResidentArena
+from experimental.sparse_read import gather_rows
+from experimental.virtual_layout import VirtualKVLayout
+
+pytestmark = pytest.mark.gpu
+
+
+def test_release_and_recommit_one_hole(gpu):
+    chunk = DEFAULT_CHUNK_BYTES
+    backing = Backing(5 * chunk - 17, chunk_bytes=chunk, device=0)
+    try:
+        assert backing.ensure([0, 1, 2, 4]) == 4
+        assert backing.reserved_bytes == 5 * chunk
+        assert backing.backed_bytes == 4 * chunk
+        raw = backing.raw
+        base = raw.data_ptr()
+        assert base == backing.base
+        assert raw.numel() == 5 * chunk - 17
+        assert base % chunk == 0, "reservation should be chunk aligned"
+        views = {i: raw[i * chunk:(i + 1) * chunk] for i in (0, 1, 2, 4)}
+        for i in (0, 1, 2, 4):
+            assert torch.count_nonzero(views[i]).item() == 0, "new chunks are zero-filled"
+        for i, value in ((0, 11), (1, 22), (2, 33), (4, 55)):
+            views[i].fill_(value)
+        assert backing.reclaim([1, 3, 1]) == 1
+        assert backing.mapped_chunks == {0, 2, 4}
+        assert backing.backed_bytes == 3 * chunk
+        for i, value in ((0, 11), (2, 33), (4, 55)):
+            assert views[i].eq(value).all().item()
+        assert backing.precommit([1]) == 1
+        assert backing.mapped_chunks == {0, 2, 4}
+        assert backing.backed_bytes == 4 * chunk
+        assert backing.ensure([1]) == 0
+        assert backing.mapped_chunks == {0, 1, 2, 4}
+        assert backing.raw.data_ptr() == base
+        assert views[1].data_ptr() == base + chunk
+        assert torch.count_nonzero(views[1]).item() == 0
+        for i, value in ((0, 11), (2, 33), (4, 55)):
+            assert views[i].data_ptr() == base + i * chunk
+            assert views[i].eq(value).all().item()
+        metrics = backing.metrics
+        assert metrics["ensure_chunks"] == 4 and metrics["reclaim_chunks"] == 1
+        assert metrics["precommit_chunks"] == 1
+    finally:
+        backing.close()
+
+
+def test_errors_are_reported_not_fatal(gpu):
+    backing = Backing(2 * DEFAULT_CHUNK_BYTES, device=0)
+    try:
+        with pytest.raises(ValueError):
+            backing.ensure([2])
+        with pytest.raises(RuntimeError, match="sink"):
+            backing.raw
+        assert backing.ensure([0, 0, 1]) == 2
+        assert backing.ensure([1]) == 0
+        assert backing.reclaim([1]) == 1 and backing.reclaim([1]) == 0
+    finally:
+        backing.close()
+    with pytest.raises(RuntimeError):
+        Backing(DEFAULT_CHUNK_BYTES, chunk_bytes=DEFAULT_CHUNK_BYTES + 1, device=0)
+
+
+def test_graph_replays_across_reclaim_and_recommit(gpu):
+    chunk = 2 << 20
+    backing = Backing(4 * chunk, chunk_bytes=chunk, device=0)
+    try:
+        assert backing.ensure([0, 1, 2]) == 3
+        raw = backing.raw
+        base = raw.data_ptr()
+        raw[0] = 7
+        raw[chunk] = 23
+        raw[2 * chunk] = 41
+        indices = torch.tensor([chunk, 2 * chunk, 0], device=gpu)
+        graph = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            result = torch.index_select(raw, 0, indices)
+
+        def replay(offsets, expected):
+            indices.copy_(torch.tensor(offsets, device=gpu))
+            graph.replay()
+            assert result.tolist() == expected
+            assert backing.raw.data_ptr() == base
+
+        replay([chunk, 2 * chunk, 0], [23, 41, 7])
+        torch.cuda.synchronize()
+        assert backing.reclaim([1], synchronize=False) == 1
+        replay([2 * chunk, 0, 0], [41, 7, 7])
+        assert backing.ensure([1]) == 1
+        raw[chunk] = 97
+        replay([chunk, 2 * chunk, 0], [97, 41, 7])
+        del graph, result
+    finally:
+        torch.cuda.synchronize()
+        backing.close()
+
+
+def support_sets(length, selected, seed=137):
+    import random
+
+    rng = random.Random(seed)
+    clustered = set()
+    run = max(1, selected // 8)
+    while len(clustered) < selected:
+        begin = rng.randrange(length)
+        for step in range(min(run, selected - len(clustered))):
+            clustered.add((begin + step) % length)
+    return {"contiguous": list(range(selected)), "uniform_random": rng.sample(range(length), selected),
+            "synthetic_clustered": sorted(clustered)}
+
+
+@pytest.mark.parametrize("width", [256, 3])
+def test_gather_rows_through_vmm_arena(gpu, coracle, width):
+    """scripts/bench_virtual_addressing.py:43-88 at reduced size, bit-exact."""
+    batch, length, selected = 3, 4096 if width == 256 else 700, 512
+    layout = VirtualKVLayout(batch, length, width)
+    arena = VmmResidentArena(layout)
+    try:
+        for req in range(batch):
+            arena.reserve(req, length)
+            view = arena.row_view(req, length, torch.bfloat16)
+            values = (torch.arange(length * width, device=gpu) + req * 17) % 97
+            view.copy_(values.reshape(length, width))
+        del view
+        raw = arena.backing.raw.view(torch.bfloat16)
+        request_ids = torch.arange(batch, device=gpu, dtype=torch.int64).flip(0)
+        lengths = torch.full((batch,), length, device=gpu, dtype=torch.int64)
+        count = batch * length
+        table = torch.arange(count, 0, -1, device=gpu, dtype=torch.int64).reshape(batch, length)
+        flat = torch.arange(count, device=gpu, dtype=torch.int64)
+        addresses = (layout.chunk_bytes // layout.itemsize + (flat // length) * (layout.request_bytes // layout.itemsize)
+                     + (flat % length) * width)
+        offsets = torch.zeros(count + 1, device=gpu, dtype=torch.int64)
+        offsets[table.flatten()] = addresses
+        output = torch.empty((batch, selected, width), device=gpu, dtype=torch.bfloat16)
+        raw_host = raw.view(torch.uint16).cpu().numpy()
+        for name, support in support_sets(length, selected).items():
+            positions = torch.tensor(support, device=gpu, dtype=torch.int64).expand(batch, -1).contiguous()
+            columns = torch.arange(width, device=gpu)
+            expected = ((positions.clamp_min(0)[..., None] * width + columns
+                         + request_ids[:, None, None] * 17) % 97).to(torch.bfloat16)
+            for indirect in (False, True):
+                gather_rows(raw, positions, request_ids, lengths, table, offsets, output, layout,
+                            indirect=indirect)
+                assert torch.equal(output, expected), (name, indirect)
+                for invalid in (-1, length):
+                    bad = positions.clone()
+                    bad[:, 0] = invalid
+                    want = expected.clone()
+                    want[:, 0] = 0
+                    gather_rows(raw, bad, request_ids, lengths, table, offsets, output, layout,
+                                indirect=indirect)
+                    assert torch.equal(output, want), (name, invalid, indirect)
+                oracle_out = coracle.gather_rows(raw_host, positions.cpu().numpy(), request_ids.cpu().numpy(),
+                                                 lengths.cpu().numpy(), table.cpu().numpy(),
+                                                 offsets.cpu().numpy(), width, layout.request_bytes // 2,
+                                                 layout.chunk_bytes // 2, indirect)
+                gather_rows(raw, positions, request_ids, lengths, table, offsets, output, layout,
+                            indirect=indirect)
+                assert np.array_equal(output.view(torch.uint16).cpu().numpy(), oracle_out)
+        pointer, before = arena.backing.base, arena.backing.backed_bytes
+        del raw, output, expected
+        arena.resize_quiescent(0, 0)
+        assert arena.backing.base == pointer
+        assert before - arena.backing.backed_bytes == layout.request_bytes
+    finally:
+        arena.close()

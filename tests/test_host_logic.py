@@ -1,0 +1,501 @@
+"""Host-side bookkeeping of the path (CPU only), ported from the reference's tests.
+
+Sources: tests/test_slots.py, tests/test_virtual_layout.py,
+tests/test_minimax_vmm.py, tests/test_backing.py:21-128 (fake native
+library), the recorded chunk-aware demotion plans, and the migration
+bandwidth estimator's closed form.
+"""
+
+import gc
+import json
+import math
+import random
+from types import SimpleNamespace
+from unittest.mock import Mock, call, patch
+
+import pytest
+
+from adaptive_sparse.kv_pool import BlockMajorLayout, PlanePoolLayout
+from adaptive_sparse.migration import plan_demote_pages
+from adaptive_sparse.migration_budget import MigrationBandwidthEstimator
+from adaptive_sparse.minimax_vmm import PhysicalPages
+from conftest import GOLDEN
+from elastic_kv.backing import Backing, _load_library
+from elastic_kv.slots import FreeSlots
+from experimental.resident_arena import VmmResidentArena
+from experimental.virtual_layout import VirtualKVLayout
+
+# ------------------------------------------------------------------ FreeSlots
+
+
+def test_slots_fragmented_claim_and_bridge_merge():
+    slots = FreeSlots(8)
+    slots.claim(slots.peek(8))
+    slots.release([1, 2, 4, 5, 7, 8])
+    ranges = slots.peek(3)
+    assert ranges == [(1, 3), (4, 5)]
+    slots.claim(ranges)
+    assert slots.ranges == [(5, 6), (7, 9)]
+    slots.release([6])
+    assert slots.ranges == [(5, 9)]
+    assert slots.count == 4
+
+
+def test_slots_peek_bounds_leave_state_intact():
+    slots = FreeSlots(2)
+    assert slots.peek(0) == []
+    assert slots.peek(3) is None
+    with pytest.raises(ValueError):
+        slots.peek(-1)
+    assert slots.ranges == [(1, 3)] and slots.count == 2
+
+
+def test_slots_remove_arbitrary_ranges():
+    slots = FreeSlots(16)
+    slots.remove([(5, 8)])
+    assert slots.ranges == [(1, 5), (8, 17)] and slots.count == 13
+    slots.remove([(1, 2), (9, 11)])
+    assert slots.ranges == [(2, 5), (8, 9), (11, 17)] and slots.count == 10
+    with pytest.raises(ValueError, match="crosses a non-free slot"):
+        slots.remove([(1, 2)])
+    with pytest.raises(ValueError, match="crosses a non-free slot"):
+        slots.remove([(4, 9)])
+
+
+def _as_ranges(values):
+    values = sorted(values)
+    ranges = []
+    start = previous = values[0]
+    for value in values[1:]:
+        if value != previous + 1:
+            ranges.append((start, previous + 1))
+            start = value
+        previous = value
+    ranges.append((start, previous + 1))
+    return ranges
+
+
+def test_slots_randomized_remove_against_set_model():
+    rng = random.Random(713)
+    capacity = 97
+    slots = FreeSlots(capacity)
+    free = set(range(1, capacity + 1))
+    for _ in range(1000):
+        if len(free) > 12 and rng.randrange(2):
+            chosen = sorted(rng.sample(sorted(free), rng.randint(1, 8)))
+            slots.remove(_as_ranges(chosen))
+            free.difference_update(chosen)
+        else:
+            live = set(range(1, capacity + 1)) - free
+            if not live:
+                continue
+            released = rng.sample(sorted(live), rng.randint(1, min(8, len(live))))
+            slots.release(sorted(released))
+            free.update(released)
+        assert slots.count == len(free)
+        assert [s for a, b in slots.ranges for s in range(a, b)] == sorted(free)
+
+
+def test_slots_randomized_conservation():
+    rng = random.Random(504)
+    capacity = 97
+    slots = FreeSlots(capacity)
+    free = set(range(1, capacity + 1))
+    for _ in range(3000):
+        live = sorted(set(range(1, capacity + 1)) - free)
+        if live and rng.randrange(2):
+            ids = sorted(rng.sample(live, rng.randint(1, min(9, len(live)))))
+            slots.release(ids)
+            free.update(ids)
+        else:
+            count = rng.randint(0, 10)
+            before = slots.ranges.copy()
+            ranges = slots.peek(count)
+            assert slots.ranges == before
+            if count > len(free):
+                assert ranges is None
+            else:
+                chosen = [s for a, b in ranges for s in range(a, b)]
+                assert chosen == sorted(free)[:count]
+                slots.claim(ranges)
+                free.difference_update(chosen)
+        assert slots.count == len(free)
+        assert [s for a, b in slots.ranges for s in range(a, b)] == sorted(free)
+        assert all(a[1] < b[0] for a, b in zip(slots.ranges, slots.ranges[1:]))
+
+
+# ------------------------------------------------------------------ layouts / arena
+
+
+def test_layout_alignment_and_crossing_rows():
+    layout = VirtualKVLayout(2, 3, 3, chunk_bytes=8)
+    assert layout.capacity_bytes == 56
+    assert layout.request_offset(1) == 32
+    assert layout.token_offset(0, 1) == 14
+    assert layout.prefix_chunks(0, 0) == set()
+    assert layout.selected_chunks(0, []) == set()
+    assert layout.selected_chunks(0, [1, 1]) == {1, 2}
+    assert layout.prefix_chunks(0, 3) == {1, 2, 3}
+    assert layout.prefix_chunks(1, 3) == {4, 5, 6}
+
+
+def test_layout_rejects_invalid_fields_and_indices():
+    fields = dict(max_requests=2, max_tokens=3, row_elements=3, itemsize=2, chunk_bytes=8)
+    for field in fields:
+        with pytest.raises(ValueError):
+            VirtualKVLayout(**(fields | {field: 0}))
+        with pytest.raises(TypeError):
+            VirtualKVLayout(**(fields | {field: True}))
+    layout = VirtualKVLayout(**fields)
+    for index in (-1, 2):
+        with pytest.raises(ValueError):
+            layout.selected_chunks(index, [])
+    for position in (-1, 3):
+        with pytest.raises(ValueError):
+            layout.selected_chunks(0, [position])
+    for length in (-1, 4):
+        with pytest.raises(ValueError):
+            layout.prefix_chunks(0, length)
+
+
+@pytest.fixture
+def arena_calls():
+    calls = Mock()
+    layout = VirtualKVLayout(2, 5, 3, chunk_bytes=8)
+    arena = VmmResidentArena(layout, backing_factory=calls.factory, synchronize=calls.sync)
+    return calls, calls.factory.return_value, arena
+
+
+def test_arena_lifecycle_preserves_live_tail_chunk(arena_calls):
+    calls, _, arena = arena_calls
+    arena.reserve(0, 3)
+    arena.reserve(0, 1)
+    arena.reserve(1, 1)
+    arena.resize_quiescent(0, 2)
+    arena.close()
+    arena.close()
+    assert calls.mock_calls == [
+        call.factory(72, chunk_bytes=8, device=0), call.factory().ensure({0}),
+        call.factory().ensure({1, 2, 3}), call.factory().ensure({5}),
+        call.sync(), call.factory().reclaim({3}, synchronize=False),
+        call.sync(), call.factory().close(),
+    ]
+    with pytest.raises(RuntimeError):
+        arena.reserve(0, 1)
+
+
+def test_arena_view_checks_extent_and_dtype(arena_calls):
+    _, backing, arena = arena_calls
+    dtype = SimpleNamespace(itemsize=2)
+    arena.reserve(1, 2)
+    arena.row_view(1, 2, dtype)
+    backing.raw.narrow.assert_called_once_with(0, 40, 12)
+    backing.raw.narrow.return_value.view.assert_called_once_with(dtype)
+    backing.raw.narrow.return_value.view.return_value.reshape.assert_called_once_with(2, 3)
+    with pytest.raises(ValueError):
+        arena.row_view(1, 3, dtype)
+    with pytest.raises(ValueError):
+        arena.row_view(1, 2, SimpleNamespace(itemsize=4))
+
+
+def test_arena_backing_failure_stops_use_and_close_still_syncs(arena_calls):
+    calls, backing, arena = arena_calls
+    backing.ensure.side_effect = RuntimeError("allocation failed")
+    with pytest.raises(RuntimeError, match="allocation failed"):
+        arena.reserve(0, 2)
+    assert arena.length(0) == 0
+    with pytest.raises(RuntimeError):
+        arena.row_view(0, 0, SimpleNamespace(itemsize=2))
+    arena.close()
+    calls.sync.assert_called_once()
+    backing.close.assert_called_once()
+
+
+def test_plane_pool_layout_chunk_math():
+    layout = PlanePoolLayout(layers=2, kv=2, rows=5, row_bytes=3, chunk_bytes=8)
+    assert layout.plane_chunks == 2 and layout.plane_stride == 16 and layout.capacity_bytes == 64
+    assert layout.plane_offset(1, 1) == 48
+    # slot 2 covers bytes [6, 9) of each plane -> chunks 0 and 1 of every plane
+    assert layout.chunks_for_slots([2]) == {0, 1, 2, 3, 4, 5, 6, 7}
+    assert layout.chunks_for_slots([0]) == {0, 2, 4, 6}
+    assert layout.chunks_for_slot_range(3, 5) == {1, 3, 5, 7}
+    planes = layout.kv_planes(1000, 0)
+    assert planes.row_offset(1, 1, 4) == 48 + 12
+    block = BlockMajorLayout(blocks=4, layers=3, kv=2, row_bytes=5, chunk_bytes=16)
+    assert block.block_bytes == 30 and block.capacity_bytes == 128
+    assert block.chunks_for_blocks([1]) == {1, 2, 3}
+    assert block.kv_planes(0, 0).row_offset(2, 1, 3) == 90 + 25
+
+
+# ------------------------------------------------------------------ PhysicalPages
+
+
+class _ChunkBacking:
+    def __init__(self):
+        self.mapped_chunks = set()
+        self.fail = False
+
+    @property
+    def backed_bytes(self):
+        return len(self.mapped_chunks) * 8
+
+    def ensure(self, indices):
+        if self.fail:
+            raise RuntimeError("map failed")
+        self.mapped_chunks.update(indices)
+
+    def reclaim(self, indices, *, synchronize):
+        assert not synchronize
+        self.mapped_chunks.difference_update(indices)
+        return len(indices)
+
+
+def test_pages_crossing_shared_chunks_tail_reuse_and_sink():
+    backing = _ChunkBacking()
+    syncs = []
+    pages = PhysicalPages(backing, 2, 4, [(0, 3), (8, 2)], lambda: syncs.append(True), chunk_bytes=8)
+    assert pages.chunks(1) == {0, 1, 8}
+    pages.acquire([1, 2, 2])
+    pages.acquire([2])
+    pages.release({1})
+    assert pages.stats()["reclaimable_bytes"] == 0
+    pages.release({2})
+    assert pages.trim_quiescent() == 24
+    assert backing.mapped_chunks == {0, 8}
+    assert syncs == [True]
+    with pytest.raises(RuntimeError):
+        pages.release({0})
+
+
+def test_pages_failed_map_does_not_change_ownership():
+    backing = _ChunkBacking()
+    pages = PhysicalPages(backing, 1, 3, [(0, 8)], lambda: None, chunk_bytes=8)
+    backing.fail = True
+    with pytest.raises(RuntimeError, match="map failed"):
+        pages.acquire([1])
+    assert pages.pages == {0}
+    assert pages.refs == {0: 1}
+
+
+# ------------------------------------------------------------------ demotion plans
+
+
+def _tracker_from_snapshot(snapshot):
+    tracker = PhysicalPages.__new__(PhysicalPages)
+    tracker.page_size = snapshot["page_size"]
+    tracker.planes = [tuple(p) for p in snapshot["planes"]]
+    tracker.chunk_bytes = snapshot["chunk_bytes"]
+    tracker._chunk_cache = None
+    tracker.refs = {int(k): v for k, v in snapshot["refs"].items()}
+    return tracker
+
+
+@pytest.mark.parametrize("rank", range(4))
+def test_chunk_aware_plans_reproduce_recorded_snapshots(rank):
+    snapshot = json.loads((GOLDEN / f"demotion_plans_rank{rank}.json").read_text())[0]
+    tracker = _tracker_from_snapshot(snapshot)
+    assert snapshot["requests"]
+    for row, request in snapshot["requests"].items():
+        retained, released = plan_demote_pages(tracker, request["page_ids"], len(request["retained"]),
+                                               chunk_aware=True)
+        assert list(retained) == request["retained"], row
+        assert list(released) == request["released"], row
+
+
+def test_default_plan_keeps_the_first_pages_and_validates():
+    assert plan_demote_pages(None, [5, 3, 9], 2, chunk_aware=False) == ((5, 3), (9,))
+    for pages, keep in (([1, 2], 0), ([1, 2], 3), ([1, 1], 1)):
+        with pytest.raises(ValueError):
+            plan_demote_pages(None, pages, keep, chunk_aware=False)
+    with pytest.raises(RuntimeError):
+        plan_demote_pages(None, [1, 2], 1, chunk_aware=True)
+
+
+def test_chunk_aware_plan_keeps_pages_sharing_chunks():
+    # pages 1..4 with 2 pages per chunk; chunk 0 also held by the sink
+    tracker = SimpleNamespace(chunks=lambda p: {p // 2}, refs={0: 2, 1: 2, 2: 1})
+    retained, released = plan_demote_pages(tracker, [4, 3, 2, 1], 2, chunk_aware=True)
+    # page 1 shares chunk 0 with the sink (no exclusive chunk) -> free to keep;
+    # then page 4's chunk 2 is exclusive to it alone, page 2/3 share chunk 1 (supply 2)
+    assert retained == (1, 2) and released == (4, 3)
+
+
+# ------------------------------------------------------------------ estimator
+
+
+def test_estimator_ewma_closed_form_and_caps():
+    est = MigrationBandwidthEstimator(1 << 30, 0.25)
+    assert est.bandwidth("demotion") == float(1 << 30)
+    assert est.observe("demotion", 0, 1.0) is None and est.samples("demotion") == 0
+    assert est.observe("demotion", 4000, 2.0) == 2000.0
+    assert est.bandwidth("demotion") == 2000.0
+    assert est.observe("demotion", 8000, 1.0) == 8000.0
+    assert est.bandwidth("demotion") == 0.25 * 8000 + 0.75 * 2000
+    assert est.samples("demotion") == 2 and est.samples("promotion") == 0
+    assert est.effective_byte_cap(10_000, 0) == 10_000
+    assert est.effective_byte_cap(10_000, 1000) == math.floor(3500.0)
+    assert est.snapshot() == {"demotion": 3500.0, "promotion": float(1 << 30)}
+    for bad in ((True, 0.5), (0, 0.5), (1, 0.0), (1, 1.5), (1, float("nan"))):
+        with pytest.raises(ValueError):
+            MigrationBandwidthEstimator(*bad)
+    with pytest.raises(ValueError):
+        est.observe("sideways", 1, 1.0)
+    with pytest.raises(ValueError):
+        est.effective_byte_cap(0, 1)
+
+
+# ------------------------------------------------------------------ Backing over a fake library
+
+
+class _FakeLibrary:
+    def __init__(self, reserved_units=2, *, partial_failure=False, rollback_on_failure=False,
+                 close_failure=False):
+        self.mapped = 0
+        self.calls = []
+        self.reserved_units = reserved_units
+        self.partial_failure = partial_failure
+        self.rollback_on_failure = rollback_on_failure
+        self.close_failure = close_failure
+        self.failure = None
+        self.poisoned = False
+
+    def ev_create(self, *_):
+        return 1
+
+    def ev_base(self, _):
+        return 1 << 40
+
+    def ev_backed(self, _):
+        return self.mapped
+
+    def ev_reserved(self, _):
+        return self.reserved_units
+
+    def ev_granularity(self, _):
+        return 1
+
+    def _commit(self, kind, count):
+        if self.partial_failure:
+            self.calls.append((kind + "-partial", count))
+            self.failure = b"injected partial map failure"
+            if not self.rollback_on_failure:
+                self.mapped += max(0, count - 1)
+                self.poisoned = True
+            return 1
+        self.mapped += count
+        self.calls.append((kind, count))
+        return 0
+
+    def ev_ensure(self, _, ids, count):
+        return self._commit("ensure", count)
+
+    def ev_precommit(self, _, ids, count):
+        return self._commit("precommit", count)
+
+    def ev_drop(self, _, ids, count):
+        self.mapped -= count
+        self.calls.append(("drop", count))
+        return 0
+
+    def ev_poisoned(self, _):
+        return int(self.poisoned)
+
+    def ev_close(self, _):
+        if self.close_failure:
+            self.failure = b"injected close failure"
+            return 1
+        self.mapped = 0
+        return 0
+
+    def ev_error(self):
+        return self.failure or b""
+
+
+def _backing(library, chunk=1 << 20, units=2):
+    with patch("elastic_kv.backing._load_library", return_value=library):
+        return Backing(units * chunk, chunk, 0, library="fake.so")
+
+
+def test_missing_library_has_actionable_build_error():
+    _load_library.cache_clear()
+    with patch("elastic_kv.backing.ct.CDLL", side_effect=OSError("missing native library")):
+        with pytest.raises(RuntimeError, match="build_native.py"):
+            _load_library("missing-libelastic-vmm.so")
+    _load_library.cache_clear()
+
+
+def test_outdated_library_requests_a_rebuild():
+    _load_library.cache_clear()
+    names = ("ev_create", "ev_ensure", "ev_precommit", "ev_drop", "ev_base", "ev_backed",
+             "ev_reserved", "ev_granularity", "ev_close", "ev_error")
+    library = SimpleNamespace(**{name: Mock() for name in names})
+    with patch("elastic_kv.backing.ct.CDLL", return_value=library):
+        with pytest.raises(RuntimeError, match="ABI is outdated"):
+            _load_library("old-libelastic-vmm.so")
+    _load_library.cache_clear()
+
+
+def test_broker_environment_is_rejected(monkeypatch):
+    monkeypatch.setenv("EKV_GLOBAL_BROKER_PATH", "/tmp/broker")
+    with pytest.raises(ValueError, match="broker"):
+        _backing(_FakeLibrary(2 << 20))
+
+
+def test_backing_bookkeeping_over_fake_library():
+    chunk = 1 << 20
+    library = _FakeLibrary(4 * chunk)
+    backing = _backing(library, chunk, 4)
+    assert backing.ensure([0, 1]) == 2
+    assert backing.ensure([1]) == 0
+    assert backing.precommit([2, 1]) == 1
+    assert backing.mapped_chunks == {0, 1}
+    assert backing.ensure([2]) == 0            # precommitted: only waits
+    assert backing.mapped_chunks == {0, 1, 2}
+    assert backing.reclaim([1, 3], synchronize=False) == 1
+    with pytest.raises(ValueError):
+        backing.ensure([4])
+    assert library.calls == [("ensure", 2), ("precommit", 1), ("ensure", 0), ("drop", 1)]
+    metrics = backing.metrics
+    assert metrics["ensure_calls"] == 2 and metrics["precommit_chunks"] == 1
+    assert metrics["reclaim_chunks"] == 1 and metrics["backed_bytes"] == 2
+    assert backing.broker_snapshot is None and backing.claim_broker_capacity("r", 1) is None
+    backing.close()
+    with pytest.raises(RuntimeError):
+        backing.ensure([0])
+
+
+def test_partial_failure_poisons_and_clean_rollback_allows_retry():
+    library = _FakeLibrary(2 << 20, partial_failure=True)
+    backing = _backing(library)
+    with pytest.raises(RuntimeError, match="partial map failure"):
+        backing.ensure([0, 1])
+    assert backing._poisoned
+    with pytest.raises(RuntimeError):
+        backing.ensure([0])
+    library = _FakeLibrary(2 << 20, partial_failure=True, rollback_on_failure=True)
+    backing = _backing(library)
+    with pytest.raises(RuntimeError, match="partial map failure"):
+        backing.ensure([0, 1])
+    assert backing.mapped_chunks == frozenset() and not backing._poisoned
+    library.partial_failure = False
+    assert backing.ensure([0, 1]) == 2
+    backing.close()
+
+
+def test_failed_close_can_be_retried_and_gc_closes():
+    library = _FakeLibrary(2 << 20, close_failure=True)
+    backing = _backing(library)
+    backing.ensure([0])
+    with pytest.raises(RuntimeError, match="close failure"):
+        backing.close()
+    library.close_failure = False
+    backing.close()
+    assert library.mapped == 0
+    library = _FakeLibrary(2 << 20)
+
+    def allocate_and_drop():
+        _backing(library).ensure([0])
+
+    allocate_and_drop()
+    gc.collect()
+    assert library.mapped == 0

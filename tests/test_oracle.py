@@ -1,0 +1,324 @@
+"""Pin the CPU oracle before trusting it (CPU only).
+
+Each oracle function is checked against at least one of: a known-answer
+vector from the reference's tests, a closed form the reference states, a
+brute-force loop written directly from the reference's per-lane definition,
+and the other (independent) restatement.
+"""
+
+import random
+
+import numpy as np
+import pytest
+
+from oracle import oracle as ref
+
+# ------------------------------------------------------------------ helpers
+
+
+def brute_force_lookup(topk, table, mapping, rows, lengths, selected, block_size, initial):
+    """Per-lane loop of adaptive_sparse/resident_lookup.py:14-26 on Python lists."""
+    out = [[list(row) for row in layer] for layer in initial]
+    for layer in range(len(topk)):
+        for row in selected:
+            for lane in range(len(topk[layer][row]) * block_size):
+                block = topk[layer][row][lane // block_size]
+                position = block * block_size + lane % block_size
+                if block >= 0 and position < lengths[row]:
+                    logical = table[rows[row]][position]
+                    out[layer][row][lane] = logical if mapping is None else mapping[logical]
+                else:
+                    out[layer][row][lane] = -1
+    return out
+
+
+def smoke_inputs():
+    """Inputs of the reference's tests/smoke_resident_lookup.py:8-13."""
+    topk = [[[1, -1, 2] + [-1] * 13, [0] * 16, [0, 2, -1] + [-1] * 13]]
+    rows = [3, 0, 1]
+    lengths = [130, 0, 0]
+    table = [[i * 300 + j for j in range(300)] for i in range(4)]
+    mapping = [i * 3 + 5 for i in range(1200)]
+    selected = [2, 0]
+    initial = np.full((1, 3, 2048), -77, dtype=np.int32)
+    return topk, table, mapping, rows, lengths, selected, initial
+
+
+def random_lookup_case(rng, layers, batch, k, block_size, table_rows, table_cols, layered, with_map):
+    topk = rng.integers(-1, table_cols // block_size + 2, size=(layers, batch, k))
+    rows = rng.integers(0, table_rows, size=batch)
+    lengths = rng.integers(0, table_cols + 3, size=batch)
+    shape = (layers, table_rows, table_cols) if layered else (table_rows, table_cols)
+    n = 97
+    table = rng.integers(0, n, size=shape)
+    mapping = None
+    if with_map:
+        mapping = rng.integers(-3, 40, size=(n,))
+        mapping[rng.random(n) < 0.4] = 0  # not resident
+    selected = rng.permutation(batch)[: max(1, batch - 1)]
+    initial = np.full((layers, batch, k * block_size), -77, dtype=np.int32)
+    return topk, table, mapping, rows, lengths, selected, initial
+
+
+# ------------------------------------------------------------------ lookup
+
+
+@pytest.mark.parametrize("which", ["numpy", "c"])
+def test_lookup_reference_smoke_vectors(which, coracle):
+    topk, table, mapping, rows, lengths, selected, initial = smoke_inputs()
+    run = ref.resolve_resident if which == "numpy" else coracle.resolve_resident
+    out, _, _ = run(topk, table, mapping, rows, lengths, selected, 128, initial)
+    expected = out[0].tolist()
+    # Known answers from tests/smoke_resident_lookup.py:21-23.
+    assert expected[0][:3] == [3089, 3092, -1]
+    assert expected[0][-1] == -1 and expected[2] == [-1] * 2048
+    assert expected[1] == [-77] * 2048
+    brute = brute_force_lookup(topk, table, mapping, rows, lengths, selected, 128, initial.tolist())
+    assert expected == brute[0]
+
+
+@pytest.mark.parametrize("batch", [1, 2, 4])
+@pytest.mark.parametrize("which", ["numpy", "c"])
+def test_lookup_reference_closed_form(batch, which, coracle):
+    """tests/bench_resident_lookup.py:24-42 inputs against its closed form."""
+    selected = np.arange(batch)
+    rows = selected[::-1].copy()
+    lengths = np.full(batch, 8192)
+    table = np.arange(batch * 8192).reshape(batch, 8192) + 1
+    mapping = np.arange(batch * 8192 + 1) * 3 + 5
+    topk = np.broadcast_to(np.arange(16) * 4, (1, batch, 16))
+    run = ref.resolve_resident if which == "numpy" else coracle.resolve_resident
+    out, _, _ = run(topk, table, mapping, rows, lengths, selected, 128,
+                    np.zeros((1, batch, 2048), np.int32))
+    closed = [[((batch - 1 - row) * 8192 + block * 512 + offset + 1) * 3 + 5
+               for block in range(16) for offset in range(128)] for row in range(batch)]
+    assert out[0].tolist() == closed
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_lookup_numpy_c_and_brute_force_agree(seed, coracle):
+    rng = np.random.default_rng(seed)
+    block_size = [1, 2, 3, 4, 8, 1][seed]
+    layered = seed % 2 == 0
+    with_map = seed % 3 != 2
+    case = random_lookup_case(rng, layers=2, batch=5, k=7, block_size=block_size, table_rows=6,
+                              table_cols=23, layered=layered, with_map=with_map)
+    topk, table, mapping, rows, lengths, selected, initial = case
+    a, am, ac = ref.resolve_resident(*case[:6], block_size, initial, with_misses=True)
+    b, bm, bc = coracle.resolve_resident(*case[:6], block_size, initial, with_misses=True)
+    assert np.array_equal(a, b)
+    assert np.array_equal(ac, bc)
+    for (layer, row), lanes in am.items():
+        assert bm[layer, row, : bc[layer, row]].tolist() == lanes.tolist()
+    # brute force needs in-range indices: restrict to rows whose lanes are all in bounds
+    safe = [row for row in selected
+            if all(0 <= p < table.shape[-1] for p in range(lengths[row]))]
+    tables = [table[layer] if layered else table for layer in range(2)]
+    for layer in range(2):
+        brute = brute_force_lookup([topk[layer]], tables[layer],
+                                   None if mapping is None else mapping, rows, lengths, safe,
+                                   block_size, [initial[layer]])
+        for row in safe:
+            assert a[layer, row].tolist() == brute[0][row]
+
+
+def test_miss_list_is_ordered_nonzero_of_resident_zero():
+    """Miss compaction == torch.nonzero(valid & out == 0), row-major, built by hand."""
+    topk = [[[0, 1, -1, 2]]]
+    table = [[5, 6, 7, 8, 9, 10, 11, 12]]
+    mapping = [0] * 5 + [3, 0, 4, 0, 0, 9, 0, 0]
+    out, misses, counts = ref.resolve_resident(topk, table, mapping, [0], [5], [0], 2,
+                                               np.zeros((1, 1, 8), np.int32), with_misses=True)
+    # lanes: blk0 -> pos 0,1 -> logical 5,6 -> 3,0 ; blk1 -> pos 2,3 -> 4,0 ;
+    # blk -1 -> -1,-1 ; blk2 -> pos 4 -> logical 9 -> 0, pos 5 >= length -> -1
+    assert out[0, 0].tolist() == [3, 0, 4, 0, -1, -1, 0, -1]
+    assert misses[(0, 0)].tolist() == [1, 3, 6]
+    assert counts[0, 0] == 3
+
+
+def test_miss_semantics_match_reference_access_trace_kat():
+    """tests/test_hisparse_access_trace.py:170-199 through the lookup."""
+    # Long path: hot capacity 4, prestate [2, 1, -1, 6], seq_len 7, blocks [1, -1, 3, 1, 4], bs 2.
+    selected, hits = ref.access_tokens([1, -1, 3, 1, 4], 2, 7, 4, [2, 1, -1, 6])
+    assert selected == [2, 3, 6, 2, 3] and hits == [2, 6]
+    resident = {2, 1, 6} | {7 - 1}
+    table = [[slot + 1 if pos in resident else 0 for slot, pos in enumerate(range(10))]]
+    out, misses, _ = ref.resolve_resident([[[1, -1, 3, 1, 4]]], table, None, [0], [7], [0], 2,
+                                          np.zeros((1, 1, 10), np.int32), with_misses=True)
+    lanes = out[0, 0]
+    positions = [b * 2 + j for b in [1, -1, 3, 1, 4] for j in range(2)]
+    valid = [i for i, p in enumerate(positions) if [1, -1, 3, 1, 4][i // 2] >= 0 and p < 7]
+    assert [positions[i] for i in valid] == selected
+    miss_lanes = set(misses[(0, 0)].tolist())
+    assert sorted({positions[i] for i in valid if i not in miss_lanes}) == hits
+    assert all(lanes[i] > 0 for i in valid if i not in miss_lanes)
+    # Short path: seq_len 4 <= capacity 4, everything resident.
+    selected, hits = ref.access_tokens([1, 0, 2], 2, 4, 4, [3, 4, 5, 0])
+    assert selected == [2, 3, 0, 1] and hits == [0, 1, 2, 3]
+    out, misses, _ = ref.resolve_resident([[[1, 0, 2]]], [[1, 2, 3, 4, 5, 6]], None, [0], [4], [0], 2,
+                                          np.zeros((1, 1, 6), np.int32), with_misses=True)
+    assert misses[(0, 0)].tolist() == []
+    assert out[0, 0].tolist() == [3, 4, 1, 2, -1, -1]
+
+
+def test_access_tokens_agree_with_lookup_on_random_hot_sets():
+    rng = random.Random(11)
+    for _ in range(200):
+        seq_len = rng.randint(1, 40)
+        capacity = rng.randint(1, 12)
+        bs = rng.randint(1, 4)
+        blocks = [rng.randint(-1, seq_len // bs + 1) for _ in range(rng.randint(1, 6))]
+        prestate = rng.sample(range(seq_len), min(capacity, seq_len))
+        selected, hits = ref.access_tokens(blocks, bs, seq_len, capacity, prestate)
+        if seq_len <= capacity:
+            resident = set(range(seq_len))
+        else:
+            resident = set(prestate) | {seq_len - 1}
+        width = 48
+        table = [[(p + 1) if p in resident else 0 for p in range(width)]]
+        out, misses, _ = ref.resolve_resident([[blocks]], table, None, [0], [seq_len], [0], bs,
+                                              np.zeros((1, 1, len(blocks) * bs), np.int32),
+                                              with_misses=True)
+        lane_pos = [b * bs + j for b in blocks for j in range(bs)]
+        valid = [i for i in range(len(lane_pos)) if blocks[i // bs] >= 0 and lane_pos[i] < seq_len]
+        assert [lane_pos[i] for i in valid] == selected
+        miss = set(misses[(0, 0)].tolist())
+        assert sorted({lane_pos[i] for i in valid if i not in miss}) == hits
+
+
+def test_lru_replay_reference_kat():
+    """tests/test_hisparse_locality_replay.py:15-24 (windows of 2 steps)."""
+    steps = [[0, 1], [2, 0], [1, 0]]
+    cap2 = ref.lru_misses(steps, 2)
+    cap3 = ref.lru_misses(steps, 3)
+    assert sum(cap2[:2]) == 3 and cap2[2] == 1
+    assert cap3[2] == 0
+
+
+# ------------------------------------------------------------------ gathers
+
+
+def bf16_bits(values):
+    """uint16 bit patterns of small integers as bfloat16 (exact)."""
+    return (np.asarray(values, dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def support_sets(length, selected, seed=137):
+    """Support sets of scripts/analyze_virtual_layout.py:11-27 (stdlib random)."""
+    rng = random.Random(seed)
+    clustered = set()
+    run = max(1, selected // 8)
+    while len(clustered) < selected:
+        begin = rng.randrange(length)
+        for step in range(min(run, selected - len(clustered))):
+            clustered.add((begin + step) % length)
+    return {
+        "contiguous": list(range(selected)),
+        "uniform_random": rng.sample(range(length), selected),
+        "synthetic_clustered": sorted(clustered),
+    }
+
+
+def virtual_addressing_case(batch=3, length=64, width=8, chunk_bytes=256):
+    """Payload and tables of scripts/bench_virtual_addressing.py:43-63 in numpy."""
+    row_bytes = width * 2
+    request_bytes = -(-length * row_bytes // chunk_bytes) * chunk_bytes
+    capacity = chunk_bytes + batch * request_bytes
+    raw = np.zeros(capacity // 2, dtype=np.uint16)
+    for req in range(batch):
+        start = (chunk_bytes + req * request_bytes) // 2
+        raw[start:start + length * width] = bf16_bits((np.arange(length * width) + req * 17) % 97)
+    request_ids = np.arange(batch)[::-1].copy()
+    lengths = np.full(batch, length)
+    count = batch * length
+    table = np.arange(count, 0, -1).reshape(batch, length)
+    flat = np.arange(count)
+    addresses = chunk_bytes // 2 + (flat // length) * (request_bytes // 2) + (flat % length) * width
+    offsets = np.zeros(count + 1, dtype=np.int64)
+    offsets[table.flatten()] = addresses
+    return raw, request_ids, lengths, table, offsets, request_bytes // 2, chunk_bytes // 2
+
+
+@pytest.mark.parametrize("indirect", [False, True])
+@pytest.mark.parametrize("which", ["numpy", "c"])
+def test_gather_rows_reference_closed_form(indirect, which, coracle):
+    batch, length, width, selected = 3, 64, 8, 16
+    raw, request_ids, lengths, table, offsets, request_stride, sink = virtual_addressing_case(
+        batch, length, width)
+    run = ref.gather_rows if which == "numpy" else coracle.gather_rows
+    for name, support in support_sets(length, selected).items():
+        positions = np.broadcast_to(np.array(support), (batch, selected)).copy()
+        expected = bf16_bits((np.clip(positions, 0, None)[..., None] * width + np.arange(width)
+                              + request_ids[:, None, None] * 17) % 97)
+        out = run(raw, positions, request_ids, lengths, table, offsets, width, request_stride, sink, indirect)
+        assert np.array_equal(out, expected), name
+        for invalid in (-1, length):
+            bad = positions.copy()
+            bad[:, 0] = invalid
+            want = expected.copy()
+            want[:, 0] = 0
+            out = run(raw, bad, request_ids, lengths, table, offsets, width, request_stride, sink, indirect)
+            assert np.array_equal(out, want), (name, invalid)
+
+
+def test_support_sets_reproduce_reference_geometry():
+    """results/virtual-addressing-cpu/geometry.json chunk counts (1 / 16 / 8)."""
+    import json
+
+    from conftest import GOLDEN
+    from experimental.virtual_layout import VirtualKVLayout
+
+    geometry = json.loads((GOLDEN / "virtual_addressing_geometry.json").read_text())
+    layout = VirtualKVLayout(1, geometry["length"], geometry["row_elements"],
+                             chunk_bytes=geometry["chunk_bytes"])
+    sets = support_sets(geometry["length"], geometry["selected"])
+    for case in geometry["cases"]:
+        positions = sets[case["pattern"]]
+        assert len(set(positions)) == case["unique_tokens"]
+        assert len(layout.selected_chunks(0, positions)) == case["fixed_position_chunks"]
+    assert len(layout.prefix_chunks(0, geometry["length"])) * geometry["chunk_bytes"] == \
+        geometry["full_request_backing_bytes"]
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_gather_kv_numpy_c_and_closed_form_agree(seed, coracle):
+    rng = np.random.default_rng(100 + seed)
+    layers, kv, rows, row_bytes = 3, 2, 11, 24
+    plane = rows * row_bytes + 8
+    pool_bytes = layers * kv * plane
+    # Closed-form payload: byte j of row (l, v, s) is (31*l + 7*v + 3*s + j) % 251.
+    pool = np.zeros(pool_bytes, dtype=np.uint8)
+    for l in range(layers):
+        for v in range(kv):
+            for s in range(rows):
+                start = (l * kv + v) * plane + s * row_bytes
+                pool[start:start + row_bytes] = (31 * l + 7 * v + 3 * s + np.arange(row_bytes)) % 251
+    slots = rng.integers(-1, rows + 2, size=(layers, 4, 5))
+    a = ref.gather_kv(pool, kv * plane, plane, row_bytes, row_bytes, rows, slots, kv)
+    b = coracle.gather_kv(pool, kv * plane, plane, row_bytes, row_bytes, rows, slots, kv)
+    assert np.array_equal(a, b)
+    for bi in range(4):
+        for l in range(layers):
+            for v in range(kv):
+                for k in range(5):
+                    s = slots[l, bi, k]
+                    want = ((31 * l + 7 * v + 3 * s + np.arange(row_bytes)) % 251 if 1 <= s < rows
+                            else np.zeros(row_bytes))
+                    assert np.array_equal(a[bi, l, v, k], want)
+
+
+def test_scatter_inverts_gather(coracle):
+    rng = np.random.default_rng(7)
+    layers, kv, rows, row_bytes = 2, 2, 40, 16
+    plane = rows * row_bytes
+    pool = rng.integers(0, 256, size=layers * kv * plane, dtype=np.uint8)
+    slots = np.stack([rng.permutation(np.arange(1, rows))[:12].reshape(3, 4) for _ in range(layers)])
+    dense = coracle.gather_kv(pool, kv * plane, plane, row_bytes, row_bytes, rows, slots, kv)
+    cleared = pool.copy()
+    for l in range(layers):
+        for v in range(kv):
+            for s in slots[l].ravel():
+                start = l * kv * plane + v * plane + s * row_bytes
+                cleared[start:start + row_bytes] = 0
+    restored = coracle.scatter_kv(cleared, kv * plane, plane, row_bytes, row_bytes, rows, slots, kv, dense)
+    assert np.array_equal(restored, pool)
