@@ -32,7 +32,7 @@ for entry in (str(ROOT / "elastic-kv-vmm_amd"), str(ROOT)):
 
 METRIC = "sparse KV gather GB/s (% of HBM peak) + Top-K lookups/s at K=2048, 1 GPU"
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = ROOT / "profiles" / "gather_kv_hisparse_decode_hbm_traffic.txt"
+TRAFFIC_FILE = ROOT / "profiles" / "gather_kv_hisparse_decode.md"
 
 
 def log(message):
@@ -140,7 +140,7 @@ def cpu_baseline(torch, args, topk, table, pool_layout, raw, slots, output, budg
     sample_bytes = R * K * 2 * pool_layout.row_bytes + hits * 2 * pool_layout.row_bytes + R * K * 4
     durations = []
     started = time.perf_counter()
-    while not durations or (time.perf_counter() - started < budget_s and len(durations) < 50):
+    while not durations or (time.perf_counter() - started < budget_s and len(durations) < 1000):
         t0 = time.perf_counter()
         s, _, _ = oracle.resolve_resident(topk0, table0, None, rows, lengths, rows, 1, init, with_misses=True)
         oracle.gather_kv(pool0, 2 * plane, plane, pool_layout.row_bytes, pool_layout.row_bytes,
