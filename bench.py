@@ -1,19 +1,27 @@
-"""Benchmark of the sparse-KV decode read path on one MI355X.
+"""Benchmarks of the sparse-KV residency path on one MI355X.
 
-Workload (HiSparse Top-K decode read at one GPU's shard): 128 requests x
-65,536-token context, 60 layers, 2 KV heads x head_dim 128 bf16 (512 B per K
-or V row), Top-K = 2048 per (request, layer) with 80 % of the indices drawn
-from the last 4096 tokens and 20 % uniform over the rest, hot capacity 4096
-slots per request holding the 4096 most recent tokens (a seeded permutation
-of the request's slots). The KV pool is a VMM Backing of 2 MiB chunks.
+Default workload (--workload decode-read), HiSparse Top-K decode read at one
+GPU's shard: 128 requests x 65,536-token context, 60 layers, 2 KV heads x
+head_dim 128 bf16 (512 B per K or V row), Top-K = 2048 per (request, layer)
+with 80 % of the indices from the last 4096 tokens and 20 % uniform over the
+rest, hot capacity 4096 slots per request holding the 4096 most recent tokens
+(a seeded permutation of the request's slots). The KV pool is a VMM Backing of
+2 MiB chunks. One step = resident lookup + miss compaction over all 60 layers
+(one launch) + the Top-K K/V gather of all 60 layers (one launch) into a dense
+[128, 60, 2, 2048, 256] bf16 output. `value` = the gather's algorithmic bytes
+per step (512 B written per row, + 512 B read per resident row, + 4 B slot)
+divided by the measured step time, lookup included.
 
-One step = resident lookup + miss compaction over all 60 layers (one launch)
-followed by the Top-K K/V gather of all 60 layers (one launch) into a dense
-[128, 60, 2, 2048, 256] bf16 output. `value` is the gather's algorithmic
-bytes per step (512 B written per row, plus 512 B read per resident row, plus
-the 4 B slot) divided by the measured step time (lookup included).
+Other workloads (same JSON contract, for the other configurations):
+  topk-gather   8 requests x 8192 context, 28 layers x 8 heads x 128, two-level
+                lookup (req_to_token -> logical -> slot), Top-K 2048 shared by
+                all layers, hot capacity 4096 (~50 % misses)
+  block-gather  64 requests x 256 blocks of 16 tokens, 36 layers x 8 heads x
+                128, block tables from a permutation of a 20k-block pool
+  migration     per tick: 512 scattered 2.25 MiB blocks packed, copied to
+                pinned host and back, unpacked into freshly mapped chunks
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--capacity C]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
 
 import argparse
@@ -32,7 +40,8 @@ for entry in (str(ROOT / "elastic-kv-vmm_amd"), str(ROOT)):
 
 METRIC = "sparse KV gather GB/s (% of HBM peak) + Top-K lookups/s at K=2048, 1 GPU"
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = ROOT / "profiles" / "gather_kv_hisparse_decode.md"
+PCIE_PEAK_GBS = 64.0   # PCIe Gen5 x16, per direction, theoretical
+PROFILES = ROOT / "profiles"
 
 
 def log(message):
@@ -44,24 +53,130 @@ def parse_args():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
-    parser.add_argument("--requests", type=int, default=128)
-    parser.add_argument("--context", type=int, default=65536)
-    parser.add_argument("--layers", type=int, default=60)
-    parser.add_argument("--topk", type=int, default=2048)
-    parser.add_argument("--capacity", type=int, default=4096)
-    parser.add_argument("--recent", type=int, default=4096, help="recency window of the 80 %% share")
+    parser.add_argument("--workload", default="decode-read",
+                        choices=["decode-read", "topk-gather", "block-gather", "migration"])
+    parser.add_argument("--capacity", type=int, default=4096, help="hot slots per request (decode-read)")
     parser.add_argument("--seed", type=int, default=2024)
     parser.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-copy-ceiling", action="store_true")
     return parser.parse_args()
 
 
-def make_inputs(torch, args, device):
-    """Seeded synthetic Top-K indices and hot-slot tables, generated on the device."""
-    L, R, T, K, C, W = args.layers, args.requests, args.context, args.topk, args.capacity, args.recent
-    gen = torch.Generator(device=device).manual_seed(args.seed)
-    recent_count = (K * 4) // 5                     # 1638 of 2048
-    uniform_count = K - recent_count                # 410 of 2048
+# ------------------------------------------------------------------ shared helpers
+
+
+def cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def time_cpu(fn, budget_s):
+    """Median wall time of fn() over repeated runs within the budget."""
+    durations = []
+    started = time.perf_counter()
+    while not durations or (time.perf_counter() - started < budget_s and len(durations) < 1000):
+        t0 = time.perf_counter()
+        fn()
+        durations.append(time.perf_counter() - t0)
+    return statistics.median(durations), len(durations)
+
+
+def time_copy_ceiling(torch, device, nbytes=8 << 30, reps=10):
+    """Device-to-device copy bandwidth (read + write bytes / time) of torch's copy."""
+    src = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    stop.record()
+    stop.synchronize()
+    seconds = start.elapsed_time(stop) / 1000.0 / reps
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2 * nbytes / seconds / 1e9
+
+
+def read_traffic(name):
+    """HBM bytes per launch from a committed rocprof counter summary, if any."""
+    path = PROFILES / name
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def timed_steps(torch, steps, phases):
+    """Run `steps` steps of the given (name, fn) phases; per-phase event times (ms) and wall ms/step."""
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    for step in range(steps):
+        marks = events[step]
+        marks[0].record()
+        for i, (_, fn) in enumerate(phases):
+            fn()
+            marks[i + 1].record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - wall0) * 1e3 / steps
+    per_phase = {name: statistics.mean(events[s][i].elapsed_time(events[s][i + 1]) for s in range(steps))
+                 for i, (name, _) in enumerate(phases)}
+    return wall_ms, per_phase
+
+
+def roofline(achieved_gbs, kernel, algorithmic_bytes, avg_ms, traffic):
+    return {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kernel,
+            "algorithmic_bytes_per_launch": algorithmic_bytes, "avg_launch_ms": round(avg_ms, 4)}
+
+
+def envelope(args, value, step_ms, config, roof, baseline, extra, unit="GB/s", metric=METRIC):
+    result = {
+        "metric": metric, "value": round(value, 2), "unit": unit, "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(step_ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded inputs; bf16 ~N(0,1) or random-byte KV payload)",
+        "config": config, "roofline": roof, "cpu_baseline": baseline,
+    }
+    result.update(extra)
+    return result
+
+
+def make_pool(torch, layout, device, seed):
+    """A fully committed VMM pool of the layout, filled with bf16 ~N(0,1)."""
+    from elastic_kv.backing import Backing
+
+    backing = Backing(layout.capacity_bytes, layout.chunk_bytes, device=device.index or 0)
+    t0 = time.perf_counter()
+    backing.ensure(range(backing.chunk_count))
+    commit_s = time.perf_counter() - t0
+    log(f"committed {backing.chunk_count} chunks ({layout.capacity_bytes / 1e9:.1f} GB) in {commit_s:.2f} s")
+    raw = backing.raw
+    gen = torch.Generator(device=device).manual_seed(seed)
+    for plane in range(layout.planes):
+        raw.narrow(0, plane * layout.plane_stride, layout.plane_bytes).view(torch.bfloat16).normal_(generator=gen)
+    return backing, raw, commit_s
+
+
+# ------------------------------------------------------------------ decode-read (HiSparse Top-K decode)
+
+
+def decode_inputs(torch, device, L, R, T, K, C, W, seed):
+    """Seeded Top-K indices (80 % recent / 20 % uniform) and hot-slot tables, on the device."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    recent_count = (K * 4) // 5
+    uniform_count = K - recent_count
     recent = torch.rand((L, R, W), generator=gen, device=device).argsort(-1)[..., :recent_count]
     recent = (recent + (T - W)).to(torch.int32)
     uniform = torch.rand((L, R, T - W), generator=gen, device=device).topk(uniform_count, dim=-1).indices
@@ -83,134 +198,26 @@ def make_inputs(torch, args, device):
     return topk, table, rows, lengths
 
 
-def time_copy_ceiling(torch, device, nbytes=8 << 30, reps=10):
-    """Device-to-device copy bandwidth (read + write bytes / time)."""
-    src = torch.empty(nbytes, dtype=torch.uint8, device=device)
-    dst = torch.empty_like(src)
-    src.fill_(1)
-    dst.copy_(src)
-    torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
-        dst.copy_(src)
-    stop.record()
-    stop.synchronize()
-    seconds = start.elapsed_time(stop) / 1000.0 / reps
-    del src, dst
-    torch.cuda.empty_cache()
-    return 2 * nbytes / seconds / 1e9
-
-
-def read_traffic():
-    """HBM bytes per gather launch from the committed rocprof counter summary."""
-    if not TRAFFIC_FILE.exists():
-        return None
-    for line in TRAFFIC_FILE.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch:"):
-            return int(float(line.split(":", 1)[1]))
-    return None
-
-
-def cpu_baseline(torch, args, topk, table, pool_layout, raw, slots, output, budget_s):
-    """Time the C oracle (one core) on layer 0 of the same workload; check parity too."""
+def run_decode_read(torch, args, device):
     import numpy as np
-
-    from oracle.oracle import COracle
-
-    oracle = COracle()
-    R, K, T = args.requests, args.topk, args.context
-    topk0 = topk[0:1].cpu().numpy()
-    table0 = table[0].cpu().numpy()
-    rows = np.arange(R)
-    lengths = np.full(R, T)
-    # Layer 0's K and V planes, copied to host.
-    plane = pool_layout.plane_stride
-    pool0 = raw.narrow(0, 0, 2 * plane).cpu().numpy()
-    init = np.zeros((1, R, K), np.int32)
-    want_slots, _, want_counts = oracle.resolve_resident(topk0, table0, None, rows, lengths, rows, 1, init,
-                                                         with_misses=True)
-    parity_lookup = bool(np.array_equal(slots[0:1].cpu().numpy(), want_slots))
-    want_rows = oracle.gather_kv(pool0, 2 * plane, plane, pool_layout.row_bytes, pool_layout.row_bytes,
-                                 pool_layout.rows, want_slots, 2)
-    got_rows = output[:, 0:1].contiguous().view(torch.uint8).reshape(want_rows.shape).cpu().numpy()
-    parity_gather = bool(np.array_equal(got_rows, want_rows))
-    del got_rows
-    hits = int((want_slots > 0).sum())
-    sample_bytes = R * K * 2 * pool_layout.row_bytes + hits * 2 * pool_layout.row_bytes + R * K * 4
-    durations = []
-    started = time.perf_counter()
-    while not durations or (time.perf_counter() - started < budget_s and len(durations) < 1000):
-        t0 = time.perf_counter()
-        s, _, _ = oracle.resolve_resident(topk0, table0, None, rows, lengths, rows, 1, init, with_misses=True)
-        oracle.gather_kv(pool0, 2 * plane, plane, pool_layout.row_bytes, pool_layout.row_bytes,
-                         pool_layout.rows, s, 2)
-        durations.append(time.perf_counter() - t0)
-    median = statistics.median(durations)
-    cpu_model = ""
-    try:
-        for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {
-        "value": round(sample_bytes / median / 1e9, 3),
-        "unit": "GB/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": (f"layer 0 of the same workload ({R} requests x {K} lookups + {2 * R * K} gathered "
-                   f"{pool_layout.row_bytes} B rows, {sample_bytes / 1e6:.1f} MB algorithmic), C oracle "
-                   f"single-threaded, median of {len(durations)} runs ({median * 1e3:.1f} ms each) "
-                   f"on {cpu_model or platform.processor()} ({len(os.sched_getaffinity(0))} cores visible)"),
-        "parity_layer0": {"lookup": parity_lookup, "gather": parity_gather},
-    }
-
-
-def main():
-    args = parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported by this build "
-              "(the path has no cross-GPU step; see the sharding notes)", file=sys.stderr)
-        return 2
-    import torch
 
     from adaptive_sparse.kv_pool import PlanePoolLayout
     from adaptive_sparse.resident_lookup import resolve_resident
     from adaptive_sparse.sparse_read import gather_kv
-    from elastic_kv.backing import Backing
 
-    device = torch.device("cuda:0")
-    torch.cuda.set_device(device)
-    L, R, K, C = args.layers, args.requests, args.topk, args.capacity
+    L, R, T, K, C, W = 60, 128, 65536, 2048, args.capacity, 4096
     row_bytes = 2 * 128 * 2
-    log("measuring device copy ceiling")
-    copy_gbs = time_copy_ceiling(torch, device)
-    log(f"copy ceiling {copy_gbs:.0f} GB/s")
-
     layout = PlanePoolLayout(layers=L, kv=2, rows=1 + R * C, row_bytes=row_bytes)
-    backing = Backing(layout.capacity_bytes, layout.chunk_bytes, device=0)
-    t0 = time.perf_counter()
-    backing.ensure(range(backing.chunk_count))
-    commit_s = time.perf_counter() - t0
-    log(f"committed {backing.chunk_count} chunks ({layout.capacity_bytes / 1e9:.1f} GB) in {commit_s:.2f} s")
-    raw = backing.raw
-    gen = torch.Generator(device=device).manual_seed(args.seed + 1)
-    for plane in range(layout.planes):
-        raw.narrow(0, plane * layout.plane_stride, layout.plane_bytes).view(torch.bfloat16).normal_(generator=gen)
+    backing, raw, commit_s = make_pool(torch, layout, device, args.seed + 1)
     planes = layout.kv_planes(backing.base, 0, owner=backing)
-    topk, table, rows, lengths = make_inputs(torch, args, device)
-    selected = rows
+    topk, table, rows, lengths = decode_inputs(torch, device, L, R, T, K, C, W, args.seed)
     slots = torch.empty((L, R, K), dtype=torch.int32, device=device)
     misses = torch.empty_like(slots)
     counts = torch.empty((L, R), dtype=torch.int32, device=device)
     output = torch.empty((R, L, 2, K, 256), dtype=torch.bfloat16, device=device)
-    torch.cuda.synchronize()
-    log("inputs ready")
 
     def lookup():
-        resolve_resident(topk, table, None, rows, lengths, selected, slots, 1, misses=misses, miss_count=counts)
+        resolve_resident(topk, table, None, rows, lengths, rows, slots, 1, misses=misses, miss_count=counts)
 
     def gather():
         gather_kv(planes, slots, output)
@@ -224,67 +231,345 @@ def main():
     lanes = L * R * K
     lookup_bytes = 12 * lanes + 4 * miss_total + 4 * L * R
     gather_bytes = lanes * 2 * row_bytes + hits * 2 * row_bytes + lanes * 4
-
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    for step in range(args.steps):
-        e0, e1, e2 = events[step]
-        e0.record()
-        lookup()
-        e1.record()
-        gather()
-        e2.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    lookup_ms = [events[i][0].elapsed_time(events[i][1]) for i in range(args.steps)]
-    gather_ms = [events[i][1].elapsed_time(events[i][2]) for i in range(args.steps)]
-    step_ms = wall * 1e3 / args.steps
-    gather_avg_ms = statistics.mean(gather_ms)
-    lookup_avg_ms = statistics.mean(lookup_ms)
-    value = gather_bytes / (step_ms / 1e3) / 1e9
-    achieved = gather_bytes / (gather_avg_ms / 1e3) / 1e9
-    log(f"step {step_ms:.3f} ms, gather {gather_avg_ms:.3f} ms ({achieved:.0f} GB/s), "
-        f"lookup {lookup_avg_ms * 1e3:.1f} us")
+    step_ms, phase = timed_steps(torch, args.steps, [("lookup", lookup), ("gather", gather)])
+    achieved = gather_bytes / (phase["gather"] / 1e3) / 1e9
+    log(f"step {step_ms:.3f} ms, gather {phase['gather']:.3f} ms ({achieved:.0f} GB/s), "
+        f"lookup {phase['lookup'] * 1e3:.1f} us")
 
     baseline = None
     if not args.no_cpu_baseline:
-        log("CPU baseline (C oracle, one core, layer 0) + layer-0 parity")
-        baseline = cpu_baseline(torch, args, topk, table, layout, raw, slots, output, args.cpu_seconds)
-        log(f"cpu baseline {baseline['value']} GB/s, parity {baseline['parity_layer0']}")
+        from oracle.oracle import COracle
 
-    result = {
-        "metric": METRIC,
-        "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(step_ms, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded; bf16 ~N(0,1) KV, Top-K 80% last-4096 / 20% uniform)",
-        "config": {"workload": "hisparse-topk-decode-read", "requests": R, "context": args.context,
-                   "layers": L, "kv_heads": 2, "head_dim": 128, "topk": K, "hot_capacity": C,
-                   "pool_bytes": layout.capacity_bytes, "chunk_bytes": layout.chunk_bytes},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
-                     "kernel": "copy_small_rows<KvGather,16> (ekv_gather_kv)",
-                     "algorithmic_bytes_per_launch": gather_bytes, "avg_launch_ms": round(gather_avg_ms, 4)},
-        "cpu_baseline": baseline,
-        "lookups_per_s": round(lanes / (lookup_avg_ms / 1e3), 1),
-        "lookup_us_per_step": round(lookup_avg_ms * 1e3, 2),
-        "lookup_gbs": round(lookup_bytes / (lookup_avg_ms / 1e3) / 1e9, 1),
-        "hit_rate": round(hits / lanes, 4),
-        "copy_ceiling_gbs": round(copy_gbs, 1),
-        "pool_commit_s": round(commit_s, 3),
-    }
-    print(json.dumps(result), flush=True)
+        oracle = COracle()
+        topk0, table0 = topk[0:1].cpu().numpy(), table[0].cpu().numpy()
+        idx, full = np.arange(R), np.full(R, T)
+        plane = layout.plane_stride
+        pool0 = raw.narrow(0, 0, 2 * plane).cpu().numpy()
+        init = np.zeros((1, R, K), np.int32)
+
+        def sample():
+            s, _, _ = oracle.resolve_resident(topk0, table0, None, idx, full, idx, 1, init, with_misses=True)
+            return s, oracle.gather_kv(pool0, 2 * plane, plane, row_bytes, row_bytes, layout.rows, s, 2)
+
+        want_slots, want_rows = sample()
+        parity = {"lookup": bool(np.array_equal(slots[0:1].cpu().numpy(), want_slots)),
+                  "gather": bool(np.array_equal(
+                      output[:, 0:1].contiguous().view(torch.uint8).reshape(want_rows.shape).cpu().numpy(),
+                      want_rows))}
+        layer_hits = int((want_slots > 0).sum())
+        sample_bytes = R * K * 2 * row_bytes + layer_hits * 2 * row_bytes + R * K * 4
+        median, runs = time_cpu(sample, args.cpu_seconds)
+        baseline = {"value": round(sample_bytes / median / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                    "sample": (f"layer 0 of the same step ({R} x {K} lookups + {2 * R * K} gathered {row_bytes} B "
+                               f"rows, {sample_bytes / 1e6:.1f} MB algorithmic): C oracle on one thread, median of "
+                               f"{runs} runs ({median * 1e3:.1f} ms each), {cpu_model()}, "
+                               f"{len(os.sched_getaffinity(0))} cores visible"),
+                    "parity_layer0": parity}
+        log(f"cpu baseline {baseline['value']} GB/s, parity {parity}")
+
+    config = {"workload": "hisparse-topk-decode-read", "requests": R, "context": T, "layers": L, "kv_heads": 2,
+              "head_dim": 128, "topk": K, "hot_capacity": C, "pool_bytes": layout.capacity_bytes,
+              "chunk_bytes": layout.chunk_bytes}
+    extra = {"lookups_per_s": round(lanes / (phase["lookup"] / 1e3), 1),
+             "lookup_us_per_step": round(phase["lookup"] * 1e3, 2),
+             "lookup_gbs": round(lookup_bytes / (phase["lookup"] / 1e3) / 1e9, 1),
+             "hit_rate": round(hits / lanes, 4), "pool_commit_s": round(commit_s, 3)}
+    roof = roofline(achieved, "copy_small_rows<KvGather,16> (ekv_gather_kv)", gather_bytes, phase["gather"],
+                    read_traffic("gather_kv_hisparse_decode.md"))
+    result = envelope(args, gather_bytes / (step_ms / 1e3) / 1e9, step_ms, config, roof, baseline, extra)
     del raw, output
     torch.cuda.synchronize()
     backing.close()
+    return result
+
+
+# ------------------------------------------------------------------ topk-gather (two-level lookup + shared Top-K)
+
+
+def run_topk_gather(torch, args, device):
+    import numpy as np
+
+    from adaptive_sparse.kv_pool import PlanePoolLayout
+    from adaptive_sparse.resident_lookup import resolve_resident
+    from adaptive_sparse.sparse_read import gather_kv
+
+    R, T, L, K, C = 8, 8192, 28, 2048, 4096
+    row_bytes = 8 * 128 * 2
+    rng = np.random.default_rng(args.seed)
+    table = (np.arange(R * T, dtype=np.int64).reshape(R, T) + 1)       # req_to_token: logical ids
+    mapping = np.zeros(R * T + 1, dtype=np.int64)                       # logical -> global hot slot
+    for r in range(R):
+        resident = rng.choice(T, C, replace=False)
+        mapping[r * T + resident + 1] = r * C + rng.permutation(C) + 1
+    topk = np.stack([rng.choice(T, K, replace=False) for _ in range(R)])[None].astype(np.int32)
+    layout = PlanePoolLayout(layers=L, kv=2, rows=1 + R * C, row_bytes=row_bytes)
+    backing, raw, commit_s = make_pool(torch, layout, device, args.seed + 1)
+    planes = layout.kv_planes(backing.base, 0, owner=backing)
+    t = lambda a, dt: torch.tensor(a, dtype=dt, device=device)  # noqa: E731
+    topk_d, table_d, map_d = t(topk, torch.int32), t(table, torch.int64), t(mapping, torch.int64)
+    rows = torch.arange(R, device=device)
+    lengths = torch.full((R,), T, dtype=torch.int32, device=device)
+    slots = torch.empty((1, R, K), dtype=torch.int32, device=device)
+    misses = torch.empty_like(slots)
+    counts = torch.empty((1, R), dtype=torch.int32, device=device)
+    output = torch.empty((R, L, 2, K, row_bytes // 2), dtype=torch.bfloat16, device=device)
+
+    def lookup():
+        resolve_resident(topk_d, table_d, map_d, rows, lengths, rows, slots, 1, misses=misses, miss_count=counts)
+
+    def gather():
+        gather_kv(planes, slots.expand(L, R, K), output)
+
+    for _ in range(args.warmup):
+        lookup()
+        gather()
+    torch.cuda.synchronize()
+    hits = int((slots > 0).sum().item())
+    lanes = R * K
+    gather_bytes = lanes * L * 2 * row_bytes + hits * L * 2 * row_bytes + lanes * L * 4
+    step_ms, phase = timed_steps(torch, args.steps, [("lookup", lookup), ("gather", gather)])
+    achieved = gather_bytes / (phase["gather"] / 1e3) / 1e9
+    log(f"step {step_ms:.3f} ms, gather {phase['gather']:.3f} ms ({achieved:.0f} GB/s), "
+        f"lookup {phase['lookup'] * 1e3:.1f} us, hit rate {hits / lanes:.3f}")
+    baseline = None
+    if not args.no_cpu_baseline:
+        from oracle.oracle import COracle
+
+        oracle = COracle()
+        pool = raw.cpu().numpy()
+        idx, full = np.arange(R), np.full(R, T)
+        init = np.zeros((1, R, K), np.int32)
+
+        def sample():
+            s, _, _ = oracle.resolve_resident(topk, table, mapping, idx, full, idx, 1, init, with_misses=True)
+            return s, oracle.gather_kv(pool, planes.layer_stride, planes.kv_stride, row_bytes, row_bytes,
+                                       layout.rows, s[0], 2, shared_layers=L)
+
+        want_slots, want_rows = sample()
+        parity = {"lookup": bool(np.array_equal(slots.cpu().numpy(), want_slots)),
+                  "gather": bool(np.array_equal(output.view(torch.uint8).reshape(want_rows.shape).cpu().numpy(),
+                                                want_rows))}
+        del want_rows
+        median, runs = time_cpu(sample, args.cpu_seconds)
+        baseline = {"value": round(gather_bytes / median / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                    "sample": (f"the full step (lookup + {L}-layer gather, {gather_bytes / 1e9:.2f} GB algorithmic): "
+                               f"C oracle on one thread, median of {runs} runs ({median * 1e3:.0f} ms), {cpu_model()}"),
+                    "parity_full": parity}
+        log(f"cpu baseline {baseline['value']} GB/s, parity {parity}")
+    config = {"workload": "resident-lookup-topk-gather", "requests": R, "context": T, "layers": L, "kv_heads": 8,
+              "head_dim": 128, "topk": K, "hot_capacity": C, "lookup": "two-level (req_to_token -> mapping)"}
+    extra = {"lookups_per_s": round(lanes / (phase["lookup"] / 1e3), 1),
+             "lookup_us_per_step": round(phase["lookup"] * 1e3, 2), "hit_rate": round(hits / lanes, 4),
+             "pool_commit_s": round(commit_s, 3)}
+    roof = roofline(achieved, "copy_small_rows<KvGather,16> (ekv_gather_kv)", gather_bytes, phase["gather"], None)
+    result = envelope(args, gather_bytes / (step_ms / 1e3) / 1e9, step_ms, config, roof, baseline, extra)
+    del raw, output
+    torch.cuda.synchronize()
+    backing.close()
+    return result
+
+
+# ------------------------------------------------------------------ block-gather (vLLM-style)
+
+
+def run_block_gather(torch, args, device):
+    import numpy as np
+
+    from adaptive_sparse.kv_pool import PlanePoolLayout
+    from adaptive_sparse.sparse_read import gather_kv
+
+    R, NB, L, POOL = 64, 256, 36, 20000
+    row_bytes = 16 * 8 * 128 * 2                 # one 16-token block of one plane
+    rng = np.random.default_rng(args.seed)
+    tables = rng.permutation(POOL)[: R * NB].reshape(R, NB)
+    layout = PlanePoolLayout(layers=L, kv=2, rows=POOL, row_bytes=row_bytes)
+    backing, raw, commit_s = make_pool(torch, layout, device, args.seed + 1)
+    planes = layout.kv_planes(backing.base, 0, owner=backing)
+    tables_d = torch.tensor(tables, dtype=torch.int32, device=device)
+    output = torch.empty((R, L, 2, NB, row_bytes // 2), dtype=torch.bfloat16, device=device)
+
+    def gather():
+        gather_kv(planes, tables_d.unsqueeze(0).expand(L, R, NB), output, zero_below=0)
+
+    for _ in range(args.warmup):
+        gather()
+    torch.cuda.synchronize()
+    units = R * NB * L * 2
+    gather_bytes = units * 2 * row_bytes + units * 4
+    step_ms, phase = timed_steps(torch, args.steps, [("gather", gather)])
+    achieved = gather_bytes / (phase["gather"] / 1e3) / 1e9
+    log(f"step {step_ms:.3f} ms, gather {phase['gather']:.3f} ms ({achieved:.0f} GB/s)")
+    baseline = None
+    if not args.no_cpu_baseline:
+        from oracle.oracle import COracle
+
+        oracle = COracle()
+        plane = layout.plane_stride
+        pool0 = raw.narrow(0, 0, 2 * plane).cpu().numpy()
+
+        def sample():
+            return oracle.gather_kv(pool0, 2 * plane, plane, row_bytes, row_bytes, POOL, tables[None], 2,
+                                    zero_below=0)
+
+        want = sample()
+        parity = bool(np.array_equal(output[:, 0:1].contiguous().view(torch.uint8).reshape(want.shape).cpu().numpy(),
+                                     want))
+        del want
+        sample_bytes = R * NB * 2 * (2 * row_bytes + 4)
+        median, runs = time_cpu(sample, args.cpu_seconds)
+        baseline = {"value": round(sample_bytes / median / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                    "sample": (f"layer 0 of the same step ({R * NB * 2} block-planes, {sample_bytes / 1e9:.2f} GB "
+                               f"algorithmic): C oracle on one thread, median of {runs} runs "
+                               f"({median * 1e3:.0f} ms), {cpu_model()}"),
+                    "parity_layer0": {"gather": parity}}
+        log(f"cpu baseline {baseline['value']} GB/s, parity {parity}")
+    config = {"workload": "vllm-block-gather", "requests": R, "blocks_per_request": NB, "block_tokens": 16,
+              "layers": L, "kv_heads": 8, "head_dim": 128, "pool_blocks": POOL, "pool_bytes": layout.capacity_bytes}
+    roof = roofline(achieved, "copy_small_rows<KvGather,16> (ekv_gather_kv, 32 KiB rows)", gather_bytes,
+                    phase["gather"], None)
+    result = envelope(args, gather_bytes / (step_ms / 1e3) / 1e9, step_ms, config, roof, baseline,
+                      {"pool_commit_s": round(commit_s, 3)}, metric="block gather GB/s (% of HBM peak), 1 GPU")
+    del raw, output
+    torch.cuda.synchronize()
+    backing.close()
+    return result
+
+
+# ------------------------------------------------------------------ migration (demote/promote round trip)
+
+
+def run_migration(torch, args, device):
+    import numpy as np
+
+    from adaptive_sparse.kv_pool import BlockMajorLayout
+    from adaptive_sparse.migration_engine import MigrationEngine, PagedKVPool
+
+    BLOCKS, LIVE, MOVE = 2048, 1024, 512
+    layout = BlockMajorLayout(blocks=BLOCKS, layers=36, kv=2, row_bytes=16 * 8 * 128 * 2)
+    pool = PagedKVPool(layout, device=device.index or 0)
+    rng = np.random.default_rng(args.seed)
+    live = sorted(rng.choice(np.arange(1, BLOCKS), size=LIVE, replace=False).tolist())
+    pool.allocate(live)
+    gen = torch.Generator(device=device).manual_seed(args.seed)
+    for page in live:
+        pool.page_view(page).view(torch.bfloat16).normal_(generator=gen)
+    engine = MigrationEngine(pool, max_pages=MOVE, sub_batch=64)
+    snapshot = torch.empty((MOVE, layout.block_bytes), dtype=torch.uint8, device=device)
+    moved = 2 * MOVE * layout.block_bytes
+    ticks, verified = [], True
+    phases = {"map_s": [], "move_s": [], "trim_s": []}
+    for tick in range(args.warmup + args.steps):
+        sources = rng.choice(live, size=MOVE, replace=False).tolist()
+        free = sorted(set(range(1, BLOCKS)) - set(live))
+        targets = rng.choice(free, size=MOVE, replace=False).tolist()
+        engine.pack(sources, snapshot)                  # reference copy, outside the timed tick
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        pool.allocate(targets)                          # hipMemMap-commit + zero the destination chunks
+        t1 = time.perf_counter()
+        host = engine.round_trip(sources, targets)      # pack -> D2H -> H2D -> unpack, pipelined
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        pool.release(sources)
+        pool.trim()                                     # unmap chunks only the sources used
+        t3 = time.perf_counter()
+        engine.release_host(host)
+        check = torch.empty_like(snapshot)
+        engine.pack(targets, check)
+        verified &= bool(torch.equal(check, snapshot))
+        del check
+        live = sorted(set(live) - set(sources) | set(targets))
+        if tick >= args.warmup:
+            ticks.append(t3 - t0)
+            phases["map_s"].append(t1 - t0)
+            phases["move_s"].append(t2 - t1)
+            phases["trim_s"].append(t3 - t2)
+    tick_s = statistics.mean(ticks)
+    # Phase breakdown of one non-pipelined move (events per stream).
+    sources = rng.choice(live, size=MOVE, replace=False).tolist()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    engine.pack(sources, engine.out_staging)
+    ev[1].record()
+    engine.host.copy_(engine.out_staging, non_blocking=True)
+    ev[2].record()
+    engine.in_staging.copy_(engine.host, non_blocking=True)
+    ev[3].record()
+    engine.unpack(sources, engine.in_staging)
+    ev[4].record()
+    torch.cuda.synchronize()
+    pack_ms, d2h_ms, h2d_ms, unpack_ms = (ev[i].elapsed_time(ev[i + 1]) for i in range(4))
+    one_way = MOVE * layout.block_bytes
+    pack_bytes = 2 * one_way + MOVE * 4
+    log(f"tick {tick_s * 1e3:.1f} ms ({moved / tick_s / 1e9:.1f} GB/s migrated), pack {pack_ms:.2f} ms, "
+        f"D2H {d2h_ms:.1f} ms, H2D {h2d_ms:.1f} ms, unpack {unpack_ms:.2f} ms, verified {verified}")
+    baseline = None
+    if not args.no_cpu_baseline:
+        from oracle.oracle import COracle
+
+        oracle = COracle()
+        count = 64
+        page_ids = np.array(sorted(rng.choice(live, size=count, replace=False)))
+        host_pool = np.zeros(layout.capacity_bytes, dtype=np.uint8)
+        for p in page_ids:
+            host_pool[p * layout.block_bytes:(p + 1) * layout.block_bytes] = pool.page_view(int(p)).cpu().numpy()
+        slots = np.broadcast_to(page_ids, (layout.layers, 1, count))
+        planes = pool.planes
+
+        def sample():
+            packed = oracle.gather_kv(host_pool, planes.layer_stride, planes.kv_stride, planes.row_stride,
+                                      planes.row_bytes, planes.rows, slots, layout.kv)
+            oracle.scatter_kv(host_pool, planes.layer_stride, planes.kv_stride, planes.row_stride, planes.row_bytes,
+                              planes.rows, slots, layout.kv, packed)
+
+        median, runs = time_cpu(sample, args.cpu_seconds)
+        sample_bytes = 2 * count * layout.block_bytes
+        baseline = {"value": round(sample_bytes / median / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                    "sample": (f"pack + unpack of {count} blocks in host memory (no PCIe leg exists on the CPU path), "
+                               f"C oracle on one thread, median of {runs} runs, {cpu_model()}")}
+    config = {"workload": "page-migration-round-trip", "blocks_per_tick": MOVE, "block_bytes": layout.block_bytes,
+              "layers": 36, "kv_heads": 8, "head_dim": 128, "block_tokens": 16, "pool_blocks": BLOCKS}
+    roof = roofline(pack_bytes / (pack_ms / 1e3) / 1e9, "copy_small_rows<KvGather,16> (pack, 32 KiB rows)",
+                    pack_bytes, pack_ms, None)
+    extra = {"verified_round_trip": verified, "tick_ms": round(tick_s * 1e3, 3),
+             "phase_ms": {"map_and_zero": round(statistics.mean(phases["map_s"]) * 1e3, 3),
+                          "pipelined_move": round(statistics.mean(phases["move_s"]) * 1e3, 3),
+                          "release_and_unmap": round(statistics.mean(phases["trim_s"]) * 1e3, 3),
+                          "pack": round(pack_ms, 3), "d2h": round(d2h_ms, 3), "h2d": round(h2d_ms, 3),
+                          "unpack": round(unpack_ms, 3)},
+             "link_gbs": {"d2h": round(one_way / (d2h_ms / 1e3) / 1e9, 2),
+                          "h2d": round(one_way / (h2d_ms / 1e3) / 1e9, 2), "peak_per_direction": PCIE_PEAK_GBS},
+             "pack_gbs": round(pack_bytes / (pack_ms / 1e3) / 1e9, 1),
+             "unpack_gbs": round(pack_bytes / (unpack_ms / 1e3) / 1e9, 1)}
+    result = envelope(args, moved / tick_s / 1e9, tick_s * 1e3, config, roof, baseline, extra,
+                      metric="migrated GB/s (D2H + H2D bytes per tick / tick time), 1 GPU")
+    pool.close()
+    return result
+
+
+WORKLOADS = {"decode-read": run_decode_read, "topk-gather": run_topk_gather,
+             "block-gather": run_block_gather, "migration": run_migration}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: this path has no "
+              "cross-GPU step in this build (each GPU runs its own shard independently)", file=sys.stderr)
+        return 2
+    import torch
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    copy_gbs = None
+    if not args.no_copy_ceiling:
+        log("measuring device copy ceiling")
+        copy_gbs = time_copy_ceiling(torch, device)
+        log(f"copy ceiling {copy_gbs:.0f} GB/s")
+    result = WORKLOADS[args.workload](torch, args, device)
+    result["copy_ceiling_gbs"] = None if copy_gbs is None else round(copy_gbs, 1)
+    print(json.dumps(result), flush=True)
     return 0
 
 

@@ -1,0 +1,238 @@
+"""Byte movement of page migration: HIP pack/unpack + pinned-host copies.
+
+Replaces the third-party host-copy kernels the reference migrates through
+(adaptive_sparse/migration.py:109-111 backup_from_device_all_layer and
+:232-237 load_to_device_per_layer) with this build's own path:
+
+  demote:  pool pages --pack (ekv_gather_kv)--> device staging
+                      --hipMemcpyAsync D2H (side stream)--> pinned host
+  promote: pinned host --hipMemcpyAsync H2D (side stream)--> device staging
+                      --unpack (ekv_scatter_kv)--> freshly committed pool pages
+
+Pages are moved in sub-batches so that packing, the two PCIe directions and
+unpacking overlap; events order each sub-batch across the three streams. All
+streams have the default priority.
+"""
+
+from dataclasses import dataclass
+
+import torch
+
+from elastic_kv.backing import Backing
+from elastic_kv.slots import FreeSlots
+
+from .kv_pool import BlockMajorLayout
+from .minimax_vmm import PhysicalPages
+from .sparse_read import gather_kv, scatter_kv
+
+
+class PagedKVPool:
+    """Block-major paged KV pool over one VMM Backing with refcounted chunks.
+
+    Page p holds layers x kv plane rows of row_bytes contiguously; page 0 is
+    the permanent sink. `pages` tracks ownership (PhysicalPages with one
+    plane of block_bytes rows), `free` hands out page ids.
+    """
+
+    def __init__(self, layout, device=0, backing_factory=Backing):
+        if not isinstance(layout, BlockMajorLayout):
+            raise TypeError("layout must be a BlockMajorLayout")
+        self.layout = layout
+        self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
+        index = self.device.index or 0
+        self.backing = backing_factory(layout.capacity_bytes, layout.chunk_bytes, index)
+        self.pages = PhysicalPages(self.backing, 1, layout.blocks - 1, [(0, layout.block_bytes)],
+                                   lambda: torch.cuda.synchronize(self.device), chunk_bytes=layout.chunk_bytes)
+        self.free = FreeSlots(layout.blocks - 1)
+        self.planes = layout.kv_planes(self.backing.base, index, owner=self.backing)
+
+    def page_view(self, page):
+        """uint8 view of one page's bytes (its chunks must be mapped)."""
+        return self.backing.raw.narrow(0, page * self.layout.block_bytes, self.layout.block_bytes)
+
+    def allocate(self, pages):
+        """Take specific free page ids and commit their chunks (map + zero)."""
+        ids = sorted(int(p) for p in pages)
+        ranges = []
+        for page in ids:
+            if ranges and ranges[-1][1] == page:
+                ranges[-1] = (ranges[-1][0], page + 1)
+            else:
+                ranges.append((page, page + 1))
+        self.free.remove(ranges)
+        try:
+            self.pages.acquire(ids)
+        except Exception:
+            self.free.release(ids)
+            raise
+
+    def release(self, pages):
+        ids = sorted(int(p) for p in pages)
+        self.pages.release(set(ids))
+        self.free.release(ids)
+
+    def trim(self):
+        """Unmap chunks no page owns; returns the released bytes."""
+        return self.pages.trim_quiescent()
+
+    def close(self):
+        torch.cuda.synchronize(self.device)
+        self.backing.close()
+
+
+@dataclass
+class HostPages:
+    """Rows of the engine's pinned host buffer holding demoted pages, in order."""
+
+    rows: torch.Tensor      # int64 host-buffer rows, one per page
+    pages: tuple            # the source pages, same order
+
+
+class MigrationEngine:
+    """Pack/unpack kernels + pinned host staging for one PagedKVPool."""
+
+    def __init__(self, pool, max_pages, *, sub_batch=64):
+        layout = pool.layout
+        self.pool = pool
+        self.device = pool.device
+        self.block_bytes = layout.block_bytes
+        self.sub_batch = max(1, int(sub_batch))
+        self.max_pages = int(max_pages)
+        self.out_staging = torch.empty((self.max_pages, layout.block_bytes), dtype=torch.uint8, device=self.device)
+        self.in_staging = torch.empty_like(self.out_staging)
+        self.host = torch.empty((self.max_pages, layout.block_bytes), dtype=torch.uint8, pin_memory=True)
+        self.host_free = FreeSlots(self.max_pages)
+        self.d2h = torch.cuda.Stream(self.device)
+        self.h2d = torch.cuda.Stream(self.device)
+
+    # ------------------------------------------------------------ kernels
+
+    def _dense(self, staging, start, count):
+        """(1, L, KV, count, row) view of staging rows [start, start + count)."""
+        layout = self.pool.layout
+        block = staging.narrow(0, start, count).view(count, layout.layers, layout.kv, layout.row_bytes)
+        return block.permute(1, 2, 0, 3).unsqueeze(0)
+
+    def _slots(self, pages):
+        layout = self.pool.layout
+        ids = torch.as_tensor(list(pages), dtype=torch.int64).to(self.device, non_blocking=True)
+        return ids.view(1, 1, -1).expand(layout.layers, 1, len(pages))
+
+    def pack(self, pages, staging, start=0):
+        """staging[start + i] = bytes of page pages[i] (on the current stream)."""
+        if pages:
+            gather_kv(self.pool.planes, self._slots(pages), self._dense(staging, start, len(pages)), zero_below=1)
+
+    def unpack(self, pages, staging, start=0):
+        """Bytes of page pages[i] = staging[start + i] (on the current stream)."""
+        if pages:
+            scatter_kv(self.pool.planes, self._slots(pages), self._dense(staging, start, len(pages)), zero_below=1)
+
+    # ------------------------------------------------------------ host rows
+
+    def reserve_host(self, count):
+        ranges = self.host_free.peek(count)
+        if ranges is None:
+            raise MemoryError("pinned host staging is full")
+        self.host_free.claim(ranges)
+        return torch.tensor([r for a, b in ranges for r in range(a - 1, b - 1)], dtype=torch.int64)
+
+    def release_host(self, host):
+        self.host_free.release(sorted(int(r) + 1 for r in host.rows.tolist()))
+
+    # ------------------------------------------------------------ transfers
+
+    def _host_runs(self, rows):
+        """Contiguous runs (host_start, offset_in_list, length) of host rows."""
+        values = rows.tolist()
+        runs = []
+        for i, row in enumerate(values):
+            if runs and runs[-1][0] + runs[-1][2] == row:
+                runs[-1][2] += 1
+            else:
+                runs.append([row, i, 1])
+        return runs
+
+    def demote(self, pages, host_rows=None):
+        """Copy pages to pinned host rows; returns HostPages when the D2H is queued.
+
+        The pack kernels run on the current stream and the D2H copies on a
+        side stream; call wait() (or synchronize) before reading the host rows.
+        """
+        pages = tuple(int(p) for p in pages)
+        if len(pages) > self.max_pages:
+            raise ValueError("more pages than the staging holds")
+        rows = self.reserve_host(len(pages)) if host_rows is None else host_rows
+        compute = torch.cuda.current_stream(self.device)
+        for start in range(0, len(pages), self.sub_batch):
+            chunk = pages[start:start + self.sub_batch]
+            self.pack(chunk, self.out_staging, start)
+            packed = torch.cuda.Event()
+            packed.record(compute)
+            self.d2h.wait_event(packed)
+            with torch.cuda.stream(self.d2h):
+                self._copy_rows(rows[start:start + len(chunk)], self.out_staging, start, to_host=True)
+        self._done = torch.cuda.Event()
+        self._done.record(self.d2h)
+        return HostPages(rows=rows, pages=pages)
+
+    def promote(self, host, destinations):
+        """Copy demoted pages from pinned host into `destinations` (already allocated)."""
+        destinations = tuple(int(p) for p in destinations)
+        if len(destinations) != len(host.pages):
+            raise ValueError("one destination per demoted page")
+        compute = torch.cuda.current_stream(self.device)
+        ready = torch.cuda.Event()
+        ready.record(compute)
+        self.h2d.wait_event(ready)
+        if getattr(self, "_done", None) is not None:
+            self.h2d.wait_event(self._done)
+        for start in range(0, len(destinations), self.sub_batch):
+            chunk = destinations[start:start + self.sub_batch]
+            with torch.cuda.stream(self.h2d):
+                self._copy_rows(host.rows[start:start + len(chunk)], self.in_staging, start, to_host=False)
+                landed = torch.cuda.Event()
+                landed.record(self.h2d)
+            compute.wait_event(landed)
+            self.unpack(chunk, self.in_staging, start)
+
+    def round_trip(self, pages, destinations):
+        """Demote `pages` and promote them into `destinations`, pipelined per sub-batch."""
+        pages = tuple(int(p) for p in pages)
+        destinations = tuple(int(p) for p in destinations)
+        if len(pages) != len(destinations) or len(pages) > self.max_pages:
+            raise ValueError("pages and destinations must pair up within the staging size")
+        rows = self.reserve_host(len(pages))
+        compute = torch.cuda.current_stream(self.device)
+        for start in range(0, len(pages), self.sub_batch):
+            sources = pages[start:start + self.sub_batch]
+            targets = destinations[start:start + self.sub_batch]
+            span = rows[start:start + len(sources)]
+            self.pack(sources, self.out_staging, start)
+            packed = torch.cuda.Event()
+            packed.record(compute)
+            self.d2h.wait_event(packed)
+            with torch.cuda.stream(self.d2h):
+                self._copy_rows(span, self.out_staging, start, to_host=True)
+                copied = torch.cuda.Event()
+                copied.record(self.d2h)
+            self.h2d.wait_event(copied)
+            with torch.cuda.stream(self.h2d):
+                self._copy_rows(span, self.in_staging, start, to_host=False)
+                landed = torch.cuda.Event()
+                landed.record(self.h2d)
+            compute.wait_event(landed)
+            self.unpack(targets, self.in_staging, start)
+        return HostPages(rows=rows, pages=pages)
+
+    def _copy_rows(self, rows, staging, start, *, to_host):
+        for host_start, offset, length in self._host_runs(rows):
+            device_part = staging.narrow(0, start + offset, length)
+            host_part = self.host.narrow(0, host_start, length)
+            if to_host:
+                host_part.copy_(device_part, non_blocking=True)
+            else:
+                device_part.copy_(host_part, non_blocking=True)
+
+    def wait(self):
+        torch.cuda.synchronize(self.device)

@@ -66,6 +66,7 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(const LookupArgs a) {
     const int64_t req = a.rows[row];
     const int64_t length = a.lengths[row];
     const bool req_ok = req >= 0 && req < a.table_rows;
+    const bool table_ok = req_ok && a.table_cols > 0;  // uniform: the row has at least one entry
     const TopkT* topk = static_cast<const TopkT*>(a.topk) + layer * a.topk_sl + row * a.topk_sb;
     const TableT* table = static_cast<const TableT*>(a.table) + layer * a.table_sl + (req_ok ? req : 0) * a.table_sr;
     int32_t* out = a.out + layer * a.out_sl + row * a.out_sb;
@@ -76,40 +77,46 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(const LookupArgs a) {
 
     for (uint32_t chunk = 0; chunk < a.width; chunk += kChunkLanes) {
         const uint32_t first = chunk + wave * kWaveSpan + lane;
+        // Every load below is unconditional: lanes that must not read use a
+        // clamped in-bounds index and their value is masked afterwards, so
+        // the 8 loads of a phase are all in flight before the first wait.
         int64_t block[kIters];
 #pragma unroll
         for (int i = 0; i < kIters; ++i) {
             const uint32_t o = first + i * 64;
-            block[i] = -1;
-            if (o < a.width) {
-                const uint32_t b = unit_blocks ? o : a.block_div.div(o);
-                block[i] = static_cast<int64_t>(topk[b * a.topk_sk]);
-            }
+            const uint32_t lane_o = o < a.width ? o : a.width - 1;
+            const uint32_t b = unit_blocks ? lane_o : a.block_div.div(lane_o);
+            block[i] = static_cast<int64_t>(topk[b * a.topk_sk]);
         }
         int64_t value[kIters];
         bool hit_path[kIters];  // valid and every index in bounds
 #pragma unroll
         for (int i = 0; i < kIters; ++i) {
             const uint32_t o = first + i * 64;
+            const bool active = o < a.width;
             const uint32_t offset = unit_blocks ? 0u : o - a.block_div.div(o) * a.block_size;
             const int64_t pos = block[i] * a.block_size + offset;
-            const bool valid = o < a.width && block[i] >= 0 && pos < length;
-            hit_path[i] = valid && req_ok && pos < a.table_cols;
-            value[i] = hit_path[i] ? static_cast<int64_t>(table[pos * a.table_sc]) : -1;
+            const bool valid = active && block[i] >= 0 && pos < length;
+            hit_path[i] = valid && table_ok && pos < a.table_cols;
+            const int64_t at = hit_path[i] ? pos : 0;
+            value[i] = table_ok ? static_cast<int64_t>(table[at * a.table_sc]) : 0;
+        }
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+            value[i] = hit_path[i] ? value[i] : -1;
         }
         if constexpr (!std::is_same<MapT, NoMap>::value) {
             const MapT* mapping = static_cast<const MapT*>(a.mapping) + layer * a.map_sl;
+            int64_t mapped[kIters];
 #pragma unroll
             for (int i = 0; i < kIters; ++i) {
-                if (hit_path[i]) {
-                    const int64_t logical = value[i];
-                    if (logical >= 0 && logical < a.map_len) {
-                        value[i] = static_cast<int64_t>(mapping[logical * a.map_s]);
-                    } else {
-                        value[i] = -1;
-                        hit_path[i] = false;
-                    }
-                }
+                hit_path[i] = hit_path[i] && value[i] >= 0 && value[i] < a.map_len;
+                const int64_t at = hit_path[i] ? value[i] : 0;
+                mapped[i] = a.map_len > 0 ? static_cast<int64_t>(mapping[at * a.map_s]) : 0;
+            }
+#pragma unroll
+            for (int i = 0; i < kIters; ++i) {
+                value[i] = hit_path[i] ? mapped[i] : -1;
             }
         }
         uint64_t miss_mask[kIters];

@@ -1,0 +1,123 @@
+"""GPU tests of page migration: pack/unpack through pinned host, transactions.
+
+The round trip is self-pinning: destination pages must hold exactly the
+bytes the source pages held before demotion (the reference's bitwise
+migration check, adaptive_sparse/logical_shadow.py:88-123, compares the same
+way through int16 views). Packing is also checked against the oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from adaptive_sparse.kv_pool import BlockMajorLayout
+from adaptive_sparse.migration import (
+    MigrationCoordinator, MigrationRequest, abort_demote, abort_promote, commit_demote, commit_promote,
+    prepare_demote, prepare_promote,
+)
+from adaptive_sparse.migration_engine import MigrationEngine, PagedKVPool
+
+pytestmark = pytest.mark.gpu
+
+# The migration block of the page-migration workload: 16 tokens x 8 heads x 128 bf16 per plane,
+# 36 layers x K/V planes -> 2.25 MiB per block.
+BLOCK = dict(layers=36, kv=2, row_bytes=16 * 8 * 128 * 2)
+
+
+def fill(pool, pages, seed):
+    gen = torch.Generator(device=pool.device).manual_seed(seed)
+    for page in pages:
+        pool.page_view(page).copy_(torch.randint(0, 256, (pool.layout.block_bytes,), dtype=torch.uint8,
+                                                 device=pool.device, generator=gen))
+
+
+@pytest.mark.parametrize("sub_batch", [5, 64])
+def test_round_trip_is_byte_exact_and_pack_matches_oracle(gpu, coracle, sub_batch):
+    layout = BlockMajorLayout(blocks=48, **BLOCK)
+    pool = PagedKVPool(layout, device=0)
+    try:
+        rng = np.random.default_rng(sub_batch)
+        live = sorted(rng.choice(np.arange(1, 48), size=24, replace=False).tolist())
+        pool.allocate(live)
+        fill(pool, live, 1)
+        sources = rng.choice(live, size=13, replace=False).tolist()
+        free = sorted(set(range(1, 48)) - set(live))
+        targets = rng.choice(free, size=13, replace=False).tolist()
+        before = {p: pool.page_view(p).clone() for p in sources}
+        engine = MigrationEngine(pool, max_pages=16, sub_batch=sub_batch)
+        pool.allocate(targets)
+        host = engine.round_trip(sources, targets)
+        engine.wait()
+        for s, t in zip(sources, targets):
+            assert torch.equal(pool.page_view(t), before[s]), (s, t)
+        # the pinned host rows hold the demoted pages in order
+        for i, s in enumerate(sources):
+            assert torch.equal(engine.host[int(host.rows[i])], before[s].cpu())
+        # pack == oracle gather of the same pool bytes (only mapped pages are copied to the host)
+        raw = np.zeros(layout.capacity_bytes, dtype=np.uint8)
+        for s in sources:
+            raw[s * layout.block_bytes:(s + 1) * layout.block_bytes] = before[s].cpu().numpy()
+        planes = pool.planes
+        want = coracle.gather_kv(raw, planes.layer_stride, planes.kv_stride, planes.row_stride, planes.row_bytes,
+                                 planes.rows, np.array(sources)[None, None, :].repeat(layout.layers, 0), layout.kv)
+        packed = engine.out_staging[:13].view(13, layout.layers, layout.kv, layout.row_bytes).permute(1, 2, 0, 3)
+        assert np.array_equal(packed.unsqueeze(0).cpu().numpy(), want)
+        # demote side releases the sources; chunks only they used are unmapped
+        backed = pool.backing.backed_bytes
+        pool.release(sources)
+        released = pool.trim()
+        assert released > 0 and pool.backing.backed_bytes == backed - released
+        for t in targets:
+            assert torch.equal(pool.page_view(t), before[sources[targets.index(t)]])
+    finally:
+        pool.close()
+
+
+def test_transactions_demote_promote_cycle(gpu):
+    layout = BlockMajorLayout(blocks=64, **BLOCK)
+    pool = PagedKVPool(layout, device=0)
+    try:
+        engine = MigrationEngine(pool, max_pages=32, sub_batch=4)
+        mapping = torch.zeros(100, dtype=torch.int64, device=gpu)
+        pages = list(range(3, 3 + 20))
+        pool.allocate(pages)
+        fill(pool, pages, 7)
+        logical = torch.arange(40, 60, device=gpu)
+        mapping[logical] = torch.tensor(pages, device=gpu)
+        original = {i: pool.page_view(p).clone() for i, p in enumerate(pages)}
+        coordinator = MigrationCoordinator(pool, engine, mapping, keep_pages=6)
+        request = MigrationRequest(row=2, logical=logical)
+        published = []
+        sync = torch.cuda.synchronize
+
+        prepared = prepare_demote(coordinator, request, sync)
+        assert len(prepared.retained_rows) == 6 and len(prepared.released_rows) == 14
+        abort_demote(prepared)
+        with pytest.raises(RuntimeError):
+            abort_demote(prepared)
+        assert engine.host_free.count == 32
+
+        prepared = prepare_demote(coordinator, request, sync)
+        backed = pool.backing.backed_bytes
+        released = commit_demote(prepared, published.append, sync, trim_quiescent=pool.trim)
+        assert published == [2] and prepared.status == "committed"
+        assert (mapping[logical] == 0).all()
+        assert released > 0 and pool.backing.backed_bytes == backed - released
+        assert coordinator.hot[2] == tuple(pages[i] for i in prepared.retained_rows)
+        with pytest.raises(RuntimeError):
+            commit_demote(prepared, published.append, sync)
+
+        promotion = prepare_promote(coordinator, request, sync)
+        abort_promote(promotion)
+        promotion = prepare_promote(coordinator, request, sync, destinations=list(range(40, 60)))
+        grown = commit_promote(promotion, published.append, sync)
+        assert published == [2, 2] and promotion.status == "committed"
+        assert mapping[logical].tolist() == list(range(40, 60))
+        assert grown >= 0 and 2 not in coordinator.host_backed and 2 not in coordinator.hot
+        for i in range(20):
+            assert torch.equal(pool.page_view(40 + i), original[i]), i
+        assert engine.host_free.count == 32
+        with pytest.raises(RuntimeError, match="missing committed host KV"):
+            prepare_promote(coordinator, request, sync)
+    finally:
+        pool.close()
