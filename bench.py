@@ -202,7 +202,7 @@ def run_decode_read(torch, args, device):
     import numpy as np
 
     from adaptive_sparse.kv_pool import PlanePoolLayout
-    from adaptive_sparse.resident_lookup import resolve_resident
+    from adaptive_sparse.resident_lookup import build_residency_bits, resolve_resident
     from adaptive_sparse.sparse_read import gather_kv
 
     L, R, T, K, C, W = 60, 128, 65536, 2048, args.capacity, 4096
@@ -215,13 +215,26 @@ def run_decode_read(torch, args, device):
     misses = torch.empty_like(slots)
     counts = torch.empty((L, R), dtype=torch.int32, device=device)
     output = torch.empty((R, L, 2, K, 256), dtype=torch.bfloat16, device=device)
+    bits = build_residency_bits(table)          # maintained with the table; built once here
+
+    def lookup_plain():
+        resolve_resident(topk, table, None, rows, lengths, rows, slots, 1, misses=misses, miss_count=counts)
 
     def lookup():
-        resolve_resident(topk, table, None, rows, lengths, rows, slots, 1, misses=misses, miss_count=counts)
+        resolve_resident(topk, table, None, rows, lengths, rows, slots, 1, misses=misses, miss_count=counts,
+                         resident_bits=bits)
 
     def gather():
         gather_kv(planes, slots, output)
 
+    lookup_plain()
+    plain = (slots.clone(), misses.clone(), counts.clone())
+    lookup()
+    torch.cuda.synchronize()
+    same = (torch.equal(plain[0], slots) and torch.equal(plain[2], counts)
+            and all(torch.equal(plain[1][l, r, :c], misses[l, r, :c])
+                    for l, r, c in ((0, 0, int(counts[0, 0])), (L - 1, R - 1, int(counts[L - 1, R - 1])))))
+    del plain
     for _ in range(args.warmup):
         lookup()
         gather()
@@ -232,9 +245,13 @@ def run_decode_read(torch, args, device):
     lookup_bytes = 12 * lanes + 4 * miss_total + 4 * L * R
     gather_bytes = lanes * 2 * row_bytes + hits * 2 * row_bytes + lanes * 4
     step_ms, phase = timed_steps(torch, args.steps, [("lookup", lookup), ("gather", gather)])
+    _, plain_phase = timed_steps(torch, max(3, args.steps // 2), [("lookup", lookup_plain)])
+    lookup()
+    torch.cuda.synchronize()
     achieved = gather_bytes / (phase["gather"] / 1e3) / 1e9
     log(f"step {step_ms:.3f} ms, gather {phase['gather']:.3f} ms ({achieved:.0f} GB/s), "
-        f"lookup {phase['lookup'] * 1e3:.1f} us")
+        f"lookup {phase['lookup'] * 1e3:.1f} us with the residency bitmap "
+        f"({plain_phase['lookup'] * 1e3:.1f} us without), identical results {same}")
 
     baseline = None
     if not args.no_cpu_baseline:
@@ -272,7 +289,10 @@ def run_decode_read(torch, args, device):
               "chunk_bytes": layout.chunk_bytes}
     extra = {"lookups_per_s": round(lanes / (phase["lookup"] / 1e3), 1),
              "lookup_us_per_step": round(phase["lookup"] * 1e3, 2),
+             "lookup_us_per_layer": round(phase["lookup"] * 1e3 / L, 2),
              "lookup_gbs": round(lookup_bytes / (phase["lookup"] / 1e3) / 1e9, 1),
+             "lookup_us_without_bitmap": round(plain_phase["lookup"] * 1e3, 2),
+             "lookup_bitmap_matches_plain": same,
              "hit_rate": round(hits / lanes, 4), "pool_commit_s": round(commit_s, 3)}
     roof = roofline(achieved, "copy_small_rows<KvGather,16> (ekv_gather_kv)", gather_bytes, phase["gather"],
                     read_traffic("gather_kv_hisparse_decode.md"))

@@ -11,7 +11,9 @@ Extensions (all optional, none changes the reference behaviour):
     resident) in ascending lane order, and their number;
   * mapping=None: single-level lookup, the table value is the slot itself;
   * a leading layer dimension L on topk / output (table and mapping may then
-    carry it too), so all layers of a decode step resolve in one launch.
+    carry it too), so all layers of a decode step resolve in one launch;
+  * resident_bits (single level only): a residency bitmap built by
+    build_residency_bits; non-resident lanes then skip their table read.
 """
 
 import ctypes as ct
@@ -22,7 +24,7 @@ from elastic_kv import _native
 
 
 def resolve_resident(topk, table, mapping, rows, lengths, selected, output, block_size, *,
-                     misses=None, miss_count=None):
+                     misses=None, miss_count=None, resident_bits=None):
     """Write only selected rows into an existing [L, B, K * block_size] tensor.
 
     For selected row r, layer l and lane o: block = topk[l, r, o // bs],
@@ -36,7 +38,11 @@ def resolve_resident(topk, table, mapping, rows, lengths, selected, output, bloc
         return
     if (misses is None) != (miss_count is None):
         raise ValueError("misses and miss_count must be given together")
+    if resident_bits is not None and mapping is not None:
+        raise ValueError("resident_bits needs the single-level form (mapping=None)")
     tensors = [topk, table, rows, lengths, selected, output]
+    if resident_bits is not None:
+        tensors.append(resident_bits)
     if mapping is not None:
         tensors.append(mapping)
     if misses is not None:
@@ -46,12 +52,35 @@ def resolve_resident(topk, table, mapping, rows, lengths, selected, output, bloc
     views = [_native.describe(t, name) for t, name in (
         (topk, "topk"), (table, "table"), (rows, "rows"), (lengths, "lengths"),
         (selected, "selected"), (output, "output"))]
-    mapping_view = ct.byref(_native.describe(mapping, "mapping")) if mapping is not None else None
+    if resident_bits is not None:
+        entry, mapping_view = lib.ekv_resolve_resident_bits, ct.byref(_native.describe(resident_bits, "bits"))
+    else:
+        entry = lib.ekv_resolve_resident
+        mapping_view = ct.byref(_native.describe(mapping, "mapping")) if mapping is not None else None
     miss_view = ct.byref(_native.describe(misses, "misses")) if misses is not None else None
     count_view = ct.byref(_native.describe(miss_count, "miss_count")) if miss_count is not None else None
     with torch.cuda.device(device):
-        status = lib.ekv_resolve_resident(
+        status = entry(
             ct.byref(views[0]), ct.byref(views[1]), mapping_view, ct.byref(views[2]),
             ct.byref(views[3]), ct.byref(views[4]), ct.byref(views[5]), miss_view, count_view,
             int(block_size), _native.stream_handle(device))
     _native.check(lib, status, "resolve_resident")
+
+
+def build_residency_bits(table, out=None):
+    """Residency bitmap of a single-level table: bit p of row q = table[.., q, p] != 0.
+
+    Returns an int32 tensor [.., R, ceil(T / 32)] (or fills `out`).
+    """
+    if table.dim() not in (2, 3):
+        raise ValueError("table must be [R, T] or [L, R, T]")
+    words = (table.shape[-1] + 31) // 32
+    if out is None:
+        out = torch.empty((*table.shape[:-1], words), dtype=torch.int32, device=table.device)
+    device = _native.device_of(table, out)
+    lib = _native.kernel_library()
+    table_view, out_view = _native.describe(table, "table"), _native.describe(out, "resident_bits")
+    with torch.cuda.device(device):
+        status = lib.ekv_residency_bits(ct.byref(table_view), ct.byref(out_view), _native.stream_handle(device))
+    _native.check(lib, status, "build_residency_bits")
+    return out

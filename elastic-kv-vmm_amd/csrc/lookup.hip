@@ -29,6 +29,7 @@ constexpr int kWaveSpan = 64 * kIters;         // 512 lanes per wave per chunk
 constexpr int kChunkLanes = kThreads * kIters; // 2048 lanes per chunk
 
 struct NoMap {};
+struct Bits {};   // single level, with a residency bitmap in front of the table
 
 struct LookupArgs {
     const void* topk;
@@ -37,6 +38,8 @@ struct LookupArgs {
     int64_t table_sl, table_sr, table_sc, table_rows, table_cols;
     const void* mapping;
     int64_t map_sl, map_s, map_len;
+    const int32_t* bits;                 // [L?, R, W] words, bit p of a row = table[row, p] != 0
+    int64_t bits_sl, bits_sr, bits_sw;
     IndexRef rows, lengths, selected;
     int32_t* out;
     int64_t out_sl, out_sb, out_so;
@@ -89,6 +92,7 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(const LookupArgs a) {
             block[i] = static_cast<int64_t>(topk[b * a.topk_sk]);
         }
         int64_t value[kIters];
+        int64_t position[kIters];
         bool hit_path[kIters];  // valid and every index in bounds
 #pragma unroll
         for (int i = 0; i < kIters; ++i) {
@@ -98,14 +102,39 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(const LookupArgs a) {
             const int64_t pos = block[i] * a.block_size + offset;
             const bool valid = active && block[i] >= 0 && pos < length;
             hit_path[i] = valid && table_ok && pos < a.table_cols;
-            const int64_t at = hit_path[i] ? pos : 0;
-            value[i] = table_ok ? static_cast<int64_t>(table[at * a.table_sc]) : 0;
+            position[i] = hit_path[i] ? pos : 0;
+        }
+        bool resident[kIters];
+        if constexpr (std::is_same<MapT, Bits>::value) {
+            // A non-resident lane skips its table entry: it re-reads entry 0 of
+            // the row, which every such lane shares (one cached line), so
+            // misses cost 1 bit of HBM instead of a 128 B line.
+            const int32_t* bits_row = a.bits + layer * a.bits_sl + (req_ok ? req : 0) * a.bits_sr;
+            uint32_t word[kIters];
+#pragma unroll
+            for (int i = 0; i < kIters; ++i) {
+                word[i] = table_ok ? static_cast<uint32_t>(bits_row[(position[i] >> 5) * a.bits_sw]) : 0u;
+            }
+#pragma unroll
+            for (int i = 0; i < kIters; ++i) {
+                resident[i] = hit_path[i] && ((word[i] >> (position[i] & 31)) & 1u);
+                position[i] = resident[i] ? position[i] : 0;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kIters; ++i) {
+                resident[i] = true;
+            }
         }
 #pragma unroll
         for (int i = 0; i < kIters; ++i) {
-            value[i] = hit_path[i] ? value[i] : -1;
+            value[i] = table_ok ? static_cast<int64_t>(table[position[i] * a.table_sc]) : 0;
         }
-        if constexpr (!std::is_same<MapT, NoMap>::value) {
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+            value[i] = hit_path[i] ? (resident[i] ? value[i] : 0) : -1;
+        }
+        if constexpr (!std::is_same<MapT, NoMap>::value && !std::is_same<MapT, Bits>::value) {
             const MapT* mapping = static_cast<const MapT*>(a.mapping) + layer * a.map_sl;
             int64_t mapped[kIters];
 #pragma unroll
@@ -179,7 +208,9 @@ void launch_typed(const LookupArgs& a, bool compact, dim3 grid, hipStream_t stre
 
 template <typename TopkT, typename TableT>
 void launch_map(const LookupArgs& a, int32_t map_dtype, bool compact, dim3 grid, hipStream_t stream) {
-    if (a.mapping == nullptr) {
+    if (a.bits != nullptr) {
+        launch_typed<TopkT, TableT, Bits>(a, compact, grid, stream);
+    } else if (a.mapping == nullptr) {
         launch_typed<TopkT, TableT, NoMap>(a, compact, grid, stream);
     } else if (map_dtype == EKV_INT64) {
         launch_typed<TopkT, TableT, int64_t>(a, compact, grid, stream);
@@ -201,7 +232,7 @@ void launch_table(const LookupArgs& a, int32_t table_dtype, int32_t map_dtype, b
 int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const ekv_tensor* mapping_p,
                      const ekv_tensor* rows_p, const ekv_tensor* lengths_p, const ekv_tensor* selected_p,
                      const ekv_tensor* output_p, const ekv_tensor* misses_p, const ekv_tensor* counts_p,
-                     int64_t block_size, void* stream) {
+                     const ekv_tensor* bits_p, int64_t block_size, void* stream) {
     const ekv_tensor& topk = need(topk_p, "topk");
     const ekv_tensor& table = need(table_p, "table");
     const ekv_tensor& rows = need(rows_p, "rows");
@@ -247,6 +278,24 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
         } else if (mapping->ndim != 1) {
             throw std::invalid_argument("mapping must be [N] or [L, N]");
         }
+    }
+    if (bits_p != nullptr) {
+        const ekv_tensor& bits = need(bits_p, "resident_bits");
+        if (mapping_p != nullptr) {
+            throw std::invalid_argument("resident_bits needs the single-level form (mapping = NULL)");
+        }
+        if (bits.dtype != EKV_INT32 || bits.ndim != table.ndim) {
+            throw std::invalid_argument("resident_bits must be int32 with the table's number of dimensions");
+        }
+        if (layered_table) {
+            need_dim(bits, 0, layers, "resident_bits");
+        }
+        const int d = layered_table ? 1 : 0;
+        need_dim(bits, d, table.shape[d], "resident_bits");
+        if (bits.shape[d + 1] < (table.shape[d + 1] + 31) / 32) {
+            throw std::invalid_argument("resident_bits needs ceil(T / 32) words per row");
+        }
+        need_data(bits, "resident_bits");
     }
     if ((misses_p == nullptr) != (counts_p == nullptr)) {
         throw std::invalid_argument("misses and miss_count must be given together");
@@ -302,6 +351,13 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
         a.map_s = mapping->stride[mapping->ndim - 1];
         a.map_len = mapping->shape[mapping->ndim - 1];
     }
+    if (bits_p != nullptr) {
+        const int d = layered_table ? 1 : 0;
+        a.bits = static_cast<const int32_t*>(bits_p->data);
+        a.bits_sl = layered_table ? bits_p->stride[0] : 0;
+        a.bits_sr = bits_p->stride[d];
+        a.bits_sw = bits_p->stride[d + 1];
+    }
     a.rows = index_ref(rows, 0);
     a.lengths = index_ref(lengths, 0);
     a.selected = index_ref(selected, 0);
@@ -341,8 +397,100 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
     return 0;
 }
 
+// One wave turns 64 consecutive table entries into two bitmap words with a
+// ballot; a grid-stride loop covers every (layer, row, 64-entry group).
+template <typename TableT>
+__global__ __launch_bounds__(kThreads) void residency_bits_kernel(const TableT* __restrict__ table, int64_t t_sl,
+                                                                  int64_t t_sr, int64_t t_sc, int64_t rows,
+                                                                  int64_t cols, int32_t* __restrict__ bits,
+                                                                  int64_t b_sl, int64_t b_sr, int64_t b_sw,
+                                                                  int64_t groups_per_row, int64_t total_groups) {
+    const int lane = threadIdx.x & 63;
+    const int64_t waves = int64_t{gridDim.x} * (kThreads / 64);
+    for (int64_t g = int64_t{blockIdx.x} * (kThreads / 64) + (threadIdx.x >> 6); g < total_groups; g += waves) {
+        const int64_t group = g % groups_per_row;
+        const int64_t row_index = g / groups_per_row;   // layer * rows + row
+        const int64_t layer = row_index / rows;
+        const int64_t row = row_index - layer * rows;
+        const int64_t pos = group * 64 + lane;
+        const bool in_row = pos < cols;
+        const int64_t at = in_row ? pos : 0;
+        const bool set = in_row && table[layer * t_sl + row * t_sr + at * t_sc] != 0;
+        const uint64_t mask = __ballot(set);
+        int32_t* out = bits + layer * b_sl + row * b_sr;
+        const int64_t word = group * 2;
+        if (lane == 0) {
+            out[word * b_sw] = static_cast<int32_t>(static_cast<uint32_t>(mask));
+        } else if (lane == 1 && group * 64 + 32 < cols) {
+            out[(word + 1) * b_sw] = static_cast<int32_t>(static_cast<uint32_t>(mask >> 32));
+        }
+    }
+}
+
+int residency_bits(const ekv_tensor* table_p, const ekv_tensor* bits_p, void* stream) {
+    const ekv_tensor& table = need(table_p, "table");
+    const ekv_tensor& bits = need(bits_p, "resident_bits");
+    need_index(table, "table");
+    if (table.ndim != 2 && table.ndim != 3) {
+        throw std::invalid_argument("table must be [R, T] or [L, R, T]");
+    }
+    if (bits.dtype != EKV_INT32 || bits.ndim != table.ndim) {
+        throw std::invalid_argument("resident_bits must be int32 with the table's number of dimensions");
+    }
+    const bool layered = table.ndim == 3;
+    const int d = layered ? 1 : 0;
+    const int64_t layers = layered ? table.shape[0] : 1;
+    if (layered) {
+        need_dim(bits, 0, layers, "resident_bits");
+    }
+    need_dim(bits, d, table.shape[d], "resident_bits");
+    const int64_t rows = table.shape[d], cols = table.shape[d + 1];
+    if (bits.shape[d + 1] < (cols + 31) / 32) {
+        throw std::invalid_argument("resident_bits needs ceil(T / 32) words per row");
+    }
+    const int64_t groups_per_row = (cols + 63) / 64;
+    const int64_t total = layers * rows * groups_per_row;
+    if (total == 0) {
+        return 0;
+    }
+    need_data(table, "table");
+    need_data(bits, "resident_bits");
+    const int64_t blocks = std::min<int64_t>((total + 3) / 4, 65536);
+    const auto s = static_cast<hipStream_t>(stream);
+    const int64_t t_sl = layered ? table.stride[0] : 0, b_sl = layered ? bits.stride[0] : 0;
+    if (table.dtype == EKV_INT64) {
+        residency_bits_kernel<int64_t><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, s>>>(
+            static_cast<const int64_t*>(table.data), t_sl, table.stride[d], table.stride[d + 1], rows, cols,
+            static_cast<int32_t*>(bits.data), b_sl, bits.stride[d], bits.stride[d + 1], groups_per_row, total);
+    } else {
+        residency_bits_kernel<int32_t><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, s>>>(
+            static_cast<const int32_t*>(table.data), t_sl, table.stride[d], table.stride[d + 1], rows, cols,
+            static_cast<int32_t*>(bits.data), b_sl, bits.stride[d], bits.stride[d + 1], groups_per_row, total);
+    }
+    check_hip(hipGetLastError(), "launch residency bits");
+    return 0;
+}
+
 }  // namespace
 }  // namespace ekv
+
+extern "C" int ekv_resolve_resident_bits(const ekv_tensor* topk, const ekv_tensor* table,
+                                         const ekv_tensor* resident_bits, const ekv_tensor* rows,
+                                         const ekv_tensor* lengths, const ekv_tensor* selected,
+                                         const ekv_tensor* output, const ekv_tensor* misses,
+                                         const ekv_tensor* miss_count, int64_t block_size, void* stream) {
+    return ekv::guarded(-1, [&] {
+        if (resident_bits == nullptr) {
+            throw std::invalid_argument("resident_bits is required");
+        }
+        return ekv::resolve_resident(topk, table, nullptr, rows, lengths, selected, output, misses, miss_count,
+                                     resident_bits, block_size, stream);
+    });
+}
+
+extern "C" int ekv_residency_bits(const ekv_tensor* table, const ekv_tensor* resident_bits, void* stream) {
+    return ekv::guarded(-1, [&] { return ekv::residency_bits(table, resident_bits, stream); });
+}
 
 extern "C" int ekv_resolve_resident(const ekv_tensor* topk, const ekv_tensor* table, const ekv_tensor* mapping,
                                     const ekv_tensor* rows, const ekv_tensor* lengths,
@@ -351,7 +499,7 @@ extern "C" int ekv_resolve_resident(const ekv_tensor* topk, const ekv_tensor* ta
                                     int64_t block_size, void* stream) {
     return ekv::guarded(-1, [&] {
         return ekv::resolve_resident(topk, table, mapping, rows, lengths, selected, output, misses, miss_count,
-                                     block_size, stream);
+                                     nullptr, block_size, stream);
     });
 }
 

@@ -98,6 +98,31 @@ int ekv_resolve_resident(const ekv_tensor* topk, const ekv_tensor* table,
                          void* stream);
 
 /*
+ * Single-level resident lookup with a residency bitmap in front of the table.
+ * Same contract as ekv_resolve_resident with mapping = NULL; resident_bits
+ * [R, W] or [L, R, W] int32 (W >= ceil(T/32)) must hold bit p of row q set
+ * exactly when table[q, p] != 0 (ekv_residency_bits builds it). Lanes whose
+ * bit is clear return slot 0 without reading their table entry, so random
+ * misses cost one bit of bandwidth instead of a cache line.
+ * No reference counterpart: an acceleration of ekv_resolve_resident
+ * (adaptive_sparse/resident_lookup.py:29-40 semantics are unchanged).
+ */
+int ekv_resolve_resident_bits(const ekv_tensor* topk, const ekv_tensor* table,
+                              const ekv_tensor* resident_bits, const ekv_tensor* rows,
+                              const ekv_tensor* lengths, const ekv_tensor* selected,
+                              const ekv_tensor* output, const ekv_tensor* misses,
+                              const ekv_tensor* miss_count, int64_t block_size,
+                              void* stream);
+
+/*
+ * resident_bits[.., q, w] bit j = (table[.., q, 32w + j] != 0) for every
+ * position of the table; bits past T in the last word are 0.
+ * No reference counterpart (maintenance of the bitmap above).
+ */
+int ekv_residency_bits(const ekv_tensor* table, const ekv_tensor* resident_bits,
+                       void* stream);
+
+/*
  * Row gather over a fixed-position virtual layout.
  * Replaces: experimental/sparse_read.py:33-51 (gather_rows) and its kernel
  * :11-30.

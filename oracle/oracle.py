@@ -83,6 +83,18 @@ def resolve_resident(topk, table, mapping, rows, lengths, selected, block_size, 
     return out, misses, counts
 
 
+def residency_bits(table):
+    """int32 words of a residency bitmap: bit j of word w of a row = table[.., 32w + j] != 0."""
+    table = np.asarray(table)
+    resident = table != 0
+    words = -(-table.shape[-1] // 32)
+    pad = words * 32 - table.shape[-1]
+    resident = np.concatenate([resident, np.zeros((*table.shape[:-1], pad), bool)], axis=-1)
+    weights = (np.uint64(1) << np.arange(32, dtype=np.uint64))
+    packed = (resident.reshape(*table.shape[:-1], words, 32).astype(np.uint64) * weights).sum(-1)
+    return packed.astype(np.uint32).view(np.int32)
+
+
 def access_tokens(blocks, block_size, seq_len, hot_capacity, prestate):
     """Selected tokens and sorted hit tokens of one HiSparse swap-in.
 

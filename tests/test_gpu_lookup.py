@@ -135,3 +135,44 @@ def test_shape_errors_raise(gpu):
     with pytest.raises(RuntimeError, match="int32"):
         resolve_resident(topk, table, None, rows, lengths, rows,
                          torch.zeros((1, 2, 8), dtype=torch.int64, device=gpu), 2)
+
+
+@pytest.mark.parametrize("layered", [False, True])
+@pytest.mark.parametrize("bs", [1, 3])
+def test_bitmap_lookup_equals_plain_lookup_and_oracle(gpu, coracle, layered, bs):
+    from adaptive_sparse.resident_lookup import build_residency_bits
+    from oracle import oracle as ref
+
+    rng = np.random.default_rng(77 + bs + 10 * layered)
+    layers, batch, k, rrows, cols = 2, 5, 300, 6, 1000
+    topk = rng.integers(-1, cols // bs + 2, size=(layers, batch, k))
+    rows = rng.integers(0, rrows, size=batch)
+    lengths = rng.integers(0, cols + 3, size=batch)
+    table = rng.integers(1, 1 << 20, size=(layers, rrows, cols) if layered else (rrows, cols))
+    table[rng.random(table.shape) < 0.6] = 0
+    selected = np.arange(batch)
+    t = lambda a, dt: torch.tensor(a, dtype=dt, device=gpu)  # noqa: E731
+    table_d = t(table, torch.int32)
+    bits = build_residency_bits(table_d)
+    assert np.array_equal(bits.cpu().numpy(), ref.residency_bits(table))
+    width = k * bs
+    outs = []
+    for use_bits in (False, True):
+        out = torch.full((layers, batch, width), -7, dtype=torch.int32, device=gpu)
+        misses = torch.full_like(out, -5)
+        counts = torch.zeros((layers, batch), dtype=torch.int32, device=gpu)
+        resolve_resident(t(topk, torch.int32), table_d, None, t(rows, torch.int64), t(lengths, torch.int32),
+                         t(selected, torch.int64), out, bs, misses=misses, miss_count=counts,
+                         resident_bits=bits if use_bits else None)
+        outs.append((out.cpu().numpy(), misses.cpu().numpy(), counts.cpu().numpy()))
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert np.array_equal(outs[0][2], outs[1][2])
+    want, want_misses, want_counts = coracle.resolve_resident(topk, table, None, rows, lengths, selected, bs,
+                                                              np.full((layers, batch, width), -7, np.int32),
+                                                              with_misses=True)
+    assert np.array_equal(outs[1][0], want)
+    assert np.array_equal(outs[1][2], want_counts)
+    for layer in range(layers):
+        for row in range(batch):
+            c = want_counts[layer, row]
+            assert np.array_equal(outs[1][1][layer, row, :c], want_misses[layer, row, :c])

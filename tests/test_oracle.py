@@ -322,3 +322,13 @@ def test_scatter_inverts_gather(coracle):
                 cleared[start:start + row_bytes] = 0
     restored = coracle.scatter_kv(cleared, kv * plane, plane, row_bytes, row_bytes, rows, slots, kv, dense)
     assert np.array_equal(restored, pool)
+
+
+def test_residency_bits_little_endian_words():
+    table = np.zeros((2, 70), np.int64)
+    table[0, [0, 31, 32, 69]] = [5, 6, 7, 8]
+    table[1, 33] = -1
+    words = ref.residency_bits(table).view(np.uint32)
+    assert words.shape == (2, 3)
+    assert words[0].tolist() == [1 | (1 << 31), 1, 1 << 5]
+    assert words[1].tolist() == [0, 1 << 1, 0]
