@@ -8,17 +8,28 @@
 // Launch shape: one 256-thread workgroup (4 waves) per (selected row, layer).
 // A row of `width` lanes is walked in chunks of 2048 lanes; wave w owns lanes
 // [512w, 512w + 512) of a chunk and processes them as 8 iterations of 64
-// consecutive lanes, so a wave's lane order is the row's lane order. All 8
-// Top-K loads of a lane are issued before its 8 table loads, which are issued
-// before any dependent mapping load, to keep many independent loads in flight.
+// consecutive lanes, so a wave's lane order is the row's lane order.
+// Every global load is unconditional (lanes that must not read use a clamped,
+// in-bounds index and their value is masked afterwards), so the 8 loads of a
+// phase are in flight together instead of waiting after each one.
 // Miss compaction: each iteration's misses form a 64-bit ballot; a lane's rank
 // in the miss list is (misses of lower waves in this chunk) + (misses of
 // earlier iterations of its wave) + mbcnt(ballot). One LDS exchange of the 4
 // wave totals per chunk; no atomics, so the list order is deterministic.
+//
+// Two kernels share this structure:
+//   resolve_single_kernel - single level (the table value is the slot), with
+//     an optional residency bitmap staged in LDS: lanes whose bit is clear are
+//     misses without touching their table entry;
+//   resolve_mapped_kernel - two levels (table -> logical id -> mapping -> slot),
+//     the reference's form.
 #include "../../include/ekv_kernels.h"
 #include "ekv_common.h"
 #include "ekv_fastdiv.h"
 #include "ekv_tensor_util.h"
+
+#include <algorithm>
+#include <type_traits>
 
 namespace ekv {
 namespace {
@@ -27,9 +38,9 @@ constexpr int kThreads = 256;
 constexpr int kIters = 8;                      // 64-lane iterations per wave per chunk
 constexpr int kWaveSpan = 64 * kIters;         // 512 lanes per wave per chunk
 constexpr int kChunkLanes = kThreads * kIters; // 2048 lanes per chunk
-
-struct NoMap {};
-struct Bits {};   // single level, with a residency bitmap in front of the table
+// Bitmap rows up to this many 32-bit words (T <= 131072 tokens) are staged in
+// LDS with coalesced loads; the per-lane bit tests are then LDS reads.
+constexpr int kStagedBitWords = 4096;
 
 struct LookupArgs {
     const void* topk;
@@ -40,6 +51,7 @@ struct LookupArgs {
     int64_t map_sl, map_s, map_len;
     const int32_t* bits;                 // [L?, R, W] words, bit p of a row = table[row, p] != 0
     int64_t bits_sl, bits_sr, bits_sw;
+    int64_t bits_words;                  // words covering the table row: ceil(table_cols / 32)
     IndexRef rows, lengths, selected;
     int32_t* out;
     int64_t out_sl, out_sb, out_so;
@@ -58,9 +70,89 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
 }
 
-template <typename TopkT, typename TableT, typename MapT, bool kCompact>
-__global__ __launch_bounds__(kThreads) void resolve_kernel(const LookupArgs a) {
+// Top-K block ids of the 8 lanes of this thread in the current chunk.
+template <typename TopkT>
+__device__ __forceinline__ void load_blocks(const LookupArgs& a, const TopkT* topk, uint32_t first,
+                                            int64_t (&block)[kIters]) {
+    const bool unit_blocks = a.block_size == 1;
+#pragma unroll
+    for (int i = 0; i < kIters; ++i) {
+        const uint32_t o = first + i * 64;
+        const uint32_t lane_o = o < a.width ? o : a.width - 1;
+        const uint32_t b = unit_blocks ? lane_o : a.block_div.div(lane_o);
+        block[i] = static_cast<int64_t>(topk[b * a.topk_sk]);
+    }
+}
+
+// Token position of each lane and whether it is valid and inside the table
+// (valid = block >= 0 && pos < length, as in the reference, plus bounds).
+__device__ __forceinline__ void lane_positions(const LookupArgs& a, uint32_t first, const int64_t (&block)[kIters],
+                                               int64_t bound, bool table_ok, int64_t (&pos)[kIters],
+                                               bool (&hit)[kIters]) {
+    const bool unit_blocks = a.block_size == 1;
+#pragma unroll
+    for (int i = 0; i < kIters; ++i) {
+        const uint32_t o = first + i * 64;
+        const uint32_t offset = unit_blocks ? 0u : o - a.block_div.div(o) * a.block_size;
+        const int64_t p = block[i] * a.block_size + offset;
+        hit[i] = o < a.width && block[i] >= 0 && p < bound && table_ok;
+        pos[i] = hit[i] ? p : 0;
+    }
+}
+
+// Output stores, then the ordered miss list of this chunk; returns the new
+// running miss count of the row. Every thread of the workgroup must call it.
+template <bool kCompact>
+__device__ __forceinline__ int32_t emit(const LookupArgs& a, int32_t* out, int32_t* misses, uint32_t first,
+                                        const int32_t (&slot)[kIters], const bool (&hit)[kIters], int32_t running,
+                                        int32_t* wave_totals, int lane, int wave) {
+    uint64_t miss_mask[kIters];
+#pragma unroll
+    for (int i = 0; i < kIters; ++i) {
+        const uint32_t o = first + i * 64;
+        if (o < a.width) {
+            out[static_cast<int64_t>(o) * a.out_so] = slot[i];
+        }
+        if constexpr (kCompact) {
+            miss_mask[i] = __ballot(hit[i] && slot[i] == 0);
+        }
+    }
+    if constexpr (!kCompact) {
+        return running;
+    } else {
+        int32_t wave_total = 0;
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+            wave_total += __popcll(miss_mask[i]);
+        }
+        if (lane == 0) {
+            wave_totals[wave] = wave_total;
+        }
+        __syncthreads();
+        int32_t rank = running;
+        int32_t chunk_total = 0;
+#pragma unroll
+        for (int w = 0; w < kThreads / 64; ++w) {
+            rank += w < wave ? wave_totals[w] : 0;
+            chunk_total += wave_totals[w];
+        }
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+            if ((miss_mask[i] >> lane) & 1u) {
+                const int64_t at = rank + static_cast<int32_t>(lanes_below(miss_mask[i]));
+                misses[at * a.miss_so] = static_cast<int32_t>(first + i * 64);
+            }
+            rank += __popcll(miss_mask[i]);
+        }
+        __syncthreads();  // wave_totals is rewritten by the next chunk
+        return running + chunk_total;
+    }
+}
+
+template <typename TopkT, typename TableT, bool kBits, bool kCompact>
+__global__ __launch_bounds__(kThreads) void resolve_single_kernel(const LookupArgs a) {
     __shared__ int32_t wave_totals[kThreads / 64];
+    __shared__ uint32_t staged_bits[kBits ? kStagedBitWords : 1];
     const int64_t row = a.selected[blockIdx.x];
     if (row < 0 || row >= a.batch) {
         return;  // uniform over the workgroup
@@ -68,57 +160,47 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(const LookupArgs a) {
     const int64_t layer = blockIdx.y;
     const int64_t req = a.rows[row];
     const int64_t length = a.lengths[row];
-    const bool req_ok = req >= 0 && req < a.table_rows;
-    const bool table_ok = req_ok && a.table_cols > 0;  // uniform: the row has at least one entry
+    const bool table_ok = req >= 0 && req < a.table_rows && a.table_cols > 0;  // uniform
+    const int64_t req_at = table_ok ? req : 0;
+    const int64_t bound = length < a.table_cols ? length : a.table_cols;
     const TopkT* topk = static_cast<const TopkT*>(a.topk) + layer * a.topk_sl + row * a.topk_sb;
-    const TableT* table = static_cast<const TableT*>(a.table) + layer * a.table_sl + (req_ok ? req : 0) * a.table_sr;
+    const TableT* table = static_cast<const TableT*>(a.table) + layer * a.table_sl + req_at * a.table_sr;
+    const int32_t* bits_row = kBits ? a.bits + layer * a.bits_sl + req_at * a.bits_sr : nullptr;
+    const bool bits_in_lds = kBits && table_ok && a.bits_words <= kStagedBitWords;  // uniform
     int32_t* out = a.out + layer * a.out_sl + row * a.out_sb;
+    int32_t* misses = kCompact ? a.misses + layer * a.miss_sl + row * a.miss_sb : nullptr;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const bool unit_blocks = a.block_size == 1;
     int32_t running = 0;
 
     for (uint32_t chunk = 0; chunk < a.width; chunk += kChunkLanes) {
         const uint32_t first = chunk + wave * kWaveSpan + lane;
-        // Every load below is unconditional: lanes that must not read use a
-        // clamped in-bounds index and their value is masked afterwards, so
-        // the 8 loads of a phase are all in flight before the first wait.
         int64_t block[kIters];
-#pragma unroll
-        for (int i = 0; i < kIters; ++i) {
-            const uint32_t o = first + i * 64;
-            const uint32_t lane_o = o < a.width ? o : a.width - 1;
-            const uint32_t b = unit_blocks ? lane_o : a.block_div.div(lane_o);
-            block[i] = static_cast<int64_t>(topk[b * a.topk_sk]);
+        load_blocks(a, topk, first, block);
+        if (bits_in_lds && chunk == 0) {
+            // Issued after the Top-K loads so both are in flight together.
+            for (int64_t w = threadIdx.x; w < a.bits_words; w += kThreads) {
+                staged_bits[w] = static_cast<uint32_t>(bits_row[w * a.bits_sw]);
+            }
+            __syncthreads();
         }
-        int64_t value[kIters];
-        int64_t position[kIters];
-        bool hit_path[kIters];  // valid and every index in bounds
-#pragma unroll
-        for (int i = 0; i < kIters; ++i) {
-            const uint32_t o = first + i * 64;
-            const bool active = o < a.width;
-            const uint32_t offset = unit_blocks ? 0u : o - a.block_div.div(o) * a.block_size;
-            const int64_t pos = block[i] * a.block_size + offset;
-            const bool valid = active && block[i] >= 0 && pos < length;
-            hit_path[i] = valid && table_ok && pos < a.table_cols;
-            position[i] = hit_path[i] ? pos : 0;
-        }
+        int64_t pos[kIters];
+        bool hit[kIters];
+        lane_positions(a, first, block, bound, table_ok, pos, hit);
         bool resident[kIters];
-        if constexpr (std::is_same<MapT, Bits>::value) {
-            // A non-resident lane skips its table entry: it re-reads entry 0 of
-            // the row, which every such lane shares (one cached line), so
-            // misses cost 1 bit of HBM instead of a 128 B line.
-            const int32_t* bits_row = a.bits + layer * a.bits_sl + (req_ok ? req : 0) * a.bits_sr;
+        if constexpr (kBits) {
             uint32_t word[kIters];
 #pragma unroll
             for (int i = 0; i < kIters; ++i) {
-                word[i] = table_ok ? static_cast<uint32_t>(bits_row[(position[i] >> 5) * a.bits_sw]) : 0u;
+                word[i] = bits_in_lds ? staged_bits[pos[i] >> 5]
+                                      : (table_ok ? static_cast<uint32_t>(bits_row[(pos[i] >> 5) * a.bits_sw]) : 0u);
             }
 #pragma unroll
             for (int i = 0; i < kIters; ++i) {
-                resident[i] = hit_path[i] && ((word[i] >> (position[i] & 31)) & 1u);
-                position[i] = resident[i] ? position[i] : 0;
+                // A non-resident lane re-reads entry 0 of the row (shared by all
+                // such lanes, one cached line) instead of its own entry.
+                resident[i] = hit[i] && ((word[i] >> (pos[i] & 31)) & 1u);
+                pos[i] = resident[i] ? pos[i] : 0;
             }
         } else {
 #pragma unroll
@@ -126,69 +208,17 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(const LookupArgs a) {
                 resident[i] = true;
             }
         }
+        int32_t value[kIters];
 #pragma unroll
         for (int i = 0; i < kIters; ++i) {
-            value[i] = table_ok ? static_cast<int64_t>(table[position[i] * a.table_sc]) : 0;
+            value[i] = table_ok ? static_cast<int32_t>(table[pos[i] * a.table_sc]) : 0;
         }
+        int32_t slot[kIters];
 #pragma unroll
         for (int i = 0; i < kIters; ++i) {
-            value[i] = hit_path[i] ? (resident[i] ? value[i] : 0) : -1;
+            slot[i] = hit[i] ? (resident[i] ? value[i] : 0) : -1;
         }
-        if constexpr (!std::is_same<MapT, NoMap>::value && !std::is_same<MapT, Bits>::value) {
-            const MapT* mapping = static_cast<const MapT*>(a.mapping) + layer * a.map_sl;
-            int64_t mapped[kIters];
-#pragma unroll
-            for (int i = 0; i < kIters; ++i) {
-                hit_path[i] = hit_path[i] && value[i] >= 0 && value[i] < a.map_len;
-                const int64_t at = hit_path[i] ? value[i] : 0;
-                mapped[i] = a.map_len > 0 ? static_cast<int64_t>(mapping[at * a.map_s]) : 0;
-            }
-#pragma unroll
-            for (int i = 0; i < kIters; ++i) {
-                value[i] = hit_path[i] ? mapped[i] : -1;
-            }
-        }
-        uint64_t miss_mask[kIters];
-#pragma unroll
-        for (int i = 0; i < kIters; ++i) {
-            const uint32_t o = first + i * 64;
-            const int32_t slot = static_cast<int32_t>(value[i]);
-            if (o < a.width) {
-                out[static_cast<int64_t>(o) * a.out_so] = slot;
-            }
-            if constexpr (kCompact) {
-                miss_mask[i] = __ballot(hit_path[i] && slot == 0);
-            }
-        }
-        if constexpr (kCompact) {
-            int32_t wave_total = 0;
-#pragma unroll
-            for (int i = 0; i < kIters; ++i) {
-                wave_total += __popcll(miss_mask[i]);
-            }
-            if (lane == 0) {
-                wave_totals[wave] = wave_total;
-            }
-            __syncthreads();
-            int32_t rank = running;
-            int32_t chunk_total = 0;
-#pragma unroll
-            for (int w = 0; w < kThreads / 64; ++w) {
-                rank += w < wave ? wave_totals[w] : 0;
-                chunk_total += wave_totals[w];
-            }
-            int32_t* misses = a.misses + layer * a.miss_sl + row * a.miss_sb;
-#pragma unroll
-            for (int i = 0; i < kIters; ++i) {
-                if ((miss_mask[i] >> lane) & 1u) {
-                    const int64_t at = rank + static_cast<int32_t>(lanes_below(miss_mask[i]));
-                    misses[at * a.miss_so] = static_cast<int32_t>(first + i * 64);
-                }
-                rank += __popcll(miss_mask[i]);
-            }
-            running += chunk_total;
-            __syncthreads();  // wave_totals is rewritten by the next chunk
-        }
+        running = emit<kCompact>(a, out, misses, first, slot, hit, running, wave_totals, lane, wave);
     }
     if constexpr (kCompact) {
         if (threadIdx.x == 0) {
@@ -197,25 +227,87 @@ __global__ __launch_bounds__(kThreads) void resolve_kernel(const LookupArgs a) {
     }
 }
 
-template <typename TopkT, typename TableT, typename MapT>
-void launch_typed(const LookupArgs& a, bool compact, dim3 grid, hipStream_t stream) {
-    if (compact) {
-        resolve_kernel<TopkT, TableT, MapT, true><<<grid, dim3(kThreads), 0, stream>>>(a);
-    } else {
-        resolve_kernel<TopkT, TableT, MapT, false><<<grid, dim3(kThreads), 0, stream>>>(a);
+template <typename TopkT, typename TableT, typename MapT, bool kCompact>
+__global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupArgs a) {
+    __shared__ int32_t wave_totals[kThreads / 64];
+    const int64_t row = a.selected[blockIdx.x];
+    if (row < 0 || row >= a.batch) {
+        return;  // uniform over the workgroup
+    }
+    const int64_t layer = blockIdx.y;
+    const int64_t req = a.rows[row];
+    const int64_t length = a.lengths[row];
+    const bool table_ok = req >= 0 && req < a.table_rows && a.table_cols > 0;  // uniform
+    const int64_t bound = length < a.table_cols ? length : a.table_cols;
+    const TopkT* topk = static_cast<const TopkT*>(a.topk) + layer * a.topk_sl + row * a.topk_sb;
+    const TableT* table =
+        static_cast<const TableT*>(a.table) + layer * a.table_sl + (table_ok ? req : 0) * a.table_sr;
+    const MapT* mapping = static_cast<const MapT*>(a.mapping) + layer * a.map_sl;
+    int32_t* out = a.out + layer * a.out_sl + row * a.out_sb;
+    int32_t* misses = kCompact ? a.misses + layer * a.miss_sl + row * a.miss_sb : nullptr;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    int32_t running = 0;
+
+    for (uint32_t chunk = 0; chunk < a.width; chunk += kChunkLanes) {
+        const uint32_t first = chunk + wave * kWaveSpan + lane;
+        int64_t block[kIters];
+        load_blocks(a, topk, first, block);
+        int64_t pos[kIters];
+        bool hit[kIters];
+        lane_positions(a, first, block, bound, table_ok, pos, hit);
+        int64_t logical[kIters];
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+            logical[i] = table_ok ? static_cast<int64_t>(table[pos[i] * a.table_sc]) : 0;
+        }
+        int64_t mapped[kIters];
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+            hit[i] = hit[i] && logical[i] >= 0 && logical[i] < a.map_len;
+            const int64_t at = hit[i] ? logical[i] : 0;
+            mapped[i] = a.map_len > 0 ? static_cast<int64_t>(mapping[at * a.map_s]) : 0;
+        }
+        int32_t slot[kIters];
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+            slot[i] = hit[i] ? static_cast<int32_t>(mapped[i]) : -1;
+        }
+        running = emit<kCompact>(a, out, misses, first, slot, hit, running, wave_totals, lane, wave);
+    }
+    if constexpr (kCompact) {
+        if (threadIdx.x == 0) {
+            a.counts[layer * a.count_sl + row * a.count_sb] = running;
+        }
     }
 }
 
 template <typename TopkT, typename TableT>
-void launch_map(const LookupArgs& a, int32_t map_dtype, bool compact, dim3 grid, hipStream_t stream) {
-    if (a.bits != nullptr) {
-        launch_typed<TopkT, TableT, Bits>(a, compact, grid, stream);
-    } else if (a.mapping == nullptr) {
-        launch_typed<TopkT, TableT, NoMap>(a, compact, grid, stream);
+void launch_with_table(const LookupArgs& a, int32_t map_dtype, bool compact, dim3 grid, hipStream_t stream) {
+    const dim3 block(kThreads);
+    if (a.mapping == nullptr) {
+        const bool bits = a.bits != nullptr;
+        if (bits && compact) {
+            resolve_single_kernel<TopkT, TableT, true, true><<<grid, block, 0, stream>>>(a);
+        } else if (bits) {
+            resolve_single_kernel<TopkT, TableT, true, false><<<grid, block, 0, stream>>>(a);
+        } else if (compact) {
+            resolve_single_kernel<TopkT, TableT, false, true><<<grid, block, 0, stream>>>(a);
+        } else {
+            resolve_single_kernel<TopkT, TableT, false, false><<<grid, block, 0, stream>>>(a);
+        }
     } else if (map_dtype == EKV_INT64) {
-        launch_typed<TopkT, TableT, int64_t>(a, compact, grid, stream);
+        if (compact) {
+            resolve_mapped_kernel<TopkT, TableT, int64_t, true><<<grid, block, 0, stream>>>(a);
+        } else {
+            resolve_mapped_kernel<TopkT, TableT, int64_t, false><<<grid, block, 0, stream>>>(a);
+        }
     } else {
-        launch_typed<TopkT, TableT, int32_t>(a, compact, grid, stream);
+        if (compact) {
+            resolve_mapped_kernel<TopkT, TableT, int32_t, true><<<grid, block, 0, stream>>>(a);
+        } else {
+            resolve_mapped_kernel<TopkT, TableT, int32_t, false><<<grid, block, 0, stream>>>(a);
+        }
     }
 }
 
@@ -223,9 +315,9 @@ template <typename TopkT>
 void launch_table(const LookupArgs& a, int32_t table_dtype, int32_t map_dtype, bool compact, dim3 grid,
                   hipStream_t stream) {
     if (table_dtype == EKV_INT64) {
-        launch_map<TopkT, int64_t>(a, map_dtype, compact, grid, stream);
+        launch_with_table<TopkT, int64_t>(a, map_dtype, compact, grid, stream);
     } else {
-        launch_map<TopkT, int32_t>(a, map_dtype, compact, grid, stream);
+        launch_with_table<TopkT, int32_t>(a, map_dtype, compact, grid, stream);
     }
 }
 
@@ -357,6 +449,7 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
         a.bits_sl = layered_table ? bits_p->stride[0] : 0;
         a.bits_sr = bits_p->stride[d];
         a.bits_sw = bits_p->stride[d + 1];
+        a.bits_words = (a.table_cols + 31) / 32;
     }
     a.rows = index_ref(rows, 0);
     a.lengths = index_ref(lengths, 0);
