@@ -1,0 +1,101 @@
+"""Hot-buffer swap-in: LRU replacement of missed tokens, promoted from pinned host.
+
+The single GPU replacement of the host-backed swap in the reference's decode
+path (adaptive_sparse/request_residency.py:805-832, which calls SGLang's
+load_blocks_to_device_buffer_mha): after the resident lookup has produced
+slots and an ordered miss list, swap_in picks LRU victims in every
+(layer, request) hot buffer, rewrites the token->slot table (and its
+residency bitmap), patches the looked-up slots of the missed lanes and emits
+(host row -> slot) promotion lists; move_kv then copies those rows from the
+pinned host copy into the pool. The replacement policy is the reference's
+batch-token LRU (benchmarks/hisparse_locality_replay.py:90-99).
+"""
+
+import ctypes as ct
+
+import torch
+
+from elastic_kv import _native
+
+from .kv_pool import KVPlanes
+from .sparse_read import _planes_struct
+
+INT32_MIN = -(1 << 31)
+
+
+class HotBuffers:
+    """LRU hot buffers of `capacity` slots per (layer, request).
+
+    table [L, R, T] int32: token -> global slot (0 = not resident); bits: its
+    residency bitmap; slot_token [L, R, C]: token held by each slot (-1 =
+    empty); stamps [L, R, C]: recency stamps; slot_base [R]: global slot of
+    each request's local slot 0 (request r owns slots base .. base + C - 1).
+    """
+
+    def __init__(self, layers, requests, context, capacity, device, *, slot_base=None, with_bits=True):
+        self.layers, self.requests, self.context, self.capacity = layers, requests, context, capacity
+        self.device = torch.device(device)
+        kw = dict(dtype=torch.int32, device=self.device)
+        self.table = torch.zeros((layers, requests, context), **kw)
+        self.bits = torch.zeros((layers, requests, (context + 31) // 32), **kw) if with_bits else None
+        self.slot_token = torch.full((layers, requests, capacity), -1, **kw)
+        self.stamps = torch.full((layers, requests, capacity), INT32_MIN, **kw)
+        if slot_base is None:
+            slot_base = torch.arange(requests, dtype=torch.int64, device=self.device) * capacity + 1
+        self.slot_base = slot_base
+        self.step = 0
+
+    def install(self, tokens, local_slots):
+        """Make `tokens` [L, R, n] resident in `local_slots` [L, R, n] (setup, not the hot path).
+
+        Their recency follows their order along the last dimension (first =
+        least recent), ahead of anything installed later.
+        """
+        L, R, n = tokens.shape
+        tokens = tokens.to(self.device, torch.int64)
+        local = local_slots.to(self.device, torch.int64)
+        glob = (local + self.slot_base.view(1, R, 1)).to(torch.int32)
+        self.table.scatter_(2, tokens, glob)
+        self.slot_token.scatter_(2, local, tokens.to(torch.int32))
+        rank = torch.arange(n, device=self.device, dtype=torch.int32).expand(L, R, n)
+        self.stamps.scatter_(2, local, rank - n - 1)
+        if self.bits is not None:
+            from .resident_lookup import build_residency_bits
+
+            build_residency_bits(self.table, out=self.bits)
+
+
+def swap_in(topk, block_size, rows, selected, slots, misses, miss_count, buffers, host_table,
+            promote_src, promote_dst, *, step=None):
+    """Run one swap-in step (see module docstring); advances buffers.step."""
+    step = buffers.step if step is None else step
+    tensors = [topk, rows, selected, slots, misses, miss_count, buffers.table, buffers.slot_token,
+               buffers.stamps, buffers.slot_base, host_table, promote_src, promote_dst]
+    if buffers.bits is not None:
+        tensors.append(buffers.bits)
+    device = _native.device_of(*tensors)
+    lib = _native.kernel_library()
+    views = [_native.describe(t, "swap_in tensor") for t in tensors[:13]]
+    bits_view = ct.byref(_native.describe(buffers.bits, "bits")) if buffers.bits is not None else None
+    ordered = [views[0], views[1], views[2], views[3], views[4], views[5], views[6], None, views[7], views[8],
+               views[9], views[10], views[11], views[12]]
+    args = [ct.byref(v) if v is not None else bits_view for v in ordered]
+    with torch.cuda.device(device):
+        status = lib.ekv_swap_in(args[0], int(block_size), *args[1:], int(step), _native.stream_handle(device))
+    _native.check(lib, status, "swap_in")
+    buffers.step = step + 1
+
+
+def move_kv(src_planes, src_rows, dst_planes, dst_rows, counts, *, zero_below=1):
+    """dst(l, kv)[dst_rows[l, b, i]] = src(l, kv)[src_rows[l, b, i]] for i < counts[l, b]."""
+    for planes in (src_planes, dst_planes):
+        if not isinstance(planes, KVPlanes):
+            raise TypeError("planes must be KVPlanes")
+    device = _native.device_of(src_rows, dst_rows, counts)
+    lib = _native.kernel_library()
+    src_view, dst_view = _planes_struct(src_planes), _planes_struct(dst_planes)
+    views = [_native.describe(t, n) for t, n in ((src_rows, "src_rows"), (dst_rows, "dst_rows"), (counts, "counts"))]
+    with torch.cuda.device(device):
+        status = lib.ekv_move_kv(ct.byref(src_view), ct.byref(views[0]), ct.byref(dst_view), ct.byref(views[1]),
+                                 ct.byref(views[2]), int(zero_below), _native.stream_handle(device))
+    _native.check(lib, status, "move_kv")

@@ -44,7 +44,9 @@ constexpr int kUnroll = EKV_COPY_UNROLL;  // independent VW-byte loads in flight
 // +13 % on the 60-layer decode gather compared with plain tile order.
 constexpr int64_t kXcdCount = 8;
 
-enum Mode : int { KvGather = 0, KvScatter = 1, RowsDirect = 2, RowsIndirect = 3, KvGather64 = 4, KvScatter64 = 5 };
+enum Mode : int {
+    KvGather = 0, KvScatter = 1, RowsDirect = 2, RowsIndirect = 3, KvGather64 = 4, KvScatter64 = 5, KvMove = 6
+};
 
 constexpr bool is_kv_mode(int m) { return m == KvGather || m == KvScatter || m == KvGather64 || m == KvScatter64; }
 constexpr bool is_gather_mode(int m) { return m == KvGather || m == KvGather64; }
@@ -88,6 +90,17 @@ struct EngineArgs {
     FastDiv div_k, div_kv, div_b;
     bool small_units;        // units < 2^31: decompose with FastDiv
 
+    // Move mode: rows src_rows[l, b, i] of the source planes -> rows
+    // dst_rows[l, b, i] of the destination planes, for i < counts[l, b].
+    const char* msrc;
+    int64_t ms_layer_stride, ms_kv_stride, ms_row_stride, ms_rows;
+    const int32_t* move_src_rows;
+    int64_t msr_l, msr_b, msr_i;
+    const int32_t* move_dst_rows;
+    int64_t mdr_l, mdr_b, mdr_i;
+    const int32_t* move_counts;
+    int64_t mc_l, mc_b;
+
     // Rows modes: unit u = b * S + s.
     const char* raw;
     int64_t raw_elems, itemsize, width, request_stride, sink;
@@ -109,28 +122,46 @@ __device__ __forceinline__ int64_t load_index(const void* p, int64_t i, int32_t 
 
 // (source offset, destination offset) in bytes of one row; -1 source means a
 // zero row, -1 destination means the row is not written.
+__device__ __forceinline__ void split_unit(const EngineArgs& a, int64_t u, int64_t& l, int64_t& b, int64_t& kv,
+                                           int64_t& k) {
+    if (a.small_units) {
+        const uint32_t u32 = static_cast<uint32_t>(u);
+        const uint32_t q1 = a.div_k.div(u32);
+        k = u32 - q1 * static_cast<uint32_t>(a.K);
+        const uint32_t q2 = a.div_kv.div(q1);
+        kv = q1 - q2 * static_cast<uint32_t>(a.KV);
+        const uint32_t q3 = a.div_b.div(q2);
+        b = q2 - q3 * static_cast<uint32_t>(a.B);
+        l = q3;
+    } else {
+        k = u % a.K;
+        int64_t q = u / a.K;
+        kv = q % a.KV;
+        q /= a.KV;
+        b = q % a.B;
+        l = q / a.B;
+    }
+}
+
 template <int M>
 __device__ __forceinline__ void locate(const EngineArgs& a, int64_t u, int64_t& src, int64_t& dst) {
-    if constexpr (is_kv_mode(M)) {
+    if constexpr (M == KvMove) {
+        int64_t l, b, kv, k;
+        split_unit(a, u, l, b, kv, k);
+        src = -1;
+        dst = -1;
+        if (k < a.move_counts[l * a.mc_l + b * a.mc_b]) {
+            const int64_t from = a.move_src_rows[l * a.msr_l + b * a.msr_b + k * a.msr_i];
+            const int64_t to = a.move_dst_rows[l * a.mdr_l + b * a.mdr_b + k * a.mdr_i];
+            if (from >= 0 && from < a.ms_rows && to >= a.zero_below && to < a.pool_rows) {
+                src = l * a.ms_layer_stride + kv * a.ms_kv_stride + from * a.ms_row_stride;
+                dst = l * a.layer_stride + kv * a.kv_stride + to * a.row_stride;
+            }
+        }
+    } else if constexpr (is_kv_mode(M)) {
         using SlotT = typename std::conditional<(M == KvGather64 || M == KvScatter64), int64_t, int32_t>::type;
         int64_t k, kv, b, l;
-        if (a.small_units) {
-            const uint32_t u32 = static_cast<uint32_t>(u);
-            const uint32_t q1 = a.div_k.div(u32);
-            k = u32 - q1 * static_cast<uint32_t>(a.K);
-            const uint32_t q2 = a.div_kv.div(q1);
-            kv = q1 - q2 * static_cast<uint32_t>(a.KV);
-            const uint32_t q3 = a.div_b.div(q2);
-            b = q2 - q3 * static_cast<uint32_t>(a.B);
-            l = q3;
-        } else {
-            k = u % a.K;
-            int64_t q = u / a.K;
-            kv = q % a.KV;
-            q /= a.KV;
-            b = q % a.B;
-            l = q / a.B;
-        }
+        split_unit(a, u, l, b, kv, k);
         const int64_t slot = static_cast<const SlotT*>(a.slots)[l * a.s_sl + b * a.s_sb + k * a.s_sk];
         const bool valid = slot >= a.zero_below && slot < a.pool_rows;
         const int64_t pool_off = l * a.layer_stride + kv * a.kv_stride + slot * a.row_stride;
@@ -523,8 +554,124 @@ int gather_rows(const ekv_tensor* raw_p, const ekv_tensor* positions_p, const ek
     return 0;
 }
 
+int move_kv(const ekv_planes* src, const ekv_tensor* src_rows_p, const ekv_planes* dst,
+            const ekv_tensor* dst_rows_p, const ekv_tensor* counts_p, int64_t zero_below, void* stream) {
+    need_planes(src);
+    need_planes(dst);
+    const ekv_tensor& src_rows = need(src_rows_p, "src_rows");
+    const ekv_tensor& dst_rows = need(dst_rows_p, "dst_rows");
+    const ekv_tensor& counts = need(counts_p, "counts");
+    need_ndim(src_rows, 3, "src_rows");
+    need_ndim(dst_rows, 3, "dst_rows");
+    need_ndim(counts, 2, "counts");
+    for (const auto* t : {&src_rows, &dst_rows, &counts}) {
+        if (t->dtype != EKV_INT32) {
+            throw std::invalid_argument("move lists and counts must be int32");
+        }
+    }
+    const int64_t L = src_rows.shape[0], B = src_rows.shape[1], K = src_rows.shape[2];
+    for (int d = 0; d < 3; ++d) {
+        need_dim(dst_rows, d, src_rows.shape[d], "dst_rows");
+    }
+    need_dim(counts, 0, L, "counts");
+    need_dim(counts, 1, B, "counts");
+    if (src->row_bytes != dst->row_bytes || src->kv != dst->kv) {
+        throw std::invalid_argument("source and destination planes differ in row bytes or kv");
+    }
+    if (L > src->layers || L > dst->layers) {
+        throw std::invalid_argument("move lists name more layers than the planes hold");
+    }
+    if (zero_below < 0) {
+        throw std::invalid_argument("zero_below must be >= 0");
+    }
+    const int64_t units = L * B * dst->kv * K;
+    if (units == 0 || dst->row_bytes == 0) {
+        return 0;
+    }
+    if (src->base == nullptr || dst->base == nullptr) {
+        throw std::invalid_argument("null plane base");
+    }
+    for (const auto* t : {&src_rows, &dst_rows, &counts}) {
+        need_data(*t, "move list");
+    }
+    EngineArgs a{};
+    a.units = units;
+    a.row_bytes = dst->row_bytes;
+    a.layer_stride = dst->layer_stride;
+    a.kv_stride = dst->kv_stride;
+    a.row_stride = dst->row_stride;
+    a.pool_rows = dst->rows;
+    a.zero_below = zero_below;
+    a.msrc = static_cast<const char*>(src->base);
+    a.ms_layer_stride = src->layer_stride;
+    a.ms_kv_stride = src->kv_stride;
+    a.ms_row_stride = src->row_stride;
+    a.ms_rows = src->rows;
+    a.move_src_rows = static_cast<const int32_t*>(src_rows.data);
+    a.msr_l = src_rows.stride[0], a.msr_b = src_rows.stride[1], a.msr_i = src_rows.stride[2];
+    a.move_dst_rows = static_cast<const int32_t*>(dst_rows.data);
+    a.mdr_l = dst_rows.stride[0], a.mdr_b = dst_rows.stride[1], a.mdr_i = dst_rows.stride[2];
+    a.move_counts = static_cast<const int32_t*>(counts.data);
+    a.mc_l = counts.stride[0], a.mc_b = counts.stride[1];
+    a.K = K;
+    a.KV = dst->kv;
+    a.B = B;
+    a.small_units = units < (int64_t{1} << 31);
+    if (a.small_units) {
+        a.div_k = FastDiv(static_cast<uint32_t>(K));
+        a.div_kv = FastDiv(static_cast<uint32_t>(dst->kv));
+        a.div_b = FastDiv(static_cast<uint32_t>(B));
+    }
+    a.src_base = a.msrc;
+    a.dst_base = static_cast<char*>(dst->base);
+    const int vw = pick_vector_width({dst->row_bytes, reinterpret_cast<int64_t>(src->base), src->layer_stride,
+                                      src->kv_stride, src->row_stride, reinterpret_cast<int64_t>(dst->base),
+                                      dst->layer_stride, dst->kv_stride, dst->row_stride});
+    launch_vw<KvMove>(a, vw, static_cast<hipStream_t>(stream));
+    check_hip(hipGetLastError(), "launch KV move");
+    return 0;
+}
+
+// Pinned host memory that kernels can read and write directly.
+int host_alloc(uint64_t bytes, void** host, void** device) {
+    if (host == nullptr || device == nullptr || bytes == 0) {
+        throw std::invalid_argument("host_alloc needs a positive size and two out pointers");
+    }
+    *host = nullptr;
+    *device = nullptr;
+    void* memory = nullptr;
+    check_hip(hipHostMalloc(&memory, bytes, hipHostMallocDefault), "hipHostMalloc");
+    void* mapped = nullptr;
+    const hipError_t status = hipHostGetDevicePointer(&mapped, memory, 0);
+    if (status != hipSuccess || mapped == nullptr) {
+        (void)hipHostFree(memory);
+        fail_hip(status == hipSuccess ? hipErrorInvalidValue : status, "hipHostGetDevicePointer");
+    }
+    *host = memory;
+    *device = mapped;
+    return 0;
+}
+
 }  // namespace
 }  // namespace ekv
+
+extern "C" int ekv_move_kv(const ekv_planes* src, const ekv_tensor* src_rows, const ekv_planes* dst,
+                           const ekv_tensor* dst_rows, const ekv_tensor* counts, int64_t zero_below, void* stream) {
+    return ekv::guarded(-1, [&] { return ekv::move_kv(src, src_rows, dst, dst_rows, counts, zero_below, stream); });
+}
+
+extern "C" int ekv_host_alloc(uint64_t bytes, void** host, void** device) {
+    return ekv::guarded(-1, [&] { return ekv::host_alloc(bytes, host, device); });
+}
+
+extern "C" int ekv_host_free(void* host) {
+    return ekv::guarded(-1, [&] {
+        if (host != nullptr) {
+            ekv::check_hip(hipHostFree(host), "hipHostFree");
+        }
+        return 0;
+    });
+}
 
 extern "C" int ekv_gather_kv(const ekv_planes* planes, const ekv_tensor* slots, const ekv_kv_rows* out,
                              int64_t zero_below, void* stream) {

@@ -1,0 +1,341 @@
+// Hot-buffer swap-in with batch-token LRU replacement (gfx950).
+//
+// Policy: benchmarks/hisparse_locality_replay.py:90-99 - per (request, layer)
+// stream, misses are counted at entry, hits are touched (moved to most recent,
+// in selection order), least-recent entries are evicted until the misses fit,
+// then the misses are inserted in selection order. Here the hot buffer of a
+// (layer, request) row is `capacity` slots; the reference's ordered dict is
+// represented by one recency stamp per slot:
+//   touched hit of lane o at step s: stamp = s * 2W + o
+//   inserted miss of lane o:         stamp = s * 2W + W + o      (W = lanes per row)
+//   empty slot:                      stamp = INT32_MIN
+// so sorting slots by (stamp, slot) reproduces the dict's order, and the m
+// victims of a step (m = misses) are the m smallest keys: empty slots first,
+// then the least recently used entries. The i-th miss (in lane order) takes
+// the i-th victim.
+//
+// One 256-thread workgroup per (row, layer): hits are touched in LDS, the
+// (stamp, slot) keys are bitonic-sorted in LDS, then each victim clears its
+// old token from the token->slot table and residency bitmap, takes the new
+// token, and writes one promotion (host row -> global slot) record. The
+// lookup's slot output of every miss lane is patched to its new slot, so the
+// gather that follows reads the promoted row.
+#include "../../include/ekv_kernels.h"
+#include "ekv_common.h"
+#include "ekv_fastdiv.h"
+#include "ekv_tensor_util.h"
+
+#include <algorithm>
+#include <climits>
+
+namespace ekv {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxCapacity = 8192;   // slots per hot buffer sortable in LDS
+
+struct SwapArgs {
+    const void* topk;
+    int32_t topk64;
+    int64_t topk_sl, topk_sb, topk_sk;
+    uint32_t block_size;
+    FastDiv block_div;
+    IndexRef rows, selected, slot_base;
+    int32_t* slots;                 // [L, B, W] lookup output, patched for misses
+    int64_t sl_l, sl_b, sl_o;
+    const int32_t* misses;          // [L, B, W] miss lanes
+    int64_t mi_l, mi_b, mi_o;
+    const int32_t* counts;          // [L, B]
+    int64_t ct_l, ct_b;
+    int32_t* table;                 // [L, R, T] token -> global slot (0 = not resident)
+    int64_t tb_l, tb_r, tb_t, table_cols;
+    int32_t* bits;                  // [L, R, ceil(T/32)] residency bitmap (may be null)
+    int64_t bt_l, bt_r, bt_w;
+    int32_t* slot_token;            // [L, R, C] token held by each slot (-1 = empty)
+    int64_t st_l, st_r, st_c;
+    int32_t* stamps;                // [L, R, C] recency stamps
+    int64_t sp_l, sp_r, sp_c;
+    IndexRef host_table;            // [R, T] token -> host row, addressed with explicit strides
+    int64_t host_sr, host_st;
+    int32_t* promote_src;           // [L, B, W] host row per promotion
+    int64_t ps_l, ps_b, ps_o;
+    int32_t* promote_dst;           // [L, B, W] global slot per promotion
+    int64_t pd_l, pd_b, pd_o;
+    int64_t batch, table_rows, capacity, capacity_pow2;
+    uint32_t width;
+    int64_t step;
+};
+
+__device__ __forceinline__ int64_t lane_position(const SwapArgs& a, const void* topk_row, uint32_t lane) {
+    const uint32_t b = a.block_size == 1 ? lane : a.block_div.div(lane);
+    const int64_t block = a.topk64 ? static_cast<const int64_t*>(topk_row)[b * a.topk_sk]
+                                   : static_cast<int64_t>(static_cast<const int32_t*>(topk_row)[b * a.topk_sk]);
+    const uint32_t offset = a.block_size == 1 ? 0u : lane - b * a.block_size;
+    return block * a.block_size + offset;
+}
+
+__global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
+    extern __shared__ unsigned char shared[];
+    uint64_t* keys = reinterpret_cast<uint64_t*>(shared);                     // capacity_pow2 entries
+    int32_t* stamp = reinterpret_cast<int32_t*>(keys + a.capacity_pow2);      // capacity entries
+    const int64_t b = a.selected[blockIdx.x];
+    if (b < 0 || b >= a.batch) {
+        return;
+    }
+    const int64_t l = blockIdx.y;
+    const int64_t req = a.rows[b];
+    if (req < 0 || req >= a.table_rows) {
+        return;  // uniform: a row outside the tables has nothing resident
+    }
+    const int64_t base = a.slot_base[req];
+    const int64_t C = a.capacity;
+    const int64_t W = a.width;
+    const int64_t stamp_base = a.step * 2 * W;
+    int32_t* slots = a.slots + l * a.sl_l + b * a.sl_b;
+    int32_t* table = a.table + l * a.tb_l + req * a.tb_r;
+    int32_t* slot_token = a.slot_token + l * a.st_l + req * a.st_r;
+    int32_t* stamps = a.stamps + l * a.sp_l + req * a.sp_r;
+    const void* topk_row = a.topk64
+        ? static_cast<const void*>(static_cast<const int64_t*>(a.topk) + l * a.topk_sl + b * a.topk_sb)
+        : static_cast<const void*>(static_cast<const int32_t*>(a.topk) + l * a.topk_sl + b * a.topk_sb);
+
+    for (int64_t s = threadIdx.x; s < C; s += kThreads) {
+        stamp[s] = stamps[s * a.sp_c];
+    }
+    __syncthreads();
+    // Touch hits (unique tokens per row, so at most one lane per slot).
+    for (int64_t o = threadIdx.x; o < W; o += kThreads) {
+        const int64_t local = static_cast<int64_t>(slots[o * a.sl_o]) - base;
+        if (slots[o * a.sl_o] > 0 && local >= 0 && local < C) {
+            stamp[local] = static_cast<int32_t>(stamp_base + o);
+        }
+    }
+    __syncthreads();
+    const int32_t counted = a.counts[l * a.ct_l + b * a.ct_b];
+    const int32_t m = counted < 0 ? 0 : (counted > W ? static_cast<int32_t>(W) : counted);
+    if (m > 0) {
+        for (int64_t s = threadIdx.x; s < a.capacity_pow2; s += kThreads) {
+            keys[s] = s < C ? (static_cast<uint64_t>(static_cast<uint32_t>(stamp[s]) ^ 0x80000000u) << 32) |
+                                  static_cast<uint64_t>(s)
+                            : ~uint64_t{0};
+        }
+        __syncthreads();
+        const int64_t n = a.capacity_pow2;
+        for (int64_t k = 2; k <= n; k <<= 1) {
+            for (int64_t j = k >> 1; j > 0; j >>= 1) {
+                for (int64_t i = threadIdx.x; i < n; i += kThreads) {
+                    const int64_t partner = i ^ j;
+                    if (partner > i) {
+                        const uint64_t x = keys[i], y = keys[partner];
+                        const bool ascending = (i & k) == 0;
+                        if ((x > y) == ascending) {
+                            keys[i] = y;
+                            keys[partner] = x;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        }
+        const int32_t* misses = a.misses + l * a.mi_l + b * a.mi_b;
+        int32_t* promote_src = a.promote_src + l * a.ps_l + b * a.ps_b;
+        int32_t* promote_dst = a.promote_dst + l * a.pd_l + b * a.pd_b;
+        int32_t* bits = a.bits != nullptr ? a.bits + l * a.bt_l + req * a.bt_r : nullptr;
+        for (int64_t i = threadIdx.x; i < m; i += kThreads) {
+            const int64_t victim = static_cast<int64_t>(keys[i] & 0xffffffffu);
+            const int32_t lane = misses[i * a.mi_o];
+            if (lane < 0 || lane >= W || victim >= C) {
+                continue;  // not a miss list written by the lookup
+            }
+            const int64_t token = lane_position(a, topk_row, static_cast<uint32_t>(lane));
+            if (token < 0 || token >= a.table_cols) {
+                continue;
+            }
+            const int32_t old = slot_token[victim * a.st_c];
+            if (old >= 0 && old < a.table_cols) {
+                table[old * a.tb_t] = 0;
+                if (bits != nullptr) {
+                    atomicAnd(reinterpret_cast<unsigned int*>(bits + (old >> 5) * a.bt_w), ~(1u << (old & 31)));
+                }
+            }
+            const int32_t global = static_cast<int32_t>(base + victim);
+            table[token * a.tb_t] = global;
+            if (bits != nullptr) {
+                atomicOr(reinterpret_cast<unsigned int*>(bits + (token >> 5) * a.bt_w), 1u << (token & 31));
+            }
+            slot_token[victim * a.st_c] = static_cast<int32_t>(token);
+            stamp[victim] = static_cast<int32_t>(stamp_base + W + lane);
+            promote_src[i * a.ps_o] = static_cast<int32_t>(a.host_table[req * a.host_sr + token * a.host_st]);
+            promote_dst[i * a.pd_o] = global;
+            slots[static_cast<int64_t>(lane) * a.sl_o] = global;
+        }
+        __syncthreads();
+    }
+    for (int64_t s = threadIdx.x; s < C; s += kThreads) {
+        stamps[s * a.sp_c] = stamp[s];
+    }
+}
+
+void need_i32(const ekv_tensor& t, const char* name) {
+    if (t.dtype != EKV_INT32) {
+        throw std::invalid_argument(std::string(name) + " must be int32");
+    }
+}
+
+int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows_p, const ekv_tensor* selected_p,
+            const ekv_tensor* slots_p, const ekv_tensor* misses_p, const ekv_tensor* counts_p,
+            const ekv_tensor* table_p, const ekv_tensor* bits_p, const ekv_tensor* slot_token_p,
+            const ekv_tensor* stamps_p, const ekv_tensor* slot_base_p, const ekv_tensor* host_table_p,
+            const ekv_tensor* promote_src_p, const ekv_tensor* promote_dst_p, int64_t step, void* stream) {
+    const ekv_tensor& topk = need(topk_p, "topk");
+    const ekv_tensor& rows = need(rows_p, "rows");
+    const ekv_tensor& selected = need(selected_p, "selected");
+    const ekv_tensor& slots = need(slots_p, "slots");
+    const ekv_tensor& misses = need(misses_p, "misses");
+    const ekv_tensor& counts = need(counts_p, "miss_count");
+    const ekv_tensor& table = need(table_p, "table");
+    const ekv_tensor& slot_token = need(slot_token_p, "slot_token");
+    const ekv_tensor& stamps = need(stamps_p, "stamps");
+    const ekv_tensor& slot_base = need(slot_base_p, "slot_base");
+    const ekv_tensor& host_table = need(host_table_p, "host_table");
+    const ekv_tensor& promote_src = need(promote_src_p, "promote_src");
+    const ekv_tensor& promote_dst = need(promote_dst_p, "promote_dst");
+    need_ndim(topk, 3, "topk");
+    need_index(topk, "topk");
+    const int64_t L = topk.shape[0], B = topk.shape[1], K = topk.shape[2];
+    if (block_size < 1 || block_size >= (int64_t{1} << 31)) {
+        throw std::invalid_argument("block_size must be positive");
+    }
+    const int64_t W = K * block_size;
+    for (const auto* t : {&slots, &misses, &promote_src, &promote_dst}) {
+        need_ndim(*t, 3, "slots/misses/promote lists");
+        need_i32(*t, "slots/misses/promote lists");
+        need_dim(*t, 0, L, "slots/misses/promote lists");
+        need_dim(*t, 1, B, "slots/misses/promote lists");
+        need_dim(*t, 2, W, "slots/misses/promote lists");
+    }
+    need_ndim(counts, 2, "miss_count");
+    need_i32(counts, "miss_count");
+    need_dim(counts, 0, L, "miss_count");
+    need_dim(counts, 1, B, "miss_count");
+    for (const auto* t : {&table, &slot_token, &stamps}) {
+        need_ndim(*t, 3, "table/slot_token/stamps");
+        need_i32(*t, "table/slot_token/stamps");
+        need_dim(*t, 0, L, "table/slot_token/stamps");
+    }
+    const int64_t R = table.shape[1], T = table.shape[2], C = slot_token.shape[2];
+    need_dim(slot_token, 1, R, "slot_token");
+    need_dim(stamps, 1, R, "stamps");
+    need_dim(stamps, 2, C, "stamps");
+    if (C < 1 || C > kMaxCapacity) {
+        throw std::invalid_argument("capacity must be 1.." + std::to_string(kMaxCapacity));
+    }
+    if (W > C) {
+        throw std::invalid_argument("lanes per row exceed the hot capacity");
+    }
+    if (T >= (int64_t{1} << 31) || step < 0 || (step + 1) * 2 * W >= (int64_t{1} << 31)) {
+        throw std::invalid_argument("token count or step outside the 32-bit stamp range");
+    }
+    need_ndim(rows, 1, "rows");
+    need_ndim(selected, 1, "selected");
+    need_ndim(slot_base, 1, "slot_base");
+    need_index(rows, "rows");
+    need_index(selected, "selected");
+    need_index(slot_base, "slot_base");
+    need_dim(rows, 0, B, "rows");
+    need_dim(slot_base, 0, R, "slot_base");
+    need_ndim(host_table, 2, "host_table");
+    need_index(host_table, "host_table");
+    need_dim(host_table, 0, R, "host_table");
+    need_dim(host_table, 1, T, "host_table");
+    if (bits_p != nullptr) {
+        const ekv_tensor& bits = need(bits_p, "resident_bits");
+        need_ndim(bits, 3, "resident_bits");
+        need_i32(bits, "resident_bits");
+        need_dim(bits, 0, L, "resident_bits");
+        need_dim(bits, 1, R, "resident_bits");
+        if (bits.shape[2] < (T + 31) / 32) {
+            throw std::invalid_argument("resident_bits needs ceil(T / 32) words per row");
+        }
+    }
+    const int64_t count = selected.shape[0];
+    if (count == 0 || L == 0 || W == 0) {
+        return 0;
+    }
+    if (L > 65535 || count > 0x7fffffff) {
+        throw std::invalid_argument("too many layers or rows for one launch");
+    }
+    SwapArgs a{};
+    a.topk = topk.data;
+    a.topk64 = topk.dtype == EKV_INT64;
+    a.topk_sl = topk.stride[0];
+    a.topk_sb = topk.stride[1];
+    a.topk_sk = topk.stride[2];
+    a.block_size = static_cast<uint32_t>(block_size);
+    a.block_div = FastDiv(static_cast<uint32_t>(block_size));
+    a.rows = index_ref(rows, 0);
+    a.selected = index_ref(selected, 0);
+    a.slot_base = index_ref(slot_base, 0);
+    a.slots = static_cast<int32_t*>(slots.data);
+    a.sl_l = slots.stride[0], a.sl_b = slots.stride[1], a.sl_o = slots.stride[2];
+    a.misses = static_cast<const int32_t*>(misses.data);
+    a.mi_l = misses.stride[0], a.mi_b = misses.stride[1], a.mi_o = misses.stride[2];
+    a.counts = static_cast<const int32_t*>(counts.data);
+    a.ct_l = counts.stride[0], a.ct_b = counts.stride[1];
+    a.table = static_cast<int32_t*>(table.data);
+    a.tb_l = table.stride[0], a.tb_r = table.stride[1], a.tb_t = table.stride[2], a.table_cols = T;
+    if (bits_p != nullptr) {
+        a.bits = static_cast<int32_t*>(bits_p->data);
+        a.bt_l = bits_p->stride[0], a.bt_r = bits_p->stride[1], a.bt_w = bits_p->stride[2];
+    }
+    a.slot_token = static_cast<int32_t*>(slot_token.data);
+    a.st_l = slot_token.stride[0], a.st_r = slot_token.stride[1], a.st_c = slot_token.stride[2];
+    a.stamps = static_cast<int32_t*>(stamps.data);
+    a.sp_l = stamps.stride[0], a.sp_r = stamps.stride[1], a.sp_c = stamps.stride[2];
+    a.host_table = index_ref(host_table, 0);
+    a.host_table.stride = 1;
+    a.host_sr = host_table.stride[0];
+    a.host_st = host_table.stride[1];
+    a.promote_src = static_cast<int32_t*>(promote_src.data);
+    a.ps_l = promote_src.stride[0], a.ps_b = promote_src.stride[1], a.ps_o = promote_src.stride[2];
+    a.promote_dst = static_cast<int32_t*>(promote_dst.data);
+    a.pd_l = promote_dst.stride[0], a.pd_b = promote_dst.stride[1], a.pd_o = promote_dst.stride[2];
+    a.batch = B;
+    a.table_rows = R;
+    a.capacity = C;
+    a.capacity_pow2 = 1;
+    while (a.capacity_pow2 < C) {
+        a.capacity_pow2 <<= 1;
+    }
+    a.width = static_cast<uint32_t>(W);
+    a.step = step;
+    for (const auto* t : {&topk, &rows, &selected, &slots, &misses, &counts, &table, &slot_token, &stamps,
+                          &slot_base, &host_table, &promote_src, &promote_dst}) {
+        need_data(*t, "tensor");
+    }
+    const size_t lds = static_cast<size_t>(a.capacity_pow2) * sizeof(uint64_t) + static_cast<size_t>(C) * 4;
+    if (lds > 64 * 1024) {
+        check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(swap_in_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)),
+                  "raise the swap-in LDS limit");
+    }
+    const dim3 grid(static_cast<uint32_t>(count), static_cast<uint32_t>(L));
+    swap_in_kernel<<<grid, dim3(kThreads), lds, static_cast<hipStream_t>(stream)>>>(a);
+    check_hip(hipGetLastError(), "launch swap-in");
+    return 0;
+}
+
+}  // namespace
+}  // namespace ekv
+
+extern "C" int ekv_swap_in(const ekv_tensor* topk, int64_t block_size, const ekv_tensor* rows,
+                           const ekv_tensor* selected, const ekv_tensor* slots, const ekv_tensor* misses,
+                           const ekv_tensor* miss_count, const ekv_tensor* table, const ekv_tensor* resident_bits,
+                           const ekv_tensor* slot_token, const ekv_tensor* stamps, const ekv_tensor* slot_base,
+                           const ekv_tensor* host_table, const ekv_tensor* promote_src,
+                           const ekv_tensor* promote_dst, int64_t step, void* stream) {
+    return ekv::guarded(-1, [&] {
+        return ekv::swap_in(topk, block_size, rows, selected, slots, misses, miss_count, table, resident_bits,
+                            slot_token, stamps, slot_base, host_table, promote_src, promote_dst, step, stream);
+    });
+}

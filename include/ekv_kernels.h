@@ -166,6 +166,54 @@ int ekv_gather_kv(const ekv_planes* planes, const ekv_tensor* slots,
 int ekv_scatter_kv(const ekv_planes* planes, const ekv_tensor* slots,
                    const ekv_kv_rows* src, int64_t zero_below, void* stream);
 
+/*
+ * Hot-buffer swap-in with batch-token LRU replacement, run after the lookup.
+ * Policy: benchmarks/hisparse_locality_replay.py:90-99 (misses counted at
+ * entry, hits touched in selection order, least-recent evicted, misses
+ * inserted in selection order). Replaces the policy part of the third-party
+ * load_blocks_to_device_buffer_mha called at
+ * adaptive_sparse/request_residency.py:805-809,829-832.
+ *   topk [L, B, K] + block_size, rows [B], selected [S]: the lookup's inputs
+ *   slots [L, B, W] int32: the lookup's output; miss lanes are patched in place
+ *   misses [L, B, W], miss_count [L, B] int32: the lookup's miss list
+ *   table [L, R, T] int32: token -> global slot (0 = not resident), updated
+ *   resident_bits [L, R, >= ceil(T/32)] int32 or NULL: kept equal to table != 0
+ *   slot_token [L, R, C] int32 (-1 = empty), stamps [L, R, C] int32: LRU state
+ *   slot_base [R]: global slot of local slot 0 of each request's hot buffer
+ *   host_table [R, T]: token -> host row of the pinned host copy
+ *   promote_src / promote_dst [L, B, W] int32: i < miss_count[l, b] get the
+ *   host row and the global slot of the i-th promotion (feed to ekv_move_kv)
+ * Stamps are step * 2W + lane; `step` must grow by one per call and keep
+ * (step + 1) * 2W below 2^31. Tokens must be unique within a row. C <= 8192.
+ */
+int ekv_swap_in(const ekv_tensor* topk, int64_t block_size, const ekv_tensor* rows,
+                const ekv_tensor* selected, const ekv_tensor* slots,
+                const ekv_tensor* misses, const ekv_tensor* miss_count,
+                const ekv_tensor* table, const ekv_tensor* resident_bits,
+                const ekv_tensor* slot_token, const ekv_tensor* stamps,
+                const ekv_tensor* slot_base, const ekv_tensor* host_table,
+                const ekv_tensor* promote_src, const ekv_tensor* promote_dst,
+                int64_t step, void* stream);
+
+/*
+ * Row moves between two plane sets: for i < counts[l, b] and both kv planes,
+ *   dst(l, kv)[dst_rows[l, b, i]] = src(l, kv)[src_rows[l, b, i]]
+ * when 0 <= src row < src->rows and zero_below <= dst row < dst->rows (other
+ * entries move nothing). src may be mapped pinned host memory
+ * (ekv_host_alloc), which makes this the promote-from-host copy.
+ * Replaces the byte movement of load_to_device_per_layer used by
+ * adaptive_sparse/migration.py:232-237 for scattered token rows.
+ */
+int ekv_move_kv(const ekv_planes* src, const ekv_tensor* src_rows,
+                const ekv_planes* dst, const ekv_tensor* dst_rows,
+                const ekv_tensor* counts, int64_t zero_below, void* stream);
+
+/* Pinned host memory (hipHostMalloc) plus the device pointer kernels use to
+ * read and write it. Free with ekv_host_free(host). No reference counterpart
+ * (the reference's pinned pools are SGLang's HostKVCache). */
+int ekv_host_alloc(uint64_t bytes, void** host, void** device);
+int ekv_host_free(void* host);
+
 #ifdef __cplusplus
 }
 #endif

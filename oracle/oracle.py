@@ -138,6 +138,54 @@ def lru_misses(steps, capacity):
     return result
 
 
+def swap_in(step, block_size, topk, rows, selected, slots, misses, counts, table, slot_token, stamps, slot_base,
+            host_table):
+    """Batch-token LRU swap-in after a lookup, on numpy arrays (copies are returned).
+
+    Per selected row b (request r = rows[b]) of every layer: hits touch their
+    slot (stamp = step*2W + lane), the m = counts[l, b] misses take the m
+    slots with the smallest (stamp, slot) - empty slots (-2^31) first - in
+    lane order; a victim's old token leaves the table, the new token enters
+    it, its stamp becomes step*2W + W + lane, and promotion i records
+    (host_table[r, token], global slot). Returns a dict of the new arrays.
+    """
+    topk = np.asarray(topk, dtype=np.int64)
+    L, B, K = topk.shape
+    W = K * block_size
+    slots = np.array(slots, dtype=np.int32, copy=True)
+    table = np.array(table, dtype=np.int32, copy=True)
+    slot_token = np.array(slot_token, dtype=np.int32, copy=True)
+    stamps = np.array(stamps, dtype=np.int64, copy=True)
+    C = slot_token.shape[2]
+    src = np.full((L, B, W), -1, dtype=np.int32)
+    dst = np.full((L, B, W), -1, dtype=np.int32)
+    for layer in range(L):
+        for b in selected:
+            r = int(rows[b])
+            base = int(slot_base[r])
+            stamp = stamps[layer, r]
+            for lane in range(W):
+                slot = int(slots[layer, b, lane])
+                if slot > 0 and 0 <= slot - base < C:
+                    stamp[slot - base] = step * 2 * W + lane
+            order = sorted(range(C), key=lambda v: (stamp[v], v))
+            for i in range(int(counts[layer, b])):
+                victim = order[i]
+                lane = int(misses[layer, b, i])
+                token = int(topk[layer, b, lane // block_size]) * block_size + lane % block_size
+                old = int(slot_token[layer, r, victim])
+                if old >= 0:
+                    table[layer, r, old] = 0
+                table[layer, r, token] = base + victim
+                slot_token[layer, r, victim] = token
+                stamp[victim] = step * 2 * W + W + lane
+                src[layer, b, i] = host_table[r, token]
+                dst[layer, b, i] = base + victim
+                slots[layer, b, lane] = base + victim
+    return {"slots": slots, "table": table, "slot_token": slot_token, "stamps": stamps.astype(np.int32),
+            "promote_src": src, "promote_dst": dst}
+
+
 # ---------------------------------------------------------------- gathers (numpy)
 
 def gather_rows(raw, positions, request_ids, lengths, request_table, slot_offsets, width,

@@ -1,0 +1,104 @@
+"""GPU parity of the LRU swap-in and the promote-from-host copy against the oracle.
+
+Each step: HIP lookup (bitmap) -> HIP swap-in -> promote from pinned host
+(move_kv) -> gather. After every step the whole LRU state (table, bitmap,
+slot owners, stamps), the patched slots and the promotion lists must equal
+the oracle's, and every gathered K/V row must equal the pinned-host row of
+its token.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from adaptive_sparse.host_arena import HostArena
+from adaptive_sparse.kv_pool import KVPlanes
+from adaptive_sparse.resident_lookup import resolve_resident
+from adaptive_sparse.sparse_read import gather_kv
+from adaptive_sparse.swap_in import HotBuffers, move_kv, swap_in
+from oracle import oracle as ref
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("capacity", [64, 50])
+def test_lookup_swap_promote_gather_cycle(gpu, capacity):
+    L, R, T, K, row_bytes = 2, 3, 300, 32, 64
+    rng = np.random.default_rng(capacity)
+    buffers = HotBuffers(L, R, T, capacity, gpu)
+    # Start with the 40 most recent tokens resident in random slots.
+    recent = torch.arange(T - 40, T).expand(L, R, 40)
+    local = torch.stack([torch.stack([torch.tensor(rng.permutation(capacity)[:40]) for _ in range(R)])
+                         for _ in range(L)])
+    buffers.install(recent, local)
+    host_table = torch.arange(R * T, dtype=torch.int32).reshape(R, T)
+    plane = R * T * row_bytes
+    arena = HostArena(L * 2 * plane)
+    try:
+        arena.host.copy_(torch.randint(0, 256, (L * 2 * plane,), dtype=torch.uint8))
+        host_planes = KVPlanes(base=arena.device_ptr, device=0, layers=L, kv=2, layer_stride=2 * plane,
+                               kv_stride=plane, row_stride=row_bytes, row_bytes=row_bytes, rows=R * T, owner=arena)
+        pool_rows = 1 + R * capacity
+        pool = torch.zeros(L * 2 * pool_rows * row_bytes, dtype=torch.uint8, device=gpu)
+        pool_planes = KVPlanes(base=pool.data_ptr(), device=0, layers=L, kv=2, layer_stride=2 * pool_rows * row_bytes,
+                               kv_stride=pool_rows * row_bytes, row_stride=row_bytes, row_bytes=row_bytes,
+                               rows=pool_rows, owner=pool)
+        # Prefill the resident rows from the host copy (as a promotion of the installed tokens).
+        first_src = host_table.to(gpu)[torch.arange(R).view(1, R, 1), recent.to(gpu)].expand(L, R, 40).contiguous()
+        first_dst = (local.to(gpu) + buffers.slot_base.view(1, R, 1)).to(torch.int32).contiguous()
+        move_kv(host_planes, first_src.to(torch.int32), pool_planes, first_dst,
+                torch.full((L, R), 40, dtype=torch.int32, device=gpu))
+        host = arena.host.numpy().reshape(L, 2, R * T, row_bytes)
+        rows = torch.arange(R, device=gpu)
+        lengths = torch.full((R,), T, dtype=torch.int32, device=gpu)
+        state = {"table": buffers.table.cpu().numpy(), "slot_token": buffers.slot_token.cpu().numpy(),
+                 "stamps": buffers.stamps.cpu().numpy()}
+        for step in range(6):
+            near = [np.concatenate([rng.choice(np.arange(T - 50, T), 24, replace=False),
+                                    rng.choice(np.arange(0, T - 50), 8, replace=False)])
+                    for _ in range(L * R)]
+            topk = np.stack([rng.permutation(x) for x in near]).reshape(L, R, K)
+            topk_d = torch.tensor(topk, dtype=torch.int32, device=gpu)
+            slots = torch.empty((L, R, K), dtype=torch.int32, device=gpu)
+            misses = torch.full((L, R, K), -1, dtype=torch.int32, device=gpu)
+            counts = torch.empty((L, R), dtype=torch.int32, device=gpu)
+            resolve_resident(topk_d, buffers.table, None, rows, lengths, rows, slots, 1, misses=misses,
+                             miss_count=counts, resident_bits=buffers.bits)
+            want_slots, want_misses, want_counts = ref.resolve_resident(
+                topk, state["table"], None, np.arange(R), np.full(R, T), np.arange(R), 1,
+                np.zeros((L, R, K), np.int32), with_misses=True)
+            assert np.array_equal(slots.cpu().numpy(), want_slots), step
+            assert np.array_equal(counts.cpu().numpy(), want_counts), step
+            miss_np = np.full((L, R, K), -1, np.int32)
+            for (layer, r), lanes in want_misses.items():
+                miss_np[layer, r, :len(lanes)] = lanes
+            promote_src = torch.full((L, R, K), -9, dtype=torch.int32, device=gpu)
+            promote_dst = torch.full((L, R, K), -9, dtype=torch.int32, device=gpu)
+            swap_in(topk_d, 1, rows, rows, slots, misses, counts, buffers, host_table.to(gpu), promote_src,
+                    promote_dst)
+            state = ref.swap_in(step, 1, topk, np.arange(R), np.arange(R), want_slots, miss_np, want_counts,
+                                state["table"], state["slot_token"], state["stamps"],
+                                buffers.slot_base.cpu().numpy(), host_table.numpy())
+            assert np.array_equal(slots.cpu().numpy(), state["slots"]), step
+            assert np.array_equal(buffers.table.cpu().numpy(), state["table"]), step
+            assert np.array_equal(buffers.slot_token.cpu().numpy(), state["slot_token"]), step
+            assert np.array_equal(buffers.stamps.cpu().numpy(), state["stamps"]), step
+            assert np.array_equal(buffers.bits.cpu().numpy(), ref.residency_bits(state["table"])), step
+            got_src, got_dst = promote_src.cpu().numpy(), promote_dst.cpu().numpy()
+            for layer in range(L):
+                for r in range(R):
+                    c = want_counts[layer, r]
+                    assert np.array_equal(got_src[layer, r, :c], state["promote_src"][layer, r, :c])
+                    assert np.array_equal(got_dst[layer, r, :c], state["promote_dst"][layer, r, :c])
+            move_kv(host_planes, promote_src, pool_planes, promote_dst, counts)
+            out = torch.empty((R, L, 2, K, row_bytes), dtype=torch.uint8, device=gpu)
+            gather_kv(pool_planes, slots, out)
+            got = out.cpu().numpy()
+            for layer in range(L):
+                for r in range(R):
+                    host_rows = host_table.numpy()[r, topk[layer, r]]
+                    for kv in range(2):
+                        assert np.array_equal(got[r, layer, kv], host[layer, kv, host_rows]), (step, layer, r, kv)
+    finally:
+        torch.cuda.synchronize()
+        arena.close()

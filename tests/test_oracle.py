@@ -332,3 +332,56 @@ def test_residency_bits_little_endian_words():
     assert words.shape == (2, 3)
     assert words[0].tolist() == [1 | (1 << 31), 1, 1 << 5]
     assert words[1].tolist() == [0, 1 << 1, 0]
+
+
+def _lookup_swap_steps(step_tokens, capacity, context, block_size=1):
+    """Drive lookup + swap-in for one (layer, request) stream; returns per-step miss counts."""
+    from collections import OrderedDict
+
+    table = np.zeros((1, 1, context), np.int32)
+    slot_token = np.full((1, 1, capacity), -1, np.int32)
+    stamps = np.full((1, 1, capacity), -(1 << 31), np.int32)
+    host_table = np.arange(context)[None] + 1000
+    model = OrderedDict()
+    misses_per_step = []
+    for step, tokens in enumerate(step_tokens):
+        K = max(len(t) for t in step_tokens)
+        topk = np.full((1, 1, K), -1, np.int64)
+        topk[0, 0, :len(tokens)] = tokens
+        out, miss_lists, counts = ref.resolve_resident(topk, table[0], None, [0], [context], [0], block_size,
+                                                       np.zeros((1, 1, K), np.int32), with_misses=True)
+        miss = np.zeros((1, 1, K), np.int32)
+        lanes = miss_lists[(0, 0)]
+        miss[0, 0, :len(lanes)] = lanes
+        state = ref.swap_in(step, block_size, topk, [0], [0], out, miss, counts, table, slot_token, stamps,
+                            [1], host_table)
+        table, slot_token, stamps = state["table"], state["slot_token"], state["stamps"]
+        misses_per_step.append(int(counts[0, 0]))
+        # every selected token is now resident, in the slot the patched output names
+        assert all(state["slots"][0, 0, i] == table[0, 0, t] > 0 for i, t in enumerate(tokens))
+        assert state["promote_src"][0, 0, :counts[0, 0]].tolist() == [1000 + tokens[i] for i in lanes]
+        # the cache contents equal an OrderedDict run of the reference policy
+        missing = [t for t in tokens if t not in model]
+        for t in tokens:
+            if t in model:
+                model.move_to_end(t)
+        while len(model) + len(missing) > capacity:
+            model.popitem(last=False)
+        model.update((t, None) for t in missing)
+        assert set(np.nonzero(table[0, 0])[0].tolist()) == set(model)
+        assert sorted(slot_token[0, 0][slot_token[0, 0] >= 0].tolist()) == sorted(model)
+    return misses_per_step
+
+
+def test_swap_in_reproduces_reference_lru_kat():
+    """tests/test_hisparse_locality_replay.py:15-24 through lookup + swap-in."""
+    steps = [[0, 1], [2, 0], [1, 0]]
+    assert _lookup_swap_steps(steps, capacity=2, context=4) == ref.lru_misses(steps, 2) == [2, 1, 1]
+    assert _lookup_swap_steps(steps, capacity=3, context=4) == ref.lru_misses(steps, 3) == [2, 1, 0]
+
+
+def test_swap_in_matches_lru_replay_on_random_streams():
+    rng = random.Random(29)
+    for capacity, context, k in ((8, 40, 6), (16, 100, 16), (5, 12, 5)):
+        steps = [rng.sample(range(context), rng.randint(1, k)) for _ in range(40)]
+        assert _lookup_swap_steps(steps, capacity, context) == ref.lru_misses(steps, capacity)
