@@ -20,6 +20,12 @@ Other workloads (same JSON contract, for the other configurations):
                 128, block tables from a permutation of a 20k-block pool
   migration     per tick: 512 scattered 2.25 MiB blocks packed, copied to
                 pinned host and back, unpacked into freshly mapped chunks
+  composite     elastic decode step: 128 requests with contexts uniform in
+                [4096, 32768], 60 layers x 2 heads x 128, Top-K 2048 with the
+                decode-read locality mix, hot capacity 4096 (LRU); per step
+                5 % of pool chunks are unmapped and remapped (their hot slots
+                invalidated), then lookup + compaction, LRU swap-in, promote
+                of misses from pinned host, gather
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -54,7 +60,9 @@ def parse_args():
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--workload", default="decode-read",
-                        choices=["decode-read", "topk-gather", "block-gather", "migration"])
+                        choices=["decode-read", "topk-gather", "block-gather", "migration", "composite"])
+    parser.add_argument("--remap-fraction", type=float, default=0.05,
+                        help="share of pool chunks unmapped and remapped per composite step")
     parser.add_argument("--capacity", type=int, default=4096, help="hot slots per request (decode-read)")
     parser.add_argument("--seed", type=int, default=2024)
     parser.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample")
@@ -568,8 +576,178 @@ def run_migration(torch, args, device):
     return result
 
 
+# ------------------------------------------------------------------ composite (config 5)
+
+
+def composite_topk(torch, device, L, R, K, lengths, gen, recent_window=4096):
+    """Per (layer, request): K unique tokens, 80 % from the last 4096 of the request's context, 20 % from the rest."""
+    T = int(lengths.max())
+    uniform_want = K - (K * 4) // 5
+    older = (lengths - recent_window).clamp_min(0)                               # [R]
+    u_count = torch.minimum(older, torch.full_like(older, uniform_want))         # uniform picks per request
+    r_count = K - u_count
+    recent = torch.rand((L, R, recent_window), generator=gen, device=device).argsort(-1)[..., :K]
+    recent = recent + older.view(1, R, 1)
+    keys = torch.rand((L, R, T), generator=gen, device=device)
+    keys.masked_fill_(torch.arange(T, device=device).view(1, 1, T) >= older.view(1, R, 1), 2.0)
+    uniform = keys.topk(uniform_want, dim=-1, largest=False).indices              # valid where < older
+    del keys
+    lane = torch.arange(K, device=device).view(1, 1, K)
+    take_recent = lane < r_count.view(1, R, 1)
+    pick = torch.where(take_recent, recent, torch.gather(uniform, -1, (lane - r_count.view(1, R, 1)).clamp(0, uniform_want - 1)))
+    order = torch.rand((L, R, K), generator=gen, device=device).argsort(-1)
+    return torch.gather(pick, -1, order).to(torch.int32).contiguous()
+
+
+def run_composite(torch, args, device):
+    import numpy as np
+
+    from adaptive_sparse.host_arena import HostArena
+    from adaptive_sparse.kv_pool import KVPlanes, PlanePoolLayout
+    from adaptive_sparse.resident_lookup import build_residency_bits, resolve_resident
+    from adaptive_sparse.sparse_read import gather_kv
+    from adaptive_sparse.swap_in import INT32_MIN, HotBuffers, move_kv, swap_in
+
+    L, R, K, C, HOST_ROWS = 60, 128, 2048, 4096, 65536
+    row_bytes = 512
+    gen = torch.Generator(device=device).manual_seed(args.seed)
+    lengths = torch.randint(4096, 32769, (R,), generator=gen, device=device)
+    T = int(lengths.max())
+    layout = PlanePoolLayout(layers=L, kv=2, rows=1 + R * C, row_bytes=row_bytes)
+    backing, raw, commit_s = make_pool(torch, layout, device, args.seed + 1)
+    planes = layout.kv_planes(backing.base, 0, owner=backing)
+    # Pinned, device-mapped host copy: 65,536 rows per plane; token t of request r lives at row (r*T + t) % rows.
+    host_plane = HOST_ROWS * row_bytes
+    arena = HostArena(2 * L * host_plane)
+    fill = torch.empty(host_plane, dtype=torch.uint8, device=device)
+    for p in range(2 * L):
+        fill.view(torch.bfloat16).normal_(generator=gen)
+        arena.host.narrow(0, p * host_plane, host_plane).copy_(fill)
+    del fill
+    host_planes = KVPlanes(base=arena.device_ptr, device=0, layers=L, kv=2, layer_stride=2 * host_plane,
+                           kv_stride=host_plane, row_stride=row_bytes, row_bytes=row_bytes, rows=HOST_ROWS, owner=arena)
+    host_table = ((torch.arange(R, device=device).view(R, 1) * T + torch.arange(T, device=device).view(1, T))
+                  % HOST_ROWS).to(torch.int32)
+    buffers = HotBuffers(L, R, T, C, device)
+    recent = (lengths.view(1, R, 1) - C + torch.arange(C, device=device).view(1, 1, C)).expand(L, R, C)
+    local = torch.rand((L, R, C), generator=gen, device=device).argsort(-1)
+    buffers.install(recent, local)
+    rows = torch.arange(R, device=device)
+    lengths32 = lengths.to(torch.int32)
+    # Prefill the hot rows from the host copy.
+    all_lanes = torch.full((L, R), C, dtype=torch.int32, device=device)
+    move_kv(host_planes, host_table[rows.view(1, R, 1), recent].to(torch.int32).contiguous(), planes,
+            (local + buffers.slot_base.view(1, R, 1)).to(torch.int32).contiguous(), all_lanes)
+    slots = torch.empty((L, R, K), dtype=torch.int32, device=device)
+    misses = torch.empty_like(slots)
+    counts = torch.empty((L, R), dtype=torch.int32, device=device)
+    promote_src = torch.empty_like(slots)
+    promote_dst = torch.empty_like(slots)
+    output = torch.empty((R, L, 2, K, 256), dtype=torch.bfloat16, device=device)
+    chunk_rows = layout.chunk_bytes // row_bytes
+    remap_count = int(round(args.remap_fraction * backing.chunk_count))
+    rng = np.random.default_rng(args.seed)
+    torch.cuda.synchronize()
+    log(f"composite ready: T={T}, host arena {arena.nbytes / 1e9:.1f} GB, remap {remap_count} chunks/step")
+
+    def remap():
+        """Unmap + remap `remap_count` random chunks (never chunk 0); their hot slots become empty."""
+        chosen = rng.choice(np.arange(1, backing.chunk_count), size=remap_count, replace=False)
+        ids = torch.tensor(chosen, device=device)
+        plane, within = ids // layout.plane_chunks, ids % layout.plane_chunks
+        slot = (within.view(-1, 1) * chunk_rows + torch.arange(chunk_rows, device=device).view(1, -1))
+        layer = (plane // 2).view(-1, 1).expand_as(slot)
+        keep = (slot >= 1) & (slot < layout.rows)
+        slot, layer = slot[keep], layer[keep]
+        req, loc = (slot - 1) // C, (slot - 1) % C
+        token = buffers.slot_token[layer, req, loc].long()
+        held = token >= 0
+        buffers.table[layer[held], req[held], token[held]] = 0
+        buffers.slot_token[layer, req, loc] = -1
+        buffers.stamps[layer, req, loc] = INT32_MIN
+        build_residency_bits(buffers.table, out=buffers.bits)
+        backing.reclaim(chosen.tolist())          # synchronizes, then hipMemUnmap + release
+        backing.ensure(chosen.tolist())           # hipMemCreate + map + access + zero fill
+
+    def lookup():
+        resolve_resident(topk, buffers.table, None, rows, lengths32, rows, slots, 1, misses=misses,
+                         miss_count=counts, resident_bits=buffers.bits)
+
+    def swap():
+        swap_in(topk, 1, rows, rows, slots, misses, counts, buffers, host_table, promote_src, promote_dst)
+
+    def promote():
+        move_kv(host_planes, promote_src, planes, promote_dst, counts)
+
+    def gather():
+        gather_kv(planes, slots, output)
+
+    phases = {name: [] for name in ("remap_ms", "lookup_ms", "swap_ms", "promote_ms", "gather_ms", "step_ms")}
+    promoted, verified = [], True
+    for step in range(args.warmup + args.steps):
+        topk = composite_topk(torch, device, L, R, K, lengths, gen)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        if remap_count:
+            remap()
+        t1 = time.perf_counter()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+        ev[0].record()
+        lookup()
+        ev[1].record()
+        swap()
+        ev[2].record()
+        promote()
+        ev[3].record()
+        gather()
+        ev[4].record()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        promoted.append(int(counts.sum().item()))
+        if step == args.warmup + args.steps - 1 or step == 0:
+            # every lane is resident now: its gathered rows must be its token's host rows
+            for layer in (0, L - 1):
+                host_rows = torch.gather(host_table, 1, topk[layer].long()).long()        # [R, K]
+                for kv in range(2):
+                    base = (layer * 2 + kv) * host_plane
+                    expect = arena.host.narrow(0, base, host_plane).view(HOST_ROWS, row_bytes)[host_rows.cpu()]
+                    got = output[:, layer, kv].contiguous().view(torch.uint8).view(R, K, row_bytes).cpu()
+                    verified &= bool(torch.equal(got, expect))
+        if step >= args.warmup:
+            phases["remap_ms"].append((t1 - t0) * 1e3)
+            for i, name in enumerate(("lookup_ms", "swap_ms", "promote_ms", "gather_ms")):
+                phases[name].append(ev[i].elapsed_time(ev[i + 1]))
+            phases["step_ms"].append((t2 - t0) * 1e3)
+    mean = {k: statistics.mean(v) for k, v in phases.items()}
+    lanes = L * R * K
+    misses_per_step = statistics.mean(promoted[args.warmup:])
+    gather_bytes = lanes * 2 * row_bytes * 2 + lanes * 4             # every lane resident after promotion
+    promote_bytes = misses_per_step * 2 * row_bytes
+    log(f"step {mean['step_ms']:.1f} ms = remap {mean['remap_ms']:.1f} + lookup {mean['lookup_ms']:.3f} + swap "
+        f"{mean['swap_ms']:.3f} + promote {mean['promote_ms']:.2f} + gather {mean['gather_ms']:.2f} ms; "
+        f"{misses_per_step / lanes:.3f} of lanes promoted; verified {verified}")
+    config = {"workload": "composite-elastic-decode", "requests": R, "context": "uniform [4096, 32768]", "layers": L,
+              "kv_heads": 2, "head_dim": 128, "topk": K, "hot_capacity": C, "remap_fraction": args.remap_fraction,
+              "host_rows_per_plane": HOST_ROWS}
+    achieved = gather_bytes / (mean["gather_ms"] / 1e3) / 1e9
+    roof = roofline(achieved, "copy_small_rows<KvGather,16> (ekv_gather_kv)", gather_bytes, mean["gather_ms"], None)
+    extra = {"verified_against_host_copy": verified, "phase_ms": {k: round(v, 3) for k, v in mean.items()},
+             "promoted_rows_per_step": round(misses_per_step), "promoted_fraction": round(misses_per_step / lanes, 4),
+             "promote_gbs_over_pcie": round(promote_bytes / (mean["promote_ms"] / 1e3) / 1e9, 2),
+             "lookups_per_s": round(lanes / (mean["lookup_ms"] / 1e3), 1),
+             "step_ms_without_remap": round(mean["step_ms"] - mean["remap_ms"], 3),
+             "remapped_chunks_per_step": remap_count, "pool_commit_s": round(commit_s, 3)}
+    result = envelope(args, gather_bytes / (mean["step_ms"] / 1e3) / 1e9, mean["step_ms"], config, roof, None, extra,
+                      metric="composite decode step: gathered GB/s per step (lookup, LRU swap-in, promote, gather, remap)")
+    del raw, output
+    torch.cuda.synchronize()
+    backing.close()
+    arena.close()
+    return result
+
+
 WORKLOADS = {"decode-read": run_decode_read, "topk-gather": run_topk_gather,
-             "block-gather": run_block_gather, "migration": run_migration}
+             "block-gather": run_block_gather, "migration": run_migration, "composite": run_composite}
 
 
 def main():
