@@ -254,6 +254,17 @@ def run_decode_read(torch, args, device):
     gather_bytes = lanes * 2 * row_bytes + hits * 2 * row_bytes + lanes * 4
     step_ms, phase = timed_steps(torch, args.steps, [("lookup", lookup), ("gather", gather)])
     _, plain_phase = timed_steps(torch, max(3, args.steps // 2), [("lookup", lookup_plain)])
+    # Reference points of the same engine on the same shapes: sequential slots
+    # (every row read, contiguous) and all-miss slots (write-only zero fill).
+    seq = (torch.arange(K, device=device, dtype=torch.int32).view(1, 1, K) + 1
+           + torch.arange(R, device=device, dtype=torch.int32).view(1, R, 1) * C).expand(L, R, K).contiguous()
+    none = torch.zeros_like(slots)
+    ceilings = {}
+    for name, probe, nbytes in (("sequential_all_hit", seq, lanes * 2048 + lanes * 4),
+                                ("all_miss_write_only", none, lanes * 1024 + lanes * 4)):
+        _, ph = timed_steps(torch, 5, [("g", lambda s=probe: gather_kv(planes, s, output))])
+        ceilings[name] = round(nbytes / (ph["g"] / 1e3) / 1e9, 1)
+    del seq, none
     lookup()
     torch.cuda.synchronize()
     achieved = gather_bytes / (phase["gather"] / 1e3) / 1e9
@@ -301,6 +312,7 @@ def run_decode_read(torch, args, device):
              "lookup_gbs": round(lookup_bytes / (phase["lookup"] / 1e3) / 1e9, 1),
              "lookup_us_without_bitmap": round(plain_phase["lookup"] * 1e3, 2),
              "lookup_bitmap_matches_plain": same,
+             "engine_gbs_same_shapes": ceilings,
              "hit_rate": round(hits / lanes, 4), "pool_commit_s": round(commit_s, 3)}
     roof = roofline(achieved, "copy_small_rows<KvGather,16> (ekv_gather_kv)", gather_bytes, phase["gather"],
                     read_traffic("gather_kv_hisparse_decode.md"))
@@ -650,8 +662,11 @@ def run_composite(torch, args, device):
     torch.cuda.synchronize()
     log(f"composite ready: T={T}, host arena {arena.nbytes / 1e9:.1f} GB, remap {remap_count} chunks/step")
 
+    remap_parts = {"invalidate_ms": [], "unmap_ms": [], "map_ms": []}
+
     def remap():
         """Unmap + remap `remap_count` random chunks (never chunk 0); their hot slots become empty."""
+        r0 = time.perf_counter()
         chosen = rng.choice(np.arange(1, backing.chunk_count), size=remap_count, replace=False)
         ids = torch.tensor(chosen, device=device)
         plane, within = ids // layout.plane_chunks, ids % layout.plane_chunks
@@ -666,8 +681,14 @@ def run_composite(torch, args, device):
         buffers.slot_token[layer, req, loc] = -1
         buffers.stamps[layer, req, loc] = INT32_MIN
         build_residency_bits(buffers.table, out=buffers.bits)
+        torch.cuda.synchronize()
+        r1 = time.perf_counter()
         backing.reclaim(chosen.tolist())          # synchronizes, then hipMemUnmap + release
+        r2 = time.perf_counter()
         backing.ensure(chosen.tolist())           # hipMemCreate + map + access + zero fill
+        r3 = time.perf_counter()
+        for key, value in zip(remap_parts, (r1 - r0, r2 - r1, r3 - r2)):
+            remap_parts[key].append(value * 1e3)
 
     def lookup():
         resolve_resident(topk, buffers.table, None, rows, lengths32, rows, slots, 1, misses=misses,
@@ -736,6 +757,7 @@ def run_composite(torch, args, device):
              "promote_gbs_over_pcie": round(promote_bytes / (mean["promote_ms"] / 1e3) / 1e9, 2),
              "lookups_per_s": round(lanes / (mean["lookup_ms"] / 1e3), 1),
              "step_ms_without_remap": round(mean["step_ms"] - mean["remap_ms"], 3),
+             "remap_parts_ms": {k: round(statistics.mean(v[args.warmup:] or v), 2) for k, v in remap_parts.items()},
              "remapped_chunks_per_step": remap_count, "pool_commit_s": round(commit_s, 3)}
     result = envelope(args, gather_bytes / (mean["step_ms"] / 1e3) / 1e9, mean["step_ms"], config, roof, None, extra,
                       metric="composite decode step: gathered GB/s per step (lookup, LRU swap-in, promote, gather, remap)")

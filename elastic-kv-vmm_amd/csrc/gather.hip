@@ -201,11 +201,22 @@ __device__ __forceinline__ void locate(const EngineArgs& a, int64_t u, int64_t& 
     }
 }
 
+#ifndef EKV_COPY_NT_LOAD
+#define EKV_COPY_NT_LOAD 0
+#endif
+#ifndef EKV_COPY_NT_STORE
+#define EKV_COPY_NT_STORE 1
+#endif
+
 template <int VW>
 __device__ __forceinline__ typename Vec<VW>::type load_vec(const char* p, bool aligned) {
     using V = typename Vec<VW>::type;
     if (aligned) {
+#if EKV_COPY_NT_LOAD
+        return __builtin_nontemporal_load(reinterpret_cast<const V*>(p));
+#else
         return *reinterpret_cast<const V*>(p);
+#endif
     }
     V v;
     __builtin_memcpy(&v, p, VW);
@@ -215,7 +226,11 @@ __device__ __forceinline__ typename Vec<VW>::type load_vec(const char* p, bool a
 template <int VW>
 __device__ __forceinline__ void store_vec(char* p, typename Vec<VW>::type v) {
     using V = typename Vec<VW>::type;
+#if EKV_COPY_NT_STORE
     __builtin_nontemporal_store(v, reinterpret_cast<V*>(p));
+#else
+    *reinterpret_cast<V*>(p) = v;
+#endif
 }
 
 __device__ __forceinline__ int64_t tile_of(const EngineArgs& a, int64_t iteration_tile) {

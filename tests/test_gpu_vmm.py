@@ -180,3 +180,79 @@ def test_gather_rows_through_vmm_arena(gpu, coracle, width):
         assert before - arena.backing.backed_bytes == layout.request_bytes
     finally:
         arena.close()
+
+
+def test_decode_step_graph_replays_across_remap(gpu):
+    """Lookup + compaction + gather captured in one graph, replayed with new Top-K
+    contents and across a reclaim/recommit of pool chunks (stable VA); every
+    replay must equal an eager run of the same step."""
+    from adaptive_sparse.kv_pool import PlanePoolLayout
+    from adaptive_sparse.resident_lookup import build_residency_bits, resolve_resident
+    from adaptive_sparse.sparse_read import gather_kv
+
+    L, R, T, K, C = 3, 4, 2048, 64, 256
+    layout = PlanePoolLayout(layers=L, kv=2, rows=1 + R * C, row_bytes=512)
+    backing = Backing(layout.capacity_bytes, layout.chunk_bytes, device=0)
+    try:
+        backing.ensure(range(backing.chunk_count))
+        raw = backing.raw
+        gen = torch.Generator(device=gpu).manual_seed(5)
+        raw.view(torch.bfloat16).normal_(generator=gen)
+        planes = layout.kv_planes(backing.base, 0, owner=backing)
+        table = torch.zeros((L, R, T), dtype=torch.int32, device=gpu)
+        perm = torch.rand((L, R, C), generator=gen, device=gpu).argsort(-1).to(torch.int32)
+        table[:, :, T - C:] = perm + (torch.arange(R, device=gpu, dtype=torch.int32) * C + 1).view(1, R, 1)
+        bits = build_residency_bits(table)
+        rows = torch.arange(R, device=gpu)
+        lengths = torch.full((R,), T, dtype=torch.int32, device=gpu)
+        topk = torch.zeros((L, R, K), dtype=torch.int32, device=gpu)
+        slots = torch.zeros((L, R, K), dtype=torch.int32, device=gpu)
+        misses = torch.zeros_like(slots)
+        counts = torch.zeros((L, R), dtype=torch.int32, device=gpu)
+        out = torch.zeros((R, L, 2, K, 256), dtype=torch.bfloat16, device=gpu)
+
+        def step():
+            resolve_resident(topk, table, None, rows, lengths, rows, slots, 1, misses=misses, miss_count=counts,
+                             resident_bits=bits)
+            gather_kv(planes, slots, out)
+
+        def new_topk(seed):
+            g = torch.Generator(device=gpu).manual_seed(seed)
+            picks = torch.rand((L, R, T), generator=g, device=gpu).argsort(-1)[..., :K]
+            topk.copy_(picks.to(torch.int32))
+
+        new_topk(0)
+        step()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        for seed in range(1, 6):
+            new_topk(seed)
+            step()                                   # eager reference of this step
+            eager = (slots.clone(), misses.clone(), counts.clone(), out.clone())
+            slots.zero_(), misses.zero_(), counts.zero_(), out.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(slots, eager[0]) and torch.equal(counts, eager[2]), seed
+            assert torch.equal(out, eager[3]), seed
+            for l in range(L):
+                for r in range(R):
+                    c = int(counts[l, r])
+                    assert torch.equal(misses[l, r, :c], eager[1][l, r, :c])
+            if seed == 3:
+                # Unmap and recommit a pool chunk between replays (same VA, zero-filled), then
+                # restore its bytes: the graph keeps working against the stable address.
+                chunk = backing.chunk_count - 1
+                saved = raw.narrow(0, chunk * layout.chunk_bytes, layout.chunk_bytes).clone()
+                torch.cuda.synchronize()
+                assert backing.reclaim([chunk], synchronize=False) == 1
+                assert backing.ensure([chunk]) == 1
+                restored = raw.narrow(0, chunk * layout.chunk_bytes, layout.chunk_bytes)
+                assert torch.count_nonzero(restored).item() == 0
+                restored.copy_(saved)
+                assert backing.raw.data_ptr() == backing.base
+        del graph
+    finally:
+        torch.cuda.synchronize()
+        backing.close()
