@@ -143,6 +143,35 @@ def timed_steps(torch, steps, phases):
     return wall_ms, per_phase
 
 
+def back_to_back_ms(torch, fn, reps=20):
+    """Mean event time (ms) of `reps` consecutive calls of fn on the current stream."""
+    fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        fn()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / reps
+
+
+def graph_replay_ms(torch, fn, reps=10):
+    """Mean event time (ms) of one replay of a HIP graph capturing fn."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    ms = back_to_back_ms(torch, graph.replay, reps)
+    del graph
+    return ms
+
+
 def roofline(achieved_gbs, kernel, algorithmic_bytes, avg_ms, traffic):
     return {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kernel,
@@ -265,12 +294,27 @@ def run_decode_read(torch, args, device):
         _, ph = timed_steps(torch, 5, [("g", lambda s=probe: gather_kv(planes, s, output))])
         ceilings[name] = round(nbytes / (ph["g"] / 1e3) / 1e9, 1)
     del seq, none
+    # The lookup alone: back-to-back launches of the 60-layer lookup, and one
+    # launch per layer (as a decode step interleaved with attention issues
+    # them) replayed from a HIP graph.
+    lookup_alone_ms = back_to_back_ms(torch, lookup)
+    per_layer = [(topk[l:l + 1], table[l:l + 1], bits[l:l + 1], slots[l:l + 1], misses[l:l + 1], counts[l:l + 1])
+                 for l in range(L)]
+
+    def lookup_by_layer():
+        for tk, tb, bt, sl, ms, ct in per_layer:
+            resolve_resident(tk, tb, None, rows, lengths, rows, sl, 1, misses=ms, miss_count=ct, resident_bits=bt)
+
+    per_layer_graph_ms = graph_replay_ms(torch, lookup_by_layer)
+    del per_layer
     lookup()
+    gather()  # the probes above overwrote the output
     torch.cuda.synchronize()
     achieved = gather_bytes / (phase["gather"] / 1e3) / 1e9
     log(f"step {step_ms:.3f} ms, gather {phase['gather']:.3f} ms ({achieved:.0f} GB/s), "
-        f"lookup {phase['lookup'] * 1e3:.1f} us with the residency bitmap "
-        f"({plain_phase['lookup'] * 1e3:.1f} us without), identical results {same}")
+        f"lookup {phase['lookup'] * 1e3:.1f} us in the step with the residency bitmap "
+        f"({plain_phase['lookup'] * 1e3:.1f} us without), {lookup_alone_ms * 1e3:.1f} us back to back, "
+        f"{per_layer_graph_ms * 1e3 / L:.2f} us per one-layer launch in a graph, identical results {same}")
 
     baseline = None
     if not args.no_cpu_baseline:
@@ -310,6 +354,8 @@ def run_decode_read(torch, args, device):
              "lookup_us_per_step": round(phase["lookup"] * 1e3, 2),
              "lookup_us_per_layer": round(phase["lookup"] * 1e3 / L, 2),
              "lookup_gbs": round(lookup_bytes / (phase["lookup"] / 1e3) / 1e9, 1),
+             "lookup_us_back_to_back": round(lookup_alone_ms * 1e3, 2),
+             "lookup_us_per_layer_launch_graph": round(per_layer_graph_ms * 1e3 / L, 2),
              "lookup_us_without_bitmap": round(plain_phase["lookup"] * 1e3, 2),
              "lookup_bitmap_matches_plain": same,
              "engine_gbs_same_shapes": ceilings,

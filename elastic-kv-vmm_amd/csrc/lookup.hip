@@ -23,6 +23,14 @@
 //     misses without touching their table entry;
 //   resolve_mapped_kernel - two levels (table -> logical id -> mapping -> slot),
 //     the reference's form.
+// Recent window: decode Top-K sets concentrate on the most recent tokens, and
+// lanes that gather single table entries cost one L2 request each. Both
+// kernels therefore stage the table entries of the last kWindow positions
+// before the row's length in LDS with coalesced 16-byte loads (two-level
+// lookups only for int32 tables); lanes inside the window read LDS, lanes
+// outside it read the bitmap and the table as before. Results do not depend
+// on where the window lies. 1024 entries measured best on the 60-layer decode
+// shapes: larger windows cost occupancy (LDS) more than they save.
 #include "../../include/ekv_kernels.h"
 #include "ekv_common.h"
 #include "ekv_fastdiv.h"
@@ -34,13 +42,41 @@
 namespace ekv {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kIters = 8;                      // 64-lane iterations per wave per chunk
-constexpr int kWaveSpan = 64 * kIters;         // 512 lanes per wave per chunk
-constexpr int kChunkLanes = kThreads * kIters; // 2048 lanes per chunk
-// Bitmap rows up to this many 32-bit words (T <= 131072 tokens) are staged in
-// LDS with coalesced loads; the per-lane bit tests are then LDS reads.
-constexpr int kStagedBitWords = 4096;
+// Tuning knobs (compile-time; the defaults measured best on the 60-layer
+// decode shapes, 128 requests x 2048 lanes x 65,536-token tables):
+//   EKV_LOOKUP_THREADS / EKV_LOOKUP_ITERS  workgroup size and 64-lane
+//       iterations per wave (a row chunk is THREADS * ITERS lanes);
+//   EKV_LOOKUP_WINDOW        table entries of the recent window staged in LDS
+//       (a multiple of 128; 0 = off);
+//   EKV_LOOKUP_STAGE_BITS    stage bitmap rows of up to
+//       EKV_LOOKUP_STAGED_BIT_WORDS words in LDS (else lanes read their word);
+//   EKV_LOOKUP_DENSE         32-bit byte-offset addressing for unit-stride rows.
+#ifndef EKV_LOOKUP_THREADS
+#define EKV_LOOKUP_THREADS 256
+#endif
+#ifndef EKV_LOOKUP_ITERS
+#define EKV_LOOKUP_ITERS 8
+#endif
+#ifndef EKV_LOOKUP_WINDOW
+#define EKV_LOOKUP_WINDOW 1024
+#endif
+#ifndef EKV_LOOKUP_STAGE_BITS
+#define EKV_LOOKUP_STAGE_BITS 1
+#endif
+#ifndef EKV_LOOKUP_STAGED_BIT_WORDS
+#define EKV_LOOKUP_STAGED_BIT_WORDS 4096
+#endif
+#ifndef EKV_LOOKUP_DENSE
+#define EKV_LOOKUP_DENSE 1
+#endif
+constexpr int kThreads = EKV_LOOKUP_THREADS;
+constexpr int kIters = EKV_LOOKUP_ITERS;        // 64-lane iterations per wave per chunk
+constexpr int kWaveSpan = 64 * kIters;          // 512 lanes per wave per chunk
+constexpr int kChunkLanes = kThreads * kIters;  // 2048 lanes per chunk
+constexpr int kStagedBitWords = EKV_LOOKUP_STAGED_BIT_WORDS;  // 4096 words: T <= 131072 tokens
+constexpr int kWindow = EKV_LOOKUP_WINDOW;
+static_assert(kWindow % 128 == 0, "the window must keep 16-byte alignment of the staged bitmap");
+static_assert(kThreads % 64 == 0 && kThreads <= 1024, "whole waves per workgroup");
 
 struct LookupArgs {
     const void* topk;
@@ -60,6 +96,8 @@ struct LookupArgs {
     int32_t* counts;
     int64_t count_sl, count_sb;
     int64_t batch;
+    int32_t window;                      // stage the recent window (int32 table)
+    int32_t bits_staged;                 // stage the bitmap row in LDS
     uint32_t width;
     uint32_t block_size;
     FastDiv block_div;
@@ -70,51 +108,157 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
                                      __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
 }
 
+// Element `index` of a row at `base` with element stride `stride`. The dense
+// form (stride 1 and row extents below 4 GiB, both checked on the host)
+// addresses with a 32-bit byte offset from the workgroup-uniform base, so a
+// lane's address takes one VGPR instead of two.
+template <bool kDense, typename T>
+__device__ __forceinline__ T* element(T* base, int64_t stride, uint32_t index) {
+    if constexpr (kDense) {
+        using Byte = std::conditional_t<std::is_const_v<T>, const char, char>;
+        return reinterpret_cast<T*>(reinterpret_cast<Byte*>(base) + index * static_cast<uint32_t>(sizeof(T)));
+    } else {
+        return base + static_cast<int64_t>(index) * stride;
+    }
+}
+
+// Staging of table windows and bitmap rows into LDS, by the whole workgroup;
+// the caller synchronizes. Loads are issued in groups of 4 per thread with
+// clamped (in-bounds) indices before the group's LDS stores. (Issuing every
+// load of both regions before any store needs more VGPRs and measured slower
+// on the 60-layer decode shapes: occupancy matters more than the saved round
+// trip.)
+
+template <typename T>
+__device__ __forceinline__ bool dense_int32(const T* src, int64_t stride) {
+    return sizeof(T) == 4 && stride == 1 && (reinterpret_cast<uintptr_t>(src) & 15) == 0;
+}
+
+// Any element type and stride: dst[0, n) = int32(src[j * stride]), in groups
+// of 4 loads per thread.
+template <typename T>
+__device__ __forceinline__ void stage_words(uint32_t* dst, const T* src, int64_t stride, int64_t n) {
+    for (int64_t first = 0; first < n; first += 4 * kThreads) {
+        T v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int64_t j = first + threadIdx.x + k * kThreads;
+            v[k] = src[(j < n ? j : n - 1) * stride];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int64_t j = first + threadIdx.x + k * kThreads;
+            dst[j < n ? j : n - 1] = static_cast<uint32_t>(static_cast<int32_t>(v[k]));
+        }
+    }
+}
+
+// A dense, 16-byte aligned int32 region, 16-byte pieces in groups of 4 per
+// thread.
+__device__ __forceinline__ void stage_vector(uint32_t* dst, const int32_t* src, int64_t n) {
+    if (n <= 0) {
+        return;
+    }
+    const int64_t n4 = n >> 2;
+    for (int64_t first = 0; first < n4; first += 4 * kThreads) {
+        int4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int64_t j = first + threadIdx.x + k * kThreads;
+            v[k] = reinterpret_cast<const int4*>(src)[j < n4 ? j : n4 - 1];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int64_t j = first + threadIdx.x + k * kThreads;
+            if (j < n4) {
+                reinterpret_cast<int4*>(dst)[j] = v[k];
+            }
+        }
+    }
+    const int64_t t = (n4 << 2) + threadIdx.x;
+    if (t < n) {
+        dst[t] = static_cast<uint32_t>(src[t]);
+    }
+}
+
+// Stages win_n table entries from win_src and bits_n bitmap words from
+// bits_src (either count may be 0).
+template <typename TableT>
+__device__ __forceinline__ void stage_rows(uint32_t* win_dst, const TableT* win_src, int64_t win_stride,
+                                           int64_t win_n, uint32_t* bits_dst, const int32_t* bits_src,
+                                           int64_t bits_stride, int64_t bits_n) {
+    const bool fast = (win_n == 0 || dense_int32(win_src, win_stride)) &&
+                      (bits_n == 0 || dense_int32(bits_src, bits_stride));  // uniform
+    if constexpr (sizeof(TableT) == 4) {
+        if (fast) {
+            stage_vector(win_dst, reinterpret_cast<const int32_t*>(win_src), win_n);
+            stage_vector(bits_dst, bits_src, bits_n);
+            return;
+        }
+    }
+    if (win_n > 0) {
+        stage_words(win_dst, win_src, win_stride, win_n);
+    }
+    if (bits_n > 0) {
+        stage_words(bits_dst, bits_src, bits_stride, bits_n);
+    }
+}
+
+// The recent window of a table row: positions [start, start + count), with
+// start a multiple of 128 and count <= kWindow; empty when staging is off.
+struct Window {
+    int64_t start = 0;
+    int64_t count = 0;
+};
+
+__device__ __forceinline__ Window recent_window(const LookupArgs& a, int64_t bound, bool table_ok) {
+    Window w;
+    if (kWindow > 0 && a.window && table_ok && bound > 0) {
+        w.start = bound > kWindow ? ((bound - kWindow) & ~int64_t{127}) : 0;
+        w.count = bound - w.start < kWindow ? bound - w.start : kWindow;
+    }
+    return w;
+}
+
 // Top-K block ids of the 8 lanes of this thread in the current chunk.
-template <typename TopkT>
+template <bool kDense, typename TopkT>
 __device__ __forceinline__ void load_blocks(const LookupArgs& a, const TopkT* topk, uint32_t first,
-                                            int64_t (&block)[kIters]) {
-    const bool unit_blocks = a.block_size == 1;
+                                            TopkT (&block)[kIters]) {
 #pragma unroll
     for (int i = 0; i < kIters; ++i) {
         const uint32_t o = first + i * 64;
         const uint32_t lane_o = o < a.width ? o : a.width - 1;
-        const uint32_t b = unit_blocks ? lane_o : a.block_div.div(lane_o);
-        block[i] = static_cast<int64_t>(topk[b * a.topk_sk]);
+        const uint32_t b = a.block_div.div(lane_o);  // exact for block_size 1 too
+        block[i] = *element<kDense>(topk, a.topk_sk, b);
     }
 }
 
-// Token position of each lane and whether it is valid and inside the table
+// Token position of lane o and whether it is valid and inside the table
 // (valid = block >= 0 && pos < length, as in the reference, plus bounds).
-__device__ __forceinline__ void lane_positions(const LookupArgs& a, uint32_t first, const int64_t (&block)[kIters],
-                                               int64_t bound, bool table_ok, int64_t (&pos)[kIters],
-                                               bool (&hit)[kIters]) {
-    const bool unit_blocks = a.block_size == 1;
-#pragma unroll
-    for (int i = 0; i < kIters; ++i) {
-        const uint32_t o = first + i * 64;
-        const uint32_t offset = unit_blocks ? 0u : o - a.block_div.div(o) * a.block_size;
-        const int64_t p = block[i] * a.block_size + offset;
-        hit[i] = o < a.width && block[i] >= 0 && p < bound && table_ok;
-        pos[i] = hit[i] ? p : 0;
-    }
+// Positions of valid lanes are below the table width (< 2^31); other lanes get 0.
+template <typename TopkT>
+__device__ __forceinline__ uint32_t lane_position(const LookupArgs& a, uint32_t o, TopkT block, int64_t bound,
+                                                  bool table_ok, bool& valid) {
+    const uint32_t offset = o - a.block_div.div(o) * a.block_size;
+    const int64_t p = static_cast<int64_t>(block) * a.block_size + offset;
+    valid = o < a.width && block >= 0 && p < bound && table_ok;
+    return valid ? static_cast<uint32_t>(p) : 0u;
 }
 
 // Output stores, then the ordered miss list of this chunk; returns the new
 // running miss count of the row. Every thread of the workgroup must call it.
-template <bool kCompact>
+// A lane is a miss when its slot is 0 (invalid lanes hold -1). The ballots are
+// taken twice, before and after the wave-total exchange, so no 64-bit masks
+// stay live across the barrier.
+template <bool kCompact, bool kDense = false>
 __device__ __forceinline__ int32_t emit(const LookupArgs& a, int32_t* out, int32_t* misses, uint32_t first,
-                                        const int32_t (&slot)[kIters], const bool (&hit)[kIters], int32_t running,
-                                        int32_t* wave_totals, int lane, int wave) {
-    uint64_t miss_mask[kIters];
+                                        const int32_t (&slot)[kIters], int32_t running, int32_t* wave_totals,
+                                        int lane, int wave) {
 #pragma unroll
     for (int i = 0; i < kIters; ++i) {
         const uint32_t o = first + i * 64;
         if (o < a.width) {
-            out[static_cast<int64_t>(o) * a.out_so] = slot[i];
-        }
-        if constexpr (kCompact) {
-            miss_mask[i] = __ballot(hit[i] && slot[i] == 0);
+            *element<kDense>(out, a.out_so, o) = slot[i];
         }
     }
     if constexpr (!kCompact) {
@@ -123,7 +267,7 @@ __device__ __forceinline__ int32_t emit(const LookupArgs& a, int32_t* out, int32
         int32_t wave_total = 0;
 #pragma unroll
         for (int i = 0; i < kIters; ++i) {
-            wave_total += __popcll(miss_mask[i]);
+            wave_total += __popcll(__ballot(first + i * 64 < a.width && slot[i] == 0));
         }
         if (lane == 0) {
             wave_totals[wave] = wave_total;
@@ -138,21 +282,26 @@ __device__ __forceinline__ int32_t emit(const LookupArgs& a, int32_t* out, int32
         }
 #pragma unroll
         for (int i = 0; i < kIters; ++i) {
-            if ((miss_mask[i] >> lane) & 1u) {
-                const int64_t at = rank + static_cast<int32_t>(lanes_below(miss_mask[i]));
-                misses[at * a.miss_so] = static_cast<int32_t>(first + i * 64);
+            const uint32_t o = first + i * 64;
+            const bool miss = o < a.width && slot[i] == 0;
+            const uint64_t mask = __ballot(miss);
+            if (miss) {
+                *element<kDense>(misses, a.miss_so, static_cast<uint32_t>(rank) + lanes_below(mask)) =
+                    static_cast<int32_t>(o);
             }
-            rank += __popcll(miss_mask[i]);
+            rank += __popcll(mask);
         }
         __syncthreads();  // wave_totals is rewritten by the next chunk
         return running + chunk_total;
     }
 }
 
-template <typename TopkT, typename TableT, bool kBits, bool kCompact>
+template <typename TopkT, typename TableT, bool kBits, bool kCompact, bool kDense>
 __global__ __launch_bounds__(kThreads) void resolve_single_kernel(const LookupArgs a) {
+    // Dynamic LDS: [kWindow] staged window entries (when a.window), then the
+    // staged bitmap row (when a.bits_staged), indexed by absolute word.
+    extern __shared__ __align__(16) uint32_t lds[];
     __shared__ int32_t wave_totals[kThreads / 64];
-    __shared__ uint32_t staged_bits[kBits ? kStagedBitWords : 1];
     const int64_t row = a.selected[blockIdx.x];
     if (row < 0 || row >= a.batch) {
         return;  // uniform over the workgroup
@@ -166,7 +315,10 @@ __global__ __launch_bounds__(kThreads) void resolve_single_kernel(const LookupAr
     const TopkT* topk = static_cast<const TopkT*>(a.topk) + layer * a.topk_sl + row * a.topk_sb;
     const TableT* table = static_cast<const TableT*>(a.table) + layer * a.table_sl + req_at * a.table_sr;
     const int32_t* bits_row = kBits ? a.bits + layer * a.bits_sl + req_at * a.bits_sr : nullptr;
-    const bool bits_in_lds = kBits && table_ok && a.bits_words <= kStagedBitWords;  // uniform
+    const bool bits_in_lds = kBits && table_ok && a.bits_staged;  // uniform
+    const Window win = recent_window(a, bound, table_ok);
+    const int32_t* window = reinterpret_cast<const int32_t*>(lds);
+    uint32_t* staged_bits = lds + (a.window ? kWindow : 0);
     int32_t* out = a.out + layer * a.out_sl + row * a.out_sb;
     int32_t* misses = kCompact ? a.misses + layer * a.miss_sl + row * a.miss_sb : nullptr;
     const int lane = threadIdx.x & 63;
@@ -175,50 +327,45 @@ __global__ __launch_bounds__(kThreads) void resolve_single_kernel(const LookupAr
 
     for (uint32_t chunk = 0; chunk < a.width; chunk += kChunkLanes) {
         const uint32_t first = chunk + wave * kWaveSpan + lane;
-        int64_t block[kIters];
-        load_blocks(a, topk, first, block);
-        if (bits_in_lds && chunk == 0) {
-            // Issued after the Top-K loads so both are in flight together.
-            for (int64_t w = threadIdx.x; w < a.bits_words; w += kThreads) {
-                staged_bits[w] = static_cast<uint32_t>(bits_row[w * a.bits_sw]);
-            }
+        TopkT block[kIters];
+        load_blocks<kDense>(a, topk, first, block);
+        if (chunk == 0 && (win.count > 0 || bits_in_lds)) {
+            // Issued after the Top-K loads so all of them are in flight together.
+            stage_rows(lds, table + win.start * a.table_sc, a.table_sc, win.count, staged_bits, bits_row, a.bits_sw,
+                       bits_in_lds ? a.bits_words : 0);
             __syncthreads();
         }
-        int64_t pos[kIters];
-        bool hit[kIters];
-        lane_positions(a, first, block, bound, table_ok, pos, hit);
-        bool resident[kIters];
-        if constexpr (kBits) {
-            uint32_t word[kIters];
-#pragma unroll
-            for (int i = 0; i < kIters; ++i) {
-                word[i] = bits_in_lds ? staged_bits[pos[i] >> 5]
-                                      : (table_ok ? static_cast<uint32_t>(bits_row[(pos[i] >> 5) * a.bits_sw]) : 0u);
-            }
-#pragma unroll
-            for (int i = 0; i < kIters; ++i) {
-                // A non-resident lane re-reads entry 0 of the row (shared by all
-                // such lanes, one cached line) instead of its own entry.
-                resident[i] = hit[i] && ((word[i] >> (pos[i] & 31)) & 1u);
-                pos[i] = resident[i] ? pos[i] : 0;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < kIters; ++i) {
-                resident[i] = true;
-            }
-        }
-        int32_t value[kIters];
-#pragma unroll
-        for (int i = 0; i < kIters; ++i) {
-            value[i] = table_ok ? static_cast<int32_t>(table[pos[i] * a.table_sc]) : 0;
-        }
+        // Lanes inside the window take their slot from LDS; the others read
+        // the bitmap (when given) and, if resident, their table entry.
         int32_t slot[kIters];
+        uint32_t at[kIters];   // table position read from global memory (0 when none is needed)
+        uint32_t global = 0;   // bit i: slot[i] is the global read
 #pragma unroll
         for (int i = 0; i < kIters; ++i) {
-            slot[i] = hit[i] ? (resident[i] ? value[i] : 0) : -1;
+            bool valid;
+            const uint32_t p = lane_position(a, first + i * 64, block[i], bound, table_ok, valid);
+            const int64_t rel = static_cast<int64_t>(p) - win.start;
+            const bool inside = valid && rel >= 0 && rel < win.count;
+            bool need = valid && !inside;
+            if constexpr (kBits) {
+                const uint32_t w = inside ? 0u : p >> 5;
+                const uint32_t word =
+                    bits_in_lds ? staged_bits[w]
+                                : (table_ok ? static_cast<uint32_t>(*element<kDense>(bits_row, a.bits_sw, w)) : 0u);
+                need = need && ((word >> (p & 31)) & 1u);
+            }
+            slot[i] = inside ? window[rel] : (valid ? 0 : -1);
+            at[i] = need ? p : 0u;
+            global |= static_cast<uint32_t>(need) << i;
         }
-        running = emit<kCompact>(a, out, misses, first, slot, hit, running, wave_totals, lane, wave);
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+            // Lanes that need no global read re-read entry 0 of the row (one
+            // cached line shared by all of them) so the loads stay unconditional.
+            const int32_t value = table_ok ? static_cast<int32_t>(*element<kDense>(table, a.table_sc, at[i])) : 0;
+            slot[i] = (global >> i) & 1u ? value : slot[i];
+        }
+        running = emit<kCompact, kDense>(a, out, misses, first, slot, running, wave_totals, lane, wave);
     }
     if constexpr (kCompact) {
         if (threadIdx.x == 0) {
@@ -229,6 +376,9 @@ __global__ __launch_bounds__(kThreads) void resolve_single_kernel(const LookupAr
 
 template <typename TopkT, typename TableT, typename MapT, bool kCompact>
 __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupArgs a) {
+    // Dynamic LDS: [kWindow] staged logical ids of the recent window (int32
+    // tables only, so a staged id is the table value itself).
+    extern __shared__ __align__(16) uint32_t lds[];
     __shared__ int32_t wave_totals[kThreads / 64];
     const int64_t row = a.selected[blockIdx.x];
     if (row < 0 || row >= a.batch) {
@@ -243,6 +393,8 @@ __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupAr
     const TableT* table =
         static_cast<const TableT*>(a.table) + layer * a.table_sl + (table_ok ? req : 0) * a.table_sr;
     const MapT* mapping = static_cast<const MapT*>(a.mapping) + layer * a.map_sl;
+    const Window win = recent_window(a, bound, table_ok);
+    const int32_t* window = reinterpret_cast<const int32_t*>(lds);
     int32_t* out = a.out + layer * a.out_sl + row * a.out_sb;
     int32_t* misses = kCompact ? a.misses + layer * a.miss_sl + row * a.miss_sb : nullptr;
     const int lane = threadIdx.x & 63;
@@ -251,29 +403,44 @@ __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupAr
 
     for (uint32_t chunk = 0; chunk < a.width; chunk += kChunkLanes) {
         const uint32_t first = chunk + wave * kWaveSpan + lane;
-        int64_t block[kIters];
-        load_blocks(a, topk, first, block);
-        int64_t pos[kIters];
-        bool hit[kIters];
-        lane_positions(a, first, block, bound, table_ok, pos, hit);
+        TopkT block[kIters];
+        load_blocks<false>(a, topk, first, block);
+        if (chunk == 0 && win.count > 0) {
+            stage_rows(lds, table + win.start * a.table_sc, a.table_sc, win.count, nullptr,
+                       static_cast<const int32_t*>(nullptr), 0, 0);
+            __syncthreads();
+        }
+        uint32_t pos[kIters];
+        uint32_t valid_bits = 0;   // bit i: lane i of this thread is valid
+        uint32_t inside_bits = 0;  // bit i: its position lies in the staged window
         int64_t logical[kIters];
 #pragma unroll
         for (int i = 0; i < kIters; ++i) {
-            logical[i] = table_ok ? static_cast<int64_t>(table[pos[i] * a.table_sc]) : 0;
+            bool valid;
+            pos[i] = lane_position(a, first + i * 64, block[i], bound, table_ok, valid);
+            const int64_t rel = static_cast<int64_t>(pos[i]) - win.start;
+            const bool inside = valid && rel >= 0 && rel < win.count;
+            valid_bits |= static_cast<uint32_t>(valid) << i;
+            inside_bits |= static_cast<uint32_t>(inside) << i;
+            logical[i] = table_ok ? static_cast<int64_t>(table[(inside ? 0u : pos[i]) * a.table_sc]) : 0;
         }
+        uint32_t hit_bits = 0;
         int64_t mapped[kIters];
 #pragma unroll
         for (int i = 0; i < kIters; ++i) {
-            hit[i] = hit[i] && logical[i] >= 0 && logical[i] < a.map_len;
-            const int64_t at = hit[i] ? logical[i] : 0;
-            mapped[i] = a.map_len > 0 ? static_cast<int64_t>(mapping[at * a.map_s]) : 0;
+            if ((inside_bits >> i) & 1u) {
+                logical[i] = window[static_cast<int64_t>(pos[i]) - win.start];
+            }
+            const bool hit = ((valid_bits >> i) & 1u) && logical[i] >= 0 && logical[i] < a.map_len;
+            hit_bits |= static_cast<uint32_t>(hit) << i;
+            mapped[i] = a.map_len > 0 ? static_cast<int64_t>(mapping[(hit ? logical[i] : 0) * a.map_s]) : 0;
         }
         int32_t slot[kIters];
 #pragma unroll
         for (int i = 0; i < kIters; ++i) {
-            slot[i] = hit[i] ? static_cast<int32_t>(mapped[i]) : -1;
+            slot[i] = (hit_bits >> i) & 1u ? static_cast<int32_t>(mapped[i]) : -1;
         }
-        running = emit<kCompact>(a, out, misses, first, slot, hit, running, wave_totals, lane, wave);
+        running = emit<kCompact>(a, out, misses, first, slot, running, wave_totals, lane, wave);
     }
     if constexpr (kCompact) {
         if (threadIdx.x == 0) {
@@ -283,41 +450,53 @@ __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupAr
 }
 
 template <typename TopkT, typename TableT>
-void launch_with_table(const LookupArgs& a, int32_t map_dtype, bool compact, dim3 grid, hipStream_t stream) {
+void launch_with_table(const LookupArgs& a, int32_t map_dtype, bool compact, bool dense, dim3 grid,
+                       hipStream_t stream) {
     const dim3 block(kThreads);
+    const size_t lds = sizeof(uint32_t) * ((a.window ? kWindow : 0) + (a.bits_staged ? a.bits_words : 0));
     if (a.mapping == nullptr) {
         const bool bits = a.bits != nullptr;
-        if (bits && compact) {
-            resolve_single_kernel<TopkT, TableT, true, true><<<grid, block, 0, stream>>>(a);
+        if (dense) {
+            if (bits && compact) {
+                resolve_single_kernel<TopkT, TableT, true, true, true><<<grid, block, lds, stream>>>(a);
+            } else if (bits) {
+                resolve_single_kernel<TopkT, TableT, true, false, true><<<grid, block, lds, stream>>>(a);
+            } else if (compact) {
+                resolve_single_kernel<TopkT, TableT, false, true, true><<<grid, block, lds, stream>>>(a);
+            } else {
+                resolve_single_kernel<TopkT, TableT, false, false, true><<<grid, block, lds, stream>>>(a);
+            }
+        } else if (bits && compact) {
+            resolve_single_kernel<TopkT, TableT, true, true, false><<<grid, block, lds, stream>>>(a);
         } else if (bits) {
-            resolve_single_kernel<TopkT, TableT, true, false><<<grid, block, 0, stream>>>(a);
+            resolve_single_kernel<TopkT, TableT, true, false, false><<<grid, block, lds, stream>>>(a);
         } else if (compact) {
-            resolve_single_kernel<TopkT, TableT, false, true><<<grid, block, 0, stream>>>(a);
+            resolve_single_kernel<TopkT, TableT, false, true, false><<<grid, block, lds, stream>>>(a);
         } else {
-            resolve_single_kernel<TopkT, TableT, false, false><<<grid, block, 0, stream>>>(a);
+            resolve_single_kernel<TopkT, TableT, false, false, false><<<grid, block, lds, stream>>>(a);
         }
     } else if (map_dtype == EKV_INT64) {
         if (compact) {
-            resolve_mapped_kernel<TopkT, TableT, int64_t, true><<<grid, block, 0, stream>>>(a);
+            resolve_mapped_kernel<TopkT, TableT, int64_t, true><<<grid, block, lds, stream>>>(a);
         } else {
-            resolve_mapped_kernel<TopkT, TableT, int64_t, false><<<grid, block, 0, stream>>>(a);
+            resolve_mapped_kernel<TopkT, TableT, int64_t, false><<<grid, block, lds, stream>>>(a);
         }
     } else {
         if (compact) {
-            resolve_mapped_kernel<TopkT, TableT, int32_t, true><<<grid, block, 0, stream>>>(a);
+            resolve_mapped_kernel<TopkT, TableT, int32_t, true><<<grid, block, lds, stream>>>(a);
         } else {
-            resolve_mapped_kernel<TopkT, TableT, int32_t, false><<<grid, block, 0, stream>>>(a);
+            resolve_mapped_kernel<TopkT, TableT, int32_t, false><<<grid, block, lds, stream>>>(a);
         }
     }
 }
 
 template <typename TopkT>
-void launch_table(const LookupArgs& a, int32_t table_dtype, int32_t map_dtype, bool compact, dim3 grid,
+void launch_table(const LookupArgs& a, int32_t table_dtype, int32_t map_dtype, bool compact, bool dense, dim3 grid,
                   hipStream_t stream) {
     if (table_dtype == EKV_INT64) {
-        launch_with_table<TopkT, int64_t>(a, map_dtype, compact, grid, stream);
+        launch_with_table<TopkT, int64_t>(a, map_dtype, compact, dense, grid, stream);
     } else {
-        launch_with_table<TopkT, int32_t>(a, map_dtype, compact, grid, stream);
+        launch_with_table<TopkT, int32_t>(a, map_dtype, compact, dense, grid, stream);
     }
 }
 
@@ -476,15 +655,30 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
     if (block_size >= (int64_t{1} << 31)) {
         throw std::invalid_argument("block_size must be below 2^31");
     }
+    if (a.table_cols >= (int64_t{1} << 31)) {
+        throw std::invalid_argument("tables wider than 2^31 - 1 positions are not supported");
+    }
     a.block_div = FastDiv(static_cast<uint32_t>(block_size));
+    // Staging the window reads kWindow entries per (row, layer); it pays once a
+    // row has at least a quarter as many lanes. Two-level lookups stage only
+    // int32 tables (a staged int32 id must equal the table value).
+    a.window = kWindow > 0 && width >= kWindow / 4 && (mapping == nullptr || table.dtype == EKV_INT32) ? 1 : 0;
+    a.bits_staged = EKV_LOOKUP_STAGE_BITS && bits_p != nullptr && a.bits_words <= kStagedBitWords ? 1 : 0;
 
     const dim3 grid(static_cast<uint32_t>(count), static_cast<uint32_t>(layers));
     const auto s = static_cast<hipStream_t>(stream);
     const int32_t map_dtype = mapping ? mapping->dtype : 0;
+    // Dense rows (unit inner strides, every row extent below 4 GiB) take the
+    // 32-bit byte-offset addressing of element<true>.
+    constexpr int64_t kFourGiB = int64_t{1} << 32;
+    const bool dense = EKV_LOOKUP_DENSE && a.topk_sk == 1 && a.table_sc == 1 && a.out_so == 1 && (!compact || a.miss_so == 1) &&
+                       (a.bits == nullptr || a.bits_sw == 1) && k * itemsize(topk.dtype) < kFourGiB &&
+                       a.table_cols * itemsize(table.dtype) < kFourGiB && width * 4 < kFourGiB &&
+                       a.bits_words * 4 < kFourGiB;
     if (topk.dtype == EKV_INT64) {
-        launch_table<int64_t>(a, table.dtype, map_dtype, compact, grid, s);
+        launch_table<int64_t>(a, table.dtype, map_dtype, compact, dense, grid, s);
     } else {
-        launch_table<int32_t>(a, table.dtype, map_dtype, compact, grid, s);
+        launch_table<int32_t>(a, table.dtype, map_dtype, compact, dense, grid, s);
     }
     check_hip(hipGetLastError(), "launch resident lookup");
     return 0;

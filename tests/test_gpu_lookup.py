@@ -176,3 +176,89 @@ def test_bitmap_lookup_equals_plain_lookup_and_oracle(gpu, coracle, layered, bs)
         for row in range(batch):
             c = want_counts[layer, row]
             assert np.array_equal(outs[1][1][layer, row, :c], want_misses[layer, row, :c])
+
+
+# Rows wide enough (>= 1024 lanes) that the kernels stage the table entries of
+# the recent window (the last 4096 positions before the row's length) in LDS.
+WINDOW_CASES = [
+    # layers, batch, k, block_size, table_rows, table_cols, layered, two-level, table dtype, table layout, bitmap
+    (2, 4, 1536, 1, 5, 10000, True, False, torch.int32, "dense", True),
+    (1, 3, 512, 4, 4, 9001, False, False, torch.int32, "offset", True),
+    (2, 3, 1200, 1, 3, 6000, False, False, torch.int64, "dense", False),
+    (1, 4, 1024, 1, 4, 7000, True, False, torch.int32, "strided", True),
+    (1, 2, 2048, 1, 2, 140000, False, False, torch.int32, "dense", True),
+    (2, 3, 1500, 1, 4, 5000, False, True, torch.int32, "dense", False),
+    (1, 3, 2048, 1, 3, 3000, False, False, torch.int32, "offset", False),
+]
+
+
+def laid_out(values, dtype, layout, device):
+    """`values` as a dense tensor, a view whose rows start 4 bytes off 16-byte
+    alignment, or a view with element stride 2 along the last dimension."""
+    source = torch.tensor(values, dtype=dtype, device=device)
+    if layout == "dense":
+        return source
+    if layout == "offset":
+        backing = torch.zeros((*source.shape[:-1], source.shape[-1] + 1), dtype=dtype, device=device)
+        view = backing[..., 1:]
+    else:
+        backing = torch.zeros((*source.shape, 2), dtype=dtype, device=device)
+        view = backing[..., 0]
+    view.copy_(source)
+    return view
+
+
+@pytest.mark.parametrize("case", range(len(WINDOW_CASES)))
+def test_recent_window_parity_with_oracle(gpu, coracle, case):
+    from adaptive_sparse.resident_lookup import build_residency_bits
+
+    layers, batch, k, bs, rrows, cols, layered, mapped, table_dtype, layout, use_bits = WINDOW_CASES[case]
+    rng = np.random.default_rng(500 + case)
+    choices = [cols, cols + 5, cols - 77, 4000, 0, 130, -3, cols - 4096 - 1]
+    lengths = np.array([choices[rng.integers(len(choices))] for _ in range(batch)])
+    lengths[0] = cols - 1
+    rows = rng.integers(0, rrows, size=batch)
+    topk = rng.integers(-1, cols // bs + 2, size=(layers, batch, k))
+    for r in range(batch):
+        hi = max(1, min(lengths[r], cols) // bs)
+        recent = rng.integers(max(0, hi - 4300 // bs), hi + 1, size=(layers, k))
+        near = rng.random((layers, k)) < 0.8
+        topk[:, r][near] = recent[near]
+    shape = (layers, rrows, cols) if layered else (rrows, cols)
+    n = 6000
+    mapping = None
+    if mapped:
+        table = rng.integers(-2, n + 2, size=shape)
+        mapping = rng.integers(1, 1 << 20, size=n)
+        mapping[rng.random(n) < 0.3] = 0
+    else:
+        table = rng.integers(1, 1 << 20, size=shape)
+        table[rng.random(shape) < 0.4] = 0
+    selected = rng.permutation(batch)
+    width = k * bs
+    initial = np.full((layers, batch, width), -77, np.int32)
+    want, want_misses, want_counts = coracle.resolve_resident(topk, table, mapping, rows, lengths, selected,
+                                                              bs, initial, with_misses=True)
+    t = lambda a, dt: torch.tensor(a, dtype=dt, device=gpu)  # noqa: E731
+    table_d = laid_out(table, table_dtype, layout, gpu)
+    bits = None
+    if use_bits:
+        bits = build_residency_bits(table_d.to(torch.int32).contiguous())
+        if layout == "strided":
+            spread = torch.zeros((*bits.shape, 2), dtype=torch.int32, device=gpu)
+            spread[..., 1].copy_(bits)
+            bits = spread[..., 1]
+    output = t(initial, torch.int32)
+    misses = torch.full((layers, batch, width), -5, dtype=torch.int32, device=gpu)
+    counts = torch.full((layers, batch), -5, dtype=torch.int32, device=gpu)
+    resolve_resident(t(topk, torch.int32), table_d, None if mapping is None else t(mapping, torch.int32),
+                     t(rows, torch.int64), t(lengths, torch.int32), t(selected, torch.int64), output, bs,
+                     misses=misses, miss_count=counts, resident_bits=bits)
+    assert np.array_equal(output.cpu().numpy(), want)
+    assert np.array_equal(counts.cpu().numpy(), want_counts)
+    got_misses = misses.cpu().numpy()
+    for layer in range(layers):
+        for row in range(batch):
+            c = want_counts[layer, row]
+            assert np.array_equal(got_misses[layer, row, :c], want_misses[layer, row, :c])
+            assert (got_misses[layer, row, c:] == -5).all()
