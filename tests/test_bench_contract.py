@@ -1,0 +1,35 @@
+"""CPU checks of the bench.py command-line contract and of loud failure
+when the native kernels are missing."""
+
+import subprocess
+import sys
+from types import SimpleNamespace
+from unittest.mock import patch
+
+import pytest
+
+from conftest import ROOT
+
+
+def test_bench_refuses_more_than_one_gpu():
+    result = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2", "--steps", "1"],
+                            capture_output=True, text=True, timeout=120)
+    assert result.returncode == 2
+    assert "one GPU only" in result.stderr
+    assert result.stdout == ""
+
+
+def test_kernel_library_without_kernels_raises():
+    from elastic_kv import _native
+    from elastic_kv.backing import _load_library
+
+    names = ("ev_create", "ev_ensure", "ev_precommit", "ev_drop", "ev_base", "ev_backed", "ev_reserved",
+             "ev_granularity", "ev_close", "ev_error", "ev_poisoned")
+    library = SimpleNamespace(**{name: lambda *a: 0 for name in names})
+    _load_library.cache_clear()
+    try:
+        with patch("elastic_kv.backing.ct.CDLL", return_value=library):
+            with pytest.raises(RuntimeError, match="lacks ekv_"):
+                _native.kernel_library("no-kernels-libelastic-vmm.so")
+    finally:
+        _load_library.cache_clear()
