@@ -59,6 +59,34 @@ def test_release_and_recommit_one_hole(gpu):
         backing.close()
 
 
+def test_admission_precommits_lookahead_chunks_of_a_real_backing(gpu):
+    from elastic_kv.admission import PhysicalAdmission
+
+    chunk = DEFAULT_CHUNK_BYTES
+    slot_bytes = 512
+    backing = Backing(8 * chunk, chunk_bytes=chunk, device=0)
+    try:
+        assert backing.ensure([0]) == 1
+        ctrl = PhysicalAdmission([backing], slot_bytes, chunk, precommit_lookahead=2, precommit_limit=2,
+                                 device=0)
+        # The free device memory bounds nothing here: slots of chunks 0-2.
+        per_chunk = chunk // slot_bytes
+        assert ctrl.physical_available_tokens(3 * per_chunk - 1, [(1, 3 * per_chunk)]) == 3 * per_chunk - 1
+        admitted = [(1, per_chunk + 5)]                    # ends inside chunk 1
+        assert backing.ensure([0, 1]) == 1
+        added = ctrl.precommit_after(admitted, backing.reserved_bytes // chunk,
+                                     lambda c: c not in backing.mapped_chunks)
+        assert added == [2]                                # chunk 1 is live; its successor is prewarmed
+        assert ctrl.backed_chunks() == {0, 1, 2}
+        assert backing.backed_bytes == 3 * chunk and backing.mapped_chunks == {0, 1}
+        assert backing.ensure([2]) == 0                    # already mapped; the zero fill is fenced here
+        ctrl.admitted([2])
+        assert torch.count_nonzero(backing.raw[2 * chunk:3 * chunk]).item() == 0
+        assert ctrl.counters["precommit_chunks"] == 1
+    finally:
+        backing.close()
+
+
 def test_errors_are_reported_not_fatal(gpu):
     backing = Backing(2 * DEFAULT_CHUNK_BYTES, device=0)
     try:
