@@ -172,6 +172,16 @@ def graph_replay_ms(torch, fn, reps=10):
     return ms
 
 
+def lookup_roofline(algorithmic_bytes, avg_ms, traffic):
+    """HBM roofline of the 60-layer lookup launch: algorithmic and (profiled) moved bytes per second."""
+    achieved = algorithmic_bytes / (avg_ms / 1e3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "moved_gbs": None if traffic is None else round(traffic / (avg_ms / 1e3) / 1e9, 1),
+            "kernel": "resolve_single_kernel<bits, compact> (ekv_resolve_resident_bits)",
+            "algorithmic_bytes_per_launch": algorithmic_bytes, "avg_launch_ms": round(avg_ms, 4)}
+
+
 def roofline(achieved_gbs, kernel, algorithmic_bytes, avg_ms, traffic):
     return {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kernel,
@@ -355,6 +365,8 @@ def run_decode_read(torch, args, device):
              "lookup_us_per_layer": round(phase["lookup"] * 1e3 / L, 2),
              "lookup_gbs": round(lookup_bytes / (phase["lookup"] / 1e3) / 1e9, 1),
              "lookup_us_back_to_back": round(lookup_alone_ms * 1e3, 2),
+             "lookup_roofline": lookup_roofline(lookup_bytes, lookup_alone_ms,
+                                                read_traffic("resolve_resident_hisparse_decode.md")),
              "lookup_us_per_layer_launch_graph": round(per_layer_graph_ms * 1e3 / L, 2),
              "lookup_us_without_bitmap": round(plain_phase["lookup"] * 1e3, 2),
              "lookup_bitmap_matches_plain": same,

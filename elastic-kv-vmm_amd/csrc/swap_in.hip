@@ -144,11 +144,13 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
         for (int64_t i = threadIdx.x; i < m; i += kThreads) {
             const int64_t victim = static_cast<int64_t>(keys[i] & 0xffffffffu);
             const int32_t lane = misses[i * a.mi_o];
-            if (lane < 0 || lane >= W || victim >= C) {
-                continue;  // not a miss list written by the lookup
-            }
-            const int64_t token = lane_position(a, topk_row, static_cast<uint32_t>(lane));
-            if (token < 0 || token >= a.table_cols) {
+            const int64_t token =
+                lane >= 0 && lane < W ? lane_position(a, topk_row, static_cast<uint32_t>(lane)) : int64_t{-1};
+            if (victim >= C || token < 0 || token >= a.table_cols) {
+                // Not an entry of a miss list written by the lookup: record
+                // an empty promotion so the move that follows skips it.
+                promote_src[i * a.ps_o] = -1;
+                promote_dst[i * a.pd_o] = -1;
                 continue;
             }
             const int32_t old = slot_token[victim * a.st_c];

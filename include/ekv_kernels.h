@@ -184,7 +184,10 @@ int ekv_scatter_kv(const ekv_planes* planes, const ekv_tensor* slots,
  *   promote_src / promote_dst [L, B, W] int32: i < miss_count[l, b] get the
  *   host row and the global slot of the i-th promotion (feed to ekv_move_kv)
  * Stamps are step * 2W + lane; `step` must grow by one per call and keep
- * (step + 1) * 2W below 2^31. Tokens must be unique within a row. C <= 8192.
+ * (step + 1) * 2W below 2^31. Tokens must be unique within a row, W <= C <=
+ * 8192, and the selected rows must name distinct requests (one workgroup
+ * updates each (layer, request) hot buffer). Miss-list entries that name no
+ * valid lane get promote_src = promote_dst = -1, which ekv_move_kv skips.
  */
 int ekv_swap_in(const ekv_tensor* topk, int64_t block_size, const ekv_tensor* rows,
                 const ekv_tensor* selected, const ekv_tensor* slots,

@@ -102,3 +102,26 @@ def test_lookup_swap_promote_gather_cycle(gpu, capacity):
     finally:
         torch.cuda.synchronize()
         arena.close()
+
+
+def test_miss_entries_without_a_lane_record_empty_promotions(gpu):
+    # A miss list the lookup did not write (lane -1, lane past the row) must not
+    # leave stale promotion records behind for the move that follows.
+    L, R, T, C, K = 1, 1, 64, 8, 4
+    buffers = HotBuffers(L, R, T, C, gpu)
+    topk = torch.tensor([[[5, 6, 7, 9]]], dtype=torch.int32, device=gpu)
+    rows = torch.arange(R, device=gpu)
+    slots = torch.zeros((L, R, K), dtype=torch.int32, device=gpu)
+    misses = torch.tensor([[[0, -1, 99, 2]]], dtype=torch.int32, device=gpu)
+    counts = torch.tensor([[4]], dtype=torch.int32, device=gpu)
+    host_table = torch.arange(R * T, dtype=torch.int32, device=gpu).reshape(R, T)
+    promote_src = torch.full((L, R, K), 77, dtype=torch.int32, device=gpu)
+    promote_dst = torch.full((L, R, K), 77, dtype=torch.int32, device=gpu)
+    swap_in(topk, 1, rows, rows, slots, misses, counts, buffers, host_table, promote_src, promote_dst)
+    src, dst = promote_src.cpu().tolist()[0][0], promote_dst.cpu().tolist()[0][0]
+    assert src[1] == dst[1] == -1 and src[2] == dst[2] == -1
+    assert src[0] == 5 and src[3] == 7                      # lanes 0 and 2 select tokens 5 and 7
+    assert dst[0] > 0 and dst[3] > 0 and dst[0] != dst[3]
+    assert slots.cpu().tolist()[0][0][0] == dst[0] and slots.cpu().tolist()[0][0][2] == dst[3]
+    table = buffers.table.cpu()[0, 0]
+    assert table[5] == dst[0] and table[7] == dst[3] and int((table != 0).sum()) == 2
