@@ -125,3 +125,61 @@ def test_miss_entries_without_a_lane_record_empty_promotions(gpu):
     assert slots.cpu().tolist()[0][0][0] == dst[0] and slots.cpu().tolist()[0][0][2] == dst[3]
     table = buffers.table.cpu()[0, 0]
     assert table[5] == dst[0] and table[7] == dst[3] and int((table != 0).sum()) == 2
+
+
+@pytest.mark.parametrize("bs", [2, 3])
+def test_paged_blocks_lookup_and_swap_in_match_oracle(gpu, bs):
+    # Top-K over blocks of bs tokens, -1 padding and rows shorter than the
+    # table: lookup and swap-in state after every step equal the oracle's.
+    L, R, T, C, K = 2, 3, 240, 32, 8   # C >= W = 16 or 24; evictions start within the 5 steps
+    W = K * bs
+    rng = np.random.default_rng(40 + bs)
+    buffers = HotBuffers(L, R, T, C, gpu)
+    host_table = torch.arange(R * T, dtype=torch.int32).reshape(R, T)
+    lengths = np.array([T, T - 5, T - 17])
+    rows = torch.arange(R, device=gpu)
+    state = {"table": buffers.table.cpu().numpy(), "slot_token": buffers.slot_token.cpu().numpy(),
+             "stamps": buffers.stamps.cpu().numpy()}
+    blocks_total = T // bs
+    for step in range(5):
+        topk = np.empty((L, R, K), np.int64)
+        for layer in range(L):
+            for r in range(R):
+                recent = rng.choice(np.arange(blocks_total - 12, blocks_total), 6, replace=False)
+                old = rng.choice(np.arange(0, blocks_total - 12), K - 6, replace=False)
+                picks = rng.permutation(np.concatenate([recent, old]))
+                picks[rng.random(K) < 0.15] = -1
+                topk[layer, r] = picks
+        topk_d = torch.tensor(topk, dtype=torch.int32, device=gpu)
+        slots = torch.empty((L, R, W), dtype=torch.int32, device=gpu)
+        misses = torch.full((L, R, W), -1, dtype=torch.int32, device=gpu)
+        counts = torch.empty((L, R), dtype=torch.int32, device=gpu)
+        resolve_resident(topk_d, buffers.table, None, rows, torch.tensor(lengths, dtype=torch.int32, device=gpu),
+                         rows, slots, bs, misses=misses, miss_count=counts, resident_bits=buffers.bits)
+        want_slots, want_misses, want_counts = ref.resolve_resident(
+            topk, state["table"], None, np.arange(R), lengths, np.arange(R), bs,
+            np.zeros((L, R, W), np.int32), with_misses=True)
+        assert np.array_equal(slots.cpu().numpy(), want_slots), step
+        assert np.array_equal(counts.cpu().numpy(), want_counts), step
+        miss_np = np.full((L, R, W), -1, np.int32)
+        for (layer, r), lanes in want_misses.items():
+            miss_np[layer, r, :len(lanes)] = lanes
+        assert np.array_equal(misses.cpu().numpy(), miss_np), step
+        promote_src = torch.full((L, R, W), -9, dtype=torch.int32, device=gpu)
+        promote_dst = torch.full((L, R, W), -9, dtype=torch.int32, device=gpu)
+        swap_in(topk_d, bs, rows, rows, slots, misses, counts, buffers, host_table.to(gpu), promote_src,
+                promote_dst)
+        state = ref.swap_in(step, bs, topk, np.arange(R), np.arange(R), want_slots, miss_np, want_counts,
+                            state["table"], state["slot_token"], state["stamps"], buffers.slot_base.cpu().numpy(),
+                            host_table.numpy())
+        assert np.array_equal(slots.cpu().numpy(), state["slots"]), step
+        assert np.array_equal(buffers.table.cpu().numpy(), state["table"]), step
+        assert np.array_equal(buffers.slot_token.cpu().numpy(), state["slot_token"]), step
+        assert np.array_equal(buffers.stamps.cpu().numpy(), state["stamps"]), step
+        assert np.array_equal(buffers.bits.cpu().numpy(), ref.residency_bits(state["table"])), step
+        got_src, got_dst = promote_src.cpu().numpy(), promote_dst.cpu().numpy()
+        for layer in range(L):
+            for r in range(R):
+                c = want_counts[layer, r]
+                assert np.array_equal(got_src[layer, r, :c], state["promote_src"][layer, r, :c])
+                assert np.array_equal(got_dst[layer, r, :c], state["promote_dst"][layer, r, :c])
