@@ -24,6 +24,7 @@
 #include "ekv_common.h"
 #include "ekv_fastdiv.h"
 #include "ekv_tensor_util.h"
+#include "ekv_vec.h"
 
 #include <algorithm>
 #include <cstdlib>
@@ -50,16 +51,6 @@ enum Mode : int {
 
 constexpr bool is_kv_mode(int m) { return m == KvGather || m == KvScatter || m == KvGather64 || m == KvScatter64; }
 constexpr bool is_gather_mode(int m) { return m == KvGather || m == KvGather64; }
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-
-template <int VW> struct Vec;
-template <> struct Vec<16> { using type = u32x4; };
-template <> struct Vec<8> { using type = u32x2; };
-template <> struct Vec<4> { using type = uint32_t; };
-template <> struct Vec<2> { using type = uint16_t; };
-template <> struct Vec<1> { using type = uint8_t; };
 
 struct EngineArgs {
     // Byte bases: the engine copies from src_base + src_off to dst_base + dst_off.
@@ -337,17 +328,6 @@ __global__ __launch_bounds__(kThreads) void copy_large_rows(const EngineArgs a) 
             }
         }
     }
-}
-
-// Largest power of two <= 16 that divides every value.
-int pick_vector_width(std::initializer_list<int64_t> values) {
-    int vw = 16;
-    for (const int64_t v : values) {
-        while (vw > 1 && (v % vw) != 0) {
-            vw >>= 1;
-        }
-    }
-    return vw;
 }
 
 int64_t env_int(const char* name, int64_t fallback) {

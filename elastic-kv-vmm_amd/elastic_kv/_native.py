@@ -72,6 +72,8 @@ _SIGNATURES = {
     "ekv_swap_in": ([_P_TENSOR, ct.c_int64] + [_P_TENSOR] * 13 + [ct.c_int64, ct.c_void_p], ct.c_int),
     "ekv_move_kv": ([ct.POINTER(EkvPlanes), _P_TENSOR, ct.POINTER(EkvPlanes), _P_TENSOR, _P_TENSOR, ct.c_int64,
                      ct.c_void_p], ct.c_int),
+    "ekv_compare_kv": ([ct.POINTER(EkvPlanes), _P_TENSOR, ct.POINTER(EkvPlanes), _P_TENSOR, _P_TENSOR,
+                        ct.c_void_p], ct.c_int),
     "ekv_host_alloc": ([ct.c_uint64, ct.POINTER(ct.c_void_p), ct.POINTER(ct.c_void_p)], ct.c_int),
     "ekv_host_free": ([ct.c_void_p], ct.c_int),
 }

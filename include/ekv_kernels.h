@@ -211,6 +211,18 @@ int ekv_move_kv(const ekv_planes* src, const ekv_tensor* src_rows,
                 const ekv_planes* dst, const ekv_tensor* dst_rows,
                 const ekv_tensor* counts, int64_t zero_below, void* stream);
 
+/*
+ * Byte-exact comparison of K/V rows of two plane sets (same kv, row_bytes):
+ *   equal[l, b, w] = 1 when, in every kv plane, row a_rows[l, b, w] of `a`
+ *   equals row b_rows[l, b, w] of `b` byte for byte; 0 when a byte differs;
+ *   -1 when either index lies outside [0, rows) of its planes (nothing read).
+ *   a_rows, b_rows [L, B, W] int32/int64; equal [L, B, W] int32.
+ * Replaces the int16 row comparisons of LogicalShadow.check / check_complete
+ * (adaptive_sparse/logical_shadow.py:72-75, 108-123).
+ */
+int ekv_compare_kv(const ekv_planes* a, const ekv_tensor* a_rows, const ekv_planes* b,
+                   const ekv_tensor* b_rows, const ekv_tensor* equal, void* stream);
+
 /* Pinned host memory (hipHostMalloc) plus the device pointer kernels use to
  * read and write it. Free with ekv_host_free(host). No reference counterpart
  * (the reference's pinned pools are SGLang's HostKVCache). */

@@ -243,6 +243,63 @@ _I32P = ct.POINTER(ct.c_int32)
 _U8P = ct.POINTER(ct.c_uint8)
 
 
+def shadow_check(blocks, table, lengths, rows, block_size, physical, live_pages, page_size, capacity, written,
+                 pool_k, pool_v, shadow_k, shadow_v):
+    """One LogicalShadow.check, lane by lane (adaptive_sparse/logical_shadow.py:46-86).
+
+    Arrays are numpy: blocks [1, B, K]; table [R, T]; lengths, rows [B];
+    physical [1, B, K * block_size] or None; live_pages [P] bool or None;
+    written [capacity] bool; pool_k/pool_v [N, row] and shadow_k/shadow_v
+    [capacity, row] uint8 rows. Returns (counts, clean_blocks, physical_out)
+    with counts = (checked tokens, checked bytes, uninitialized logical,
+    invalid physical, mismatched, calls = 1, malformed blocks).
+    """
+    blocks = np.asarray(blocks)
+    _, B, K = blocks.shape
+    W = K * block_size
+    N = pool_k.shape[0]
+    T = table.shape[1]
+    row_bytes = pool_k.shape[1] + pool_v.shape[1]
+    clean = np.full_like(blocks, -1)
+    out = np.zeros((1, B, W), dtype=np.int64)
+    tokens = uninitialized = invalid = mismatched = malformed = 0
+    for b in range(B):
+        length = int(lengths[b])
+        limit = (length + block_size - 1) // block_size
+        leading = True
+        for k in range(K):
+            block = int(blocks[0, b, k])
+            valid_block = 0 <= block < limit
+            leading = leading and valid_block
+            if (block != -1 and not valid_block) or (valid_block and not leading):
+                malformed += 1
+            clean[0, b, k] = block if leading else -1
+            for j in range(block_size):
+                o = k * block_size + j
+                position = int(clean[0, b, k]) * block_size + j
+                selected = 0 <= position < length
+                bounded = selected and position < T
+                logical = int(table[int(rows[b]), position if bounded else 0])
+                logical_ok = bounded and page_size <= logical < capacity
+                logical = logical if logical_ok else 0
+                source_ok = logical_ok and bool(written[logical])
+                phys = logical if physical is None else int(physical[0, b, o])
+                in_range = page_size <= phys < N
+                safe = phys if in_range else 0
+                backed = in_range if live_pages is None else in_range and bool(live_pages[safe // page_size])
+                safe = safe if backed else 0
+                same = (np.array_equal(pool_k[safe], shadow_k[logical])
+                        and np.array_equal(pool_v[safe], shadow_v[logical]))
+                checked = selected and source_ok and backed
+                tokens += checked
+                uninitialized += selected and not source_ok
+                invalid += selected and not backed
+                mismatched += checked and not same
+                out[0, b, o] = 0 if (selected and not backed) else phys
+    counts = (tokens, tokens * row_bytes, uninitialized, invalid, mismatched, 1, malformed)
+    return counts, clean, out
+
+
 def _i64(array):
     return np.ascontiguousarray(array, dtype=np.int64)
 

@@ -385,3 +385,43 @@ def test_swap_in_matches_lru_replay_on_random_streams():
     for capacity, context, k in ((8, 40, 6), (16, 100, 16), (5, 12, 5)):
         steps = [rng.sample(range(context), rng.randint(1, k)) for _ in range(40)]
         assert _lookup_swap_steps(steps, capacity, context) == ref.lru_misses(steps, capacity)
+
+
+def _shadow_case():
+    """Two rows over a capacity-8 shadow: row 0 reads logical 2, 3 (written) and 4 (never
+    written); row 1 has a leading block, then an out-of-range block (malformed) and a
+    valid block after the break (malformed); its table maps to logical 0 and 9, both invalid."""
+    rowb = 4
+    table = np.array([[0, 1, 2, 3, 4, 5, 6, 7], [0, 9, 7, 7, 1, 0, 3, 3]])
+    written = np.array([0, 1, 1, 1, 0, 1, 1, 1], dtype=bool)
+    rng = np.random.default_rng(5)
+    shadow_k = rng.integers(0, 256, (8, rowb), dtype=np.uint8)
+    shadow_v = rng.integers(0, 256, (8, rowb), dtype=np.uint8)
+    pool_k, pool_v = shadow_k.copy(), shadow_v.copy()
+    return table, written, shadow_k, shadow_v, pool_k, pool_v, rowb
+
+
+def test_shadow_check_hand_counted_case():
+    table, written, shadow_k, shadow_v, pool_k, pool_v, rowb = _shadow_case()
+    pool_v[3, 1] ^= 0x40                       # logical 3 differs in its V row
+    blocks = np.array([[[1, 2, -1], [0, 5, 1]]])
+    counts, clean, out = ref.shadow_check(blocks, table, np.array([5, 6]), np.array([0, 1]), 2, None, None, 1, 8,
+                                          written, pool_k, pool_v, shadow_k, shadow_v)
+    # checked: logical 2 and 3; uninitialized: logical 4 and row 1's two lanes;
+    # invalid physical: row 1's two lanes (physical = logical 0); mismatched: logical 3.
+    assert counts == (2, 2 * 2 * rowb, 3, 2, 1, 1, 2)
+    assert clean.tolist() == [[[1, 2, -1], [0, -1, -1]]]
+    assert out.tolist() == [[[2, 3, 4, 0, 0, 0], [0, 0, 0, 0, 0, 0]]]
+
+
+def test_shadow_check_with_physical_slots_and_live_pages():
+    table, written, shadow_k, shadow_v, pool_k, pool_v, rowb = _shadow_case()
+    pool_k[6], pool_v[6] = shadow_k[3], shadow_v[3]   # physical 6 holds logical 3
+    physical = np.array([[[5, 6, 7, 8, 2, 3]]])
+    live = np.array([1, 1, 1, 1, 1, 0, 1, 1], dtype=bool)
+    counts, _, out = ref.shadow_check(np.array([[[1, 2, -1]]]), table[:1], np.array([5]), np.array([0]), 2,
+                                      physical, live, 1, 8, written, pool_k, pool_v, shadow_k, shadow_v)
+    # lane 0: page 5 not live (invalid, zeroed); lane 1: checked, equal; lane 2: logical 4 never
+    # written; lanes 3-5 are not selected and keep their physical slots.
+    assert counts == (1, 2 * rowb, 1, 1, 0, 1, 0)
+    assert out.tolist() == [[[0, 6, 7, 8, 2, 3]]]
