@@ -138,9 +138,22 @@ def timed_steps(torch, steps, phases):
             marks[i + 1].record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - wall0) * 1e3 / steps
-    per_phase = {name: statistics.mean(events[s][i].elapsed_time(events[s][i + 1]) for s in range(steps))
-                 for i, (name, _) in enumerate(phases)}
+    samples = {name: [events[s][i].elapsed_time(events[s][i + 1]) for s in range(steps)]
+               for i, (name, _) in enumerate(phases)}
+    per_phase = {name: statistics.mean(values) for name, values in samples.items()}
+    LAST_SAMPLES.clear()
+    LAST_SAMPLES.update(samples)
     return wall_ms, per_phase
+
+
+LAST_SAMPLES = {}   # per-phase event times (ms) of the latest timed_steps call
+
+
+def spread(values_ms, scale=1.0, digits=4):
+    """Median and 95th percentile of event times (scaled, e.g. 1e3 for us)."""
+    ordered = sorted(values_ms)
+    p95 = ordered[min(len(ordered) - 1, int(round(0.95 * (len(ordered) - 1))))]
+    return {"median": round(statistics.median(ordered) * scale, digits), "p95": round(p95 * scale, digits)}
 
 
 def back_to_back_ms(torch, fn, reps=20):
@@ -292,6 +305,7 @@ def run_decode_read(torch, args, device):
     lookup_bytes = 12 * lanes + 4 * miss_total + 4 * L * R
     gather_bytes = lanes * 2 * row_bytes + hits * 2 * row_bytes + lanes * 4
     step_ms, phase = timed_steps(torch, args.steps, [("lookup", lookup), ("gather", gather)])
+    step_spread = {"gather_ms": spread(LAST_SAMPLES["gather"]), "lookup_us": spread(LAST_SAMPLES["lookup"], 1e3, 2)}
     _, plain_phase = timed_steps(torch, max(3, args.steps // 2), [("lookup", lookup_plain)])
     # Reference points of the same engine on the same shapes: sequential slots
     # (every row read, contiguous) and all-miss slots (write-only zero fill).
@@ -371,6 +385,7 @@ def run_decode_read(torch, args, device):
              "lookup_us_without_bitmap": round(plain_phase["lookup"] * 1e3, 2),
              "lookup_bitmap_matches_plain": same,
              "engine_gbs_same_shapes": ceilings,
+             "event_spread": step_spread,
              "hit_rate": round(hits / lanes, 4), "pool_commit_s": round(commit_s, 3)}
     roof = roofline(achieved, "copy_small_rows<KvGather,16> (ekv_gather_kv)", gather_bytes, phase["gather"],
                     read_traffic("gather_kv_hisparse_decode.md"))

@@ -30,14 +30,19 @@ class HotBuffers:
     residency bitmap; slot_token [L, R, C]: token held by each slot (-1 =
     empty); stamps [L, R, C]: recency stamps; slot_base [R]: global slot of
     each request's local slot 0 (request r owns slots base .. base + C - 1).
+    table and bits are views into storage whose rows are padded to a multiple
+    of 128 positions, so every row starts 16-byte aligned and the lookup can
+    stage its recent window and bitmap row with 16-byte loads.
     """
 
     def __init__(self, layers, requests, context, capacity, device, *, slot_base=None, with_bits=True):
         self.layers, self.requests, self.context, self.capacity = layers, requests, context, capacity
         self.device = torch.device(device)
         kw = dict(dtype=torch.int32, device=self.device)
-        self.table = torch.zeros((layers, requests, context), **kw)
-        self.bits = torch.zeros((layers, requests, (context + 31) // 32), **kw) if with_bits else None
+        padded = -(-context // 128) * 128
+        self.table = torch.zeros((layers, requests, padded), **kw)[..., :context]
+        words = (context + 31) // 32
+        self.bits = torch.zeros((layers, requests, padded // 32), **kw)[..., :words] if with_bits else None
         self.slot_token = torch.full((layers, requests, capacity), -1, **kw)
         self.stamps = torch.full((layers, requests, capacity), INT32_MIN, **kw)
         if slot_base is None:
