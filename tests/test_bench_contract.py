@@ -33,3 +33,22 @@ def test_kernel_library_without_kernels_raises():
                 _native.kernel_library("no-kernels-libelastic-vmm.so")
     finally:
         _load_library.cache_clear()
+
+
+def test_product_code_never_imports_the_oracle():
+    # The oracle is test infrastructure: the package must not import it (bench.py's
+    # CPU-baseline leg and __graft_entry__.smoke are the only non-test users).
+    import ast
+
+    offenders = []
+    for path in sorted((ROOT / "elastic-kv-vmm_amd").rglob("*.py")):
+        tree = ast.parse(path.read_text(), filename=str(path))
+        for node in ast.walk(tree):
+            names = []
+            if isinstance(node, ast.Import):
+                names = [alias.name for alias in node.names]
+            elif isinstance(node, ast.ImportFrom) and node.module:
+                names = [node.module]
+            if any(name == "oracle" or name.startswith("oracle.") for name in names):
+                offenders.append(f"{path.relative_to(ROOT)}:{node.lineno}")
+    assert offenders == []
