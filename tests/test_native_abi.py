@@ -7,7 +7,6 @@ validation before any HIP call.
 import ctypes as ct
 import re
 import subprocess
-from pathlib import Path
 
 import pytest
 
