@@ -236,13 +236,6 @@ def gather_kv(pool, layer_stride, kv_stride, row_stride, row_bytes, rows, slots,
     return out
 
 
-# ---------------------------------------------------------------- C oracle
-
-_I64P = ct.POINTER(ct.c_int64)
-_I32P = ct.POINTER(ct.c_int32)
-_U8P = ct.POINTER(ct.c_uint8)
-
-
 def shadow_check(blocks, table, lengths, rows, block_size, physical, live_pages, page_size, capacity, written,
                  pool_k, pool_v, shadow_k, shadow_v):
     """One LogicalShadow.check, lane by lane (adaptive_sparse/logical_shadow.py:46-86).
@@ -298,6 +291,39 @@ def shadow_check(blocks, table, lengths, rows, block_size, physical, live_pages,
                 out[0, b, o] = 0 if (selected and not backed) else phys
     counts = (tokens, tokens * row_bytes, uninitialized, invalid, mismatched, 1, malformed)
     return counts, clean, out
+
+
+def move_kv(src, src_layout, dst, dst_layout, src_rows, dst_rows, counts, kv, zero_below=0):
+    """Row moves between two byte pools (the promote of a swap-in), returning a new dst.
+
+    layouts are (layer_stride, kv_stride, row_stride, row_bytes, rows). For
+    every layer l, row b, i < min(counts[l, b], K) and plane kv: row dst_rows[l, b, i]
+    of dst takes row src_rows[l, b, i] of src, when 0 <= src row < rows and
+    zero_below <= dst row < rows; other entries move nothing.
+    """
+    src = np.asarray(src, dtype=np.uint8)
+    out = np.array(dst, dtype=np.uint8, copy=True)
+    s_ls, s_kvs, s_rs, row_bytes, s_rows = src_layout
+    d_ls, d_kvs, d_rs, _, d_rows = dst_layout
+    L, B, K = np.shape(src_rows)
+    for layer in range(L):
+        for b in range(B):
+            for i in range(min(K, max(0, int(counts[layer][b])))):
+                frm, to = int(src_rows[layer][b][i]), int(dst_rows[layer][b][i])
+                if not (0 <= frm < s_rows and zero_below <= to < d_rows):
+                    continue
+                for plane in range(kv):
+                    a = layer * s_ls + plane * s_kvs + frm * s_rs
+                    z = layer * d_ls + plane * d_kvs + to * d_rs
+                    out[z:z + row_bytes] = src[a:a + row_bytes]
+    return out
+
+
+# ---------------------------------------------------------------- C oracle
+
+_I64P = ct.POINTER(ct.c_int64)
+_I32P = ct.POINTER(ct.c_int32)
+_U8P = ct.POINTER(ct.c_uint8)
 
 
 def _i64(array):

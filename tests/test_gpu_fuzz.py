@@ -1,0 +1,179 @@
+"""Seeded random configurations of the HIP kernels against the oracle (bit-exact).
+
+Each case draws its shapes, dtypes, strides (views of larger buffers), block
+size, table form (single or two level, with or without a layer dimension,
+with or without the residency bitmap), lengths, selections, row sizes and
+vector widths, plane strides and zero_below from a seed. The cases are small
+(the oracle runs in milliseconds) and together cover the kernels' branches:
+the recent-window staging, the bitmap staged in LDS or read per lane, the
+dense and strided addressing, every vector width of the copy engine, and
+large rows cut into segments.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from adaptive_sparse.kv_pool import KVPlanes
+from adaptive_sparse.resident_lookup import build_residency_bits, resolve_resident
+from adaptive_sparse.sparse_read import gather_kv, scatter_kv
+from adaptive_sparse.swap_in import move_kv
+from oracle import oracle as ref
+
+pytestmark = pytest.mark.gpu
+
+INDEX_DTYPES = (torch.int32, torch.int64)
+
+
+def on_gpu(array, dtype, device, strided):
+    """`array` on the device, optionally as a view with stride 2 along the last dimension."""
+    source = torch.tensor(array, dtype=dtype)
+    if not strided:
+        return source.to(device)
+    spread = torch.zeros((*source.shape, 2), dtype=dtype)
+    spread[..., 0] = source
+    return spread.to(device)[..., 0]
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_lookup_random_configurations(gpu, coracle, seed):
+    rng = np.random.default_rng(7000 + seed)
+    layers = int(rng.integers(1, 4))
+    batch = int(rng.integers(1, 9))
+    bs = int(rng.choice([1, 1, 1, 2, 3, 8, 16]))
+    k = int(rng.integers(1, 2600 // bs + 2))
+    rrows = int(rng.integers(1, 10))
+    cols = int(rng.integers(1, 7000))
+    layered = bool(rng.random() < 0.5)
+    mapped = bool(rng.random() < 0.35)
+    use_bits = (not mapped) and bool(rng.random() < 0.6)
+    compact = bool(rng.random() < 0.8)
+    strided = {name: bool(rng.random() < 0.25) for name in ("topk", "table", "output")}
+    topk_dtype, table_dtype, map_dtype = (INDEX_DTYPES[int(rng.integers(2))] for _ in range(3))
+
+    lengths = rng.integers(-2, cols + 5, size=batch)
+    rows = rng.integers(0, rrows, size=batch)
+    width = k * bs
+    topk = rng.integers(-1, cols // bs + 2, size=(layers, batch, k))
+    for r in range(batch):  # a recent-heavy share, as decode Top-K sets are
+        hi = max(1, min(int(lengths[r]), cols) // bs)
+        near = rng.random((layers, k)) < 0.6
+        topk[:, r][near] = rng.integers(max(0, hi - 1200 // bs), hi + 1, size=(layers, k))[near]
+    shape = (layers, rrows, cols) if layered else (rrows, cols)
+    n = 5000
+    mapping = None
+    if mapped:
+        table = rng.integers(-2, n + 2, size=shape)
+        mapping = rng.integers(1, 1 << 20, size=n)
+        mapping[rng.random(n) < 0.3] = 0
+    else:
+        table = rng.integers(1, 1 << 20, size=shape)
+        table[rng.random(shape) < 0.4] = 0
+    selected = rng.permutation(batch)[: int(rng.integers(1, batch + 1))]
+    initial = np.full((layers, batch, width), -77, np.int32)
+    want, want_misses, want_counts = coracle.resolve_resident(topk, table, mapping, rows, lengths, selected, bs,
+                                                              initial, with_misses=True)
+
+    table_d = on_gpu(table, table_dtype, gpu, strided["table"])
+    bits = build_residency_bits(table_d) if use_bits else None
+    output = on_gpu(initial, torch.int32, gpu, strided["output"])
+    misses = torch.full((layers, batch, width), -5, dtype=torch.int32, device=gpu) if compact else None
+    counts = torch.full((layers, batch), -5, dtype=torch.int32, device=gpu) if compact else None
+    resolve_resident(on_gpu(topk, topk_dtype, gpu, strided["topk"]), table_d,
+                     None if mapping is None else torch.tensor(mapping, dtype=map_dtype, device=gpu),
+                     torch.tensor(rows, device=gpu), torch.tensor(lengths, dtype=torch.int32, device=gpu),
+                     torch.tensor(selected, device=gpu), output, bs, misses=misses, miss_count=counts,
+                     resident_bits=bits)
+    assert np.array_equal(output.cpu().numpy(), want), (seed, layers, batch, bs, k, cols, layered, mapped, use_bits)
+    if compact:
+        got_counts, got_misses = counts.cpu().numpy(), misses.cpu().numpy()
+        for layer in range(layers):
+            for row in range(batch):
+                if row in selected:
+                    c = want_counts[layer, row]
+                    assert got_counts[layer, row] == c
+                    assert np.array_equal(got_misses[layer, row, :c], want_misses[layer, row, :c])
+                else:
+                    assert got_counts[layer, row] == -5
+
+
+def random_planes(rng, gpu, layers, kv, rows, row_bytes):
+    row_stride = row_bytes + int(rng.choice([0, 0, 2, 8, 16, 48]))
+    plane = rows * row_stride + int(rng.choice([0, 16, 64, 100]))
+    layer_gap = int(rng.choice([0, 32, 4096]))
+    total = layers * (kv * plane + layer_gap) + 64
+    offset = int(rng.choice([0, 0, 2, 4, 8, 16]))                 # base alignment below 16 bytes
+    host = rng.integers(0, 256, total + offset, dtype=np.uint8)
+    device = torch.tensor(host, device=gpu)
+    planes = KVPlanes(base=device.data_ptr() + offset, device=gpu.index or 0, layers=layers, kv=kv,
+                      layer_stride=kv * plane + layer_gap, kv_stride=plane, row_stride=row_stride,
+                      row_bytes=row_bytes, rows=rows, owner=device)
+    return device, host[offset:], planes
+
+
+ROW_BYTES = (2, 6, 8, 24, 64, 128, 512, 1000, 2048, 4096, 40960)
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_gather_and_scatter_random_configurations(gpu, coracle, seed):
+    rng = np.random.default_rng(8000 + seed)
+    layers, kv = int(rng.integers(1, 4)), int(rng.choice([1, 2]))
+    row_bytes = int(rng.choice(ROW_BYTES))
+    rows = int(rng.integers(1, 200 if row_bytes < 4096 else 12))
+    batch = int(rng.integers(1, 5))
+    k = int(rng.integers(1, 300 if row_bytes < 4096 else 6))
+    zero_below = int(rng.choice([0, 1, 3]))
+    device, host, planes = random_planes(rng, gpu, layers, kv, rows, row_bytes)
+    slots = rng.integers(-2, rows + 3, size=(layers, batch, k))
+    slot_dtype = INDEX_DTYPES[int(rng.integers(2))]
+    spare = int(rng.choice([0, 0, 3]))
+    big = torch.full((batch, layers, kv, k + spare, row_bytes), 0xAB, dtype=torch.uint8, device=gpu)
+    out = big[:, :, :, spare:]
+    gather_kv(planes, torch.tensor(slots, dtype=slot_dtype, device=gpu), out, zero_below=zero_below)
+    want = coracle.gather_kv(host, planes.layer_stride, planes.kv_stride, planes.row_stride, row_bytes, rows,
+                             slots, kv, zero_below=zero_below)
+    assert np.array_equal(out.cpu().numpy(), want), (seed, layers, kv, rows, row_bytes, batch, k, zero_below)
+
+    # Scatter distinct in-range slots back from new rows; every other byte stays.
+    valid = np.arange(zero_below, rows)
+    if valid.size:
+        count = min(valid.size, batch * k)
+        distinct = rng.permutation(valid)[:count]
+        targets = np.full(batch * k, -1, dtype=np.int64)
+        targets[rng.permutation(batch * k)[:count]] = distinct
+        targets = np.broadcast_to(targets.reshape(1, batch, k), (layers, batch, k)).copy()
+        source = rng.integers(0, 256, size=(batch, layers, kv, k, row_bytes), dtype=np.uint8)
+        scatter_kv(planes, torch.tensor(targets, device=gpu), torch.tensor(source, device=gpu),
+                   zero_below=zero_below)
+        want_pool = coracle.scatter_kv(host, planes.layer_stride, planes.kv_stride, planes.row_stride, row_bytes,
+                                       rows, targets, kv, source, zero_below=zero_below)
+        offset = planes.base - device.data_ptr()
+        assert np.array_equal(device.cpu().numpy()[offset:], want_pool), seed
+
+
+@pytest.mark.parametrize("seed", range(15))
+def test_move_random_configurations(gpu, seed):
+    rng = np.random.default_rng(9000 + seed)
+    layers, kv = int(rng.integers(1, 4)), int(rng.choice([1, 2]))
+    row_bytes = int(rng.choice(ROW_BYTES[:9]))
+    src_rows_n, dst_rows_n = int(rng.integers(1, 150)), int(rng.integers(1, 150))
+    batch, k = int(rng.integers(1, 5)), int(rng.integers(1, 40))
+    zero_below = int(rng.choice([0, 1]))
+    src_dev, src_host, src_planes = random_planes(rng, gpu, layers, kv, src_rows_n, row_bytes)
+    dst_dev, dst_host, dst_planes = random_planes(rng, gpu, layers, kv, dst_rows_n, row_bytes)
+    src_rows = rng.integers(-2, src_rows_n + 2, size=(layers, batch, k))
+    # Destinations are distinct within a layer (two moves into one row would race).
+    dst_rows = np.full((layers, batch, k), -1, dtype=np.int64)
+    for layer in range(layers):
+        picks = rng.permutation(np.arange(-1, dst_rows_n + 2))[: batch * k]
+        dst_rows[layer].flat[: picks.size] = picks
+    counts = rng.integers(-1, k + 2, size=(layers, batch))
+    dst_before = dst_dev.cpu().numpy().copy()
+    t = lambda a: torch.tensor(a, dtype=torch.int32, device=gpu)  # noqa: E731
+    move_kv(src_planes, t(src_rows), dst_planes, t(dst_rows), t(counts), zero_below=zero_below)
+    offset = dst_planes.base - dst_dev.data_ptr()
+    layout = lambda p, n: (p.layer_stride, p.kv_stride, p.row_stride, row_bytes, n)  # noqa: E731
+    want = ref.move_kv(src_host, layout(src_planes, src_rows_n), dst_before[offset:], layout(dst_planes, dst_rows_n),
+                       src_rows, dst_rows, counts, kv, zero_below=zero_below)
+    assert np.array_equal(dst_dev.cpu().numpy()[offset:], want), seed
+    assert np.array_equal(dst_dev.cpu().numpy()[:offset], dst_before[:offset])

@@ -425,3 +425,28 @@ def test_shadow_check_with_physical_slots_and_live_pages():
     # written; lanes 3-5 are not selected and keep their physical slots.
     assert counts == (1, 2 * rowb, 1, 1, 0, 1, 0)
     assert out.tolist() == [[[0, 6, 7, 8, 2, 3]]]
+
+
+def test_move_kv_hand_case_and_gather_identity():
+    rng = np.random.default_rng(9)
+    kv, row = 2, 4
+    src = rng.integers(1, 256, 2 * kv * 5 * row, dtype=np.uint8)          # 2 layers x 2 planes x 5 rows
+    dst = np.zeros(2 * kv * 6 * row, dtype=np.uint8)                      # 2 layers x 2 planes x 6 rows
+    src_layout = (kv * 5 * row, 5 * row, row, row, 5)
+    dst_layout = (kv * 6 * row, 6 * row, row, row, 6)
+    src_rows = [[[1, 4, 7]], [[0, 2, 3]]]
+    dst_rows = [[[2, 0, 3]], [[5, 1, 4]]]
+    counts = [[3], [2]]                                                   # layer 1 moves only its first two
+    out = ref.move_kv(src, src_layout, dst, dst_layout, src_rows, dst_rows, counts, kv, zero_below=1)
+    planes = out.reshape(2, kv, 6, row)
+    source = src.reshape(2, kv, 5, row)
+    # layer 0: 1 -> 2 moves; 4 -> 0 is below zero_below; 7 is past the source rows.
+    assert np.array_equal(planes[0, :, 2], source[0, :, 1])
+    assert not planes[0, :, [0, 1, 3, 4, 5]].any()
+    # layer 1: 0 -> 5 and 2 -> 1 move; the third entry is past the count.
+    assert np.array_equal(planes[1, :, 5], source[1, :, 0]) and np.array_equal(planes[1, :, 1], source[1, :, 2])
+    assert not planes[1, :, [0, 2, 3, 4]].any()
+    # Reading the moved rows back at their destinations gives the source rows.
+    moved_src = np.array([[[1]], [[0]]]); moved_dst = np.array([[[2]], [[5]]])
+    assert np.array_equal(ref.gather_kv(out, *dst_layout[:4], 6, moved_dst, kv),
+                          ref.gather_kv(src, *src_layout[:4], 5, moved_src, kv, zero_below=0))
