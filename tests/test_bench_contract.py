@@ -52,3 +52,22 @@ def test_product_code_never_imports_the_oracle():
             if any(name == "oracle" or name.startswith("oracle.") for name in names):
                 offenders.append(f"{path.relative_to(ROOT)}:{node.lineno}")
     assert offenders == []
+
+
+def test_kernels_refuse_cpu_tensors():
+    # No CPU fallback exists: every hot-path wrapper raises on host tensors.
+    import torch
+
+    from adaptive_sparse.kv_pool import KVPlanes
+    from adaptive_sparse.resident_lookup import build_residency_bits, resolve_resident
+    from adaptive_sparse.sparse_read import gather_kv
+
+    i32 = lambda *shape: torch.zeros(shape, dtype=torch.int32)  # noqa: E731
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        resolve_resident(i32(1, 2, 4), i32(2, 8), None, torch.arange(2), i32(2), torch.arange(2), i32(1, 2, 4), 1)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        build_residency_bits(i32(2, 64))
+    planes = KVPlanes(base=0, device=0, layers=1, kv=2, layer_stride=0, kv_stride=64, row_stride=8, row_bytes=8,
+                      rows=8, owner=None)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        gather_kv(planes, i32(1, 2, 3), torch.zeros((2, 1, 2, 3, 8), dtype=torch.uint8))
