@@ -237,6 +237,9 @@ def decode_inputs(torch, device, L, R, T, K, C, W, seed):
     gen = torch.Generator(device=device).manual_seed(seed)
     recent_count = (K * 4) // 5
     uniform_count = K - recent_count
+    if not (recent_count <= W <= T and uniform_count <= T - W and C <= T):
+        # The index gathers below would read past their sources.
+        raise ValueError(f"decode inputs need {recent_count} <= W <= T, {uniform_count} <= T - W and C <= T")
     recent = torch.rand((L, R, W), generator=gen, device=device).argsort(-1)[..., :recent_count]
     recent = (recent + (T - W)).to(torch.int32)
     uniform = torch.rand((L, R, T - W), generator=gen, device=device).topk(uniform_count, dim=-1).indices
@@ -668,6 +671,8 @@ def composite_topk(torch, device, L, R, K, lengths, gen, recent_window=4096):
     """Per (layer, request): K unique tokens, 80 % from the last 4096 of the request's context, 20 % from the rest."""
     T = int(lengths.max())
     uniform_want = K - (K * 4) // 5
+    if recent_window < K or T < uniform_want:
+        raise ValueError("composite Top-K needs recent_window >= K and contexts of at least the uniform picks")
     older = (lengths - recent_window).clamp_min(0)                               # [R]
     u_count = torch.minimum(older, torch.full_like(older, uniform_want))         # uniform picks per request
     r_count = K - u_count

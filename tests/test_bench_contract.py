@@ -71,3 +71,13 @@ def test_kernels_refuse_cpu_tensors():
                       rows=8, owner=None)
     with pytest.raises(ValueError, match="no CPU fallback"):
         gather_kv(planes, i32(1, 2, 3), torch.zeros((2, 1, 2, 3, 8), dtype=torch.uint8))
+
+
+def test_decode_inputs_reject_shapes_that_cannot_hold_the_picks():
+    # A recent region smaller than the 80 % recent picks would make the index
+    # gathers read past their sources; the generator refuses such shapes.
+    import bench
+    import torch
+
+    with pytest.raises(ValueError, match="decode inputs need"):
+        bench.decode_inputs(torch, torch.device("cpu"), 1, 1, 65536, 2048, 1024, 1024, 0)
