@@ -477,7 +477,8 @@ def run_topk_gather(torch, args, device):
     extra = {"lookups_per_s": round(lanes / (phase["lookup"] / 1e3), 1),
              "lookup_us_per_step": round(phase["lookup"] * 1e3, 2), "hit_rate": round(hits / lanes, 4),
              "pool_commit_s": round(commit_s, 3)}
-    roof = roofline(achieved, "copy_small_rows<KvGather,16> (ekv_gather_kv)", gather_bytes, phase["gather"], None)
+    roof = roofline(achieved, "copy_small_rows<KvGather,16> (ekv_gather_kv)", gather_bytes, phase["gather"],
+                    read_traffic("gather_kv_topk_gather.md"))
     result = envelope(args, gather_bytes / (step_ms / 1e3) / 1e9, step_ms, config, roof, baseline, extra)
     del raw, output
     torch.cuda.synchronize()
@@ -542,7 +543,7 @@ def run_block_gather(torch, args, device):
     config = {"workload": "vllm-block-gather", "requests": R, "blocks_per_request": NB, "block_tokens": 16,
               "layers": L, "kv_heads": 8, "head_dim": 128, "pool_blocks": POOL, "pool_bytes": layout.capacity_bytes}
     roof = roofline(achieved, "copy_small_rows<KvGather,16> (ekv_gather_kv, 32 KiB rows)", gather_bytes,
-                    phase["gather"], None)
+                    phase["gather"], read_traffic("gather_kv_block_gather.md"))
     result = envelope(args, gather_bytes / (step_ms / 1e3) / 1e9, step_ms, config, roof, baseline,
                       {"pool_commit_s": round(commit_s, 3)}, metric="block gather GB/s (% of HBM peak), 1 GPU")
     del raw, output
@@ -647,7 +648,7 @@ def run_migration(torch, args, device):
     config = {"workload": "page-migration-round-trip", "blocks_per_tick": MOVE, "block_bytes": layout.block_bytes,
               "layers": 36, "kv_heads": 8, "head_dim": 128, "block_tokens": 16, "pool_blocks": BLOCKS}
     roof = roofline(pack_bytes / (pack_ms / 1e3) / 1e9, "copy_small_rows<KvGather,16> (pack, 32 KiB rows)",
-                    pack_bytes, pack_ms, None)
+                    pack_bytes, pack_ms, read_traffic("pack_page_migration.md"))
     extra = {"verified_round_trip": verified, "tick_ms": round(tick_s * 1e3, 3),
              "phase_ms": {"map_and_zero": round(statistics.mean(phases["map_s"]) * 1e3, 3),
                           "pipelined_move": round(statistics.mean(phases["move_s"]) * 1e3, 3),
