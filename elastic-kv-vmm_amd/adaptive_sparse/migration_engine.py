@@ -104,6 +104,11 @@ class MigrationEngine:
         self.host_free = FreeSlots(self.max_pages)
         self.d2h = torch.cuda.Stream(self.device)
         self.h2d = torch.cuda.Stream(self.device)
+        # The latest queued copies of each direction: the next pack into the
+        # device staging waits for the D2H reads of it, and the next D2H into
+        # host rows waits for the H2D reads of them.
+        self._d2h_done = None
+        self._h2d_done = None
 
     # ------------------------------------------------------------ kernels
 
@@ -164,6 +169,7 @@ class MigrationEngine:
             raise ValueError("more pages than the staging holds")
         rows = self.reserve_host(len(pages)) if host_rows is None else host_rows
         compute = torch.cuda.current_stream(self.device)
+        self._order_reuse(compute)
         for start in range(0, len(pages), self.sub_batch):
             chunk = pages[start:start + self.sub_batch]
             self.pack(chunk, self.out_staging, start)
@@ -172,9 +178,16 @@ class MigrationEngine:
             self.d2h.wait_event(packed)
             with torch.cuda.stream(self.d2h):
                 self._copy_rows(rows[start:start + len(chunk)], self.out_staging, start, to_host=True)
-        self._done = torch.cuda.Event()
-        self._done.record(self.d2h)
+        self._d2h_done = torch.cuda.Event()
+        self._d2h_done.record(self.d2h)
         return HostPages(rows=rows, pages=pages)
+
+    def _order_reuse(self, compute):
+        """Order this call's writes after the previous calls' reads of the same buffers."""
+        if self._d2h_done is not None:
+            compute.wait_event(self._d2h_done)       # packing rewrites the device staging
+        if self._h2d_done is not None:
+            self.d2h.wait_event(self._h2d_done)      # D2H copies rewrite host rows
 
     def promote(self, host, destinations):
         """Copy demoted pages from pinned host into `destinations` (already allocated)."""
@@ -184,9 +197,9 @@ class MigrationEngine:
         compute = torch.cuda.current_stream(self.device)
         ready = torch.cuda.Event()
         ready.record(compute)
-        self.h2d.wait_event(ready)
-        if getattr(self, "_done", None) is not None:
-            self.h2d.wait_event(self._done)
+        self.h2d.wait_event(ready)                   # earlier unpacks read the same device staging
+        if self._d2h_done is not None:
+            self.h2d.wait_event(self._d2h_done)      # the host rows must have landed
         for start in range(0, len(destinations), self.sub_batch):
             chunk = destinations[start:start + self.sub_batch]
             with torch.cuda.stream(self.h2d):
@@ -195,6 +208,7 @@ class MigrationEngine:
                 landed.record(self.h2d)
             compute.wait_event(landed)
             self.unpack(chunk, self.in_staging, start)
+        self._h2d_done = landed if destinations else self._h2d_done
 
     def round_trip(self, pages, destinations):
         """Demote `pages` and promote them into `destinations`, pipelined per sub-batch."""
@@ -204,6 +218,10 @@ class MigrationEngine:
             raise ValueError("pages and destinations must pair up within the staging size")
         rows = self.reserve_host(len(pages))
         compute = torch.cuda.current_stream(self.device)
+        self._order_reuse(compute)
+        ready = torch.cuda.Event()
+        ready.record(compute)
+        self.h2d.wait_event(ready)                   # earlier unpacks read the same device staging
         for start in range(0, len(pages), self.sub_batch):
             sources = pages[start:start + self.sub_batch]
             targets = destinations[start:start + self.sub_batch]
@@ -223,6 +241,8 @@ class MigrationEngine:
                 landed.record(self.h2d)
             compute.wait_event(landed)
             self.unpack(targets, self.in_staging, start)
+        if pages:
+            self._d2h_done, self._h2d_done = copied, landed
         return HostPages(rows=rows, pages=pages)
 
     def _copy_rows(self, rows, staging, start, *, to_host):

@@ -121,3 +121,33 @@ def test_transactions_demote_promote_cycle(gpu):
             prepare_promote(coordinator, request, sync)
     finally:
         pool.close()
+
+
+def test_back_to_back_demotes_and_promotes_without_host_syncs(gpu):
+    # Consecutive calls reuse the device staging and released host rows; the
+    # engine orders them with events, so no host synchronization is needed
+    # between calls for every byte to land where it belongs.
+    layout = BlockMajorLayout(blocks=40, **BLOCK)
+    pool = PagedKVPool(layout, device=0)
+    try:
+        first, second = list(range(1, 9)), list(range(9, 17))
+        pool.allocate(first + second)
+        fill(pool, first + second, 3)
+        before = {p: pool.page_view(p).clone() for p in first + second}
+        engine = MigrationEngine(pool, max_pages=8, sub_batch=3)
+        host_a = engine.demote(first)
+        targets_a = list(range(17, 25))
+        pool.allocate(targets_a)
+        engine.promote(host_a, targets_a)
+        engine.release_host(host_a)                  # its rows are reused by the next demote at once
+        host_b = engine.demote(second)
+        targets_b = list(range(25, 33))
+        pool.allocate(targets_b)
+        engine.promote(host_b, targets_b)
+        engine.wait()
+        for s, t in zip(first, targets_a):
+            assert torch.equal(pool.page_view(t), before[s]), (s, t)
+        for s, t in zip(second, targets_b):
+            assert torch.equal(pool.page_view(t), before[s]), (s, t)
+    finally:
+        pool.close()
