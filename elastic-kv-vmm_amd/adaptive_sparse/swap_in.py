@@ -69,11 +69,40 @@ class HotBuffers:
 
             build_residency_bits(self.table, out=self.bits)
 
+    def rebase(self):
+        """Renumber the recency stamps and restart the step counter.
+
+        Every non-empty slot gets stamp rank - C, where rank orders the
+        slots by (stamp, slot) as the LRU does. Empty slots stay INT32_MIN.
+        The eviction order is unchanged, and later steps' stamps (>= 0) stay
+        more recent than every renumbered one.
+        """
+        ranks = _ranks_from_stamps(self.stamps).to(torch.int32)
+        empty = self.stamps == INT32_MIN
+        self.stamps.copy_(torch.where(empty, torch.full_like(ranks, INT32_MIN), ranks - self.capacity))
+        self.step = 0
+
+
+def _ranks_from_stamps(stamps):
+    """Per row, the rank of every slot's (stamp, slot) key, 0 = least recent."""
+    order = torch.argsort(stamps.to(torch.int64), dim=-1, stable=True)
+    ranks = torch.empty_like(order)
+    ranks.scatter_(-1, order, torch.arange(stamps.shape[-1], device=stamps.device).expand_as(order))
+    return ranks
+
 
 def swap_in(topk, block_size, rows, selected, slots, misses, miss_count, buffers, host_table,
             promote_src, promote_dst, *, step=None):
-    """Run one swap-in step (see module docstring); advances buffers.step."""
-    step = buffers.step if step is None else step
+    """Run one swap-in step (see module docstring); advances buffers.step.
+
+    Stamps are step * 2W + lane in int32; before they would overflow, the
+    buffers' stamps are renumbered (HotBuffers.rebase) and the step restarts.
+    """
+    width = topk.shape[2] * block_size
+    if step is None:
+        if (buffers.step + 1) * 2 * width >= (1 << 31):
+            buffers.rebase()
+        step = buffers.step
     tensors = [topk, rows, selected, slots, misses, miss_count, buffers.table, buffers.slot_token,
                buffers.stamps, buffers.slot_base, host_table, promote_src, promote_dst]
     if buffers.bits is not None:

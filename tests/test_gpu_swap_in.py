@@ -183,3 +183,36 @@ def test_paged_blocks_lookup_and_swap_in_match_oracle(gpu, bs):
                 c = want_counts[layer, r]
                 assert np.array_equal(got_src[layer, r, :c], state["promote_src"][layer, r, :c])
                 assert np.array_equal(got_dst[layer, r, :c], state["promote_dst"][layer, r, :c])
+
+
+def test_rebase_mid_stream_changes_no_decision(gpu):
+    # Two hot-buffer sets see the same Top-K stream; one is rebased after step 2
+    # (as swap_in does before its stamps would overflow). Every later table,
+    # slot and promotion must be the same.
+    L, R, T, C, K = 2, 2, 400, 24, 16
+    rng = np.random.default_rng(77)
+    plain, rebased = HotBuffers(L, R, T, C, gpu), HotBuffers(L, R, T, C, gpu)
+    rows = torch.arange(R, device=gpu)
+    lengths = torch.full((R,), T, dtype=torch.int32, device=gpu)
+    host_table = torch.arange(R * T, dtype=torch.int32, device=gpu).reshape(R, T)
+    for step in range(6):
+        topk = torch.tensor(np.stack([rng.permutation(np.concatenate([
+            rng.choice(np.arange(T - 40, T), 12, replace=False), rng.choice(np.arange(0, T - 40), 4, replace=False)]))
+            for _ in range(L * R)]).reshape(L, R, K), dtype=torch.int32, device=gpu)
+        results = []
+        for buffers in (plain, rebased):
+            if buffers is rebased and step == 3:
+                buffers.rebase()
+            slots = torch.empty((L, R, K), dtype=torch.int32, device=gpu)
+            misses = torch.full((L, R, K), -1, dtype=torch.int32, device=gpu)
+            counts = torch.empty((L, R), dtype=torch.int32, device=gpu)
+            resolve_resident(topk, buffers.table, None, rows, lengths, rows, slots, 1, misses=misses,
+                             miss_count=counts, resident_bits=buffers.bits)
+            src = torch.full((L, R, K), -9, dtype=torch.int32, device=gpu)
+            dst = torch.full((L, R, K), -9, dtype=torch.int32, device=gpu)
+            swap_in(topk, 1, rows, rows, slots, misses, counts, buffers, host_table, src, dst)
+            results.append((slots.cpu(), counts.cpu(), src.cpu(), dst.cpu(), buffers.table.cpu(),
+                            buffers.slot_token.cpu()))
+        for a, b in zip(*results):
+            assert torch.equal(a, b), step
+    assert rebased.step == 3 and plain.step == 6

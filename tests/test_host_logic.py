@@ -499,3 +499,28 @@ def test_failed_close_can_be_retried_and_gc_closes():
     allocate_and_drop()
     gc.collect()
     assert library.mapped == 0
+
+
+def test_hot_buffer_rebase_keeps_the_lru_order():
+    import torch
+
+    from adaptive_sparse.swap_in import INT32_MIN, HotBuffers
+
+    buffers = HotBuffers(2, 3, 100, 8, "cpu", with_bits=False)
+    gen = torch.Generator().manual_seed(4)
+    stamps = torch.randint(-50, (1 << 31) - 1, (2, 3, 8), generator=gen, dtype=torch.int64).to(torch.int32)
+    stamps[0, 1, [2, 5]] = INT32_MIN                    # empty slots
+    stamps[1, 2, 3] = stamps[1, 2, 6]                   # a tie: broken by slot index
+    buffers.stamps.copy_(stamps)
+    buffers.step = 123
+
+    def lru_order(values):
+        return [sorted(range(8), key=lambda s: (int(row[s]), s)) for row in values.reshape(-1, 8)]
+
+    before = lru_order(stamps)
+    buffers.rebase()
+    assert buffers.step == 0
+    assert lru_order(buffers.stamps) == before
+    kept = buffers.stamps[buffers.stamps != INT32_MIN]
+    assert int(kept.min()) >= -8 and int(kept.max()) < 0
+    assert (buffers.stamps == INT32_MIN).sum() == 2
