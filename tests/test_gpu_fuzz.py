@@ -35,7 +35,7 @@ def on_gpu(array, dtype, device, strided):
     return spread.to(device)[..., 0]
 
 
-@pytest.mark.parametrize("seed", range(40))
+@pytest.mark.parametrize("seed", range(100))
 def test_lookup_random_configurations(gpu, coracle, seed):
     rng = np.random.default_rng(7000 + seed)
     layers = int(rng.integers(1, 4))
@@ -114,7 +114,7 @@ def random_planes(rng, gpu, layers, kv, rows, row_bytes):
 ROW_BYTES = (2, 6, 8, 24, 64, 128, 512, 1000, 2048, 4096, 40960)
 
 
-@pytest.mark.parametrize("seed", range(30))
+@pytest.mark.parametrize("seed", range(60))
 def test_gather_and_scatter_random_configurations(gpu, coracle, seed):
     rng = np.random.default_rng(8000 + seed)
     layers, kv = int(rng.integers(1, 4)), int(rng.choice([1, 2]))
@@ -151,7 +151,7 @@ def test_gather_and_scatter_random_configurations(gpu, coracle, seed):
         assert np.array_equal(device.cpu().numpy()[offset:], want_pool), seed
 
 
-@pytest.mark.parametrize("seed", range(15))
+@pytest.mark.parametrize("seed", range(30))
 def test_move_random_configurations(gpu, seed):
     rng = np.random.default_rng(9000 + seed)
     layers, kv = int(rng.integers(1, 4)), int(rng.choice([1, 2]))
@@ -177,3 +177,61 @@ def test_move_random_configurations(gpu, seed):
                        src_rows, dst_rows, counts, kv, zero_below=zero_below)
     assert np.array_equal(dst_dev.cpu().numpy()[offset:], want), seed
     assert np.array_equal(dst_dev.cpu().numpy()[:offset], dst_before[:offset])
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_swap_in_random_configurations(gpu, seed):
+    from adaptive_sparse.swap_in import HotBuffers, swap_in
+
+    rng = np.random.default_rng(9500 + seed)
+    L, R = int(rng.integers(1, 3)), int(rng.integers(1, 5))
+    bs = int(rng.choice([1, 1, 2, 3]))
+    K = int(rng.integers(2, 24))
+    W = K * bs
+    T = int(rng.integers(max(W, 2 * K) * 2, 600))
+    C = int(rng.integers(W, W + 40))
+    lengths = np.maximum(rng.integers(T // 2, T + 3, size=R), 1)
+    buffers = HotBuffers(L, R, T, C, gpu)
+    host_table = rng.permutation(R * T).astype(np.int32).reshape(R, T)
+    state = {"table": buffers.table.cpu().numpy(), "slot_token": buffers.slot_token.cpu().numpy(),
+             "stamps": buffers.stamps.cpu().numpy()}
+    rows = torch.arange(R, device=gpu)
+    selected = rng.permutation(R)[: int(rng.integers(1, R + 1))]
+    blocks_total = T // bs
+    for step in range(4):
+        topk = np.stack([rng.permutation(blocks_total)[:K] for _ in range(L * R)]).reshape(L, R, K)
+        topk[rng.random(topk.shape) < 0.1] = -1
+        topk_d = torch.tensor(topk, dtype=torch.int32, device=gpu)
+        slots = torch.full((L, R, W), -3, dtype=torch.int32, device=gpu)
+        misses = torch.full((L, R, W), -1, dtype=torch.int32, device=gpu)
+        counts = torch.zeros((L, R), dtype=torch.int32, device=gpu)
+        resolve_resident(topk_d, buffers.table, None, rows, torch.tensor(lengths, dtype=torch.int32, device=gpu),
+                         torch.tensor(selected, device=gpu), slots, bs, misses=misses, miss_count=counts,
+                         resident_bits=buffers.bits)
+        want_slots, want_misses, want_counts = ref.resolve_resident(
+            topk, state["table"], None, np.arange(R), lengths, selected, bs, np.full((L, R, W), -3, np.int32),
+            with_misses=True)
+        want_counts_full = np.zeros((L, R), np.int32)
+        miss_np = np.full((L, R, W), -1, np.int32)
+        for (layer, r), lanes in want_misses.items():
+            miss_np[layer, r, :len(lanes)] = lanes
+            want_counts_full[layer, r] = len(lanes)
+        assert np.array_equal(slots.cpu().numpy(), want_slots), (seed, step)
+        promote_src = torch.full((L, R, W), -9, dtype=torch.int32, device=gpu)
+        promote_dst = torch.full((L, R, W), -9, dtype=torch.int32, device=gpu)
+        swap_in(topk_d, bs, rows, torch.tensor(selected, device=gpu), slots, misses, counts, buffers,
+                torch.tensor(host_table, device=gpu), promote_src, promote_dst)
+        state = ref.swap_in(step, bs, topk, np.arange(R), selected, want_slots, miss_np, want_counts_full,
+                            state["table"], state["slot_token"], state["stamps"], buffers.slot_base.cpu().numpy(),
+                            host_table)
+        assert np.array_equal(slots.cpu().numpy(), state["slots"]), (seed, step)
+        assert np.array_equal(buffers.table.cpu().numpy(), state["table"]), (seed, step)
+        assert np.array_equal(buffers.slot_token.cpu().numpy(), state["slot_token"]), (seed, step)
+        assert np.array_equal(buffers.stamps.cpu().numpy(), state["stamps"]), (seed, step)
+        assert np.array_equal(buffers.bits.cpu().numpy(), ref.residency_bits(state["table"])), (seed, step)
+        got_src, got_dst = promote_src.cpu().numpy(), promote_dst.cpu().numpy()
+        for layer in range(L):
+            for r in selected:
+                c = want_counts_full[layer, r]
+                assert np.array_equal(got_src[layer, r, :c], state["promote_src"][layer, r, :c]), (seed, step)
+                assert np.array_equal(got_dst[layer, r, :c], state["promote_dst"][layer, r, :c]), (seed, step)
