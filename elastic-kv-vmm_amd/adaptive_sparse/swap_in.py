@@ -35,7 +35,8 @@ class HotBuffers:
     stage its recent window and bitmap row with 16-byte loads.
     """
 
-    def __init__(self, layers, requests, context, capacity, device, *, slot_base=None, with_bits=True):
+    def __init__(self, layers, requests, context, capacity, device, *, slot_base=None, with_bits=True,
+                 step_counter=False):
         self.layers, self.requests, self.context, self.capacity = layers, requests, context, capacity
         self.device = torch.device(device)
         kw = dict(dtype=torch.int32, device=self.device)
@@ -49,6 +50,9 @@ class HotBuffers:
             slot_base = torch.arange(requests, dtype=torch.int64, device=self.device) * capacity + 1
         self.slot_base = slot_base
         self.step = 0
+        # With a device step counter the swap-in reads and advances the step on
+        # the GPU, so a captured HIP graph replays consecutive steps.
+        self.step_counter = torch.zeros(1, dtype=torch.int64, device=self.device) if step_counter else None
 
     def install(self, tokens, local_slots):
         """Make `tokens` [L, R, n] resident in `local_slots` [L, R, n] (setup, not the hot path).
@@ -81,6 +85,17 @@ class HotBuffers:
         empty = self.stamps == INT32_MIN
         self.stamps.copy_(torch.where(empty, torch.full_like(ranks, INT32_MIN), ranks - self.capacity))
         self.step = 0
+        if self.step_counter is not None:
+            self.step_counter.zero_()
+
+    def steps_left(self, width):
+        """Swap-in steps of `width` lanes per row before the stamps need a rebase.
+
+        Reads the device counter when there is one (a synchronizing read):
+        graph replays advance it without the host seeing them.
+        """
+        step = int(self.step_counter.item()) if self.step_counter is not None else self.step
+        return max(0, ((1 << 31) - 1) // (2 * width) - 1 - step)
 
 
 def _ranks_from_stamps(stamps):
@@ -97,8 +112,12 @@ def swap_in(topk, block_size, rows, selected, slots, misses, miss_count, buffers
 
     Stamps are step * 2W + lane in int32; before they would overflow, the
     buffers' stamps are renumbered (HotBuffers.rebase) and the step restarts.
+    With a device step counter (HotBuffers(step_counter=True)) the kernel
+    reads the step from it and advances it, so the call can be captured in a
+    HIP graph; graph users check steps_left() and rebase in time.
     """
     width = topk.shape[2] * block_size
+    counted = buffers.step_counter is not None and step is None
     if step is None:
         if (buffers.step + 1) * 2 * width >= (1 << 31):
             buffers.rebase()
@@ -115,7 +134,12 @@ def swap_in(topk, block_size, rows, selected, slots, misses, miss_count, buffers
                views[9], views[10], views[11], views[12]]
     args = [ct.byref(v) if v is not None else bits_view for v in ordered]
     with torch.cuda.device(device):
-        status = lib.ekv_swap_in(args[0], int(block_size), *args[1:], int(step), _native.stream_handle(device))
+        if counted:
+            counter = _native.describe(buffers.step_counter, "step_counter")
+            status = lib.ekv_swap_in_counted(args[0], int(block_size), *args[1:], ct.byref(counter),
+                                             _native.stream_handle(device))
+        else:
+            status = lib.ekv_swap_in(args[0], int(block_size), *args[1:], int(step), _native.stream_handle(device))
     _native.check(lib, status, "swap_in")
     buffers.step = step + 1
 

@@ -64,6 +64,7 @@ struct SwapArgs {
     int64_t batch, table_rows, capacity, capacity_pow2;
     uint32_t width;
     int64_t step;
+    const int64_t* step_counter;    // when set, the step is read from device memory (graph replays)
 };
 
 __device__ __forceinline__ int64_t lane_position(const SwapArgs& a, const void* topk_row, uint32_t lane) {
@@ -90,7 +91,20 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
     const int64_t base = a.slot_base[req];
     const int64_t C = a.capacity;
     const int64_t W = a.width;
-    const int64_t stamp_base = a.step * 2 * W;
+    const int64_t step = a.step_counter != nullptr ? *a.step_counter : a.step;  // uniform
+    if (step < 0 || (step + 1) * 2 * W >= (int64_t{1} << 31)) {
+        // Stamps would overflow (a device counter the caller did not rebase in
+        // time): change nothing, and record empty promotions so the move that
+        // follows copies nothing; the missed lanes keep slot 0 (zero rows).
+        const int32_t counted = a.counts[l * a.ct_l + b * a.ct_b];
+        const int64_t m = counted < 0 ? 0 : (counted > W ? W : counted);
+        for (int64_t i = threadIdx.x; i < m; i += kThreads) {
+            a.promote_src[l * a.ps_l + b * a.ps_b + i * a.ps_o] = -1;
+            a.promote_dst[l * a.pd_l + b * a.pd_b + i * a.pd_o] = -1;
+        }
+        return;
+    }
+    const int64_t stamp_base = step * 2 * W;
     int32_t* slots = a.slots + l * a.sl_l + b * a.sl_b;
     int32_t* table = a.table + l * a.tb_l + req * a.tb_r;
     int32_t* slot_token = a.slot_token + l * a.st_l + req * a.st_r;
@@ -178,6 +192,13 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
     }
 }
 
+// One thread advances the device step counter after the swap-in of a replay.
+__global__ void advance_step_kernel(int64_t* counter) {
+    if (threadIdx.x == 0) {
+        counter[0] += 1;
+    }
+}
+
 void need_i32(const ekv_tensor& t, const char* name) {
     if (t.dtype != EKV_INT32) {
         throw std::invalid_argument(std::string(name) + " must be int32");
@@ -188,7 +209,8 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
             const ekv_tensor* slots_p, const ekv_tensor* misses_p, const ekv_tensor* counts_p,
             const ekv_tensor* table_p, const ekv_tensor* bits_p, const ekv_tensor* slot_token_p,
             const ekv_tensor* stamps_p, const ekv_tensor* slot_base_p, const ekv_tensor* host_table_p,
-            const ekv_tensor* promote_src_p, const ekv_tensor* promote_dst_p, int64_t step, void* stream) {
+            const ekv_tensor* promote_src_p, const ekv_tensor* promote_dst_p, int64_t step,
+            const ekv_tensor* step_counter_p, void* stream) {
     const ekv_tensor& topk = need(topk_p, "topk");
     const ekv_tensor& rows = need(rows_p, "rows");
     const ekv_tensor& selected = need(selected_p, "selected");
@@ -238,6 +260,14 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
     if (T >= (int64_t{1} << 31) || step < 0 || (step + 1) * 2 * W >= (int64_t{1} << 31)) {
         throw std::invalid_argument("token count or step outside the 32-bit stamp range");
     }
+    int64_t* counter = nullptr;
+    if (step_counter_p != nullptr) {
+        const ekv_tensor& c = need(step_counter_p, "step_counter");
+        if (c.dtype != EKV_INT64 || numel(c) != 1 || c.data == nullptr) {
+            throw std::invalid_argument("step_counter must be one int64 element in device memory");
+        }
+        counter = static_cast<int64_t*>(c.data);
+    }
     need_ndim(rows, 1, "rows");
     need_ndim(selected, 1, "selected");
     need_ndim(slot_base, 1, "slot_base");
@@ -262,6 +292,10 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
     }
     const int64_t count = selected.shape[0];
     if (count == 0 || L == 0 || W == 0) {
+        if (counter != nullptr) {
+            advance_step_kernel<<<dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream)>>>(counter);
+            check_hip(hipGetLastError(), "launch step advance");
+        }
         return 0;
     }
     if (L > 65535 || count > 0x7fffffff) {
@@ -311,6 +345,7 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
     }
     a.width = static_cast<uint32_t>(W);
     a.step = step;
+    a.step_counter = counter;
     for (const auto* t : {&topk, &rows, &selected, &slots, &misses, &counts, &table, &slot_token, &stamps,
                           &slot_base, &host_table, &promote_src, &promote_dst}) {
         need_data(*t, "tensor");
@@ -322,8 +357,13 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
                   "raise the swap-in LDS limit");
     }
     const dim3 grid(static_cast<uint32_t>(count), static_cast<uint32_t>(L));
-    swap_in_kernel<<<grid, dim3(kThreads), lds, static_cast<hipStream_t>(stream)>>>(a);
+    const auto s = static_cast<hipStream_t>(stream);
+    swap_in_kernel<<<grid, dim3(kThreads), lds, s>>>(a);
     check_hip(hipGetLastError(), "launch swap-in");
+    if (counter != nullptr) {
+        advance_step_kernel<<<dim3(1), dim3(64), 0, s>>>(counter);
+        check_hip(hipGetLastError(), "launch step advance");
+    }
     return 0;
 }
 
@@ -338,6 +378,24 @@ extern "C" int ekv_swap_in(const ekv_tensor* topk, int64_t block_size, const ekv
                            const ekv_tensor* promote_dst, int64_t step, void* stream) {
     return ekv::guarded(-1, [&] {
         return ekv::swap_in(topk, block_size, rows, selected, slots, misses, miss_count, table, resident_bits,
-                            slot_token, stamps, slot_base, host_table, promote_src, promote_dst, step, stream);
+                            slot_token, stamps, slot_base, host_table, promote_src, promote_dst, step, nullptr,
+                            stream);
+    });
+}
+
+extern "C" int ekv_swap_in_counted(const ekv_tensor* topk, int64_t block_size, const ekv_tensor* rows,
+                                   const ekv_tensor* selected, const ekv_tensor* slots, const ekv_tensor* misses,
+                                   const ekv_tensor* miss_count, const ekv_tensor* table,
+                                   const ekv_tensor* resident_bits, const ekv_tensor* slot_token,
+                                   const ekv_tensor* stamps, const ekv_tensor* slot_base,
+                                   const ekv_tensor* host_table, const ekv_tensor* promote_src,
+                                   const ekv_tensor* promote_dst, const ekv_tensor* step_counter, void* stream) {
+    return ekv::guarded(-1, [&] {
+        if (step_counter == nullptr) {
+            throw std::invalid_argument("step_counter is required");
+        }
+        return ekv::swap_in(topk, block_size, rows, selected, slots, misses, miss_count, table, resident_bits,
+                            slot_token, stamps, slot_base, host_table, promote_src, promote_dst, 0, step_counter,
+                            stream);
     });
 }

@@ -70,6 +70,7 @@ _SIGNATURES = {
     "ekv_scatter_kv": ([ct.POINTER(EkvPlanes), _P_TENSOR, ct.POINTER(EkvKvRows), ct.c_int64, ct.c_void_p],
                        ct.c_int),
     "ekv_swap_in": ([_P_TENSOR, ct.c_int64] + [_P_TENSOR] * 13 + [ct.c_int64, ct.c_void_p], ct.c_int),
+    "ekv_swap_in_counted": ([_P_TENSOR, ct.c_int64] + [_P_TENSOR] * 14 + [ct.c_void_p], ct.c_int),
     "ekv_move_kv": ([ct.POINTER(EkvPlanes), _P_TENSOR, ct.POINTER(EkvPlanes), _P_TENSOR, _P_TENSOR, ct.c_int64,
                      ct.c_void_p], ct.c_int),
     "ekv_compare_kv": ([ct.POINTER(EkvPlanes), _P_TENSOR, ct.POINTER(EkvPlanes), _P_TENSOR, _P_TENSOR,

@@ -199,6 +199,24 @@ int ekv_swap_in(const ekv_tensor* topk, int64_t block_size, const ekv_tensor* ro
                 int64_t step, void* stream);
 
 /*
+ * ekv_swap_in with the step read from device memory: step_counter [1] int64
+ * holds the step of this call and is incremented after the swap-in (a second
+ * launch on the same stream), so a captured HIP graph replays consecutive
+ * steps. The caller keeps (step + 1) * 2W below 2^31 (rebasing the stamps
+ * and the counter in time); a call past that limit changes nothing and
+ * records empty promotions.
+ * No reference counterpart: the graph-replayable form of ekv_swap_in.
+ */
+int ekv_swap_in_counted(const ekv_tensor* topk, int64_t block_size, const ekv_tensor* rows,
+                        const ekv_tensor* selected, const ekv_tensor* slots,
+                        const ekv_tensor* misses, const ekv_tensor* miss_count,
+                        const ekv_tensor* table, const ekv_tensor* resident_bits,
+                        const ekv_tensor* slot_token, const ekv_tensor* stamps,
+                        const ekv_tensor* slot_base, const ekv_tensor* host_table,
+                        const ekv_tensor* promote_src, const ekv_tensor* promote_dst,
+                        const ekv_tensor* step_counter, void* stream);
+
+/*
  * Row moves between two plane sets: for i < counts[l, b] and both kv planes,
  *   dst(l, kv)[dst_rows[l, b, i]] = src(l, kv)[src_rows[l, b, i]]
  * when 0 <= src row < src->rows and zero_below <= dst row < dst->rows (other

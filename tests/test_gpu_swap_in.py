@@ -216,3 +216,84 @@ def test_rebase_mid_stream_changes_no_decision(gpu):
         for a, b in zip(*results):
             assert torch.equal(a, b), step
     assert rebased.step == 3 and plain.step == 6
+
+
+def test_whole_decode_step_replays_from_one_graph(gpu):
+    # Lookup -> swap-in (device step counter) -> promote from pinned host -> gather,
+    # captured once and replayed for five steps with new Top-K contents. After every
+    # replay the LRU state equals the oracle's at that step and every gathered row is
+    # its token's host row.
+    L, R, T, K, row_bytes, capacity = 2, 3, 300, 32, 64, 64
+    rng = np.random.default_rng(21)
+    buffers = HotBuffers(L, R, T, capacity, gpu, step_counter=True)
+    host_table = torch.arange(R * T, dtype=torch.int32).reshape(R, T)
+    host_table_d = host_table.to(gpu)
+    plane = R * T * row_bytes
+    arena = HostArena(L * 2 * plane)
+    try:
+        arena.host.copy_(torch.randint(0, 256, (L * 2 * plane,), dtype=torch.uint8))
+        host_planes = KVPlanes(base=arena.device_ptr, device=0, layers=L, kv=2, layer_stride=2 * plane,
+                               kv_stride=plane, row_stride=row_bytes, row_bytes=row_bytes, rows=R * T, owner=arena)
+        pool_rows = 1 + R * capacity
+        pool = torch.zeros(L * 2 * pool_rows * row_bytes, dtype=torch.uint8, device=gpu)
+        pool_planes = KVPlanes(base=pool.data_ptr(), device=0, layers=L, kv=2, layer_stride=2 * pool_rows * row_bytes,
+                               kv_stride=pool_rows * row_bytes, row_stride=row_bytes, row_bytes=row_bytes,
+                               rows=pool_rows, owner=pool)
+        host = arena.host.numpy().reshape(L, 2, R * T, row_bytes)
+        rows = torch.arange(R, device=gpu)
+        lengths = torch.full((R,), T, dtype=torch.int32, device=gpu)
+        topk_d = torch.zeros((L, R, K), dtype=torch.int32, device=gpu)
+        slots = torch.empty((L, R, K), dtype=torch.int32, device=gpu)
+        misses = torch.full((L, R, K), -1, dtype=torch.int32, device=gpu)
+        counts = torch.empty((L, R), dtype=torch.int32, device=gpu)
+        promote_src = torch.full((L, R, K), -9, dtype=torch.int32, device=gpu)
+        promote_dst = torch.full((L, R, K), -9, dtype=torch.int32, device=gpu)
+        out = torch.empty((R, L, 2, K, row_bytes), dtype=torch.uint8, device=gpu)
+
+        def decode_step():
+            resolve_resident(topk_d, buffers.table, None, rows, lengths, rows, slots, 1, misses=misses,
+                             miss_count=counts, resident_bits=buffers.bits)
+            swap_in(topk_d, 1, rows, rows, slots, misses, counts, buffers, host_table_d, promote_src, promote_dst)
+            move_kv(host_planes, promote_src, pool_planes, promote_dst, counts)
+            gather_kv(pool_planes, slots, out)
+
+        state = {"table": buffers.table.cpu().numpy(), "slot_token": buffers.slot_token.cpu().numpy(),
+                 "stamps": buffers.stamps.cpu().numpy()}
+        graph = None
+        for step in range(6):
+            near = [np.concatenate([rng.choice(np.arange(T - 50, T), 24, replace=False),
+                                    rng.choice(np.arange(0, T - 50), 8, replace=False)]) for _ in range(L * R)]
+            topk = np.stack([rng.permutation(x) for x in near]).reshape(L, R, K)
+            topk_d.copy_(torch.tensor(topk, dtype=torch.int32))
+            if step == 0:
+                decode_step()                        # eager step 0, also loads every kernel
+                torch.cuda.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    decode_step()                    # recorded, not run
+            else:
+                graph.replay()
+            torch.cuda.synchronize()
+            assert int(buffers.step_counter.item()) == step + 1
+            want_slots, want_misses, want_counts = ref.resolve_resident(
+                topk, state["table"], None, np.arange(R), np.full(R, T), np.arange(R), 1,
+                np.zeros((L, R, K), np.int32), with_misses=True)
+            miss_np = np.full((L, R, K), -1, np.int32)
+            for (layer, r), lanes in want_misses.items():
+                miss_np[layer, r, :len(lanes)] = lanes
+            state = ref.swap_in(step, 1, topk, np.arange(R), np.arange(R), want_slots, miss_np, want_counts,
+                                state["table"], state["slot_token"], state["stamps"],
+                                buffers.slot_base.cpu().numpy(), host_table.numpy())
+            assert np.array_equal(slots.cpu().numpy(), state["slots"]), step
+            assert np.array_equal(buffers.table.cpu().numpy(), state["table"]), step
+            assert np.array_equal(buffers.stamps.cpu().numpy(), state["stamps"]), step
+            got = out.cpu().numpy()
+            for layer in range(L):
+                for r in range(R):
+                    host_rows = host_table.numpy()[r, topk[layer, r]]
+                    for kv in range(2):
+                        assert np.array_equal(got[r, layer, kv], host[layer, kv, host_rows]), (step, layer, r, kv)
+        del graph
+    finally:
+        torch.cuda.synchronize()
+        arena.close()
