@@ -719,7 +719,7 @@ def run_composite(torch, args, device):
                            kv_stride=host_plane, row_stride=row_bytes, row_bytes=row_bytes, rows=HOST_ROWS, owner=arena)
     host_table = ((torch.arange(R, device=device).view(R, 1) * T + torch.arange(T, device=device).view(1, T))
                   % HOST_ROWS).to(torch.int32)
-    buffers = HotBuffers(L, R, T, C, device)
+    buffers = HotBuffers(L, R, T, C, device, step_counter=True)   # graph-replayable swap-in
     recent = (lengths.view(1, R, 1) - C + torch.arange(C, device=device).view(1, 1, C)).expand(L, R, C)
     local = torch.rand((L, R, C), generator=gen, device=device).argsort(-1)
     buffers.install(recent, local)
@@ -769,6 +769,8 @@ def run_composite(torch, args, device):
         for key, value in zip(remap_parts, (r1 - r0, r2 - r1, r3 - r2)):
             remap_parts[key].append(value * 1e3)
 
+    topk = torch.zeros((L, R, K), dtype=torch.int32, device=device)   # refilled in place every step
+
     def lookup():
         resolve_resident(topk, buffers.table, None, rows, lengths32, rows, slots, 1, misses=misses,
                          miss_count=counts, resident_bits=buffers.bits)
@@ -784,8 +786,20 @@ def run_composite(torch, args, device):
 
     phases = {name: [] for name in ("remap_ms", "lookup_ms", "swap_ms", "promote_ms", "gather_ms", "step_ms")}
     promoted, verified = [], True
+    def verify():
+        # every lane is resident after the step: its gathered rows must be its token's host rows
+        ok = True
+        for layer in (0, L - 1):
+            host_rows = torch.gather(host_table, 1, topk[layer].long()).long()        # [R, K]
+            for kv in range(2):
+                base = (layer * 2 + kv) * host_plane
+                expect = arena.host.narrow(0, base, host_plane).view(HOST_ROWS, row_bytes)[host_rows.cpu()]
+                got = output[:, layer, kv].contiguous().view(torch.uint8).view(R, K, row_bytes).cpu()
+                ok &= bool(torch.equal(got, expect))
+        return ok
+
     for step in range(args.warmup + args.steps):
-        topk = composite_topk(torch, device, L, R, K, lengths, gen)
+        topk.copy_(composite_topk(torch, device, L, R, K, lengths, gen))
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         if remap_count:
@@ -805,19 +819,35 @@ def run_composite(torch, args, device):
         t2 = time.perf_counter()
         promoted.append(int(counts.sum().item()))
         if step == args.warmup + args.steps - 1 or step == 0:
-            # every lane is resident now: its gathered rows must be its token's host rows
-            for layer in (0, L - 1):
-                host_rows = torch.gather(host_table, 1, topk[layer].long()).long()        # [R, K]
-                for kv in range(2):
-                    base = (layer * 2 + kv) * host_plane
-                    expect = arena.host.narrow(0, base, host_plane).view(HOST_ROWS, row_bytes)[host_rows.cpu()]
-                    got = output[:, layer, kv].contiguous().view(torch.uint8).view(R, K, row_bytes).cpu()
-                    verified &= bool(torch.equal(got, expect))
+            verified &= verify()
         if step >= args.warmup:
             phases["remap_ms"].append((t1 - t0) * 1e3)
             for i, name in enumerate(("lookup_ms", "swap_ms", "promote_ms", "gather_ms")):
                 phases[name].append(ev[i].elapsed_time(ev[i + 1]))
             phases["step_ms"].append((t2 - t0) * 1e3)
+    # The same step replayed from one HIP graph (the swap-in reads its LRU step from
+    # the device counter), with the chunk remap between replays.
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        lookup()
+        swap()
+        promote()
+        gather()
+    graph_ms, graph_verified = [], True
+    for replay in range(max(2, min(args.steps, 5))):
+        topk.copy_(composite_topk(torch, device, L, R, K, lengths, gen))
+        torch.cuda.synchronize()
+        if remap_count:
+            remap()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        stop.record()
+        stop.synchronize()
+        graph_ms.append(start.elapsed_time(stop))
+        graph_verified &= verify()
+    del graph
+    log(f"graph replays: {statistics.mean(graph_ms):.2f} ms of GPU time per step, verified {graph_verified}")
     mean = {k: statistics.mean(v) for k, v in phases.items()}
     lanes = L * R * K
     misses_per_step = statistics.mean(promoted[args.warmup:])
@@ -837,7 +867,9 @@ def run_composite(torch, args, device):
              "lookups_per_s": round(lanes / (mean["lookup_ms"] / 1e3), 1),
              "step_ms_without_remap": round(mean["step_ms"] - mean["remap_ms"], 3),
              "remap_parts_ms": {k: round(statistics.mean(v[args.warmup:] or v), 2) for k, v in remap_parts.items()},
-             "remapped_chunks_per_step": remap_count, "pool_commit_s": round(commit_s, 3)}
+             "remapped_chunks_per_step": remap_count, "pool_commit_s": round(commit_s, 3),
+             "graph_replay": {"replays": len(graph_ms), "gpu_ms_per_step": round(statistics.mean(graph_ms), 3),
+                              "verified_against_host_copy": graph_verified}}
     result = envelope(args, gather_bytes / (mean["step_ms"] / 1e3) / 1e9, mean["step_ms"], config, roof, None, extra,
                       metric="composite decode step: gathered GB/s per step (lookup, LRU swap-in, promote, gather, remap)")
     del raw, output
