@@ -222,7 +222,9 @@ def test_whole_decode_step_replays_from_one_graph(gpu):
     # Lookup -> swap-in (device step counter) -> promote from pinned host -> gather,
     # captured once and replayed for five steps with new Top-K contents. After every
     # replay the LRU state equals the oracle's at that step and every gathered row is
-    # its token's host row.
+    # its token's host row. Replays 3 and 4 carry a padded batch row (length 0, as a
+    # graph captured for a larger batch runs): it must yield -1 slots, no misses, no
+    # promotions and zero rows, and leave its hot buffer untouched.
     L, R, T, K, row_bytes, capacity = 2, 3, 300, 32, 64, 64
     rng = np.random.default_rng(21)
     buffers = HotBuffers(L, R, T, capacity, gpu, step_counter=True)
@@ -265,6 +267,10 @@ def test_whole_decode_step_replays_from_one_graph(gpu):
                                     rng.choice(np.arange(0, T - 50), 8, replace=False)]) for _ in range(L * R)]
             topk = np.stack([rng.permutation(x) for x in near]).reshape(L, R, K)
             topk_d.copy_(torch.tensor(topk, dtype=torch.int32))
+            step_lengths = np.full(R, T)
+            if step in (3, 4):
+                step_lengths[1] = 0                  # a padded row
+            lengths.copy_(torch.tensor(step_lengths, dtype=torch.int32))
             if step == 0:
                 decode_step()                        # eager step 0, also loads every kernel
                 torch.cuda.synchronize()
@@ -276,7 +282,7 @@ def test_whole_decode_step_replays_from_one_graph(gpu):
             torch.cuda.synchronize()
             assert int(buffers.step_counter.item()) == step + 1
             want_slots, want_misses, want_counts = ref.resolve_resident(
-                topk, state["table"], None, np.arange(R), np.full(R, T), np.arange(R), 1,
+                topk, state["table"], None, np.arange(R), step_lengths, np.arange(R), 1,
                 np.zeros((L, R, K), np.int32), with_misses=True)
             miss_np = np.full((L, R, K), -1, np.int32)
             for (layer, r), lanes in want_misses.items():
@@ -290,6 +296,10 @@ def test_whole_decode_step_replays_from_one_graph(gpu):
             got = out.cpu().numpy()
             for layer in range(L):
                 for r in range(R):
+                    if step_lengths[r] == 0:
+                        assert (slots[layer, r] == -1).all() and int(counts[layer, r]) == 0, step
+                        assert not got[r, layer].any(), step
+                        continue
                     host_rows = host_table.numpy()[r, topk[layer, r]]
                     for kv in range(2):
                         assert np.array_equal(got[r, layer, kv], host[layer, kv, host_rows]), (step, layer, r, kv)
