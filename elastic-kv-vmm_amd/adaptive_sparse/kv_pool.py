@@ -150,3 +150,41 @@ class BlockMajorLayout:
                         layer_stride=self.kv * self.row_bytes, kv_stride=self.row_bytes,
                         row_stride=self.block_bytes, row_bytes=self.row_bytes, rows=self.blocks,
                         owner=owner)
+
+
+class BlockSegments:
+    """Chunk projection of vLLM-style KV tensors sharing one backing allocation.
+
+    Follows vllm_integration/adapter.py:31-64 (Residency): every layer tensor
+    is a segment (start, block_stride) of the allocation, block b of a
+    segment occupies [start + b * block_stride, + page_bytes), and a block's
+    chunks are those every segment's page touches.
+    """
+
+    def __init__(self, segments, page_bytes, num_blocks, allocation_bytes, chunk_bytes=2 << 20):
+        self.segments = [(int(start), int(stride)) for start, stride in segments]
+        self.page_bytes = int(page_bytes)
+        self.num_blocks = int(num_blocks)
+        self.chunk_bytes = int(chunk_bytes)
+        _positive("page_bytes", self.page_bytes)
+        _positive("chunk_bytes", self.chunk_bytes)
+        if self.num_blocks < 2:
+            raise ValueError("a block layout needs at least two blocks (block 0 is the sink)")
+        if any(start < 0 or stride <= 0 or start + (self.num_blocks - 1) * stride + self.page_bytes > allocation_bytes
+               for start, stride in self.segments):
+            raise ValueError("KV tensor segments exceed the allocation")
+
+    def chunks(self, blocks):
+        """Chunk ids holding any byte of the given blocks in any segment."""
+        indices = set()
+        for block in blocks:
+            if not 0 <= block < self.num_blocks:
+                raise ValueError(f"Invalid KV block {block}")
+            for start, stride in self.segments:
+                offset = start + block * stride
+                indices.update(range(offset // self.chunk_bytes, (offset + self.page_bytes - 1) // self.chunk_bytes + 1))
+        return indices
+
+    def sink_chunks(self):
+        """Chunks that stay mapped for the sink block 0 (and chunk 0)."""
+        return self.chunks([0]) | {0}

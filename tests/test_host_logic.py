@@ -524,3 +524,24 @@ def test_hot_buffer_rebase_keeps_the_lru_order():
     kept = buffers.stamps[buffers.stamps != INT32_MIN]
     assert int(kept.min()) >= -8 and int(kept.max()) < 0
     assert (buffers.stamps == INT32_MIN).sum() == 2
+
+
+def test_block_segments_hand_case_and_plane_layout_equivalence():
+    from adaptive_sparse.kv_pool import BlockSegments, PlanePoolLayout
+
+    # Two segments, 100-byte pages in 256-byte chunks.
+    seg = BlockSegments([(0, 100), (1000, 100)], page_bytes=100, num_blocks=8, allocation_bytes=1800,
+                        chunk_bytes=256)
+    assert seg.chunks([2]) == {0, 1, 4, 5}                      # bytes 200-299 and 1200-1299
+    assert seg.sink_chunks() == {0, 3, 4}                        # block 0: bytes 0-99 and 1000-1099
+    with pytest.raises(ValueError, match="Invalid KV block"):
+        seg.chunks([8])
+    with pytest.raises(ValueError, match="exceed"):
+        BlockSegments([(0, 100), (1000, 100)], 100, 9, 1800, 256)
+    # The block-gather geometry (36 layers x K/V planes of 20,000 blocks of 32 KiB) projects the
+    # same chunks through either description.
+    layout = PlanePoolLayout(layers=36, kv=2, rows=20000, row_bytes=32768)
+    segments = BlockSegments([(layout.plane_offset(l, kv), 32768) for l in range(36) for kv in range(2)],
+                             32768, 20000, layout.capacity_bytes, layout.chunk_bytes)
+    for blocks in ([0], [1, 63, 64], [19999], list(range(100, 140))):
+        assert segments.chunks(blocks) == layout.chunks_for_slots(blocks)
