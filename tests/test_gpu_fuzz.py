@@ -3,7 +3,8 @@
 Each case draws its shapes, dtypes, strides (views of larger buffers), block
 size, table form (single or two level, with or without a layer dimension,
 with or without the residency bitmap), lengths, selections, row sizes and
-vector widths, plane strides and zero_below from a seed. The cases are small
+vector widths, plane strides and zero_below from a seed, including request
+rows outside the table and selection entries outside the batch. The cases are small
 (the oracle runs in milliseconds) and together cover the kernels' branches:
 the recent-window staging, the bitmap staged in LDS or read per lane, the
 dense and strided addressing, every vector width of the copy engine, and
@@ -53,6 +54,8 @@ def test_lookup_random_configurations(gpu, coracle, seed):
 
     lengths = rng.integers(-2, cols + 5, size=batch)
     rows = rng.integers(0, rrows, size=batch)
+    stray = rng.random(batch) < 0.1          # request rows outside the table resolve to -1
+    rows[stray] = rng.choice([-1, rrows, rrows + 7], size=int(stray.sum()))
     width = k * bs
     topk = rng.integers(-1, cols // bs + 2, size=(layers, batch, k))
     for r in range(batch):  # a recent-heavy share, as decode Top-K sets are
@@ -70,6 +73,8 @@ def test_lookup_random_configurations(gpu, coracle, seed):
         table = rng.integers(1, 1 << 20, size=shape)
         table[rng.random(shape) < 0.4] = 0
     selected = rng.permutation(batch)[: int(rng.integers(1, batch + 1))]
+    if rng.random() < 0.2:                   # selection entries outside the batch are skipped
+        selected = np.concatenate([selected, [-1, batch]])
     initial = np.full((layers, batch, width), -77, np.int32)
     want, want_misses, want_counts = coracle.resolve_resident(topk, table, mapping, rows, lengths, selected, bs,
                                                               initial, with_misses=True)
