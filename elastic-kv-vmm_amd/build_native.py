@@ -18,7 +18,7 @@ PACKAGE_ROOT = Path(__file__).resolve().parent
 SOURCE_DIR = PACKAGE_ROOT / "csrc"
 BUILD_DIR = PACKAGE_ROOT / "_build"
 LIBRARY = PACKAGE_ROOT / "lib" / "libelastic_vmm.so"
-SOURCES = ("vmm_backing.hip", "lookup.hip", "gather.hip", "swap_in.hip", "compare.hip")
+SOURCES = ("vmm_backing.hip", "lookup.hip", "gather.hip", "swap_in.hip", "compare.hip", "hisparse_swap.hip")
 OFFLOAD_ARCH = "gfx950"
 
 COMMON_FLAGS = [

@@ -1,0 +1,675 @@
+// HiSparse hot-buffer swap-in with the calling convention of SGLang's
+// load_blocks_to_device_buffer_mha (gfx950).
+//
+// The reference's decode path reaches that third-party kernel through its
+// HiSparse coordinator (adaptive_sparse/request_residency.py:805-809,829-832).
+// Its observable behaviour is pinned by the reference's own smoke test
+// (tests/smoke_minimax_swap.py:18-67) and models:
+//   - selected tokens: each Top-K block >= 0 expanded to block * bs + j,
+//     kept when below the row's length, in Top-K order
+//     (adaptive_sparse/hisparse_access_trace.py:59-64);
+//   - the newest token (length - 1) always hits (:68-70), at the reserved
+//     slot H (its data was written there by the decode step, so it is never
+//     copied);
+//   - any other token hits when one of the H hot slots holds it;
+//   - batch-token LRU (benchmarks/hisparse_locality_replay.py:90-99): misses
+//     are counted at entry, hits are touched in selection order, the misses
+//     take the least recent slots (empty slots first) and are inserted in
+//     selection order; their K and V rows are copied from the pinned host
+//     cache into the device rows of their slots;
+//   - the output lists the device location of every selected token in
+//     selection order, then -1 (tests/smoke_minimax_swap.py:58-66).
+// State per request r: device_buffer_tokens[r, i] (token in slot i, -1 =
+// empty; column H untouched), lru_slots[r, 0..H) (slots from least to most
+// recent), device_buffer_locs[r, i] (device row of slot i; column H is the
+// reserved newest-token row), host_cache_locs[r, t] (host row of token t).
+//
+// One 256-thread workgroup per batch row:
+//   1. the hot tokens are hashed into LDS (open addressing, at least 2H
+//      buckets holding slot ids, so every probe sequence meets an empty
+//      bucket);
+//   2. each lane probes the hash: a hit records its slot, a miss claims a
+//      bucket for its token. A token repeated in a row (a repeated Top-K
+//      block) is classified once, by its first lane (atomicMin), and its
+//      other lanes reuse that lane's location, so the hot buffer never holds
+//      a token twice;
+//   3. ranks in selection order (output position, hit rank, miss rank) are
+//      wave ballot + mbcnt prefix sums with one LDS exchange per chunk;
+//   4. prefix sums over the old LRU order give each slot's place in the new
+//      order and the victims (empty slots first, then untouched slots);
+//   5. the misses' rows are copied from mapped pinned host memory, 16 bytes
+//      per lane when rows and bases allow.
+// Locations outside the device buffer are reported as -1 and never written.
+#include "../../include/ekv_kernels.h"
+#include "ekv_common.h"
+#include "ekv_fastdiv.h"
+#include "ekv_tensor_util.h"
+#include "ekv_vec.h"
+
+#include <climits>
+
+namespace ekv {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int64_t kMaxHot = 4096;     // hot slots per request (LDS holds the hash and the order)
+constexpr int64_t kMaxLanes = 2048;   // selected lanes per row (Top-K blocks x block size)
+constexpr int32_t kEmpty = -1;
+
+enum LaneKind : uint8_t { kInvalid = 0, kNewest = 1, kHit = 2, kMiss = 3 };
+
+struct HsArgs {
+    const void* topk;                  // [B, K] block ids
+    int32_t topk64;
+    int64_t topk_sb, topk_sk;
+    int32_t* tokens;                   // device_buffer_tokens [R, >= H + 1] int32
+    int64_t tok_sr, tok_ss;
+    const void* host_locs;             // host_cache_locs [R, T]
+    int32_t host_locs64;
+    int64_t hl_sr, hl_st;
+    const void* dev_locs;              // device_buffer_locs [R, >= H + 1]
+    int32_t dev_locs64;
+    int64_t dl_sr, dl_ss;
+    void* lru;                         // lru_slots [R, H] int16 or int32
+    int32_t lru32;
+    int64_t lru_sr, lru_ss;
+    int32_t* out;                      // top_k_device_locs [B, W] int32
+    int64_t out_sb, out_so;
+    IndexRef req, seq;                 // [B]
+    IndexRef num_real;                 // [1] (data null: every row is real)
+    const char* host_k;                // mapped pinned host rows
+    int64_t host_kv, host_rs, host_rows;
+    char* dev_k;                       // device rows
+    int64_t dev_kv, dev_rs, dev_rows;
+    int64_t row_bytes;
+    int64_t batch, R, T, H, HB;
+    uint32_t hb_shift;                 // 32 - log2(HB)
+    uint32_t width;                    // W = K * block size
+    uint32_t block_size;
+    FastDiv block_div;
+};
+
+struct Lds {
+    int32_t* hash;        // [HB] slot id (< H), H + lane (pending miss), or kEmpty
+    int32_t* tok;         // [H] token per slot
+    int32_t* first_touch; // [H] lowest lane that hit the slot (INT32_MAX: none)
+    int16_t* hit_rank;    // [H] rank of the slot's first hit among first hits (-1: none)
+    int16_t* order;       // [H] old LRU order
+    int16_t* victim;      // [W] slot taken by the m-th miss (-1: none)
+    int16_t* miss_lane;   // [W] lane of the m-th miss
+    int16_t* lane_rank;   // [W] miss rank of a lane that owns its token's miss
+    int32_t* lane_tok;    // [W]
+    int32_t* lane_aux;    // [W] hit: slot; miss: hash bucket
+    int32_t* lane_pos;    // [W] output position (-1: not selected)
+    int32_t* miss_host;   // [W] host row of the m-th miss
+    int32_t* miss_loc;    // [W] device row of the m-th miss (-1: none)
+    uint8_t* lane_kind;   // [W]
+    int32_t* scratch;     // [3 * kWaves + 4]
+};
+
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
+
+// Exclusive ranks of N flags over the workgroup's threads in thread order,
+// and their totals. Every thread must call it (two barriers).
+template <int N>
+__device__ __forceinline__ void rank_flags(const bool (&flag)[N], int32_t (&rank)[N], int32_t (&total)[N],
+                                           int32_t* scratch) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    uint64_t mask[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        mask[k] = __ballot(flag[k]);
+        if (lane == 0) {
+            scratch[k * kWaves + wave] = __popcll(mask[k]);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        int32_t before = 0, all = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const int32_t c = scratch[k * kWaves + w];
+            before += w < wave ? c : 0;
+            all += c;
+        }
+        rank[k] = before + static_cast<int32_t>(lanes_below(mask[k]));
+        total[k] = all;
+    }
+    __syncthreads();  // scratch is rewritten by the next call
+}
+
+__device__ __forceinline__ int64_t load_index(const void* base, int32_t is64, int64_t offset) {
+    return is64 ? static_cast<const int64_t*>(base)[offset]
+                : static_cast<int64_t>(static_cast<const int32_t*>(base)[offset]);
+}
+
+__device__ __forceinline__ uint32_t bucket_of(const HsArgs& a, int32_t token) {
+    return (static_cast<uint32_t>(token) * 0x9E3779B1u) >> a.hb_shift;
+}
+
+// A hash entry read while other lanes may be claiming buckets.
+__device__ __forceinline__ int32_t load_entry(const Lds& s, uint32_t bucket) {
+    return __hip_atomic_load(&s.hash[bucket], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Device row of slot `slot` (0..H), or -1 when outside the device buffer.
+__device__ __forceinline__ int64_t device_row(const HsArgs& a, int64_t r, int64_t slot) {
+    const int64_t row = load_index(a.dev_locs, a.dev_locs64, r * a.dl_sr + slot * a.dl_ss);
+    return row >= 0 && row < a.dev_rows ? row : -1;
+}
+
+template <typename V>
+__device__ __forceinline__ void copy_rows(const HsArgs& a, const Lds& s, int32_t misses) {
+    // Wave w copies misses w, w + 4, ...: both planes of one row per pass,
+    // all of the pass's loads issued before its stores.
+    constexpr int64_t kWidth = sizeof(V);
+    const int64_t pieces = a.row_bytes / kWidth;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    for (int32_t m = wave; m < misses; m += kWaves) {
+        const int64_t dst_row = s.miss_loc[m];
+        const int64_t src_row = s.miss_host[m];
+        if (dst_row < 0 || src_row < 0) {
+            continue;  // uniform over the wave
+        }
+        for (int64_t first = 0; first < 2 * pieces; first += 4 * 64) {
+            V v[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int64_t p = first + k * 64 + lane;
+                const int64_t kv = p >= pieces ? 1 : 0;
+                const int64_t at = p < 2 * pieces ? p - kv * pieces : 0;
+                v[k] = *reinterpret_cast<const V*>(a.host_k + kv * a.host_kv + src_row * a.host_rs + at * kWidth);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int64_t p = first + k * 64 + lane;
+                if (p < 2 * pieces) {
+                    const int64_t kv = p >= pieces ? 1 : 0;
+                    *reinterpret_cast<V*>(a.dev_k + kv * a.dev_kv + dst_row * a.dev_rs + (p - kv * pieces) * kWidth) =
+                        v[k];
+                }
+            }
+        }
+    }
+}
+
+template <int kVecWidth>
+__global__ __launch_bounds__(kThreads) void hisparse_swap_kernel(const HsArgs a) {
+    extern __shared__ __align__(16) unsigned char shared[];
+    const int64_t b = blockIdx.x;
+    const int64_t H = a.H, W = a.width;
+    Lds s;
+    {
+        unsigned char* p = shared;
+        auto take = [&p](int64_t bytes) {
+            unsigned char* at = p;
+            p += (bytes + 15) & ~int64_t{15};
+            return at;
+        };
+        s.hash = reinterpret_cast<int32_t*>(take(a.HB * 4));
+        s.tok = reinterpret_cast<int32_t*>(take(H * 4));
+        s.first_touch = reinterpret_cast<int32_t*>(take(H * 4));
+        s.hit_rank = reinterpret_cast<int16_t*>(take(H * 2));
+        s.order = reinterpret_cast<int16_t*>(take(H * 2));
+        s.victim = reinterpret_cast<int16_t*>(take(W * 2));
+        s.miss_lane = reinterpret_cast<int16_t*>(take(W * 2));
+        s.lane_rank = reinterpret_cast<int16_t*>(take(W * 2));
+        s.lane_tok = reinterpret_cast<int32_t*>(take(W * 4));
+        s.lane_aux = reinterpret_cast<int32_t*>(take(W * 4));
+        s.lane_pos = reinterpret_cast<int32_t*>(take(W * 4));
+        s.miss_host = reinterpret_cast<int32_t*>(take(W * 4));
+        s.miss_loc = reinterpret_cast<int32_t*>(take(W * 4));
+        s.lane_kind = reinterpret_cast<uint8_t*>(take(W));
+        s.scratch = reinterpret_cast<int32_t*>(take((3 * kWaves + 4) * 4));
+    }
+    int32_t* out = a.out + b * a.out_sb;
+    const int64_t real = a.num_real.data != nullptr ? a.num_real[0] : a.batch;
+    const int64_t r = a.req[b];
+    const int64_t length = a.seq[b];
+    if (b >= real || r < 0 || r >= a.R || length <= 0) {
+        // Padding row (or a request outside the state): -1 only, state untouched.
+        for (int64_t o = threadIdx.x; o < W; o += kThreads) {
+            out[o * a.out_so] = -1;
+        }
+        return;  // uniform over the workgroup
+    }
+    int32_t* tokens = a.tokens + r * a.tok_sr;
+
+    // 1. Load the hot tokens and the LRU order; build the hash.
+    for (int64_t i = threadIdx.x; i < H; i += kThreads) {
+        s.tok[i] = tokens[i * a.tok_ss];
+        s.first_touch[i] = INT_MAX;
+        s.hit_rank[i] = -1;
+        const int64_t slot = a.lru32 ? static_cast<const int32_t*>(a.lru)[r * a.lru_sr + i * a.lru_ss]
+                                     : static_cast<const int16_t*>(a.lru)[r * a.lru_sr + i * a.lru_ss];
+        s.order[i] = static_cast<int16_t>(slot >= 0 && slot < H ? slot : -1);
+    }
+    for (int64_t j = threadIdx.x; j < a.HB; j += kThreads) {
+        s.hash[j] = kEmpty;
+    }
+    for (int64_t m = threadIdx.x; m < W; m += kThreads) {
+        s.victim[m] = -1;
+    }
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < H; i += kThreads) {
+        const int32_t t = s.tok[i];
+        if (t < 0) {
+            continue;
+        }
+        uint32_t h = bucket_of(a, t);
+        for (int64_t probe = 0; probe < a.HB; ++probe, h = (h + 1) & static_cast<uint32_t>(a.HB - 1)) {
+            int32_t v = load_entry(s, h);
+            if (v == kEmpty) {
+                v = atomicCAS(&s.hash[h], kEmpty, static_cast<int32_t>(i));
+                if (v == kEmpty) {
+                    break;
+                }
+            }
+            if (s.tok[v] == t) {
+                // The token is in two slots (a state the coordinator does not
+                // produce): the lowest slot is the one found.
+                atomicMin(&s.hash[h], static_cast<int32_t>(i));
+                break;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 2. Classify every lane; hits mark their slot, misses claim a bucket.
+    const void* topk_row = a.topk64 ? static_cast<const void*>(static_cast<const int64_t*>(a.topk) + b * a.topk_sb)
+                                    : static_cast<const void*>(static_cast<const int32_t*>(a.topk) + b * a.topk_sb);
+    for (int64_t o = threadIdx.x; o < W; o += kThreads) {
+        const uint32_t k = a.block_div.div(static_cast<uint32_t>(o));
+        const int64_t block = load_index(topk_row, a.topk64, k * a.topk_sk);
+        const int64_t t = block * a.block_size + (static_cast<uint32_t>(o) - k * a.block_size);
+        uint8_t kind = kInvalid;
+        int32_t aux = -1;
+        if (block >= 0 && t < length && t < a.T) {
+            if (t == length - 1) {
+                kind = kNewest;
+            } else {
+                s.lane_tok[o] = static_cast<int32_t>(t);
+                __threadfence_block();  // the token is visible before this lane's claim is
+                uint32_t h = bucket_of(a, static_cast<int32_t>(t));
+                for (int64_t probe = 0; probe < a.HB; ++probe, h = (h + 1) & static_cast<uint32_t>(a.HB - 1)) {
+                    int32_t v = load_entry(s, h);
+                    if (v == kEmpty) {
+                        v = atomicCAS(&s.hash[h], kEmpty, static_cast<int32_t>(H + o));
+                        if (v == kEmpty) {
+                            kind = kMiss;
+                            aux = static_cast<int32_t>(h);
+                            break;
+                        }
+                    }
+                    // v is set: a resident slot, or a miss claimed by some lane
+                    // (lane_tok of a claiming lane is written before its claim).
+                    if (v < H) {
+                        if (s.tok[v] == t) {
+                            kind = kHit;
+                            aux = v;
+                            atomicMin(&s.first_touch[v], static_cast<int32_t>(o));
+                            break;
+                        }
+                    } else if (s.lane_tok[v - H] == t) {
+                        kind = kMiss;
+                        aux = static_cast<int32_t>(h);
+                        atomicMin(&s.hash[h], static_cast<int32_t>(H + o));
+                        break;
+                    }
+                }
+            }
+        }
+        s.lane_kind[o] = kind;
+        s.lane_aux[o] = aux;
+    }
+    __syncthreads();
+
+    // 3. First lanes of each token, host rows, ranks in selection order;
+    //    outputs of the newest token and of hits.
+    const int64_t reserved = device_row(a, r, H);
+    int32_t base[3] = {0, 0, 0};  // selected, first hits, first misses so far
+    for (int64_t chunk = 0; chunk < W; chunk += kThreads) {
+        const int64_t o = chunk + threadIdx.x;
+        uint8_t kind = o < W ? s.lane_kind[o] : kInvalid;
+        const int32_t aux = o < W ? s.lane_aux[o] : -1;
+        int64_t host_row = -1;
+        if (kind == kMiss) {
+            host_row = load_index(a.host_locs, a.host_locs64, r * a.hl_sr + s.lane_tok[o] * a.hl_st);
+            if (host_row < 0 || host_row >= a.host_rows) {
+                kind = kInvalid;  // every lane of this token sees the same row
+                s.lane_kind[o] = kInvalid;
+            }
+        }
+        const bool first_hit = kind == kHit && s.first_touch[aux] == o;
+        const bool first_miss = kind == kMiss && s.hash[aux] == H + o;
+        const bool flags[3] = {kind != kInvalid, first_hit, first_miss};
+        int32_t rank[3], total[3];
+        rank_flags<3>(flags, rank, total, s.scratch);
+        if (o < W) {
+            const int32_t pos = base[0] + rank[0];
+            s.lane_pos[o] = kind != kInvalid ? pos : -1;
+            if (kind == kNewest) {
+                out[pos * a.out_so] = static_cast<int32_t>(reserved);
+            } else if (kind == kHit) {
+                out[pos * a.out_so] = static_cast<int32_t>(device_row(a, r, aux));
+            }
+            if (first_hit) {
+                s.hit_rank[aux] = static_cast<int16_t>(base[1] + rank[1]);
+            }
+            if (first_miss) {
+                const int32_t m = base[2] + rank[2];
+                s.lane_rank[o] = static_cast<int16_t>(m);
+                s.miss_lane[m] = static_cast<int16_t>(o);
+                s.miss_host[m] = static_cast<int32_t>(host_row);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            base[k] += total[k];
+        }
+    }
+    const int32_t selected = base[0], hits = base[1], misses = base[2];
+    __syncthreads();  // hit_rank and the miss lists were written after the last ranking barrier
+
+    // 4. New LRU order and victims, when the row touched the hot buffer.
+    if (hits + misses > 0) {
+        // Counts of empty and untouched slots in the old order.
+        int32_t counted[2] = {0, 0};
+        for (int64_t chunk = 0; chunk < H; chunk += kThreads) {
+            const int64_t i = chunk + threadIdx.x;
+            const int32_t slot = i < H ? s.order[i] : -1;
+            const bool listed = slot >= 0;
+            const bool touched = listed && s.hit_rank[slot] >= 0;
+            const bool flags[2] = {listed && !touched && s.tok[slot] < 0, listed && !touched && s.tok[slot] >= 0};
+            int32_t rank[2], total[2];
+            rank_flags<2>(flags, rank, total, s.scratch);
+            counted[0] += total[0];
+            counted[1] += total[1];
+        }
+        const int32_t empty = counted[0], untouched = counted[1];
+        const int32_t taken_empty = misses < empty ? misses : empty;
+        const int32_t taken_untouched = misses - taken_empty < untouched ? misses - taken_empty : untouched;
+        const int32_t kept_empty = empty - taken_empty, kept_untouched = untouched - taken_untouched;
+        const int32_t hit_base = kept_empty + kept_untouched, miss_base = hit_base + hits;
+        int32_t seen[2] = {0, 0};
+        for (int64_t chunk = 0; chunk < H; chunk += kThreads) {
+            const int64_t i = chunk + threadIdx.x;
+            const int32_t slot = i < H ? s.order[i] : -1;
+            const bool listed = slot >= 0;
+            const bool touched = listed && s.hit_rank[slot] >= 0;
+            const bool is_empty = listed && !touched && s.tok[slot] < 0;
+            const bool is_untouched = listed && !touched && s.tok[slot] >= 0;
+            const bool flags[2] = {is_empty, is_untouched};
+            int32_t rank[2], total[2];
+            rank_flags<2>(flags, rank, total, s.scratch);
+            int64_t pos = -1;
+            if (is_empty) {
+                const int32_t e = seen[0] + rank[0];
+                if (e < taken_empty) {
+                    s.victim[e] = static_cast<int16_t>(slot);
+                    pos = miss_base + e;
+                } else {
+                    pos = e - taken_empty;
+                }
+            } else if (is_untouched) {
+                const int32_t u = seen[1] + rank[1];
+                if (u < taken_untouched) {
+                    s.victim[taken_empty + u] = static_cast<int16_t>(slot);
+                    pos = miss_base + taken_empty + u;
+                } else {
+                    pos = kept_empty + (u - taken_untouched);
+                }
+            } else if (touched) {
+                pos = hit_base + s.hit_rank[slot];
+            }
+            if (pos >= 0 && pos < H) {
+                if (a.lru32) {
+                    static_cast<int32_t*>(a.lru)[r * a.lru_sr + pos * a.lru_ss] = slot;
+                } else {
+                    static_cast<int16_t*>(a.lru)[r * a.lru_sr + pos * a.lru_ss] = static_cast<int16_t>(slot);
+                }
+            }
+            seen[0] += total[0];
+            seen[1] += total[1];
+        }
+        __syncthreads();  // the victims were written after the last ranking barrier
+
+        // 5. Misses take their victims: token table, locations.
+        for (int64_t m = threadIdx.x; m < misses; m += kThreads) {
+            const int32_t slot = s.victim[m];
+            int32_t loc = -1;
+            if (slot >= 0) {
+                tokens[static_cast<int64_t>(slot) * a.tok_ss] = s.lane_tok[s.miss_lane[m]];
+                loc = static_cast<int32_t>(device_row(a, r, slot));
+            }
+            s.miss_loc[m] = loc;
+        }
+        __syncthreads();
+    }
+
+    // 6. Outputs of miss lanes (a repeated token reuses its first lane's
+    //    location) and the -1 tail.
+    for (int64_t o = threadIdx.x; o < W; o += kThreads) {
+        if (s.lane_kind[o] == kMiss) {
+            const int32_t owner = s.hash[s.lane_aux[o]] - static_cast<int32_t>(H);
+            out[s.lane_pos[o] * a.out_so] = s.miss_loc[s.lane_rank[owner]];
+        }
+    }
+    for (int64_t o = selected + threadIdx.x; o < W; o += kThreads) {
+        out[o * a.out_so] = -1;
+    }
+
+    // 7. Copy the misses' K and V rows from the host cache.
+    copy_rows<typename Vec<kVecWidth>::type>(a, s, misses);
+}
+
+size_t lds_bytes(int64_t H, int64_t HB, int64_t W) {
+    auto round = [](int64_t bytes) { return static_cast<size_t>((bytes + 15) & ~int64_t{15}); };
+    return round(HB * 4) + round(H * 4) * 2 + round(H * 2) * 2 + round(W * 2) * 3 + round(W * 4) * 5 + round(W) +
+           round((3 * kWaves + 4) * 4);
+}
+
+template <int kVecWidth>
+void launch(const HsArgs& a, size_t lds, hipStream_t stream) {
+    const auto kernel = hisparse_swap_kernel<kVecWidth>;
+    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(lds)),
+              "raise the swap-in LDS limit");
+    kernel<<<dim3(static_cast<uint32_t>(a.batch)), dim3(kThreads), lds, stream>>>(a);
+    check_hip(hipGetLastError(), "launch hisparse swap-in");
+}
+
+void need_index2(const ekv_tensor& t, const char* name) {
+    need_ndim(t, 2, name);
+    need_index(t, name);
+}
+
+void need_plane_pair(const ekv_planes* p, const char* name) {
+    if (p == nullptr || p->base == nullptr) {
+        throw std::invalid_argument(std::string(name) + " is required");
+    }
+    if (p->layers != 1 || p->kv != 2 || p->rows < 0 || p->row_bytes <= 0 || p->row_stride < p->row_bytes) {
+        throw std::invalid_argument(std::string(name) + " must be one layer of K and V planes of whole rows");
+    }
+    if (p->rows >= (int64_t{1} << 31)) {
+        throw std::invalid_argument(std::string(name) + " has more than 2^31 - 1 rows");
+    }
+}
+
+int hisparse_swap_in(const ekv_tensor* topk_p, const ekv_tensor* tokens_p, const ekv_tensor* host_locs_p,
+                     const ekv_tensor* dev_locs_p, const ekv_planes* host, const ekv_planes* dev,
+                     const ekv_tensor* out_p, const ekv_tensor* req_p, const ekv_tensor* seq_p,
+                     const ekv_tensor* lru_p, int64_t hot, int64_t block_size, const ekv_tensor* num_real_p,
+                     void* stream) {
+    const ekv_tensor& topk = need(topk_p, "top_k_blocks");
+    const ekv_tensor& tokens = need(tokens_p, "device_buffer_tokens");
+    const ekv_tensor& host_locs = need(host_locs_p, "host_cache_locs");
+    const ekv_tensor& dev_locs = need(dev_locs_p, "device_buffer_locs");
+    const ekv_tensor& out = need(out_p, "top_k_device_locs");
+    const ekv_tensor& req = need(req_p, "req_pool_indices");
+    const ekv_tensor& seq = need(seq_p, "seq_lens");
+    const ekv_tensor& lru = need(lru_p, "lru_slots");
+    need_plane_pair(host, "host cache");
+    need_plane_pair(dev, "device buffer");
+    if (host->row_bytes != dev->row_bytes) {
+        throw std::invalid_argument("host and device rows differ in size");
+    }
+    need_index2(topk, "top_k_blocks");
+    const int64_t B = topk.shape[0], K = topk.shape[1];
+    if (block_size < 1 || block_size > kMaxLanes) {
+        throw std::invalid_argument("sparse_block_size must be 1.." + std::to_string(kMaxLanes));
+    }
+    const int64_t W = K * block_size;
+    if (hot < 1 || hot > kMaxHot) {
+        throw std::invalid_argument("hot_buffer_size must be 1.." + std::to_string(kMaxHot));
+    }
+    if (W > kMaxLanes || W > hot) {
+        throw std::invalid_argument("Top-K blocks x block size must not exceed hot_buffer_size or " +
+                                    std::to_string(kMaxLanes));
+    }
+    need_ndim(out, 2, "top_k_device_locs");
+    if (out.dtype != EKV_INT32) {
+        throw std::invalid_argument("top_k_device_locs must be int32");
+    }
+    need_dim(out, 0, B, "top_k_device_locs");
+    need_dim(out, 1, W, "top_k_device_locs");
+    need_ndim(tokens, 2, "device_buffer_tokens");
+    if (tokens.dtype != EKV_INT32) {
+        throw std::invalid_argument("device_buffer_tokens must be int32");
+    }
+    const int64_t R = tokens.shape[0];
+    if (tokens.shape[1] < hot + 1) {
+        throw std::invalid_argument("device_buffer_tokens needs hot_buffer_size + 1 columns");
+    }
+    need_index2(dev_locs, "device_buffer_locs");
+    need_dim(dev_locs, 0, R, "device_buffer_locs");
+    if (dev_locs.shape[1] < hot + 1) {
+        throw std::invalid_argument("device_buffer_locs needs hot_buffer_size + 1 columns");
+    }
+    need_index2(host_locs, "host_cache_locs");
+    need_dim(host_locs, 0, R, "host_cache_locs");
+    const int64_t T = host_locs.shape[1];
+    if (T >= (int64_t{1} << 31)) {
+        throw std::invalid_argument("host_cache_locs has more than 2^31 - 1 tokens per request");
+    }
+    need_ndim(lru, 2, "lru_slots");
+    if (lru.dtype != EKV_INT16 && lru.dtype != EKV_INT32) {
+        throw std::invalid_argument("lru_slots must be int16 or int32");
+    }
+    need_dim(lru, 0, R, "lru_slots");
+    need_dim(lru, 1, hot, "lru_slots");
+    for (const auto* one : {&req, &seq}) {
+        need_ndim(*one, 1, "req_pool_indices/seq_lens");
+        need_index(*one, "req_pool_indices/seq_lens");
+        need_dim(*one, 0, B, "req_pool_indices/seq_lens");
+    }
+    IndexRef num_real;
+    if (num_real_p != nullptr) {
+        const ekv_tensor& n = need(num_real_p, "num_real_reqs");
+        need_index(n, "num_real_reqs");
+        if (numel(n) != 1 || n.data == nullptr) {
+            throw std::invalid_argument("num_real_reqs must hold one element");
+        }
+        num_real = index_ref(n, 0);
+    }
+    if (B == 0 || W == 0) {
+        return 0;
+    }
+    if (B > 0x7fffffff) {
+        throw std::invalid_argument("too many rows for one launch");
+    }
+    for (const auto* t : {&topk, &tokens, &host_locs, &dev_locs, &out, &req, &seq, &lru}) {
+        need_data(*t, "tensor");
+    }
+    HsArgs a{};
+    a.topk = topk.data;
+    a.topk64 = topk.dtype == EKV_INT64;
+    a.topk_sb = topk.stride[0], a.topk_sk = topk.stride[1];
+    a.tokens = static_cast<int32_t*>(tokens.data);
+    a.tok_sr = tokens.stride[0], a.tok_ss = tokens.stride[1];
+    a.host_locs = host_locs.data;
+    a.host_locs64 = host_locs.dtype == EKV_INT64;
+    a.hl_sr = host_locs.stride[0], a.hl_st = host_locs.stride[1];
+    a.dev_locs = dev_locs.data;
+    a.dev_locs64 = dev_locs.dtype == EKV_INT64;
+    a.dl_sr = dev_locs.stride[0], a.dl_ss = dev_locs.stride[1];
+    a.lru = lru.data;
+    a.lru32 = lru.dtype == EKV_INT32;
+    a.lru_sr = lru.stride[0], a.lru_ss = lru.stride[1];
+    a.out = static_cast<int32_t*>(out.data);
+    a.out_sb = out.stride[0], a.out_so = out.stride[1];
+    a.req = index_ref(req, 0);
+    a.seq = index_ref(seq, 0);
+    a.num_real = num_real;
+    a.host_k = static_cast<const char*>(host->base);
+    a.host_kv = host->kv_stride, a.host_rs = host->row_stride, a.host_rows = host->rows;
+    a.dev_k = static_cast<char*>(dev->base);
+    a.dev_kv = dev->kv_stride, a.dev_rs = dev->row_stride, a.dev_rows = dev->rows;
+    a.row_bytes = dev->row_bytes;
+    a.batch = B, a.R = R, a.T = T, a.H = hot;
+    a.HB = 1;
+    while (a.HB < 2 * hot) {
+        a.HB <<= 1;
+    }
+    int log2 = 0;
+    while ((int64_t{1} << log2) < a.HB) {
+        ++log2;
+    }
+    a.hb_shift = static_cast<uint32_t>(32 - log2);
+    if (log2 == 0) {
+        a.hb_shift = 31;  // HB = 1 cannot happen (hot >= 1 gives HB >= 2); kept well defined
+    }
+    a.width = static_cast<uint32_t>(W);
+    a.block_size = static_cast<uint32_t>(block_size);
+    a.block_div = FastDiv(static_cast<uint32_t>(block_size));
+    const size_t lds = lds_bytes(hot, a.HB, W);
+    // Widest copy unit dividing the row size, the row strides, the plane
+    // offsets and both base addresses.
+    const int vw = pick_vector_width({a.row_bytes, a.host_rs, a.dev_rs, a.host_kv, a.dev_kv,
+                                      static_cast<int64_t>(reinterpret_cast<uintptr_t>(a.host_k)),
+                                      static_cast<int64_t>(reinterpret_cast<uintptr_t>(a.dev_k))});
+    const auto st = static_cast<hipStream_t>(stream);
+    switch (vw) {
+        case 16: launch<16>(a, lds, st); break;
+        case 8: launch<8>(a, lds, st); break;
+        case 4: launch<4>(a, lds, st); break;
+        case 2: launch<2>(a, lds, st); break;
+        default: launch<1>(a, lds, st); break;
+    }
+    return 0;
+}
+
+}  // namespace
+}  // namespace ekv
+
+extern "C" int ekv_hisparse_swap_in(const ekv_tensor* top_k_blocks, const ekv_tensor* device_buffer_tokens,
+                                    const ekv_tensor* host_cache_locs, const ekv_tensor* device_buffer_locs,
+                                    const ekv_planes* host_cache, const ekv_planes* device_buffer,
+                                    const ekv_tensor* top_k_device_locs, const ekv_tensor* req_pool_indices,
+                                    const ekv_tensor* seq_lens, const ekv_tensor* lru_slots,
+                                    int64_t hot_buffer_size, int64_t sparse_block_size,
+                                    const ekv_tensor* num_real_reqs, void* stream) {
+    return ekv::guarded(-1, [&] {
+        return ekv::hisparse_swap_in(top_k_blocks, device_buffer_tokens, host_cache_locs, device_buffer_locs,
+                                     host_cache, device_buffer, top_k_device_locs, req_pool_indices, seq_lens,
+                                     lru_slots, hot_buffer_size, sparse_block_size, num_real_reqs, stream);
+    });
+}
+
+extern "C" int ekv_host_device_pointer(void* host, void** device) {
+    return ekv::guarded(-1, [&] {
+        if (host == nullptr || device == nullptr) {
+            throw std::invalid_argument("host and device pointers are required");
+        }
+        ekv::check_hip(hipHostGetDevicePointer(device, host, 0),
+                       "hipHostGetDevicePointer (the memory must be pinned host memory)");
+        return 0;
+    });
+}

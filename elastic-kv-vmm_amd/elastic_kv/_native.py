@@ -75,6 +75,9 @@ _SIGNATURES = {
                      ct.c_void_p], ct.c_int),
     "ekv_compare_kv": ([ct.POINTER(EkvPlanes), _P_TENSOR, ct.POINTER(EkvPlanes), _P_TENSOR, _P_TENSOR,
                         ct.c_void_p], ct.c_int),
+    "ekv_hisparse_swap_in": ([_P_TENSOR] * 4 + [ct.POINTER(EkvPlanes)] * 2 + [_P_TENSOR] * 4
+                             + [ct.c_int64, ct.c_int64, _P_TENSOR, ct.c_void_p], ct.c_int),
+    "ekv_host_device_pointer": ([ct.c_void_p, ct.POINTER(ct.c_void_p)], ct.c_int),
     "ekv_host_alloc": ([ct.c_uint64, ct.POINTER(ct.c_void_p), ct.POINTER(ct.c_void_p)], ct.c_int),
     "ekv_host_free": ([ct.c_void_p], ct.c_int),
 }

@@ -217,6 +217,53 @@ int ekv_swap_in_counted(const ekv_tensor* topk, int64_t block_size, const ekv_te
                         const ekv_tensor* step_counter, void* stream);
 
 /*
+ * HiSparse hot-buffer swap-in with the calling convention of SGLang's
+ * load_blocks_to_device_buffer_mha, which the reference's decode path calls
+ * through its coordinator (adaptive_sparse/request_residency.py:805-809,
+ * 829-832) and checks directly in tests/smoke_minimax_swap.py:38-67. For
+ * batch row b < num_real_reqs[0] (NULL: every row), r = req_pool_indices[b],
+ * s = seq_lens[b], H = hot_buffer_size:
+ *   selected tokens: top_k_blocks[b, k] >= 0 expanded to block * bs + j
+ *     (j < bs = sparse_block_size), kept when < s and < T, in Top-K order
+ *     (adaptive_sparse/hisparse_access_trace.py:59-64);
+ *   the newest token s - 1 -> device_buffer_locs[r, H] (reserved; not copied);
+ *   a token held by slot i < H (device_buffer_tokens[r, i]) hits ->
+ *     device_buffer_locs[r, i];
+ *   misses take victims in batch-token LRU order (empty slots first, then
+ *     the least recent in lru_slots[r]; benchmarks/hisparse_locality_replay.py
+ *     :90-99), get their K and V rows copied from host row
+ *     host_cache_locs[r, t] of `host_cache`, and enter device_buffer_tokens;
+ *     lru_slots[r] becomes: unused empty slots, untouched slots (old order),
+ *     hits, misses (selection order);
+ *   top_k_device_locs[b] = device locations in selection order, then -1.
+ * A token repeated in a row is classified by its first lane and shares its
+ * location. Rows past num_real_reqs, with s <= 0 or with r outside the state
+ * get -1 only and change nothing; misses whose host row lies outside the host
+ * cache are left out; locations outside `device_buffer` are reported as -1.
+ *   top_k_blocks [B, K] int32/int64; device_buffer_tokens [R, >= H+1] int32;
+ *   host_cache_locs [R, T] and device_buffer_locs [R, >= H+1] int32/int64;
+ *   lru_slots [R, H] int16/int32 (a permutation of 0..H-1);
+ *   top_k_device_locs [B, K*bs] int32; req_pool_indices, seq_lens [B].
+ *   host_cache / device_buffer: one layer of K and V planes (kv = 2), rows of
+ *   item_size_bytes; host_cache addresses device-mapped pinned memory
+ *   (ekv_host_device_pointer).
+ * H <= 4096, K * bs <= min(H, 2048); the batch rows must name distinct
+ * requests (one workgroup updates each request's state).
+ */
+int ekv_hisparse_swap_in(const ekv_tensor* top_k_blocks, const ekv_tensor* device_buffer_tokens,
+                         const ekv_tensor* host_cache_locs, const ekv_tensor* device_buffer_locs,
+                         const ekv_planes* host_cache, const ekv_planes* device_buffer,
+                         const ekv_tensor* top_k_device_locs, const ekv_tensor* req_pool_indices,
+                         const ekv_tensor* seq_lens, const ekv_tensor* lru_slots,
+                         int64_t hot_buffer_size, int64_t sparse_block_size,
+                         const ekv_tensor* num_real_reqs, void* stream);
+
+/* Device address of pinned host memory (hipHostGetDevicePointer), for host
+ * tensors pinned by their owner (e.g. torch's pin_memory). No reference
+ * counterpart. */
+int ekv_host_device_pointer(void* host, void** device);
+
+/*
  * Row moves between two plane sets: for i < counts[l, b] and both kv planes,
  *   dst(l, kv)[dst_rows[l, b, i]] = src(l, kv)[src_rows[l, b, i]]
  * when 0 <= src row < src->rows and zero_below <= dst row < dst->rows (other

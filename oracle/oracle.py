@@ -186,6 +186,100 @@ def swap_in(step, block_size, topk, rows, selected, slots, misses, counts, table
             "promote_src": src, "promote_dst": dst}
 
 
+def hisparse_swap(top_k_blocks, tokens, host_locs, dev_locs, host_k, host_v, dev_k, dev_v, req, seq, lru, hot,
+                  block_size, num_real=None):
+    """HiSparse swap-in with SGLang's calling convention, token by token (copies are returned).
+
+    The swap the reference's decode path makes through
+    load_blocks_to_device_buffer_mha (adaptive_sparse/request_residency.py
+    :805-809; checked in tests/smoke_minimax_swap.py:18-67). Per real batch
+    row b with request r and length s > 0:
+    - selected tokens: every non-negative Top-K block expanded, tokens below
+      s and below T = host_locs width, in Top-K order
+      (adaptive_sparse/hisparse_access_trace.py:59-64);
+    - the newest token s - 1 takes the reserved slot `hot`;
+    - another token is a hit when a hot slot holds it (the lowest such slot);
+    - the other tokens are misses, taken once each in order of first
+      appearance; those whose host row lies outside host_k are dropped;
+    - batch-token LRU (benchmarks/hisparse_locality_replay.py:90-99): the
+      misses take the empty slots, then the untouched occupied slots, in
+      lru order; the new order is the unused empty slots, the untouched
+      survivors, the hit slots in order of first hit, the misses' slots;
+    - each miss's K and V rows are copied from its host row to its slot's
+      device row; device rows outside dev_k are reported as -1, never written.
+    Returns (out [B, K*bs] int32, tokens, lru, dev_k, dev_v).
+    """
+    top_k_blocks = np.asarray(top_k_blocks, dtype=np.int64)
+    tokens = np.array(tokens, dtype=np.int64, copy=True)
+    lru = np.array(lru, dtype=np.int64, copy=True)
+    dev_k = np.array(dev_k, copy=True)
+    dev_v = np.array(dev_v, copy=True)
+    host_locs = np.asarray(host_locs, dtype=np.int64)
+    dev_locs = np.asarray(dev_locs, dtype=np.int64)
+    B, K = top_k_blocks.shape
+    W = K * block_size
+    R, T = host_locs.shape
+    out = np.full((B, W), -1, dtype=np.int32)
+    real = B if num_real is None else int(num_real)
+    for b in range(B):
+        r, s = int(req[b]), int(seq[b])
+        if b >= real or not 0 <= r < R or s <= 0:
+            continue
+
+        def location(slot):
+            row = int(dev_locs[r, slot])
+            return row if 0 <= row < dev_k.shape[0] else -1
+
+        selected = [int(block) * block_size + j for block in top_k_blocks[b] if block >= 0
+                    for j in range(block_size) if int(block) * block_size + j < min(s, T)]
+        resident = {}
+        for slot in range(hot):
+            if tokens[r, slot] >= 0:
+                resident.setdefault(int(tokens[r, slot]), slot)
+        hit_slots, missed, dropped, seen = [], [], set(), set()
+        for token in selected:
+            if token == s - 1 or token in seen:
+                continue
+            seen.add(token)
+            if token in resident:
+                hit_slots.append(resident[token])
+            elif 0 <= host_locs[r, token] < host_k.shape[0]:
+                missed.append(token)
+            else:
+                dropped.add(token)
+        slot_of = {}
+        if hit_slots or missed:
+            touched = set(hit_slots)
+            listed = [int(x) for x in lru[r] if 0 <= x < hot]
+            empty = [x for x in listed if x not in touched and tokens[r, x] < 0]
+            untouched = [x for x in listed if x not in touched and tokens[r, x] >= 0]
+            taken_empty = min(len(missed), len(empty))
+            taken_untouched = min(len(missed) - taken_empty, len(untouched))
+            victims = empty[:taken_empty] + untouched[:taken_untouched]
+            order = empty[taken_empty:] + untouched[taken_untouched:] + hit_slots + victims
+            for position, slot in enumerate(order[:hot]):
+                lru[r, position] = slot
+            for token, slot in zip(missed, victims):
+                tokens[r, slot] = token
+                slot_of[token] = slot
+                row = location(slot)
+                if row >= 0:
+                    dev_k[row] = host_k[host_locs[r, token]]
+                    dev_v[row] = host_v[host_locs[r, token]]
+        position = 0
+        for token in selected:
+            if token in dropped:
+                continue
+            if token == s - 1:
+                out[b, position] = location(hot)
+            elif token in resident:
+                out[b, position] = location(resident[token])
+            else:
+                out[b, position] = location(slot_of[token]) if token in slot_of else -1
+            position += 1
+    return out, tokens.astype(np.int32), lru, dev_k, dev_v
+
+
 # ---------------------------------------------------------------- gathers (numpy)
 
 def gather_rows(raw, positions, request_ids, lengths, request_table, slot_offsets, width,

@@ -114,6 +114,28 @@ def test_kernel_entry_points_validate_before_launch(lib):
     assert typed.ekv_gather_kv(ct.byref(planes), ct.byref(slots), ct.byref(rows_out), 1, None) == -1
     assert b"kv 1 or 2" in typed.ev_error()
 
+    # HiSparse swap-in: 2 rows x 2 blocks of 4 tokens against an 8-slot hot buffer.
+    pair = _native.EkvPlanes(4096, 1, 2, 0, 1 << 20, 256, 256, 64)
+    blocks = tensor((2, 2), 1)
+    state = dict(tokens=tensor((3, 9), 1), host_locs=tensor((3, 100), 2), dev_locs=tensor((3, 9), 1),
+                 out=tensor((2, 8), 1), req=tensor((2,), 2), seq=tensor((2,), 1), lru=tensor((3, 8), 5))
+
+    def swap(hot=8, bs=4, planes=pair, **changes):
+        args = {**state, **changes}
+        return typed.ekv_hisparse_swap_in(
+            ct.byref(blocks), ct.byref(args["tokens"]), ct.byref(args["host_locs"]), ct.byref(args["dev_locs"]),
+            ct.byref(planes), ct.byref(pair), ct.byref(args["out"]), ct.byref(args["req"]), ct.byref(args["seq"]),
+            ct.byref(args["lru"]), hot, bs, None, None)
+
+    assert swap(out=tensor((2, 7), 1)) == -1 and b"top_k_device_locs dimension 1 is 7" in typed.ev_error()
+    assert swap(hot=7, lru=tensor((3, 7), 5)) == -1 and b"must not exceed hot_buffer_size" in typed.ev_error()
+    assert swap(tokens=tensor((3, 8), 1)) == -1 and b"hot_buffer_size + 1 columns" in typed.ev_error()
+    assert swap(lru=tensor((3, 8), 2)) == -1 and b"lru_slots must be int16 or int32" in typed.ev_error()
+    assert swap(hot=5000) == -1 and b"hot_buffer_size must be 1..4096" in typed.ev_error()
+    one_plane = _native.EkvPlanes(4096, 1, 1, 0, 0, 256, 256, 64)
+    assert swap(planes=one_plane) == -1 and b"one layer of K and V planes" in typed.ev_error()
+    assert typed.ekv_host_device_pointer(None, ct.byref(ct.c_void_p())) == -1
+
 
 FASTDIV_TEST = r"""
 #include "ekv_fastdiv.h"

@@ -450,3 +450,152 @@ def test_move_kv_hand_case_and_gather_identity():
     moved_src = np.array([[[1]], [[0]]]); moved_dst = np.array([[[2]], [[5]]])
     assert np.array_equal(ref.gather_kv(out, *dst_layout[:4], 6, moved_dst, kv),
                           ref.gather_kv(src, *src_layout[:4], 5, moved_src, kv, zero_below=0))
+
+
+# ------------------------------------------------------------------ HiSparse swap (SGLang convention)
+
+def bf16_rows(values):
+    """bfloat16 bytes of float32 values that bfloat16 holds exactly."""
+    bits = np.asarray(values, dtype=np.float32).view(np.uint32) >> 16
+    return bits.astype(np.uint16).view(np.uint8).reshape(*np.shape(values)[:-1], -1)
+
+
+def smoke_swap_scenario(swap, layer):
+    """tests/smoke_minimax_swap.py:18-62 for one layer; `swap` runs one call.
+
+    Returns (selected device rows per newest token, host K/V rows, device
+    K/V rows after the last call) and asserts the reference's checks.
+    """
+    block, hot, width = 128, 256, 128
+    t = np.arange(3 * block)[:, None] % 43
+    d = np.arange(width)[None, :] % 13
+    host = [bf16_rows(t + d + layer * 64 + plane * 128) for plane in range(2)]     # [384, 256 B]
+    device = [np.zeros((hot + 2, width * 2), np.uint8) for _ in range(2)]
+    locs = np.arange(1, hot + 2).reshape(1, -1)
+    tokens = np.full((1, hot + 1), -1)
+    tokens[0, :block] = np.arange(block, 2 * block)
+    for dst, src in zip(device, host):
+        dst[1:block + 1] = src[block:2 * block]
+    lru = np.arange(hot).reshape(1, -1)
+    results = []
+    for newest in range(2 * block, 2 * block + 3):
+        for dst, src in zip(device, host):
+            if newest > 2 * block:
+                src[newest - 1] = dst[hot + 1]          # back up the previous newest token
+            dst[hot + 1] = src[newest]
+        out, tokens, lru, device[0], device[1] = swap(
+            np.array([[0, 2]]), tokens, np.arange(3 * block).reshape(1, -1), locs, host[0], host[1],
+            device[0], device[1], [0], [newest + 1], lru, hot, block, 1)
+        valid = block + newest - 2 * block + 1
+        selected = out[0, :valid]
+        assert (selected > 0).all()
+        assert selected[-1] == hot + 1
+        assert (out[0, valid:] == -1).all()
+        for dst, src in zip(device, host):
+            expected = np.concatenate((src[:block], src[2 * block:newest + 1]))
+            assert np.array_equal(dst[selected], expected), (layer, newest)
+        results.append(selected.tolist())
+    return results
+
+
+def test_hisparse_swap_reproduces_reference_smoke_scenario():
+    """The reference's swap smoke test (valid locations > 0, newest token in the reserved slot,
+    -1 tail, every selected device row equal to its host row) holds for the oracle."""
+    first = smoke_swap_scenario(ref.hisparse_swap, 0)
+    second = smoke_swap_scenario(ref.hisparse_swap, 1)
+    assert first == second                               # locations do not depend on the payload
+    assert first[0][:3] == [129, 130, 131]               # block 0 fills the empty slots 128.. in order
+
+
+def _swap_state(rng, hot, context, resident_count):
+    tokens = np.full((1, hot + 1), -1)
+    resident = rng.choice(context, size=resident_count, replace=False)
+    slots = rng.choice(hot, size=resident_count, replace=False)
+    tokens[0, slots] = resident
+    lru = rng.permutation(hot).reshape(1, -1)
+    return tokens, lru
+
+
+def test_hisparse_swap_hits_follow_reference_access_model():
+    """Hits are selected ∩ (prestate ∪ {newest}) (adaptive_sparse/hisparse_access_trace.py:59-71),
+    and a short request whose tokens are all resident hits everywhere."""
+    rng = np.random.default_rng(41)
+    row_bytes = 8
+    for case in range(60):
+        hot, bs, k = int(rng.integers(4, 40)), int(rng.choice([1, 2, 4])), int(rng.integers(1, 6))
+        k = min(k, hot // bs)
+        short = case % 4 == 0
+        context = int(rng.integers(2, hot + 1)) if short else int(rng.integers(hot + 1, 4 * hot))
+        seq = context
+        if short:
+            tokens = np.full((1, hot + 1), -1)
+            tokens[0, :seq - 1] = np.arange(seq - 1)       # every token before the newest is resident
+            lru = rng.permutation(hot).reshape(1, -1)
+        else:
+            tokens, lru = _swap_state(rng, hot, seq, int(rng.integers(0, hot + 1)))
+        k = min(k, -(-seq // bs) + 1)
+        blocks = rng.choice(-(-seq // bs) + 1, size=k, replace=False) - 1      # distinct, -1 = padding
+        locs = rng.permutation(hot + 1).reshape(1, -1) + 3
+        host = rng.integers(0, 256, (seq, row_bytes), dtype=np.uint8)
+        device = np.zeros((hot + 4, row_bytes), np.uint8)
+        out, *_ = ref.hisparse_swap(blocks[None], tokens, np.arange(seq)[None], locs, host, host, device,
+                                    device, [0], [seq], lru, hot, bs)
+        selected, hits = ref.access_tokens(blocks.tolist(), bs, seq, hot, tokens[0, :hot][tokens[0, :hot] >= 0])
+        slot_of = {int(tok): slot for slot, tok in enumerate(tokens[0, :hot]) if tok >= 0}
+        got = {tok for tok, loc in zip(selected, out[0])
+               if (tok == seq - 1 and loc == locs[0, hot]) or (tok in slot_of and loc == locs[0, slot_of[tok]])}
+        assert sorted(got) == hits, case
+        assert (out[0, :len(selected)] >= 3).all() and (out[0, len(selected):] == -1).all()
+
+
+def test_hisparse_swap_lru_matches_reference_replay():
+    """Resident tokens in LRU order and miss counts follow benchmarks/hisparse_locality_replay.py:90-99
+    step by step (distinct selections, newest token never selected)."""
+    rng = np.random.default_rng(43)
+    for hot, context, k in ((8, 60, 6), (16, 200, 16), (5, 30, 5), (32, 500, 20)):
+        tokens = np.full((1, hot + 1), -1)
+        lru = rng.permutation(hot).reshape(1, -1)
+        locs = np.arange(hot + 1).reshape(1, -1)
+        host = np.zeros((context + 1, 4), np.uint8)
+        device = np.zeros((hot + 1, 4), np.uint8)
+        cache = ref.OrderedDict()
+        for _ in range(30):
+            chosen = rng.choice(context, size=int(rng.integers(1, k + 1)), replace=False)
+            out, tokens, lru, *_ = ref.hisparse_swap(chosen[None], tokens, np.arange(context + 1)[None], locs,
+                                                     host, host, device, device, [0], [context + 1], lru, hot, 1)
+            missing = [t for t in chosen.tolist() if t not in cache]
+            for t in chosen.tolist():
+                if t in cache:
+                    cache.move_to_end(t)
+            while len(cache) + len(missing) > hot:
+                cache.popitem(last=False)
+            cache.update((t, None) for t in missing)
+            resident = [int(tokens[0, slot]) for slot in lru[0] if tokens[0, slot] >= 0]
+            assert resident == list(cache)
+            assert sorted(lru[0].tolist()) == list(range(hot))
+
+
+def test_hisparse_swap_repeated_blocks_padding_and_bounds():
+    hot, bs, row = 6, 2, 4
+    host = np.arange(20 * row, dtype=np.uint8).reshape(20, row)
+    device = np.zeros((8, row), np.uint8)
+    tokens = np.full((3, hot + 1), -1)
+    tokens[0, 2] = 5                                       # request 0 holds token 5 in slot 2
+    lru = np.tile(np.arange(hot), (3, 1))
+    locs = np.tile(np.array([1, 2, 3, 4, 5, 6, 7]), (3, 1))
+    locs[0, 1] = 99                                        # slot 1's device row lies outside the buffer
+    host_locs = np.tile(np.arange(20), (3, 1))
+    host_locs[0, 8] = 50                                   # token 8 has no host row
+    blocks = np.array([[2, 0, 2, 4], [1, -1, -1, -1], [0, 1, -1, -1]])
+    out, tokens2, lru2, dk, _ = ref.hisparse_swap(blocks, tokens, host_locs, locs, host, host, device, device,
+                                                  [0, 1, 2], [10, 0, 4], lru, hot, bs, num_real=2)
+    # row 0: tokens 4 5 | 0 1 | 4 5 | 8 9; 9 is the newest (reserved row 7); 5 hits slot 2 (row 3);
+    # 4, 0, 1 miss into empty slots 0, 1, 3 (rows 1, 99 -> -1, 4); the repeated block reuses them;
+    # token 8 is dropped (no host row).
+    assert out[0].tolist() == [1, 3, -1, 4, 1, 3, 7, -1]
+    assert tokens2[0, :hot].tolist() == [4, 0, 5, 1, -1, -1]
+    assert lru2[0].tolist() == [4, 5, 2, 0, 1, 3]
+    assert np.array_equal(dk[1], host[4]) and np.array_equal(dk[4], host[1]) and not dk[[2, 3, 5, 6, 7]].any()
+    # row 1 has length 0 and row 2 is past num_real: -1 only, state unchanged.
+    assert (out[1:] == -1).all()
+    assert np.array_equal(tokens2[1:], tokens[1:]) and np.array_equal(lru2[1:], lru[1:])
