@@ -26,6 +26,10 @@ Other workloads (same JSON contract, for the other configurations):
                 5 % of pool chunks are unmapped and remapped (their hot slots
                 invalidated), then lookup + compaction, LRU swap-in, promote
                 of misses from pinned host, gather
+  hisparse-swap SGLang-convention swap-in (load_blocks_to_device_buffer_mha)
+                of one layer: 128 requests x 65,536-token context, 4096 hot
+                slots each, 16 Top-K blocks of 128 tokens (newest block, 12
+                recent, 3 older), 512 B K and V rows promoted from pinned host
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -60,7 +64,8 @@ def parse_args():
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--workload", default="decode-read",
-                        choices=["decode-read", "topk-gather", "block-gather", "migration", "composite"])
+                        choices=["decode-read", "topk-gather", "block-gather", "migration", "composite",
+                                 "hisparse-swap"])
     parser.add_argument("--remap-fraction", type=float, default=0.05,
                         help="share of pool chunks unmapped and remapped per composite step")
     parser.add_argument("--capacity", type=int, default=4096, help="hot slots per request (decode-read)")
@@ -665,6 +670,130 @@ def run_migration(torch, args, device):
     return result
 
 
+# ------------------------------------------------------------------ hisparse-swap (SGLang convention)
+
+
+def run_hisparse_swap(torch, args, device):
+    import numpy as np
+
+    from adaptive_sparse.hisparse_swap import load_blocks_to_device_buffer_mha
+
+    R, T, H, K, BS = 128, 65536, 4096, 16, 128
+    ROW = 2 * 128 * 2                        # 2 KV heads x head_dim 128, bf16
+    HOST_ROWS = 1 << 21                      # 1 GiB per plane of pinned host rows
+    W = K * BS
+    total = args.warmup + args.steps
+    rng = np.random.default_rng(args.seed)
+    # Step i: length T - total + i + 1; 13 of the 32 blocks holding the last 4096 tokens (the newest
+    # block included) and 3 older blocks - the 80 % / 20 % locality mix in 128-token blocks.
+    blocks = np.empty((total, R, K), np.int32)
+    lengths = T - total + np.arange(total) + 1
+    for step, length in enumerate(lengths):
+        last = (int(length) - 1) // BS
+        recent = last - np.argsort(rng.random((R, 31)), axis=1)[:, :12] - 1
+        older = np.argsort(rng.random((R, last - 31)), axis=1)[:, :3]
+        picked = np.concatenate([np.full((R, 1), last), recent, older], axis=1)
+        blocks[step] = np.take_along_axis(picked, np.argsort(rng.random((R, K)), axis=1), axis=1)
+    host_locs = (np.arange(T)[None, :] + np.arange(R)[:, None] * 7919) % HOST_ROWS
+    dev_locs = np.arange(R * (H + 1), dtype=np.int64).reshape(R, H + 1) + 1
+    host = torch.empty((2, HOST_ROWS, ROW), dtype=torch.uint8).pin_memory()
+    host.copy_(torch.randint(0, 256, host.shape, dtype=torch.uint8, device=device))
+    device_k = torch.zeros((R * (H + 1) + 1, ROW), dtype=torch.uint8, device=device)
+    device_v = torch.zeros_like(device_k)
+    tokens = torch.full((R, H + 1), -1, dtype=torch.int32, device=device)
+    lru = torch.arange(H, dtype=torch.int16, device=device).repeat(R, 1)
+    blocks_d = torch.tensor(blocks, device=device)
+    seq_d = torch.tensor(np.repeat(lengths[:, None], R, axis=1), dtype=torch.int32, device=device)
+    host_locs_d = torch.tensor(host_locs, device=device)
+    dev_locs_d = torch.tensor(dev_locs, dtype=torch.int32, device=device)
+    req = torch.arange(R, device=device)
+    out = torch.empty((R, W), dtype=torch.int32, device=device)
+
+    def call(step, state):
+        load_blocks_to_device_buffer_mha(
+            top_k_blocks=blocks_d[step], device_buffer_tokens=state[0], host_cache_locs=host_locs_d,
+            device_buffer_locs=dev_locs_d, host_cache_k=host[0], host_cache_v=host[1], device_buffer_k=state[2],
+            device_buffer_v=state[3], top_k_device_locs=out, req_pool_indices=req, seq_lens=seq_d[step],
+            lru_slots=state[1], item_size_bytes=ROW, hot_buffer_size=H, sparse_block_size=BS)
+
+    live = (tokens, lru, device_k, device_v)
+    for step in range(args.warmup):
+        call(step, live)
+    torch.cuda.synchronize()
+    saved = tuple(t.clone() for t in live)
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    marks[0].record()
+    for i in range(args.steps):
+        call(args.warmup + i, live)
+        marks[i + 1].record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - wall0) * 1e3 / args.steps
+    call_ms = [marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps)]
+    # Replay the timed steps from the saved state: misses per call from the slots that took new tokens,
+    # and the first timed call's results for the parity check.
+    replay = tuple(t.clone() for t in saved)
+    misses, first = [], None
+    for i in range(args.steps):
+        before = replay[0].clone()
+        call(args.warmup + i, replay)
+        misses.append(int((replay[0] != before).sum().item()))
+        if i == 0:
+            first = (out.cpu().numpy(), replay[0].cpu().numpy(), replay[1].cpu().numpy())
+    promoted = [m * 2 * ROW for m in misses]
+    mean_ms = statistics.mean(call_ms)
+    achieved = statistics.mean(promoted) / (mean_ms / 1e3) / 1e9
+    length = int(lengths[args.warmup])
+    looked_up = R * ((K - 1) * BS + (length - (length - 1) // BS * BS) - 1)   # selected tokens but the newest
+    hit_rate = 1 - statistics.mean(misses) / looked_up
+    log(f"swap-in call {mean_ms:.3f} ms, {statistics.mean(misses):.0f} misses per call (hit rate {hit_rate:.3f}), "
+        f"{achieved:.1f} GB/s promoted over PCIe")
+    baseline = None
+    parity = None
+    if not args.no_cpu_baseline:
+        from oracle import oracle as ref
+
+        host_np = host.numpy()
+        s_tokens, s_lru = saved[0].cpu().numpy(), saved[1].cpu().numpy()
+        s_k, s_v = saved[2].cpu().numpy(), saved[3].cpu().numpy()
+        step = args.warmup
+
+        def sample():
+            return ref.hisparse_swap(blocks[step], s_tokens, host_locs, dev_locs, host_np[0], host_np[1], s_k, s_v,
+                                     np.arange(R), np.full(R, lengths[step]), s_lru, H, BS)
+
+        want = sample()
+        rows = want[0][want[0] >= 0]
+        parity = {"locations": bool(np.array_equal(first[0], want[0])),
+                  "hot_state": bool(np.array_equal(first[1], want[1]) and np.array_equal(first[2], want[2]))}
+        # Rows of the first call, read back from a replay of that call alone.
+        check = tuple(t.clone() for t in saved)
+        call(step, check)
+        rows_t = torch.tensor(rows, device=device)
+        parity["rows"] = bool(np.array_equal(check[2][rows_t].cpu().numpy(), want[3][rows])
+                              and np.array_equal(check[3][rows_t].cpu().numpy(), want[4][rows]))
+        del check, want
+        median, runs = time_cpu(sample, args.cpu_seconds)
+        baseline = {"value": round(promoted[0] / median / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+                    "sample": (f"the first timed call ({R} requests, {misses[0]} misses): the Python oracle on one "
+                               f"thread, median of {runs} runs ({median * 1e3:.0f} ms), {cpu_model()}"),
+                    "parity": parity}
+        log(f"cpu baseline {baseline['value']} GB/s, parity {parity}")
+    config = {"workload": "hisparse-swap-sglang-convention", "requests": R, "context": T, "hot_buffer_size": H,
+              "topk_blocks": K, "block_tokens": BS, "row_bytes": ROW, "host_rows": HOST_ROWS,
+              "selection": "newest block + 12 of the other 31 recent blocks + 3 older blocks per call"}
+    roof = {"bound": "pcie", "achieved": round(achieved, 2), "peak": PCIE_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / PCIE_PEAK_GBS, 4), "traffic": None,
+            "kernel": "hisparse_swap_kernel<16> (ekv_hisparse_swap_in)",
+            "algorithmic_bytes_per_launch": round(statistics.mean(promoted)), "avg_launch_ms": round(mean_ms, 4)}
+    extra = {"call_ms": spread(call_ms), "misses_per_call": round(statistics.mean(misses), 1),
+             "hit_rate": round(hit_rate, 4), "tokens_per_s": round(R * W / (mean_ms / 1e3), 1)}
+    result = envelope(args, achieved, wall_ms, config, roof, baseline, extra,
+                      metric="HiSparse swap-in promoted GB/s (host rows copied per call / call time), 1 GPU")
+    return result
+
+
 # ------------------------------------------------------------------ composite (config 5)
 
 
@@ -880,7 +1009,8 @@ def run_composite(torch, args, device):
 
 
 WORKLOADS = {"decode-read": run_decode_read, "topk-gather": run_topk_gather,
-             "block-gather": run_block_gather, "migration": run_migration, "composite": run_composite}
+             "block-gather": run_block_gather, "migration": run_migration, "composite": run_composite,
+             "hisparse-swap": run_hisparse_swap}
 
 
 def main():

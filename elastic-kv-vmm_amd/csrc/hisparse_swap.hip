@@ -88,6 +88,7 @@ struct HsArgs {
     uint32_t width;                    // W = K * block size
     uint32_t block_size;
     FastDiv block_div;
+    FastDiv row_div;                   // pieces of one miss (K and V) in copy units
 };
 
 struct Lds {
@@ -166,35 +167,35 @@ __device__ __forceinline__ int64_t device_row(const HsArgs& a, int64_t r, int64_
 
 template <typename V>
 __device__ __forceinline__ void copy_rows(const HsArgs& a, const Lds& s, int32_t misses) {
-    // Wave w copies misses w, w + 4, ...: both planes of one row per pass,
-    // all of the pass's loads issued before its stores.
+    // The pieces of all misses (both planes) are dealt to the workgroup's
+    // threads in order; each thread issues 4 loads over the host link before
+    // its 4 stores, so 4 x 256 pieces are in flight per workgroup.
     constexpr int64_t kWidth = sizeof(V);
-    const int64_t pieces = a.row_bytes / kWidth;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    for (int32_t m = wave; m < misses; m += kWaves) {
-        const int64_t dst_row = s.miss_loc[m];
-        const int64_t src_row = s.miss_host[m];
-        if (dst_row < 0 || src_row < 0) {
-            continue;  // uniform over the wave
-        }
-        for (int64_t first = 0; first < 2 * pieces; first += 4 * 64) {
-            V v[4];
+    const uint32_t per_plane = static_cast<uint32_t>(a.row_bytes / kWidth);
+    const uint32_t total = static_cast<uint32_t>(misses) * 2u * per_plane;
+    for (uint32_t first = 0; first < total; first += 4 * kThreads) {
+        V v[4];
+        int64_t dst[4];
+        bool ok[4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int64_t p = first + k * 64 + lane;
-                const int64_t kv = p >= pieces ? 1 : 0;
-                const int64_t at = p < 2 * pieces ? p - kv * pieces : 0;
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t q = first + k * kThreads + threadIdx.x;
+            const uint32_t m = q < total ? a.row_div.div(q) : 0u;   // miss index
+            const uint32_t p = q - m * 2u * per_plane;              // piece within the miss's K and V rows
+            const int64_t kv = p >= per_plane ? 1 : 0;
+            const int64_t at = static_cast<int64_t>(p) - kv * per_plane;
+            ok[k] = q < total && s.miss_loc[m] >= 0;
+            dst[k] = 0;
+            if (ok[k]) {
+                const int64_t src_row = s.miss_host[m];
+                dst[k] = kv * a.dev_kv + static_cast<int64_t>(s.miss_loc[m]) * a.dev_rs + at * kWidth;
                 v[k] = *reinterpret_cast<const V*>(a.host_k + kv * a.host_kv + src_row * a.host_rs + at * kWidth);
             }
+        }
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int64_t p = first + k * 64 + lane;
-                if (p < 2 * pieces) {
-                    const int64_t kv = p >= pieces ? 1 : 0;
-                    *reinterpret_cast<V*>(a.dev_k + kv * a.dev_kv + dst_row * a.dev_rs + (p - kv * pieces) * kWidth) =
-                        v[k];
-                }
+        for (int k = 0; k < 4; ++k) {
+            if (ok[k]) {
+                *reinterpret_cast<V*>(a.dev_k + dst[k]) = v[k];
             }
         }
     }
@@ -636,6 +637,11 @@ int hisparse_swap_in(const ekv_tensor* topk_p, const ekv_tensor* tokens_p, const
                                       static_cast<int64_t>(reinterpret_cast<uintptr_t>(a.host_k)),
                                       static_cast<int64_t>(reinterpret_cast<uintptr_t>(a.dev_k))});
     const auto st = static_cast<hipStream_t>(stream);
+    const int64_t pieces = 2 * (a.row_bytes / vw);
+    if (pieces * kMaxLanes >= (int64_t{1} << 31)) {
+        throw std::invalid_argument("rows too large for one swap-in (copy pieces exceed 2^31)");
+    }
+    a.row_div = FastDiv(static_cast<uint32_t>(pieces));
     switch (vw) {
         case 16: launch<16>(a, lds, st); break;
         case 8: launch<8>(a, lds, st); break;
