@@ -46,6 +46,7 @@
 #include "ekv_tensor_util.h"
 #include "ekv_vec.h"
 
+#include <atomic>
 #include <climits>
 
 namespace ekv {
@@ -56,6 +57,7 @@ constexpr int kWaves = kThreads / 64;
 constexpr int64_t kMaxHot = 4096;     // hot slots per request (LDS holds the hash and the order)
 constexpr int64_t kMaxLanes = 2048;   // selected lanes per row (Top-K blocks x block size)
 constexpr int32_t kEmpty = -1;
+constexpr int kMaxDevices = 64;
 
 enum LaneKind : uint8_t { kInvalid = 0, kNewest = 1, kHit = 2, kMiss = 3 };
 
@@ -480,9 +482,21 @@ size_t lds_bytes(int64_t H, int64_t HB, int64_t W) {
 template <int kVecWidth>
 void launch(const HsArgs& a, size_t lds, hipStream_t stream) {
     const auto kernel = hisparse_swap_kernel<kVecWidth>;
-    check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  static_cast<int>(lds)),
-              "raise the swap-in LDS limit");
+    // The LDS limit is raised once per device, to the largest size any call
+    // needs, so calls recorded into a graph make no attribute call.
+    static std::atomic<bool> raised[kMaxDevices];
+    int device = 0;
+    check_hip(hipGetDevice(&device), "hipGetDevice");
+    if (device < 0 || device >= kMaxDevices) {
+        throw std::invalid_argument("device ordinal out of range");
+    }
+    if (!raised[device].load(std::memory_order_acquire)) {
+        check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      static_cast<int>(lds_bytes(kMaxHot, 2 * kMaxHot, kMaxLanes))),
+                  "raise the swap-in LDS limit");
+        raised[device].store(true, std::memory_order_release);
+    }
     kernel<<<dim3(static_cast<uint32_t>(a.batch)), dim3(kThreads), lds, stream>>>(a);
     check_hip(hipGetLastError(), "launch hisparse swap-in");
 }

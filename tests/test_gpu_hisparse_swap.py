@@ -209,3 +209,64 @@ def test_decode_sized_call_matches_the_oracle(gpu):
     assert np.array_equal(lru_d.cpu().numpy().astype(np.int64), want_lru)
     assert np.array_equal(device_k.cpu().numpy(), want_k) and np.array_equal(device_v.cpu().numpy(), want_v)
     assert (out >= 0).all().item()                                          # every lane selected a valid token
+
+
+def test_graph_replays_with_padding_rows_match_the_oracle(gpu):
+    # SGLang replays decode from captured graphs; rows at or past num_real_reqs are padding.
+    rng = np.random.default_rng(505)
+    batch, hot, bs, k, context, row_bytes = 4, 64, 4, 6, 400, 64
+    host_rows = batch * context
+    host_locs = rng.permutation(host_rows).reshape(batch, context)
+    dev_locs = rng.permutation(batch * (hot + 1)).reshape(batch, hot + 1) + 1
+    host = torch.randint(0, 256, (2, host_rows, row_bytes), dtype=torch.uint8).pin_memory()
+    device_k = torch.zeros((batch * (hot + 1) + 1, row_bytes), dtype=torch.uint8, device=gpu)
+    device_v = torch.zeros_like(device_k)
+    tokens = torch.full((batch, hot + 1), -1, dtype=torch.int32, device=gpu)
+    lru = torch.arange(hot, dtype=torch.int16, device=gpu).repeat(batch, 1)
+    blocks_d = torch.zeros((batch, k), dtype=torch.int32, device=gpu)
+    seq_d = torch.zeros(batch, dtype=torch.int32, device=gpu)
+    real_d = torch.zeros(1, dtype=torch.int32, device=gpu)
+    req = torch.arange(batch, device=gpu)
+    out = torch.empty((batch, k * bs), dtype=torch.int32, device=gpu)
+    host_locs_d, dev_locs_d = torch.tensor(host_locs, device=gpu), torch.tensor(dev_locs, device=gpu)
+
+    def call():
+        load_blocks_to_device_buffer_mha(
+            top_k_blocks=blocks_d, device_buffer_tokens=tokens, host_cache_locs=host_locs_d,
+            device_buffer_locs=dev_locs_d, host_cache_k=host[0], host_cache_v=host[1], device_buffer_k=device_k,
+            device_buffer_v=device_v, top_k_device_locs=out, req_pool_indices=req, seq_lens=seq_d, lru_slots=lru,
+            item_size_bytes=row_bytes, hot_buffer_size=hot, sparse_block_size=bs, num_real_reqs=real_d)
+
+    want = (tokens.cpu().numpy(), lru.cpu().numpy().astype(np.int64), device_k.cpu().numpy(),
+            device_v.cpu().numpy())
+    seq = np.full(batch, 150)
+    graph = torch.cuda.CUDAGraph()
+    for step in range(6):
+        seq = seq + 1
+        blocks = np.stack([rng.choice(-(-int(s) // bs), size=k, replace=False) for s in seq])
+        real = int(rng.integers(1, batch + 1))
+        blocks_d.copy_(torch.tensor(blocks, dtype=torch.int32))
+        seq_d.copy_(torch.tensor(seq, dtype=torch.int32))
+        real_d.fill_(real)
+        if step == 0:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                call()                                     # eager first call
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph):
+                call()                                     # recorded, not run
+        else:
+            graph.replay()
+        torch.cuda.synchronize()
+        want_out, *rest = ref.hisparse_swap(blocks, *want[:1], host_locs, dev_locs, host[0].numpy(),
+                                            host[1].numpy(), want[2], want[3], np.arange(batch), seq, want[1], hot,
+                                            bs, real)
+        want = (rest[0], rest[1], rest[2], rest[3])
+        assert np.array_equal(out.cpu().numpy()[:real], want_out[:real]), step
+        assert (out.cpu().numpy()[real:] == -1).all(), step
+        assert np.array_equal(tokens.cpu().numpy(), want[0]), step
+        assert np.array_equal(lru.cpu().numpy().astype(np.int64), want[1]), step
+        assert np.array_equal(device_k.cpu().numpy(), want[2]) and np.array_equal(device_v.cpu().numpy(), want[3])
+        torch.randn(1000, device=gpu).sum().item()        # eager work between replays
