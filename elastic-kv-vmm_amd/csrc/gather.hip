@@ -22,6 +22,7 @@
 //                           over one flat payload tensor.
 #include "../../include/ekv_kernels.h"
 #include "ekv_common.h"
+#include "ekv_device.h"
 #include "ekv_fastdiv.h"
 #include "ekv_tensor_util.h"
 #include "ekv_vec.h"
@@ -107,10 +108,6 @@ struct EngineArgs {
     int64_t S;
 };
 
-__device__ __forceinline__ int64_t load_index(const void* p, int64_t i, int32_t is64) {
-    return is64 ? static_cast<const int64_t*>(p)[i] : static_cast<int64_t>(static_cast<const int32_t*>(p)[i]);
-}
-
 // (source offset, destination offset) in bytes of one row; -1 source means a
 // zero row, -1 destination means the row is not written.
 __device__ __forceinline__ void split_unit(const EngineArgs& a, int64_t u, int64_t& l, int64_t& b, int64_t& kv,
@@ -167,8 +164,8 @@ __device__ __forceinline__ void locate(const EngineArgs& a, int64_t u, int64_t& 
     } else {
         const int64_t b = u / a.S;
         const int64_t s = u - b * a.S;
-        const int64_t position = load_index(a.positions_b.data, b * a.positions_b.stride + s * a.pos_ss,
-                                            a.positions_b.is64);
+        const int64_t position = load_index(a.positions_b.data, a.positions_b.is64,
+                                            b * a.positions_b.stride + s * a.pos_ss);
         const int64_t req = a.request_ids[b];
         const int64_t length = a.lengths[b];
         const bool valid = position >= 0 && position < length;
@@ -179,7 +176,7 @@ __device__ __forceinline__ void locate(const EngineArgs& a, int64_t u, int64_t& 
             } else {
                 if (req >= 0 && req < a.rt_rows && position < a.rt_cols) {
                     const int64_t logical =
-                        load_index(a.request_table, req * a.rt_sr + position * a.rt_sc, a.rt64);
+                        load_index(a.request_table, a.rt64, req * a.rt_sr + position * a.rt_sc);
                     if (logical >= 0 && logical < a.slot_len) {
                         element = a.slot_offsets[logical];
                     }

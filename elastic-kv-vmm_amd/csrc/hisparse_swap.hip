@@ -42,6 +42,7 @@
 // Locations outside the device buffer are reported as -1 and never written.
 #include "../../include/ekv_kernels.h"
 #include "ekv_common.h"
+#include "ekv_device.h"
 #include "ekv_fastdiv.h"
 #include "ekv_tensor_util.h"
 #include "ekv_vec.h"
@@ -111,11 +112,6 @@ struct Lds {
     int32_t* scratch;     // [3 * kWaves + 4]
 };
 
-__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
-    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
-                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
-}
-
 // Exclusive ranks of N flags over the workgroup's threads in thread order,
 // and their totals. Every thread must call it (two barriers).
 template <int N>
@@ -145,11 +141,6 @@ __device__ __forceinline__ void rank_flags(const bool (&flag)[N], int32_t (&rank
         total[k] = all;
     }
     __syncthreads();  // scratch is rewritten by the next call
-}
-
-__device__ __forceinline__ int64_t load_index(const void* base, int32_t is64, int64_t offset) {
-    return is64 ? static_cast<const int64_t*>(base)[offset]
-                : static_cast<int64_t>(static_cast<const int32_t*>(base)[offset]);
 }
 
 __device__ __forceinline__ uint32_t bucket_of(const HsArgs& a, int32_t token) {

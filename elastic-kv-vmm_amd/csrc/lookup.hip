@@ -33,6 +33,7 @@
 // shapes: larger windows cost occupancy (LDS) more than they save.
 #include "../../include/ekv_kernels.h"
 #include "ekv_common.h"
+#include "ekv_device.h"
 #include "ekv_fastdiv.h"
 #include "ekv_tensor_util.h"
 
@@ -102,11 +103,6 @@ struct LookupArgs {
     uint32_t block_size;
     FastDiv block_div;
 };
-
-__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
-    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
-                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
-}
 
 // Element `index` of a row at `base` with element stride `stride`. The dense
 // form (stride 1 and row extents below 4 GiB, both checked on the host)
