@@ -11,10 +11,12 @@ Two independent restatements of the reference semantics live here:
   * COracle, a ctypes binding of ekv_oracle.c (scalar C, following the
     Triton lookup adaptive_sparse/resident_lookup.py:14-26 lane by lane),
 plus restatements of the reference's hit semantics
-(adaptive_sparse/hisparse_access_trace.py:59-71) and batch-token LRU replay
-(benchmarks/hisparse_locality_replay.py:90-99). tests/test_oracle.py pins all
-of them against the reference's known-answer vectors, closed forms and
-brute-force loops.
+(adaptive_sparse/hisparse_access_trace.py:59-71), its batch-token LRU replay
+(benchmarks/hisparse_locality_replay.py:90-99), and the swap-in in SGLang's
+calling convention that its decode path and swap smoke test use
+(tests/smoke_minimax_swap.py:18-67). tests/test_oracle.py pins all of them
+against the reference's known-answer vectors, closed forms, its smoke
+scenarios and brute-force loops.
 """
 
 import ctypes as ct

@@ -545,3 +545,26 @@ def test_block_segments_hand_case_and_plane_layout_equivalence():
                              32768, 20000, layout.capacity_bytes, layout.chunk_bytes)
     for blocks in ([0], [1, 63, 64], [19999], list(range(100, 140))):
         assert segments.chunks(blocks) == layout.chunks_for_slots(blocks)
+
+
+# ------------------------------------------------------------------ SGLang-convention swap-in (host checks)
+
+def test_hisparse_swap_host_checks():
+    import torch
+
+    from adaptive_sparse.hisparse_swap import _row_layout, host_device_pointer, load_blocks_to_device_buffer_mha
+
+    k = torch.zeros((10, 2, 8), dtype=torch.bfloat16)
+    v = torch.zeros((10, 2, 8), dtype=torch.bfloat16)
+    row_bytes, row_stride, _, rows = _row_layout(k, v, "cache")
+    assert (row_bytes, row_stride, rows) == (32, 32, 10)
+    with pytest.raises(ValueError, match="must share shape"):
+        _row_layout(k, v[:, :1], "cache")
+    with pytest.raises(ValueError, match="rows must be contiguous"):
+        _row_layout(k.transpose(1, 2), v.transpose(1, 2), "cache")
+    with pytest.raises(ValueError, match="pinned CPU memory"):
+        host_device_pointer(k)                                     # pageable host memory
+    small = torch.zeros((1, 1), dtype=torch.int32)
+    with pytest.raises(ValueError, match="need GPU tensors"):     # no CPU fallback
+        load_blocks_to_device_buffer_mha(small, small, small, small, k, v, k, v, small, small[0], small[0], small,
+                                         32, 1, 1)
