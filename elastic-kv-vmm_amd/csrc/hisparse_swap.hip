@@ -57,6 +57,8 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int64_t kMaxHot = 4096;     // hot slots per request (LDS holds the hash and the order)
 constexpr int64_t kMaxLanes = 2048;   // selected lanes per row (Top-K blocks x block size)
+constexpr int kLanesPerThread = static_cast<int>(kMaxLanes / kThreads);
+constexpr int kBatch = 8;             // state loads in flight per thread
 constexpr int32_t kEmpty = -1;
 constexpr int kMaxDevices = 64;
 
@@ -106,6 +108,7 @@ struct Lds {
     int32_t* lane_tok;    // [W]
     int32_t* lane_aux;    // [W] hit: slot; miss: hash bucket
     int32_t* lane_pos;    // [W] output position (-1: not selected)
+    int32_t* lane_val;    // [W] hit: its device row (-1: outside the buffer); miss: its host row
     int32_t* miss_host;   // [W] host row of the m-th miss
     int32_t* miss_loc;    // [W] device row of the m-th miss (-1: none)
     uint8_t* lane_kind;   // [W]
@@ -218,6 +221,7 @@ __global__ __launch_bounds__(kThreads) void hisparse_swap_kernel(const HsArgs a)
         s.lane_tok = reinterpret_cast<int32_t*>(take(W * 4));
         s.lane_aux = reinterpret_cast<int32_t*>(take(W * 4));
         s.lane_pos = reinterpret_cast<int32_t*>(take(W * 4));
+        s.lane_val = reinterpret_cast<int32_t*>(take(W * 4));
         s.miss_host = reinterpret_cast<int32_t*>(take(W * 4));
         s.miss_loc = reinterpret_cast<int32_t*>(take(W * 4));
         s.lane_kind = reinterpret_cast<uint8_t*>(take(W));
@@ -236,14 +240,30 @@ __global__ __launch_bounds__(kThreads) void hisparse_swap_kernel(const HsArgs a)
     }
     int32_t* tokens = a.tokens + r * a.tok_sr;
 
-    // 1. Load the hot tokens and the LRU order; build the hash.
-    for (int64_t i = threadIdx.x; i < H; i += kThreads) {
-        s.tok[i] = tokens[i * a.tok_ss];
-        s.first_touch[i] = INT_MAX;
-        s.hit_rank[i] = -1;
-        const int64_t slot = a.lru32 ? static_cast<const int32_t*>(a.lru)[r * a.lru_sr + i * a.lru_ss]
-                                     : static_cast<const int16_t*>(a.lru)[r * a.lru_sr + i * a.lru_ss];
-        s.order[i] = static_cast<int16_t>(slot >= 0 && slot < H ? slot : -1);
+    // 1. Load the hot tokens and the LRU order (kBatch loads per thread in
+    //    flight at once, clamped indices); build the hash.
+    const int64_t reserved = device_row(a, r, H);
+    for (int64_t first = 0; first < H; first += kThreads * kBatch) {
+        int32_t held[kBatch];
+        int64_t listed[kBatch];
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int64_t i = first + k * kThreads + threadIdx.x;
+            const int64_t at = i < H ? i : H - 1;
+            held[k] = tokens[at * a.tok_ss];
+            listed[k] = a.lru32 ? static_cast<const int32_t*>(a.lru)[r * a.lru_sr + at * a.lru_ss]
+                                : static_cast<const int16_t*>(a.lru)[r * a.lru_sr + at * a.lru_ss];
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) {
+            const int64_t i = first + k * kThreads + threadIdx.x;
+            if (i < H) {
+                s.tok[i] = held[k];
+                s.first_touch[i] = INT_MAX;
+                s.hit_rank[i] = -1;
+                s.order[i] = static_cast<int16_t>(listed[k] >= 0 && listed[k] < H ? listed[k] : -1);
+            }
+        }
     }
     for (int64_t j = threadIdx.x; j < a.HB; j += kThreads) {
         s.hash[j] = kEmpty;
@@ -276,71 +296,109 @@ __global__ __launch_bounds__(kThreads) void hisparse_swap_kernel(const HsArgs a)
     }
     __syncthreads();
 
-    // 2. Classify every lane; hits mark their slot, misses claim a bucket.
+    // 2. Classify every lane (a thread holds lanes threadIdx.x + 256 k):
+    //    Top-K loads of all its lanes first, then the hash probes (a hit marks
+    //    its slot, a miss claims a bucket), then one batch of loads: the
+    //    device row of each hit, the host row of each miss.
     const void* topk_row = a.topk64 ? static_cast<const void*>(static_cast<const int64_t*>(a.topk) + b * a.topk_sb)
                                     : static_cast<const void*>(static_cast<const int32_t*>(a.topk) + b * a.topk_sb);
-    for (int64_t o = threadIdx.x; o < W; o += kThreads) {
-        const uint32_t k = a.block_div.div(static_cast<uint32_t>(o));
-        const int64_t block = load_index(topk_row, a.topk64, k * a.topk_sk);
-        const int64_t t = block * a.block_size + (static_cast<uint32_t>(o) - k * a.block_size);
-        uint8_t kind = kInvalid;
-        int32_t aux = -1;
-        if (block >= 0 && t < length && t < a.T) {
-            if (t == length - 1) {
-                kind = kNewest;
-            } else {
-                s.lane_tok[o] = static_cast<int32_t>(t);
-                __threadfence_block();  // the token is visible before this lane's claim is
-                uint32_t h = bucket_of(a, static_cast<int32_t>(t));
-                for (int64_t probe = 0; probe < a.HB; ++probe, h = (h + 1) & static_cast<uint32_t>(a.HB - 1)) {
-                    int32_t v = load_entry(s, h);
-                    if (v == kEmpty) {
-                        v = atomicCAS(&s.hash[h], kEmpty, static_cast<int32_t>(H + o));
+    {
+        int64_t block[kLanesPerThread];
+#pragma unroll
+        for (int k = 0; k < kLanesPerThread; ++k) {
+            const int64_t o = threadIdx.x + k * kThreads;
+            const uint32_t at = static_cast<uint32_t>(o < W ? o : W - 1);
+            block[k] = load_index(topk_row, a.topk64, a.block_div.div(at) * a.topk_sk);
+        }
+        uint8_t kinds[kLanesPerThread];
+        int32_t auxes[kLanesPerThread];
+#pragma unroll
+        for (int k = 0; k < kLanesPerThread; ++k) {
+            const int64_t o = threadIdx.x + k * kThreads;
+            const uint32_t kb = a.block_div.div(static_cast<uint32_t>(o < W ? o : 0));
+            const int64_t t = block[k] * a.block_size + (static_cast<uint32_t>(o < W ? o : 0) - kb * a.block_size);
+            uint8_t kind = kInvalid;
+            int32_t aux = -1;
+            if (o < W && block[k] >= 0 && t < length && t < a.T) {
+                if (t == length - 1) {
+                    kind = kNewest;
+                } else {
+                    s.lane_tok[o] = static_cast<int32_t>(t);
+                    __threadfence_block();  // the token is visible before this lane's claim is
+                    uint32_t h = bucket_of(a, static_cast<int32_t>(t));
+                    for (int64_t probe = 0; probe < a.HB; ++probe, h = (h + 1) & static_cast<uint32_t>(a.HB - 1)) {
+                        int32_t v = load_entry(s, h);
                         if (v == kEmpty) {
+                            v = atomicCAS(&s.hash[h], kEmpty, static_cast<int32_t>(H + o));
+                            if (v == kEmpty) {
+                                kind = kMiss;
+                                aux = static_cast<int32_t>(h);
+                                break;
+                            }
+                        }
+                        // v is set: a resident slot, or a miss claimed by some lane
+                        // (lane_tok of a claiming lane is written before its claim).
+                        if (v < H) {
+                            if (s.tok[v] == t) {
+                                kind = kHit;
+                                aux = v;
+                                atomicMin(&s.first_touch[v], static_cast<int32_t>(o));
+                                break;
+                            }
+                        } else if (s.lane_tok[v - H] == t) {
                             kind = kMiss;
                             aux = static_cast<int32_t>(h);
+                            atomicMin(&s.hash[h], static_cast<int32_t>(H + o));
                             break;
                         }
-                    }
-                    // v is set: a resident slot, or a miss claimed by some lane
-                    // (lane_tok of a claiming lane is written before its claim).
-                    if (v < H) {
-                        if (s.tok[v] == t) {
-                            kind = kHit;
-                            aux = v;
-                            atomicMin(&s.first_touch[v], static_cast<int32_t>(o));
-                            break;
-                        }
-                    } else if (s.lane_tok[v - H] == t) {
-                        kind = kMiss;
-                        aux = static_cast<int32_t>(h);
-                        atomicMin(&s.hash[h], static_cast<int32_t>(H + o));
-                        break;
                     }
                 }
             }
+            kinds[k] = kind;
+            auxes[k] = aux;
         }
-        s.lane_kind[o] = kind;
-        s.lane_aux[o] = aux;
+        int64_t rows[kLanesPerThread];
+#pragma unroll
+        for (int k = 0; k < kLanesPerThread; ++k) {
+            const int64_t o = threadIdx.x + k * kThreads;
+            rows[k] = -1;
+            if (kinds[k] == kHit) {
+                rows[k] = load_index(a.dev_locs, a.dev_locs64, r * a.dl_sr + int64_t{auxes[k]} * a.dl_ss);
+            } else if (kinds[k] == kMiss) {
+                rows[k] = load_index(a.host_locs, a.host_locs64, r * a.hl_sr + int64_t{s.lane_tok[o]} * a.hl_st);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kLanesPerThread; ++k) {
+            const int64_t o = threadIdx.x + k * kThreads;
+            if (o < W) {
+                uint8_t kind = kinds[k];
+                int32_t value = -1;
+                if (kind == kHit) {
+                    value = rows[k] >= 0 && rows[k] < a.dev_rows ? static_cast<int32_t>(rows[k]) : -1;
+                } else if (kind == kMiss) {
+                    if (rows[k] >= 0 && rows[k] < a.host_rows) {
+                        value = static_cast<int32_t>(rows[k]);
+                    } else {
+                        kind = kInvalid;  // no host row: every lane of this token sees the same row
+                    }
+                }
+                s.lane_kind[o] = kind;
+                s.lane_aux[o] = auxes[k];
+                s.lane_val[o] = value;
+            }
+        }
     }
     __syncthreads();
 
     // 3. First lanes of each token, host rows, ranks in selection order;
     //    outputs of the newest token and of hits.
-    const int64_t reserved = device_row(a, r, H);
     int32_t base[3] = {0, 0, 0};  // selected, first hits, first misses so far
     for (int64_t chunk = 0; chunk < W; chunk += kThreads) {
         const int64_t o = chunk + threadIdx.x;
-        uint8_t kind = o < W ? s.lane_kind[o] : kInvalid;
+        const uint8_t kind = o < W ? s.lane_kind[o] : kInvalid;
         const int32_t aux = o < W ? s.lane_aux[o] : -1;
-        int64_t host_row = -1;
-        if (kind == kMiss) {
-            host_row = load_index(a.host_locs, a.host_locs64, r * a.hl_sr + s.lane_tok[o] * a.hl_st);
-            if (host_row < 0 || host_row >= a.host_rows) {
-                kind = kInvalid;  // every lane of this token sees the same row
-                s.lane_kind[o] = kInvalid;
-            }
-        }
+        const int32_t value = o < W ? s.lane_val[o] : -1;   // device row of a hit, host row of a miss
         const bool first_hit = kind == kHit && s.first_touch[aux] == o;
         const bool first_miss = kind == kMiss && s.hash[aux] == H + o;
         const bool flags[3] = {kind != kInvalid, first_hit, first_miss};
@@ -352,7 +410,7 @@ __global__ __launch_bounds__(kThreads) void hisparse_swap_kernel(const HsArgs a)
             if (kind == kNewest) {
                 out[pos * a.out_so] = static_cast<int32_t>(reserved);
             } else if (kind == kHit) {
-                out[pos * a.out_so] = static_cast<int32_t>(device_row(a, r, aux));
+                out[pos * a.out_so] = value;
             }
             if (first_hit) {
                 s.hit_rank[aux] = static_cast<int16_t>(base[1] + rank[1]);
@@ -361,7 +419,7 @@ __global__ __launch_bounds__(kThreads) void hisparse_swap_kernel(const HsArgs a)
                 const int32_t m = base[2] + rank[2];
                 s.lane_rank[o] = static_cast<int16_t>(m);
                 s.miss_lane[m] = static_cast<int16_t>(o);
-                s.miss_host[m] = static_cast<int32_t>(host_row);
+                s.miss_host[m] = value;
             }
         }
 #pragma unroll
@@ -436,14 +494,25 @@ __global__ __launch_bounds__(kThreads) void hisparse_swap_kernel(const HsArgs a)
         __syncthreads();  // the victims were written after the last ranking barrier
 
         // 5. Misses take their victims: token table, locations.
-        for (int64_t m = threadIdx.x; m < misses; m += kThreads) {
-            const int32_t slot = s.victim[m];
-            int32_t loc = -1;
-            if (slot >= 0) {
-                tokens[static_cast<int64_t>(slot) * a.tok_ss] = s.lane_tok[s.miss_lane[m]];
-                loc = static_cast<int32_t>(device_row(a, r, slot));
+        {
+            int64_t loc[kLanesPerThread];
+#pragma unroll
+            for (int k = 0; k < kLanesPerThread; ++k) {
+                const int64_t m = threadIdx.x + k * kThreads;
+                const int32_t slot = m < misses ? s.victim[m] : -1;
+                loc[k] = slot >= 0 ? device_row(a, r, slot) : -1;
             }
-            s.miss_loc[m] = loc;
+#pragma unroll
+            for (int k = 0; k < kLanesPerThread; ++k) {
+                const int64_t m = threadIdx.x + k * kThreads;
+                if (m < misses) {
+                    const int32_t slot = s.victim[m];
+                    if (slot >= 0) {
+                        tokens[static_cast<int64_t>(slot) * a.tok_ss] = s.lane_tok[s.miss_lane[m]];
+                    }
+                    s.miss_loc[m] = static_cast<int32_t>(loc[k]);
+                }
+            }
         }
         __syncthreads();
     }
@@ -466,7 +535,7 @@ __global__ __launch_bounds__(kThreads) void hisparse_swap_kernel(const HsArgs a)
 
 size_t lds_bytes(int64_t H, int64_t HB, int64_t W) {
     auto round = [](int64_t bytes) { return static_cast<size_t>((bytes + 15) & ~int64_t{15}); };
-    return round(HB * 4) + round(H * 4) * 2 + round(H * 2) * 2 + round(W * 2) * 3 + round(W * 4) * 5 + round(W) +
+    return round(HB * 4) + round(H * 4) * 2 + round(H * 2) * 2 + round(W * 2) * 3 + round(W * 4) * 6 + round(W) +
            round((3 * kWaves + 4) * 4);
 }
 
