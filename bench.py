@@ -196,7 +196,7 @@ def lookup_roofline(algorithmic_bytes, avg_ms, traffic):
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "moved_gbs": None if traffic is None else round(traffic / (avg_ms / 1e3) / 1e9, 1),
-            "kernel": "resolve_single_kernel<bits, compact> (ekv_resolve_resident_bits)",
+            "kernel": "resolve_single_kernel<int32 Top-K, int16 table, bits, compact> (ekv_resolve_resident_local)",
             "algorithmic_bytes_per_launch": algorithmic_bytes, "avg_launch_ms": round(avg_ms, 4)}
 
 
@@ -284,24 +284,34 @@ def run_decode_read(torch, args, device):
     counts = torch.empty((L, R), dtype=torch.int32, device=device)
     output = torch.empty((R, L, 2, K, 256), dtype=torch.bfloat16, device=device)
     bits = build_residency_bits(table)          # maintained with the table; built once here
+    # The same residency as an int16 table of local slots (request r's hot slots start at r * C + 1).
+    slot_base = torch.arange(R, device=device, dtype=torch.int64) * C + 1
+    table16 = torch.where(table > 0, table - slot_base.view(1, R, 1).to(torch.int32) + 1, 0).to(torch.int16)
+    bits16 = build_residency_bits(table16)
 
     def lookup_plain():
         resolve_resident(topk, table, None, rows, lengths, rows, slots, 1, misses=misses, miss_count=counts)
 
-    def lookup():
+    def lookup_global():
         resolve_resident(topk, table, None, rows, lengths, rows, slots, 1, misses=misses, miss_count=counts,
                          resident_bits=bits)
+
+    def lookup():
+        resolve_resident(topk, table16, None, rows, lengths, rows, slots, 1, misses=misses, miss_count=counts,
+                         resident_bits=bits16, slot_base=slot_base)
 
     def gather():
         gather_kv(planes, slots, output)
 
     lookup_plain()
     plain = (slots.clone(), misses.clone(), counts.clone())
-    lookup()
-    torch.cuda.synchronize()
-    same = (torch.equal(plain[0], slots) and torch.equal(plain[2], counts)
-            and all(torch.equal(plain[1][l, r, :c], misses[l, r, :c])
-                    for l, r, c in ((0, 0, int(counts[0, 0])), (L - 1, R - 1, int(counts[L - 1, R - 1])))))
+    same = torch.equal(bits, bits16)
+    for variant in (lookup_global, lookup):
+        variant()
+        torch.cuda.synchronize()
+        same = same and (torch.equal(plain[0], slots) and torch.equal(plain[2], counts)
+                         and all(torch.equal(plain[1][l, r, :c], misses[l, r, :c])
+                                 for l, r, c in ((0, 0, int(counts[0, 0])), (L - 1, R - 1, int(counts[L - 1, R - 1])))))
     del plain
     for _ in range(args.warmup):
         lookup()
@@ -310,7 +320,7 @@ def run_decode_read(torch, args, device):
     hits = int((slots > 0).sum().item())
     miss_total = int(counts.sum().item())
     lanes = L * R * K
-    lookup_bytes = 12 * lanes + 4 * miss_total + 4 * L * R
+    lookup_bytes = 10 * lanes + 4 * miss_total + 4 * L * R   # 4 B index + 2 B table entry + 4 B slot per lookup
     gather_bytes = lanes * 2 * row_bytes + hits * 2 * row_bytes + lanes * 4
     step_ms, phase = timed_steps(torch, args.steps, [("lookup", lookup), ("gather", gather)])
     step_spread = {"gather_ms": spread(LAST_SAMPLES["gather"]), "lookup_us": spread(LAST_SAMPLES["lookup"], 1e3, 2)}
@@ -330,12 +340,14 @@ def run_decode_read(torch, args, device):
     # launch per layer (as a decode step interleaved with attention issues
     # them) replayed from a HIP graph.
     lookup_alone_ms = back_to_back_ms(torch, lookup)
-    per_layer = [(topk[l:l + 1], table[l:l + 1], bits[l:l + 1], slots[l:l + 1], misses[l:l + 1], counts[l:l + 1])
-                 for l in range(L)]
+    lookup_global_ms = back_to_back_ms(torch, lookup_global)
+    per_layer = [(topk[l:l + 1], table16[l:l + 1], bits16[l:l + 1], slots[l:l + 1], misses[l:l + 1],
+                  counts[l:l + 1]) for l in range(L)]
 
     def lookup_by_layer():
         for tk, tb, bt, sl, ms, ct in per_layer:
-            resolve_resident(tk, tb, None, rows, lengths, rows, sl, 1, misses=ms, miss_count=ct, resident_bits=bt)
+            resolve_resident(tk, tb, None, rows, lengths, rows, sl, 1, misses=ms, miss_count=ct, resident_bits=bt,
+                             slot_base=slot_base)
 
     per_layer_graph_ms = graph_replay_ms(torch, lookup_by_layer)
     del per_layer
@@ -344,8 +356,9 @@ def run_decode_read(torch, args, device):
     torch.cuda.synchronize()
     achieved = gather_bytes / (phase["gather"] / 1e3) / 1e9
     log(f"step {step_ms:.3f} ms, gather {phase['gather']:.3f} ms ({achieved:.0f} GB/s), "
-        f"lookup {phase['lookup'] * 1e3:.1f} us in the step with the residency bitmap "
-        f"({plain_phase['lookup'] * 1e3:.1f} us without), {lookup_alone_ms * 1e3:.1f} us back to back, "
+        f"lookup {phase['lookup'] * 1e3:.1f} us in the step (int16 local-slot table + residency bitmap; "
+        f"{plain_phase['lookup'] * 1e3:.1f} us with plain int32 table reads), {lookup_alone_ms * 1e3:.1f} us back "
+        f"to back ({lookup_global_ms * 1e3:.1f} us with the int32 table + bitmap), "
         f"{per_layer_graph_ms * 1e3 / L:.2f} us per one-layer launch in a graph, identical results {same}")
 
     baseline = None
@@ -390,8 +403,10 @@ def run_decode_read(torch, args, device):
              "lookup_roofline": lookup_roofline(lookup_bytes, lookup_alone_ms,
                                                 read_traffic("resolve_resident_hisparse_decode.md")),
              "lookup_us_per_layer_launch_graph": round(per_layer_graph_ms * 1e3 / L, 2),
+             "lookup_us_back_to_back_int32_table": round(lookup_global_ms * 1e3, 2),
              "lookup_us_without_bitmap": round(plain_phase["lookup"] * 1e3, 2),
-             "lookup_bitmap_matches_plain": same,
+             "lookup_table": "int16 local slots + slot_base, residency bitmap",
+             "lookup_variants_identical": same,
              "engine_gbs_same_shapes": ceilings,
              "event_spread": step_spread,
              "hit_rate": round(hits / lanes, 4), "pool_commit_s": round(commit_s, 3)}

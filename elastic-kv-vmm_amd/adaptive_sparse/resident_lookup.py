@@ -13,7 +13,11 @@ Extensions (all optional, none changes the reference behaviour):
   * a leading layer dimension L on topk / output (table and mapping may then
     carry it too), so all layers of a decode step resolve in one launch;
   * resident_bits (single level only): a residency bitmap built by
-    build_residency_bits; non-resident lanes then skip their table read.
+    build_residency_bits; non-resident lanes then skip their table read;
+  * slot_base (single level only): the table is int16 and holds local slots
+    (0 = not resident, v >= 1 = local slot v - 1 of the request); the slot
+    written is slot_base[rows[r]] + v - 1. Half the bytes of an int32 table
+    of global slots, with the same output.
 """
 
 import ctypes as ct
@@ -24,7 +28,7 @@ from elastic_kv import _native
 
 
 def resolve_resident(topk, table, mapping, rows, lengths, selected, output, block_size, *,
-                     misses=None, miss_count=None, resident_bits=None):
+                     misses=None, miss_count=None, resident_bits=None, slot_base=None):
     """Write only selected rows into an existing [L, B, K * block_size] tensor.
 
     For selected row r, layer l and lane o: block = topk[l, r, o // bs],
@@ -40,7 +44,13 @@ def resolve_resident(topk, table, mapping, rows, lengths, selected, output, bloc
         raise ValueError("misses and miss_count must be given together")
     if resident_bits is not None and mapping is not None:
         raise ValueError("resident_bits needs the single-level form (mapping=None)")
+    if (slot_base is not None) != (table.dtype == torch.int16):
+        raise ValueError("an int16 table holds local slots and needs slot_base (and only it)")
+    if slot_base is not None and mapping is not None:
+        raise ValueError("slot_base needs the single-level form (mapping=None)")
     tensors = [topk, table, rows, lengths, selected, output]
+    if slot_base is not None:
+        tensors.append(slot_base)
     if resident_bits is not None:
         tensors.append(resident_bits)
     if mapping is not None:
@@ -59,6 +69,16 @@ def resolve_resident(topk, table, mapping, rows, lengths, selected, output, bloc
         mapping_view = ct.byref(_native.describe(mapping, "mapping")) if mapping is not None else None
     miss_view = ct.byref(_native.describe(misses, "misses")) if misses is not None else None
     count_view = ct.byref(_native.describe(miss_count, "miss_count")) if miss_count is not None else None
+    if slot_base is not None:
+        bits_view = ct.byref(_native.describe(resident_bits, "bits")) if resident_bits is not None else None
+        base_view = _native.describe(slot_base, "slot_base")
+        with torch.cuda.device(device):
+            status = lib.ekv_resolve_resident_local(
+                ct.byref(views[0]), ct.byref(views[1]), ct.byref(base_view), bits_view, ct.byref(views[2]),
+                ct.byref(views[3]), ct.byref(views[4]), ct.byref(views[5]), miss_view, count_view,
+                int(block_size), _native.stream_handle(device))
+        _native.check(lib, status, "resolve_resident")
+        return
     with torch.cuda.device(device):
         status = entry(
             ct.byref(views[0]), ct.byref(views[1]), mapping_view, ct.byref(views[2]),

@@ -26,22 +26,28 @@ INT32_MIN = -(1 << 31)
 class HotBuffers:
     """LRU hot buffers of `capacity` slots per (layer, request).
 
-    table [L, R, T] int32: token -> global slot (0 = not resident); bits: its
-    residency bitmap; slot_token [L, R, C]: token held by each slot (-1 =
-    empty); stamps [L, R, C]: recency stamps; slot_base [R]: global slot of
-    each request's local slot 0 (request r owns slots base .. base + C - 1).
+    table [L, R, T]: token -> global slot, int32 (0 = not resident), or with
+    table_dtype=torch.int16 token -> local slot + 1 (0 = not resident; the
+    lookup then takes slot_base=self.slot_base); bits: its residency bitmap;
+    slot_token [L, R, C]: token held by each slot (-1 = empty); stamps
+    [L, R, C]: recency stamps; slot_base [R]: global slot of each request's
+    local slot 0 (request r owns slots base .. base + C - 1).
     table and bits are views into storage whose rows are padded to a multiple
     of 128 positions, so every row starts 16-byte aligned and the lookup can
     stage its recent window and bitmap row with 16-byte loads.
     """
 
     def __init__(self, layers, requests, context, capacity, device, *, slot_base=None, with_bits=True,
-                 step_counter=False):
+                 step_counter=False, table_dtype=torch.int32):
         self.layers, self.requests, self.context, self.capacity = layers, requests, context, capacity
         self.device = torch.device(device)
+        if table_dtype not in (torch.int32, torch.int16):
+            raise ValueError("table_dtype must be torch.int32 (global slots) or torch.int16 (local slots)")
+        if table_dtype == torch.int16 and capacity >= 1 << 15:
+            raise ValueError("an int16 table holds local slot + 1: capacity must be below 32768")
         kw = dict(dtype=torch.int32, device=self.device)
         padded = -(-context // 128) * 128
-        self.table = torch.zeros((layers, requests, padded), **kw)[..., :context]
+        self.table = torch.zeros((layers, requests, padded), dtype=table_dtype, device=self.device)[..., :context]
         words = (context + 31) // 32
         self.bits = torch.zeros((layers, requests, padded // 32), **kw)[..., :words] if with_bits else None
         self.slot_token = torch.full((layers, requests, capacity), -1, **kw)
@@ -63,8 +69,11 @@ class HotBuffers:
         L, R, n = tokens.shape
         tokens = tokens.to(self.device, torch.int64)
         local = local_slots.to(self.device, torch.int64)
-        glob = (local + self.slot_base.view(1, R, 1)).to(torch.int32)
-        self.table.scatter_(2, tokens, glob)
+        if self.table.dtype == torch.int16:
+            entry = (local + 1).to(torch.int16)
+        else:
+            entry = (local + self.slot_base.view(1, R, 1)).to(torch.int32)
+        self.table.scatter_(2, tokens, entry)
         self.slot_token.scatter_(2, local, tokens.to(torch.int32))
         rank = torch.arange(n, device=self.device, dtype=torch.int32).expand(L, R, n)
         self.stamps.scatter_(2, local, rank - n - 1)

@@ -96,6 +96,7 @@ struct LookupArgs {
     int64_t bits_sl, bits_sr, bits_sw;
     int64_t bits_words;                  // words covering the table row: ceil(table_cols / 32)
     IndexRef rows, lengths, selected;
+    IndexRef slot_base;                  // int16 local tables: global slot of each request's local slot 0
     int32_t* out;
     int64_t out_sl, out_sb, out_so;
     int32_t* misses;
@@ -141,6 +142,18 @@ __device__ __forceinline__ T* element(T* base, int64_t stride, uint32_t index) {
         return reinterpret_cast<T*>(reinterpret_cast<Byte*>(base) + index * static_cast<uint32_t>(sizeof(T)));
     } else {
         return base + static_cast<int64_t>(index) * stride;
+    }
+}
+
+// A table entry as a slot. int16 tables hold local slots: 0 (or a negative
+// value) is not resident, v >= 1 is local slot v - 1 of the request, whose
+// global slot is base + v - 1. Other tables hold the global slot itself.
+template <typename TableT>
+__device__ __forceinline__ int32_t entry_slot(int32_t value, int64_t base) {
+    if constexpr (std::is_same_v<TableT, int16_t>) {
+        return value > 0 ? static_cast<int32_t>(base + value - 1) : 0;
+    } else {
+        return value;
     }
 }
 
@@ -209,10 +222,13 @@ template <typename TableT>
 __device__ __forceinline__ void stage_rows(uint32_t* win_dst, const TableT* win_src, int64_t win_stride,
                                            int64_t win_n, uint32_t* bits_dst, const int32_t* bits_src,
                                            int64_t bits_stride, int64_t bits_n) {
-    const bool fast = (win_n == 0 || dense_int32(win_src, win_stride)) &&
-                      (bits_n == 0 || dense_int32(bits_src, bits_stride));  // uniform
+    const bool bits_fast = bits_n == 0 || dense_int32(bits_src, bits_stride);  // uniform
+    if (win_n == 0 && bits_fast) {
+        stage_vector(bits_dst, bits_src, bits_n);   // bitmap only (any table type)
+        return;
+    }
     if constexpr (sizeof(TableT) == 4) {
-        if (fast) {
+        if (bits_fast && dense_int32(win_src, win_stride)) {
             stage_vector(win_dst, reinterpret_cast<const int32_t*>(win_src), win_n);
             stage_vector(bits_dst, bits_src, bits_n);
             return;
@@ -333,6 +349,7 @@ __global__ __launch_bounds__(kThreads) void resolve_single_kernel(const LookupAr
     const int64_t length = a.lengths[row];
     const bool table_ok = req >= 0 && req < a.table_rows && a.table_cols > 0;  // uniform
     const int64_t req_at = table_ok ? req : 0;
+    const int64_t base = std::is_same_v<TableT, int16_t> && table_ok ? a.slot_base[req] : 0;
     const int64_t bound = length < a.table_cols ? length : a.table_cols;
     const TopkT* topk = static_cast<const TopkT*>(a.topk) + layer * a.topk_sl + row * a.topk_sb;
     const TableT* table = static_cast<const TableT*>(a.table) + layer * a.table_sl + req_at * a.table_sr;
@@ -376,7 +393,7 @@ __global__ __launch_bounds__(kThreads) void resolve_single_kernel(const LookupAr
                                 : (table_ok ? static_cast<uint32_t>(*element<kDense>(bits_row, a.bits_sw, w)) : 0u);
                 need = need && ((word >> (p & 31)) & 1u);
             }
-            slot[i] = inside ? window[rel] : (valid ? 0 : -1);
+            slot[i] = inside ? entry_slot<TableT>(window[rel], base) : (valid ? 0 : -1);
             at[i] = need ? p : 0u;
             global |= static_cast<uint32_t>(need) << i;
         }
@@ -384,7 +401,8 @@ __global__ __launch_bounds__(kThreads) void resolve_single_kernel(const LookupAr
         for (int i = 0; i < kIters; ++i) {
             // Lanes that need no global read re-read entry 0 of the row (one
             // cached line shared by all of them) so the loads stay unconditional.
-            const int32_t value = table_ok ? static_cast<int32_t>(*element<kDense>(table, a.table_sc, at[i])) : 0;
+            const int32_t value =
+                table_ok ? entry_slot<TableT>(static_cast<int32_t>(*element<kDense>(table, a.table_sc, at[i])), base) : 0;
             slot[i] = (global >> i) & 1u ? value : slot[i];
         }
         running = emit<kCompact, kDense>(a, out, misses, first, slot, running, wave_totals, lane, wave);
@@ -497,17 +515,19 @@ void launch_with_table(const LookupArgs& a, int32_t map_dtype, bool compact, boo
         } else {
             resolve_single_kernel<TopkT, TableT, false, false, false><<<grid, block, lds, stream>>>(a);
         }
-    } else if (map_dtype == EKV_INT64) {
-        if (compact) {
-            resolve_mapped_kernel<TopkT, TableT, int64_t, true><<<grid, block, lds, stream>>>(a);
+    } else if constexpr (!std::is_same_v<TableT, int16_t>) {  // local tables are single level
+        if (map_dtype == EKV_INT64) {
+            if (compact) {
+                resolve_mapped_kernel<TopkT, TableT, int64_t, true><<<grid, block, lds, stream>>>(a);
+            } else {
+                resolve_mapped_kernel<TopkT, TableT, int64_t, false><<<grid, block, lds, stream>>>(a);
+            }
         } else {
-            resolve_mapped_kernel<TopkT, TableT, int64_t, false><<<grid, block, lds, stream>>>(a);
-        }
-    } else {
-        if (compact) {
-            resolve_mapped_kernel<TopkT, TableT, int32_t, true><<<grid, block, lds, stream>>>(a);
-        } else {
-            resolve_mapped_kernel<TopkT, TableT, int32_t, false><<<grid, block, lds, stream>>>(a);
+            if (compact) {
+                resolve_mapped_kernel<TopkT, TableT, int32_t, true><<<grid, block, lds, stream>>>(a);
+            } else {
+                resolve_mapped_kernel<TopkT, TableT, int32_t, false><<<grid, block, lds, stream>>>(a);
+            }
         }
     }
 }
@@ -517,6 +537,8 @@ void launch_table(const LookupArgs& a, int32_t table_dtype, int32_t map_dtype, b
                   hipStream_t stream) {
     if (table_dtype == EKV_INT64) {
         launch_with_table<TopkT, int64_t>(a, map_dtype, compact, dense, grid, stream);
+    } else if (table_dtype == EKV_INT16) {
+        launch_with_table<TopkT, int16_t>(a, map_dtype, compact, dense, grid, stream);
     } else {
         launch_with_table<TopkT, int32_t>(a, map_dtype, compact, dense, grid, stream);
     }
@@ -525,7 +547,8 @@ void launch_table(const LookupArgs& a, int32_t table_dtype, int32_t map_dtype, b
 int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const ekv_tensor* mapping_p,
                      const ekv_tensor* rows_p, const ekv_tensor* lengths_p, const ekv_tensor* selected_p,
                      const ekv_tensor* output_p, const ekv_tensor* misses_p, const ekv_tensor* counts_p,
-                     const ekv_tensor* bits_p, int64_t block_size, void* stream) {
+                     const ekv_tensor* bits_p, int64_t block_size, void* stream,
+                     const ekv_tensor* slot_base_p = nullptr) {
     const ekv_tensor& topk = need(topk_p, "topk");
     const ekv_tensor& table = need(table_p, "table");
     const ekv_tensor& rows = need(rows_p, "rows");
@@ -551,7 +574,14 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
     if (table.ndim != 2 && table.ndim != 3) {
         throw std::invalid_argument("table must be [R, T] or [L, R, T]");
     }
-    need_index(table, "table");
+    const bool local = slot_base_p != nullptr;
+    if (local) {
+        if (table.dtype != EKV_INT16 || mapping_p != nullptr) {
+            throw std::invalid_argument("a local-slot table is int16 and single level (mapping = NULL)");
+        }
+    } else {
+        need_index(table, "table");
+    }
     const bool layered_table = table.ndim == 3;
     if (layered_table) {
         need_dim(table, 0, layers, "table");
@@ -562,6 +592,13 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
     }
     need_dim(rows, 0, batch, "rows");
     need_dim(lengths, 0, batch, "lengths");
+    if (local) {
+        const ekv_tensor& base = need(slot_base_p, "slot_base");
+        need_ndim(base, 1, "slot_base");
+        need_index(base, "slot_base");
+        need_dim(base, 0, table.shape[layered_table ? 1 : 0], "slot_base");
+        need_data(base, "slot_base");
+    }
     const ekv_tensor* mapping = nullptr;
     if (mapping_p != nullptr) {
         mapping = &need(mapping_p, "mapping");
@@ -655,6 +692,9 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
     a.rows = index_ref(rows, 0);
     a.lengths = index_ref(lengths, 0);
     a.selected = index_ref(selected, 0);
+    if (local) {
+        a.slot_base = index_ref(*slot_base_p, 0);
+    }
     a.out = static_cast<int32_t*>(output.data);
     a.out_sl = output.stride[0];
     a.out_sb = output.stride[1];
@@ -684,7 +724,10 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
     // Staging the window reads kWindow entries per (row, layer); it pays once a
     // row has at least a quarter as many lanes. Two-level lookups stage only
     // int32 tables (a staged int32 id must equal the table value).
-    a.window = kWindow > 0 && width >= kWindow / 4 && (mapping == nullptr || table.dtype == EKV_INT32) ? 1 : 0;
+    // int16 (local-slot) tables take no window: their per-lane 2-byte reads
+    // measured faster on the 60-layer decode shapes than staging them.
+    a.window = kWindow > 0 && width >= kWindow / 4 && table.dtype != EKV_INT16 &&
+                       (mapping == nullptr || table.dtype == EKV_INT32) ? 1 : 0;
     a.bits_staged = EKV_LOOKUP_STAGE_BITS && bits_p != nullptr && a.bits_words <= kStagedBitWords ? 1 : 0;
 
     const dim3 grid(static_cast<uint32_t>(count), static_cast<uint32_t>(layers));
@@ -739,7 +782,9 @@ __global__ __launch_bounds__(kThreads) void residency_bits_kernel(const TableT* 
 int residency_bits(const ekv_tensor* table_p, const ekv_tensor* bits_p, void* stream) {
     const ekv_tensor& table = need(table_p, "table");
     const ekv_tensor& bits = need(bits_p, "resident_bits");
-    need_index(table, "table");
+    if (table.dtype != EKV_INT16) {
+        need_index(table, "table");
+    }
     if (table.ndim != 2 && table.ndim != 3) {
         throw std::invalid_argument("table must be [R, T] or [L, R, T]");
     }
@@ -771,6 +816,10 @@ int residency_bits(const ekv_tensor* table_p, const ekv_tensor* bits_p, void* st
         residency_bits_kernel<int64_t><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, s>>>(
             static_cast<const int64_t*>(table.data), t_sl, table.stride[d], table.stride[d + 1], rows, cols,
             static_cast<int32_t*>(bits.data), b_sl, bits.stride[d], bits.stride[d + 1], groups_per_row, total);
+    } else if (table.dtype == EKV_INT16) {
+        residency_bits_kernel<int16_t><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, s>>>(
+            static_cast<const int16_t*>(table.data), t_sl, table.stride[d], table.stride[d + 1], rows, cols,
+            static_cast<int32_t*>(bits.data), b_sl, bits.stride[d], bits.stride[d + 1], groups_per_row, total);
     } else {
         residency_bits_kernel<int32_t><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, s>>>(
             static_cast<const int32_t*>(table.data), t_sl, table.stride[d], table.stride[d + 1], rows, cols,
@@ -794,6 +843,21 @@ extern "C" int ekv_resolve_resident_bits(const ekv_tensor* topk, const ekv_tenso
         }
         return ekv::resolve_resident(topk, table, nullptr, rows, lengths, selected, output, misses, miss_count,
                                      resident_bits, block_size, stream);
+    });
+}
+
+extern "C" int ekv_resolve_resident_local(const ekv_tensor* topk, const ekv_tensor* table,
+                                          const ekv_tensor* slot_base, const ekv_tensor* resident_bits,
+                                          const ekv_tensor* rows, const ekv_tensor* lengths,
+                                          const ekv_tensor* selected, const ekv_tensor* output,
+                                          const ekv_tensor* misses, const ekv_tensor* miss_count,
+                                          int64_t block_size, void* stream) {
+    return ekv::guarded(-1, [&] {
+        if (slot_base == nullptr) {
+            throw std::invalid_argument("slot_base is required");
+        }
+        return ekv::resolve_resident(topk, table, nullptr, rows, lengths, selected, output, misses, miss_count,
+                                     resident_bits, block_size, stream, slot_base);
     });
 }
 

@@ -47,7 +47,8 @@ struct SwapArgs {
     int64_t mi_l, mi_b, mi_o;
     const int32_t* counts;          // [L, B]
     int64_t ct_l, ct_b;
-    int32_t* table;                 // [L, R, T] token -> global slot (0 = not resident)
+    void* table;                    // [L, R, T] token -> global slot (int32) or local slot + 1 (int16); 0 = not resident
+    int32_t table16;
     int64_t tb_l, tb_r, tb_t, table_cols;
     int32_t* bits;                  // [L, R, ceil(T/32)] residency bitmap (may be null)
     int64_t bt_l, bt_r, bt_w;
@@ -73,6 +74,15 @@ __device__ __forceinline__ int64_t lane_position(const SwapArgs& a, const void* 
                                    : static_cast<int64_t>(static_cast<const int32_t*>(topk_row)[b * a.topk_sk]);
     const uint32_t offset = a.block_size == 1 ? 0u : lane - b * a.block_size;
     return block * a.block_size + offset;
+}
+
+// Writes a token -> slot table entry (int32 global slot or int16 local slot + 1).
+__device__ __forceinline__ void set_entry(const SwapArgs& a, int64_t offset, int32_t value) {
+    if (a.table16) {
+        static_cast<int16_t*>(a.table)[offset] = static_cast<int16_t>(value);
+    } else {
+        static_cast<int32_t*>(a.table)[offset] = value;
+    }
 }
 
 __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
@@ -106,7 +116,7 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
     }
     const int64_t stamp_base = step * 2 * W;
     int32_t* slots = a.slots + l * a.sl_l + b * a.sl_b;
-    int32_t* table = a.table + l * a.tb_l + req * a.tb_r;
+    const int64_t table_row = l * a.tb_l + req * a.tb_r;   // element offset of this (layer, request) row
     int32_t* slot_token = a.slot_token + l * a.st_l + req * a.st_r;
     int32_t* stamps = a.stamps + l * a.sp_l + req * a.sp_r;
     const void* topk_row = a.topk64
@@ -169,13 +179,13 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
             }
             const int32_t old = slot_token[victim * a.st_c];
             if (old >= 0 && old < a.table_cols) {
-                table[old * a.tb_t] = 0;
+                set_entry(a, table_row + old * a.tb_t, 0);
                 if (bits != nullptr) {
                     atomicAnd(reinterpret_cast<unsigned int*>(bits + (old >> 5) * a.bt_w), ~(1u << (old & 31)));
                 }
             }
             const int32_t global = static_cast<int32_t>(base + victim);
-            table[token * a.tb_t] = global;
+            set_entry(a, table_row + token * a.tb_t, a.table16 ? static_cast<int32_t>(victim + 1) : global);
             if (bits != nullptr) {
                 atomicOr(reinterpret_cast<unsigned int*>(bits + (token >> 5) * a.bt_w), 1u << (token & 31));
             }
@@ -244,7 +254,9 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
     need_dim(counts, 1, B, "miss_count");
     for (const auto* t : {&table, &slot_token, &stamps}) {
         need_ndim(*t, 3, "table/slot_token/stamps");
-        need_i32(*t, "table/slot_token/stamps");
+        if (t != &table || table.dtype != EKV_INT16) {
+            need_i32(*t, "table/slot_token/stamps");
+        }
         need_dim(*t, 0, L, "table/slot_token/stamps");
     }
     const int64_t R = table.shape[1], T = table.shape[2], C = slot_token.shape[2];
@@ -254,6 +266,7 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
     if (C < 1 || C > kMaxCapacity) {
         throw std::invalid_argument("capacity must be 1.." + std::to_string(kMaxCapacity));
     }
+    static_assert(kMaxCapacity < 32768, "int16 tables hold local slot + 1");
     if (W > C) {
         throw std::invalid_argument("lanes per row exceed the hot capacity");
     }
@@ -318,7 +331,8 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
     a.mi_l = misses.stride[0], a.mi_b = misses.stride[1], a.mi_o = misses.stride[2];
     a.counts = static_cast<const int32_t*>(counts.data);
     a.ct_l = counts.stride[0], a.ct_b = counts.stride[1];
-    a.table = static_cast<int32_t*>(table.data);
+    a.table = table.data;
+    a.table16 = table.dtype == EKV_INT16;
     a.tb_l = table.stride[0], a.tb_r = table.stride[1], a.tb_t = table.stride[2], a.table_cols = T;
     if (bits_p != nullptr) {
         a.bits = static_cast<int32_t*>(bits_p->data);

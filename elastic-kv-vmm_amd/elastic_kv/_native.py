@@ -63,6 +63,7 @@ _SIGNATURES = {
     "ekv_abi_version": ([], ct.c_int),
     "ekv_resolve_resident": ([_P_TENSOR] * 9 + [ct.c_int64, ct.c_void_p], ct.c_int),
     "ekv_resolve_resident_bits": ([_P_TENSOR] * 9 + [ct.c_int64, ct.c_void_p], ct.c_int),
+    "ekv_resolve_resident_local": ([_P_TENSOR] * 10 + [ct.c_int64, ct.c_void_p], ct.c_int),
     "ekv_residency_bits": ([_P_TENSOR, _P_TENSOR, ct.c_void_p], ct.c_int),
     "ekv_gather_rows": ([_P_TENSOR] * 7 + [ct.c_int64, ct.c_int64, ct.c_int, ct.c_void_p], ct.c_int),
     "ekv_gather_kv": ([ct.POINTER(EkvPlanes), _P_TENSOR, ct.POINTER(EkvKvRows), ct.c_int64, ct.c_void_p],

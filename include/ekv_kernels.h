@@ -115,8 +115,27 @@ int ekv_resolve_resident_bits(const ekv_tensor* topk, const ekv_tensor* table,
                               void* stream);
 
 /*
+ * ekv_resolve_resident (single level) over an int16 table of local slots:
+ * a lane whose entry v = table[.., rows[r], pos] is >= 1 gets slot
+ * slot_base[rows[r]] + v - 1, a lane with v <= 0 gets 0 (not resident);
+ * invalid lanes get -1 and the miss list is as in ekv_resolve_resident.
+ *   table [R, T] or [L, R, T] int16; slot_base [R] int32/int64;
+ *   resident_bits as in ekv_resolve_resident_bits, or NULL.
+ * Half the table bytes of the int32 global-slot form for hot buffers of up to
+ * 32767 slots per request (ekv_swap_in maintains either form).
+ * No reference counterpart: an acceleration of ekv_resolve_resident
+ * (adaptive_sparse/resident_lookup.py:29-40 semantics are unchanged).
+ */
+int ekv_resolve_resident_local(const ekv_tensor* topk, const ekv_tensor* table,
+                               const ekv_tensor* slot_base, const ekv_tensor* resident_bits,
+                               const ekv_tensor* rows, const ekv_tensor* lengths,
+                               const ekv_tensor* selected, const ekv_tensor* output,
+                               const ekv_tensor* misses, const ekv_tensor* miss_count,
+                               int64_t block_size, void* stream);
+
+/*
  * resident_bits[.., q, w] bit j = (table[.., q, 32w + j] != 0) for every
- * position of the table; bits past T in the last word are 0.
+ * position of the table (int16, int32 or int64); bits past T in the last word are 0.
  * No reference counterpart (maintenance of the bitmap above).
  */
 int ekv_residency_bits(const ekv_tensor* table, const ekv_tensor* resident_bits,
@@ -176,7 +195,8 @@ int ekv_scatter_kv(const ekv_planes* planes, const ekv_tensor* slots,
  *   topk [L, B, K] + block_size, rows [B], selected [S]: the lookup's inputs
  *   slots [L, B, W] int32: the lookup's output; miss lanes are patched in place
  *   misses [L, B, W], miss_count [L, B] int32: the lookup's miss list
- *   table [L, R, T] int32: token -> global slot (0 = not resident), updated
+ *   table [L, R, T] int32: token -> global slot (0 = not resident), or int16:
+ *   token -> local slot + 1 (the form of ekv_resolve_resident_local), updated
  *   resident_bits [L, R, >= ceil(T/32)] int32 or NULL: kept equal to table != 0
  *   slot_token [L, R, C] int32 (-1 = empty), stamps [L, R, C] int32: LRU state
  *   slot_base [R]: global slot of local slot 0 of each request's hot buffer

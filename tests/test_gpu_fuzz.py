@@ -7,7 +7,7 @@ vector widths, plane strides and zero_below from a seed, including request
 rows outside the table and selection entries outside the batch. The cases are small
 (the oracle runs in milliseconds) and together cover the kernels' branches:
 the recent-window staging, the bitmap staged in LDS or read per lane, the
-dense and strided addressing, every vector width of the copy engine, and
+int16 local-slot tables, the dense and strided addressing, every vector width of the copy engine, and
 large rows cut into segments.
 """
 
@@ -48,6 +48,7 @@ def test_lookup_random_configurations(gpu, coracle, seed):
     layered = bool(rng.random() < 0.5)
     mapped = bool(rng.random() < 0.35)
     use_bits = (not mapped) and bool(rng.random() < 0.6)
+    local = (not mapped) and bool(rng.random() < 0.3)     # int16 table of local slots + per-request bases
     compact = bool(rng.random() < 0.8)
     strided = {name: bool(rng.random() < 0.25) for name in ("topk", "table", "output")}
     topk_dtype, table_dtype, map_dtype = (INDEX_DTYPES[int(rng.integers(2))] for _ in range(3))
@@ -72,6 +73,15 @@ def test_lookup_random_configurations(gpu, coracle, seed):
     else:
         table = rng.integers(1, 1 << 20, size=shape)
         table[rng.random(shape) < 0.4] = 0
+    slot_base = None
+    if local:
+        local_table = rng.integers(1, 1 << 15, size=shape)
+        local_table[rng.random(shape) < 0.4] = 0
+        local_table[rng.random(shape) < 0.02] = -int(rng.integers(1, 1 << 15))   # negative: not resident
+        slot_base = rng.integers(1, 1 << 20, size=rrows)
+        req_axis = 1 if layered else 0
+        bases = np.expand_dims(slot_base, tuple(a for a in range(len(shape)) if a != req_axis))
+        table = np.where(local_table > 0, bases + local_table - 1, 0)          # the oracle's global form
     selected = rng.permutation(batch)[: int(rng.integers(1, batch + 1))]
     if rng.random() < 0.2:                   # selection entries outside the batch are skipped
         selected = np.concatenate([selected, [-1, batch]])
@@ -79,7 +89,7 @@ def test_lookup_random_configurations(gpu, coracle, seed):
     want, want_misses, want_counts = coracle.resolve_resident(topk, table, mapping, rows, lengths, selected, bs,
                                                               initial, with_misses=True)
 
-    table_d = on_gpu(table, table_dtype, gpu, strided["table"])
+    table_d = on_gpu(local_table if local else table, torch.int16 if local else table_dtype, gpu, strided["table"])
     bits = build_residency_bits(table_d) if use_bits else None
     output = on_gpu(initial, torch.int32, gpu, strided["output"])
     misses = torch.full((layers, batch, width), -5, dtype=torch.int32, device=gpu) if compact else None
@@ -88,8 +98,10 @@ def test_lookup_random_configurations(gpu, coracle, seed):
                      None if mapping is None else torch.tensor(mapping, dtype=map_dtype, device=gpu),
                      torch.tensor(rows, device=gpu), torch.tensor(lengths, dtype=torch.int32, device=gpu),
                      torch.tensor(selected, device=gpu), output, bs, misses=misses, miss_count=counts,
-                     resident_bits=bits)
-    assert np.array_equal(output.cpu().numpy(), want), (seed, layers, batch, bs, k, cols, layered, mapped, use_bits)
+                     resident_bits=bits,
+                     slot_base=None if slot_base is None else torch.tensor(slot_base, device=gpu))
+    assert np.array_equal(output.cpu().numpy(), want), (seed, layers, batch, bs, k, cols, layered, mapped, use_bits,
+                                                        local)
     if compact:
         got_counts, got_misses = counts.cpu().numpy(), misses.cpu().numpy()
         for layer in range(layers):

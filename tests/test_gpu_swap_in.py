@@ -307,3 +307,47 @@ def test_whole_decode_step_replays_from_one_graph(gpu):
     finally:
         torch.cuda.synchronize()
         arena.close()
+
+
+def test_local_slot_tables_follow_the_global_slot_stream(gpu):
+    # Two hot-buffer sets, one with int32 global-slot tables and one with int16
+    # local-slot tables, see the same Top-K stream over rows long enough for the
+    # lookup's window staging. Every slot, miss list, promotion and LRU state must
+    # be the same, and the int16 table must be the local form of the int32 one.
+    L, R, T, C, K = 2, 3, 5000, 600, 512
+    rng = np.random.default_rng(88)
+    base = torch.tensor([1, 700, 1500], dtype=torch.int64, device=gpu)
+    wide = HotBuffers(L, R, T, C, gpu, slot_base=base)
+    narrow = HotBuffers(L, R, T, C, gpu, slot_base=base, table_dtype=torch.int16)
+    recent = torch.arange(T - 300, T).expand(L, R, 300)
+    local = torch.stack([torch.stack([torch.tensor(rng.permutation(C)[:300]) for _ in range(R)]) for _ in range(L)])
+    for buffers in (wide, narrow):
+        buffers.install(recent, local)
+    rows = torch.arange(R, device=gpu)
+    lengths = torch.tensor([T, T - 7, T - 130], dtype=torch.int32, device=gpu)
+    host_table = torch.arange(R * T, dtype=torch.int32, device=gpu).reshape(R, T)
+    for step in range(5):
+        topk = torch.tensor(np.stack([rng.permutation(np.concatenate([
+            rng.choice(np.arange(T - 1500, T - 130), 400, replace=False),
+            rng.choice(np.arange(0, T - 1500), 112, replace=False)])) for _ in range(L * R)]).reshape(L, R, K),
+            dtype=torch.int32, device=gpu)
+        results = []
+        for buffers in (wide, narrow):
+            slots = torch.empty((L, R, K), dtype=torch.int32, device=gpu)
+            misses = torch.full((L, R, K), -1, dtype=torch.int32, device=gpu)
+            counts = torch.empty((L, R), dtype=torch.int32, device=gpu)
+            resolve_resident(topk, buffers.table, None, rows, lengths, rows, slots, 1, misses=misses,
+                             miss_count=counts, resident_bits=buffers.bits,
+                             slot_base=buffers.slot_base if buffers.table.dtype == torch.int16 else None)
+            looked_up = slots.clone()
+            src = torch.full((L, R, K), -9, dtype=torch.int32, device=gpu)
+            dst = torch.full((L, R, K), -9, dtype=torch.int32, device=gpu)
+            swap_in(topk, 1, rows, rows, slots, misses, counts, buffers, host_table, src, dst)
+            results.append((looked_up.cpu(), counts.cpu(), misses.cpu(), slots.cpu(), src.cpu(), dst.cpu(),
+                            buffers.slot_token.cpu(), buffers.stamps.cpu(), buffers.bits.cpu()))
+        for a, b in zip(*results):
+            assert torch.equal(a, b), step
+        table32, table16 = wide.table.cpu().long(), narrow.table.cpu().long()
+        local_form = torch.where(table32 > 0, table32 - base.cpu().view(1, R, 1) + 1, torch.zeros_like(table32))
+        assert torch.equal(table16, local_form), step
+        assert int(results[0][1].sum()) > 0 and int((results[0][0] > 0).sum()) > 0   # hits and misses both occur
