@@ -863,7 +863,8 @@ def run_composite(torch, args, device):
                            kv_stride=host_plane, row_stride=row_bytes, row_bytes=row_bytes, rows=HOST_ROWS, owner=arena)
     host_table = ((torch.arange(R, device=device).view(R, 1) * T + torch.arange(T, device=device).view(1, T))
                   % HOST_ROWS).to(torch.int32)
-    buffers = HotBuffers(L, R, T, C, device, step_counter=True)   # graph-replayable swap-in
+    # Graph-replayable swap-in; int16 local-slot table, as the decode-read lookup uses.
+    buffers = HotBuffers(L, R, T, C, device, step_counter=True, table_dtype=torch.int16)
     recent = (lengths.view(1, R, 1) - C + torch.arange(C, device=device).view(1, 1, C)).expand(L, R, C)
     local = torch.rand((L, R, C), generator=gen, device=device).argsort(-1)
     buffers.install(recent, local)
@@ -917,7 +918,7 @@ def run_composite(torch, args, device):
 
     def lookup():
         resolve_resident(topk, buffers.table, None, rows, lengths32, rows, slots, 1, misses=misses,
-                         miss_count=counts, resident_bits=buffers.bits)
+                         miss_count=counts, resident_bits=buffers.bits, slot_base=buffers.slot_base)
 
     def swap():
         swap_in(topk, 1, rows, rows, slots, misses, counts, buffers, host_table, promote_src, promote_dst)
