@@ -52,9 +52,9 @@ namespace {
 //   EKV_LOOKUP_STAGE_BITS    stage bitmap rows of up to
 //       EKV_LOOKUP_STAGED_BIT_WORDS words in LDS (else lanes read their word);
 //   EKV_LOOKUP_DENSE         32-bit byte-offset addressing for unit-stride rows;
-//   EKV_LOOKUP_STREAMING     non-temporal Top-K loads and slot / miss stores
-//       (read or written once): 3-5 % faster on the 60-layer shapes, and only
-//       with both (table lines, which lanes of a row share, keep the cache).
+//   EKV_LOOKUP_STREAMING     non-temporal Top-K loads and slot stores (read or
+//       written once): 3-5 % faster on the 60-layer shapes, and only with
+//       both (table lines, which lanes of a row share, keep the cache).
 #ifndef EKV_LOOKUP_THREADS
 #define EKV_LOOKUP_THREADS 256
 #endif
@@ -111,8 +111,8 @@ struct LookupArgs {
     FastDiv block_div;
 };
 
-// Loads and stores of data touched once per launch (Top-K indices, slots,
-// miss lists), with the non-temporal hint when EKV_LOOKUP_STREAMING is set.
+// Loads and stores of data touched once per launch (Top-K indices, slots),
+// with the non-temporal hint when EKV_LOOKUP_STREAMING is set.
 template <typename T>
 __device__ __forceinline__ T stream_load(const T* p) {
 #if EKV_LOOKUP_STREAMING
@@ -324,8 +324,10 @@ __device__ __forceinline__ int32_t emit(const LookupArgs& a, int32_t* out, int32
             const bool miss = o < a.width && slot[i] == 0;
             const uint64_t mask = __ballot(miss);
             if (miss) {
-                stream_store(static_cast<int32_t>(o),
-                             element<kDense>(misses, a.miss_so, static_cast<uint32_t>(rank) + lanes_below(mask)));
+                // Cached: a row's miss list starts and ends mid-line, and
+                // non-temporal stores write such partial lines as whole bursts.
+                *element<kDense>(misses, a.miss_so, static_cast<uint32_t>(rank) + lanes_below(mask)) =
+                    static_cast<int32_t>(o);
             }
             rank += __popcll(mask);
         }
