@@ -218,7 +218,17 @@ def test_rebase_mid_stream_changes_no_decision(gpu):
     assert rebased.step == 3 and plain.step == 6
 
 
-def test_whole_decode_step_replays_from_one_graph(gpu):
+def global_table(buffers):
+    """The token -> global slot table of a HotBuffers, whichever form it keeps."""
+    table = buffers.table.cpu().numpy().astype(np.int64)
+    if buffers.table.dtype == torch.int16:
+        base = buffers.slot_base.cpu().numpy().reshape(1, -1, 1)
+        table = np.where(table > 0, base + table - 1, 0)
+    return table
+
+
+@pytest.mark.parametrize("table_dtype", [torch.int32, torch.int16])
+def test_whole_decode_step_replays_from_one_graph(gpu, table_dtype):
     # Lookup -> swap-in (device step counter) -> promote from pinned host -> gather,
     # captured once and replayed for five steps with new Top-K contents. After every
     # replay the LRU state equals the oracle's at that step and every gathered row is
@@ -227,7 +237,8 @@ def test_whole_decode_step_replays_from_one_graph(gpu):
     # promotions and zero rows, and leave its hot buffer untouched.
     L, R, T, K, row_bytes, capacity = 2, 3, 300, 32, 64, 64
     rng = np.random.default_rng(21)
-    buffers = HotBuffers(L, R, T, capacity, gpu, step_counter=True)
+    buffers = HotBuffers(L, R, T, capacity, gpu, step_counter=True, table_dtype=table_dtype)
+    local = buffers.slot_base if table_dtype == torch.int16 else None
     host_table = torch.arange(R * T, dtype=torch.int32).reshape(R, T)
     host_table_d = host_table.to(gpu)
     plane = R * T * row_bytes
@@ -254,12 +265,12 @@ def test_whole_decode_step_replays_from_one_graph(gpu):
 
         def decode_step():
             resolve_resident(topk_d, buffers.table, None, rows, lengths, rows, slots, 1, misses=misses,
-                             miss_count=counts, resident_bits=buffers.bits)
+                             miss_count=counts, resident_bits=buffers.bits, slot_base=local)
             swap_in(topk_d, 1, rows, rows, slots, misses, counts, buffers, host_table_d, promote_src, promote_dst)
             move_kv(host_planes, promote_src, pool_planes, promote_dst, counts)
             gather_kv(pool_planes, slots, out)
 
-        state = {"table": buffers.table.cpu().numpy(), "slot_token": buffers.slot_token.cpu().numpy(),
+        state = {"table": global_table(buffers), "slot_token": buffers.slot_token.cpu().numpy(),
                  "stamps": buffers.stamps.cpu().numpy()}
         graph = None
         for step in range(6):
@@ -291,7 +302,7 @@ def test_whole_decode_step_replays_from_one_graph(gpu):
                                 state["table"], state["slot_token"], state["stamps"],
                                 buffers.slot_base.cpu().numpy(), host_table.numpy())
             assert np.array_equal(slots.cpu().numpy(), state["slots"]), step
-            assert np.array_equal(buffers.table.cpu().numpy(), state["table"]), step
+            assert np.array_equal(global_table(buffers), state["table"]), step
             assert np.array_equal(buffers.stamps.cpu().numpy(), state["stamps"]), step
             got = out.cpu().numpy()
             for layer in range(L):
