@@ -33,10 +33,12 @@
 //      block) is classified once, by its first lane (atomicMin), and its
 //      other lanes reuse that lane's location, so the hot buffer never holds
 //      a token twice;
-//   3. ranks in selection order (output position, hit rank, miss rank) are
-//      wave ballot + mbcnt prefix sums with one LDS exchange per chunk;
-//   4. prefix sums over the old LRU order give each slot's place in the new
-//      order and the victims (empty slots first, then untouched slots);
+//   3. ranks in selection order (output position, hit rank, miss rank): each
+//      thread counts a contiguous run of lanes, one workgroup scan (wave64
+//      shuffles + one LDS exchange) turns the counts into ranks;
+//   4. the same scan over contiguous runs of the old LRU order gives each
+//      slot's place in the new order and the victims (empty slots first, then
+//      untouched slots);
 //   5. the misses' rows are copied from mapped pinned host memory, 16 bytes
 //      per lane when rows and bases allow.
 // Locations outside the device buffer are reported as -1 and never written.
@@ -115,19 +117,26 @@ struct Lds {
     int32_t* scratch;     // [3 * kWaves + 4]
 };
 
-// Exclusive ranks of N flags over the workgroup's threads in thread order,
-// and their totals. Every thread must call it (two barriers).
+// Exclusive prefix sums of N per-thread counts over the workgroup's threads
+// in thread order, and their totals: a wave64 shuffle scan, then one LDS
+// exchange of the wave totals. Every thread must call it (two barriers).
 template <int N>
-__device__ __forceinline__ void rank_flags(const bool (&flag)[N], int32_t (&rank)[N], int32_t (&total)[N],
-                                           int32_t* scratch) {
+__device__ __forceinline__ void scan_counts(const int32_t (&count)[N], int32_t (&prefix)[N], int32_t (&total)[N],
+                                            int32_t* scratch) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    uint64_t mask[N];
+    int32_t inclusive[N];
 #pragma unroll
     for (int k = 0; k < N; ++k) {
-        mask[k] = __ballot(flag[k]);
-        if (lane == 0) {
-            scratch[k * kWaves + wave] = __popcll(mask[k]);
+        int32_t v = count[k];
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int32_t t = __shfl_up(v, d, 64);
+            v += lane >= d ? t : 0;
+        }
+        inclusive[k] = v;
+        if (lane == 63) {
+            scratch[k * kWaves + wave] = v;
         }
     }
     __syncthreads();
@@ -140,7 +149,7 @@ __device__ __forceinline__ void rank_flags(const bool (&flag)[N], int32_t (&rank
             before += w < wave ? c : 0;
             all += c;
         }
-        rank[k] = before + static_cast<int32_t>(lanes_below(mask[k]));
+        prefix[k] = before + inclusive[k] - count[k];
         total[k] = all;
     }
     __syncthreads();  // scratch is rewritten by the next call
@@ -391,94 +400,98 @@ __global__ __launch_bounds__(kThreads) void hisparse_swap_kernel(const HsArgs a)
     }
     __syncthreads();
 
-    // 3. First lanes of each token, host rows, ranks in selection order;
-    //    outputs of the newest token and of hits.
-    int32_t base[3] = {0, 0, 0};  // selected, first hits, first misses so far
-    for (int64_t chunk = 0; chunk < W; chunk += kThreads) {
-        const int64_t o = chunk + threadIdx.x;
-        const uint8_t kind = o < W ? s.lane_kind[o] : kInvalid;
-        const int32_t aux = o < W ? s.lane_aux[o] : -1;
-        const int32_t value = o < W ? s.lane_val[o] : -1;   // device row of a hit, host row of a miss
-        const bool first_hit = kind == kHit && s.first_touch[aux] == o;
-        const bool first_miss = kind == kMiss && s.hash[aux] == H + o;
-        const bool flags[3] = {kind != kInvalid, first_hit, first_miss};
-        int32_t rank[3], total[3];
-        rank_flags<3>(flags, rank, total, s.scratch);
-        if (o < W) {
-            const int32_t pos = base[0] + rank[0];
+    // 3. First lanes of each token, ranks in selection order, outputs of the
+    //    newest token and of hits. A thread takes a contiguous run of lanes,
+    //    counts, scans the counts once over the workgroup, then walks its run.
+    int32_t selected, hits, misses;
+    {
+        const int64_t per = (W + kThreads - 1) / kThreads;
+        const int64_t begin = threadIdx.x * per;
+        const int64_t end = begin + per < W ? begin + per : W;
+        auto first_hit = [&](int64_t o) { return s.lane_kind[o] == kHit && s.first_touch[s.lane_aux[o]] == o; };
+        auto first_miss = [&](int64_t o) { return s.lane_kind[o] == kMiss && s.hash[s.lane_aux[o]] == H + o; };
+        int32_t count[3] = {0, 0, 0};   // selected, first hits, first misses
+        for (int64_t o = begin; o < end; ++o) {
+            count[0] += s.lane_kind[o] != kInvalid;
+            count[1] += first_hit(o);
+            count[2] += first_miss(o);
+        }
+        int32_t prefix[3], total[3];
+        scan_counts<3>(count, prefix, total, s.scratch);
+        int32_t pos = prefix[0], hit_rank = prefix[1], miss_rank = prefix[2];
+        for (int64_t o = begin; o < end; ++o) {
+            const uint8_t kind = s.lane_kind[o];
+            const int32_t aux = s.lane_aux[o];
+            const int32_t value = s.lane_val[o];   // device row of a hit, host row of a miss
             s.lane_pos[o] = kind != kInvalid ? pos : -1;
             if (kind == kNewest) {
                 out[pos * a.out_so] = static_cast<int32_t>(reserved);
             } else if (kind == kHit) {
                 out[pos * a.out_so] = value;
             }
-            if (first_hit) {
-                s.hit_rank[aux] = static_cast<int16_t>(base[1] + rank[1]);
+            pos += kind != kInvalid;
+            if (first_hit(o)) {
+                s.hit_rank[aux] = static_cast<int16_t>(hit_rank++);
             }
-            if (first_miss) {
-                const int32_t m = base[2] + rank[2];
-                s.lane_rank[o] = static_cast<int16_t>(m);
-                s.miss_lane[m] = static_cast<int16_t>(o);
-                s.miss_host[m] = value;
+            if (first_miss(o)) {
+                s.lane_rank[o] = static_cast<int16_t>(miss_rank);
+                s.miss_lane[miss_rank] = static_cast<int16_t>(o);
+                s.miss_host[miss_rank] = value;
+                ++miss_rank;
             }
         }
-#pragma unroll
-        for (int k = 0; k < 3; ++k) {
-            base[k] += total[k];
-        }
+        selected = total[0];
+        hits = total[1];
+        misses = total[2];
     }
-    const int32_t selected = base[0], hits = base[1], misses = base[2];
-    __syncthreads();  // hit_rank and the miss lists were written after the last ranking barrier
+    __syncthreads();  // hit_rank and the miss lists are read by other threads below
 
-    // 4. New LRU order and victims, when the row touched the hot buffer.
+    // 4. New LRU order and victims, when the row touched the hot buffer. A
+    //    thread takes a contiguous run of the old order: counts of its empty
+    //    and untouched slots, one scan, then the walk that places them.
     if (hits + misses > 0) {
-        // Counts of empty and untouched slots in the old order.
-        int32_t counted[2] = {0, 0};
-        for (int64_t chunk = 0; chunk < H; chunk += kThreads) {
-            const int64_t i = chunk + threadIdx.x;
-            const int32_t slot = i < H ? s.order[i] : -1;
-            const bool listed = slot >= 0;
-            const bool touched = listed && s.hit_rank[slot] >= 0;
-            const bool flags[2] = {listed && !touched && s.tok[slot] < 0, listed && !touched && s.tok[slot] >= 0};
-            int32_t rank[2], total[2];
-            rank_flags<2>(flags, rank, total, s.scratch);
-            counted[0] += total[0];
-            counted[1] += total[1];
+        const int64_t per = (H + kThreads - 1) / kThreads;
+        const int64_t begin = threadIdx.x * per;
+        const int64_t end = begin + per < H ? begin + per : H;
+        // 0: not listed, 1: touched (hit), 2: empty, 3: untouched occupied.
+        auto class_of = [&](int32_t slot) {
+            return slot < 0 ? 0 : (s.hit_rank[slot] >= 0 ? 1 : (s.tok[slot] < 0 ? 2 : 3));
+        };
+        int32_t count[2] = {0, 0};   // empty, untouched
+        for (int64_t i = begin; i < end; ++i) {
+            const int c = class_of(s.order[i]);
+            count[0] += c == 2;
+            count[1] += c == 3;
         }
-        const int32_t empty = counted[0], untouched = counted[1];
+        int32_t prefix[2], total[2];
+        scan_counts<2>(count, prefix, total, s.scratch);
+        const int32_t empty = total[0], untouched = total[1];
         const int32_t taken_empty = misses < empty ? misses : empty;
         const int32_t taken_untouched = misses - taken_empty < untouched ? misses - taken_empty : untouched;
         const int32_t kept_empty = empty - taken_empty, kept_untouched = untouched - taken_untouched;
         const int32_t hit_base = kept_empty + kept_untouched, miss_base = hit_base + hits;
-        int32_t seen[2] = {0, 0};
-        for (int64_t chunk = 0; chunk < H; chunk += kThreads) {
-            const int64_t i = chunk + threadIdx.x;
-            const int32_t slot = i < H ? s.order[i] : -1;
-            const bool listed = slot >= 0;
-            const bool touched = listed && s.hit_rank[slot] >= 0;
-            const bool is_empty = listed && !touched && s.tok[slot] < 0;
-            const bool is_untouched = listed && !touched && s.tok[slot] >= 0;
-            const bool flags[2] = {is_empty, is_untouched};
-            int32_t rank[2], total[2];
-            rank_flags<2>(flags, rank, total, s.scratch);
+        int32_t e = prefix[0], u = prefix[1];
+        for (int64_t i = begin; i < end; ++i) {
+            const int32_t slot = s.order[i];
+            const int c = class_of(slot);
             int64_t pos = -1;
-            if (is_empty) {
-                const int32_t e = seen[0] + rank[0];
+            if (c == 2) {
                 if (e < taken_empty) {
                     s.victim[e] = static_cast<int16_t>(slot);
                     pos = miss_base + e;
                 } else {
                     pos = e - taken_empty;
                 }
-            } else if (is_untouched) {
-                const int32_t u = seen[1] + rank[1];
+                ++e;
+            } else if (c == 3) {
                 if (u < taken_untouched) {
                     s.victim[taken_empty + u] = static_cast<int16_t>(slot);
                     pos = miss_base + taken_empty + u;
                 } else {
                     pos = kept_empty + (u - taken_untouched);
                 }
-            } else if (touched) {
+                ++u;
+            } else if (c == 1) {
                 pos = hit_base + s.hit_rank[slot];
             }
             if (pos >= 0 && pos < H) {
@@ -488,10 +501,8 @@ __global__ __launch_bounds__(kThreads) void hisparse_swap_kernel(const HsArgs a)
                     static_cast<int16_t*>(a.lru)[r * a.lru_sr + pos * a.lru_ss] = static_cast<int16_t>(slot);
                 }
             }
-            seen[0] += total[0];
-            seen[1] += total[1];
         }
-        __syncthreads();  // the victims were written after the last ranking barrier
+        __syncthreads();  // the victims are read by other threads below
 
         // 5. Misses take their victims: token table, locations.
         {
