@@ -284,10 +284,15 @@ def run_decode_read(torch, args, device):
     counts = torch.empty((L, R), dtype=torch.int32, device=device)
     output = torch.empty((R, L, 2, K, 256), dtype=torch.bfloat16, device=device)
     bits = build_residency_bits(table)          # maintained with the table; built once here
-    # The same residency as an int16 table of local slots (request r's hot slots start at r * C + 1).
+    # The same residency as an int16 table of local slots (request r's hot slots start at r * C + 1),
+    # which holds hot buffers of up to 32767 slots; larger ones keep the int32 form.
     slot_base = torch.arange(R, device=device, dtype=torch.int64) * C + 1
-    table16 = torch.where(table > 0, table - slot_base.view(1, R, 1).to(torch.int32) + 1, 0).to(torch.int16)
-    bits16 = build_residency_bits(table16)
+    local_form = C < 1 << 15
+    if local_form:
+        table16 = torch.where(table > 0, table - slot_base.view(1, R, 1).to(torch.int32) + 1, 0).to(torch.int16)
+        bits16 = build_residency_bits(table16)
+    else:
+        table16, bits16, slot_base = table, bits, None
 
     def lookup_plain():
         resolve_resident(topk, table, None, rows, lengths, rows, slots, 1, misses=misses, miss_count=counts)
@@ -405,7 +410,8 @@ def run_decode_read(torch, args, device):
              "lookup_us_per_layer_launch_graph": round(per_layer_graph_ms * 1e3 / L, 2),
              "lookup_us_back_to_back_int32_table": round(lookup_global_ms * 1e3, 2),
              "lookup_us_without_bitmap": round(plain_phase["lookup"] * 1e3, 2),
-             "lookup_table": "int16 local slots + slot_base, residency bitmap",
+             "lookup_table": ("int16 local slots + slot_base, residency bitmap" if local_form
+                              else "int32 global slots, residency bitmap"),
              "lookup_variants_identical": same,
              "engine_gbs_same_shapes": ceilings,
              "event_spread": step_spread,
