@@ -320,6 +320,142 @@ def test_chunk_aware_plan_keeps_pages_sharing_chunks():
     assert retained == (1, 2) and released == (4, 3)
 
 
+# ------------------------------------------------------------------ transactions
+#
+# The order of side effects in the prepare / commit / abort split
+# (reference adaptive_sparse/migration.py:67-288): a demotion unpublishes the
+# mapping before any page is released and trims before it publishes the
+# request as host-backed; a promotion frees the host copy and the hot pages,
+# publishes the new mapping, trims, then publishes the request as resident.
+# A failed byte move gives back whatever the prepare took.
+
+
+class _FakePool:
+    def __init__(self, log, backed=1000):
+        self.log = log
+        self.pages = None
+        self.backing = SimpleNamespace(backed_bytes=backed)
+        self.free = SimpleNamespace(peek=lambda n: [(50, 50 + n)])
+
+    def release(self, pages):
+        self.log.append(("release", tuple(pages)))
+
+    def allocate(self, pages):
+        self.log.append(("allocate", tuple(pages)))
+        self.backing.backed_bytes += 10 * len(pages)
+
+    def trim(self):
+        self.log.append(("trim",))
+        return 0
+
+
+class _FakeEngine:
+    def __init__(self, log, fail=None):
+        self.log, self.fail = log, fail
+
+    def demote(self, pages):
+        if self.fail == "demote":
+            raise OSError("copy failed")
+        self.log.append(("demote", tuple(pages)))
+        return SimpleNamespace(pages=list(pages))
+
+    def promote(self, host, destinations):
+        if self.fail == "promote":
+            raise OSError("copy failed")
+        self.log.append(("promote", tuple(destinations)))
+
+    def release_host(self, host):
+        self.log.append(("release_host", tuple(host.pages)))
+
+
+def _coordinator(log, fail=None, keep=2):
+    import torch
+
+    from adaptive_sparse.migration import MigrationCoordinator
+
+    mapping = torch.zeros(16, dtype=torch.int64)
+    mapping[4:9] = torch.tensor([11, 12, 13, 14, 15])
+    return MigrationCoordinator(_FakePool(log), _FakeEngine(log, fail), mapping, keep_pages=keep)
+
+
+def test_transactions_order_side_effects_and_clean_up_failures(monkeypatch):
+    import torch
+
+    from adaptive_sparse.migration import (MigrationRequest, abort_promote, commit_demote, commit_promote,
+                                           prepare_demote, prepare_promote)
+
+    monkeypatch.delenv("EKV_CHUNK_AWARE_RETENTION", raising=False)
+    log = []
+    coordinator = _coordinator(log)
+    logical = torch.arange(4, 9)
+    request = MigrationRequest(row=3, logical=logical)
+    sync = lambda: log.append(("sync",))
+
+    def publish(kind):
+        # Each publish sees the mapping as the commit left it.
+        return lambda row: log.append((kind, row, tuple(coordinator.mapping[logical].tolist())))
+
+    prepared = prepare_demote(coordinator, request, sync)
+    assert log == [("sync",), ("demote", (11, 12, 13, 14, 15)), ("sync",)]
+    assert prepared.retained_rows == (0, 1) and prepared.released_rows == (2, 3, 4)
+    assert coordinator.mapping[logical].tolist() == [11, 12, 13, 14, 15]   # ownership unchanged by prepare
+    log.clear()
+    assert commit_demote(prepared, publish("host"), sync, trim_quiescent=lambda: log.append(("trim",)) or 30) == 30
+    assert log == [("sync",), ("release", (13, 14, 15)), ("sync",), ("trim",), ("host", 3, (0, 0, 0, 0, 0))]
+    assert coordinator.hot[3] == (11, 12) and coordinator.host_backed[3].pages == [11, 12, 13, 14, 15]
+
+    log.clear()
+    promotion = prepare_promote(coordinator, request, sync)
+    assert log == [("allocate", (50, 51, 52, 53, 54)), ("promote", (50, 51, 52, 53, 54)), ("sync",)]
+    assert coordinator.mapping[logical].tolist() == [0] * 5              # unpublished until commit
+    log.clear()
+    abort_promote(promotion)
+    assert log == [("release", (50, 51, 52, 53, 54)), ("trim",)] and promotion.status == "aborted"
+    with pytest.raises(RuntimeError, match="prepared promotion"):
+        abort_promote(promotion)
+
+    promotion = prepare_promote(coordinator, request, sync, destinations=[7, 6, 5, 4, 3])
+    log.clear()
+    assert commit_promote(promotion, publish("gpu"), sync) == 50            # growth since this prepare: 5 pages
+    assert log == [("release_host", (11, 12, 13, 14, 15)), ("release", (11, 12)), ("sync",), ("trim",),
+                   ("gpu", 3, (7, 6, 5, 4, 3))]
+    assert 3 not in coordinator.hot and 3 not in coordinator.host_backed
+    with pytest.raises(RuntimeError, match="already been resolved"):
+        commit_promote(promotion, publish("gpu"), sync)
+
+
+def test_transactions_reject_bad_state_and_undo_failed_moves(monkeypatch):
+    import torch
+
+    from adaptive_sparse.migration import MigrationRequest, prepare_demote, prepare_promote
+
+    monkeypatch.delenv("EKV_CHUNK_AWARE_RETENTION", raising=False)
+    sync = lambda: None
+    log = []
+    coordinator = _coordinator(log)
+    with pytest.raises(RuntimeError, match="missing physical locations"):
+        prepare_demote(coordinator, MigrationRequest(row=0, logical=torch.arange(3, 6)), sync)
+    coordinator.mapping[5] = 11
+    with pytest.raises(RuntimeError, match="reuses a physical page"):
+        prepare_demote(coordinator, MigrationRequest(row=0, logical=torch.arange(4, 9)), sync)
+    with pytest.raises(RuntimeError, match="missing committed host KV"):
+        prepare_promote(coordinator, MigrationRequest(row=0, logical=torch.arange(4, 9)), sync)
+
+    log = []
+    coordinator = _coordinator(log, fail="demote")
+    with pytest.raises(OSError):
+        prepare_demote(coordinator, MigrationRequest(row=1, logical=torch.arange(4, 9)), sync)
+    assert log == [] and coordinator.mapping[4:9].tolist() == [11, 12, 13, 14, 15]
+
+    log = []
+    coordinator = _coordinator(log, fail="promote")
+    coordinator.host_backed[2] = SimpleNamespace(pages=[1, 2])
+    with pytest.raises(OSError):
+        prepare_promote(coordinator, MigrationRequest(row=2, logical=torch.arange(0, 2)), sync)
+    assert log == [("allocate", (50, 51)), ("release", (50, 51)), ("trim",)]
+    assert 2 in coordinator.host_backed                                     # the host copy survives
+
+
 # ------------------------------------------------------------------ estimator
 
 
