@@ -114,6 +114,75 @@ def test_lookup_random_configurations(gpu, coracle, seed):
                     assert got_counts[layer, row] == -5
 
 
+@pytest.mark.parametrize("seed", range(40))
+def test_local_slot_runs_random_configurations(gpu, coracle, seed):
+    # The decode default: int32 Top-K, int16 local-slot table with slot bases,
+    # residency bitmap, block size 1, K a multiple of 8 and 16-byte aligned
+    # rows, which the contiguous 8-lane-run kernel serves. Widths past one
+    # 2048-lane chunk, bitmaps too wide to stage (T > 131072), stray rows and
+    # partial selections; a Top-K view shifted by one element must give the
+    # same answer through the strided kernel.
+    rng = np.random.default_rng(9100 + seed)
+    layers = int(rng.integers(1, 4))
+    batch = int(rng.integers(1, 9))
+    k = 8 * int(rng.integers(1, 700 if seed % 2 == 0 else 257))    # odd seeds: one 2048-lane chunk
+    rrows = int(rng.integers(1, 10))
+    cols = int(rng.integers(1, 7000)) if seed % 8 else int(rng.integers(131_073, 140_000))
+    if seed % 4 == 1:
+        cols = 8 * ((cols + 7) // 8)        # 16-byte aligned table rows
+    layered = bool(rng.random() < 0.7)
+    compact = bool(rng.random() < 0.85)
+    lengths = rng.integers(-2, cols + 5, size=batch)
+    rows = rng.integers(0, rrows, size=batch)
+    stray = rng.random(batch) < 0.1
+    rows[stray] = rng.choice([-1, rrows, rrows + 7], size=int(stray.sum()))
+    topk = rng.integers(-1, cols + 2, size=(layers, batch, k))
+    for r in range(batch):
+        hi = max(1, min(int(lengths[r]), cols))
+        near = rng.random((layers, k)) < 0.7
+        topk[:, r][near] = rng.integers(max(0, hi - 4096), hi + 1, size=(layers, k))[near]
+    shape = (layers, rrows, cols) if layered else (rrows, cols)
+    local_table = rng.integers(1, 1 << 15, size=shape)
+    local_table[rng.random(shape) < 0.5] = 0
+    local_table[rng.random(shape) < 0.02] = -int(rng.integers(1, 1 << 15))
+    slot_base = rng.integers(1, 1 << 20, size=rrows)
+    req_axis = 1 if layered else 0
+    bases = np.expand_dims(slot_base, tuple(a for a in range(len(shape)) if a != req_axis))
+    table = np.where(local_table > 0, bases + local_table - 1, 0)
+    selected = rng.permutation(batch)[: int(rng.integers(1, batch + 1))]
+    if rng.random() < 0.2:
+        selected = np.concatenate([selected, [-1, batch]])
+    initial = np.full((layers, batch, k), -77, np.int32)
+    want, want_misses, want_counts = coracle.resolve_resident(topk, table, None, rows, lengths, selected, 1,
+                                                              initial, with_misses=True)
+    table_d = torch.tensor(local_table, dtype=torch.int16, device=gpu)
+    bits = build_residency_bits(table_d)
+    base_d = torch.tensor(slot_base, device=gpu)
+    topk_aligned = torch.tensor(topk, dtype=torch.int32, device=gpu)
+    topk_shifted = torch.zeros(topk.size + 1, dtype=torch.int32, device=gpu)[1:].view(topk.shape)
+    topk_shifted.copy_(topk_aligned)
+    assert topk_aligned.data_ptr() % 16 == 0 and topk_shifted.data_ptr() % 16 == 4
+    for topk_d in (topk_aligned, topk_shifted):
+        output = torch.tensor(initial, device=gpu)
+        misses = torch.full((layers, batch, k), -5, dtype=torch.int32, device=gpu) if compact else None
+        counts = torch.full((layers, batch), -5, dtype=torch.int32, device=gpu) if compact else None
+        resolve_resident(topk_d, table_d, None, torch.tensor(rows, device=gpu),
+                         torch.tensor(lengths, dtype=torch.int32, device=gpu), torch.tensor(selected, device=gpu),
+                         output, 1, misses=misses, miss_count=counts, resident_bits=bits, slot_base=base_d)
+        case = (seed, layers, batch, k, cols, layered, topk_d.data_ptr() % 16)
+        assert np.array_equal(output.cpu().numpy(), want), case
+        if compact:
+            got_counts, got_misses = counts.cpu().numpy(), misses.cpu().numpy()
+            for layer in range(layers):
+                for row in range(batch):
+                    if row in selected:
+                        c = want_counts[layer, row]
+                        assert got_counts[layer, row] == c, case
+                        assert np.array_equal(got_misses[layer, row, :c], want_misses[layer, row, :c]), case
+                    else:
+                        assert got_counts[layer, row] == -5, case
+
+
 def random_planes(rng, gpu, layers, kv, rows, row_bytes):
     row_stride = row_bytes + int(rng.choice([0, 0, 2, 8, 16, 48]))
     plane = rows * row_stride + int(rng.choice([0, 16, 64, 100]))
