@@ -84,6 +84,20 @@ struct IndexRef {
         return is64 ? static_cast<const int64_t*>(data)[i * stride]
                     : static_cast<int64_t>(static_cast<const int32_t*>(data)[i * stride]);
     }
+
+    // The same value without a branch on the element type: the low word and
+    // the high word (for int32 arrays the element itself again, then replaced
+    // by its sign) are read from in-bounds addresses chosen by selects. For
+    // workgroup-uniform reads in a kernel's prologue, where a branch per index
+    // load would keep consecutive loads from being in flight together.
+    __device__ __forceinline__ int64_t fetch(int64_t i) const {
+        const char* at = static_cast<const char*>(data) + i * stride * (is64 ? 8 : 4);
+        const int32_t lo = *reinterpret_cast<const int32_t*>(at);
+        const int32_t high = *reinterpret_cast<const int32_t*>(at + (is64 ? 4 : 0));
+        const int32_t hi = is64 ? high : (lo >> 31);
+        return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                    static_cast<uint32_t>(lo));
+    }
 #endif
 };
 

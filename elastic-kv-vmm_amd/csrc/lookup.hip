@@ -353,16 +353,16 @@ __device__ __forceinline__ void resolve_single(const LookupArgs& a) {
     // staged bitmap row (when a.bits_staged), indexed by absolute word.
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ int32_t wave_totals[kThreads / 64];
-    const int64_t row = a.selected[blockIdx.x];
+    const int64_t row = a.selected.fetch(blockIdx.x);
     if (row < 0 || row >= a.batch) {
         return;  // uniform over the workgroup
     }
     const int64_t layer = blockIdx.y;
-    const int64_t req = a.rows[row];
-    const int64_t length = a.lengths[row];
+    const int64_t req = a.rows.fetch(row);
+    const int64_t length = a.lengths.fetch(row);
     const bool table_ok = req >= 0 && req < a.table_rows && a.table_cols > 0;  // uniform
     const int64_t req_at = table_ok ? req : 0;
-    const int64_t base = std::is_same_v<TableT, int16_t> && table_ok ? a.slot_base[req] : 0;
+    const int64_t base = std::is_same_v<TableT, int16_t> && table_ok ? a.slot_base.fetch(req) : 0;
     const int64_t bound = length < a.table_cols ? length : a.table_cols;
     const TopkT* topk = static_cast<const TopkT*>(a.topk) + layer * a.topk_sl + row * a.topk_sb;
     const TableT* table = static_cast<const TableT*>(a.table) + layer * a.table_sl + req_at * a.table_sr;
@@ -473,18 +473,32 @@ __device__ __forceinline__ void resolve_local_runs(const LookupArgs& a) {
 #if EKV_LOOKUP_MISS_LDS
     __shared__ int32_t chunk_misses[kChunkLanes];
 #endif
-    const int64_t row = a.selected[blockIdx.x];
+    const int64_t row = a.selected.fetch(blockIdx.x);
     if (row < 0 || row >= a.batch) {
         return;  // uniform over the workgroup
     }
     const int64_t layer = blockIdx.y;
-    const int64_t req = a.rows[row];
-    const int64_t length = a.lengths[row];
+    const int32_t* topk = static_cast<const int32_t*>(a.topk) + layer * a.topk_sl + row * a.topk_sb;
+    // Top-K ids of lanes [chunk + 4t, +4) and [chunk + 1024 + 4t, +4); a thread
+    // past the width re-reads the row's last piece.
+    const auto load_ids = [&](uint32_t chunk, i32x4 (&ids)[2]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t first = chunk + h * kHalf + threadIdx.x * kPiece;
+            ids[h] = stream_load(reinterpret_cast<const i32x4*>(
+                element<true>(topk, 1, first < a.width ? first : a.width - kPiece)));
+        }
+    };
+    // The first chunk's ids depend on the row alone, so they are requested
+    // before the request's length, table row and slot base are read.
+    i32x4 ids[2];
+    load_ids(0, ids);
+    const int64_t req = a.rows.fetch(row);
+    const int64_t length = a.lengths.fetch(row);
     const bool table_ok = req >= 0 && req < a.table_rows && a.table_cols > 0;  // uniform
     const int64_t req_at = table_ok ? req : 0;
-    const int64_t base = table_ok ? a.slot_base[req] : 0;
+    const int64_t base = table_ok ? a.slot_base.fetch(req) : 0;
     const int64_t bound = length < a.table_cols ? length : a.table_cols;
-    const int32_t* topk = static_cast<const int32_t*>(a.topk) + layer * a.topk_sl + row * a.topk_sb;
     const int16_t* table = static_cast<const int16_t*>(a.table) + layer * a.table_sl + req_at * a.table_sr;
     const int32_t* bits_row = a.bits + layer * a.bits_sl + req_at * a.bits_sr;
     const bool bits_in_lds = table_ok && a.bits_staged;  // uniform
@@ -497,11 +511,8 @@ __device__ __forceinline__ void resolve_local_runs(const LookupArgs& a) {
     for (uint32_t chunk = 0; chunk < a.width; chunk += kChunkLanes) {
         const uint32_t first[2] = {chunk + threadIdx.x * kPiece, chunk + kHalf + threadIdx.x * kPiece};
         const bool live[2] = {first[0] < a.width, first[1] < a.width};  // pieces are whole: width % 8 == 0
-        i32x4 ids[2];
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            ids[h] = stream_load(reinterpret_cast<const i32x4*>(
-                element<true>(topk, 1, live[h] ? first[h] : a.width - kPiece)));
+        if (chunk != 0) {
+            load_ids(chunk, ids);
         }
         if (chunk == 0 && bits_in_lds) {
             // Issued after the Top-K loads so all of them are in flight together.
@@ -613,16 +624,21 @@ __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupAr
     // tables only, so a staged id is the table value itself).
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ int32_t wave_totals[kThreads / 64];
-    const int64_t row = a.selected[blockIdx.x];
+    const int64_t row = a.selected.fetch(blockIdx.x);
     if (row < 0 || row >= a.batch) {
         return;  // uniform over the workgroup
     }
     const int64_t layer = blockIdx.y;
-    const int64_t req = a.rows[row];
-    const int64_t length = a.lengths[row];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const TopkT* topk = static_cast<const TopkT*>(a.topk) + layer * a.topk_sl + row * a.topk_sb;
+    // First chunk's Top-K ids before the request's metadata, as above.
+    TopkT block[kIters];
+    load_blocks<false>(a, topk, wave * kWaveSpan + lane, block);
+    const int64_t req = a.rows.fetch(row);
+    const int64_t length = a.lengths.fetch(row);
     const bool table_ok = req >= 0 && req < a.table_rows && a.table_cols > 0;  // uniform
     const int64_t bound = length < a.table_cols ? length : a.table_cols;
-    const TopkT* topk = static_cast<const TopkT*>(a.topk) + layer * a.topk_sl + row * a.topk_sb;
     const TableT* table =
         static_cast<const TableT*>(a.table) + layer * a.table_sl + (table_ok ? req : 0) * a.table_sr;
     const MapT* mapping = static_cast<const MapT*>(a.mapping) + layer * a.map_sl;
@@ -630,14 +646,13 @@ __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupAr
     const int32_t* window = reinterpret_cast<const int32_t*>(lds);
     int32_t* out = a.out + layer * a.out_sl + row * a.out_sb;
     int32_t* misses = kCompact ? a.misses + layer * a.miss_sl + row * a.miss_sb : nullptr;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
     int32_t running = 0;
 
     for (uint32_t chunk = 0; chunk < a.width; chunk += kChunkLanes) {
         const uint32_t first = chunk + wave * kWaveSpan + lane;
-        TopkT block[kIters];
-        load_blocks<false>(a, topk, first, block);
+        if (chunk != 0) {
+            load_blocks<false>(a, topk, first, block);
+        }
         if (chunk == 0 && win.count > 0) {
             stage_rows(lds, table + win.start * a.table_sc, a.table_sc, win.count, nullptr,
                        static_cast<const int32_t*>(nullptr), 0, 0);
