@@ -42,6 +42,8 @@
 #include "ekv_tensor_util.h"
 
 #include <algorithm>
+#include <atomic>
+#include <stdexcept>
 #include <type_traits>
 
 namespace ekv {
@@ -117,6 +119,7 @@ struct LookupArgs {
     int32_t window;                      // stage the recent window (int32 table)
     int32_t bits_staged;                 // stage the bitmap row in LDS
     int32_t runs;                        // int16 local form: contiguous 8-lane runs per thread
+    int32_t pipe;                        // ... of one chunk, prefetching persistent form
     uint32_t width;
     uint32_t block_size;
     FastDiv block_div;
@@ -618,6 +621,243 @@ void resolve_runs_kernel(const LookupArgs a) {
     resolve_local_runs<kCompact>(a);
 }
 
+// Prefetching form of the contiguous-pieces kernel, for rows of one chunk
+// (width <= 2048) whose bitmap rows are dense, 16-byte aligned and at most
+// 2048 words (T <= 65536), a multiple of 4 words long. A persistent grid walks
+// the (selected row, layer) items item = blockIdx.x + k * gridDim.x, at most
+// kPipeMaxItems per workgroup:
+//  - the index metadata of all of a workgroup's items (selected row, request
+//    row, length, slot base) is read once at the start, by one thread per
+//    item, into LDS, so no item waits on a chain of dependent index loads;
+//  - the next item's Top-K ids and bitmap row are loaded into registers right
+//    behind the current item's table reads, so they are in flight while the
+//    current item's table reads, stores and miss compaction complete.
+// Every load is unconditional with clamped, in-bounds addresses (a clamped
+// bitmap piece is written to LDS twice with the same value), so the compiler
+// cannot sink a load into the branch that consumes it and serialize the
+// staging; the last iteration's loads for a next item that does not exist read
+// one line of each row. Results equal the contiguous-pieces kernel's.
+#ifndef EKV_LOOKUP_PIPE
+#define EKV_LOOKUP_PIPE 1
+#endif
+#ifndef EKV_LOOKUP_PIPE_GRID
+#define EKV_LOOKUP_PIPE_GRID 1   // 1: persistent grid (resident workgroups); 0: one item per workgroup
+#endif
+constexpr uint32_t kPipeBitPieces = 2 * kThreads;   // 16-byte bitmap pieces per item: 2048 words
+constexpr uint32_t kPipeMaxItems = 16;              // items per workgroup
+constexpr uint32_t kNoRow = 0xffffffffu;
+
+// Index metadata of one item: row = kNoRow when the selected row names no
+// batch row, req = kNoRow when the request has no table row.
+struct RunsMeta {
+    uint32_t row, req, base;   // base: low 32 bits of the request's slot base
+    int32_t bound;             // positions below it are valid: min(length, T), at least 0
+};
+
+// The per-thread loads of one item: Top-K ids of lanes [4t, +4) and
+// [1024 + 4t, +4), bitmap pieces t and 256 + t (clamped to the row).
+struct RunsLoads {
+    i32x4 ids[2];
+    i32x4 bits[2];
+};
+
+// The loads of one item. A stray selection reads batch row 0 and a request
+// without a table row bitmap row 0 (in bounds, discarded). With `first_only`
+// (uniform) every thread reads the first 16-byte piece of both rows: the
+// workgroup's last iteration issues loads nobody uses, and one line each keeps
+// them unconditional without fetching two more rows.
+__device__ __forceinline__ RunsLoads runs_issue(const LookupArgs& a, uint32_t layer, const RunsMeta& m,
+                                                bool first_only) {
+    constexpr uint32_t kHalf = kThreads * 4;
+    RunsLoads l;
+    const uint32_t row = m.row != kNoRow ? m.row : 0u;
+    const int32_t* topk = static_cast<const int32_t*>(a.topk) + layer * a.topk_sl + row * a.topk_sb;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t first = h * kHalf + threadIdx.x * 4;
+        const uint32_t at = first_only ? 0u : (first < a.width ? first : a.width - 4);
+        l.ids[h] = stream_load(reinterpret_cast<const i32x4*>(element<true>(topk, 1, at)));
+    }
+    const bool table_ok = m.row != kNoRow && m.req != kNoRow;
+    const int32_t* row_bits = a.bits + layer * a.bits_sl + (table_ok ? m.req : 0u) * a.bits_sr;
+    const uint32_t last = table_ok && !first_only ? static_cast<uint32_t>(a.bits_words >> 2) - 1 : 0u;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t piece = h * kThreads + threadIdx.x;
+        l.bits[h] = *reinterpret_cast<const i32x4*>(element<true>(row_bits, 1, 4 * (piece < last ? piece : last)));
+    }
+    return l;
+}
+
+__device__ __forceinline__ RunsMeta runs_meta(const uint4* meta, uint32_t k) {
+    const uint4 v = meta[k];
+    return RunsMeta{v.x, v.y, v.z, static_cast<int32_t>(v.w)};
+}
+
+template <bool kCompact>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void resolve_runs_pipe_kernel(const LookupArgs a, uint32_t items, uint32_t count, FastDiv count_div) {
+    constexpr uint32_t kPiece = 4;
+    constexpr uint32_t kHalf = kThreads * kPiece;  // 1024 lanes
+    constexpr int kWaves = kThreads / 64;
+    __shared__ __align__(16) uint32_t staged_bits[4 * kPipeBitPieces];
+    __shared__ uint4 meta[kPipeMaxItems];
+    __shared__ int32_t wave_totals[2 * kWaves];   // [half][wave]
+    __shared__ int32_t chunk_misses[kChunkLanes];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const uint32_t first[2] = {threadIdx.x * kPiece, kHalf + threadIdx.x * kPiece};
+    const bool live_piece[2] = {first[0] < a.width, first[1] < a.width};  // pieces are whole: width % 8 == 0
+    const uint32_t last_piece = static_cast<uint32_t>(a.bits_words >> 2) - 1;
+    const uint32_t n = (items - blockIdx.x + gridDim.x - 1) / gridDim.x;  // this workgroup's items, <= kPipeMaxItems
+
+    if (threadIdx.x < n) {
+        const uint32_t item = blockIdx.x + threadIdx.x * gridDim.x;
+        const uint32_t item_layer = count_div.div(item);
+        const int64_t row = a.selected.fetch(item - item_layer * count);
+        const bool live = row >= 0 && row < a.batch;
+        uint4 m{kNoRow, kNoRow, 0u, 0u};
+        if (live) {
+            const int64_t req = a.rows.fetch(row);
+            const int64_t length = a.lengths.fetch(row);
+            const bool table_ok = req >= 0 && req < a.table_rows && a.table_cols > 0;
+            const int64_t bound = length < a.table_cols ? length : a.table_cols;
+            m.x = static_cast<uint32_t>(row);
+            m.y = table_ok ? static_cast<uint32_t>(req) : kNoRow;
+            m.z = table_ok ? static_cast<uint32_t>(a.slot_base.fetch(req)) : 0u;
+            m.w = static_cast<uint32_t>(bound > 0 ? static_cast<int32_t>(bound) : 0);
+        }
+        meta[threadIdx.x] = m;
+    }
+    __syncthreads();
+
+    RunsMeta cur = runs_meta(meta, 0);
+    uint32_t layer = count_div.div(blockIdx.x);
+    RunsLoads loads = runs_issue(a, layer, cur, false);
+    for (uint32_t k = 0;;) {
+        const bool last_item = k + 1 >= n;
+        const uint32_t k_next = last_item ? k : k + 1;
+        const uint32_t layer_next = count_div.div(blockIdx.x + k_next * gridDim.x);
+        const RunsMeta nxt = runs_meta(meta, k_next);
+        RunsLoads next_loads;
+        if (cur.row != kNoRow) {  // uniform
+            const bool table_ok = cur.req != kNoRow;
+            if (table_ok) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t piece = h * kThreads + threadIdx.x;
+                    *reinterpret_cast<i32x4*>(&staged_bits[4 * (piece < last_piece ? piece : last_piece)]) =
+                        loads.bits[h];
+                }
+            }
+            __syncthreads();
+            const int32_t block[kIters] = {loads.ids[0].x, loads.ids[0].y, loads.ids[0].z, loads.ids[0].w,
+                                           loads.ids[1].x, loads.ids[1].y, loads.ids[1].z, loads.ids[1].w};
+            int32_t slot[kIters];
+            uint32_t at[kIters];   // table position to read (0 when none is needed)
+            uint32_t need = 0;     // bit j: lane j reads its table entry
+            // Bitwise, not short-circuit: every lane reads its LDS word, so
+            // the reads are not split into one branch and wait per lane.
+#pragma unroll
+            for (int j = 0; j < kIters; ++j) {
+                const bool valid = live_piece[j / kPiece] & table_ok & (block[j] >= 0) & (block[j] < cur.bound);
+                const uint32_t p = valid ? static_cast<uint32_t>(block[j]) : 0u;
+                const uint32_t word = staged_bits[p >> 5];
+                const bool resident = (static_cast<uint32_t>(valid) & (word >> (p & 31))) != 0u;
+                slot[j] = valid ? 0 : -1;
+                at[j] = resident ? p : 0u;
+                need |= static_cast<uint32_t>(resident) << j;
+            }
+            // Lanes that need no entry re-read entry 0 of the row; without a
+            // table row every lane re-reads entry 0 of row 0 of this layer.
+            const int16_t* table = static_cast<const int16_t*>(a.table) + layer * a.table_sl +
+                                   (table_ok ? cur.req : 0u) * a.table_sr;
+            int16_t entry[kIters];
+#pragma unroll
+            for (int j = 0; j < kIters; ++j) {
+                entry[j] = *element<true>(table, 1, at[j]);
+            }
+            // The next item's loads go out behind this item's table reads.
+            next_loads = runs_issue(a, layer_next, nxt, last_item);
+#pragma unroll
+            for (int j = 0; j < kIters; ++j) {
+                const int32_t e = entry[j];
+                const int32_t value = e > 0 ? static_cast<int32_t>(cur.base + static_cast<uint32_t>(e) - 1u) : 0;
+                slot[j] = (need >> j) & 1u ? value : slot[j];
+            }
+            int32_t* out = a.out + layer * a.out_sl + cur.row * a.out_sb;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if (live_piece[h]) {
+                    stream_store(i32x4{slot[4 * h], slot[4 * h + 1], slot[4 * h + 2], slot[4 * h + 3]},
+                                 reinterpret_cast<i32x4*>(element<true>(out, 1, first[h])));
+                }
+            }
+            if constexpr (kCompact) {
+                int32_t* misses = a.misses + layer * a.miss_sl + cur.row * a.miss_sb;
+                uint32_t miss = 0;  // bit j: lane j is a miss
+#pragma unroll
+                for (int j = 0; j < kIters; ++j) {
+                    miss |= static_cast<uint32_t>(live_piece[j / kPiece] && slot[j] == 0) << j;
+                }
+                uint32_t below[2] = {0, 0};
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t c = __popc((miss >> (kPiece * h)) & 0xfu);
+                    uint32_t wave_total = 0;
+#pragma unroll
+                    for (int b = 0; b < 3; ++b) {
+                        const uint64_t plane = __ballot((c >> b) & 1u);
+                        below[h] += lanes_below(plane) << b;
+                        wave_total += static_cast<uint32_t>(__popcll(plane)) << b;
+                    }
+                    if (lane == 0) {
+                        wave_totals[h * kWaves + wave] = static_cast<int32_t>(wave_total);
+                    }
+                }
+                __syncthreads();
+                int32_t rank[2] = {static_cast<int32_t>(below[0]), static_cast<int32_t>(below[1])};
+                int32_t half_total[2] = {0, 0};
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                    for (int w = 0; w < kWaves; ++w) {
+                        rank[h] += w < wave ? wave_totals[h * kWaves + w] : 0;
+                        half_total[h] += wave_totals[h * kWaves + w];
+                    }
+                }
+                rank[1] += half_total[0];
+                const int32_t total = half_total[0] + half_total[1];
+#pragma unroll
+                for (int j = 0; j < kIters; ++j) {
+                    if ((miss >> j) & 1u) {
+                        chunk_misses[rank[j / kPiece]++] = static_cast<int32_t>(first[j / kPiece] + j % kPiece);
+                    }
+                }
+                __syncthreads();
+                for (int32_t i = threadIdx.x; i < total; i += kThreads) {
+                    *element<true>(misses, 1, static_cast<uint32_t>(i)) = chunk_misses[i];
+                }
+                if (threadIdx.x == 0) {
+                    a.counts[layer * a.count_sl + cur.row * a.count_sb] = total;
+                }
+                // The two barriers above order this item's LDS reads before
+                // the next item's writes.
+            } else {
+                __syncthreads();  // the staged bitmap is rewritten by the next item
+            }
+        } else {
+            next_loads = runs_issue(a, layer_next, nxt, last_item);
+        }
+        if (++k >= n) {
+            break;
+        }
+        cur = nxt;
+        layer = layer_next;
+        loads = next_loads;
+    }
+}
+
 template <typename TopkT, typename TableT, typename MapT, bool kCompact>
 __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupArgs a) {
     // Dynamic LDS: [kWindow] staged logical ids of the recent window (int32
@@ -697,6 +937,43 @@ __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupAr
     }
 }
 
+// Workgroups of the prefetching kernel resident on the whole device at once,
+// per device (0 = not yet queried).
+template <bool kCompact>
+uint32_t runs_pipe_resident() {
+    static std::atomic<uint32_t> resident[64];
+    int device = 0;
+    check_hip(hipGetDevice(&device), "hipGetDevice");
+    if (device < 0 || device >= 64) {
+        throw std::runtime_error("device ordinal out of range");
+    }
+    uint32_t known = resident[device].load(std::memory_order_relaxed);
+    if (known == 0) {
+        int per_cu = 0, cus = 0;
+        check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                      &per_cu, reinterpret_cast<const void*>(resolve_runs_pipe_kernel<kCompact>), kThreads, 0),
+                  "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+        check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
+                  "hipDeviceGetAttribute");
+        known = static_cast<uint32_t>(std::max(1, per_cu) * std::max(1, cus));
+        resident[device].store(known, std::memory_order_relaxed);
+    }
+    return known;
+}
+
+template <bool kCompact>
+void launch_runs_pipe(const LookupArgs& a, dim3 grid, hipStream_t stream) {
+    const uint32_t count = grid.x;
+    const uint32_t items = grid.x * grid.y;   // below 2^31 (checked by the host)
+    // Resident workgroups, or more when they would take over kPipeMaxItems items each.
+    const uint32_t groups =
+        EKV_LOOKUP_PIPE_GRID
+            ? std::min(items, std::max(runs_pipe_resident<kCompact>(), (items + kPipeMaxItems - 1) / kPipeMaxItems))
+            : items;
+    resolve_runs_pipe_kernel<kCompact><<<dim3(groups), dim3(kThreads), 0, stream>>>(a, items, count,
+                                                                                      FastDiv(count));
+}
+
 template <typename TopkT, typename TableT>
 void launch_with_table(const LookupArgs& a, int32_t map_dtype, bool compact, bool dense, dim3 grid,
                        hipStream_t stream) {
@@ -706,6 +983,14 @@ void launch_with_table(const LookupArgs& a, int32_t map_dtype, bool compact, boo
         const bool bits = a.bits != nullptr;
         if (dense) {
             if constexpr (std::is_same_v<TopkT, int32_t> && std::is_same_v<TableT, int16_t>) {
+                if (bits && a.pipe) {
+                    if (compact) {
+                        launch_runs_pipe<true>(a, grid, stream);
+                    } else {
+                        launch_runs_pipe<false>(a, grid, stream);
+                    }
+                    return;
+                }
                 if (bits && a.runs) {
                     if (compact) {
                         resolve_runs_kernel<true><<<grid, block, lds, stream>>>(a);
@@ -974,6 +1259,17 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
     a.runs = EKV_LOOKUP_RUNS && local && bits_p != nullptr && topk.dtype == EKV_INT32 && block_size == 1 &&
                      width % kIters == 0 && rows_aligned(topk.data, a.topk_sl, layers, a.topk_sb, batch) &&
                      rows_aligned(output.data, a.out_sl, layers, a.out_sb, batch)
+                 ? 1
+                 : 0;
+    // The prefetching form: rows of one chunk, a non-empty batch and table
+    // (stray selections and requests read batch row 0 and table entry 0 of
+    // row 0, and discard them), fewer than 2^31 items, and bitmap rows of
+    // whole 16-byte pieces, 16-byte aligned, 4 to 2048 words.
+    const bool bits_pieces = bits_p != nullptr && (reinterpret_cast<uintptr_t>(a.bits) & 15) == 0 &&
+                             a.bits_sw == 1 && a.bits_sr % 4 == 0 && a.bits_sl % 4 == 0 && a.bits_words % 4 == 0 &&
+                             a.bits_words > 0 && a.bits_words <= 4 * static_cast<int64_t>(kPipeBitPieces);
+    a.pipe = EKV_LOOKUP_PIPE && a.runs && dense && a.bits_staged && bits_pieces && width <= kChunkLanes &&
+                     batch > 0 && a.table_rows > 0 && a.table_cols > 0 && count * layers < (int64_t{1} << 31)
                  ? 1
                  : 0;
     if (topk.dtype == EKV_INT64) {

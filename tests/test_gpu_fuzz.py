@@ -183,6 +183,64 @@ def test_local_slot_runs_random_configurations(gpu, coracle, seed):
                         assert got_counts[layer, row] == -5, case
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_local_slot_prefetch_many_items_per_workgroup(gpu, coracle, seed):
+    # Rows of one 2048-lane chunk over bitmap rows of whole 16-byte pieces take
+    # the prefetching kernel, whose persistent grid gives each workgroup
+    # several (row, layer) items once there are more items than resident
+    # workgroups (about 2048 on MI355X): here 3,000-8,000 items, with stray
+    # request rows, stray selections, short lengths and negative entries.
+    rng = np.random.default_rng(9400 + seed)
+    layers = int(rng.integers(20, 41))
+    batch = int(rng.integers(150, 201))
+    k = 8 * int(rng.integers(1, 257))
+    rrows = int(rng.integers(batch // 2, batch + 1))
+    cols = 128 * int(rng.integers(1, 65))              # ceil(T / 32) a multiple of 4 words
+    layered = seed != 5
+    compact = seed != 4
+    lengths = rng.integers(-2, cols + 5, size=batch)
+    rows = rng.integers(0, rrows, size=batch)
+    stray = rng.random(batch) < 0.05
+    rows[stray] = rng.choice([-1, rrows, rrows + 7], size=int(stray.sum()))
+    topk = rng.integers(-1, cols + 2, size=(layers, batch, k))
+    shape = (layers, rrows, cols) if layered else (rrows, cols)
+    local_table = rng.integers(1, 1 << 15, size=shape)
+    local_table[rng.random(shape) < 0.5] = 0
+    local_table[rng.random(shape) < 0.02] = -int(rng.integers(1, 1 << 15))
+    slot_base = rng.integers(-(1 << 20), 1 << 31, size=rrows)
+    req_axis = 1 if layered else 0
+    bases = np.expand_dims(slot_base, tuple(a for a in range(len(shape)) if a != req_axis))
+    # Bases up to 2^31: the oracle's int32 cast of base + local - 1 must equal the kernel's 32-bit sum.
+    table = np.where(local_table > 0, bases + local_table - 1, 0)
+    selected = rng.permutation(batch)[: int(rng.integers(batch - 10, batch + 1))]
+    if seed % 2:
+        selected = np.concatenate([selected, [-1, batch]])
+    initial = np.full((layers, batch, k), -77, np.int32)
+    want, want_misses, want_counts = coracle.resolve_resident(topk, table, None, rows, lengths, selected, 1,
+                                                              initial, with_misses=True)
+    table_d = torch.tensor(local_table, dtype=torch.int16, device=gpu)
+    bits = build_residency_bits(table_d)
+    assert bits.stride(-2) % 4 == 0 and bits.data_ptr() % 16 == 0
+    output = torch.tensor(initial, device=gpu)
+    misses = torch.full((layers, batch, k), -5, dtype=torch.int32, device=gpu) if compact else None
+    counts = torch.full((layers, batch), -5, dtype=torch.int32, device=gpu) if compact else None
+    resolve_resident(torch.tensor(topk, dtype=torch.int32, device=gpu), table_d, None, torch.tensor(rows, device=gpu),
+                     torch.tensor(lengths, dtype=torch.int32, device=gpu), torch.tensor(selected, device=gpu),
+                     output, 1, misses=misses, miss_count=counts, resident_bits=bits,
+                     slot_base=torch.tensor(slot_base, device=gpu))
+    case = (seed, layers, batch, k, cols, layered)
+    assert np.array_equal(output.cpu().numpy(), want), case
+    if compact:
+        got_counts, got_misses = counts.cpu().numpy(), misses.cpu().numpy()
+        chosen = np.zeros(batch, bool)
+        chosen[selected[(selected >= 0) & (selected < batch)]] = True
+        assert np.array_equal(got_counts[:, chosen], want_counts[:, chosen]), case
+        assert (got_counts[:, ~chosen] == -5).all(), case
+        lanes = np.arange(k)
+        valid = lanes[None, None, :] < want_counts[:, :, None]
+        assert np.array_equal(np.where(valid, got_misses, 0)[:, chosen], np.where(valid, want_misses, 0)[:, chosen]), case
+
+
 def random_planes(rng, gpu, layers, kv, rows, row_bytes):
     row_stride = row_bytes + int(rng.choice([0, 0, 2, 8, 16, 48]))
     plane = rows * row_stride + int(rng.choice([0, 16, 64, 100]))
