@@ -196,7 +196,7 @@ def lookup_roofline(algorithmic_bytes, avg_ms, traffic):
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "moved_gbs": None if traffic is None else round(traffic / (avg_ms / 1e3) / 1e9, 1),
-            "kernel": "resolve_runs_kernel<compact> (ekv_resolve_resident_local: int32 Top-K, int16 table, bitmap)",
+            "kernel": "resolve_runs_pipe_kernel<compact> (ekv_resolve_resident_local: int32 Top-K, int16 table, bitmap)",
             "algorithmic_bytes_per_launch": algorithmic_bytes, "avg_launch_ms": round(avg_ms, 4)}
 
 
