@@ -203,25 +203,28 @@ __device__ __forceinline__ void stage_words(uint32_t* dst, const T* src, int64_t
 }
 
 // A dense, 16-byte aligned int32 region, 16-byte pieces in groups of 4 per
-// thread.
+// thread. The stores go to the same in-range index as the loads (a piece
+// past the end is folded back to j - n4, or to the last piece, and written
+// twice with the same value): a store under `j < n4` let the compiler move
+// each load into its store's branch and wait after each one. Folding to
+// j - n4 rather than always to the last piece keeps the duplicate LDS stores
+// of a wave on distinct addresses.
 __device__ __forceinline__ void stage_vector(uint32_t* dst, const int32_t* src, int64_t n) {
     if (n <= 0) {
         return;
     }
     const int64_t n4 = n >> 2;
+    // Piece j, or for j past the end a piece that is in range.
+    const auto fold = [n4](int64_t j) { return j < n4 ? j : (j - n4 < n4 ? j - n4 : n4 - 1); };
     for (int64_t first = 0; first < n4; first += 4 * kThreads) {
         int4 v[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const int64_t j = first + threadIdx.x + k * kThreads;
-            v[k] = reinterpret_cast<const int4*>(src)[j < n4 ? j : n4 - 1];
+            v[k] = reinterpret_cast<const int4*>(src)[fold(first + threadIdx.x + k * kThreads)];
         }
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const int64_t j = first + threadIdx.x + k * kThreads;
-            if (j < n4) {
-                reinterpret_cast<int4*>(dst)[j] = v[k];
-            }
+            reinterpret_cast<int4*>(dst)[fold(first + threadIdx.x + k * kThreads)] = v[k];
         }
     }
     const int64_t t = (n4 << 2) + threadIdx.x;
