@@ -40,6 +40,16 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kUnroll = EKV_COPY_UNROLL;  // independent VW-byte loads in flight per lane
+// KV gathers of small rows reserve LDS they do not use, so that at most 3 of
+// their workgroups share a CU (160 KiB of LDS per CU on MI355X; 4 KiB static
+// + 48 KiB reserved per workgroup). Fewer gathers in flight per CU measured
+// faster on the decode shapes: 5 per CU (the register limit) 5.08 ms, 4 per
+// CU 5.01 ms, 3 per CU 4.91 ms, 2 per CU 5.06 ms for 31.5 M rows of 512 B.
+// (Large rows, and the lookup kernels, measured no gain from fewer groups.)
+#ifndef EKV_GATHER_LDS_RESERVE
+#define EKV_GATHER_LDS_RESERVE 49152
+#endif
+constexpr size_t kGatherLdsReserve = EKV_GATHER_LDS_RESERVE;
 // MI355X has 8 XCDs; workgroups are dispatched to them round robin. Dealing
 // each XCD one contiguous range of tiles keeps neighbouring rows (same
 // request region of a plane, adjacent slot reads) on one XCD's L2 and TLBs:
@@ -363,7 +373,8 @@ void launch_engine(EngineArgs a, hipStream_t stream) {
         return;
     }
     if (small) {
-        copy_small_rows<M, VW><<<dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream>>>(a);
+        copy_small_rows<M, VW><<<dim3(static_cast<uint32_t>(grid)), dim3(kThreads),
+                                 is_gather_mode(M) ? kGatherLdsReserve : 0, stream>>>(a);
     } else {
         copy_large_rows<M, VW><<<dim3(static_cast<uint32_t>(grid)), dim3(kThreads), 0, stream>>>(a);
     }
