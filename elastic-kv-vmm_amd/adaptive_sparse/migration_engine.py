@@ -71,9 +71,22 @@ class PagedKVPool:
         self.pages.release(set(ids))
         self.free.release(ids)
 
-    def trim(self):
-        """Unmap chunks no page owns; returns the released bytes."""
-        return self.pages.trim_quiescent()
+    def trim(self, after=None):
+        """Unmap chunks no page owns; returns the released bytes.
+
+        By default the device is synchronized first. `after` is an event after
+        which no device work reads or writes the released pages (a round
+        trip's `packed` event): the host waits for it instead, so the copies
+        and kernels queued behind it keep running while the chunks are
+        unmapped.
+        """
+        if after is None:
+            return self.pages.trim_quiescent()
+        pending = self.pages.reclaimable_chunks()
+        if not pending:
+            return 0
+        after.synchronize()
+        return self.backing.reclaim(pending, synchronize=False) * self.layout.chunk_bytes
 
     def close(self):
         torch.cuda.synchronize(self.device)
@@ -86,6 +99,7 @@ class HostPages:
 
     rows: torch.Tensor      # int64 host-buffer rows, one per page
     pages: tuple            # the source pages, same order
+    packed: object = None   # round_trip: event after the last read of the source pages
 
 
 class MigrationEngine:
@@ -222,9 +236,12 @@ class MigrationEngine:
         ready = torch.cuda.Event()
         ready.record(compute)
         self.h2d.wait_event(ready)                   # earlier unpacks read the same device staging
+        # Every sub-batch is packed first (each releases its D2H copy at once),
+        # so the source pages are free once the last pack has run; the unpacks
+        # follow on the compute stream, each behind its own H2D copy.
+        arrivals = []
         for start in range(0, len(pages), self.sub_batch):
             sources = pages[start:start + self.sub_batch]
-            targets = destinations[start:start + self.sub_batch]
             span = rows[start:start + len(sources)]
             self.pack(sources, self.out_staging, start)
             packed = torch.cuda.Event()
@@ -239,11 +256,15 @@ class MigrationEngine:
                 self._copy_rows(span, self.in_staging, start, to_host=False)
                 landed = torch.cuda.Event()
                 landed.record(self.h2d)
+            arrivals.append((start, landed))
+        all_packed = torch.cuda.Event()
+        all_packed.record(compute)
+        for start, landed in arrivals:
             compute.wait_event(landed)
-            self.unpack(targets, self.in_staging, start)
+            self.unpack(destinations[start:start + self.sub_batch], self.in_staging, start)
         if pages:
             self._d2h_done, self._h2d_done = copied, landed
-        return HostPages(rows=rows, pages=pages)
+        return HostPages(rows=rows, pages=pages, packed=all_packed)
 
     def _copy_rows(self, rows, staging, start, *, to_host):
         for host_start, offset, length in self._host_runs(rows):

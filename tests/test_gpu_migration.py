@@ -73,6 +73,41 @@ def test_round_trip_is_byte_exact_and_pack_matches_oracle(gpu, coracle, sub_batc
         pool.close()
 
 
+@pytest.mark.parametrize("sub_batch", [3, 64])
+def test_trim_after_packed_event_overlaps_the_copies(gpu, sub_batch):
+    # The sources are released and their chunks unmapped once the round trip's
+    # packs have run (host waits on the `packed` event only), while the D2H,
+    # H2D and unpacks queued behind them are still in flight; every target
+    # page must still receive its source bytes.
+    layout = BlockMajorLayout(blocks=64, **BLOCK)
+    pool = PagedKVPool(layout, device=0)
+    try:
+        rng = np.random.default_rng(100 + sub_batch)
+        live = sorted(rng.choice(np.arange(1, 64), size=30, replace=False).tolist())
+        pool.allocate(live)
+        fill(pool, live, 2)
+        sources = rng.choice(live, size=20, replace=False).tolist()
+        free = sorted(set(range(1, 64)) - set(live))
+        targets = rng.choice(free, size=20, replace=False).tolist()
+        before = {p: pool.page_view(p).clone() for p in sources}
+        torch.cuda.synchronize()
+        engine = MigrationEngine(pool, max_pages=20, sub_batch=sub_batch)
+        pool.allocate(targets)
+        backed = pool.backing.backed_bytes
+        host = engine.round_trip(sources, targets)
+        assert host.packed is not None
+        pool.release(sources)
+        released = pool.trim(after=host.packed)
+        engine.wait()
+        assert released > 0 and pool.backing.backed_bytes == backed - released
+        for s, t in zip(sources, targets):
+            assert torch.equal(pool.page_view(t), before[s]), (s, t)
+        for i, s in enumerate(sources):
+            assert torch.equal(engine.host[int(host.rows[i])], before[s].cpu())
+    finally:
+        pool.close()
+
+
 def test_transactions_demote_promote_cycle(gpu):
     layout = BlockMajorLayout(blocks=64, **BLOCK)
     pool = PagedKVPool(layout, device=0)
