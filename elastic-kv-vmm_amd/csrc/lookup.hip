@@ -1271,8 +1271,10 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
     const bool bits_pieces = bits_p != nullptr && (reinterpret_cast<uintptr_t>(a.bits) & 15) == 0 &&
                              a.bits_sw == 1 && a.bits_sr % 4 == 0 && a.bits_sl % 4 == 0 && a.bits_words % 4 == 0 &&
                              a.bits_words > 0 && a.bits_words <= 4 * static_cast<int64_t>(kPipeBitPieces);
+    // Batch and table rows are kept as 32-bit indices (all ones = none).
     a.pipe = EKV_LOOKUP_PIPE && a.runs && dense && a.bits_staged && bits_pieces && width <= kChunkLanes &&
-                     batch > 0 && a.table_rows > 0 && a.table_cols > 0 && count * layers < (int64_t{1} << 31)
+                     batch > 0 && batch < (int64_t{1} << 31) && a.table_rows > 0 &&
+                     a.table_rows < (int64_t{1} << 31) && a.table_cols > 0 && count * layers < (int64_t{1} << 31)
                  ? 1
                  : 0;
     if (topk.dtype == EKV_INT64) {
