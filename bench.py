@@ -1022,7 +1022,8 @@ def run_composite(torch, args, device):
              "promote_gbs_over_pcie": round(promote_bytes / (mean["promote_ms"] / 1e3) / 1e9, 2),
              "lookups_per_s": round(lanes / (mean["lookup_ms"] / 1e3), 1),
              "step_ms_without_remap": round(mean["step_ms"] - mean["remap_ms"], 3),
-             "remap_parts_ms": {k: round(statistics.mean(v[args.warmup:] or v), 2) for k, v in remap_parts.items()},
+             "remap_parts_ms": {k: round(statistics.mean(v[args.warmup:] or v), 2) if v else 0.0
+                                for k, v in remap_parts.items()},
              "remapped_chunks_per_step": remap_count, "pool_commit_s": round(commit_s, 3),
              "graph_replay": {"replays": len(graph_ms), "gpu_ms_per_step": round(statistics.mean(graph_ms), 3),
                               "verified_against_host_copy": graph_verified}}

@@ -90,13 +90,16 @@ def resolve_resident(topk, table, mapping, rows, lengths, selected, output, bloc
 def build_residency_bits(table, out=None):
     """Residency bitmap of a single-level table: bit p of row q = table[.., q, p] != 0.
 
-    Returns an int32 tensor [.., R, ceil(T / 32)] (or fills `out`).
+    Returns an int32 tensor [.., R, W] (or fills `out`, which needs at least
+    ceil(T / 32) words per row). W is ceil(T / 32) rounded up to a multiple of
+    4: every row is whole 16-byte pieces, and the words past ceil(T / 32) are
+    zero, so the lookup can stage a row with 16-byte loads for any T.
     """
     if table.dim() not in (2, 3):
         raise ValueError("table must be [R, T] or [L, R, T]")
-    words = (table.shape[-1] + 31) // 32
+    words = -(-((table.shape[-1] + 31) // 32) // 4) * 4
     if out is None:
-        out = torch.empty((*table.shape[:-1], words), dtype=torch.int32, device=table.device)
+        out = torch.zeros((*table.shape[:-1], words), dtype=torch.int32, device=table.device)
     device = _native.device_of(table, out)
     lib = _native.kernel_library()
     table_view, out_view = _native.describe(table, "table"), _native.describe(out, "resident_bits")

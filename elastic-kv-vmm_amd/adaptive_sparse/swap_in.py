@@ -48,8 +48,8 @@ class HotBuffers:
         kw = dict(dtype=torch.int32, device=self.device)
         padded = -(-context // 128) * 128
         self.table = torch.zeros((layers, requests, padded), dtype=table_dtype, device=self.device)[..., :context]
-        words = (context + 31) // 32
-        self.bits = torch.zeros((layers, requests, padded // 32), **kw)[..., :words] if with_bits else None
+        # The bitmap keeps its padded width (whole 16-byte pieces, zero past ceil(context / 32)).
+        self.bits = torch.zeros((layers, requests, padded // 32), **kw) if with_bits else None
         self.slot_token = torch.full((layers, requests, capacity), -1, **kw)
         self.stamps = torch.full((layers, requests, capacity), INT32_MIN, **kw)
         if slot_base is None:

@@ -683,7 +683,7 @@ __device__ __forceinline__ RunsLoads runs_issue(const LookupArgs& a, uint32_t la
     }
     const bool table_ok = m.row != kNoRow && m.req != kNoRow;
     const int32_t* row_bits = a.bits + layer * a.bits_sl + (table_ok ? m.req : 0u) * a.bits_sr;
-    const uint32_t last = table_ok && !first_only ? static_cast<uint32_t>(a.bits_words >> 2) - 1 : 0u;
+    const uint32_t last = table_ok && !first_only ? static_cast<uint32_t>((a.bits_words + 3) >> 2) - 1 : 0u;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const uint32_t piece = h * kThreads + threadIdx.x;
@@ -711,7 +711,7 @@ void resolve_runs_pipe_kernel(const LookupArgs a, uint32_t items, uint32_t count
     const int wave = threadIdx.x >> 6;
     const uint32_t first[2] = {threadIdx.x * kPiece, kHalf + threadIdx.x * kPiece};
     const bool live_piece[2] = {first[0] < a.width, first[1] < a.width};  // pieces are whole: width % 8 == 0
-    const uint32_t last_piece = static_cast<uint32_t>(a.bits_words >> 2) - 1;
+    const uint32_t last_piece = static_cast<uint32_t>((a.bits_words + 3) >> 2) - 1;
     const uint32_t n = (items - blockIdx.x + gridDim.x - 1) / gridDim.x;  // this workgroup's items, <= kPipeMaxItems
 
     if (threadIdx.x < n) {
@@ -1266,11 +1266,15 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
                  : 0;
     // The prefetching form: rows of one chunk, a non-empty batch and table
     // (stray selections and requests read batch row 0 and table entry 0 of
-    // row 0, and discard them), fewer than 2^31 items, and bitmap rows of
-    // whole 16-byte pieces, 16-byte aligned, 4 to 2048 words.
+    // row 0, and discard them), fewer than 2^31 items, and bitmap rows of at
+    // most 2048 words that start 16-byte aligned and whose tensor covers
+    // ceil(words / 4) whole 16-byte pieces (the staging reads whole pieces;
+    // build_residency_bits pads rows that way).
+    const int64_t bits_pieces_needed = (a.bits_words + 3) / 4;
     const bool bits_pieces = bits_p != nullptr && (reinterpret_cast<uintptr_t>(a.bits) & 15) == 0 &&
-                             a.bits_sw == 1 && a.bits_sr % 4 == 0 && a.bits_sl % 4 == 0 && a.bits_words % 4 == 0 &&
-                             a.bits_words > 0 && a.bits_words <= 4 * static_cast<int64_t>(kPipeBitPieces);
+                             a.bits_sw == 1 && a.bits_sr % 4 == 0 && a.bits_sl % 4 == 0 && a.bits_words > 0 &&
+                             bits_p->shape[layered_table ? 2 : 1] >= 4 * bits_pieces_needed &&
+                             bits_pieces_needed <= static_cast<int64_t>(kPipeBitPieces);
     // Batch and table rows are kept as 32-bit indices (all ones = none).
     a.pipe = EKV_LOOKUP_PIPE && a.runs && dense && a.bits_staged && bits_pieces && width <= kChunkLanes &&
                      batch > 0 && batch < (int64_t{1} << 31) && a.table_rows > 0 &&

@@ -58,9 +58,11 @@ _live = {}
 _lock = threading.Lock()
 
 
+# The deleter can run during interpreter shutdown, after this module's
+# globals are cleared: everything it uses is bound as a default argument.
 @_DELETER
-def _release(managed):
-    key = ct.cast(managed, ct.c_void_p).value
+def _release(managed, _cast=ct.cast, _void_p=ct.c_void_p, _lock=_lock, _live=_live):
+    key = _cast(managed, _void_p).value
     with _lock:
         _live.pop(key, None)
 

@@ -23,6 +23,13 @@ from oracle import oracle as ref
 
 pytestmark = pytest.mark.gpu
 
+
+def bits_match(got, want):
+    """A bitmap padded to whole 16-byte pieces holds the oracle's ceil(T / 32) words, then zeros."""
+    words = want.shape[-1]
+    return (got.shape[-1] == -(-words // 4) * 4 and np.array_equal(got[..., :words], want)
+            and not got[..., words:].any())
+
 INDEX_DTYPES = (torch.int32, torch.int64)
 
 
@@ -372,7 +379,7 @@ def test_swap_in_random_configurations(gpu, seed):
         assert np.array_equal(buffers.table.cpu().numpy(), state["table"]), (seed, step)
         assert np.array_equal(buffers.slot_token.cpu().numpy(), state["slot_token"]), (seed, step)
         assert np.array_equal(buffers.stamps.cpu().numpy(), state["stamps"]), (seed, step)
-        assert np.array_equal(buffers.bits.cpu().numpy(), ref.residency_bits(state["table"])), (seed, step)
+        assert bits_match(buffers.bits.cpu().numpy(), ref.residency_bits(state["table"])), (seed, step)
         got_src, got_dst = promote_src.cpu().numpy(), promote_dst.cpu().numpy()
         for layer in range(L):
             for r in selected:

@@ -13,6 +13,13 @@ from adaptive_sparse.resident_lookup import resolve_resident
 pytestmark = pytest.mark.gpu
 
 
+def bits_match(got, want):
+    """A bitmap padded to whole 16-byte pieces holds the oracle's ceil(T / 32) words, then zeros."""
+    words = want.shape[-1]
+    return (got.shape[-1] == -(-words // 4) * 4 and np.array_equal(got[..., :words], want)
+            and not got[..., words:].any())
+
+
 def strided(values, dtype, device):
     """A non-contiguous view holding `values` (tests/smoke_resident_lookup.py:28-33)."""
     source = torch.tensor(values, dtype=dtype, device=device)
@@ -154,7 +161,7 @@ def test_bitmap_lookup_equals_plain_lookup_and_oracle(gpu, coracle, layered, bs)
     t = lambda a, dt: torch.tensor(a, dtype=dt, device=gpu)  # noqa: E731
     table_d = t(table, torch.int32)
     bits = build_residency_bits(table_d)
-    assert np.array_equal(bits.cpu().numpy(), ref.residency_bits(table))
+    assert bits_match(bits.cpu().numpy(), ref.residency_bits(table))
     width = k * bs
     outs = []
     for use_bits in (False, True):

@@ -21,6 +21,13 @@ from oracle import oracle as ref
 pytestmark = pytest.mark.gpu
 
 
+def bits_match(got, want):
+    """A bitmap padded to whole 16-byte pieces holds the oracle's ceil(T / 32) words, then zeros."""
+    words = want.shape[-1]
+    return (got.shape[-1] == -(-words // 4) * 4 and np.array_equal(got[..., :words], want)
+            and not got[..., words:].any())
+
+
 @pytest.mark.parametrize("capacity", [64, 50])
 def test_lookup_swap_promote_gather_cycle(gpu, capacity):
     L, R, T, K, row_bytes = 2, 3, 300, 32, 64
@@ -83,7 +90,7 @@ def test_lookup_swap_promote_gather_cycle(gpu, capacity):
             assert np.array_equal(buffers.table.cpu().numpy(), state["table"]), step
             assert np.array_equal(buffers.slot_token.cpu().numpy(), state["slot_token"]), step
             assert np.array_equal(buffers.stamps.cpu().numpy(), state["stamps"]), step
-            assert np.array_equal(buffers.bits.cpu().numpy(), ref.residency_bits(state["table"])), step
+            assert bits_match(buffers.bits.cpu().numpy(), ref.residency_bits(state["table"])), step
             got_src, got_dst = promote_src.cpu().numpy(), promote_dst.cpu().numpy()
             for layer in range(L):
                 for r in range(R):
@@ -176,7 +183,7 @@ def test_paged_blocks_lookup_and_swap_in_match_oracle(gpu, bs):
         assert np.array_equal(buffers.table.cpu().numpy(), state["table"]), step
         assert np.array_equal(buffers.slot_token.cpu().numpy(), state["slot_token"]), step
         assert np.array_equal(buffers.stamps.cpu().numpy(), state["stamps"]), step
-        assert np.array_equal(buffers.bits.cpu().numpy(), ref.residency_bits(state["table"])), step
+        assert bits_match(buffers.bits.cpu().numpy(), ref.residency_bits(state["table"])), step
         got_src, got_dst = promote_src.cpu().numpy(), promote_dst.cpu().numpy()
         for layer in range(L):
             for r in range(R):
