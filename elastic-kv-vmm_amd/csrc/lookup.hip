@@ -697,7 +697,9 @@ __device__ __forceinline__ RunsMeta runs_meta(const uint4* meta, uint32_t k) {
     return RunsMeta{v.x, v.y, v.z, static_cast<int32_t>(v.w)};
 }
 
-template <bool kCompact>
+// TableT: int16_t (local slot + 1 per entry, plus the request's slot base) or
+// int32_t (the global slot itself).
+template <bool kCompact, typename TableT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void resolve_runs_pipe_kernel(const LookupArgs a, uint32_t items, uint32_t count, FastDiv count_div) {
     constexpr uint32_t kPiece = 4;
@@ -727,7 +729,9 @@ void resolve_runs_pipe_kernel(const LookupArgs a, uint32_t items, uint32_t count
             const int64_t bound = length < a.table_cols ? length : a.table_cols;
             m.x = static_cast<uint32_t>(row);
             m.y = table_ok ? static_cast<uint32_t>(req) : kNoRow;
-            m.z = table_ok ? static_cast<uint32_t>(a.slot_base.fetch(req)) : 0u;
+            if constexpr (std::is_same_v<TableT, int16_t>) {
+                m.z = table_ok ? static_cast<uint32_t>(a.slot_base.fetch(req)) : 0u;
+            }
             m.w = static_cast<uint32_t>(bound > 0 ? static_cast<int32_t>(bound) : 0);
         }
         meta[threadIdx.x] = m;
@@ -773,9 +777,9 @@ void resolve_runs_pipe_kernel(const LookupArgs a, uint32_t items, uint32_t count
             }
             // Lanes that need no entry re-read entry 0 of the row; without a
             // table row every lane re-reads entry 0 of row 0 of this layer.
-            const int16_t* table = static_cast<const int16_t*>(a.table) + layer * a.table_sl +
-                                   (table_ok ? cur.req : 0u) * a.table_sr;
-            int16_t entry[kIters];
+            const TableT* table = static_cast<const TableT*>(a.table) + layer * a.table_sl +
+                                  (table_ok ? cur.req : 0u) * a.table_sr;
+            TableT entry[kIters];
 #pragma unroll
             for (int j = 0; j < kIters; ++j) {
                 entry[j] = *element<true>(table, 1, at[j]);
@@ -785,7 +789,10 @@ void resolve_runs_pipe_kernel(const LookupArgs a, uint32_t items, uint32_t count
 #pragma unroll
             for (int j = 0; j < kIters; ++j) {
                 const int32_t e = entry[j];
-                const int32_t value = e > 0 ? static_cast<int32_t>(cur.base + static_cast<uint32_t>(e) - 1u) : 0;
+                int32_t value = e;   // int32 tables hold the slot itself
+                if constexpr (std::is_same_v<TableT, int16_t>) {
+                    value = e > 0 ? static_cast<int32_t>(cur.base + static_cast<uint32_t>(e) - 1u) : 0;
+                }
                 slot[j] = (need >> j) & 1u ? value : slot[j];
             }
             int32_t* out = a.out + layer * a.out_sl + cur.row * a.out_sb;
@@ -942,7 +949,7 @@ __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupAr
 
 // Workgroups of the prefetching kernel resident on the whole device at once,
 // per device (0 = not yet queried).
-template <bool kCompact>
+template <bool kCompact, typename TableT>
 uint32_t runs_pipe_resident() {
     static std::atomic<uint32_t> resident[64];
     int device = 0;
@@ -954,7 +961,7 @@ uint32_t runs_pipe_resident() {
     if (known == 0) {
         int per_cu = 0, cus = 0;
         check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                      &per_cu, reinterpret_cast<const void*>(resolve_runs_pipe_kernel<kCompact>), kThreads, 0),
+                      &per_cu, reinterpret_cast<const void*>(resolve_runs_pipe_kernel<kCompact, TableT>), kThreads, 0),
                   "hipOccupancyMaxActiveBlocksPerMultiprocessor");
         check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
                   "hipDeviceGetAttribute");
@@ -964,16 +971,16 @@ uint32_t runs_pipe_resident() {
     return known;
 }
 
-template <bool kCompact>
+template <bool kCompact, typename TableT>
 void launch_runs_pipe(const LookupArgs& a, dim3 grid, hipStream_t stream) {
     const uint32_t count = grid.x;
     const uint32_t items = grid.x * grid.y;   // below 2^31 (checked by the host)
     // Resident workgroups, or more when they would take over kPipeMaxItems items each.
     const uint32_t groups =
         EKV_LOOKUP_PIPE_GRID
-            ? std::min(items, std::max(runs_pipe_resident<kCompact>(), (items + kPipeMaxItems - 1) / kPipeMaxItems))
+            ? std::min(items, std::max(runs_pipe_resident<kCompact, TableT>(), (items + kPipeMaxItems - 1) / kPipeMaxItems))
             : items;
-    resolve_runs_pipe_kernel<kCompact><<<dim3(groups), dim3(kThreads), 0, stream>>>(a, items, count,
+    resolve_runs_pipe_kernel<kCompact, TableT><<<dim3(groups), dim3(kThreads), 0, stream>>>(a, items, count,
                                                                                       FastDiv(count));
 }
 
@@ -988,9 +995,9 @@ void launch_with_table(const LookupArgs& a, int32_t map_dtype, bool compact, boo
             if constexpr (std::is_same_v<TopkT, int32_t> && std::is_same_v<TableT, int16_t>) {
                 if (bits && a.pipe) {
                     if (compact) {
-                        launch_runs_pipe<true>(a, grid, stream);
+                        launch_runs_pipe<true, int16_t>(a, grid, stream);
                     } else {
-                        launch_runs_pipe<false>(a, grid, stream);
+                        launch_runs_pipe<false, int16_t>(a, grid, stream);
                     }
                     return;
                 }
@@ -1007,6 +1014,16 @@ void launch_with_table(const LookupArgs& a, int32_t map_dtype, bool compact, boo
                         resolve_local_kernel<true><<<grid, block, lds, stream>>>(a);
                     } else {
                         resolve_local_kernel<false><<<grid, block, lds, stream>>>(a);
+                    }
+                    return;
+                }
+            }
+            if constexpr (std::is_same_v<TopkT, int32_t> && std::is_same_v<TableT, int32_t>) {
+                if (bits && a.pipe) {
+                    if (compact) {
+                        launch_runs_pipe<true, int32_t>(a, grid, stream);
+                    } else {
+                        launch_runs_pipe<false, int32_t>(a, grid, stream);
                     }
                     return;
                 }
@@ -1259,11 +1276,10 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
     const auto rows_aligned = [](const void* data, int64_t s0, int64_t n0, int64_t s1, int64_t n1) {
         return (reinterpret_cast<uintptr_t>(data) & 15) == 0 && (n0 <= 1 || s0 % 4 == 0) && (n1 <= 1 || s1 % 4 == 0);
     };
-    a.runs = EKV_LOOKUP_RUNS && local && bits_p != nullptr && topk.dtype == EKV_INT32 && block_size == 1 &&
-                     width % kIters == 0 && rows_aligned(topk.data, a.topk_sl, layers, a.topk_sb, batch) &&
-                     rows_aligned(output.data, a.out_sl, layers, a.out_sb, batch)
-                 ? 1
-                 : 0;
+    const bool pieces_layout = bits_p != nullptr && topk.dtype == EKV_INT32 && block_size == 1 &&
+                               width % kIters == 0 && rows_aligned(topk.data, a.topk_sl, layers, a.topk_sb, batch) &&
+                               rows_aligned(output.data, a.out_sl, layers, a.out_sb, batch);
+    a.runs = EKV_LOOKUP_RUNS && local && pieces_layout ? 1 : 0;
     // The prefetching form: rows of one chunk, a non-empty batch and table
     // (stray selections and requests read batch row 0 and table entry 0 of
     // row 0, and discard them), fewer than 2^31 items, and bitmap rows of at
@@ -1276,7 +1292,10 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
                              bits_p->shape[layered_table ? 2 : 1] >= 4 * bits_pieces_needed &&
                              bits_pieces_needed <= static_cast<int64_t>(kPipeBitPieces);
     // Batch and table rows are kept as 32-bit indices (all ones = none).
-    a.pipe = EKV_LOOKUP_PIPE && a.runs && dense && a.bits_staged && bits_pieces && width <= kChunkLanes &&
+    // Tables: int16 local slots, or int32 global slots in the single-level form.
+    const bool pipe_table = local || (mapping == nullptr && table.dtype == EKV_INT32);
+    a.pipe = EKV_LOOKUP_PIPE && pipe_table && pieces_layout && dense && a.bits_staged && bits_pieces &&
+                     width <= kChunkLanes &&
                      batch > 0 && batch < (int64_t{1} << 31) && a.table_rows > 0 &&
                      a.table_rows < (int64_t{1} << 31) && a.table_cols > 0 && count * layers < (int64_t{1} << 31)
                  ? 1

@@ -193,7 +193,8 @@ def test_local_slot_runs_random_configurations(gpu, coracle, seed):
 @pytest.mark.parametrize("seed", range(6))
 def test_local_slot_prefetch_many_items_per_workgroup(gpu, coracle, seed):
     # Rows of one 2048-lane chunk over bitmap rows of whole 16-byte pieces take
-    # the prefetching kernel, whose persistent grid gives each workgroup
+    # the prefetching kernel (int16 local-slot and int32 global-slot tables),
+    # whose persistent grid gives each workgroup
     # several (row, layer) items once there are more items than resident
     # workgroups (about 2048 on MI355X): here 3,000-8,000 items, with stray
     # request rows, stray selections, short lengths and negative entries.
@@ -202,7 +203,7 @@ def test_local_slot_prefetch_many_items_per_workgroup(gpu, coracle, seed):
     batch = int(rng.integers(150, 201))
     k = 8 * int(rng.integers(1, 257))
     rrows = int(rng.integers(batch // 2, batch + 1))
-    cols = 128 * int(rng.integers(1, 65))              # ceil(T / 32) a multiple of 4 words
+    cols = int(rng.integers(1, 8193)) if seed % 2 else 128 * int(rng.integers(1, 65))   # odd seeds: any T
     layered = seed != 5
     compact = seed != 4
     lengths = rng.integers(-2, cols + 5, size=batch)
@@ -235,17 +236,32 @@ def test_local_slot_prefetch_many_items_per_workgroup(gpu, coracle, seed):
                      torch.tensor(lengths, dtype=torch.int32, device=gpu), torch.tensor(selected, device=gpu),
                      output, 1, misses=misses, miss_count=counts, resident_bits=bits,
                      slot_base=torch.tensor(slot_base, device=gpu))
-    case = (seed, layers, batch, k, cols, layered)
-    assert np.array_equal(output.cpu().numpy(), want), case
-    if compact:
-        got_counts, got_misses = counts.cpu().numpy(), misses.cpu().numpy()
-        chosen = np.zeros(batch, bool)
-        chosen[selected[(selected >= 0) & (selected < batch)]] = True
-        assert np.array_equal(got_counts[:, chosen], want_counts[:, chosen]), case
-        assert (got_counts[:, ~chosen] == -5).all(), case
-        lanes = np.arange(k)
-        valid = lanes[None, None, :] < want_counts[:, :, None]
-        assert np.array_equal(np.where(valid, got_misses, 0)[:, chosen], np.where(valid, want_misses, 0)[:, chosen]), case
+    chosen = np.zeros(batch, bool)
+    chosen[selected[(selected >= 0) & (selected < batch)]] = True
+    lanes = np.arange(k)
+    valid = lanes[None, None, :] < want_counts[:, :, None]
+
+    def check(output, misses, counts, case):
+        assert np.array_equal(output.cpu().numpy(), want), case
+        if compact:
+            got_counts, got_misses = counts.cpu().numpy(), misses.cpu().numpy()
+            assert np.array_equal(got_counts[:, chosen], want_counts[:, chosen]), case
+            assert (got_counts[:, ~chosen] == -5).all(), case
+            assert np.array_equal(np.where(valid, got_misses, 0)[:, chosen],
+                                  np.where(valid, want_misses, 0)[:, chosen]), case
+
+    check(output, misses, counts, (seed, layers, batch, k, cols, layered, "int16"))
+    # The same residency as an int32 table of global slots (the int32 cast of
+    # base + local - 1, which is what the oracle compares against).
+    wrapped = (table + (1 << 31)) % (1 << 32) - (1 << 31)
+    table32 = torch.tensor(wrapped, dtype=torch.int32, device=gpu)
+    output = torch.tensor(initial, device=gpu)
+    misses = torch.full((layers, batch, k), -5, dtype=torch.int32, device=gpu) if compact else None
+    counts = torch.full((layers, batch), -5, dtype=torch.int32, device=gpu) if compact else None
+    resolve_resident(torch.tensor(topk, dtype=torch.int32, device=gpu), table32, None, torch.tensor(rows, device=gpu),
+                     torch.tensor(lengths, dtype=torch.int32, device=gpu), torch.tensor(selected, device=gpu),
+                     output, 1, misses=misses, miss_count=counts, resident_bits=build_residency_bits(table32))
+    check(output, misses, counts, (seed, layers, batch, k, cols, layered, "int32"))
 
 
 def random_planes(rng, gpu, layers, kv, rows, row_bytes):
