@@ -293,6 +293,10 @@ def run_decode_read(torch, args, device):
         bits16 = build_residency_bits(table16)
     else:
         table16, bits16, slot_base = table, bits, None
+    # The decode default: a line summary (one bit per 64 positions = one 128-byte
+    # line of the int16 table) in front of the table instead of the per-position bitmap.
+    SHIFT = 6
+    lines16 = build_residency_bits(table16, shift=SHIFT)
 
     def lookup_plain():
         resolve_resident(topk, table, None, rows, lengths, rows, slots, 1, misses=misses, miss_count=counts)
@@ -301,9 +305,13 @@ def run_decode_read(torch, args, device):
         resolve_resident(topk, table, None, rows, lengths, rows, slots, 1, misses=misses, miss_count=counts,
                          resident_bits=bits)
 
-    def lookup():
+    def lookup_bitmap():
         resolve_resident(topk, table16, None, rows, lengths, rows, slots, 1, misses=misses, miss_count=counts,
                          resident_bits=bits16, slot_base=slot_base)
+
+    def lookup():
+        resolve_resident(topk, table16, None, rows, lengths, rows, slots, 1, misses=misses, miss_count=counts,
+                         resident_bits=lines16, bits_shift=SHIFT, slot_base=slot_base)
 
     def gather():
         gather_kv(planes, slots, output)
@@ -311,7 +319,7 @@ def run_decode_read(torch, args, device):
     lookup_plain()
     plain = (slots.clone(), misses.clone(), counts.clone())
     same = torch.equal(bits, bits16)
-    for variant in (lookup_global, lookup):
+    for variant in (lookup_global, lookup_bitmap, lookup):
         variant()
         torch.cuda.synchronize()
         same = same and (torch.equal(plain[0], slots) and torch.equal(plain[2], counts)
@@ -346,16 +354,17 @@ def run_decode_read(torch, args, device):
     # them) replayed from a HIP graph.
     lookup_alone_ms = back_to_back_ms(torch, lookup)
     lookup_global_ms = back_to_back_ms(torch, lookup_global)
+    lookup_bitmap_ms = back_to_back_ms(torch, lookup_bitmap)
     # The same 20 back-to-back launches replayed from one HIP graph (no host
     # launch gaps between them), per launch.
     lookup_graph_ms = graph_replay_ms(torch, lambda: [lookup() for _ in range(20)], reps=5) / 20
-    per_layer = [(topk[l:l + 1], table16[l:l + 1], bits16[l:l + 1], slots[l:l + 1], misses[l:l + 1],
+    per_layer = [(topk[l:l + 1], table16[l:l + 1], lines16[l:l + 1], slots[l:l + 1], misses[l:l + 1],
                   counts[l:l + 1]) for l in range(L)]
 
     def lookup_by_layer():
         for tk, tb, bt, sl, ms, ct in per_layer:
             resolve_resident(tk, tb, None, rows, lengths, rows, sl, 1, misses=ms, miss_count=ct, resident_bits=bt,
-                             slot_base=slot_base)
+                             bits_shift=SHIFT, slot_base=slot_base)
 
     per_layer_graph_ms = graph_replay_ms(torch, lookup_by_layer)
     del per_layer
@@ -414,9 +423,10 @@ def run_decode_read(torch, args, device):
                                                 read_traffic("resolve_resident_hisparse_decode.md")),
              "lookup_us_per_layer_launch_graph": round(per_layer_graph_ms * 1e3 / L, 2),
              "lookup_us_back_to_back_int32_table": round(lookup_global_ms * 1e3, 2),
+             "lookup_us_back_to_back_position_bitmap": round(lookup_bitmap_ms * 1e3, 2),
              "lookup_us_without_bitmap": round(plain_phase["lookup"] * 1e3, 2),
-             "lookup_table": ("int16 local slots + slot_base, residency bitmap" if local_form
-                              else "int32 global slots, residency bitmap"),
+             "lookup_table": ("int16 local slots + slot_base, line summary (1 bit per 64 positions)" if local_form
+                              else "int32 global slots, line summary (1 bit per 64 positions)"),
              "lookup_variants_identical": same,
              "engine_gbs_same_shapes": ceilings,
              "event_spread": step_spread,

@@ -12,8 +12,12 @@ Extensions (all optional, none changes the reference behaviour):
   * mapping=None: single-level lookup, the table value is the slot itself;
   * a leading layer dimension L on topk / output (table and mapping may then
     carry it too), so all layers of a decode step resolve in one launch;
-  * resident_bits (single level only): a residency bitmap built by
-    build_residency_bits; non-resident lanes then skip their table read;
+  * resident_bits / bits_shift (single level only): a residency summary
+    built by build_residency_bits, one bit per group of 2**bits_shift
+    positions (0: per position; 6: per 128-byte line of an int16 table);
+    lanes whose group bit is clear skip their table read. A summary may be a
+    superset of the table's residency (a set bit over unresident positions
+    only costs their table reads), never a subset;
   * slot_base (single level only): the table is int16 and holds local slots
     (0 = not resident, v >= 1 = local slot v - 1 of the request); the slot
     written is slot_base[rows[r]] + v - 1. Half the bytes of an int32 table
@@ -28,7 +32,7 @@ from elastic_kv import _native
 
 
 def resolve_resident(topk, table, mapping, rows, lengths, selected, output, block_size, *,
-                     misses=None, miss_count=None, resident_bits=None, slot_base=None):
+                     misses=None, miss_count=None, resident_bits=None, bits_shift=0, slot_base=None):
     """Write only selected rows into an existing [L, B, K * block_size] tensor.
 
     For selected row r, layer l and lane o: block = topk[l, r, o // bs],
@@ -74,36 +78,52 @@ def resolve_resident(topk, table, mapping, rows, lengths, selected, output, bloc
         base_view = _native.describe(slot_base, "slot_base")
         with torch.cuda.device(device):
             status = lib.ekv_resolve_resident_local(
-                ct.byref(views[0]), ct.byref(views[1]), ct.byref(base_view), bits_view, ct.byref(views[2]),
-                ct.byref(views[3]), ct.byref(views[4]), ct.byref(views[5]), miss_view, count_view,
-                int(block_size), _native.stream_handle(device))
+                ct.byref(views[0]), ct.byref(views[1]), ct.byref(base_view), bits_view, int(bits_shift),
+                ct.byref(views[2]), ct.byref(views[3]), ct.byref(views[4]), ct.byref(views[5]), miss_view,
+                count_view, int(block_size), _native.stream_handle(device))
         _native.check(lib, status, "resolve_resident")
         return
     with torch.cuda.device(device):
-        status = entry(
-            ct.byref(views[0]), ct.byref(views[1]), mapping_view, ct.byref(views[2]),
-            ct.byref(views[3]), ct.byref(views[4]), ct.byref(views[5]), miss_view, count_view,
-            int(block_size), _native.stream_handle(device))
+        if resident_bits is not None:
+            status = entry(
+                ct.byref(views[0]), ct.byref(views[1]), mapping_view, int(bits_shift), ct.byref(views[2]),
+                ct.byref(views[3]), ct.byref(views[4]), ct.byref(views[5]), miss_view, count_view,
+                int(block_size), _native.stream_handle(device))
+        else:
+            status = entry(
+                ct.byref(views[0]), ct.byref(views[1]), mapping_view, ct.byref(views[2]),
+                ct.byref(views[3]), ct.byref(views[4]), ct.byref(views[5]), miss_view, count_view,
+                int(block_size), _native.stream_handle(device))
     _native.check(lib, status, "resolve_resident")
 
 
-def build_residency_bits(table, out=None):
-    """Residency bitmap of a single-level table: bit p of row q = table[.., q, p] != 0.
+def summary_words(context, shift=0):
+    """int32 words per row of a residency summary over `context` positions, in whole 16-byte pieces."""
+    groups = -(-context // (1 << shift))
+    return -(-(-(-groups // 32)) // 4) * 4
 
+
+def build_residency_bits(table, out=None, shift=0):
+    """Exact residency summary of a single-level table.
+
+    Bit q of row r is set when any position in [q << shift, (q + 1) << shift)
+    of table[.., r, :] is non-zero (shift 0: bit p = table[.., r, p] != 0).
     Returns an int32 tensor [.., R, W] (or fills `out`, which needs at least
-    ceil(T / 32) words per row). W is ceil(T / 32) rounded up to a multiple of
-    4: every row is whole 16-byte pieces, and the words past ceil(T / 32) are
-    zero, so the lookup can stage a row with 16-byte loads for any T.
+    ceil(ceil(T / 2**shift) / 32) words per row). W = summary_words(T, shift):
+    ceil(ceil(T / 2**shift) / 32) rounded up to a multiple of 4, so every row
+    is whole 16-byte pieces, and the words past the summary are zero, so the
+    lookup can stage a row with 16-byte loads for any T.
     """
     if table.dim() not in (2, 3):
         raise ValueError("table must be [R, T] or [L, R, T]")
-    words = -(-((table.shape[-1] + 31) // 32) // 4) * 4
     if out is None:
-        out = torch.zeros((*table.shape[:-1], words), dtype=torch.int32, device=table.device)
+        out = torch.zeros((*table.shape[:-1], summary_words(table.shape[-1], shift)), dtype=torch.int32,
+                          device=table.device)
     device = _native.device_of(table, out)
     lib = _native.kernel_library()
     table_view, out_view = _native.describe(table, "table"), _native.describe(out, "resident_bits")
     with torch.cuda.device(device):
-        status = lib.ekv_residency_bits(ct.byref(table_view), ct.byref(out_view), _native.stream_handle(device))
+        status = lib.ekv_residency_bits(ct.byref(table_view), ct.byref(out_view), int(shift),
+                                        _native.stream_handle(device))
     _native.check(lib, status, "build_residency_bits")
     return out

@@ -5,10 +5,12 @@ path (adaptive_sparse/request_residency.py:805-832, which calls SGLang's
 load_blocks_to_device_buffer_mha): after the resident lookup has produced
 slots and an ordered miss list, swap_in picks LRU victims in every
 (layer, request) hot buffer, rewrites the token->slot table (and its
-residency bitmap), patches the looked-up slots of the missed lanes and emits
+residency summary), patches the looked-up slots of the missed lanes and emits
 (host row -> slot) promotion lists; move_kv then copies those rows from the
 pinned host copy into the pool. The replacement policy is the reference's
-batch-token LRU (benchmarks/hisparse_locality_replay.py:90-99).
+batch-token LRU (benchmarks/hisparse_locality_replay.py:90-99). A token
+repeated within a row (a Top-K block listed twice) is one access by its first
+lane: the replay's rule applied to the selection with later repeats dropped.
 """
 
 import ctypes as ct
@@ -21,6 +23,8 @@ from .kv_pool import KVPlanes
 from .sparse_read import _planes_struct
 
 INT32_MIN = -(1 << 31)
+SWAP_STAMP_OVERFLOW = 1   # EKV_SWAP_STAMP_OVERFLOW
+SWAP_SHARED_REQUEST = 2   # EKV_SWAP_SHARED_REQUEST
 
 
 class HotBuffers:
@@ -28,17 +32,23 @@ class HotBuffers:
 
     table [L, R, T]: token -> global slot, int32 (0 = not resident), or with
     table_dtype=torch.int16 token -> local slot + 1 (0 = not resident; the
-    lookup then takes slot_base=self.slot_base); bits: its residency bitmap;
-    slot_token [L, R, C]: token held by each slot (-1 = empty); stamps
-    [L, R, C]: recency stamps; slot_base [R]: global slot of each request's
-    local slot 0 (request r owns slots base .. base + C - 1).
-    table and bits are views into storage whose rows are padded to a multiple
-    of 128 positions, so every row starts 16-byte aligned and the lookup can
-    stage its recent window and bitmap row with 16-byte loads.
+    lookup then takes slot_base=self.slot_base); bits: its residency summary,
+    one bit per 2**bits_shift positions (the lookup takes
+    bits_shift=self.bits_shift); slot_token [L, R, C]: token held by each
+    slot (-1 = empty); stamps [L, R, C]: recency stamps; slot_base [R]:
+    global slot of each request's local slot 0 (request r owns slots
+    base .. base + C - 1); status [1]: error bits of the swap-ins
+    (check_status reads and clears them).
+    table is a view into storage whose rows are padded to a multiple of 128
+    positions, so every row starts 16-byte aligned and the lookup can stage
+    its recent window with 16-byte loads; bits rows are whole 16-byte pieces.
+    With bits_shift > 0 the swap-in sets the bit of every inserted token but
+    keeps the bits of evicted ones (other positions of the group may still be
+    resident), so the summary is a superset; refresh_bits() makes it exact.
     """
 
     def __init__(self, layers, requests, context, capacity, device, *, slot_base=None, with_bits=True,
-                 step_counter=False, table_dtype=torch.int32):
+                 step_counter=False, table_dtype=torch.int32, bits_shift=0):
         self.layers, self.requests, self.context, self.capacity = layers, requests, context, capacity
         self.device = torch.device(device)
         if table_dtype not in (torch.int32, torch.int16):
@@ -48,8 +58,13 @@ class HotBuffers:
         kw = dict(dtype=torch.int32, device=self.device)
         padded = -(-context // 128) * 128
         self.table = torch.zeros((layers, requests, padded), dtype=table_dtype, device=self.device)[..., :context]
-        # The bitmap keeps its padded width (whole 16-byte pieces, zero past ceil(context / 32)).
-        self.bits = torch.zeros((layers, requests, padded // 32), **kw) if with_bits else None
+        self.bits_shift = int(bits_shift)
+        # The summary keeps its padded width (whole 16-byte pieces, zero past the summary's words).
+        from .resident_lookup import summary_words
+
+        words = summary_words(context, self.bits_shift)
+        self.bits = torch.zeros((layers, requests, words), **kw) if with_bits else None
+        self.status = torch.zeros(1, **kw)
         self.slot_token = torch.full((layers, requests, capacity), -1, **kw)
         self.stamps = torch.full((layers, requests, capacity), INT32_MIN, **kw)
         if slot_base is None:
@@ -77,10 +92,26 @@ class HotBuffers:
         self.slot_token.scatter_(2, local, tokens.to(torch.int32))
         rank = torch.arange(n, device=self.device, dtype=torch.int32).expand(L, R, n)
         self.stamps.scatter_(2, local, rank - n - 1)
+        self.refresh_bits()
+
+    def refresh_bits(self):
+        """Rebuild the residency summary exactly from the table (drops stale group bits)."""
         if self.bits is not None:
             from .resident_lookup import build_residency_bits
 
-            build_residency_bits(self.table, out=self.bits)
+            build_residency_bits(self.table, out=self.bits, shift=self.bits_shift)
+
+    def check_status(self):
+        """Raise if a swap-in refused a row since the last check (a synchronizing read); clears the flags."""
+        flags = int(self.status.item())
+        if flags:
+            self.status.zero_()
+            reasons = []
+            if flags & SWAP_STAMP_OVERFLOW:
+                reasons.append("recency stamps would overflow (rebase() before the step counter runs out)")
+            if flags & SWAP_SHARED_REQUEST:
+                reasons.append("two selected rows named the same request")
+            raise RuntimeError("swap_in refused rows: " + "; ".join(reasons))
 
     def rebase(self):
         """Renumber the recency stamps and restart the step counter.
@@ -116,8 +147,13 @@ def _ranks_from_stamps(stamps):
 
 
 def swap_in(topk, block_size, rows, selected, slots, misses, miss_count, buffers, host_table,
-            promote_src, promote_dst, *, step=None):
+            promote_src, promote_dst, *, step=None, check=False):
     """Run one swap-in step (see module docstring); advances buffers.step.
+
+    Rows the kernel refuses (selected rows sharing a request, stamps about
+    to overflow) change nothing and set buffers.status; check=True reads it
+    back after the call (a synchronization) and raises, otherwise call
+    buffers.check_status() when convenient.
 
     Stamps are step * 2W + lane in int32; before they would overflow, the
     buffers' stamps are renumbered (HotBuffers.rebase) and the step restarts.
@@ -137,20 +173,24 @@ def swap_in(topk, block_size, rows, selected, slots, misses, miss_count, buffers
         tensors.append(buffers.bits)
     device = _native.device_of(*tensors)
     lib = _native.kernel_library()
-    views = [_native.describe(t, "swap_in tensor") for t in tensors[:13]]
+    views = [ct.byref(_native.describe(t, "swap_in tensor")) for t in tensors[:13]]
     bits_view = ct.byref(_native.describe(buffers.bits, "bits")) if buffers.bits is not None else None
-    ordered = [views[0], views[1], views[2], views[3], views[4], views[5], views[6], None, views[7], views[8],
-               views[9], views[10], views[11], views[12]]
-    args = [ct.byref(v) if v is not None else bits_view for v in ordered]
+    status_view = ct.byref(_native.describe(buffers.status, "status"))
+    # topk | rows .. table | bits, shift | slot_token .. promote_dst
+    head, middle, tail = views[0], views[1:7], views[7:13]
+    shift = int(buffers.bits_shift)
     with torch.cuda.device(device):
         if counted:
-            counter = _native.describe(buffers.step_counter, "step_counter")
-            status = lib.ekv_swap_in_counted(args[0], int(block_size), *args[1:], ct.byref(counter),
-                                             _native.stream_handle(device))
+            counter = ct.byref(_native.describe(buffers.step_counter, "step_counter"))
+            status = lib.ekv_swap_in_counted(head, int(block_size), *middle, bits_view, shift, *tail, counter,
+                                             status_view, _native.stream_handle(device))
         else:
-            status = lib.ekv_swap_in(args[0], int(block_size), *args[1:], int(step), _native.stream_handle(device))
+            status = lib.ekv_swap_in(head, int(block_size), *middle, bits_view, shift, *tail, int(step),
+                                     status_view, _native.stream_handle(device))
     _native.check(lib, status, "swap_in")
     buffers.step = step + 1
+    if check:
+        buffers.check_status()
 
 
 def move_kv(src_planes, src_rows, dst_planes, dst_rows, counts, *, zero_below=1):

@@ -106,7 +106,8 @@ struct LookupArgs {
     int64_t map_sl, map_s, map_len;
     const int32_t* bits;                 // [L?, R, W] words, bit p of a row = table[row, p] != 0
     int64_t bits_sl, bits_sr, bits_sw;
-    int64_t bits_words;                  // words covering the table row: ceil(table_cols / 32)
+    int64_t bits_words;                  // words covering the table row: ceil(ceil(table_cols / 2^shift) / 32)
+    uint32_t bits_shift;                 // bit q of a row covers positions [q << shift, (q + 1) << shift)
     IndexRef rows, lengths, selected;
     IndexRef slot_base;                  // int16 local tables: global slot of each request's local slot 0
     int32_t* out;
@@ -124,6 +125,19 @@ struct LookupArgs {
     uint32_t block_size;
     FastDiv block_div;
 };
+
+// Residency summaries: bit q of a row covers table positions
+// [q << shift, (q + 1) << shift). shift 0 is the per-position bitmap; a
+// larger shift gives one bit per group of positions (shift 6: one bit per
+// 128-byte line of an int16 table). A set bit whose group holds no resident
+// entry only costs that lane a table read, so a summary may be a superset.
+constexpr int64_t kMaxBitsShift = 20;
+
+// Words of a summary row over `cols` positions.
+inline int64_t summary_words(int64_t cols, int64_t shift) {
+    const int64_t bits = (cols + (int64_t{1} << shift) - 1) >> shift;
+    return (bits + 31) / 32;
+}
 
 // Loads and stores of data touched once per launch (Top-K indices, slots),
 // with the non-temporal hint when EKV_LOOKUP_STREAMING is set.
@@ -406,11 +420,12 @@ __device__ __forceinline__ void resolve_single(const LookupArgs& a) {
             const bool inside = valid && rel >= 0 && rel < win.count;
             bool need = valid && !inside;
             if constexpr (kBits) {
-                const uint32_t w = inside ? 0u : p >> 5;
+                const uint32_t q = p >> a.bits_shift;
+                const uint32_t w = inside ? 0u : q >> 5;
                 const uint32_t word =
                     bits_in_lds ? staged_bits[w]
                                 : (table_ok ? static_cast<uint32_t>(*element<kDense>(bits_row, a.bits_sw, w)) : 0u);
-                need = need && ((word >> (p & 31)) & 1u);
+                need = need && ((word >> (q & 31)) & 1u);
             }
             slot[i] = inside ? entry_slot<TableT>(window[rel], base) : (valid ? 0 : -1);
             at[i] = need ? p : 0u;
@@ -533,10 +548,11 @@ __device__ __forceinline__ void resolve_local_runs(const LookupArgs& a) {
         for (int j = 0; j < kIters; ++j) {
             const bool valid = live[j / kPiece] && table_ok && block[j] >= 0 && block[j] < bound;
             const uint32_t p = valid ? static_cast<uint32_t>(block[j]) : 0u;
+            const uint32_t q = p >> a.bits_shift;
             const uint32_t word =
-                bits_in_lds ? lds[p >> 5]
-                            : (table_ok ? static_cast<uint32_t>(*element<true>(bits_row, 1, p >> 5)) : 0u);
-            const bool resident = valid && ((word >> (p & 31)) & 1u);
+                bits_in_lds ? lds[q >> 5]
+                            : (table_ok ? static_cast<uint32_t>(*element<true>(bits_row, 1, q >> 5)) : 0u);
+            const bool resident = valid && ((word >> (q & 31)) & 1u);
             slot[j] = valid ? 0 : -1;
             at[j] = resident ? p : 0u;
             need |= static_cast<uint32_t>(resident) << j;
@@ -646,7 +662,7 @@ void resolve_runs_kernel(const LookupArgs a) {
 #ifndef EKV_LOOKUP_PIPE_GRID
 #define EKV_LOOKUP_PIPE_GRID 1   // 1: persistent grid (resident workgroups); 0: one item per workgroup
 #endif
-constexpr uint32_t kPipeBitPieces = 2 * kThreads;   // 16-byte bitmap pieces per item: 2048 words
+constexpr uint32_t kPipeBitPieces = 2 * kThreads;   // 16-byte bitmap pieces per item at most: 2048 words
 constexpr uint32_t kPipeMaxItems = 16;              // items per workgroup
 constexpr uint32_t kNoRow = 0xffffffffu;
 
@@ -658,10 +674,13 @@ struct RunsMeta {
 };
 
 // The per-thread loads of one item: Top-K ids of lanes [4t, +4) and
-// [1024 + 4t, +4), bitmap pieces t and 256 + t (clamped to the row).
+// [1024 + 4t, +4), bitmap pieces t and (kBitLoads = 2) 256 + t, clamped to
+// the row. Rows of at most 256 pieces (1024 words: a per-position bitmap of
+// T <= 32768, or a coarser summary) take one piece per thread.
+template <int kBitLoads>
 struct RunsLoads {
     i32x4 ids[2];
-    i32x4 bits[2];
+    i32x4 bits[kBitLoads];
 };
 
 // The loads of one item. A stray selection reads batch row 0 and a request
@@ -669,10 +688,11 @@ struct RunsLoads {
 // (uniform) every thread reads the first 16-byte piece of both rows: the
 // workgroup's last iteration issues loads nobody uses, and one line each keeps
 // them unconditional without fetching two more rows.
-__device__ __forceinline__ RunsLoads runs_issue(const LookupArgs& a, uint32_t layer, const RunsMeta& m,
-                                                bool first_only) {
+template <int kBitLoads>
+__device__ __forceinline__ RunsLoads<kBitLoads> runs_issue(const LookupArgs& a, uint32_t layer, const RunsMeta& m,
+                                                           bool first_only) {
     constexpr uint32_t kHalf = kThreads * 4;
-    RunsLoads l;
+    RunsLoads<kBitLoads> l;
     const uint32_t row = m.row != kNoRow ? m.row : 0u;
     const int32_t* topk = static_cast<const int32_t*>(a.topk) + layer * a.topk_sl + row * a.topk_sb;
 #pragma unroll
@@ -685,7 +705,7 @@ __device__ __forceinline__ RunsLoads runs_issue(const LookupArgs& a, uint32_t la
     const int32_t* row_bits = a.bits + layer * a.bits_sl + (table_ok ? m.req : 0u) * a.bits_sr;
     const uint32_t last = table_ok && !first_only ? static_cast<uint32_t>((a.bits_words + 3) >> 2) - 1 : 0u;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < kBitLoads; ++h) {
         const uint32_t piece = h * kThreads + threadIdx.x;
         l.bits[h] = *reinterpret_cast<const i32x4*>(element<true>(row_bits, 1, 4 * (piece < last ? piece : last)));
     }
@@ -699,13 +719,13 @@ __device__ __forceinline__ RunsMeta runs_meta(const uint4* meta, uint32_t k) {
 
 // TableT: int16_t (local slot + 1 per entry, plus the request's slot base) or
 // int32_t (the global slot itself).
-template <bool kCompact, typename TableT>
+template <bool kCompact, typename TableT, int kBitLoads>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void resolve_runs_pipe_kernel(const LookupArgs a, uint32_t items, uint32_t count, FastDiv count_div) {
     constexpr uint32_t kPiece = 4;
     constexpr uint32_t kHalf = kThreads * kPiece;  // 1024 lanes
     constexpr int kWaves = kThreads / 64;
-    __shared__ __align__(16) uint32_t staged_bits[4 * kPipeBitPieces];
+    __shared__ __align__(16) uint32_t staged_bits[4 * kThreads * kBitLoads];
     __shared__ uint4 meta[kPipeMaxItems];
     __shared__ int32_t wave_totals[2 * kWaves];   // [half][wave]
     __shared__ int32_t chunk_misses[kChunkLanes];
@@ -740,18 +760,18 @@ void resolve_runs_pipe_kernel(const LookupArgs a, uint32_t items, uint32_t count
 
     RunsMeta cur = runs_meta(meta, 0);
     uint32_t layer = count_div.div(blockIdx.x);
-    RunsLoads loads = runs_issue(a, layer, cur, false);
+    RunsLoads<kBitLoads> loads = runs_issue<kBitLoads>(a, layer, cur, false);
     for (uint32_t k = 0;;) {
         const bool last_item = k + 1 >= n;
         const uint32_t k_next = last_item ? k : k + 1;
         const uint32_t layer_next = count_div.div(blockIdx.x + k_next * gridDim.x);
         const RunsMeta nxt = runs_meta(meta, k_next);
-        RunsLoads next_loads;
+        RunsLoads<kBitLoads> next_loads;
         if (cur.row != kNoRow) {  // uniform
             const bool table_ok = cur.req != kNoRow;
             if (table_ok) {
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
+                for (int h = 0; h < kBitLoads; ++h) {
                     const uint32_t piece = h * kThreads + threadIdx.x;
                     *reinterpret_cast<i32x4*>(&staged_bits[4 * (piece < last_piece ? piece : last_piece)]) =
                         loads.bits[h];
@@ -769,8 +789,9 @@ void resolve_runs_pipe_kernel(const LookupArgs a, uint32_t items, uint32_t count
             for (int j = 0; j < kIters; ++j) {
                 const bool valid = live_piece[j / kPiece] & table_ok & (block[j] >= 0) & (block[j] < cur.bound);
                 const uint32_t p = valid ? static_cast<uint32_t>(block[j]) : 0u;
-                const uint32_t word = staged_bits[p >> 5];
-                const bool resident = (static_cast<uint32_t>(valid) & (word >> (p & 31))) != 0u;
+                const uint32_t q = p >> a.bits_shift;
+                const uint32_t word = staged_bits[q >> 5];
+                const bool resident = (static_cast<uint32_t>(valid) & (word >> (q & 31))) != 0u;
                 slot[j] = valid ? 0 : -1;
                 at[j] = resident ? p : 0u;
                 need |= static_cast<uint32_t>(resident) << j;
@@ -785,7 +806,7 @@ void resolve_runs_pipe_kernel(const LookupArgs a, uint32_t items, uint32_t count
                 entry[j] = *element<true>(table, 1, at[j]);
             }
             // The next item's loads go out behind this item's table reads.
-            next_loads = runs_issue(a, layer_next, nxt, last_item);
+            next_loads = runs_issue<kBitLoads>(a, layer_next, nxt, last_item);
 #pragma unroll
             for (int j = 0; j < kIters; ++j) {
                 const int32_t e = entry[j];
@@ -857,7 +878,7 @@ void resolve_runs_pipe_kernel(const LookupArgs a, uint32_t items, uint32_t count
                 __syncthreads();  // the staged bitmap is rewritten by the next item
             }
         } else {
-            next_loads = runs_issue(a, layer_next, nxt, last_item);
+            next_loads = runs_issue<kBitLoads>(a, layer_next, nxt, last_item);
         }
         if (++k >= n) {
             break;
@@ -949,7 +970,7 @@ __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupAr
 
 // Workgroups of the prefetching kernel resident on the whole device at once,
 // per device (0 = not yet queried).
-template <bool kCompact, typename TableT>
+template <bool kCompact, typename TableT, int kBitLoads>
 uint32_t runs_pipe_resident() {
     static std::atomic<uint32_t> resident[64];
     int device = 0;
@@ -961,7 +982,8 @@ uint32_t runs_pipe_resident() {
     if (known == 0) {
         int per_cu = 0, cus = 0;
         check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                      &per_cu, reinterpret_cast<const void*>(resolve_runs_pipe_kernel<kCompact, TableT>), kThreads, 0),
+                      &per_cu, reinterpret_cast<const void*>(resolve_runs_pipe_kernel<kCompact, TableT, kBitLoads>),
+                      kThreads, 0),
                   "hipOccupancyMaxActiveBlocksPerMultiprocessor");
         check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
                   "hipDeviceGetAttribute");
@@ -971,17 +993,29 @@ uint32_t runs_pipe_resident() {
     return known;
 }
 
-template <bool kCompact, typename TableT>
-void launch_runs_pipe(const LookupArgs& a, dim3 grid, hipStream_t stream) {
+template <bool kCompact, typename TableT, int kBitLoads>
+void launch_runs_pipe_loads(const LookupArgs& a, dim3 grid, hipStream_t stream) {
     const uint32_t count = grid.x;
     const uint32_t items = grid.x * grid.y;   // below 2^31 (checked by the host)
     // Resident workgroups, or more when they would take over kPipeMaxItems items each.
     const uint32_t groups =
         EKV_LOOKUP_PIPE_GRID
-            ? std::min(items, std::max(runs_pipe_resident<kCompact, TableT>(), (items + kPipeMaxItems - 1) / kPipeMaxItems))
+            ? std::min(items, std::max(runs_pipe_resident<kCompact, TableT, kBitLoads>(),
+                                       (items + kPipeMaxItems - 1) / kPipeMaxItems))
             : items;
-    resolve_runs_pipe_kernel<kCompact, TableT><<<dim3(groups), dim3(kThreads), 0, stream>>>(a, items, count,
-                                                                                      FastDiv(count));
+    resolve_runs_pipe_kernel<kCompact, TableT, kBitLoads><<<dim3(groups), dim3(kThreads), 0, stream>>>(
+        a, items, count, FastDiv(count));
+}
+
+// One 16-byte bitmap piece per thread when the row has at most kThreads of
+// them, else two.
+template <bool kCompact, typename TableT>
+void launch_runs_pipe(const LookupArgs& a, dim3 grid, hipStream_t stream) {
+    if ((a.bits_words + 3) / 4 <= kThreads) {
+        launch_runs_pipe_loads<kCompact, TableT, 1>(a, grid, stream);
+    } else {
+        launch_runs_pipe_loads<kCompact, TableT, 2>(a, grid, stream);
+    }
 }
 
 template <typename TopkT, typename TableT>
@@ -1079,7 +1113,7 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
                      const ekv_tensor* rows_p, const ekv_tensor* lengths_p, const ekv_tensor* selected_p,
                      const ekv_tensor* output_p, const ekv_tensor* misses_p, const ekv_tensor* counts_p,
                      const ekv_tensor* bits_p, int64_t block_size, void* stream,
-                     const ekv_tensor* slot_base_p = nullptr) {
+                     const ekv_tensor* slot_base_p = nullptr, int64_t bits_shift = 0) {
     const ekv_tensor& topk = need(topk_p, "topk");
     const ekv_tensor& table = need(table_p, "table");
     const ekv_tensor& rows = need(rows_p, "rows");
@@ -1153,8 +1187,11 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
         }
         const int d = layered_table ? 1 : 0;
         need_dim(bits, d, table.shape[d], "resident_bits");
-        if (bits.shape[d + 1] < (table.shape[d + 1] + 31) / 32) {
-            throw std::invalid_argument("resident_bits needs ceil(T / 32) words per row");
+        if (bits_shift < 0 || bits_shift > kMaxBitsShift) {
+            throw std::invalid_argument("bits_shift must be 0.." + std::to_string(kMaxBitsShift));
+        }
+        if (bits.shape[d + 1] < summary_words(table.shape[d + 1], bits_shift)) {
+            throw std::invalid_argument("resident_bits needs ceil(ceil(T / 2^bits_shift) / 32) words per row");
         }
         need_data(bits, "resident_bits");
     }
@@ -1218,7 +1255,8 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
         a.bits_sl = layered_table ? bits_p->stride[0] : 0;
         a.bits_sr = bits_p->stride[d];
         a.bits_sw = bits_p->stride[d + 1];
-        a.bits_words = (a.table_cols + 31) / 32;
+        a.bits_words = summary_words(a.table_cols, bits_shift);
+        a.bits_shift = static_cast<uint32_t>(bits_shift);
     }
     a.rows = index_ref(rows, 0);
     a.lengths = index_ref(lengths, 0);
@@ -1339,7 +1377,64 @@ __global__ __launch_bounds__(kThreads) void residency_bits_kernel(const TableT* 
     }
 }
 
-int residency_bits(const ekv_tensor* table_p, const ekv_tensor* bits_p, void* stream) {
+// Summary rows of a shift > 0: one wave per summary word covers the
+// 32 << shift positions of its 32 groups, 64 consecutive entries per
+// iteration (coalesced), each lane OR-ing the bit of its entry's group; the
+// wave's bits are OR-reduced and lane 0 writes the word.
+template <typename TableT>
+__global__ __launch_bounds__(kThreads) void residency_summary_kernel(
+    const TableT* __restrict__ table, int64_t t_sl, int64_t t_sr, int64_t t_sc, int64_t rows, int64_t cols,
+    int32_t* __restrict__ bits, int64_t b_sl, int64_t b_sr, int64_t b_sw, int64_t words_per_row, int64_t total_words,
+    uint32_t shift) {
+    const int lane = threadIdx.x & 63;
+    const int64_t waves = int64_t{gridDim.x} * (kThreads / 64);
+    for (int64_t g = int64_t{blockIdx.x} * (kThreads / 64) + (threadIdx.x >> 6); g < total_words; g += waves) {
+        const int64_t word = g % words_per_row;
+        const int64_t row_index = g / words_per_row;   // layer * rows + row
+        const int64_t layer = row_index / rows;
+        const int64_t row = row_index - layer * rows;
+        const TableT* entries = table + layer * t_sl + row * t_sr;
+        const int64_t first = (word * 32) << shift;
+        const int64_t stop = std::min<int64_t>(first + (int64_t{32} << shift), cols);
+        uint32_t acc = 0;
+        for (int64_t pos = first + lane; pos < stop; pos += 64) {
+            acc |= static_cast<uint32_t>(entries[pos * t_sc] != 0) << ((pos >> shift) & 31);
+        }
+#pragma unroll
+        for (int offset = 32; offset > 0; offset >>= 1) {
+            acc |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(acc), offset));
+        }
+        if (lane == 0) {
+            bits[layer * b_sl + row * b_sr + word * b_sw] = static_cast<int32_t>(acc);
+        }
+    }
+}
+
+template <typename TableT>
+void launch_residency_bits(const ekv_tensor& table, const ekv_tensor& bits, int d, int64_t layers, int64_t rows,
+                           int64_t cols, int64_t shift, hipStream_t s) {
+    const bool layered = table.ndim == 3;
+    const int64_t t_sl = layered ? table.stride[0] : 0, b_sl = layered ? bits.stride[0] : 0;
+    const auto* entries = static_cast<const TableT*>(table.data);
+    auto* out = static_cast<int32_t*>(bits.data);
+    if (shift == 0) {
+        const int64_t groups_per_row = (cols + 63) / 64;
+        const int64_t total = layers * rows * groups_per_row;
+        const int64_t blocks = std::min<int64_t>((total + 3) / 4, 65536);
+        residency_bits_kernel<TableT><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, s>>>(
+            entries, t_sl, table.stride[d], table.stride[d + 1], rows, cols, out, b_sl, bits.stride[d],
+            bits.stride[d + 1], groups_per_row, total);
+    } else {
+        const int64_t words_per_row = summary_words(cols, shift);
+        const int64_t total = layers * rows * words_per_row;
+        const int64_t blocks = std::min<int64_t>((total + 3) / 4, 65536);
+        residency_summary_kernel<TableT><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, s>>>(
+            entries, t_sl, table.stride[d], table.stride[d + 1], rows, cols, out, b_sl, bits.stride[d],
+            bits.stride[d + 1], words_per_row, total, static_cast<uint32_t>(shift));
+    }
+}
+
+int residency_bits(const ekv_tensor* table_p, const ekv_tensor* bits_p, int64_t shift, void* stream) {
     const ekv_tensor& table = need(table_p, "table");
     const ekv_tensor& bits = need(bits_p, "resident_bits");
     if (table.dtype != EKV_INT16) {
@@ -1351,6 +1446,9 @@ int residency_bits(const ekv_tensor* table_p, const ekv_tensor* bits_p, void* st
     if (bits.dtype != EKV_INT32 || bits.ndim != table.ndim) {
         throw std::invalid_argument("resident_bits must be int32 with the table's number of dimensions");
     }
+    if (shift < 0 || shift > kMaxBitsShift) {
+        throw std::invalid_argument("bits_shift must be 0.." + std::to_string(kMaxBitsShift));
+    }
     const bool layered = table.ndim == 3;
     const int d = layered ? 1 : 0;
     const int64_t layers = layered ? table.shape[0] : 1;
@@ -1359,31 +1457,21 @@ int residency_bits(const ekv_tensor* table_p, const ekv_tensor* bits_p, void* st
     }
     need_dim(bits, d, table.shape[d], "resident_bits");
     const int64_t rows = table.shape[d], cols = table.shape[d + 1];
-    if (bits.shape[d + 1] < (cols + 31) / 32) {
-        throw std::invalid_argument("resident_bits needs ceil(T / 32) words per row");
+    if (bits.shape[d + 1] < summary_words(cols, shift)) {
+        throw std::invalid_argument("resident_bits needs ceil(ceil(T / 2^bits_shift) / 32) words per row");
     }
-    const int64_t groups_per_row = (cols + 63) / 64;
-    const int64_t total = layers * rows * groups_per_row;
-    if (total == 0) {
+    if (layers * rows * cols == 0) {
         return 0;
     }
     need_data(table, "table");
     need_data(bits, "resident_bits");
-    const int64_t blocks = std::min<int64_t>((total + 3) / 4, 65536);
     const auto s = static_cast<hipStream_t>(stream);
-    const int64_t t_sl = layered ? table.stride[0] : 0, b_sl = layered ? bits.stride[0] : 0;
     if (table.dtype == EKV_INT64) {
-        residency_bits_kernel<int64_t><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, s>>>(
-            static_cast<const int64_t*>(table.data), t_sl, table.stride[d], table.stride[d + 1], rows, cols,
-            static_cast<int32_t*>(bits.data), b_sl, bits.stride[d], bits.stride[d + 1], groups_per_row, total);
+        launch_residency_bits<int64_t>(table, bits, d, layers, rows, cols, shift, s);
     } else if (table.dtype == EKV_INT16) {
-        residency_bits_kernel<int16_t><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, s>>>(
-            static_cast<const int16_t*>(table.data), t_sl, table.stride[d], table.stride[d + 1], rows, cols,
-            static_cast<int32_t*>(bits.data), b_sl, bits.stride[d], bits.stride[d + 1], groups_per_row, total);
+        launch_residency_bits<int16_t>(table, bits, d, layers, rows, cols, shift, s);
     } else {
-        residency_bits_kernel<int32_t><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, s>>>(
-            static_cast<const int32_t*>(table.data), t_sl, table.stride[d], table.stride[d + 1], rows, cols,
-            static_cast<int32_t*>(bits.data), b_sl, bits.stride[d], bits.stride[d + 1], groups_per_row, total);
+        launch_residency_bits<int32_t>(table, bits, d, layers, rows, cols, shift, s);
     }
     check_hip(hipGetLastError(), "launch residency bits");
     return 0;
@@ -1393,22 +1481,23 @@ int residency_bits(const ekv_tensor* table_p, const ekv_tensor* bits_p, void* st
 }  // namespace ekv
 
 extern "C" int ekv_resolve_resident_bits(const ekv_tensor* topk, const ekv_tensor* table,
-                                         const ekv_tensor* resident_bits, const ekv_tensor* rows,
-                                         const ekv_tensor* lengths, const ekv_tensor* selected,
-                                         const ekv_tensor* output, const ekv_tensor* misses,
-                                         const ekv_tensor* miss_count, int64_t block_size, void* stream) {
+                                         const ekv_tensor* resident_bits, int64_t bits_shift,
+                                         const ekv_tensor* rows, const ekv_tensor* lengths,
+                                         const ekv_tensor* selected, const ekv_tensor* output,
+                                         const ekv_tensor* misses, const ekv_tensor* miss_count,
+                                         int64_t block_size, void* stream) {
     return ekv::guarded(-1, [&] {
         if (resident_bits == nullptr) {
             throw std::invalid_argument("resident_bits is required");
         }
         return ekv::resolve_resident(topk, table, nullptr, rows, lengths, selected, output, misses, miss_count,
-                                     resident_bits, block_size, stream);
+                                     resident_bits, block_size, stream, nullptr, bits_shift);
     });
 }
 
 extern "C" int ekv_resolve_resident_local(const ekv_tensor* topk, const ekv_tensor* table,
                                           const ekv_tensor* slot_base, const ekv_tensor* resident_bits,
-                                          const ekv_tensor* rows, const ekv_tensor* lengths,
+                                          int64_t bits_shift, const ekv_tensor* rows, const ekv_tensor* lengths,
                                           const ekv_tensor* selected, const ekv_tensor* output,
                                           const ekv_tensor* misses, const ekv_tensor* miss_count,
                                           int64_t block_size, void* stream) {
@@ -1417,12 +1506,13 @@ extern "C" int ekv_resolve_resident_local(const ekv_tensor* topk, const ekv_tens
             throw std::invalid_argument("slot_base is required");
         }
         return ekv::resolve_resident(topk, table, nullptr, rows, lengths, selected, output, misses, miss_count,
-                                     resident_bits, block_size, stream, slot_base);
+                                     resident_bits, block_size, stream, slot_base, bits_shift);
     });
 }
 
-extern "C" int ekv_residency_bits(const ekv_tensor* table, const ekv_tensor* resident_bits, void* stream) {
-    return ekv::guarded(-1, [&] { return ekv::residency_bits(table, resident_bits, stream); });
+extern "C" int ekv_residency_bits(const ekv_tensor* table, const ekv_tensor* resident_bits, int64_t bits_shift,
+                                  void* stream) {
+    return ekv::guarded(-1, [&] { return ekv::residency_bits(table, resident_bits, bits_shift, stream); });
 }
 
 extern "C" int ekv_resolve_resident(const ekv_tensor* topk, const ekv_tensor* table, const ekv_tensor* mapping,

@@ -14,12 +14,28 @@
 // then the least recently used entries. The i-th miss (in lane order) takes
 // the i-th victim.
 //
+// Repeated tokens. The reference's replay refuses a selection that repeats a
+// token (hisparse_locality_replay.py:55-56), but Top-K blocks expand to
+// repeats when a block id appears twice (the access-trace KAT
+// tests/test_hisparse_access_trace.py:170-199 selects [2, 3, 6, 2, 3]). This
+// kernel defines a repeated token as one access by its first lane - the
+// replay applied to the selection with later repeats dropped: a hit's stamp
+// takes its lowest lane (atomicMin in LDS), a repeated miss takes one victim
+// (an LDS hash of the miss tokens names each token's first miss), and its
+// later lanes share that slot and record empty promotions.
+//
 // One 256-thread workgroup per (row, layer): hits are touched in LDS, the
 // (stamp, slot) keys are bitonic-sorted in LDS, then each victim clears its
-// old token from the token->slot table and residency bitmap, takes the new
+// old token from the token->slot table and residency summary, takes the new
 // token, and writes one promotion (host row -> global slot) record. The
 // lookup's slot output of every miss lane is patched to its new slot, so the
 // gather that follows reads the promoted row.
+//
+// Refused rows. Two selected rows naming one request would race on its hot
+// buffer, and a step whose stamps would overflow int32 cannot be ordered:
+// such a row changes nothing, records empty promotions and ORs
+// EKV_SWAP_SHARED_REQUEST or EKV_SWAP_STAMP_OVERFLOW into the caller's
+// status word, which the host reads back.
 #include "../../include/ekv_kernels.h"
 #include "ekv_common.h"
 #include "ekv_fastdiv.h"
@@ -33,6 +49,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxCapacity = 8192;   // slots per hot buffer sortable in LDS
+constexpr int kMaxWidth = 4096;      // lanes per row whose miss tokens are hashed in LDS
+constexpr int32_t kStatusStampOverflow = EKV_SWAP_STAMP_OVERFLOW;
+constexpr int32_t kStatusSharedRequest = EKV_SWAP_SHARED_REQUEST;
 
 struct SwapArgs {
     const void* topk;
@@ -41,6 +60,7 @@ struct SwapArgs {
     uint32_t block_size;
     FastDiv block_div;
     IndexRef rows, selected, slot_base;
+    int64_t selected_count;
     int32_t* slots;                 // [L, B, W] lookup output, patched for misses
     int64_t sl_l, sl_b, sl_o;
     const int32_t* misses;          // [L, B, W] miss lanes
@@ -50,8 +70,9 @@ struct SwapArgs {
     void* table;                    // [L, R, T] token -> global slot (int32) or local slot + 1 (int16); 0 = not resident
     int32_t table16;
     int64_t tb_l, tb_r, tb_t, table_cols;
-    int32_t* bits;                  // [L, R, ceil(T/32)] residency bitmap (may be null)
+    int32_t* bits;                  // [L, R, words] residency summary (may be null)
     int64_t bt_l, bt_r, bt_w;
+    uint32_t bits_shift;            // bit q covers positions [q << shift, (q + 1) << shift)
     int32_t* slot_token;            // [L, R, C] token held by each slot (-1 = empty)
     int64_t st_l, st_r, st_c;
     int32_t* stamps;                // [L, R, C] recency stamps
@@ -66,6 +87,9 @@ struct SwapArgs {
     uint32_t width;
     int64_t step;
     const int64_t* step_counter;    // when set, the step is read from device memory (graph replays)
+    int32_t* status;                // EKV_SWAP_* error bits, OR-ed in (may be null)
+    uint32_t region_bytes;          // LDS bytes of the touch / hash / sort-key region
+    uint32_t hash_size, hash_log2;  // miss-token hash buckets: a power of two >= 2W
 };
 
 __device__ __forceinline__ int64_t lane_position(const SwapArgs& a, const void* topk_row, uint32_t lane) {
@@ -85,10 +109,54 @@ __device__ __forceinline__ void set_entry(const SwapArgs& a, int64_t offset, int
     }
 }
 
+// Exclusive prefix sum of one int per thread over the workgroup (wave64
+// shuffles, then one LDS exchange of the wave totals); `total` receives the
+// sum. Every thread must call it.
+__device__ __forceinline__ int32_t workgroup_exclusive_scan(int32_t value, int32_t* wave_totals, int32_t& total) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    int32_t inclusive = value;
+#pragma unroll
+    for (int offset = 1; offset < 64; offset <<= 1) {
+        const int32_t below = __shfl_up(inclusive, offset);
+        inclusive += lane >= offset ? below : 0;
+    }
+    if (lane == 63) {
+        wave_totals[wave] = inclusive;
+    }
+    __syncthreads();
+    int32_t before = 0;
+    total = 0;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) {
+        before += w < wave ? wave_totals[w] : 0;
+        total += wave_totals[w];
+    }
+    __syncthreads();  // wave_totals may be rewritten by the next scan
+    return before + inclusive - value;
+}
+
+__device__ __forceinline__ uint32_t token_hash(int32_t token, uint32_t log2_size) {
+    return (static_cast<uint32_t>(token) * 2654435761u) >> (32 - log2_size);
+}
+
+// Dynamic LDS of one workgroup (C = capacity, W = lanes per row):
+//   region   max(8 * pow2(C), 4 * hash_size) bytes, used three times over:
+//            touch[C] (first hit lane per slot), then the miss-token hash
+//            (miss indices), then the (stamp, slot) sort keys;
+//   stamp    [C] recency stamps;
+//   info     [W] token of miss i, later the rank of miss i among the owners;
+//   owner    [W] the first miss of the same token (-1: an entry naming no
+//            valid lane).
 __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
     extern __shared__ unsigned char shared[];
-    uint64_t* keys = reinterpret_cast<uint64_t*>(shared);                     // capacity_pow2 entries
-    int32_t* stamp = reinterpret_cast<int32_t*>(keys + a.capacity_pow2);      // capacity entries
+    __shared__ int32_t wave_totals[kThreads / 64];
+    uint64_t* keys = reinterpret_cast<uint64_t*>(shared);
+    int32_t* touch = reinterpret_cast<int32_t*>(shared);
+    int32_t* hash = reinterpret_cast<int32_t*>(shared);
+    int32_t* stamp = reinterpret_cast<int32_t*>(shared + a.region_bytes);
+    int32_t* info = stamp + a.capacity;
+    int32_t* owner = info + a.width;
     const int64_t b = a.selected[blockIdx.x];
     if (b < 0 || b >= a.batch) {
         return;
@@ -98,22 +166,35 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
     if (req < 0 || req >= a.table_rows) {
         return;  // uniform: a row outside the tables has nothing resident
     }
-    const int64_t base = a.slot_base[req];
     const int64_t C = a.capacity;
     const int64_t W = a.width;
+    const int32_t counted = a.counts[l * a.ct_l + b * a.ct_b];
+    const int32_t m = counted < 0 ? 0 : (counted > W ? static_cast<int32_t>(W) : counted);
+    int32_t* promote_src = a.promote_src + l * a.ps_l + b * a.ps_b;
+    int32_t* promote_dst = a.promote_dst + l * a.pd_l + b * a.pd_b;
+    // One workgroup owns each (layer, request) hot buffer: a second selected
+    // row naming the same request would race on it, so both rows are refused.
+    bool shared_request = false;
+    for (int64_t j = threadIdx.x; j < a.selected_count; j += kThreads) {
+        const int64_t other = a.selected[j];
+        shared_request |= j != blockIdx.x && other >= 0 && other < a.batch && a.rows[other] == req;
+    }
+    shared_request = __syncthreads_or(shared_request);
     const int64_t step = a.step_counter != nullptr ? *a.step_counter : a.step;  // uniform
-    if (step < 0 || (step + 1) * 2 * W >= (int64_t{1} << 31)) {
-        // Stamps would overflow (a device counter the caller did not rebase in
-        // time): change nothing, and record empty promotions so the move that
-        // follows copies nothing; the missed lanes keep slot 0 (zero rows).
-        const int32_t counted = a.counts[l * a.ct_l + b * a.ct_b];
-        const int64_t m = counted < 0 ? 0 : (counted > W ? W : counted);
+    const bool overflow = step < 0 || (step + 1) * 2 * W >= (int64_t{1} << 31);
+    if (shared_request || overflow) {
+        // Change nothing, record empty promotions (the move that follows
+        // copies nothing; the missed lanes keep slot 0) and flag the error.
+        if (threadIdx.x == 0 && a.status != nullptr) {
+            atomicOr(a.status, shared_request ? kStatusSharedRequest : kStatusStampOverflow);
+        }
         for (int64_t i = threadIdx.x; i < m; i += kThreads) {
-            a.promote_src[l * a.ps_l + b * a.ps_b + i * a.ps_o] = -1;
-            a.promote_dst[l * a.pd_l + b * a.pd_b + i * a.pd_o] = -1;
+            promote_src[i * a.ps_o] = -1;
+            promote_dst[i * a.pd_o] = -1;
         }
         return;
     }
+    const int64_t base = a.slot_base[req];
     const int64_t stamp_base = step * 2 * W;
     int32_t* slots = a.slots + l * a.sl_l + b * a.sl_b;
     const int64_t table_row = l * a.tb_l + req * a.tb_r;   // element offset of this (layer, request) row
@@ -123,21 +204,98 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
         ? static_cast<const void*>(static_cast<const int64_t*>(a.topk) + l * a.topk_sl + b * a.topk_sb)
         : static_cast<const void*>(static_cast<const int32_t*>(a.topk) + l * a.topk_sl + b * a.topk_sb);
 
+    // Touch hits. A token repeated in the row is one access of its first lane:
+    // the slot's stamp takes the lowest lane that hit it.
     for (int64_t s = threadIdx.x; s < C; s += kThreads) {
         stamp[s] = stamps[s * a.sp_c];
+        touch[s] = INT32_MAX;
     }
     __syncthreads();
-    // Touch hits (unique tokens per row, so at most one lane per slot).
     for (int64_t o = threadIdx.x; o < W; o += kThreads) {
-        const int64_t local = static_cast<int64_t>(slots[o * a.sl_o]) - base;
-        if (slots[o * a.sl_o] > 0 && local >= 0 && local < C) {
-            stamp[local] = static_cast<int32_t>(stamp_base + o);
+        const int32_t slot = slots[o * a.sl_o];
+        const int64_t local = static_cast<int64_t>(slot) - base;
+        if (slot > 0 && local >= 0 && local < C) {
+            atomicMin(&touch[local], static_cast<int32_t>(o));
         }
     }
     __syncthreads();
-    const int32_t counted = a.counts[l * a.ct_l + b * a.ct_b];
-    const int32_t m = counted < 0 ? 0 : (counted > W ? static_cast<int32_t>(W) : counted);
+    for (int64_t s = threadIdx.x; s < C; s += kThreads) {
+        if (touch[s] != INT32_MAX) {
+            stamp[s] = static_cast<int32_t>(stamp_base + touch[s]);
+        }
+    }
+    __syncthreads();
     if (m > 0) {
+        const int32_t* misses = a.misses + l * a.mi_l + b * a.mi_b;
+        // Tokens of the miss entries (-1: the entry names no valid lane).
+        for (int32_t i = threadIdx.x; i < m; i += kThreads) {
+            const int32_t lane = misses[i * a.mi_o];
+            const int64_t token =
+                lane >= 0 && lane < W ? lane_position(a, topk_row, static_cast<uint32_t>(lane)) : int64_t{-1};
+            info[i] = token >= 0 && token < a.table_cols ? static_cast<int32_t>(token) : -1;
+        }
+        for (uint32_t h = threadIdx.x; h < a.hash_size; h += kThreads) {
+            hash[h] = -1;
+        }
+        __syncthreads();
+        // Open-addressing hash of the miss tokens: every token ends up in one
+        // bucket holding its lowest miss index. The table holds at least 2m
+        // buckets, so every probe meets its token or an empty bucket.
+        const uint32_t mask = a.hash_size - 1;
+        for (int32_t i = threadIdx.x; i < m; i += kThreads) {
+            const int32_t token = info[i];
+            if (token < 0) {
+                continue;
+            }
+            for (uint32_t h = token_hash(token, a.hash_log2);; h = (h + 1) & mask) {
+                int32_t held = hash[h];
+                if (held < 0) {
+                    held = atomicCAS(&hash[h], -1, i);
+                    if (held < 0) {
+                        break;   // claimed
+                    }
+                }
+                if (info[held] == token) {
+                    atomicMin(&hash[h], i);
+                    break;
+                }
+            }
+        }
+        __syncthreads();
+        for (int32_t i = threadIdx.x; i < m; i += kThreads) {
+            const int32_t token = info[i];
+            int32_t first = -1;
+            if (token >= 0) {
+                for (uint32_t h = token_hash(token, a.hash_log2);; h = (h + 1) & mask) {
+                    const int32_t held = hash[h];
+                    if (held < 0) {
+                        break;   // not reached: every inserted token lies on its probe path
+                    }
+                    if (info[held] == token) {
+                        first = held;
+                        break;
+                    }
+                }
+            }
+            owner[i] = first;
+        }
+        __syncthreads();
+        // Rank of each first miss among the first misses, in miss-list order:
+        // every thread counts a contiguous run of entries, one scan.
+        const int32_t per_thread = (m + kThreads - 1) / kThreads;
+        const int32_t run_begin = min(m, static_cast<int32_t>(threadIdx.x) * per_thread);
+        const int32_t run_end = min(m, run_begin + per_thread);
+        int32_t firsts = 0;
+        for (int32_t i = run_begin; i < run_end; ++i) {
+            firsts += owner[i] == i;
+        }
+        int32_t unique = 0;
+        int32_t rank = workgroup_exclusive_scan(firsts, wave_totals, unique);
+        for (int32_t i = run_begin; i < run_end; ++i) {
+            info[i] = owner[i] == i ? rank++ : -1;
+        }
+        // The `unique` victims: the smallest (stamp, slot) keys, empty slots
+        // (INT32_MIN) first, then the least recently used.
         for (int64_t s = threadIdx.x; s < a.capacity_pow2; s += kThreads) {
             keys[s] = s < C ? (static_cast<uint64_t>(static_cast<uint32_t>(stamp[s]) ^ 0x80000000u) << 32) |
                                   static_cast<uint64_t>(s)
@@ -161,39 +319,45 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
                 __syncthreads();
             }
         }
-        const int32_t* misses = a.misses + l * a.mi_l + b * a.mi_b;
-        int32_t* promote_src = a.promote_src + l * a.ps_l + b * a.ps_b;
-        int32_t* promote_dst = a.promote_dst + l * a.pd_l + b * a.pd_b;
         int32_t* bits = a.bits != nullptr ? a.bits + l * a.bt_l + req * a.bt_r : nullptr;
-        for (int64_t i = threadIdx.x; i < m; i += kThreads) {
-            const int64_t victim = static_cast<int64_t>(keys[i] & 0xffffffffu);
+        for (int32_t i = threadIdx.x; i < m; i += kThreads) {
+            const int32_t first = owner[i];
             const int32_t lane = misses[i * a.mi_o];
-            const int64_t token =
-                lane >= 0 && lane < W ? lane_position(a, topk_row, static_cast<uint32_t>(lane)) : int64_t{-1};
-            if (victim >= C || token < 0 || token >= a.table_cols) {
-                // Not an entry of a miss list written by the lookup: record
-                // an empty promotion so the move that follows skips it.
+            if (first < 0) {
+                // Not an entry of a miss list written by the lookup: record an
+                // empty promotion so the move that follows skips it.
                 promote_src[i * a.ps_o] = -1;
                 promote_dst[i * a.pd_o] = -1;
                 continue;
             }
+            const int64_t victim = static_cast<int64_t>(keys[info[first]] & 0xffffffffu);
+            const int32_t global = static_cast<int32_t>(base + victim);
+            slots[static_cast<int64_t>(lane) * a.sl_o] = global;
+            if (first != i) {
+                // A repeat of an earlier miss: it shares that miss's slot and promotion.
+                promote_src[i * a.ps_o] = -1;
+                promote_dst[i * a.pd_o] = -1;
+                continue;
+            }
+            const int64_t token = lane_position(a, topk_row, static_cast<uint32_t>(lane));
             const int32_t old = slot_token[victim * a.st_c];
             if (old >= 0 && old < a.table_cols) {
                 set_entry(a, table_row + old * a.tb_t, 0);
-                if (bits != nullptr) {
+                if (bits != nullptr && a.bits_shift == 0) {
+                    // A coarser summary keeps the bit of the group (other
+                    // positions of it may still be resident); it stays a superset.
                     atomicAnd(reinterpret_cast<unsigned int*>(bits + (old >> 5) * a.bt_w), ~(1u << (old & 31)));
                 }
             }
-            const int32_t global = static_cast<int32_t>(base + victim);
             set_entry(a, table_row + token * a.tb_t, a.table16 ? static_cast<int32_t>(victim + 1) : global);
             if (bits != nullptr) {
-                atomicOr(reinterpret_cast<unsigned int*>(bits + (token >> 5) * a.bt_w), 1u << (token & 31));
+                const int64_t q = token >> a.bits_shift;
+                atomicOr(reinterpret_cast<unsigned int*>(bits + (q >> 5) * a.bt_w), 1u << (q & 31));
             }
             slot_token[victim * a.st_c] = static_cast<int32_t>(token);
             stamp[victim] = static_cast<int32_t>(stamp_base + W + lane);
             promote_src[i * a.ps_o] = static_cast<int32_t>(a.host_table[req * a.host_sr + token * a.host_st]);
             promote_dst[i * a.pd_o] = global;
-            slots[static_cast<int64_t>(lane) * a.sl_o] = global;
         }
         __syncthreads();
     }
@@ -217,10 +381,10 @@ void need_i32(const ekv_tensor& t, const char* name) {
 
 int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows_p, const ekv_tensor* selected_p,
             const ekv_tensor* slots_p, const ekv_tensor* misses_p, const ekv_tensor* counts_p,
-            const ekv_tensor* table_p, const ekv_tensor* bits_p, const ekv_tensor* slot_token_p,
+            const ekv_tensor* table_p, const ekv_tensor* bits_p, int64_t bits_shift, const ekv_tensor* slot_token_p,
             const ekv_tensor* stamps_p, const ekv_tensor* slot_base_p, const ekv_tensor* host_table_p,
             const ekv_tensor* promote_src_p, const ekv_tensor* promote_dst_p, int64_t step,
-            const ekv_tensor* step_counter_p, void* stream) {
+            const ekv_tensor* step_counter_p, const ekv_tensor* status_p, void* stream) {
     const ekv_tensor& topk = need(topk_p, "topk");
     const ekv_tensor& rows = need(rows_p, "rows");
     const ekv_tensor& selected = need(selected_p, "selected");
@@ -270,8 +434,19 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
     if (W > C) {
         throw std::invalid_argument("lanes per row exceed the hot capacity");
     }
+    if (W > kMaxWidth) {
+        throw std::invalid_argument("at most " + std::to_string(kMaxWidth) + " lanes per row");
+    }
     if (T >= (int64_t{1} << 31) || step < 0 || (step + 1) * 2 * W >= (int64_t{1} << 31)) {
         throw std::invalid_argument("token count or step outside the 32-bit stamp range");
+    }
+    int32_t* status = nullptr;
+    if (status_p != nullptr) {
+        const ekv_tensor& st = need(status_p, "status");
+        if (st.dtype != EKV_INT32 || numel(st) != 1 || st.data == nullptr) {
+            throw std::invalid_argument("status must be one int32 element in device memory");
+        }
+        status = static_cast<int32_t*>(st.data);
     }
     int64_t* counter = nullptr;
     if (step_counter_p != nullptr) {
@@ -299,8 +474,12 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
         need_i32(bits, "resident_bits");
         need_dim(bits, 0, L, "resident_bits");
         need_dim(bits, 1, R, "resident_bits");
-        if (bits.shape[2] < (T + 31) / 32) {
-            throw std::invalid_argument("resident_bits needs ceil(T / 32) words per row");
+        if (bits_shift < 0 || bits_shift > 20) {
+            throw std::invalid_argument("bits_shift must be 0..20");
+        }
+        const int64_t summary_bits = (T + (int64_t{1} << bits_shift) - 1) >> bits_shift;
+        if (bits.shape[2] < (summary_bits + 31) / 32) {
+            throw std::invalid_argument("resident_bits needs ceil(ceil(T / 2^bits_shift) / 32) words per row");
         }
     }
     const int64_t count = selected.shape[0];
@@ -337,7 +516,10 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
     if (bits_p != nullptr) {
         a.bits = static_cast<int32_t*>(bits_p->data);
         a.bt_l = bits_p->stride[0], a.bt_r = bits_p->stride[1], a.bt_w = bits_p->stride[2];
+        a.bits_shift = static_cast<uint32_t>(bits_shift);
     }
+    a.selected_count = count;
+    a.status = status;
     a.slot_token = static_cast<int32_t*>(slot_token.data);
     a.st_l = slot_token.stride[0], a.st_r = slot_token.stride[1], a.st_c = slot_token.stride[2];
     a.stamps = static_cast<int32_t*>(stamps.data);
@@ -364,7 +546,16 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
                           &slot_base, &host_table, &promote_src, &promote_dst}) {
         need_data(*t, "tensor");
     }
-    const size_t lds = static_cast<size_t>(a.capacity_pow2) * sizeof(uint64_t) + static_cast<size_t>(C) * 4;
+    a.hash_size = 2;
+    a.hash_log2 = 1;
+    while (a.hash_size < 2 * W) {
+        a.hash_size <<= 1;
+        ++a.hash_log2;
+    }
+    const size_t region = std::max<size_t>(static_cast<size_t>(a.capacity_pow2) * sizeof(uint64_t),
+                                           static_cast<size_t>(a.hash_size) * sizeof(int32_t));
+    a.region_bytes = static_cast<uint32_t>(region);
+    const size_t lds = region + static_cast<size_t>(C) * 4 + static_cast<size_t>(W) * 8;
     if (lds > 64 * 1024) {
         check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(swap_in_kernel),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)),
@@ -387,29 +578,30 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
 extern "C" int ekv_swap_in(const ekv_tensor* topk, int64_t block_size, const ekv_tensor* rows,
                            const ekv_tensor* selected, const ekv_tensor* slots, const ekv_tensor* misses,
                            const ekv_tensor* miss_count, const ekv_tensor* table, const ekv_tensor* resident_bits,
-                           const ekv_tensor* slot_token, const ekv_tensor* stamps, const ekv_tensor* slot_base,
-                           const ekv_tensor* host_table, const ekv_tensor* promote_src,
-                           const ekv_tensor* promote_dst, int64_t step, void* stream) {
+                           int64_t bits_shift, const ekv_tensor* slot_token, const ekv_tensor* stamps,
+                           const ekv_tensor* slot_base, const ekv_tensor* host_table, const ekv_tensor* promote_src,
+                           const ekv_tensor* promote_dst, int64_t step, const ekv_tensor* status, void* stream) {
     return ekv::guarded(-1, [&] {
         return ekv::swap_in(topk, block_size, rows, selected, slots, misses, miss_count, table, resident_bits,
-                            slot_token, stamps, slot_base, host_table, promote_src, promote_dst, step, nullptr,
-                            stream);
+                            bits_shift, slot_token, stamps, slot_base, host_table, promote_src, promote_dst, step,
+                            nullptr, status, stream);
     });
 }
 
 extern "C" int ekv_swap_in_counted(const ekv_tensor* topk, int64_t block_size, const ekv_tensor* rows,
                                    const ekv_tensor* selected, const ekv_tensor* slots, const ekv_tensor* misses,
                                    const ekv_tensor* miss_count, const ekv_tensor* table,
-                                   const ekv_tensor* resident_bits, const ekv_tensor* slot_token,
-                                   const ekv_tensor* stamps, const ekv_tensor* slot_base,
-                                   const ekv_tensor* host_table, const ekv_tensor* promote_src,
-                                   const ekv_tensor* promote_dst, const ekv_tensor* step_counter, void* stream) {
+                                   const ekv_tensor* resident_bits, int64_t bits_shift,
+                                   const ekv_tensor* slot_token, const ekv_tensor* stamps,
+                                   const ekv_tensor* slot_base, const ekv_tensor* host_table,
+                                   const ekv_tensor* promote_src, const ekv_tensor* promote_dst,
+                                   const ekv_tensor* step_counter, const ekv_tensor* status, void* stream) {
     return ekv::guarded(-1, [&] {
         if (step_counter == nullptr) {
             throw std::invalid_argument("step_counter is required");
         }
         return ekv::swap_in(topk, block_size, rows, selected, slots, misses, miss_count, table, resident_bits,
-                            slot_token, stamps, slot_base, host_table, promote_src, promote_dst, 0, step_counter,
-                            stream);
+                            bits_shift, slot_token, stamps, slot_base, host_table, promote_src, promote_dst, 0,
+                            step_counter, status, stream);
     });
 }

@@ -11,7 +11,7 @@ import torch
 
 from .backing import _load_library, library_path
 
-EKV_ABI_VERSION = 1
+EKV_ABI_VERSION = 2
 
 _DTYPE_CODES = {
     torch.int32: 1,
@@ -62,16 +62,20 @@ _P_TENSOR = ct.POINTER(EkvTensor)
 _SIGNATURES = {
     "ekv_abi_version": ([], ct.c_int),
     "ekv_resolve_resident": ([_P_TENSOR] * 9 + [ct.c_int64, ct.c_void_p], ct.c_int),
-    "ekv_resolve_resident_bits": ([_P_TENSOR] * 9 + [ct.c_int64, ct.c_void_p], ct.c_int),
-    "ekv_resolve_resident_local": ([_P_TENSOR] * 10 + [ct.c_int64, ct.c_void_p], ct.c_int),
-    "ekv_residency_bits": ([_P_TENSOR, _P_TENSOR, ct.c_void_p], ct.c_int),
+    "ekv_resolve_resident_bits": ([_P_TENSOR] * 3 + [ct.c_int64] + [_P_TENSOR] * 6 + [ct.c_int64, ct.c_void_p],
+                                  ct.c_int),
+    "ekv_resolve_resident_local": ([_P_TENSOR] * 4 + [ct.c_int64] + [_P_TENSOR] * 6 + [ct.c_int64, ct.c_void_p],
+                                   ct.c_int),
+    "ekv_residency_bits": ([_P_TENSOR, _P_TENSOR, ct.c_int64, ct.c_void_p], ct.c_int),
     "ekv_gather_rows": ([_P_TENSOR] * 7 + [ct.c_int64, ct.c_int64, ct.c_int, ct.c_void_p], ct.c_int),
     "ekv_gather_kv": ([ct.POINTER(EkvPlanes), _P_TENSOR, ct.POINTER(EkvKvRows), ct.c_int64, ct.c_void_p],
                       ct.c_int),
     "ekv_scatter_kv": ([ct.POINTER(EkvPlanes), _P_TENSOR, ct.POINTER(EkvKvRows), ct.c_int64, ct.c_void_p],
                        ct.c_int),
-    "ekv_swap_in": ([_P_TENSOR, ct.c_int64] + [_P_TENSOR] * 13 + [ct.c_int64, ct.c_void_p], ct.c_int),
-    "ekv_swap_in_counted": ([_P_TENSOR, ct.c_int64] + [_P_TENSOR] * 14 + [ct.c_void_p], ct.c_int),
+    "ekv_swap_in": ([_P_TENSOR, ct.c_int64] + [_P_TENSOR] * 7 + [ct.c_int64] + [_P_TENSOR] * 6
+                    + [ct.c_int64, _P_TENSOR, ct.c_void_p], ct.c_int),
+    "ekv_swap_in_counted": ([_P_TENSOR, ct.c_int64] + [_P_TENSOR] * 7 + [ct.c_int64] + [_P_TENSOR] * 8
+                            + [ct.c_void_p], ct.c_int),
     "ekv_move_kv": ([ct.POINTER(EkvPlanes), _P_TENSOR, ct.POINTER(EkvPlanes), _P_TENSOR, _P_TENSOR, ct.c_int64,
                      ct.c_void_p], ct.c_int),
     "ekv_compare_kv": ([ct.POINTER(EkvPlanes), _P_TENSOR, ct.POINTER(EkvPlanes), _P_TENSOR, _P_TENSOR,

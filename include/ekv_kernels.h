@@ -62,7 +62,7 @@ typedef struct ekv_kv_rows {
 } ekv_kv_rows;
 
 /* ABI revision of this header; bumped on any incompatible change. */
-#define EKV_ABI_VERSION 1
+#define EKV_ABI_VERSION 2
 int ekv_abi_version(void);
 
 /*
@@ -98,21 +98,28 @@ int ekv_resolve_resident(const ekv_tensor* topk, const ekv_tensor* table,
                          void* stream);
 
 /*
- * Single-level resident lookup with a residency bitmap in front of the table.
- * Same contract as ekv_resolve_resident with mapping = NULL; resident_bits
- * [R, W] or [L, R, W] int32 (W >= ceil(T/32)) must hold bit p of row q set
- * exactly when table[q, p] != 0 (ekv_residency_bits builds it). Lanes whose
- * bit is clear return slot 0 without reading their table entry, so random
- * misses cost one bit of bandwidth instead of a cache line.
+ * Single-level resident lookup with a residency summary in front of the
+ * table. Same contract as ekv_resolve_resident with mapping = NULL.
+ * resident_bits [R, W] or [L, R, W] int32 is a bit row per table row: bit q
+ * covers positions [q << bits_shift, (q + 1) << bits_shift), so
+ * W >= ceil(ceil(T / 2^bits_shift) / 32). Bit q must be set whenever a
+ * position it covers has table[., p] != 0; a set bit over positions that
+ * are all 0 is allowed (a superset only costs table reads).
+ *   bits_shift = 0: one bit per position (ekv_residency_bits keeps it exact);
+ *   bits_shift = 6: one bit per 64 positions = one 128-byte line of an int16
+ *   table, 1/64 of the per-position bitmap's bytes.
+ * Lanes whose bit is clear return slot 0 without reading their table entry,
+ * so misses in unresident groups cost one bit instead of a cache line.
+ * 0 <= bits_shift <= 20.
  * No reference counterpart: an acceleration of ekv_resolve_resident
  * (adaptive_sparse/resident_lookup.py:29-40 semantics are unchanged).
  */
 int ekv_resolve_resident_bits(const ekv_tensor* topk, const ekv_tensor* table,
-                              const ekv_tensor* resident_bits, const ekv_tensor* rows,
-                              const ekv_tensor* lengths, const ekv_tensor* selected,
-                              const ekv_tensor* output, const ekv_tensor* misses,
-                              const ekv_tensor* miss_count, int64_t block_size,
-                              void* stream);
+                              const ekv_tensor* resident_bits, int64_t bits_shift,
+                              const ekv_tensor* rows, const ekv_tensor* lengths,
+                              const ekv_tensor* selected, const ekv_tensor* output,
+                              const ekv_tensor* misses, const ekv_tensor* miss_count,
+                              int64_t block_size, void* stream);
 
 /*
  * ekv_resolve_resident (single level) over an int16 table of local slots:
@@ -128,18 +135,21 @@ int ekv_resolve_resident_bits(const ekv_tensor* topk, const ekv_tensor* table,
  */
 int ekv_resolve_resident_local(const ekv_tensor* topk, const ekv_tensor* table,
                                const ekv_tensor* slot_base, const ekv_tensor* resident_bits,
-                               const ekv_tensor* rows, const ekv_tensor* lengths,
+                               int64_t bits_shift, const ekv_tensor* rows, const ekv_tensor* lengths,
                                const ekv_tensor* selected, const ekv_tensor* output,
                                const ekv_tensor* misses, const ekv_tensor* miss_count,
                                int64_t block_size, void* stream);
 
 /*
- * resident_bits[.., q, w] bit j = (table[.., q, 32w + j] != 0) for every
- * position of the table (int16, int32 or int64); bits past T in the last word are 0.
- * No reference counterpart (maintenance of the bitmap above).
+ * Exact residency summary of a table (int16, int32 or int64): bit j of word
+ * w of row q = 1 when any position p in [(32w + j) << bits_shift,
+ * (32w + j + 1) << bits_shift) has table[.., q, p] != 0. Words
+ * 0 .. ceil(ceil(T / 2^bits_shift) / 32) - 1 are written, bits past the table
+ * are 0; words past them are left as they are.
+ * No reference counterpart (maintenance of the summary above).
  */
 int ekv_residency_bits(const ekv_tensor* table, const ekv_tensor* resident_bits,
-                       void* stream);
+                       int64_t bits_shift, void* stream);
 
 /*
  * Row gather over a fixed-position virtual layout.
@@ -185,6 +195,11 @@ int ekv_gather_kv(const ekv_planes* planes, const ekv_tensor* slots,
 int ekv_scatter_kv(const ekv_planes* planes, const ekv_tensor* slots,
                    const ekv_kv_rows* src, int64_t zero_below, void* stream);
 
+/* Error bits a swap-in ORs into its status word (a row so refused changes
+ * nothing and records empty promotions). */
+#define EKV_SWAP_STAMP_OVERFLOW 1  /* (step + 1) * 2W would reach 2^31 */
+#define EKV_SWAP_SHARED_REQUEST 2  /* two selected rows name one request */
+
 /*
  * Hot-buffer swap-in with batch-token LRU replacement, run after the lookup.
  * Policy: benchmarks/hisparse_locality_replay.py:90-99 (misses counted at
@@ -197,44 +212,51 @@ int ekv_scatter_kv(const ekv_planes* planes, const ekv_tensor* slots,
  *   misses [L, B, W], miss_count [L, B] int32: the lookup's miss list
  *   table [L, R, T] int32: token -> global slot (0 = not resident), or int16:
  *   token -> local slot + 1 (the form of ekv_resolve_resident_local), updated
- *   resident_bits [L, R, >= ceil(T/32)] int32 or NULL: kept equal to table != 0
+ *   resident_bits [L, R, words] int32 or NULL: a residency summary of the
+ *   table with bits_shift as in ekv_resolve_resident_bits; inserted tokens
+ *   set their bit, evicted tokens clear theirs only at bits_shift 0 (a
+ *   coarser summary stays a superset; ekv_residency_bits makes it exact)
  *   slot_token [L, R, C] int32 (-1 = empty), stamps [L, R, C] int32: LRU state
  *   slot_base [R]: global slot of local slot 0 of each request's hot buffer
  *   host_table [R, T]: token -> host row of the pinned host copy
  *   promote_src / promote_dst [L, B, W] int32: i < miss_count[l, b] get the
  *   host row and the global slot of the i-th promotion (feed to ekv_move_kv)
+ *   status NULL or [1] int32 in device memory: EKV_SWAP_* bits are OR-ed in
  * Stamps are step * 2W + lane; `step` must grow by one per call and keep
- * (step + 1) * 2W below 2^31. Tokens must be unique within a row, W <= C <=
- * 8192, and the selected rows must name distinct requests (one workgroup
- * updates each (layer, request) hot buffer). Miss-list entries that name no
- * valid lane get promote_src = promote_dst = -1, which ekv_move_kv skips.
+ * (step + 1) * 2W below 2^31. W <= min(C, 4096), C <= 8192.
+ * A token repeated within a row is one access by its first lane (the
+ * replay's rule applied to the selection with later repeats dropped): its
+ * later miss entries share the first one's slot and get empty promotions.
+ * Selected rows naming the same request are refused (status
+ * EKV_SWAP_SHARED_REQUEST). Miss-list entries that name no valid lane get
+ * promote_src = promote_dst = -1, which ekv_move_kv skips.
  */
 int ekv_swap_in(const ekv_tensor* topk, int64_t block_size, const ekv_tensor* rows,
                 const ekv_tensor* selected, const ekv_tensor* slots,
                 const ekv_tensor* misses, const ekv_tensor* miss_count,
-                const ekv_tensor* table, const ekv_tensor* resident_bits,
+                const ekv_tensor* table, const ekv_tensor* resident_bits, int64_t bits_shift,
                 const ekv_tensor* slot_token, const ekv_tensor* stamps,
                 const ekv_tensor* slot_base, const ekv_tensor* host_table,
                 const ekv_tensor* promote_src, const ekv_tensor* promote_dst,
-                int64_t step, void* stream);
+                int64_t step, const ekv_tensor* status, void* stream);
 
 /*
  * ekv_swap_in with the step read from device memory: step_counter [1] int64
  * holds the step of this call and is incremented after the swap-in (a second
  * launch on the same stream), so a captured HIP graph replays consecutive
  * steps. The caller keeps (step + 1) * 2W below 2^31 (rebasing the stamps
- * and the counter in time); a call past that limit changes nothing and
- * records empty promotions.
+ * and the counter in time); a call past that limit changes nothing, records
+ * empty promotions and sets EKV_SWAP_STAMP_OVERFLOW in `status`.
  * No reference counterpart: the graph-replayable form of ekv_swap_in.
  */
 int ekv_swap_in_counted(const ekv_tensor* topk, int64_t block_size, const ekv_tensor* rows,
                         const ekv_tensor* selected, const ekv_tensor* slots,
                         const ekv_tensor* misses, const ekv_tensor* miss_count,
-                        const ekv_tensor* table, const ekv_tensor* resident_bits,
+                        const ekv_tensor* table, const ekv_tensor* resident_bits, int64_t bits_shift,
                         const ekv_tensor* slot_token, const ekv_tensor* stamps,
                         const ekv_tensor* slot_base, const ekv_tensor* host_table,
                         const ekv_tensor* promote_src, const ekv_tensor* promote_dst,
-                        const ekv_tensor* step_counter, void* stream);
+                        const ekv_tensor* step_counter, const ekv_tensor* status, void* stream);
 
 /*
  * HiSparse hot-buffer swap-in with the calling convention of SGLang's

@@ -85,13 +85,18 @@ def resolve_resident(topk, table, mapping, rows, lengths, selected, block_size, 
     return out, misses, counts
 
 
-def residency_bits(table):
-    """int32 words of a residency bitmap: bit j of word w of a row = table[.., 32w + j] != 0."""
+def residency_bits(table, shift=0):
+    """int32 words of a residency summary: bit j of word w of a row = any(table[.., ((32w + j) << shift) + i] != 0
+    for i < 2**shift); shift 0 is the per-position bitmap (bit p = table[.., p] != 0)."""
     table = np.asarray(table)
     resident = table != 0
-    words = -(-table.shape[-1] // 32)
-    pad = words * 32 - table.shape[-1]
+    group = 1 << shift
+    groups = -(-table.shape[-1] // group)
+    pad = groups * group - table.shape[-1]
     resident = np.concatenate([resident, np.zeros((*table.shape[:-1], pad), bool)], axis=-1)
+    resident = resident.reshape(*table.shape[:-1], groups, group).any(-1)
+    words = -(-groups // 32)
+    resident = np.concatenate([resident, np.zeros((*table.shape[:-1], words * 32 - groups), bool)], axis=-1)
     weights = (np.uint64(1) << np.arange(32, dtype=np.uint64))
     packed = (resident.reshape(*table.shape[:-1], words, 32).astype(np.uint64) * weights).sum(-1)
     return packed.astype(np.uint32).view(np.int32)
@@ -145,11 +150,19 @@ def swap_in(step, block_size, topk, rows, selected, slots, misses, counts, table
     """Batch-token LRU swap-in after a lookup, on numpy arrays (copies are returned).
 
     Per selected row b (request r = rows[b]) of every layer: hits touch their
-    slot (stamp = step*2W + lane), the m = counts[l, b] misses take the m
-    slots with the smallest (stamp, slot) - empty slots (-2^31) first - in
-    lane order; a victim's old token leaves the table, the new token enters
-    it, its stamp becomes step*2W + W + lane, and promotion i records
-    (host_table[r, token], global slot). Returns a dict of the new arrays.
+    slot (stamp = step*2W + the lowest lane that hit it), the first miss
+    entry of every distinct token (in miss-list order) takes the next of the
+    slots with the smallest (stamp, slot) - empty slots (-2^31) first; a
+    victim's old token leaves the table, the new token enters it, its stamp
+    becomes step*2W + W + lane, and promotion i records
+    (host_table[r, token], global slot). A later miss entry of the same token
+    gets that slot and an empty promotion (-1, -1), as does an entry naming
+    no valid lane. This is benchmarks/hisparse_locality_replay.py:90-99
+    applied to the selection with repeated tokens reduced to their first
+    lane. Selected rows that share a request with another selected row, and
+    every row when (step + 1) * 2W reaches 2^31, change nothing and record
+    empty promotions; "status" returns the error bits (1 = stamp overflow,
+    2 = shared request). Returns a dict of the new arrays.
     """
     topk = np.asarray(topk, dtype=np.int64)
     L, B, K = topk.shape
@@ -158,23 +171,44 @@ def swap_in(step, block_size, topk, rows, selected, slots, misses, counts, table
     table = np.array(table, dtype=np.int32, copy=True)
     slot_token = np.array(slot_token, dtype=np.int32, copy=True)
     stamps = np.array(stamps, dtype=np.int64, copy=True)
+    R, T = table.shape[1], table.shape[2]
     C = slot_token.shape[2]
     src = np.full((L, B, W), -1, dtype=np.int32)
     dst = np.full((L, B, W), -1, dtype=np.int32)
+    live = [int(b) for b in selected if 0 <= int(b) < B and 0 <= int(rows[int(b)]) < R]
+    named = [int(rows[b]) for b in live]
+    status = 0
+    overflow = step < 0 or (step + 1) * 2 * W >= 1 << 31
     for layer in range(L):
-        for b in selected:
+        for b in live:
             r = int(rows[b])
+            if named.count(r) > 1 or overflow:
+                status |= 2 if named.count(r) > 1 else 1
+                continue
             base = int(slot_base[r])
             stamp = stamps[layer, r]
+            first_hit = {}
             for lane in range(W):
                 slot = int(slots[layer, b, lane])
                 if slot > 0 and 0 <= slot - base < C:
-                    stamp[slot - base] = step * 2 * W + lane
+                    first_hit.setdefault(slot - base, lane)
+            for local, lane in first_hit.items():
+                stamp[local] = step * 2 * W + lane
             order = sorted(range(C), key=lambda v: (stamp[v], v))
-            for i in range(int(counts[layer, b])):
-                victim = order[i]
+            taken = {}
+            m = max(0, min(int(counts[layer, b]), W))
+            for i in range(m):
                 lane = int(misses[layer, b, i])
+                if not 0 <= lane < W:
+                    continue
                 token = int(topk[layer, b, lane // block_size]) * block_size + lane % block_size
+                if not 0 <= token < T:
+                    continue
+                if token in taken:
+                    slots[layer, b, lane] = base + taken[token]
+                    continue
+                victim = order[len(taken)]
+                taken[token] = victim
                 old = int(slot_token[layer, r, victim])
                 if old >= 0:
                     table[layer, r, old] = 0
@@ -185,7 +219,7 @@ def swap_in(step, block_size, topk, rows, selected, slots, misses, counts, table
                 dst[layer, b, i] = base + victim
                 slots[layer, b, lane] = base + victim
     return {"slots": slots, "table": table, "slot_token": slot_token, "stamps": stamps.astype(np.int32),
-            "promote_src": src, "promote_dst": dst}
+            "promote_src": src, "promote_dst": dst, "status": status}
 
 
 def hisparse_swap(top_k_blocks, tokens, host_locs, dev_locs, host_k, host_v, dev_k, dev_v, req, seq, lru, hot,

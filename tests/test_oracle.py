@@ -334,8 +334,33 @@ def test_residency_bits_little_endian_words():
     assert words[1].tolist() == [0, 1 << 1, 0]
 
 
+def test_residency_summary_groups_the_bitmap():
+    """A summary at shift s is the OR of each group of 2**s bitmap bits (brute force from the definition)."""
+    table = np.zeros((2, 200), np.int64)
+    table[0, [0, 63, 64, 199]] = [5, 6, 7, 8]
+    table[1, 130] = -1
+    words = ref.residency_bits(table, shift=6).view(np.uint32)
+    assert words.shape == (2, 1)
+    assert words[0].tolist() == [0b1011] and words[1].tolist() == [0b100]
+    rng = np.random.default_rng(3)
+    for shift in (0, 1, 3, 5, 6, 7):
+        t = rng.integers(0, 2, (3, 4, 1000)) * rng.integers(1, 9, (3, 4, 1000))
+        got = ref.residency_bits(t, shift).view(np.uint32)
+        for layer in range(3):
+            for row in range(4):
+                for group in range(-(-1000 // (1 << shift))):
+                    want = bool(t[layer, row, group << shift:(group + 1) << shift].any())
+                    assert bool((got[layer, row, group // 32] >> (group % 32)) & 1) == want
+
+
 def _lookup_swap_steps(step_tokens, capacity, context, block_size=1):
-    """Drive lookup + swap-in for one (layer, request) stream; returns per-step miss counts."""
+    """Drive lookup + swap-in for one (layer, request) stream; returns per-step promotion counts.
+
+    Checks after every step that the hot buffer holds exactly the tokens of
+    an OrderedDict run of the reference policy (hisparse_locality_replay.py
+    :90-99) over the selections with repeated tokens reduced to their first
+    occurrence, in the same recency order.
+    """
     from collections import OrderedDict
 
     table = np.zeros((1, 1, context), np.int32)
@@ -343,9 +368,9 @@ def _lookup_swap_steps(step_tokens, capacity, context, block_size=1):
     stamps = np.full((1, 1, capacity), -(1 << 31), np.int32)
     host_table = np.arange(context)[None] + 1000
     model = OrderedDict()
-    misses_per_step = []
+    promoted_per_step = []
+    K = max(len(t) for t in step_tokens)
     for step, tokens in enumerate(step_tokens):
-        K = max(len(t) for t in step_tokens)
         topk = np.full((1, 1, K), -1, np.int64)
         topk[0, 0, :len(tokens)] = tokens
         out, miss_lists, counts = ref.resolve_resident(topk, table[0], None, [0], [context], [0], block_size,
@@ -356,21 +381,30 @@ def _lookup_swap_steps(step_tokens, capacity, context, block_size=1):
         state = ref.swap_in(step, block_size, topk, [0], [0], out, miss, counts, table, slot_token, stamps,
                             [1], host_table)
         table, slot_token, stamps = state["table"], state["slot_token"], state["stamps"]
-        misses_per_step.append(int(counts[0, 0]))
+        assert state["status"] == 0
         # every selected token is now resident, in the slot the patched output names
         assert all(state["slots"][0, 0, i] == table[0, 0, t] > 0 for i, t in enumerate(tokens))
-        assert state["promote_src"][0, 0, :counts[0, 0]].tolist() == [1000 + tokens[i] for i in lanes]
-        # the cache contents equal an OrderedDict run of the reference policy
-        missing = [t for t in tokens if t not in model]
-        for t in tokens:
+        # one promotion per distinct missed token, at its first miss entry
+        first_entry = {}
+        for i, lane in enumerate(lanes.tolist()):
+            first_entry.setdefault(tokens[lane], i)
+        want_src = [1000 + tokens[lane] if first_entry[tokens[lane]] == i else -1 for i, lane in enumerate(lanes)]
+        assert state["promote_src"][0, 0, :counts[0, 0]].tolist() == want_src
+        promoted_per_step.append(len(first_entry))
+        # the cache contents and order equal an OrderedDict run of the reference policy
+        unique = list(dict.fromkeys(tokens))
+        missing = [t for t in unique if t not in model]
+        for t in unique:
             if t in model:
                 model.move_to_end(t)
         while len(model) + len(missing) > capacity:
             model.popitem(last=False)
         model.update((t, None) for t in missing)
+        held = slot_token[0, 0]
+        by_recency = sorted((int(stamps[0, 0, v]), int(held[v])) for v in range(capacity) if held[v] >= 0)
+        assert [t for _, t in by_recency] == list(model)
         assert set(np.nonzero(table[0, 0])[0].tolist()) == set(model)
-        assert sorted(slot_token[0, 0][slot_token[0, 0] >= 0].tolist()) == sorted(model)
-    return misses_per_step
+    return promoted_per_step
 
 
 def test_swap_in_reproduces_reference_lru_kat():
@@ -385,6 +419,70 @@ def test_swap_in_matches_lru_replay_on_random_streams():
     for capacity, context, k in ((8, 40, 6), (16, 100, 16), (5, 12, 5)):
         steps = [rng.sample(range(context), rng.randint(1, k)) for _ in range(40)]
         assert _lookup_swap_steps(steps, capacity, context) == ref.lru_misses(steps, capacity)
+
+
+def test_swap_in_repeated_tokens_follow_the_deduplicated_replay():
+    """Repeats (a Top-K block listed twice) are one access of the first lane."""
+    rng = random.Random(31)
+    for capacity, context, k in ((8, 30, 8), (12, 50, 12), (4, 9, 4)):
+        steps = [rng.choices(range(context), k=rng.randint(1, k)) for _ in range(40)]
+        assert any(len(set(s)) < len(s) for s in steps)
+        unique = [list(dict.fromkeys(s)) for s in steps]
+        assert _lookup_swap_steps(steps, capacity, context) == ref.lru_misses(unique, capacity)
+
+
+def test_swap_in_access_trace_kat_with_a_repeated_block():
+    """tests/test_hisparse_access_trace.py:170-199: blocks [1, -1, 3, 1, 4], bs 2, seq_len 7, hot capacity 4,
+    prestate [2, 1, -1, 6] selects [2, 3, 6, 2, 3] and hits [2, 6]; token 3 misses twice and takes one slot."""
+    prestate = [2, 1, -1, 6]
+    context, bs = 10, 2
+    slot_token = np.array([[prestate]], np.int32)
+    table = np.zeros((1, 1, context), np.int32)
+    stamps = np.full((1, 1, 4), -(1 << 31), np.int32)
+    for slot, token in enumerate(prestate):
+        if token >= 0:
+            table[0, 0, token] = 1 + slot
+            stamps[0, 0, slot] = slot - 8
+    blocks = np.array([[[1, -1, 3, 1, 4]]])
+    out, miss_lists, counts = ref.resolve_resident(blocks, table[0], None, [0], [7], [0], bs,
+                                                   np.zeros((1, 1, 10), np.int32), with_misses=True)
+    lanes = miss_lists[(0, 0)].tolist()
+    assert lanes == [1, 7]              # token 3 at lanes 1 and 7 (block 1 twice)
+    miss = np.zeros((1, 1, 10), np.int32)
+    miss[0, 0, :2] = lanes
+    state = ref.swap_in(0, bs, blocks, [0], [0], out, miss, counts, table, slot_token, stamps, [1],
+                        np.arange(context)[None] + 100)
+    # the one promotion fills the empty slot 2 (global slot 3) for both lanes
+    assert state["promote_src"][0, 0, :2].tolist() == [103, -1]
+    assert state["promote_dst"][0, 0, :2].tolist() == [3, -1]
+    assert state["slots"][0, 0, 1] == state["slots"][0, 0, 7] == 3
+    assert state["slot_token"][0, 0].tolist() == [2, 1, 3, 6]
+    hits = sorted({2 * b + j for b in [1, 3] for j in range(bs) if 2 * b + j < 7} - {3})
+    assert hits == [2, 6]               # the KAT's prestate hits
+    # touch order: token 2 (lane 0) then 6 (lane 4), then the inserted 3; token 1 stays least recent
+    order = [int(state["slot_token"][0, 0, v]) for v in np.argsort(state["stamps"][0, 0], kind="stable")]
+    assert order == [1, 2, 6, 3]
+
+
+def test_swap_in_refuses_shared_requests_and_overflowing_steps():
+    table = np.zeros((1, 2, 8), np.int32)
+    slot_token = np.full((1, 2, 4), -1, np.int32)
+    stamps = np.full((1, 2, 4), -(1 << 31), np.int32)
+    topk = np.array([[[1, 2], [3, 4], [5, 6]]])
+    out = np.zeros((1, 3, 2), np.int32)
+    miss = np.array([[[0, 1], [0, 1], [0, 1]]], np.int32)
+    counts = np.full((1, 3), 2, np.int32)
+    host = np.arange(16).reshape(2, 8)
+    # rows 0 and 2 name request 1: both refused; row 1 (request 0) proceeds
+    state = ref.swap_in(0, 1, topk, [1, 0, 1], [0, 1, 2], out, miss, counts, table, slot_token, stamps, [1, 5],
+                        host)
+    assert state["status"] == 2
+    assert state["promote_src"][0, 0].tolist() == [-1, -1] and state["promote_src"][0, 2].tolist() == [-1, -1]
+    assert state["promote_src"][0, 1].tolist() == [3, 4]
+    assert state["table"][0, 1].tolist() == [0] * 8
+    state = ref.swap_in((1 << 30) // 2, 1, topk, [1, 0, 1], [1], out, miss, counts, table, slot_token, stamps,
+                        [1, 5], host)
+    assert state["status"] == 1 and state["promote_src"][0, 1].tolist() == [-1, -1]
 
 
 def _shadow_case():
