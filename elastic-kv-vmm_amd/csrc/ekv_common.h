@@ -1,6 +1,8 @@
-// Shared host-side plumbing of libelastic_vmm: error capture across the C ABI,
-// HIP status checks and a current-device guard.
+// Shared host-side plumbing of libelastic_vmm: HIP status checks, a
+// current-device guard and (from ekv_errors.h) error capture across the C ABI.
 #pragma once
+
+#include "ekv_errors.h"
 
 #include <hip/hip_runtime.h>
 
@@ -9,9 +11,6 @@
 #include <string>
 
 namespace ekv {
-
-// Thread-local message of the last failed ABI call (read by ev_error()).
-std::string& last_error();
 
 [[noreturn]] inline void fail_hip(hipError_t status, const char* what) {
     throw std::runtime_error(std::string(what) + ": " + hipGetErrorName(status) + " (" +
@@ -22,20 +21,6 @@ inline void check_hip(hipError_t status, const char* what) {
     if (status != hipSuccess) {
         fail_hip(status, what);
     }
-}
-
-// Runs `body` and converts any C++ exception into `error_value` plus a message.
-template <typename Result, typename Body>
-Result guarded(Result error_value, Body&& body) noexcept {
-    try {
-        last_error().clear();
-        return body();
-    } catch (const std::exception& e) {
-        last_error() = e.what();
-    } catch (...) {
-        last_error() = "unknown native error";
-    }
-    return error_value;
 }
 
 // Makes `device` current for the lifetime of the guard and restores the
