@@ -7,12 +7,21 @@ with 80 % of the indices from the last 4096 tokens and 20 % uniform over the
 rest, hot capacity 4096 slots per request holding the 4096 most recent tokens
 (a seeded permutation of the request's slots). The KV pool is a VMM Backing of
 2 MiB chunks. One step = resident lookup + miss compaction over all 60 layers
-(one launch) + the Top-K K/V gather of all 60 layers (one launch) into a dense
+(one launch; int16 local-slot table behind a line summary, one bit per 64
+positions) + the Top-K K/V gather of all 60 layers (one launch) into a dense
 [128, 60, 2, 2048, 256] bf16 output. `value` = the gather's algorithmic bytes
 per step (512 B written per row, + 512 B read per resident row, + 4 B slot)
 divided by the measured step time, lookup included.
 
-Other workloads (same JSON contract, for the other configurations):
+The default line also carries, as extra keys, the streaming ceilings of this
+box (own read / write / copy kernels), the lookup variants timed in
+alternating arms, and configs 1, 2 and 4 (topk-gather, block-gather,
+migration below), each with its own roofline, parity flags and CPU baseline.
+The CPU baseline is the reference's torch CPU path restated
+(oracle/torch_path.py: adaptive_sparse/request_residency.py:819-825, nonzero,
+index_select) at all visible host threads and at one thread.
+
+Other workloads (same JSON contract):
   topk-gather   8 requests x 8192 context, 28 layers x 8 heads x 128, two-level
                 lookup (req_to_token -> logical -> slot), Top-K 2048 shared by
                 all layers, hot capacity 4096 (~50 % misses)
@@ -70,9 +79,14 @@ def parse_args():
                         help="share of pool chunks unmapped and remapped per composite step")
     parser.add_argument("--capacity", type=int, default=4096, help="hot slots per request (decode-read)")
     parser.add_argument("--seed", type=int, default=2024)
-    parser.add_argument("--cpu-seconds", type=float, default=12.0, help="bound of the CPU baseline sample")
+    parser.add_argument("--cpu-seconds", type=float, default=8.0,
+                        help="bound of each CPU baseline sample (per thread count)")
+    parser.add_argument("--extras-cpu-seconds", type=float, default=3.0,
+                        help="bound of each CPU baseline sample of the extra configs")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-copy-ceiling", action="store_true")
+    parser.add_argument("--no-extras", action="store_true",
+                        help="decode-read only: skip configs 1, 2 and 4 in the default line")
     return parser.parse_args()
 
 
@@ -100,23 +114,64 @@ def time_cpu(fn, budget_s):
     return statistics.median(durations), len(durations)
 
 
-def time_copy_ceiling(torch, device, nbytes=8 << 30, reps=10):
-    """Device-to-device copy bandwidth (read + write bytes / time) of torch's copy."""
+def cpu_rates(torch, fn, nbytes, budget_s):
+    """GB/s of fn() (moving `nbytes` algorithmic bytes) at every visible host thread and at one thread."""
+    threads = len(os.sched_getaffinity(0))
+    before = torch.get_num_threads()
+    result = {}
+    try:
+        for label, count in (("all", threads), ("one", 1)):
+            torch.set_num_threads(count)
+            median, runs = time_cpu(fn, budget_s)
+            result[label] = {"gbs": round(nbytes / median / 1e9, 3), "threads": count, "runs": runs,
+                             "ms": round(median * 1e3, 2)}
+    finally:
+        torch.set_num_threads(before)
+    return result
+
+
+def cpu_budget(args, workload):
+    """Seconds per CPU-baseline sample: the full budget for the workload asked for, less for extras."""
+    return args.cpu_seconds if args.workload == workload else args.extras_cpu_seconds
+
+
+def cpu_baseline_entry(rates, sample, parity):
+    """The cpu_baseline object: the all-thread rate as `value`, the one-thread rate beside it."""
+    return {"value": rates["all"]["gbs"], "unit": "GB/s", "cores": rates["all"]["threads"], "kind": "port",
+            "value_1_thread": rates["one"]["gbs"],
+            "sample": (f"{sample}; torch CPU restatement of the reference path (oracle/torch_path.py), median of "
+                       f"{rates['all']['runs']} runs at {rates['all']['threads']} threads ({rates['all']['ms']} ms) "
+                       f"and {rates['one']['runs']} at 1 thread ({rates['one']['ms']} ms), {cpu_model()}"),
+            "parity": parity}
+
+
+def stream_ceilings(torch, device, nbytes=8 << 30, reps=10):
+    """GB/s of this box's own streaming kernels (ekv_stream_probe): read-only, write-only and copy,
+    without a workgroup cap and at 2, 3 and 4 workgroups per CU; plus torch's device copy."""
+    from elastic_kv import _native
+
+    lib = _native.kernel_library()
     src = torch.empty(nbytes, dtype=torch.uint8, device=device)
     dst = torch.empty_like(src)
     src.fill_(1)
-    dst.copy_(src)
+    result = {}
+    for name, mode, moved in (("read", 0, nbytes), ("write", 1, nbytes), ("copy", 2, 2 * nbytes)):
+        per = {}
+        for per_cu in (0, 2, 3, 4):
+            def probe(mode=mode, per_cu=per_cu):
+                status = lib.ekv_stream_probe(mode, src.data_ptr(), dst.data_ptr(), nbytes, per_cu,
+                                              _native.stream_handle(device))
+                _native.check(lib, status, "stream probe")
+
+            ms = back_to_back_ms(torch, probe, reps)
+            per["max_per_cu" if per_cu == 0 else f"{per_cu}_per_cu"] = round(moved / (ms / 1e3) / 1e9, 1)
+        result[name] = {"best_gbs": max(per.values()), **per}
     torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
-        dst.copy_(src)
-    stop.record()
-    stop.synchronize()
-    seconds = start.elapsed_time(stop) / 1000.0 / reps
+    ms = back_to_back_ms(torch, lambda: dst.copy_(src), reps)
+    result["torch_copy_gbs"] = round(2 * nbytes / (ms / 1e3) / 1e9, 1)
     del src, dst
     torch.cuda.empty_cache()
-    return 2 * nbytes / seconds / 1e9
+    return result
 
 
 def read_traffic(name):
@@ -161,10 +216,16 @@ def spread(values_ms, scale=1.0, digits=4):
     return {"median": round(statistics.median(ordered) * scale, digits), "p95": round(p95 * scale, digits)}
 
 
-def back_to_back_ms(torch, fn, reps=20):
-    """Mean event time (ms) of `reps` consecutive calls of fn on the current stream."""
+def back_to_back_ms(torch, fn, reps=20, lead=None):
+    """Mean event time (ms) of `reps` consecutive calls of fn on the current stream.
+
+    With `lead`, a longer kernel is queued first, so the host has queued the
+    timed calls before the GPU reaches them (no host launch gaps inside).
+    """
     fn()
     torch.cuda.synchronize()
+    if lead is not None:
+        lead()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(reps):
@@ -172,6 +233,31 @@ def back_to_back_ms(torch, fn, reps=20):
     stop.record()
     stop.synchronize()
     return start.elapsed_time(stop) / reps
+
+
+def in_step_events(torch, steps, phases, lead):
+    """Per-phase event times (ms) of `steps` steps queued behind `lead`, so no host launch gap is timed."""
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    lead()
+    for marks in events:
+        marks[0].record()
+        for i, (_, fn) in enumerate(phases):
+            fn()
+            marks[i + 1].record()
+    torch.cuda.synchronize()
+    return {name: [marks[i].elapsed_time(marks[i + 1]) for marks in events] for i, (name, _) in enumerate(phases)}
+
+
+def alternating_arms(torch, arms, rounds=6, reps=10, lead=None):
+    """Per-launch event times (ms) of each (name, fn) arm: every round times each arm `reps` times back to
+    back, starting from a different arm each round (scripts/bench_virtual_addressing.py:93-103 alternates
+    its arms the same way)."""
+    samples = {name: [] for name, _ in arms}
+    for r in range(rounds):
+        for name, fn in arms[r % len(arms):] + arms[:r % len(arms)]:
+            samples[name].append(back_to_back_ms(torch, fn, reps, lead))
+    return samples
 
 
 def graph_replay_ms(torch, fn, reps=10):
@@ -188,16 +274,6 @@ def graph_replay_ms(torch, fn, reps=10):
     ms = back_to_back_ms(torch, graph.replay, reps)
     del graph
     return ms
-
-
-def lookup_roofline(algorithmic_bytes, avg_ms, traffic):
-    """HBM roofline of the 60-layer lookup launch: algorithmic and (profiled) moved bytes per second."""
-    achieved = algorithmic_bytes / (avg_ms / 1e3) / 1e9
-    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "moved_gbs": None if traffic is None else round(traffic / (avg_ms / 1e3) / 1e9, 1),
-            "kernel": "resolve_runs_pipe_kernel<compact> (ekv_resolve_resident_local: int32 Top-K, int16 table, bitmap)",
-            "algorithmic_bytes_per_launch": algorithmic_bytes, "avg_launch_ms": round(avg_ms, 4)}
 
 
 def roofline(achieved_gbs, kernel, algorithmic_bytes, avg_ms, traffic):
@@ -316,15 +392,16 @@ def run_decode_read(torch, args, device):
     def gather():
         gather_kv(planes, slots, output)
 
+    # Every lookup variant must give the same slots, counts and miss lists.
+    lane = torch.arange(K, device=device).view(1, 1, K)
     lookup_plain()
-    plain = (slots.clone(), misses.clone(), counts.clone())
-    same = torch.equal(bits, bits16)
+    plain = (slots.clone(), counts.clone(), torch.where(lane < counts.unsqueeze(-1), misses, -1))
+    same = True
     for variant in (lookup_global, lookup_bitmap, lookup):
         variant()
-        torch.cuda.synchronize()
-        same = same and (torch.equal(plain[0], slots) and torch.equal(plain[2], counts)
-                         and all(torch.equal(plain[1][l, r, :c], misses[l, r, :c])
-                                 for l, r, c in ((0, 0, int(counts[0, 0])), (L - 1, R - 1, int(counts[L - 1, R - 1])))))
+        same = same and torch.equal(plain[0], slots) and torch.equal(plain[1], counts) and torch.equal(
+            plain[2], torch.where(lane < counts.unsqueeze(-1), misses, -1))
+    same = bool(same)
     del plain
     for _ in range(args.warmup):
         lookup()
@@ -335,28 +412,32 @@ def run_decode_read(torch, args, device):
     lanes = L * R * K
     lookup_bytes = 10 * lanes + 4 * miss_total + 4 * L * R   # 4 B index + 2 B table entry + 4 B slot per lookup
     gather_bytes = lanes * 2 * row_bytes + hits * 2 * row_bytes + lanes * 4
-    step_ms, phase = timed_steps(torch, args.steps, [("lookup", lookup), ("gather", gather)])
-    step_spread = {"gather_ms": spread(LAST_SAMPLES["gather"]), "lookup_us": spread(LAST_SAMPLES["lookup"], 1e3, 2)}
-    _, plain_phase = timed_steps(torch, max(3, args.steps // 2), [("lookup", lookup_plain)])
+    # The timed steps: wall clock, bracketed by synchronizations.
+    step_ms, _ = timed_steps(torch, args.steps, [("lookup", lookup), ("gather", gather)])
+    # The same steps queued behind one gather (the host runs ahead, so no launch gap is timed):
+    # per-kernel event times inside the step, the lookup right after the previous step's gather.
+    phase_samples = in_step_events(torch, args.steps, [("lookup", lookup), ("gather", gather)], gather)
+    phase = {name: statistics.mean(values) for name, values in phase_samples.items()}
+    step_spread = {"gather_ms": spread(phase_samples["gather"]), "lookup_us": spread(phase_samples["lookup"], 1e3, 2)}
+    # The lookup variants alone, back to back, in alternating arms.
+    arm_samples = alternating_arms(torch, [("line_summary", lookup), ("position_bitmap", lookup_bitmap),
+                                           ("int32_table_bitmap", lookup_global), ("int32_table_plain", lookup_plain)],
+                                   rounds=6, reps=10, lead=gather)
+    arms = {name: {"median_us": round(statistics.median(v) * 1e3, 2), "min_us": round(min(v) * 1e3, 2)}
+            for name, v in arm_samples.items()}
     # Reference points of the same engine on the same shapes: sequential slots
     # (every row read, contiguous) and all-miss slots (write-only zero fill).
     seq = (torch.arange(K, device=device, dtype=torch.int32).view(1, 1, K) + 1
            + torch.arange(R, device=device, dtype=torch.int32).view(1, R, 1) * C).expand(L, R, K).contiguous()
     none = torch.zeros_like(slots)
-    ceilings = {}
+    engine = {}
     for name, probe, nbytes in (("sequential_all_hit", seq, lanes * 2048 + lanes * 4),
                                 ("all_miss_write_only", none, lanes * 1024 + lanes * 4)):
-        _, ph = timed_steps(torch, 5, [("g", lambda s=probe: gather_kv(planes, s, output))])
-        ceilings[name] = round(nbytes / (ph["g"] / 1e3) / 1e9, 1)
+        ms = back_to_back_ms(torch, lambda s=probe: gather_kv(planes, s, output), 5)
+        engine[name] = round(nbytes / (ms / 1e3) / 1e9, 1)
     del seq, none
-    # The lookup alone: back-to-back launches of the 60-layer lookup, and one
-    # launch per layer (as a decode step interleaved with attention issues
-    # them) replayed from a HIP graph.
-    lookup_alone_ms = back_to_back_ms(torch, lookup)
-    lookup_global_ms = back_to_back_ms(torch, lookup_global)
-    lookup_bitmap_ms = back_to_back_ms(torch, lookup_bitmap)
-    # The same 20 back-to-back launches replayed from one HIP graph (no host
-    # launch gaps between them), per launch.
+    # The 20 back-to-back 60-layer launches replayed from one HIP graph, and one
+    # launch per layer (as a decode step interleaved with attention issues them).
     lookup_graph_ms = graph_replay_ms(torch, lambda: [lookup() for _ in range(20)], reps=5) / 20
     per_layer = [(topk[l:l + 1], table16[l:l + 1], lines16[l:l + 1], slots[l:l + 1], misses[l:l + 1],
                   counts[l:l + 1]) for l in range(L)]
@@ -372,63 +453,66 @@ def run_decode_read(torch, args, device):
     gather()  # the probes above overwrote the output
     torch.cuda.synchronize()
     achieved = gather_bytes / (phase["gather"] / 1e3) / 1e9
-    log(f"step {step_ms:.3f} ms, gather {phase['gather']:.3f} ms ({achieved:.0f} GB/s), "
-        f"lookup {phase['lookup'] * 1e3:.1f} us in the step (int16 local-slot table + residency bitmap; "
-        f"{plain_phase['lookup'] * 1e3:.1f} us with plain int32 table reads), {lookup_alone_ms * 1e3:.1f} us back "
-        f"to back ({lookup_graph_ms * 1e3:.1f} us replayed from a graph; {lookup_global_ms * 1e3:.1f} us with the "
-        f"int32 table + bitmap), "
+    log(f"step {step_ms:.3f} ms, gather {phase['gather']:.3f} ms ({achieved:.0f} GB/s), lookup "
+        f"{phase['lookup'] * 1e3:.1f} us in the step (median {step_spread['lookup_us']['median']} us; "
+        f"int16 table + line summary), arms {arms}, {lookup_graph_ms * 1e3:.1f} us back to back from a graph, "
         f"{per_layer_graph_ms * 1e3 / L:.2f} us per one-layer launch in a graph, identical results {same}")
 
     baseline = None
     if not args.no_cpu_baseline:
-        from oracle.oracle import COracle
+        from oracle import torch_path
 
-        oracle = COracle()
-        topk0, table0 = topk[0:1].cpu().numpy(), table[0].cpu().numpy()
-        idx, full = np.arange(R), np.full(R, T)
-        plane = layout.plane_stride
-        pool0 = raw.narrow(0, 0, 2 * plane).cpu().numpy()
-        init = np.zeros((1, R, K), np.int32)
+        # Layer 0 of the step on the host, as the reference's CPU path computes it:
+        # req_to_token -> mapping (here the hot-slot table), nonzero, index_select.
+        topk0 = topk[0].cpu()
+        mapping = table[0].reshape(-1).cpu()
+        req_to_token = torch.arange(R * T, dtype=torch.int64).view(R, T)
+        rows_c, lengths_c = rows.cpu(), lengths.cpu()
+        planes0 = raw.narrow(0, 0, 2 * layout.plane_stride).view(2, layout.plane_stride)
+        planes0 = planes0[:, :layout.plane_bytes].reshape(2, layout.rows, row_bytes).cpu()
 
         def sample():
-            s, _, _ = oracle.resolve_resident(topk0, table0, None, idx, full, idx, 1, init, with_misses=True)
-            return s, oracle.gather_kv(pool0, 2 * plane, plane, row_bytes, row_bytes, layout.rows, s, 2)
+            s, m = torch_path.lookup(topk0, req_to_token, mapping, rows_c, lengths_c, rows_c, 1)
+            return s, m, torch_path.gather(planes0, s.reshape(-1))
 
-        want_slots, want_rows = sample()
-        parity = {"lookup": bool(np.array_equal(slots[0:1].cpu().numpy(), want_slots)),
-                  "gather": bool(np.array_equal(
-                      output[:, 0:1].contiguous().view(torch.uint8).reshape(want_rows.shape).cpu().numpy(),
-                      want_rows))}
+        want_slots, want_misses, want_rows = sample()
+        got_misses = misses[0].cpu()
+        got_counts = counts[0].cpu()
+        parity = {"lookup": bool(torch.equal(slots[0].cpu(), want_slots)),
+                  "misses": bool(torch.equal(got_counts, torch.bincount(want_misses[:, 0], minlength=R).to(torch.int32))
+                                 and all(torch.equal(got_misses[r, :int(got_counts[r])],
+                                                     want_misses[want_misses[:, 0] == r, 1].to(torch.int32))
+                                         for r in range(R))),
+                  "gather": bool(torch.equal(output[:, 0].contiguous().view(torch.uint8).cpu(),
+                                             want_rows.view(2, R, K, row_bytes).transpose(0, 1)))}
+        del want_rows
         layer_hits = int((want_slots > 0).sum())
         sample_bytes = R * K * 2 * row_bytes + layer_hits * 2 * row_bytes + R * K * 4
-        median, runs = time_cpu(sample, args.cpu_seconds)
-        baseline = {"value": round(sample_bytes / median / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-                    "sample": (f"layer 0 of the same step ({R} x {K} lookups + {2 * R * K} gathered {row_bytes} B "
-                               f"rows, {sample_bytes / 1e6:.1f} MB algorithmic): C oracle on one thread, median of "
-                               f"{runs} runs ({median * 1e3:.1f} ms each), {cpu_model()}, "
-                               f"{len(os.sched_getaffinity(0))} cores visible"),
-                    "parity_layer0": parity}
-        log(f"cpu baseline {baseline['value']} GB/s, parity {parity}")
+        rates = cpu_rates(torch, sample, sample_bytes, args.cpu_seconds)
+        baseline = cpu_baseline_entry(
+            rates, f"layer 0 of the same step ({R} x {K} lookups, miss list, {2 * R * K} gathered {row_bytes} B "
+                   f"rows: {sample_bytes / 1e6:.1f} MB algorithmic)", parity)
+        log(f"cpu baseline {rates}, parity {parity}")
 
     config = {"workload": "hisparse-topk-decode-read", "requests": R, "context": T, "layers": L, "kv_heads": 2,
               "head_dim": 128, "topk": K, "hot_capacity": C, "pool_bytes": layout.capacity_bytes,
               "chunk_bytes": layout.chunk_bytes}
+    lookup_traffic = read_traffic("resolve_resident_hisparse_decode.md")
     extra = {"lookups_per_s": round(lanes / (phase["lookup"] / 1e3), 1),
              "lookup_us_per_step": round(phase["lookup"] * 1e3, 2),
              "lookup_us_per_layer": round(phase["lookup"] * 1e3 / L, 2),
              "lookup_gbs": round(lookup_bytes / (phase["lookup"] / 1e3) / 1e9, 1),
-             "lookup_us_back_to_back": round(lookup_alone_ms * 1e3, 2),
+             "lookup_roofline": roofline(lookup_bytes / (phase["lookup"] / 1e3) / 1e9,
+                                         "resolve_runs_pipe_kernel<compact, int16, 1> (ekv_resolve_resident_local: "
+                                         "int16 table, line summary), in the step", lookup_bytes, phase["lookup"],
+                                         lookup_traffic),
+             "lookup_arms_back_to_back": arms,
              "lookup_us_back_to_back_graph": round(lookup_graph_ms * 1e3, 2),
-             "lookup_roofline": lookup_roofline(lookup_bytes, lookup_alone_ms,
-                                                read_traffic("resolve_resident_hisparse_decode.md")),
              "lookup_us_per_layer_launch_graph": round(per_layer_graph_ms * 1e3 / L, 2),
-             "lookup_us_back_to_back_int32_table": round(lookup_global_ms * 1e3, 2),
-             "lookup_us_back_to_back_position_bitmap": round(lookup_bitmap_ms * 1e3, 2),
-             "lookup_us_without_bitmap": round(plain_phase["lookup"] * 1e3, 2),
              "lookup_table": ("int16 local slots + slot_base, line summary (1 bit per 64 positions)" if local_form
                               else "int32 global slots, line summary (1 bit per 64 positions)"),
              "lookup_variants_identical": same,
-             "engine_gbs_same_shapes": ceilings,
+             "engine_gbs_same_shapes": engine,
              "event_spread": step_spread,
              "hit_rate": round(hits / lanes, 4), "pool_commit_s": round(commit_s, 3)}
     roof = roofline(achieved, "copy_small_rows<KvGather,16> (ekv_gather_kv)", gather_bytes, phase["gather"],
@@ -490,29 +574,33 @@ def run_topk_gather(torch, args, device):
         f"lookup {phase['lookup'] * 1e3:.1f} us, hit rate {hits / lanes:.3f}")
     baseline = None
     if not args.no_cpu_baseline:
-        from oracle.oracle import COracle
+        from oracle import torch_path
 
-        oracle = COracle()
-        pool = raw.cpu().numpy()
-        idx, full = np.arange(R), np.full(R, T)
-        init = np.zeros((1, R, K), np.int32)
+        # The whole step on the host: the reference's two-level torch resolver once,
+        # then index_select of the 28 layers' K and V planes.
+        host_planes = raw.view(-1)[:L * 2 * layout.plane_stride].view(L, 2, layout.plane_stride)
+        host_planes = host_planes[..., :layout.plane_bytes].reshape(L, 2, layout.rows, row_bytes).cpu()
+        topk_c, table_c, map_c = torch.tensor(topk[0]), torch.tensor(table), torch.tensor(mapping)
+        idx, full = torch.arange(R), torch.full((R,), T)
 
         def sample():
-            s, _, _ = oracle.resolve_resident(topk, table, mapping, idx, full, idx, 1, init, with_misses=True)
-            return s, oracle.gather_kv(pool, planes.layer_stride, planes.kv_stride, row_bytes, row_bytes,
-                                       layout.rows, s[0], 2, shared_layers=L)
+            s, m = torch_path.lookup(topk_c, table_c, map_c, idx, full, idx, 1)
+            return s, m, [torch_path.gather(host_planes[l], s.reshape(-1)) for l in range(L)]
 
-        want_slots, want_rows = sample()
-        parity = {"lookup": bool(np.array_equal(slots.cpu().numpy(), want_slots)),
-                  "gather": bool(np.array_equal(output.view(torch.uint8).reshape(want_rows.shape).cpu().numpy(),
-                                                want_rows))}
-        del want_rows
-        median, runs = time_cpu(sample, args.cpu_seconds)
-        baseline = {"value": round(gather_bytes / median / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-                    "sample": (f"the full step (lookup + {L}-layer gather, {gather_bytes / 1e9:.2f} GB algorithmic): "
-                               f"C oracle on one thread, median of {runs} runs ({median * 1e3:.0f} ms), {cpu_model()}"),
-                    "parity_full": parity}
-        log(f"cpu baseline {baseline['value']} GB/s, parity {parity}")
+        want_slots, want_misses, want_rows = sample()
+        got_counts = counts[0].cpu()
+        got = output.view(torch.uint8).cpu()        # [R, L, 2, K, row]
+        parity = {"lookup": bool(torch.equal(slots[0].cpu(), want_slots)),
+                  "misses": bool(torch.equal(got_counts, torch.bincount(want_misses[:, 0], minlength=R)
+                                             .to(torch.int32))),
+                  "gather": all(torch.equal(got[:, l], want_rows[l].view(2, R, K, row_bytes).transpose(0, 1))
+                                for l in range(L))}
+        del want_rows, got
+        rates = cpu_rates(torch, sample, gather_bytes, cpu_budget(args, "topk-gather"))
+        baseline = cpu_baseline_entry(rates, f"the full step (two-level lookup + {L}-layer gather, "
+                                             f"{gather_bytes / 1e9:.2f} GB algorithmic)", parity)
+        del host_planes
+        log(f"cpu baseline {rates}, parity {parity}")
     config = {"workload": "resident-lookup-topk-gather", "requests": R, "context": T, "layers": L, "kv_heads": 8,
               "head_dim": 128, "topk": K, "hot_capacity": C, "lookup": "two-level (req_to_token -> mapping)"}
     extra = {"lookups_per_s": round(lanes / (phase["lookup"] / 1e3), 1),
@@ -559,28 +647,25 @@ def run_block_gather(torch, args, device):
     log(f"step {step_ms:.3f} ms, gather {phase['gather']:.3f} ms ({achieved:.0f} GB/s)")
     baseline = None
     if not args.no_cpu_baseline:
-        from oracle.oracle import COracle
+        from oracle import torch_path
 
-        oracle = COracle()
-        plane = layout.plane_stride
-        pool0 = raw.narrow(0, 0, 2 * plane).cpu().numpy()
+        planes0 = raw.narrow(0, 0, 2 * layout.plane_stride).view(2, layout.plane_stride)
+        planes0 = planes0[:, :layout.plane_bytes].reshape(2, POOL, row_bytes).cpu()
+        blocks = torch.tensor(tables, dtype=torch.int32).reshape(-1)
 
         def sample():
-            return oracle.gather_kv(pool0, 2 * plane, plane, row_bytes, row_bytes, POOL, tables[None], 2,
-                                    zero_below=0)
+            return torch_path.gather(planes0, blocks, zero_below=0)
 
         want = sample()
-        parity = bool(np.array_equal(output[:, 0:1].contiguous().view(torch.uint8).reshape(want.shape).cpu().numpy(),
-                                     want))
+        parity = {"gather": bool(torch.equal(output[:, 0].contiguous().view(torch.uint8).cpu(),
+                                             want.view(2, R, NB, row_bytes).transpose(0, 1)))}
         del want
         sample_bytes = R * NB * 2 * (2 * row_bytes + 4)
-        median, runs = time_cpu(sample, args.cpu_seconds)
-        baseline = {"value": round(sample_bytes / median / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-                    "sample": (f"layer 0 of the same step ({R * NB * 2} block-planes, {sample_bytes / 1e9:.2f} GB "
-                               f"algorithmic): C oracle on one thread, median of {runs} runs "
-                               f"({median * 1e3:.0f} ms), {cpu_model()}"),
-                    "parity_layer0": {"gather": parity}}
-        log(f"cpu baseline {baseline['value']} GB/s, parity {parity}")
+        rates = cpu_rates(torch, sample, sample_bytes, cpu_budget(args, "block-gather"))
+        baseline = cpu_baseline_entry(rates, f"layer 0 of the same step ({R * NB * 2} block-planes of {row_bytes} B, "
+                                             f"{sample_bytes / 1e9:.2f} GB algorithmic)", parity)
+        del planes0
+        log(f"cpu baseline {rates}, parity {parity}")
     config = {"workload": "vllm-block-gather", "requests": R, "blocks_per_request": NB, "block_tokens": 16,
               "layers": L, "kv_heads": 8, "head_dim": 128, "pool_blocks": POOL, "pool_bytes": layout.capacity_bytes}
     roof = roofline(achieved, "copy_small_rows<KvGather,16> (ekv_gather_kv, 32 KiB rows)", gather_bytes,
@@ -664,28 +749,26 @@ def run_migration(torch, args, device):
         f"D2H {d2h_ms:.1f} ms, H2D {h2d_ms:.1f} ms, unpack {unpack_ms:.2f} ms, verified {verified}")
     baseline = None
     if not args.no_cpu_baseline:
-        from oracle.oracle import COracle
-
-        oracle = COracle()
+        # Pack + unpack of 64 blocks in host memory with torch (index_select into
+        # staging, index_copy_ back): the byte movement without a PCIe leg.
         count = 64
-        page_ids = np.array(sorted(rng.choice(live, size=count, replace=False)))
-        host_pool = np.zeros(layout.capacity_bytes, dtype=np.uint8)
-        for p in page_ids:
-            host_pool[p * layout.block_bytes:(p + 1) * layout.block_bytes] = pool.page_view(int(p)).cpu().numpy()
-        slots = np.broadcast_to(page_ids, (layout.layers, 1, count))
-        planes = pool.planes
+        page_ids = torch.tensor(sorted(rng.choice(live, size=count, replace=False).tolist()))
+        host_pool = torch.zeros((BLOCKS, layout.block_bytes), dtype=torch.uint8)
+        for p in page_ids.tolist():
+            host_pool[p] = pool.page_view(p).cpu()
+        original = host_pool[page_ids].clone()
 
         def sample():
-            packed = oracle.gather_kv(host_pool, planes.layer_stride, planes.kv_stride, planes.row_stride,
-                                      planes.row_bytes, planes.rows, slots, layout.kv)
-            oracle.scatter_kv(host_pool, planes.layer_stride, planes.kv_stride, planes.row_stride, planes.row_bytes,
-                              planes.rows, slots, layout.kv, packed)
+            staging = host_pool.index_select(0, page_ids)
+            host_pool.index_copy_(0, page_ids, staging)
+            return staging
 
-        median, runs = time_cpu(sample, args.cpu_seconds)
-        sample_bytes = 2 * count * layout.block_bytes
-        baseline = {"value": round(sample_bytes / median / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-                    "sample": (f"pack + unpack of {count} blocks in host memory (no PCIe leg exists on the CPU path), "
-                               f"C oracle on one thread, median of {runs} runs, {cpu_model()}")}
+        parity = {"round_trip": bool(torch.equal(sample(), original) and torch.equal(host_pool[page_ids], original))}
+        sample_bytes = 2 * 2 * count * layout.block_bytes
+        rates = cpu_rates(torch, sample, sample_bytes, cpu_budget(args, "migration"))
+        baseline = cpu_baseline_entry(rates, f"pack + unpack of {count} blocks in host memory ({sample_bytes / 1e9:.2f}"
+                                             f" GB read + written; no PCIe leg exists on the CPU path)", parity)
+        del host_pool
     config = {"workload": "page-migration-round-trip", "blocks_per_tick": MOVE, "block_bytes": layout.block_bytes,
               "layers": 36, "kv_heads": 8, "head_dim": 128, "block_tokens": 16, "pool_blocks": BLOCKS}
     roof = roofline(pack_bytes / (pack_ms / 1e3) / 1e9, "copy_small_rows<KvGather,16> (pack, 32 KiB rows)",
@@ -1051,6 +1134,17 @@ WORKLOADS = {"decode-read": run_decode_read, "topk-gather": run_topk_gather,
              "hisparse-swap": run_hisparse_swap}
 
 
+EXTRA_CONFIGS = (("config1_topk_gather", "topk-gather"), ("config2_block_gather", "block-gather"),
+                 ("config4_migration", "migration"))
+
+
+def summary(result):
+    """The fields of another workload's line that the default line carries for it."""
+    keys = ("metric", "value", "unit", "ms_per_step", "roofline", "cpu_baseline", "config", "lookup_us_per_step",
+            "hit_rate", "verified_round_trip", "tick_ms", "link_gbs", "pack_gbs", "unpack_gbs", "phase_ms")
+    return {key: result[key] for key in keys if key in result}
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -1061,13 +1155,20 @@ def main():
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
-    copy_gbs = None
+    ceilings = None
     if not args.no_copy_ceiling:
-        log("measuring device copy ceiling")
-        copy_gbs = time_copy_ceiling(torch, device)
-        log(f"copy ceiling {copy_gbs:.0f} GB/s")
+        log("measuring streaming ceilings (own read / write / copy kernels)")
+        ceilings = stream_ceilings(torch, device)
+        log(f"ceilings {ceilings}")
     result = WORKLOADS[args.workload](torch, args, device)
-    result["copy_ceiling_gbs"] = None if copy_gbs is None else round(copy_gbs, 1)
+    result["copy_ceiling_gbs"] = None if ceilings is None else ceilings["copy"]["best_gbs"]
+    result["stream_ceilings_gbs"] = ceilings
+    if args.workload == "decode-read" and not args.no_extras:
+        torch.cuda.empty_cache()
+        for key, workload in EXTRA_CONFIGS:
+            log(f"extra: {workload}")
+            result[key] = summary(WORKLOADS[workload](torch, args, device))
+            torch.cuda.empty_cache()
     print(json.dumps(result), flush=True)
     return 0
 

@@ -15,10 +15,15 @@ import sys
 from pathlib import Path
 
 PACKAGE_ROOT = Path(__file__).resolve().parent
+if str(PACKAGE_ROOT) not in sys.path:
+    sys.path.insert(0, str(PACKAGE_ROOT))
+
+from elastic_kv._source_hash import source_hash  # noqa: E402
 SOURCE_DIR = PACKAGE_ROOT / "csrc"
 BUILD_DIR = PACKAGE_ROOT / "_build"
 LIBRARY = PACKAGE_ROOT / "lib" / "libelastic_vmm.so"
-SOURCES = ("vmm_backing.hip", "lookup.hip", "gather.hip", "swap_in.hip", "compare.hip", "hisparse_swap.hip")
+SOURCES = ("vmm_backing.hip", "lookup.hip", "gather.hip", "swap_in.hip", "compare.hip", "hisparse_swap.hip",
+           "stream_probe.hip", "build_info.hip")
 OFFLOAD_ARCH = "gfx950"
 
 COMMON_FLAGS = [
@@ -43,8 +48,8 @@ def hipcc():
     return found
 
 
-def _compile(compiler, source, obj, verbose):
-    command = [compiler, *COMMON_FLAGS, "-c", str(source), "-o", str(obj)]
+def _compile(compiler, source, obj, verbose, extra=()):
+    command = [compiler, *COMMON_FLAGS, *extra, "-c", str(source), "-o", str(obj)]
     if verbose:
         print(" ".join(command), flush=True)
     result = subprocess.run(command, capture_output=True, text=True)
@@ -59,6 +64,7 @@ def build(verbose=False):
     BUILD_DIR.mkdir(exist_ok=True)
     LIBRARY.parent.mkdir(exist_ok=True)
     jobs = min(len(SOURCES), max(1, (os.cpu_count() or 1)))
+    fingerprint = source_hash()
     objects = []
     with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
         futures = []
@@ -66,7 +72,8 @@ def build(verbose=False):
             source = SOURCE_DIR / name
             obj = BUILD_DIR / (Path(name).stem + ".o")
             objects.append(obj)
-            futures.append(pool.submit(_compile, compiler, source, obj, verbose))
+            extra = [f"-DEKV_SOURCE_HASH={fingerprint}"] if name == "build_info.hip" else []
+            futures.append(pool.submit(_compile, compiler, source, obj, verbose, extra))
         for future in futures:
             warnings = future.result()
             if verbose and warnings.strip():

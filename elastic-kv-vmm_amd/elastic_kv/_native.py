@@ -9,6 +9,7 @@ import ctypes as ct
 
 import torch
 
+from ._source_hash import source_hash
 from .backing import _load_library, library_path
 
 EKV_ABI_VERSION = 2
@@ -61,6 +62,7 @@ class EkvKvRows(ct.Structure):
 _P_TENSOR = ct.POINTER(EkvTensor)
 _SIGNATURES = {
     "ekv_abi_version": ([], ct.c_int),
+    "ekv_source_hash": ([], ct.c_char_p),
     "ekv_resolve_resident": ([_P_TENSOR] * 9 + [ct.c_int64, ct.c_void_p], ct.c_int),
     "ekv_resolve_resident_bits": ([_P_TENSOR] * 3 + [ct.c_int64] + [_P_TENSOR] * 6 + [ct.c_int64, ct.c_void_p],
                                   ct.c_int),
@@ -85,6 +87,7 @@ _SIGNATURES = {
     "ekv_host_device_pointer": ([ct.c_void_p, ct.POINTER(ct.c_void_p)], ct.c_int),
     "ekv_host_alloc": ([ct.c_uint64, ct.POINTER(ct.c_void_p), ct.POINTER(ct.c_void_p)], ct.c_int),
     "ekv_host_free": ([ct.c_void_p], ct.c_int),
+    "ekv_stream_probe": ([ct.c_int, ct.c_void_p, ct.c_void_p, ct.c_uint64, ct.c_int, ct.c_void_p], ct.c_int),
 }
 KERNEL_SYMBOLS = tuple(_SIGNATURES)
 
@@ -106,6 +109,12 @@ def kernel_library(library=None):
         version = lib.ekv_abi_version()
         if version != EKV_ABI_VERSION:
             raise RuntimeError(f"libelastic_vmm.so kernel ABI {version} != {EKV_ABI_VERSION}; rebuild it")
+        built, tree = lib.ekv_source_hash().decode(), source_hash()
+        if tree is not None and built != tree:
+            raise RuntimeError(
+                f"libelastic_vmm.so was built from other sources (library {built}, tree {tree}); rebuild it "
+                "with `python elastic-kv-vmm_amd/build_native.py`"
+            )
         lib._ekv_typed = True
     return lib
 

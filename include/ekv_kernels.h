@@ -65,6 +65,11 @@ typedef struct ekv_kv_rows {
 #define EKV_ABI_VERSION 2
 int ekv_abi_version(void);
 
+/* Fingerprint (32 hex digits) of the sources the library was built from; the
+ * Python loader refuses a library whose fingerprint is not the one of the
+ * sources beside it. No reference counterpart. */
+const char* ekv_source_hash(void);
+
 /*
  * Resident lookup with optional miss compaction.
  * Replaces: adaptive_sparse/resident_lookup.py:29-40 (resolve_resident) and
@@ -329,6 +334,26 @@ int ekv_move_kv(const ekv_planes* src, const ekv_tensor* src_rows,
  */
 int ekv_compare_kv(const ekv_planes* a, const ekv_tensor* a_rows, const ekv_planes* b,
                    const ekv_tensor* b_rows, const ekv_tensor* equal, void* stream);
+
+/* Modes of ekv_stream_probe. */
+#define EKV_PROBE_READ 0   /* read src (fold, no stores)       */
+#define EKV_PROBE_WRITE 1  /* write zeros to dst                */
+#define EKV_PROBE_COPY 2   /* dst = src                         */
+
+/*
+ * Streaming bandwidth probe over `bytes` of dense device memory (16-byte
+ * aligned, a multiple of 16): one launch of the read-only, write-only or
+ * copy kernel, with the row-copy engine's access style (16-byte lanes, 8
+ * loads in flight per lane, non-temporal stores, 32 KiB tiles dealt to the
+ * XCDs in contiguous ranges). workgroups_per_cu > 0 reserves LDS so that at
+ * most that many workgroups share a CU; 0 leaves the register limit. dst must
+ * hold `bytes` bytes in every mode (the read probe never writes it unless src
+ * holds a planted pattern); src may be NULL for EKV_PROBE_WRITE.
+ * No reference counterpart: the on-box ceilings the kernels above are
+ * measured against.
+ */
+int ekv_stream_probe(int mode, const void* src, void* dst, uint64_t bytes, int workgroups_per_cu,
+                     void* stream);
 
 /* Pinned host memory (hipHostMalloc) plus the device pointer kernels use to
  * read and write it. Free with ekv_host_free(host). No reference counterpart

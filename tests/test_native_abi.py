@@ -170,3 +170,22 @@ def test_fast_division_is_exact_below_2_pow_31(tmp_path):
     subprocess.run(["g++", "-O2", "-std=c++17", "-I", str(ROOT / "elastic-kv-vmm_amd" / "csrc"),
                     str(source), "-o", str(binary)], check=True)
     assert subprocess.run([str(binary)], capture_output=True, text=True).stdout.strip() == "ok"
+
+
+def test_library_fingerprint_matches_the_sources(lib):
+    from elastic_kv._source_hash import source_hash
+
+    lib.ekv_source_hash.restype = ct.c_char_p
+    assert lib.ekv_source_hash().decode() == source_hash()
+
+
+def test_library_built_from_other_sources_is_refused(monkeypatch):
+    from elastic_kv import _native, backing
+
+    backing._load_library.cache_clear()
+    try:
+        monkeypatch.setattr(_native, "source_hash", lambda: "0" * 32)
+        with pytest.raises(RuntimeError, match="built from other sources"):
+            _native.kernel_library()
+    finally:
+        backing._load_library.cache_clear()

@@ -697,3 +697,49 @@ def test_hisparse_swap_repeated_blocks_padding_and_bounds():
     # row 1 has length 0 and row 2 is past num_real: -1 only, state unchanged.
     assert (out[1:] == -1).all()
     assert np.array_equal(tokens2[1:], tokens[1:]) and np.array_equal(lru2[1:], lru[1:])
+
+
+def test_torch_cpu_path_reproduces_reference_smoke_vectors():
+    """tests/smoke_resident_lookup.py:8-23 through the torch restatement of request_residency.py:819-825."""
+    import torch
+
+    from oracle import torch_path
+
+    topk = torch.tensor([[1, -1, 2] + [-1] * 13, [0] * 16, [0, 2, -1] + [-1] * 13])
+    rows, lengths = torch.tensor([3, 0, 1]), torch.tensor([130, 0, 0])
+    table = torch.tensor([[(i * 300 + j) for j in range(300)] for i in range(4)])
+    mapping = torch.tensor([i * 3 + 5 for i in range(1200)])
+    slots, misses = torch_path.lookup(topk, table, mapping, rows, lengths, torch.tensor([2, 0]), 128)
+    assert slots[1, :3].tolist() == [3089, 3092, -1] and slots[1, -1] == -1
+    assert slots[0].tolist() == [-1] * 2048
+    assert misses.numel() == 0
+
+
+def test_torch_cpu_path_matches_the_numpy_oracle():
+    import torch
+
+    from oracle import torch_path
+
+    rng = np.random.default_rng(17)
+    for block_size in (1, 2, 4):
+        B, R, T, K, N = 6, 5, 300, 24, 900
+        topk = rng.integers(-1, T // block_size + 3, (1, B, K))
+        req_to_token = rng.integers(0, N, (R, T))
+        mapping = rng.integers(0, 40, N) * (rng.random(N) < 0.6)
+        rows, lengths = rng.integers(0, R, B), rng.integers(0, T + 1, B)
+        selected = np.array([4, 0, 2])
+        want, want_misses, _ = ref.resolve_resident(topk, req_to_token, mapping, rows, lengths, selected,
+                                                    block_size, np.zeros((1, B, K * block_size), np.int32),
+                                                    with_misses=True)
+        got, misses = torch_path.lookup(*(torch.tensor(a) for a in (topk[0], req_to_token, mapping, rows, lengths,
+                                                                     selected)), block_size)
+        assert np.array_equal(got.numpy(), want[0, selected])
+        for i, row in enumerate(selected):
+            lanes = misses[misses[:, 0] == i, 1].numpy()
+            assert np.array_equal(lanes, want_misses[(0, int(row))])
+        planes = torch.tensor(rng.integers(0, 256, (2, 41, 8), dtype=np.uint8))
+        flat = got.flatten()
+        rows_out = torch_path.gather(planes, flat)
+        pool = planes.numpy().reshape(-1)
+        expect = ref.gather_kv(pool, 2 * 41 * 8, 41 * 8, 8, 8, 41, flat.numpy().reshape(1, 1, -1), 2)
+        assert np.array_equal(rows_out.numpy().reshape(-1), expect.reshape(-1))
