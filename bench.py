@@ -712,7 +712,7 @@ def run_migration(torch, args, device):
         t1 = time.perf_counter()
         host = engine.round_trip(sources, targets)      # pack -> D2H -> H2D -> unpack, pipelined
         pool.release(sources)
-        pool.trim(after=host.packed)                    # unmap chunks only the sources used, once packed,
+        pool.trim(after=host.packed, pages=sources)     # unmap chunks only the sources used, once packed,
         t2 = time.perf_counter()                        # while the PCIe legs and unpacks still run
         torch.cuda.synchronize()
         t3 = time.perf_counter()

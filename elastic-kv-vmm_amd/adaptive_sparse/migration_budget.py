@@ -1,81 +1,88 @@
-"""Migration bandwidth estimation and byte/time admission caps (pure CPU).
+"""Migration bandwidth estimation and byte / time admission caps (pure CPU).
 
-Same API and arithmetic as the reference's adaptive_sparse/migration_budget.py:6-107:
-a configured rate is used until a direction has a real sample, then an EWMA
-(rate = alpha * sample + (1 - alpha) * rate) of successful transfers.
+The interface of the reference's adaptive_sparse/migration_budget.py:6-107:
+each direction (demotion, promotion) reports the configured rate until it has
+seen a transfer of real size, then the exponentially weighted mean
+rate <- alpha * sample + (1 - alpha) * rate of its successful transfers; a
+time cap turns that rate into a byte cap, never above the configured one.
+Here each direction's state is one small record, and the argument checks
+are shared predicates.
 """
 
 import math
+from dataclasses import dataclass
 
-_DIRECTIONS = ("demotion", "promotion")
 
-
-def _is_int(value):
+def _integer(value):
     return isinstance(value, int) and not isinstance(value, bool)
 
 
-class MigrationBandwidthEstimator:
-    """Direction-specific transfer throughput from committed migrations."""
+def _real(value):
+    return isinstance(value, (int, float)) and not isinstance(value, bool) and math.isfinite(value)
 
-    DIRECTIONS = _DIRECTIONS
+
+def _require(ok, message):
+    if not ok:
+        raise ValueError(message)
+
+
+@dataclass
+class _Direction:
+    rate: float = None     # bytes/s; None until the first sample
+    samples: int = 0
+
+    def fold(self, sample, alpha):
+        self.rate = sample if self.rate is None else alpha * sample + (1.0 - alpha) * self.rate
+        self.samples += 1
+
+
+class MigrationBandwidthEstimator:
+    """Per-direction transfer throughput of committed migrations and the caps it implies."""
+
+    DIRECTIONS = ("demotion", "promotion")
 
     def __init__(self, initial_bandwidth_bytes_per_s, ewma_alpha):
-        if not _is_int(initial_bandwidth_bytes_per_s) or initial_bandwidth_bytes_per_s <= 0:
-            raise ValueError("initial bandwidth must be a positive integer")
-        if (isinstance(ewma_alpha, bool) or not isinstance(ewma_alpha, (int, float))
-                or not math.isfinite(ewma_alpha) or not 0 < ewma_alpha <= 1):
-            raise ValueError("EWMA alpha must be in (0, 1]")
+        _require(_integer(initial_bandwidth_bytes_per_s) and initial_bandwidth_bytes_per_s > 0,
+                 "initial bandwidth must be a positive integer")
+        _require(_real(ewma_alpha) and 0 < ewma_alpha <= 1, "EWMA alpha must be in (0, 1]")
         self.initial_bandwidth_bytes_per_s = initial_bandwidth_bytes_per_s
         self.ewma_alpha = float(ewma_alpha)
-        self._rates = {}
-        self._samples = dict.fromkeys(_DIRECTIONS, 0)
+        self._state = {direction: _Direction() for direction in self.DIRECTIONS}
 
-    @classmethod
-    def _check_direction(cls, direction):
-        if direction not in cls.DIRECTIONS:
-            raise ValueError(f"unknown migration direction: {direction}")
+    def _direction(self, direction):
+        state = self._state.get(direction)
+        _require(state is not None, f"unknown migration direction: {direction}")
+        return state
 
     def observe(self, direction, transfer_bytes, elapsed_seconds):
-        """Fold one transfer into the direction's rate; return its bandwidth or None."""
-        self._check_direction(direction)
-        if not _is_int(transfer_bytes) or transfer_bytes < 0:
-            raise ValueError("transfer bytes must be a nonnegative integer")
-        if (isinstance(elapsed_seconds, bool) or not isinstance(elapsed_seconds, (int, float))
-                or not math.isfinite(elapsed_seconds)):
-            raise ValueError("elapsed seconds must be finite")
+        """Fold one transfer into `direction`'s rate; returns its bandwidth, or None for an empty one."""
+        state = self._direction(direction)
+        _require(_integer(transfer_bytes) and transfer_bytes >= 0, "transfer bytes must be a nonnegative integer")
+        _require(_real(elapsed_seconds), "elapsed seconds must be finite")
         if transfer_bytes == 0 or elapsed_seconds <= 0:
             return None
         sample = transfer_bytes / float(elapsed_seconds)
-        if direction in self._rates:
-            alpha = self.ewma_alpha
-            self._rates[direction] = alpha * sample + (1 - alpha) * self._rates[direction]
-        else:
-            self._rates[direction] = sample
-        self._samples[direction] += 1
+        state.fold(sample, self.ewma_alpha)
         return sample
 
     def bandwidth(self, direction):
-        self._check_direction(direction)
-        return self._rates.get(direction, float(self.initial_bandwidth_bytes_per_s))
+        rate = self._direction(direction).rate
+        return float(self.initial_bandwidth_bytes_per_s) if rate is None else rate
 
     def samples(self, direction):
-        self._check_direction(direction)
-        return self._samples[direction]
+        return self._direction(direction).samples
 
     def effective_byte_cap(self, byte_cap, time_cap_ms, direction="demotion"):
-        """Largest byte count allowed by both the byte cap and the time cap."""
-        self._check_direction(direction)
-        if not _is_int(byte_cap) or byte_cap < 1:
-            raise ValueError("byte cap must be a positive integer")
-        if not _is_int(time_cap_ms) or time_cap_ms < 0:
-            raise ValueError("time cap must be a nonnegative integer")
+        """The most bytes both caps allow: byte_cap, lowered to what `direction` moves in time_cap_ms (0 = no time cap)."""
+        rate = self.bandwidth(direction)
+        _require(_integer(byte_cap) and byte_cap >= 1, "byte cap must be a positive integer")
+        _require(_integer(time_cap_ms) and time_cap_ms >= 0, "time cap must be a nonnegative integer")
         if time_cap_ms == 0:
             return byte_cap
-        transferable = int(self.bandwidth(direction) * time_cap_ms / 1000.0)
-        return min(byte_cap, max(0, transferable))
+        return min(byte_cap, max(0, int(rate * time_cap_ms / 1000.0)))
 
     def snapshot(self):
         return {direction: self.bandwidth(direction) for direction in self.DIRECTIONS}
 
     def sample_counts(self):
-        return dict(self._samples)
+        return {direction: state.samples for direction, state in self._state.items()}

@@ -71,22 +71,27 @@ class PagedKVPool:
         self.pages.release(set(ids))
         self.free.release(ids)
 
-    def trim(self, after=None):
+    def trim(self, after=None, pages=None):
         """Unmap chunks no page owns; returns the released bytes.
 
-        By default the device is synchronized first. `after` is an event after
-        which no device work reads or writes the released pages (a round
-        trip's `packed` event): the host waits for it instead, so the copies
-        and kernels queued behind it keep running while the chunks are
-        unmapped.
+        By default the device is synchronized first and every such chunk is
+        released. With `after`, an event after which no device work touches
+        `pages` (pages just released, e.g. a round trip's sources with its
+        `packed` event), the host waits for that event only and releases only
+        the chunks those pages covered: the copies and kernels queued behind
+        the event keep running, and chunks freed earlier, whose readers may
+        still be queued on another stream, are left to a synchronized trim.
         """
         if after is None:
             return self.pages.trim_quiescent()
-        pending = self.pages.reclaimable_chunks()
-        if not pending:
+        if pages is None:
+            raise ValueError("trim(after=...) needs the released pages whose chunks the event fences")
+        covered = set().union(*(self.pages.chunks(int(page)) for page in pages)) if len(pages) else set()
+        idle = self.pages.reclaimable_chunks() & covered
+        if not idle:
             return 0
         after.synchronize()
-        return self.backing.reclaim(pending, synchronize=False) * self.layout.chunk_bytes
+        return self.backing.reclaim(idle, synchronize=False) * self.layout.chunk_bytes
 
     def close(self):
         torch.cuda.synchronize(self.device)

@@ -1,11 +1,16 @@
 """Physical page ownership projected onto packed, chunk-aligned K/V planes.
 
-PhysicalPages restates the reference's adaptive_sparse/minimax_vmm.py:20-98:
-page p of every plane (plane_chunk, row_bytes) spans page_size rows starting
-at plane_chunk * chunk_bytes + p * page_size * row_bytes; a chunk stays
-mapped while any owned page touches it; page 0 is the permanent sink.
-The SGLang pool installation of that module is serving-layer code outside
-this path.
+The ownership contract of the reference's adaptive_sparse/minimax_vmm.py:20-98:
+page p of a plane whose first chunk is c and whose rows are r bytes covers
+bytes [p * page_size * r, (p + 1) * page_size * r) from chunk c on; a chunk
+stays committed while any owned page covers it; page 0 is the permanent sink;
+trimming releases the committed chunks no page covers. The SGLang pool
+installation around it in the reference is serving-layer code outside this
+path.
+
+Two parts here: PageFootprints, the pure page -> chunk-set projection
+(optionally memoized), and PhysicalPages, the owned-page set and per-chunk
+reference counts kept over a Backing.
 """
 
 from time import perf_counter_ns
@@ -13,93 +18,110 @@ from time import perf_counter_ns
 CHUNK_BYTES = 2 << 20
 
 
+class PageFootprints:
+    """page -> frozenset of the chunk ids its rows cover in any plane."""
+
+    def __init__(self, page_size, planes, chunk_bytes=CHUNK_BYTES, memoize=False):
+        self.page_size = page_size
+        self.planes = [tuple(plane) for plane in planes]   # (first chunk, row bytes) per plane
+        self.chunk_bytes = chunk_bytes
+        self._memo = {} if memoize else None
+
+    def __call__(self, page):
+        if self._memo is not None and page in self._memo:
+            return self._memo[page]
+        covered = set()
+        for first_chunk, row_bytes in self.planes:
+            page_bytes = self.page_size * row_bytes
+            start, stop = page * page_bytes, (page + 1) * page_bytes        # [start, stop) in the plane
+            covered.update(range(first_chunk + start // self.chunk_bytes,
+                                 first_chunk + (stop - 1) // self.chunk_bytes + 1))
+        footprint = frozenset(covered)
+        if self._memo is not None:
+            self._memo[page] = footprint
+        return footprint
+
+
 class PhysicalPages:
-    """Refcounted chunk ownership for the pages handed out by an allocator."""
+    """Refcounted chunk ownership of the pages an allocator hands out (pages 1..page_count).
+
+    backing: ensure(ids), reclaim(ids, synchronize=False), mapped_chunks and
+    backed_bytes, as elastic_kv.backing.Backing provides; synchronize: waits
+    for every device user (called once per non-empty trim). fast_decode
+    memoizes page footprints.
+    """
 
     def __init__(self, backing, page_size, page_count, planes, synchronize,
                  chunk_bytes=CHUNK_BYTES, fast_decode=False):
+        self.footprints = PageFootprints(page_size, planes, chunk_bytes, memoize=fast_decode)
         self.backing = backing
-        self.page_size = page_size
         self.page_count = page_count
-        self.planes = planes
         self.synchronize = synchronize
-        self.chunk_bytes = chunk_bytes
         self.trim_sync_ns = 0
-        self.fast_decode = fast_decode
-        self.fast_no_new_page = 0
-        self.decode_new_page = 0
-        self._chunk_cache = {} if fast_decode else None
         self.pages = {0}
-        self.refs = dict.fromkeys(self.chunks(0), 1)
-        self.backing.ensure(set(self.refs))
+        self.refs = dict.fromkeys(self.footprints(0), 1)
+        backing.ensure(set(self.refs))
+
+    page_size = property(lambda self: self.footprints.page_size)
+    planes = property(lambda self: self.footprints.planes)
+    chunk_bytes = property(lambda self: self.footprints.chunk_bytes)
 
     def chunks(self, page):
-        """Chunk ids that page `page` touches in any plane."""
-        if self._chunk_cache is not None:
-            cached = self._chunk_cache.get(page)
-            if cached is not None:
-                return cached
-        span = self.page_size
-        touched = set()
-        for plane_chunk, row_bytes in self.planes:
-            first = page * span * row_bytes
-            last = first + span * row_bytes - 1
-            touched.update(range(plane_chunk + first // self.chunk_bytes,
-                                 plane_chunk + last // self.chunk_bytes + 1))
-        result = frozenset(touched)
-        if self._chunk_cache is not None:
-            self._chunk_cache[page] = result
-        return result
+        return self.footprints(page)
 
     def acquire(self, pages):
-        """Take ownership of pages, committing chunks no owned page uses yet."""
-        pages = set(pages)
-        if any(page <= 0 or page > self.page_count for page in pages):
+        """Own `pages`, committing every chunk they cover first; ownership is unchanged if that fails."""
+        wanted = set(pages)
+        if not all(0 < page <= self.page_count for page in wanted):
             raise ValueError("invalid physical page")
-        fresh = pages - self.pages
-        footprints = [self.chunks(page) for page in fresh]
-        if footprints:
-            self.backing.ensure(set().union(*footprints))
-        for footprint in footprints:
-            for chunk in footprint:
+        fresh = wanted - self.pages
+        covers = [self.footprints(page) for page in fresh]
+        if covers:
+            self.backing.ensure(frozenset().union(*covers))
+        for cover in covers:
+            for chunk in cover:
                 self.refs[chunk] = self.refs.get(chunk, 0) + 1
-        self.pages.update(fresh)
+        self.pages |= fresh
 
     def validate_release(self, pages):
         if 0 in pages or not pages <= self.pages:
             raise RuntimeError("invalid or duplicate physical free")
 
     def release(self, pages):
-        """Drop ownership; chunks reaching zero refs become reclaimable."""
+        """Give up `pages`; chunks no remaining page covers become reclaimable."""
         self.validate_release(pages)
         for page in pages:
-            for chunk in self.chunks(page):
-                remaining = self.refs[chunk] - 1
-                if remaining:
-                    self.refs[chunk] = remaining
-                else:
+            for chunk in self.footprints(page):
+                if self.refs[chunk] == 1:
                     del self.refs[chunk]
-        self.pages.difference_update(pages)
+                else:
+                    self.refs[chunk] -= 1
+        self.pages -= pages
 
     def clear(self):
         self.release(self.pages - {0})
 
     def reclaimable_chunks(self):
-        return set(self.backing.mapped_chunks) - self.refs.keys()
+        """Committed chunks that no owned page covers."""
+        return set(self.backing.mapped_chunks).difference(self.refs)
 
     def stats(self):
         return {"backed_bytes": self.backing.backed_bytes,
                 "reclaimable_bytes": len(self.reclaimable_chunks()) * self.chunk_bytes,
-                "owned_pages": len(self.pages) - 1, "trim_sync_ns": self.trim_sync_ns,
-                "fast_no_new_page": self.fast_no_new_page,
-                "decode_new_page": self.decode_new_page}
+                "owned_pages": len(self.pages) - 1, "trim_sync_ns": self.trim_sync_ns}
 
-    def trim_quiescent(self):
-        """Unmap chunks no page owns. Call only with all device users idle."""
-        pending = self.reclaimable_chunks()
-        if not pending:
+    def trim_quiescent(self, only=None):
+        """Release reclaimable chunks (those in `only`, if given); returns the bytes released.
+
+        Call only with every device user idle: it synchronizes once, then
+        unmaps without another wait.
+        """
+        idle = self.reclaimable_chunks()
+        if only is not None:
+            idle &= set(only)
+        if not idle:
             return 0
         started = perf_counter_ns()
         self.synchronize()
         self.trim_sync_ns += perf_counter_ns() - started
-        return self.backing.reclaim(pending, synchronize=False) * self.chunk_bytes
+        return self.backing.reclaim(idle, synchronize=False) * self.chunk_bytes

@@ -1,19 +1,24 @@
-"""Byte layout of independent, chunk-aligned request KV regions.
+"""Chunk-aligned virtual regions of per-request KV rows.
 
-Same layout as the reference's experimental/virtual_layout.py:14-61 (it is an
-addressing contract shared with gather_rows' direct mode): chunk 0 is a sink,
-request r owns a chunk-aligned region starting at chunk_bytes + r *
-request_bytes, and token t of request r starts row_bytes * t into it.
+The address map of the reference's experimental/virtual_layout.py:14-61, which
+is the addressing contract of gather_rows' direct mode, so every number here
+equals the reference's: the first chunk is a sink; request r owns
+`chunks_per_request` chunks (the fewest that hold max_tokens rows) starting at
+chunk 1 + r * chunks_per_request; token t's row starts t * row_bytes into the
+request's region.
 """
 
 from dataclasses import dataclass, fields
 
 
-def _require_int(name, value, low, high=None):
+def _whole(name, value, low, high=None):
+    """Check that value is an int (bool is not) within [low, high]."""
     if type(value) is not int:
-        raise TypeError(f"{name} must be an integer")
+        raise TypeError(f"{name} must be an integer, got {type(value).__name__}")
     if value < low or (high is not None and value > high):
-        raise ValueError(f"{name} outside supported range")
+        bound = f"[{low}, {high}]" if high is not None else f">= {low}"
+        raise ValueError(f"{name} outside supported range: {value} not in {bound}")
+    return value
 
 
 @dataclass(frozen=True)
@@ -25,44 +30,57 @@ class VirtualKVLayout:
     chunk_bytes: int = 2 << 20
 
     def __post_init__(self):
-        for field in fields(self):
-            _require_int(field.name, getattr(self, field.name), 1)
+        for spec in fields(self):
+            _whole(spec.name, getattr(self, spec.name), 1)
+
+    # ------------------------------------------------------------ sizes
 
     @property
     def row_bytes(self):
         return self.row_elements * self.itemsize
 
     @property
+    def chunks_per_request(self):
+        """Chunks of one request region: its max_tokens rows, rounded up."""
+        return -(-(self.max_tokens * self.row_bytes) // self.chunk_bytes)
+
+    @property
     def request_bytes(self):
-        """Bytes of one request region: its rows rounded up to whole chunks."""
-        return -(-self.max_tokens * self.row_bytes // self.chunk_bytes) * self.chunk_bytes
+        return self.chunks_per_request * self.chunk_bytes
 
     @property
     def capacity_bytes(self):
-        return self.chunk_bytes + self.max_requests * self.request_bytes
+        return (1 + self.max_requests * self.chunks_per_request) * self.chunk_bytes
+
+    # ------------------------------------------------------------ offsets
 
     def request_offset(self, req):
-        _require_int("request index", req, 0, self.max_requests - 1)
-        return self.chunk_bytes + req * self.request_bytes
+        _whole("request index", req, 0, self.max_requests - 1)
+        return (1 + req * self.chunks_per_request) * self.chunk_bytes
 
     def token_offset(self, req, token):
-        _require_int("token position", token, 0, self.max_tokens - 1)
+        _whole("token position", token, 0, self.max_tokens - 1)
         return self.request_offset(req) + token * self.row_bytes
 
-    def _chunks_covering(self, start, size):
-        if not size:
+    # ------------------------------------------------------------ chunk sets
+
+    def _span(self, first_byte, size):
+        """Ids of the chunks that bytes [first_byte, first_byte + size) touch."""
+        if size == 0:
             return range(0)
-        return range(start // self.chunk_bytes, (start + size - 1) // self.chunk_bytes + 1)
+        last_byte = first_byte + size - 1
+        return range(first_byte // self.chunk_bytes, last_byte // self.chunk_bytes + 1)
 
     def prefix_chunks(self, req, length):
-        """Chunks holding tokens [0, length) of request `req`."""
-        _require_int("prefix length", length, 0, self.max_tokens)
-        return frozenset(self._chunks_covering(self.request_offset(req), length * self.row_bytes))
+        """Chunks holding the rows of tokens [0, length) of request `req`."""
+        _whole("prefix length", length, 0, self.max_tokens)
+        return frozenset(self._span(self.request_offset(req), length * self.row_bytes))
 
     def selected_chunks(self, req, positions):
-        """Chunks touched by the rows of the given token positions."""
-        self.request_offset(req)
-        chunks = set()
+        """Chunks holding the rows of the given token positions of request `req`."""
+        base = self.request_offset(req)
+        touched = set()
         for token in positions:
-            chunks.update(self._chunks_covering(self.token_offset(req, token), self.row_bytes))
-        return frozenset(chunks)
+            _whole("token position", token, 0, self.max_tokens - 1)
+            touched.update(self._span(base + token * self.row_bytes, self.row_bytes))
+        return frozenset(touched)

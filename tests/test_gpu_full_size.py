@@ -3,11 +3,14 @@
 At full size the oracle would take minutes, so these tests check properties
 that do not depend on size instead:
 - the HiSparse decode read (128 requests x 65,536 tokens x 60 layers,
-  Top-K 2048, hot capacity 4096) is built so that its results have closed
-  forms. Each (layer, request) selects 1638 distinct tokens from the last
-  4096 positions, all resident, and 410 distinct tokens from the rest, none
-  resident. So every row has exactly 410 misses, and those misses are exactly
-  the lanes that selected an old token;
+  Top-K 2048, hot capacity 2048, 4096 or 8192 holding the most recent
+  tokens) is built so that its results have closed forms. Each (layer,
+  request) selects 1638 distinct tokens from the last 4096 positions and 410
+  distinct tokens from the rest; a lane misses exactly when its token lies
+  below T - C (at C = 4096: exactly the 410 old picks of every row), its miss
+  list is those lanes in order, and a hit's slot is its table entry. Every
+  table form is checked: int32 global slots and int16 local slots behind the
+  per-position bitmap, and the decode default, int16 behind the line summary;
 - every gathered K/V plane must equal torch.index_select of the pool plane
   at the resolved slots, with zero rows for misses. index_select is the
   textbook gather.
@@ -42,11 +45,19 @@ def plane_rows(raw, layout, layer, kv):
     return raw.narrow(0, layout.plane_offset(layer, kv), layout.plane_bytes).view(layout.rows, layout.row_bytes)
 
 
-def test_decode_read_at_full_size(gpu):
-    L, R, T, K, C, W = 60, 128, 65536, 2048, 4096, 4096
+@pytest.mark.parametrize("capacity", [2048, 4096, 8192])
+def test_decode_read_at_full_size(gpu, capacity):
+    """Closed forms of the decode read at every hot capacity, through each table form.
+
+    The hot set is the C most recent tokens, so a lane misses exactly when it
+    picked a token below T - C: at C = 4096 that is the 410 old picks of every
+    row, at C = 2048 also the recent picks in [T - 4096, T - 2048), at
+    C = 8192 only the old picks below T - 8192.
+    """
+    L, R, T, K, C, W = 60, 128, 65536, 2048, capacity, 4096
     recent_count, old_count = 1638, 410
     row_bytes = 512
-    gen = torch.Generator(device=gpu).manual_seed(31)
+    gen = torch.Generator(device=gpu).manual_seed(31 + capacity)
     recent = torch.rand((L, R, W), generator=gen, device=gpu).argsort(-1)[..., :recent_count] + (T - W)
     old = torch.rand((L, R, T - W), generator=gen, device=gpu).topk(old_count, dim=-1).indices
     topk = torch.cat([recent, old], dim=-1)
@@ -54,29 +65,41 @@ def test_decode_read_at_full_size(gpu):
     topk = torch.gather(topk, -1, torch.rand((L, R, K), generator=gen, device=gpu).argsort(-1))
     topk = topk.to(torch.int32).contiguous()
     table = torch.zeros((L, R, T), dtype=torch.int32, device=gpu)
-    base = (torch.arange(R, device=gpu, dtype=torch.int32) * C + 1).view(1, R, 1)
-    table[:, :, T - C:] = torch.rand((L, R, C), generator=gen, device=gpu).argsort(-1).to(torch.int32) + base
-    bits = build_residency_bits(table)
+    base = torch.arange(R, device=gpu, dtype=torch.int64) * C + 1
+    table[:, :, T - C:] = (torch.rand((L, R, C), generator=gen, device=gpu).argsort(-1)
+                           + base.view(1, R, 1)).to(torch.int32)
+    table16 = torch.where(table > 0, table - base.view(1, R, 1) + 1, 0).to(torch.int16)
     rows = torch.arange(R, device=gpu)
     lengths = torch.full((R,), T, dtype=torch.int32, device=gpu)
-    slots = torch.full((L, R, K), -7, dtype=torch.int32, device=gpu)
-    misses = torch.full((L, R, K), -5, dtype=torch.int32, device=gpu)
-    counts = torch.full((L, R), -5, dtype=torch.int32, device=gpu)
-    resolve_resident(topk, table, None, rows, lengths, rows, slots, 1, misses=misses, miss_count=counts,
-                     resident_bits=bits)
-    torch.cuda.synchronize()
-    print(f"[full-size decode] lookup done, counts {int(counts.min())}..{int(counts.max())}", flush=True)
-
-    # Lookup: closed forms.
-    assert bool((counts == old_count).all())
     is_old = topk < T - C
+    miss_count = is_old.sum(-1).to(torch.int32)
     lanes = torch.arange(K, device=gpu, dtype=torch.int32).expand(L, R, K)
-    want_misses = torch.sort(torch.where(is_old, lanes, K), dim=-1).values[..., :old_count]
-    assert torch.equal(misses[..., :old_count], want_misses)
-    assert bool((misses[..., old_count:] == -5).all())
-    assert bool((slots[is_old] == 0).all())
-    assert torch.equal(torch.where(is_old, 0, torch.gather(table, -1, topk.long())), slots)
-    del is_old, lanes, want_misses, table, bits
+    want_misses = torch.sort(torch.where(is_old, lanes, K), dim=-1).values
+    want_slots = torch.where(is_old, 0, torch.gather(table, -1, topk.long()))
+    forms = {"int32 table + position bitmap": dict(table=table, resident_bits=build_residency_bits(table)),
+             "int16 table + position bitmap": dict(table=table16, resident_bits=build_residency_bits(table16),
+                                                   slot_base=base),
+             "int16 table + line summary (decode default)": dict(table=table16, slot_base=base, bits_shift=6,
+                                                                 resident_bits=build_residency_bits(table16, shift=6))}
+    slots = None
+    for name, form in forms.items():
+        slots = torch.full((L, R, K), -7, dtype=torch.int32, device=gpu)
+        misses = torch.full((L, R, K), -5, dtype=torch.int32, device=gpu)
+        counts = torch.full((L, R), -5, dtype=torch.int32, device=gpu)
+        resolve_resident(topk, form.pop("table"), None, rows, lengths, rows, slots, 1, misses=misses,
+                         miss_count=counts, **form)
+        torch.cuda.synchronize()
+        print(f"[full-size decode C={C}] {name}: counts {int(counts.min())}..{int(counts.max())}", flush=True)
+        assert torch.equal(counts, miss_count), name
+        filled = lanes < counts.unsqueeze(-1)
+        assert torch.equal(torch.where(filled, misses, K), want_misses), name
+        assert bool((misses[~filled] == -5).all()), name
+        assert torch.equal(slots, want_slots), name
+    if C == 4096:
+        assert bool((miss_count == old_count).all())
+    hit_rate = float((want_slots > 0).float().mean())
+    print(f"[full-size decode C={C}] hit rate {hit_rate:.4f}", flush=True)
+    del is_old, lanes, want_misses, table, table16, forms, want_slots
 
     # Gather: every plane against index_select, misses as zero rows.
     layout = PlanePoolLayout(layers=L, kv=2, rows=1 + R * C, row_bytes=row_bytes)
@@ -85,7 +108,7 @@ def test_decode_read_at_full_size(gpu):
         out = torch.empty((R, L, 2, K, row_bytes), dtype=torch.uint8, device=gpu)
         gather_kv(layout.kv_planes(backing.base, 0, owner=backing), slots, out)
         torch.cuda.synchronize()
-        print("[full-size decode] gather done", flush=True)
+        print(f"[full-size decode C={C}] gather done", flush=True)
         for layer in range(L):
             hit = (slots[layer] > 0).unsqueeze(-1)
             for kv in range(2):

@@ -87,19 +87,29 @@ def test_trim_after_packed_event_overlaps_the_copies(gpu, sub_batch):
         pool.allocate(live)
         fill(pool, live, 2)
         sources = rng.choice(live, size=20, replace=False).tolist()
+        spare = next(p for p in live if p not in sources)      # released earlier, not fenced by the event
         free = sorted(set(range(1, 64)) - set(live))
         targets = rng.choice(free, size=20, replace=False).tolist()
         before = {p: pool.page_view(p).clone() for p in sources}
         torch.cuda.synchronize()
         engine = MigrationEngine(pool, max_pages=20, sub_batch=sub_batch)
         pool.allocate(targets)
+        pool.release([spare])
         backed = pool.backing.backed_bytes
         host = engine.round_trip(sources, targets)
         assert host.packed is not None
         pool.release(sources)
-        released = pool.trim(after=host.packed)
+        with pytest.raises(ValueError, match="released pages"):
+            pool.trim(after=host.packed)
+        idle = pool.pages.reclaimable_chunks()
+        fenced = idle & set().union(*(pool.pages.chunks(p) for p in sources))
+        released = pool.trim(after=host.packed, pages=sources)
         engine.wait()
-        assert released > 0 and pool.backing.backed_bytes == backed - released
+        assert released == len(fenced) * layout.chunk_bytes > 0
+        assert pool.backing.backed_bytes == backed - released
+        # chunks the event does not fence (the spare's own) are left for a synchronized trim
+        assert pool.pages.reclaimable_chunks() == idle - fenced
+        assert pool.trim() == len(idle - fenced) * layout.chunk_bytes
         for s, t in zip(sources, targets):
             assert torch.equal(pool.page_view(t), before[s]), (s, t)
         for i, s in enumerate(sources):

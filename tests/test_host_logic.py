@@ -18,7 +18,7 @@ import pytest
 from adaptive_sparse.kv_pool import BlockMajorLayout, PlanePoolLayout
 from adaptive_sparse.migration import plan_demote_pages
 from adaptive_sparse.migration_budget import MigrationBandwidthEstimator
-from adaptive_sparse.minimax_vmm import PhysicalPages
+from adaptive_sparse.minimax_vmm import PageFootprints, PhysicalPages
 from conftest import GOLDEN
 from elastic_kv.backing import Backing, _load_library
 from elastic_kv.slots import FreeSlots
@@ -281,13 +281,9 @@ def test_pages_failed_map_does_not_change_ownership():
 
 
 def _tracker_from_snapshot(snapshot):
-    tracker = PhysicalPages.__new__(PhysicalPages)
-    tracker.page_size = snapshot["page_size"]
-    tracker.planes = [tuple(p) for p in snapshot["planes"]]
-    tracker.chunk_bytes = snapshot["chunk_bytes"]
-    tracker._chunk_cache = None
-    tracker.refs = {int(k): v for k, v in snapshot["refs"].items()}
-    return tracker
+    """The planner's view of a recorded tracker: page footprints and chunk reference counts."""
+    footprints = PageFootprints(snapshot["page_size"], snapshot["planes"], snapshot["chunk_bytes"])
+    return SimpleNamespace(chunks=footprints, refs={int(k): v for k, v in snapshot["refs"].items()})
 
 
 @pytest.mark.parametrize("rank", range(4))
@@ -704,3 +700,54 @@ def test_hisparse_swap_host_checks():
     with pytest.raises(ValueError, match="need GPU tensors"):     # no CPU fallback
         load_blocks_to_device_buffer_mha(small, small, small, small, k, v, k, v, small, small[0], small[0], small,
                                          32, 1, 1)
+
+
+# ------------------------------------------------------------------ PlaneProjection
+
+
+class _RecordingBacking:
+    """Records the chunk ids a PlaneProjection sends to its backing."""
+
+    def __init__(self, capacity_bytes, chunk_bytes, device):
+        self.created = (capacity_bytes, chunk_bytes, device)
+        self.calls = []
+        self.backed_bytes = 0
+        self.metrics = {"ensure_calls": 0}
+        self.raw = None
+
+    def ensure(self, ids):
+        self.calls.append(("ensure", sorted(ids)))
+
+    def precommit(self, ids):
+        self.calls.append(("precommit", sorted(ids)))
+
+    def reclaim(self, ids, *, synchronize):
+        self.calls.append(("reclaim", sorted(ids), synchronize))
+
+
+def test_plane_projection_commits_each_logical_chunk_in_every_plane():
+    """elastic_kv/adapter.py:82-138: logical chunk c is chunk p * plane_chunks + c of plane p."""
+    import torch
+
+    from elastic_kv.adapter import PlaneProjection
+
+    projection = PlaneProjection(20, 3, 8, 1, backing_factory=_RecordingBacking)
+    backing = projection.backing
+    assert (projection.plane_chunks, projection.plane_stride) == (3, 24)
+    assert backing.created == (72, 8, 1)
+    projection.ensure([0, 2])
+    projection.ensure([2])                                   # held and ready: no call
+    assert projection.precommit([2, 1]) == 1                 # only chunk 1 is new
+    assert projection.precommit([1]) == 0
+    assert projection.mapped_chunks == {0, 2} and projection.precommitted_chunks == {1}
+    assert projection.metrics["precommitted_chunks"] == 1
+    projection.ensure([1])                                   # waits for the precommitted chunk
+    assert projection.mapped_chunks == {0, 1, 2} and projection.precommitted_chunks == set()
+    projection.reclaim([2, 5], synchronize=False)
+    assert projection.allocated_chunks == {0, 1}
+    assert backing.calls == [("ensure", [0, 2, 3, 5, 6, 8]), ("precommit", [1, 4, 7]), ("ensure", [1, 4, 7]),
+                             ("reclaim", [2, 5, 8], False)]
+    backing.raw = torch.arange(72, dtype=torch.uint8)
+    views = projection.views(torch.int16, (2, 5))
+    assert [v.shape for v in views] == [(2, 5)] * 3
+    assert [v.view(torch.uint8)[0, :2].tolist() for v in views] == [[0, 1], [24, 25], [48, 49]]
