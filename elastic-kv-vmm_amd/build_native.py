@@ -23,7 +23,7 @@ SOURCE_DIR = PACKAGE_ROOT / "csrc"
 BUILD_DIR = PACKAGE_ROOT / "_build"
 LIBRARY = PACKAGE_ROOT / "lib" / "libelastic_vmm.so"
 SOURCES = ("vmm_backing.hip", "lookup.hip", "gather.hip", "swap_in.hip", "compare.hip", "hisparse_swap.hip",
-           "stream_probe.hip", "build_info.hip")
+           "stream_probe.hip", "decode_step.hip", "build_info.hip")
 OFFLOAD_ARCH = "gfx950"
 
 COMMON_FLAGS = [

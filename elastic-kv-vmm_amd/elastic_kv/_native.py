@@ -88,6 +88,8 @@ _SIGNATURES = {
     "ekv_host_alloc": ([ct.c_uint64, ct.POINTER(ct.c_void_p), ct.POINTER(ct.c_void_p)], ct.c_int),
     "ekv_host_free": ([ct.c_void_p], ct.c_int),
     "ekv_stream_probe": ([ct.c_int, ct.c_void_p, ct.c_void_p, ct.c_uint64, ct.c_int, ct.c_void_p], ct.c_int),
+    "ekv_decode_step_workspace_bytes": ([ct.c_int64, ct.c_int64, ct.c_int64], ct.c_uint64),
+    "ekv_decode_step": ([ct.c_void_p, ct.c_void_p, ct.c_uint64, ct.c_void_p], ct.c_int),
 }
 KERNEL_SYMBOLS = tuple(_SIGNATURES)
 

@@ -335,6 +335,56 @@ int ekv_move_kv(const ekv_planes* src, const ekv_tensor* src_rows,
 int ekv_compare_kv(const ekv_planes* a, const ekv_tensor* a_rows, const ekv_planes* b,
                    const ekv_tensor* b_rows, const ekv_tensor* equal, void* stream);
 
+/* The arguments of ekv_decode_step: those of the lookup, the swap-in, the
+ * promote move and the gather it runs, with the intermediates left out. */
+typedef struct ekv_step_args {
+    const ekv_tensor* topk;           /* [L, B, K] Top-K block ids, -1 = padding */
+    int64_t block_size;
+    const ekv_tensor* rows;           /* [B] request of each batch row */
+    const ekv_tensor* lengths;        /* [B] */
+    const ekv_tensor* selected;       /* [S] batch rows to serve; they name distinct requests */
+    const ekv_tensor* table;          /* [L, R, T]: int16 local slot + 1, or int32 global slot; 0 = not resident */
+    const ekv_tensor* resident_bits;  /* NULL or its residency summary ... */
+    int64_t bits_shift;               /* ... one bit per 2^bits_shift positions */
+    const ekv_tensor* slot_base;      /* [R] global slot of each request's local slot 0 */
+    const ekv_tensor* slot_token;     /* [L, R, C] LRU state, as ekv_swap_in */
+    const ekv_tensor* stamps;         /* [L, R, C] */
+    int64_t step;                     /* the LRU step (>= 0), or -1 with step_counter */
+    const ekv_tensor* step_counter;   /* NULL or [1] int64 in device memory (graph replays) */
+    const ekv_tensor* status;         /* NULL or [1] int32: EKV_SWAP_* bits */
+    const ekv_tensor* host_table;     /* [R, T] token -> row of the host planes */
+    const ekv_planes* host;           /* K/V rows in mapped pinned host memory */
+    const ekv_planes* pool;           /* the hot K/V pool */
+    const ekv_tensor* slots;          /* out [L, B, K * block_size] int32: each lane's slot after the swap-in */
+    const ekv_kv_rows* out;           /* out: the gathered K/V rows of every lane */
+} ekv_step_args;
+
+/*
+ * Workspace bytes ekv_decode_step needs for L layers x B rows x W lanes per
+ * row: the miss list and two promotion lists ([L, B, W] int32 each) and the
+ * miss counts ([L, B] int32), each 256-byte aligned. UINT64_MAX on error.
+ */
+uint64_t ekv_decode_step_workspace_bytes(int64_t layers, int64_t batch, int64_t width);
+
+/*
+ * One decode step: ekv_resolve_resident_local (int16 table) /
+ * ekv_resolve_resident_bits / ekv_resolve_resident with miss compaction ->
+ * ekv_swap_in (or ekv_swap_in_counted with step_counter) -> ekv_move_kv of
+ * the promotions from args->host into args->pool -> ekv_gather_kv of every
+ * lane's slot into args->out, queued in that order on `stream`. Each stage
+ * keeps its own entry point's contract; the miss list, counts and promotion
+ * lists live in `workspace` (a 256-byte aligned device buffer of at least
+ * ekv_decode_step_workspace_bytes; its contents on entry do not matter: the
+ * counts are zeroed by a kernel first, so rows outside `selected` promote
+ * nothing). After the step every selected lane's slot holds its token's row;
+ * rows outside `selected` keep their slots and are gathered as they stand.
+ * Records no memset, so the call can be captured in a HIP graph.
+ * Replaces, for one layer or several: the lookup + host-backed swap of the
+ * reference's decode path (adaptive_sparse/request_residency.py:805-832) and
+ * the read of the selected rows that follows it.
+ */
+int ekv_decode_step(const ekv_step_args* args, void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* Modes of ekv_stream_probe. */
 #define EKV_PROBE_READ 0   /* read src (fold, no stores)       */
 #define EKV_PROBE_WRITE 1  /* write zeros to dst                */
