@@ -18,7 +18,17 @@
 #include "ekv_tensor_util.h"
 
 #include <algorithm>
+#include <mutex>
 #include <string>
+
+// The allocation-free form (ekv_decode_step_static) keeps its workspace in
+// this file-scope device array: every GPU the library runs on holds one copy
+// (32 MiB) until the process ends, and every call on that GPU shares it. In
+// host code `scratch` names a host-side stand-in, never the device memory:
+// its device address is taken once per device with hipGetSymbolAddress
+// (static_address below) and only that address is used.
+constexpr uint64_t kStaticWorkspaceBytes = uint64_t{32} << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticWorkspaceBytes];
 
 namespace ekv {
 namespace {
@@ -127,8 +137,56 @@ int decode_step(const ekv_step_args& s, void* workspace, uint64_t workspace_byte
     return 0;
 }
 
+constexpr int kMaxDevices = 64;
+
+// Device address of the current device's `scratch` (taken on the first call on
+// that device, with the device current).
+void* static_address() {
+    static std::mutex lock;
+    static void* address[kMaxDevices] = {};
+    int device = -1;
+    check_hip(hipGetDevice(&device), "hipGetDevice");
+    if (device < 0 || device >= kMaxDevices) {
+        throw std::runtime_error("device ordinal " + std::to_string(device) + " out of range");
+    }
+    std::lock_guard<std::mutex> guard(lock);
+    if (address[device] == nullptr) {
+        void* found = nullptr;
+        check_hip(hipGetSymbolAddress(&found, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        if (found == nullptr) {
+            throw std::runtime_error("hipGetSymbolAddress(scratch) returned no address");
+        }
+        address[device] = found;
+    }
+    return address[device];
+}
+
+int decode_step_static(const ekv_step_args& s, void* stream) {
+    const ekv_tensor& topk = need(s.topk, "topk");
+    need_ndim(topk, 3, "topk");
+    if (s.block_size < 1) {
+        throw std::invalid_argument("block_size must be positive");
+    }
+    const uint64_t needed = step_workspace_bytes(topk.shape[0], topk.shape[1], topk.shape[2] * s.block_size);
+    if (needed > kStaticWorkspaceBytes) {
+        throw std::invalid_argument("the step needs " + std::to_string(needed) +
+                                    " workspace bytes, more than the static workspace's " +
+                                    std::to_string(kStaticWorkspaceBytes) + "; split it over fewer layers or rows");
+    }
+    return decode_step(s, static_address(), kStaticWorkspaceBytes, stream);
+}
+
 }  // namespace
 }  // namespace ekv
+
+extern "C" int ekv_decode_step_static(const ekv_step_args* args, void* stream) {
+    return ekv::guarded(-1, [&] {
+        if (args == nullptr) {
+            throw std::invalid_argument("args is required");
+        }
+        return ekv::decode_step_static(*args, stream);
+    });
+}
 
 extern "C" uint64_t ekv_decode_step_workspace_bytes(int64_t layers, int64_t batch, int64_t width) {
     return ekv::guarded(~uint64_t{0}, [&] { return ekv::step_workspace_bytes(layers, batch, width); });

@@ -90,6 +90,7 @@ _SIGNATURES = {
     "ekv_stream_probe": ([ct.c_int, ct.c_void_p, ct.c_void_p, ct.c_uint64, ct.c_int, ct.c_void_p], ct.c_int),
     "ekv_decode_step_workspace_bytes": ([ct.c_int64, ct.c_int64, ct.c_int64], ct.c_uint64),
     "ekv_decode_step": ([ct.c_void_p, ct.c_void_p, ct.c_uint64, ct.c_void_p], ct.c_int),
+    "ekv_decode_step_static": ([ct.c_void_p, ct.c_void_p], ct.c_int),
 }
 KERNEL_SYMBOLS = tuple(_SIGNATURES)
 

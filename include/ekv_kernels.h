@@ -385,6 +385,22 @@ uint64_t ekv_decode_step_workspace_bytes(int64_t layers, int64_t batch, int64_t 
  */
 int ekv_decode_step(const ekv_step_args* args, void* workspace, uint64_t workspace_bytes, void* stream);
 
+/*
+ * ekv_decode_step without a workspace argument and without any allocation:
+ * the miss list, counts and promotion lists live in a file-scope device
+ * array of the library, 32 MiB per GPU (held from the first call until the
+ * process ends), so the step may take at most
+ * ekv_decode_step_workspace_bytes(L, B, W) <= 33554432 bytes (e.g. 8 layers
+ * x 128 rows x 2048 lanes); a larger step fails with a message (split it over
+ * fewer layers or rows). Every call on one GPU shares that array: calls that
+ * overlap on one GPU (other streams, other threads) race, so they must be
+ * ordered. Otherwise it behaves exactly as ekv_decode_step.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).
+ */
+int ekv_decode_step_static(const ekv_step_args* args, void* stream);
+
 /* Modes of ekv_stream_probe. */
 #define EKV_PROBE_READ 0   /* read src (fold, no stores)       */
 #define EKV_PROBE_WRITE 1  /* write zeros to dst                */
