@@ -85,6 +85,8 @@ def parse_args():
                         help="bound of each CPU baseline sample of the extra configs")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-copy-ceiling", action="store_true")
+    parser.add_argument("--profile-ranges", action="store_true",
+                        help="keep EKV_PROFILE_RANGES=1 (ekv/* profiler and roctx ranges); timed runs drop it")
     parser.add_argument("--no-extras", action="store_true",
                         help="decode-read only: skip configs 1, 2 and 4 in the default line")
     return parser.parse_args()
@@ -1138,6 +1140,14 @@ EXTRA_CONFIGS = (("config1_topk_gather", "topk-gather"), ("config2_block_gather"
                  ("config4_migration", "migration"))
 
 
+def apply_profile_switch(environment, keep):
+    """Diagnostic ranges cost host time per call: a timed run has none unless asked."""
+    if keep:
+        environment["EKV_PROFILE_RANGES"] = "1"
+    else:
+        environment.pop("EKV_PROFILE_RANGES", None)
+
+
 def summary(result):
     """The fields of another workload's line that the default line carries for it."""
     keys = ("metric", "value", "unit", "ms_per_step", "roofline", "cpu_baseline", "config", "lookup_us_per_step",
@@ -1151,6 +1161,7 @@ def main():
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: this path has no "
               "cross-GPU step in this build (each GPU runs its own shard independently)", file=sys.stderr)
         return 2
+    apply_profile_switch(os.environ, args.profile_ranges)
     import torch
 
     device = torch.device("cuda:0")
@@ -1163,6 +1174,7 @@ def main():
     result = WORKLOADS[args.workload](torch, args, device)
     result["copy_ceiling_gbs"] = None if ceilings is None else ceilings["copy"]["best_gbs"]
     result["stream_ceilings_gbs"] = ceilings
+    result["profile_ranges"] = args.profile_ranges
     if args.workload == "decode-read" and not args.no_extras:
         torch.cuda.empty_cache()
         for key, workload in EXTRA_CONFIGS:

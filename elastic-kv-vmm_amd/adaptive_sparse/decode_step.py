@@ -17,6 +17,7 @@ import torch
 from elastic_kv import _native
 
 from .kv_pool import KVPlanes
+from .profile_ranges import profile_range
 from .sparse_read import _dense_struct, _planes_struct
 
 _P_TENSOR = ct.POINTER(_native.EkvTensor)
@@ -72,6 +73,7 @@ def step_args(topk, rows, lengths, selected, buffers, host_table, host_planes, p
     return args, keep
 
 
+@profile_range("native/decode_step")
 def decode_step(topk, rows, lengths, buffers, host_table, host_planes, pool_planes, slots, output, *,
                 block_size=1, selected=None, step=None, workspace=None):
     """Lookup -> swap-in -> promote -> gather for the selected rows of every layer of `topk`.

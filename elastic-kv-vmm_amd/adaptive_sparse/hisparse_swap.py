@@ -26,6 +26,8 @@ import torch
 
 from elastic_kv import _native
 
+from .profile_ranges import profile_range
+
 MAX_HOT = 4096
 MAX_LANES = 2048
 
@@ -57,6 +59,7 @@ def host_device_pointer(tensor):
     return device.value
 
 
+@profile_range("native/hisparse_swap")
 def load_blocks_to_device_buffer_mha(top_k_blocks, device_buffer_tokens, host_cache_locs, device_buffer_locs,
                                      host_cache_k, host_cache_v, device_buffer_k, device_buffer_v,
                                      top_k_device_locs, req_pool_indices, seq_lens, lru_slots, item_size_bytes,

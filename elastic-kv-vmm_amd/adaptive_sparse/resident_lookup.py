@@ -30,7 +30,10 @@ import torch
 
 from elastic_kv import _native
 
+from .profile_ranges import profile_range
 
+
+@profile_range("native/lookup")
 def resolve_resident(topk, table, mapping, rows, lengths, selected, output, block_size, *,
                      misses=None, miss_count=None, resident_bits=None, bits_shift=0, slot_base=None):
     """Write only selected rows into an existing [L, B, K * block_size] tensor.

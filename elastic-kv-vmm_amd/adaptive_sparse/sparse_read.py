@@ -16,6 +16,7 @@ from elastic_kv import _native
 from experimental.sparse_read import gather_rows  # noqa: F401  (re-export)
 
 from .kv_pool import KVPlanes
+from .profile_ranges import profile_range
 
 
 def _planes_struct(planes):
@@ -66,6 +67,7 @@ def _kv_call(entry, planes, slots, dense, zero_below, name):
     _native.check(lib, status, entry)
 
 
+@profile_range("native/gather")
 def gather_kv(planes, slots, output, *, zero_below=1):
     """output[b, l, kv, k] = plane(l, kv)[slots[l, b, k]] for valid slots.
 
@@ -76,6 +78,7 @@ def gather_kv(planes, slots, output, *, zero_below=1):
     _kv_call("ekv_gather_kv", planes, slots, output, zero_below, "output")
 
 
+@profile_range("native/scatter")
 def scatter_kv(planes, slots, source, *, zero_below=1):
     """plane(l, kv)[slots[l, b, k]] = source[b, l, kv, k] for valid slots."""
     _kv_call("ekv_scatter_kv", planes, slots, source, zero_below, "source")

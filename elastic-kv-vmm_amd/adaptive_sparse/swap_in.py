@@ -20,6 +20,7 @@ import torch
 from elastic_kv import _native
 
 from .kv_pool import KVPlanes
+from .profile_ranges import profile_range
 from .sparse_read import _planes_struct
 
 INT32_MIN = -(1 << 31)
@@ -146,6 +147,7 @@ def _ranks_from_stamps(stamps):
     return ranks
 
 
+@profile_range("native/swap")
 def swap_in(topk, block_size, rows, selected, slots, misses, miss_count, buffers, host_table,
             promote_src, promote_dst, *, step=None, check=False):
     """Run one swap-in step (see module docstring); advances buffers.step.
@@ -193,6 +195,7 @@ def swap_in(topk, block_size, rows, selected, slots, misses, miss_count, buffers
         buffers.check_status()
 
 
+@profile_range("native/promote")
 def move_kv(src_planes, src_rows, dst_planes, dst_rows, counts, *, zero_below=1):
     """dst(l, kv)[dst_rows[l, b, i]] = src(l, kv)[src_rows[l, b, i]] for i < counts[l, b]."""
     for planes in (src_planes, dst_planes):
