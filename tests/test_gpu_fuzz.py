@@ -264,6 +264,77 @@ def test_local_slot_prefetch_many_items_per_workgroup(gpu, coracle, seed):
     check(output, misses, counts, (seed, layers, batch, k, cols, layered, "int32"))
 
 
+@pytest.mark.parametrize("seed", range(40))
+def test_summary_lookup_random_configurations(gpu, coracle, seed):
+    # Single-level lookups behind residency summaries of random coarseness
+    # (shift 0-9): summaries of at most 64 words per row take the one-wave-per-
+    # item kernel (its rows are walked in passes of 512 lanes, here 1-10 of
+    # them, the last one partial), wider ones the prefetching or strided
+    # kernels. int16 local-slot and int32 global-slot tables; exact summaries
+    # and supersets with stray bits past the length and past the table; stray
+    # rows and selections, lengths past the table, negative entries.
+    rng = np.random.default_rng(9700 + seed)
+    layers = int(rng.integers(1, 5))
+    batch = int(rng.integers(1, 13))
+    k = 8 * int(rng.integers(1, 600))
+    rrows = int(rng.integers(1, 10))
+    cols = int(rng.integers(1, 140_000)) if seed % 3 else int(rng.integers(1, 3000))
+    shift = int(rng.integers(0, 10))
+    layered = bool(rng.random() < 0.7)
+    compact = bool(rng.random() < 0.85)
+    local = seed % 2 == 0
+    lengths = rng.integers(-2, cols + 5, size=batch)
+    rows = rng.integers(0, rrows, size=batch)
+    stray = rng.random(batch) < 0.1
+    rows[stray] = rng.choice([-1, rrows, rrows + 7], size=int(stray.sum()))
+    topk = rng.integers(-1, cols + 2, size=(layers, batch, k))
+    for r in range(batch):
+        hi = max(1, min(int(lengths[r]), cols))
+        near = rng.random((layers, k)) < 0.7
+        topk[:, r][near] = rng.integers(max(0, hi - 4096), hi + 1, size=(layers, k))[near]
+    shape = (layers, rrows, cols) if layered else (rrows, cols)
+    local_table = rng.integers(1, 1 << 15, size=shape)
+    local_table[rng.random(shape) < 0.9] = 0
+    local_table[rng.random(shape) < 0.01] = -int(rng.integers(1, 1 << 15))
+    slot_base = rng.integers(1, 1 << 20, size=rrows)
+    req_axis = 1 if layered else 0
+    bases = np.expand_dims(slot_base, tuple(a for a in range(len(shape)) if a != req_axis))
+    table = np.where(local_table > 0, bases + local_table - 1, 0)
+    selected = rng.permutation(batch)[: int(rng.integers(1, batch + 1))]
+    if rng.random() < 0.2:
+        selected = np.concatenate([selected, [-1, batch]])
+    initial = np.full((layers, batch, k), -77, np.int32)
+    want, want_misses, want_counts = coracle.resolve_resident(topk, table, None, rows, lengths, selected, 1,
+                                                              initial, with_misses=True)
+    if local:
+        table_d, base_d = torch.tensor(local_table, dtype=torch.int16, device=gpu), torch.tensor(slot_base, device=gpu)
+    else:
+        table_d, base_d = torch.tensor(table, dtype=torch.int32, device=gpu), None
+    bits = build_residency_bits(table_d, shift=shift)
+    if seed % 4 >= 2:
+        extra = (rng.random(bits.shape) < 0.3) * rng.integers(0, 1 << 31, bits.shape)
+        bits |= torch.tensor(extra, dtype=torch.int32, device=gpu)
+    output = torch.tensor(initial, device=gpu)
+    misses = torch.full((layers, batch, k), -5, dtype=torch.int32, device=gpu) if compact else None
+    counts = torch.full((layers, batch), -5, dtype=torch.int32, device=gpu) if compact else None
+    resolve_resident(torch.tensor(topk, dtype=torch.int32, device=gpu), table_d, None, torch.tensor(rows, device=gpu),
+                     torch.tensor(lengths, dtype=torch.int32, device=gpu), torch.tensor(selected, device=gpu),
+                     output, 1, misses=misses, miss_count=counts, resident_bits=bits, bits_shift=shift,
+                     slot_base=base_d)
+    case = (seed, layers, batch, k, cols, shift, layered, local)
+    assert np.array_equal(output.cpu().numpy(), want), case
+    if compact:
+        got_counts, got_misses = counts.cpu().numpy(), misses.cpu().numpy()
+        for layer in range(layers):
+            for row in range(batch):
+                if row in selected:
+                    c = want_counts[layer, row]
+                    assert got_counts[layer, row] == c, case
+                    assert np.array_equal(got_misses[layer, row, :c], want_misses[layer, row, :c]), case
+                else:
+                    assert got_counts[layer, row] == -5, case
+
+
 def random_planes(rng, gpu, layers, kv, rows, row_bytes):
     row_stride = row_bytes + int(rng.choice([0, 0, 2, 8, 16, 48]))
     plane = rows * row_stride + int(rng.choice([0, 16, 64, 100]))
