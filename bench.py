@@ -16,7 +16,9 @@ divided by the measured step time, lookup included.
 The default line also carries, as extra keys, the streaming ceilings of this
 box (own read / write / copy kernels), the lookup variants timed in
 alternating arms, and configs 1, 2 and 4 (topk-gather, block-gather,
-migration below), each with its own roofline, parity flags and CPU baseline.
+migration below), each with its own roofline, parity flags and CPU baseline;
+config 4 also with the VMM spare pool (--spare-chunks: reclaimed chunks'
+memory kept for the next commits).
 The CPU baseline is the reference's torch CPU path restated
 (oracle/torch_path.py: adaptive_sparse/request_residency.py:819-825, nonzero,
 index_select) at all visible host threads and at one thread.
@@ -78,6 +80,8 @@ def parse_args():
     parser.add_argument("--remap-fraction", type=float, default=0.05,
                         help="share of pool chunks unmapped and remapped per composite step")
     parser.add_argument("--capacity", type=int, default=4096, help="hot slots per request (decode-read)")
+    parser.add_argument("--spare-chunks", type=int, default=0,
+                        help="VMM spare pool of the migration and composite pools (0: release at once)")
     parser.add_argument("--seed", type=int, default=2024)
     parser.add_argument("--cpu-seconds", type=float, default=8.0,
                         help="bound of each CPU baseline sample (per thread count)")
@@ -692,6 +696,8 @@ def run_migration(torch, args, device):
     BLOCKS, LIVE, MOVE = 2048, 1024, 512
     layout = BlockMajorLayout(blocks=BLOCKS, layers=36, kv=2, row_bytes=16 * 8 * 128 * 2)
     pool = PagedKVPool(layout, device=device.index or 0)
+    if args.spare_chunks:
+        pool.backing.set_spare_chunks(args.spare_chunks)   # the sources' chunks serve the next tick's targets
     rng = np.random.default_rng(args.seed)
     live = sorted(rng.choice(np.arange(1, BLOCKS), size=LIVE, replace=False).tolist())
     pool.allocate(live)
@@ -772,7 +778,8 @@ def run_migration(torch, args, device):
                                              f" GB read + written; no PCIe leg exists on the CPU path)", parity)
         del host_pool
     config = {"workload": "page-migration-round-trip", "blocks_per_tick": MOVE, "block_bytes": layout.block_bytes,
-              "layers": 36, "kv_heads": 8, "head_dim": 128, "block_tokens": 16, "pool_blocks": BLOCKS}
+              "layers": 36, "kv_heads": 8, "head_dim": 128, "block_tokens": 16, "pool_blocks": BLOCKS,
+              "spare_chunks": args.spare_chunks}
     roof = roofline(pack_bytes / (pack_ms / 1e3) / 1e9, "copy_small_rows<KvGather,16> (pack, 32 KiB rows)",
                     pack_bytes, pack_ms, read_traffic("pack_page_migration.md"))
     extra = {"verified_round_trip": verified, "tick_ms": round(tick_s * 1e3, 3),
@@ -988,6 +995,8 @@ def run_composite(torch, args, device):
     output = torch.empty((R, L, 2, K, 256), dtype=torch.bfloat16, device=device)
     chunk_rows = layout.chunk_bytes // row_bytes
     remap_count = int(round(args.remap_fraction * backing.chunk_count))
+    if args.spare_chunks:
+        backing.set_spare_chunks(args.spare_chunks)   # reclaimed chunks' memory kept for the re-ensure
     rng = np.random.default_rng(args.seed)
     torch.cuda.synchronize()
     log(f"composite ready: T={T}, host arena {arena.nbytes / 1e9:.1f} GB, remap {remap_count} chunks/step")
@@ -1013,7 +1022,7 @@ def run_composite(torch, args, device):
         build_residency_bits(buffers.table, out=buffers.bits)
         torch.cuda.synchronize()
         r1 = time.perf_counter()
-        backing.reclaim(chosen.tolist())          # synchronizes, then hipMemUnmap + release
+        backing.reclaim(chosen.tolist())          # synchronizes, then hipMemUnmap + release (or keep)
         r2 = time.perf_counter()
         backing.ensure(chosen.tolist())           # hipMemCreate + map + access + zero fill
         r3 = time.perf_counter()
@@ -1109,6 +1118,7 @@ def run_composite(torch, args, device):
         f"{misses_per_step / lanes:.3f} of lanes promoted; verified {verified}")
     config = {"workload": "composite-elastic-decode", "requests": R, "context": "uniform [4096, 32768]", "layers": L,
               "kv_heads": 2, "head_dim": 128, "topk": K, "hot_capacity": C, "remap_fraction": args.remap_fraction,
+              "spare_chunks": args.spare_chunks,
               "host_rows_per_plane": HOST_ROWS}
     achieved = gather_bytes / (mean["gather_ms"] / 1e3) / 1e9
     roof = roofline(achieved, "copy_small_rows<KvGather,16> (ekv_gather_kv)", gather_bytes, mean["gather_ms"], None)
@@ -1136,8 +1146,12 @@ WORKLOADS = {"decode-read": run_decode_read, "topk-gather": run_topk_gather,
              "hisparse-swap": run_hisparse_swap}
 
 
-EXTRA_CONFIGS = (("config1_topk_gather", "topk-gather"), ("config2_block_gather", "block-gather"),
-                 ("config4_migration", "migration"))
+# (key, workload, argument overrides) of the other configurations the default line carries.
+MIGRATION_SPARE_CHUNKS = 700   # > the ~500 chunks a 512-block tick frees and maps
+EXTRA_CONFIGS = (("config1_topk_gather", "topk-gather", {}), ("config2_block_gather", "block-gather", {}),
+                 ("config4_migration", "migration", {}),
+                 ("config4_migration_spare_pool", "migration",
+                  {"spare_chunks": MIGRATION_SPARE_CHUNKS, "no_cpu_baseline": True}))
 
 
 def apply_profile_switch(environment, keep):
@@ -1177,9 +1191,10 @@ def main():
     result["profile_ranges"] = args.profile_ranges
     if args.workload == "decode-read" and not args.no_extras:
         torch.cuda.empty_cache()
-        for key, workload in EXTRA_CONFIGS:
-            log(f"extra: {workload}")
-            result[key] = summary(WORKLOADS[workload](torch, args, device))
+        for key, workload, overrides in EXTRA_CONFIGS:
+            log(f"extra: {key}")
+            result[key] = summary(WORKLOADS[workload](torch, argparse.Namespace(**{**vars(args), **overrides}),
+                                                      device))
             torch.cuda.empty_cache()
     print(json.dumps(result), flush=True)
     return 0

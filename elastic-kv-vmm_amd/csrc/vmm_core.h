@@ -14,7 +14,14 @@
 //   * a decommit that fails part-way poisons the object (the chunks released
 //     before the failure cannot be restored);
 //   * a failed close keeps the object alive so the close can be retried (the
-//     one deliberate difference from the reference).
+//     one deliberate difference from the reference);
+//   * an optional spare pool (off by default; no reference counterpart): up
+//     to `spare limit` physical chunks that a decommit unmapped are kept
+//     instead of released, and the next commits map them instead of creating
+//     new ones (zero-filled like any committed chunk). It saves a create and
+//     a release per recycled chunk, whose cost grows with the number of live
+//     allocations, and holds that memory until a commit takes it, the limit
+//     is lowered, or the object closes.
 //
 // The driver is a template parameter: HipDriver (vmm_backing.hip) on the GPU,
 // a fault-injecting driver in the native tests. A driver provides, with int
@@ -110,7 +117,12 @@ public:
             for (const uint64_t id : fresh) {
                 Chunk& chunk = chunks_[id];
                 ++touched;
-                check(driver_.create(chunk_bytes_, &chunk.handle), "hipMemCreate");
+                if (!spare_.empty()) {
+                    chunk.handle = spare_.back();   // a rollback releases it like a created one
+                    spare_.pop_back();
+                } else {
+                    check(driver_.create(chunk_bytes_, &chunk.handle), "hipMemCreate");
+                }
                 chunk.created = true;
                 check(driver_.map(address(id), chunk_bytes_, chunk.handle), "hipMemMap");
                 chunk.mapped = true;
@@ -161,7 +173,7 @@ public:
         wait_for_zero();
         for (const uint64_t id : mapped) {
             auto it = chunks_.find(id);
-            const int status = release(id, it->second);
+            const int status = release(id, it->second, /*keep_spare=*/true);
             if (status != 0) {
                 // Earlier chunks of this call are gone already; the caller
                 // must tear the object down.
@@ -196,7 +208,9 @@ public:
                     record(status);
                     it = status == 0 ? chunks_.erase(it) : std::next(it);
                 }
-                if (chunks_.empty() && base_) {
+                spare_limit_ = 0;
+                record(release_spares(0));
+                if (chunks_.empty() && spare_.empty() && base_) {
                     const int status = driver_.free_range(base_, reserved_bytes_);
                     record(status);
                     if (status == 0) {
@@ -226,6 +240,32 @@ public:
             check(status, "close backing");
         }
     }
+
+    // Keep up to `chunks` decommitted physical chunks for reuse (0 = release
+    // every decommitted chunk at once, the reference's behaviour). Lowering
+    // the limit releases the chunks held above it.
+    void set_spare_limit(uint64_t chunks) {
+        if (!open_) {
+            throw std::runtime_error("backing is closed");
+        }
+        if (poisoned_) {
+            throw std::runtime_error("backing is poisoned after a partial HIP failure");
+        }
+        if (chunks > reserved_bytes_ / chunk_bytes_) {
+            throw std::invalid_argument("spare limit exceeds the reservation's chunk count");
+        }
+        typename Driver::Scope scope(driver_);
+        check(scope.status(), "select the device");
+        spare_.reserve(static_cast<size_t>(chunks));   // a decommit then never allocates to keep one
+        spare_limit_ = chunks;
+        const int status = release_spares(static_cast<size_t>(chunks));
+        if (status != 0) {
+            poisoned_ = true;
+            check(status, "release spare chunk");
+        }
+    }
+
+    uint64_t spare() const { return static_cast<uint64_t>(spare_.size()) * chunk_bytes_; }
 
     uint64_t base() const { return base_; }
     uint64_t granularity() const { return granularity_; }
@@ -290,7 +330,9 @@ private:
         return result;
     }
 
-    int release(uint64_t id, Chunk& chunk) noexcept {
+    // Unmaps and releases a chunk; with keep_spare, a created chunk goes to
+    // the spare pool instead while it holds fewer than the limit.
+    int release(uint64_t id, Chunk& chunk, bool keep_spare = false) noexcept {
         if (chunk.mapped) {
             const int status = driver_.unmap(address(id), chunk_bytes_);
             if (status != 0) {
@@ -298,12 +340,29 @@ private:
             }
             chunk.mapped = false;
         }
+        if (chunk.created && keep_spare && spare_.size() < spare_limit_) {
+            spare_.push_back(chunk.handle);   // capacity reserved by set_spare_limit
+            chunk.created = false;
+            return 0;
+        }
         if (chunk.created) {
             const int status = driver_.release(chunk.handle);
             if (status != 0) {
                 return status;
             }
             chunk.created = false;
+        }
+        return 0;
+    }
+
+    // Releases spare chunks until at most `keep` remain; the first failure (0 if none).
+    int release_spares(size_t keep) noexcept {
+        while (spare_.size() > keep) {
+            const int status = driver_.release(spare_.back());
+            if (status != 0) {
+                return status;
+            }
+            spare_.pop_back();
         }
         return 0;
     }
@@ -318,6 +377,8 @@ private:
     bool stream_open_ = false;
     bool open_ = false;
     std::map<uint64_t, Chunk> chunks_;
+    std::vector<uint64_t> spare_;   // unmapped physical chunks kept for reuse
+    uint64_t spare_limit_ = 0;
 };
 
 constexpr uint64_t kInvalid = std::numeric_limits<uint64_t>::max();
@@ -375,6 +436,15 @@ struct Abi {
     static int poisoned(void* handle) {
         return guarded(-1, [&] { return require(handle).poisoned() ? 1 : 0; });
     }
+    static int set_spare(void* handle, uint64_t chunks) {
+        return guarded(-1, [&] {
+            require(handle).set_spare_limit(chunks);
+            return 0;
+        });
+    }
+    static uint64_t spare(void* handle) {
+        return guarded(kInvalid, [&] { return require(handle).spare(); });
+    }
     static int close(void* handle) {
         return guarded(-1, [&] {
             if (handle == nullptr) {
@@ -418,6 +488,8 @@ struct Abi {
     uint64_t ev_reserved(void* handle) { return ::ekv::vmm::Abi<DRIVER>::reserved(handle); }                  \
     uint64_t ev_granularity(void* handle) { return ::ekv::vmm::Abi<DRIVER>::granularity(handle); }            \
     int ev_poisoned(void* handle) { return ::ekv::vmm::Abi<DRIVER>::poisoned(handle); }                       \
+    int ev_set_spare(void* handle, uint64_t chunks) { return ::ekv::vmm::Abi<DRIVER>::set_spare(handle, chunks); } \
+    uint64_t ev_spare(void* handle) { return ::ekv::vmm::Abi<DRIVER>::spare(handle); }                        \
     const char* ev_error(void) { return ::ekv::last_error().c_str(); }                                        \
     int ev_close(void* handle) { return ::ekv::vmm::Abi<DRIVER>::close(handle); }                             \
     }

@@ -80,6 +80,21 @@ uint64_t ev_granularity(void* handle);
  * Replaces: native/elastic_vmm.cpp:353-355 (ev_poisoned). */
 int ev_poisoned(void* handle);
 
+/* Keep up to `chunks` physical chunks that ev_drop unmaps, instead of
+ * releasing them, for the next ev_ensure / ev_precommit to map (they are
+ * zero-filled like new chunks); 0, the default, releases every dropped chunk
+ * at once. Lowering the limit releases the chunks held above it; ev_close
+ * releases them all. Saves a create and a release per recycled chunk, and
+ * holds that memory (ev_spare) until a commit takes it. Returns 0, or -1 on
+ * error (a limit above the reservation's chunk count, a closed or poisoned
+ * object; a failed release poisons it).
+ * No reference counterpart: for callers that decommit and recommit chunks
+ * every step (remapping, migration) and can keep that memory. */
+int ev_set_spare(void* handle, uint64_t chunks);
+
+/* Bytes held by the spare pool; UINT64_MAX on error. No reference counterpart. */
+uint64_t ev_spare(void* handle);
+
 /* Message of the last failed call on this thread ("" after a success).
  * Shared by every entry point of this library, ekv_* included.
  * Replaces: native/elastic_vmm.cpp:357 (ev_error). */

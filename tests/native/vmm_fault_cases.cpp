@@ -209,6 +209,58 @@ void failed_close_can_be_retried(Op op, const char* what) {
     expect_clean();
 }
 
+// The spare pool: dropped chunks up to the limit keep their physical memory,
+// later commits map it instead of creating (and zero it like new chunks),
+// lowering the limit and close release it, and a commit that fails after
+// taking a spare chunk releases it with the rest of its batch.
+void spare_pool() {
+    current = "spare pool";
+    void* h = open_backing(8);
+    CHECK(ev_spare(h) == 0);
+    CHECK(ev_set_spare(h, 9) == -1 && error_has("chunk count"));
+    CHECK(ev_set_spare(h, 3) == 0);
+    CHECK(ensure(h, {0, 1, 2, 3, 4}) == 0);
+    CHECK(fake_calls(kCreate) == 5);
+    CHECK(drop(h, {1, 2, 3, 4}) == 0);                       // three kept, one released
+    CHECK(ev_spare(h) == 3 * kChunk && ev_backed(h) == kChunk);
+    CHECK(fake_calls(kRelease) == 1 && fake_live_handles() == 4 && fake_live_maps() == 1);
+    const long zeros = fake_calls(kZero);
+    CHECK(ensure(h, {5, 6}) == 0);                           // both from the pool
+    CHECK(fake_calls(kCreate) == 5 && ev_spare(h) == kChunk && ev_backed(h) == 3 * kChunk);
+    CHECK(fake_calls(kZero) == zeros + 1);                   // one run, zero-filled like new chunks
+    CHECK(ensure(h, {7}) == 0 && ev_spare(h) == 0);           // the last spare
+    CHECK(ensure(h, {2}) == 0 && fake_calls(kCreate) == 6);   // pool empty: created
+    // a failed batch releases the spare chunk it had taken
+    CHECK(drop(h, {5, 6}) == 0 && ev_spare(h) == 2 * kChunk);
+    const long released = fake_calls(kRelease);
+    fake_fail(kMap, 2, 0);                                    // the batch's second map fails
+    CHECK(ensure(h, {3, 4}) == -1 && error_has("hipMemMap"));
+    CHECK(ev_poisoned(h) == 0 && ev_spare(h) == 0 && ev_backed(h) == 3 * kChunk);
+    CHECK(fake_calls(kRelease) == released + 2);
+    CHECK(fake_violations() == 0);
+    // lowering the limit releases what is held above it
+    CHECK(drop(h, {0, 2}) == 0 && ev_spare(h) == 2 * kChunk);
+    CHECK(ev_set_spare(h, 1) == 0 && ev_spare(h) == kChunk);
+    CHECK(ev_set_spare(h, 0) == 0 && ev_spare(h) == 0);
+    const long before = fake_calls(kRelease);
+    CHECK(ensure(h, {1}) == 0 && drop(h, {1}) == 0);          // limit 0: released at once
+    CHECK(ev_spare(h) == 0 && fake_calls(kRelease) == before + 1);
+    // close releases the pool
+    CHECK(ev_set_spare(h, 4) == 0 && drop(h, {7}) == 0 && ev_spare(h) == kChunk);
+    CHECK(ev_close(h) == 0);
+    expect_clean();
+    // a release that fails while lowering the limit poisons the object
+    h = open_backing(4);
+    CHECK(ev_set_spare(h, 2) == 0 && ensure(h, {0, 1}) == 0 && drop(h, {0, 1}) == 0);
+    fake_fail(kRelease, 1, 0);
+    CHECK(ev_set_spare(h, 0) == -1 && error_has("release spare chunk"));
+    CHECK(ev_poisoned(h) == 1 && ensure(h, {2}) == -1);
+    fake_reset();
+    CHECK(ev_close(h) == 0);
+    expect_clean();
+    CHECK(ev_set_spare(nullptr, 1) == -1 && ev_spare(nullptr) == UINT64_MAX);
+}
+
 void create_failures() {
     current = "create";
     fake_reset();
@@ -250,6 +302,7 @@ int main() {
     failed_close_can_be_retried(kFree, "close: free fails");
     failed_close_can_be_retried(kCloseStream, "close: stream fails");
     create_failures();
+    spare_pool();
     if (failures != 0) {
         std::fprintf(stderr, "%d check(s) failed; last contract violation: %s\n", failures, fake_last_violation());
         return 1;

@@ -196,3 +196,53 @@ def test_back_to_back_demotes_and_promotes_without_host_syncs(gpu):
             assert torch.equal(pool.page_view(t), before[s]), (s, t)
     finally:
         pool.close()
+
+
+def test_full_tick_of_512_blocks_round_trips_byte_exact(gpu):
+    # The page-migration workload at its own size: a 2048-block pool (4.5 GiB) with
+    # 1024 live blocks; each of two ticks maps 512 fresh destination blocks, packs
+    # 512 scattered sources into staging, copies them to pinned host and back,
+    # unpacks them, and unmaps the chunks only the sources used once the packs have
+    # run. Every destination must hold its source's bytes, every pinned host row its
+    # source, and the pool must shrink by exactly the fenced chunks.
+    blocks, live_count, move = 2048, 1024, 512
+    layout = BlockMajorLayout(blocks=blocks, **BLOCK)
+    pool = PagedKVPool(layout, device=0)
+    try:
+        rng = np.random.default_rng(512)
+        live = sorted(rng.choice(np.arange(1, blocks), size=live_count, replace=False).tolist())
+        pool.allocate(live)
+        gen = torch.Generator(device=gpu).manual_seed(4)
+        for page in live:
+            pool.page_view(page).copy_(torch.randint(0, 256, (layout.block_bytes,), dtype=torch.uint8,
+                                                     device=gpu, generator=gen))
+        engine = MigrationEngine(pool, max_pages=move, sub_batch=64)
+        for tick in range(2):
+            sources = rng.choice(live, size=move, replace=False).tolist()
+            free = sorted(set(range(1, blocks)) - set(live))
+            targets = rng.choice(free, size=move, replace=False).tolist()
+            snapshot = torch.empty((move, layout.block_bytes), dtype=torch.uint8, device=gpu)
+            engine.pack(sources, snapshot)
+            torch.cuda.synchronize()
+            pool.allocate(targets)
+            host = engine.round_trip(sources, targets)
+            pool.release(sources)
+            idle = pool.pages.reclaimable_chunks()
+            fenced = idle & set().union(*(pool.pages.chunks(p) for p in sources))
+            backed = pool.backing.backed_bytes
+            released = pool.trim(after=host.packed, pages=sources)
+            engine.wait()
+            print(f"[migration] tick {tick}: {len(fenced)} chunks unmapped", flush=True)
+            assert released == len(fenced) * layout.chunk_bytes > 0, tick
+            assert pool.backing.backed_bytes == backed - released, tick
+            for i, t in enumerate(targets):
+                assert torch.equal(pool.page_view(t), snapshot[i]), (tick, i)
+            rows = host.rows.tolist()
+            for i in rng.choice(move, size=32, replace=False).tolist():   # pinned host rows, sampled
+                assert torch.equal(engine.host[int(rows[i])], snapshot[i].cpu()), (tick, i)
+            engine.release_host(host)
+            live = sorted(set(live) - set(sources) | set(targets))
+            del snapshot
+    finally:
+        torch.cuda.synchronize()
+        pool.close()

@@ -19,6 +19,44 @@ from experimental.virtual_layout import VirtualKVLayout
 pytestmark = pytest.mark.gpu
 
 
+def test_spare_pool_recycles_reclaimed_chunks_zeroed(gpu):
+    # With a spare pool, reclaimed chunks keep their physical memory and the next
+    # ensure maps it at other addresses: the data written there before must not
+    # show (every committed chunk is zero-filled), the accounting must follow,
+    # and lowering the limit or closing must give the memory back.
+    chunk = DEFAULT_CHUNK_BYTES
+    backing = Backing(8 * chunk, chunk_bytes=chunk, device=0, spare_chunks=3)
+    try:
+        assert backing.ensure(range(6)) == 6
+        raw = backing.raw
+        for i in range(6):
+            raw[i * chunk:(i + 1) * chunk].fill_(i + 1)
+        assert backing.reclaim([2, 3, 4, 5]) == 4
+        assert backing.spare_bytes == 3 * chunk and backing.backed_bytes == 2 * chunk
+        assert backing.ensure([6, 7, 3]) == 3                     # all three from the pool
+        assert backing.spare_bytes == 0 and backing.backed_bytes == 5 * chunk
+        for i in (3, 6, 7):
+            assert torch.count_nonzero(raw[i * chunk:(i + 1) * chunk]).item() == 0, i
+        for i in (0, 1):
+            assert raw[i * chunk:(i + 1) * chunk].eq(i + 1).all().item()
+        raw[6 * chunk:7 * chunk].fill_(9)
+        assert backing.reclaim([6, 7]) == 2 and backing.spare_bytes == 2 * chunk
+        backing.set_spare_chunks(1)
+        assert backing.spare_bytes == chunk
+        assert backing.ensure([6]) == 1 and backing.spare_bytes == 0
+        assert torch.count_nonzero(raw[6 * chunk:7 * chunk]).item() == 0
+        backing.set_spare_chunks(0)
+        assert backing.reclaim([6]) == 1 and backing.spare_bytes == 0
+        with pytest.raises(ValueError, match="spare_chunks"):
+            backing.set_spare_chunks(9)
+        backing.set_spare_chunks(4)
+        assert backing.reclaim([0, 1]) == 2 and backing.spare_bytes == 2 * chunk
+        del raw
+    finally:
+        torch.cuda.synchronize()
+        backing.close()
+
+
 def test_release_and_recommit_one_hole(gpu):
     chunk = DEFAULT_CHUNK_BYTES
     backing = Backing(5 * chunk - 17, chunk_bytes=chunk, device=0)

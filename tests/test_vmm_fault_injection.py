@@ -147,3 +147,23 @@ def test_unreferenced_backing_releases_its_reservation(fake_library):
     del backing
     gc.collect()
     assert _clean(lib)
+
+
+def test_spare_pool_through_the_python_backing(fake_library):
+    path, lib = fake_library
+    lib.fake_reset()
+    backing = Backing(4 * CHUNK, CHUNK, 0, library=path, spare_chunks=2)
+    lib.fake_calls.restype = ct.c_long
+    assert backing.ensure([0, 1, 2]) == 3 and lib.fake_calls(OPS["create"]) == 3
+    assert backing.reclaim([0, 1, 2], synchronize=False) == 3
+    assert backing.spare_bytes == 2 * CHUNK and backing.backed_bytes == 0
+    assert lib.fake_calls(OPS["release"]) == 1 and lib.fake_live_handles() == 2
+    assert backing.ensure([3, 2]) == 2 and lib.fake_calls(OPS["create"]) == 3     # both recycled
+    assert backing.spare_bytes == 0 and backing.mapped_chunks == {2, 3}
+    with pytest.raises(ValueError, match="spare_chunks"):
+        backing.set_spare_chunks(5)
+    backing.reclaim([2], synchronize=False)
+    backing.set_spare_chunks(0)                  # gives the kept chunk back
+    assert backing.spare_bytes == 0 and lib.fake_live_handles() == 1
+    backing.close()
+    assert _clean(lib)
