@@ -497,7 +497,11 @@ def run_decode_read(torch, args, device):
         rates = cpu_rates(torch, sample, sample_bytes, args.cpu_seconds)
         baseline = cpu_baseline_entry(
             rates, f"layer 0 of the same step ({R} x {K} lookups, miss list, {2 * R * K} gathered {row_bytes} B "
-                   f"rows: {sample_bytes / 1e6:.1f} MB algorithmic)", parity)
+                   f"rows: {sample_bytes / 1e6:.1f} MB algorithmic); x{L} layers extrapolated: "
+                   f"{rates['all']['ms'] * L / 1e3:.2f} s per step at {rates['all']['threads']} threads, "
+                   f"{rates['one']['ms'] * L / 1e3:.2f} s at 1", parity)
+        baseline["step_ms_extrapolated"] = {"all_threads": round(rates["all"]["ms"] * L, 1),
+                                            "one_thread": round(rates["one"]["ms"] * L, 1), "layers": L}
         log(f"cpu baseline {rates}, parity {parity}")
 
     config = {"workload": "hisparse-topk-decode-read", "requests": R, "context": T, "layers": L, "kv_heads": 2,
