@@ -513,7 +513,7 @@ def run_decode_read(torch, args, device):
              "lookup_us_per_layer": round(phase["lookup"] * 1e3 / L, 2),
              "lookup_gbs": round(lookup_bytes / (phase["lookup"] / 1e3) / 1e9, 1),
              "lookup_roofline": roofline(lookup_bytes / (phase["lookup"] / 1e3) / 1e9,
-                                         "resolve_runs_pipe_kernel<compact, int16, 1> (ekv_resolve_resident_local: "
+                                         "resolve_runs_pipe2_kernel<compact, int16> (ekv_resolve_resident_local: "
                                          "int16 table, line summary), in the step", lookup_bytes, phase["lookup"],
                                          lookup_traffic),
              "lookup_arms_back_to_back": arms,

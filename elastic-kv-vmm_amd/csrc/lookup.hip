@@ -23,10 +23,14 @@
 //     misses without touching their table entry;
 //   resolve_mapped_kernel - two levels (table -> logical id -> mapping -> slot),
 //     the reference's form.
-// The decode default (int16 local-slot table + bitmap, block size 1, aligned
-// rows) takes a third kernel, resolve_runs_kernel, which keeps the lane order
-// but gives each thread two contiguous 4-lane pieces (16-byte Top-K loads and
-// slot stores) and assembles each chunk's miss list in LDS.
+// The decode form (single-level int16 local-slot or int32 table behind a
+// residency summary, block size 1, aligned rows) takes kernels that keep the
+// lane order but give each thread two contiguous 4-lane pieces (16-byte Top-K
+// loads and slot stores) and assemble each chunk's miss list in LDS:
+// resolve_runs_kernel, and for rows of one chunk the persistent prefetching
+// forms resolve_runs_pipe_kernel and resolve_runs_pipe2_kernel (two stages:
+// the next item's table reads are in flight during the current item's
+// compaction; the default for summary rows of at most 1024 words).
 // Recent window: decode Top-K sets concentrate on the most recent tokens, and
 // lanes that gather single table entries cost one L2 request each. Both
 // kernels therefore stage the table entries of the last kWindow positions
@@ -968,6 +972,216 @@ __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupAr
     }
 }
 
+// Two-stage form of the prefetching kernel (summary rows of at most 1024
+// words): item k + 1's summary row is staged and its table reads are issued
+// before item k's misses are compacted, so those reads (and item k + 2's
+// Top-K ids and summary row, issued behind them) are in flight through item
+// k's compaction barriers, which the one-stage kernel runs with only the next
+// item's Top-K in flight. The summary row is staged in two LDS buffers used
+// alternately: item k + 1 writes the buffer item k - 1 read, and item k - 1's
+// compaction barriers separate the two.
+#ifndef EKV_LOOKUP_PIPE2
+#define EKV_LOOKUP_PIPE2 1
+#endif
+
+// One item between its two stages: its table entries in flight and its lanes'
+// classification.
+struct RunsPending {
+    int32_t entry[kIters];
+    uint32_t need;      // bit j: lane j is resident, its entry decides its slot
+    uint32_t invalid;   // bit j: lane j is padding or out of range (slot -1)
+};
+
+// First stage of an item: stage its summary row in `staged` (after a barrier
+// every thread passes), classify its lanes and issue its table reads.
+template <typename TableT>
+__device__ __forceinline__ void runs_begin(const LookupArgs& a, uint32_t layer, const RunsMeta& m,
+                                           const RunsLoads<1>& loads, uint32_t* staged, uint32_t last_piece,
+                                           const bool (&live_piece)[2], RunsPending& p) {
+    const bool table_ok = m.row != kNoRow && m.req != kNoRow;   // uniform
+    if (table_ok) {
+        *reinterpret_cast<i32x4*>(&staged[4 * (threadIdx.x < last_piece ? threadIdx.x : last_piece)]) =
+            loads.bits[0];
+    }
+    __syncthreads();
+    const int32_t block[kIters] = {loads.ids[0].x, loads.ids[0].y, loads.ids[0].z, loads.ids[0].w,
+                                   loads.ids[1].x, loads.ids[1].y, loads.ids[1].z, loads.ids[1].w};
+    uint32_t at[kIters];
+    p.need = 0;
+    p.invalid = 0;
+#pragma unroll
+    for (int j = 0; j < kIters; ++j) {
+        const bool valid = live_piece[j / 4] & table_ok & (block[j] >= 0) & (block[j] < m.bound);
+        const uint32_t pos = valid ? static_cast<uint32_t>(block[j]) : 0u;
+        const uint32_t q = pos >> a.bits_shift;
+        const uint32_t word = staged[q >> 5];
+        const bool resident = (static_cast<uint32_t>(valid) & (word >> (q & 31))) != 0u;
+        at[j] = resident ? pos : 0u;
+        p.need |= static_cast<uint32_t>(resident) << j;
+        p.invalid |= static_cast<uint32_t>(!valid) << j;
+    }
+    const TableT* table =
+        static_cast<const TableT*>(a.table) + layer * a.table_sl + (table_ok ? m.req : 0u) * a.table_sr;
+#pragma unroll
+    for (int j = 0; j < kIters; ++j) {
+        p.entry[j] = *element<true>(table, 1, at[j]);
+    }
+}
+
+template <bool kCompact, typename TableT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void resolve_runs_pipe2_kernel(const LookupArgs a, uint32_t items, uint32_t count, FastDiv count_div) {
+    constexpr uint32_t kPiece = 4;
+    constexpr uint32_t kHalf = kThreads * kPiece;  // 1024 lanes
+    constexpr int kWaves = kThreads / 64;
+    __shared__ __align__(16) uint32_t staged_bits[2][4 * kThreads];
+    __shared__ uint4 meta[kPipeMaxItems];
+    __shared__ int32_t wave_totals[2 * kWaves];   // [half][wave]
+    __shared__ int32_t chunk_misses[kChunkLanes];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const uint32_t first[2] = {threadIdx.x * kPiece, kHalf + threadIdx.x * kPiece};
+    const bool live_piece[2] = {first[0] < a.width, first[1] < a.width};  // pieces are whole: width % 8 == 0
+    const uint32_t last_piece = static_cast<uint32_t>((a.bits_words + 3) >> 2) - 1;
+    const uint32_t n = (items - blockIdx.x + gridDim.x - 1) / gridDim.x;  // this workgroup's items, <= kPipeMaxItems
+
+    if (threadIdx.x < n) {
+        const uint32_t item = blockIdx.x + threadIdx.x * gridDim.x;
+        const uint32_t item_layer = count_div.div(item);
+        const int64_t row = a.selected.fetch(item - item_layer * count);
+        const bool live = row >= 0 && row < a.batch;
+        uint4 m{kNoRow, kNoRow, 0u, 0u};
+        if (live) {
+            const int64_t req = a.rows.fetch(row);
+            const int64_t length = a.lengths.fetch(row);
+            const bool table_ok = req >= 0 && req < a.table_rows && a.table_cols > 0;
+            const int64_t bound = length < a.table_cols ? length : a.table_cols;
+            m.x = static_cast<uint32_t>(row);
+            m.y = table_ok ? static_cast<uint32_t>(req) : kNoRow;
+            if constexpr (std::is_same_v<TableT, int16_t>) {
+                m.z = table_ok ? static_cast<uint32_t>(a.slot_base.fetch(req)) : 0u;
+            }
+            m.w = static_cast<uint32_t>(bound > 0 ? static_cast<int32_t>(bound) : 0);
+        }
+        meta[threadIdx.x] = m;
+    }
+    __syncthreads();
+
+    // Stage one of item 0, then the loads of item 1 (one line of each row when
+    // there is none).
+    RunsMeta cur = runs_meta(meta, 0);
+    uint32_t layer = count_div.div(blockIdx.x);
+    RunsPending pend;
+    runs_begin<TableT>(a, layer, cur, runs_issue<1>(a, layer, cur, false), staged_bits[0], last_piece, live_piece,
+                       pend);
+    uint32_t k_next = n > 1 ? 1u : 0u;
+    RunsMeta nxt = runs_meta(meta, k_next);
+    uint32_t layer_next = count_div.div(blockIdx.x + k_next * gridDim.x);
+    RunsLoads<1> next_loads = runs_issue<1>(a, layer_next, nxt, n <= 1);
+    for (uint32_t k = 0;; ++k) {
+        // Item k's slots from its table entries.
+        int32_t slot[kIters];
+#pragma unroll
+        for (int j = 0; j < kIters; ++j) {
+            const int32_t e = pend.entry[j];
+            int32_t value = e;   // int32 tables hold the slot itself
+            if constexpr (std::is_same_v<TableT, int16_t>) {
+                value = e > 0 ? static_cast<int32_t>(cur.base + static_cast<uint32_t>(e) - 1u) : 0;
+            }
+            slot[j] = (pend.need >> j) & 1u ? value : ((pend.invalid >> j) & 1u ? -1 : 0);
+        }
+        const bool live = cur.row != kNoRow;   // uniform
+        if (live) {
+            int32_t* out = a.out + layer * a.out_sl + cur.row * a.out_sb;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if (live_piece[h]) {
+                    stream_store(i32x4{slot[4 * h], slot[4 * h + 1], slot[4 * h + 2], slot[4 * h + 3]},
+                                 reinterpret_cast<i32x4*>(element<true>(out, 1, first[h])));
+                }
+            }
+        }
+        uint32_t miss = 0;  // bit j: lane j is a miss
+        if constexpr (kCompact) {
+#pragma unroll
+            for (int j = 0; j < kIters; ++j) {
+                miss |= static_cast<uint32_t>(live && live_piece[j / kPiece] && slot[j] == 0) << j;
+            }
+        }
+        // Stage one of item k + 1 and the loads of item k + 2, ahead of item k's compaction.
+        const bool more = k + 1 < n;   // uniform
+        RunsMeta after = nxt;
+        uint32_t layer_after = layer_next;
+        RunsLoads<1> after_loads = next_loads;
+        if (more) {
+            runs_begin<TableT>(a, layer_next, nxt, next_loads, staged_bits[(k + 1) & 1], last_piece, live_piece,
+                               pend);
+            const uint32_t k_after = k + 2 < n ? k + 2 : k + 1;
+            after = runs_meta(meta, k_after);
+            layer_after = count_div.div(blockIdx.x + k_after * gridDim.x);
+            after_loads = runs_issue<1>(a, layer_after, after, k + 2 >= n);
+        }
+        if constexpr (kCompact) {
+            uint32_t below[2] = {0, 0};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t c = __popc((miss >> (kPiece * h)) & 0xfu);
+                uint32_t wave_total = 0;
+#pragma unroll
+                for (int b = 0; b < 3; ++b) {
+                    const uint64_t plane = __ballot((c >> b) & 1u);
+                    below[h] += lanes_below(plane) << b;
+                    wave_total += static_cast<uint32_t>(__popcll(plane)) << b;
+                }
+                if (lane == 0) {
+                    wave_totals[h * kWaves + wave] = static_cast<int32_t>(wave_total);
+                }
+            }
+            __syncthreads();
+            int32_t rank[2] = {static_cast<int32_t>(below[0]), static_cast<int32_t>(below[1])};
+            int32_t half_total[2] = {0, 0};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) {
+                    rank[h] += w < wave ? wave_totals[h * kWaves + w] : 0;
+                    half_total[h] += wave_totals[h * kWaves + w];
+                }
+            }
+            rank[1] += half_total[0];
+            const int32_t total = half_total[0] + half_total[1];
+#pragma unroll
+            for (int j = 0; j < kIters; ++j) {
+                if ((miss >> j) & 1u) {
+                    chunk_misses[rank[j / kPiece]++] = static_cast<int32_t>(first[j / kPiece] + j % kPiece);
+                }
+            }
+            __syncthreads();
+            if (live) {
+                int32_t* misses = a.misses + layer * a.miss_sl + cur.row * a.miss_sb;
+                for (int32_t i = threadIdx.x; i < total; i += kThreads) {
+                    *element<true>(misses, 1, static_cast<uint32_t>(i)) = chunk_misses[i];
+                }
+                if (threadIdx.x == 0) {
+                    a.counts[layer * a.count_sl + cur.row * a.count_sb] = total;
+                }
+            }
+            // The two barriers above also separate item k's reads of its
+            // staged summary from item k + 2's writes to the same buffer.
+        } else {
+            __syncthreads();   // ... which this barrier does without compaction
+        }
+        if (!more) {
+            break;
+        }
+        cur = nxt;
+        layer = layer_next;
+        nxt = after;
+        layer_next = layer_after;
+        next_loads = after_loads;
+    }
+}
+
 // Workgroups of the prefetching kernel resident on the whole device at once,
 // per device (0 = not yet queried).
 template <bool kCompact, typename TableT, int kBitLoads>
@@ -993,6 +1207,39 @@ uint32_t runs_pipe_resident() {
     return known;
 }
 
+// Workgroups of the two-stage kernel resident on the whole device at once.
+template <bool kCompact, typename TableT>
+uint32_t runs_pipe2_resident() {
+    static std::atomic<uint32_t> resident[64];
+    int device = 0;
+    check_hip(hipGetDevice(&device), "hipGetDevice");
+    if (device < 0 || device >= 64) {
+        throw std::runtime_error("device ordinal out of range");
+    }
+    uint32_t known = resident[device].load(std::memory_order_relaxed);
+    if (known == 0) {
+        int per_cu = 0, cus = 0;
+        check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                      &per_cu, reinterpret_cast<const void*>(resolve_runs_pipe2_kernel<kCompact, TableT>), kThreads, 0),
+                  "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+        check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
+                  "hipDeviceGetAttribute");
+        known = static_cast<uint32_t>(std::max(1, per_cu) * std::max(1, cus));
+        resident[device].store(known, std::memory_order_relaxed);
+    }
+    return known;
+}
+
+template <bool kCompact, typename TableT>
+void launch_runs_pipe2(const LookupArgs& a, dim3 grid, hipStream_t stream) {
+    const uint32_t count = grid.x;
+    const uint32_t items = grid.x * grid.y;   // below 2^31 (checked by the host)
+    const uint32_t groups = std::min(items, std::max(runs_pipe2_resident<kCompact, TableT>(),
+                                                     (items + kPipeMaxItems - 1) / kPipeMaxItems));
+    resolve_runs_pipe2_kernel<kCompact, TableT><<<dim3(groups), dim3(kThreads), 0, stream>>>(a, items, count,
+                                                                                            FastDiv(count));
+}
+
 template <bool kCompact, typename TableT, int kBitLoads>
 void launch_runs_pipe_loads(const LookupArgs& a, dim3 grid, hipStream_t stream) {
     const uint32_t count = grid.x;
@@ -1012,6 +1259,10 @@ void launch_runs_pipe_loads(const LookupArgs& a, dim3 grid, hipStream_t stream) 
 template <bool kCompact, typename TableT>
 void launch_runs_pipe(const LookupArgs& a, dim3 grid, hipStream_t stream) {
     if ((a.bits_words + 3) / 4 <= kThreads) {
+        if (EKV_LOOKUP_PIPE2 && EKV_LOOKUP_PIPE_GRID) {
+            launch_runs_pipe2<kCompact, TableT>(a, grid, stream);
+            return;
+        }
         launch_runs_pipe_loads<kCompact, TableT, 1>(a, grid, stream);
     } else {
         launch_runs_pipe_loads<kCompact, TableT, 2>(a, grid, stream);
