@@ -26,20 +26,13 @@ def _unchanged(function):
 
 
 def _marker():
-    """torch.cuda.nvtx when this torch build has a marker library, else None."""
+    """torch.cuda.nvtx (roctx on ROCm) when this torch build has it, else None."""
     try:
         import torch
     except ImportError:
         return None
     nvtx = getattr(torch.cuda, "nvtx", None)
-    if nvtx is None:
-        return None
-    try:
-        nvtx.range_push("ekv/probe")
-        nvtx.range_pop()
-    except (RuntimeError, AttributeError):
-        return None
-    return nvtx
+    return nvtx if nvtx is not None and hasattr(nvtx, "range_push") else None
 
 
 def profile_range(name):
@@ -50,19 +43,28 @@ def profile_range(name):
     from torch.profiler import record_function
 
     label = f"ekv/{name}"
-    marker = _marker()
+    marker = [_marker()]   # dropped after a marker call fails (a torch build without a marker library)
+
+    def push():
+        if marker[0] is None:
+            return False
+        try:
+            marker[0].range_push(label)
+            return True
+        except RuntimeError:
+            marker[0] = None
+            return False
 
     def decorate(function):
         @wraps(function)
         def measured(*args, **kwargs):
             with record_function(label):
-                if marker is None:
+                if not push():
                     return function(*args, **kwargs)
-                marker.range_push(label)
                 try:
                     return function(*args, **kwargs)
                 finally:
-                    marker.range_pop()
+                    marker[0].range_pop()
 
         return measured
 
