@@ -41,6 +41,11 @@ Other workloads (same JSON contract):
                 of one layer: 128 requests x 65,536-token context, 4096 hot
                 slots each, 16 Top-K blocks of 128 tokens (newest block, 12
                 recent, 3 older), 512 B K and V rows promoted from pinned host
+  lookup-micro  the reference's resident-lookup microbenchmark
+                (tests/bench_resident_lookup.py): batch 1/2/4, 8192-token rows,
+                16 Top-K blocks of 128 tokens, two-level int64 lookup, per-call
+                p50/p95 with the host launch included (time-like: lower is
+                better; vs_baseline against the reference's A100 Triton p50)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -76,7 +81,7 @@ def parse_args():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--workload", default="decode-read",
                         choices=["decode-read", "topk-gather", "block-gather", "migration", "composite",
-                                 "hisparse-swap"])
+                                 "hisparse-swap", "lookup-micro"])
     parser.add_argument("--remap-fraction", type=float, default=0.05,
                         help="share of pool chunks unmapped and remapped per composite step")
     parser.add_argument("--capacity", type=int, default=4096, help="hot slots per request (decode-read)")
@@ -926,6 +931,113 @@ def run_hisparse_swap(torch, args, device):
     return result
 
 
+# ------------------------------------------------------------------ lookup-micro (the reference's microbenchmark)
+
+# The reference's published figures for this microbenchmark (results/lookup-micro/results.json, A100-SXM4-80GB):
+# p50 microseconds per call of its Triton resolver and of its torch indexing sequence, batch 1 / 2 / 4.
+REFERENCE_LOOKUP_MICRO_US = {"triton_p50": {1: 30.54, 2: 30.00, 4: 30.08}, "torch_p50": {1: 213.80, 2: 211.06, 4: 211.88}}
+
+
+def run_lookup_micro(torch, args, device):
+    """tests/bench_resident_lookup.py of the reference, on this build's resolve_resident.
+
+    Per batch of 1, 2 and 4 requests: a two-level lookup (int64 table -> int64
+    mapping) of 16 Top-K blocks of 128 tokens (2048 lanes per row) over
+    8192-token rows, the closed form ((B-1-row)*8192 + block*512 + off + 1)*3 + 5
+    checked first; then 100 warm-up calls of each path and 40 rounds of 100
+    calls, the two paths alternating, HIP events per round (time per call,
+    host launch included, as the reference measures). The torch path is the
+    reference's indexing sequence on the GPU. Also the same 100 calls replayed
+    from one HIP graph (no host launch).
+    """
+    from adaptive_sparse.resident_lookup import resolve_resident
+
+    per_batch = {}
+    for batch in (1, 2, 4):
+        selected = torch.arange(batch, device=device)
+        rows = selected.flip(0)
+        lengths = torch.full((batch,), 8192, dtype=torch.int32, device=device)
+        table = torch.arange(batch * 8192, device=device).reshape(batch, 8192) + 1
+        mapping = torch.arange(batch * 8192 + 1, device=device) * 3 + 5
+        topk = (torch.arange(16, device=device) * 4).int().expand(1, batch, 16).contiguous()
+        lane = torch.arange(128, device=device)
+
+        def torch_lookup():
+            result = torch.empty((batch, 2048), device=device, dtype=torch.int32)
+            blocks = topk[0, selected].long()
+            positions = (blocks.unsqueeze(-1) * 128 + lane).flatten(1)
+            valid = (positions >= 0) & (positions < lengths[selected, None])
+            logical = table[rows[selected, None], positions.masked_fill(~valid, 0)]
+            result[selected] = mapping[logical].masked_fill(~valid, -1).int()
+            return result.unsqueeze(0)
+
+        def hip_lookup(out=None):
+            result = torch.empty((1, batch, 2048), device=device, dtype=torch.int32) if out is None else out
+            resolve_resident(topk, table, mapping, rows, lengths, selected, result, 128)
+            return result
+
+        expected = torch.tensor([[((batch - 1 - row) * 8192 + block * 512 + offset + 1) * 3 + 5
+                                  for block in range(16) for offset in range(128)] for row in range(batch)],
+                                dtype=torch.int32, device=device).unsqueeze(0)
+        correct = bool(torch.equal(torch_lookup(), expected) and torch.equal(hip_lookup(), expected))
+        timings = {"hip": [], "torch": []}
+        methods = [("hip", hip_lookup), ("torch", torch_lookup)]
+        for _, call in methods:
+            for _ in range(100):
+                call()
+        torch.cuda.synchronize()
+        for round_number in range(40):
+            for name, call in methods[::(-1 if round_number % 2 else 1)]:
+                begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                begin.record()
+                for _ in range(100):
+                    call()
+                end.record()
+                end.synchronize()
+                timings[name].append(begin.elapsed_time(end) * 10)     # us per call
+        # The same 100 calls replayed from one HIP graph.
+        out = torch.empty((1, batch, 2048), device=device, dtype=torch.int32)
+        hip_lookup(out)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(100):
+                hip_lookup(out)
+        graph.replay()
+        torch.cuda.synchronize()
+        correct &= bool(torch.equal(out, expected))
+        replays = []
+        for _ in range(20):
+            begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            begin.record()
+            graph.replay()
+            end.record()
+            end.synchronize()
+            replays.append(begin.elapsed_time(end) * 10)
+        del graph
+        stats = {name: {"p50_us": round(statistics.median(v), 2),
+                        "p95_us": round(statistics.quantiles(v, n=20, method="inclusive")[18], 2)}
+                 for name, v in timings.items()}
+        per_batch[batch] = {"correct": correct, **stats, "graph_us_per_call": round(statistics.median(replays), 2),
+                            "reference_a100_triton_p50_us": REFERENCE_LOOKUP_MICRO_US["triton_p50"][batch],
+                            "reference_a100_torch_p50_us": REFERENCE_LOOKUP_MICRO_US["torch_p50"][batch]}
+        log(f"lookup micro batch {batch}: {per_batch[batch]}")
+    value = per_batch[1]["hip"]["p50_us"]
+    config = {"workload": "resident-lookup-micro", "context": 8192, "topk_blocks": 16, "block_size": 128,
+              "lanes_per_row": 2048, "batches": [1, 2, 4], "lookup": "two-level (int64 table -> int64 mapping)",
+              "rounds": 40, "calls_per_round": 100, "warmup_calls": 100}
+    result = envelope(args, value, value / 1e3, config, None, None,
+                      {"per_batch": {str(b): v for b, v in per_batch.items()},
+                       "correct": all(v["correct"] for v in per_batch.values())},
+                      unit="us", metric="resident lookup us per call (p50, batch 1, host launch included)")
+    result["higher_is_better"] = False
+    result["vs_baseline"] = round(value / REFERENCE_LOOKUP_MICRO_US["triton_p50"][1], 4)
+    result["dtype"] = "int64"
+    result["data"] = "the reference microbenchmark's closed-form inputs"
+    result["steps"], result["warmup"] = 40 * 100, 100   # per path and batch: 40 rounds of 100 calls
+    return result
+
+
 # ------------------------------------------------------------------ composite (config 5)
 
 
@@ -1145,7 +1257,7 @@ def run_composite(torch, args, device):
     return result
 
 
-WORKLOADS = {"decode-read": run_decode_read, "topk-gather": run_topk_gather,
+WORKLOADS = {"decode-read": run_decode_read, "topk-gather": run_topk_gather, "lookup-micro": run_lookup_micro,
              "block-gather": run_block_gather, "migration": run_migration, "composite": run_composite,
              "hisparse-swap": run_hisparse_swap}
 
@@ -1155,7 +1267,8 @@ MIGRATION_SPARE_CHUNKS = 700   # > the ~500 chunks a 512-block tick frees and ma
 EXTRA_CONFIGS = (("config1_topk_gather", "topk-gather", {}), ("config2_block_gather", "block-gather", {}),
                  ("config4_migration", "migration", {}),
                  ("config4_migration_spare_pool", "migration",
-                  {"spare_chunks": MIGRATION_SPARE_CHUNKS, "no_cpu_baseline": True}))
+                  {"spare_chunks": MIGRATION_SPARE_CHUNKS, "no_cpu_baseline": True}),
+                 ("lookup_micro", "lookup-micro", {}))
 
 
 def apply_profile_switch(environment, keep):
@@ -1169,7 +1282,8 @@ def apply_profile_switch(environment, keep):
 def summary(result):
     """The fields of another workload's line that the default line carries for it."""
     keys = ("metric", "value", "unit", "ms_per_step", "roofline", "cpu_baseline", "config", "lookup_us_per_step",
-            "hit_rate", "verified_round_trip", "tick_ms", "link_gbs", "pack_gbs", "unpack_gbs", "phase_ms")
+            "hit_rate", "verified_round_trip", "tick_ms", "link_gbs", "pack_gbs", "unpack_gbs", "phase_ms",
+            "higher_is_better", "vs_baseline", "per_batch", "correct")
     return {key: result[key] for key in keys if key in result}
 
 

@@ -101,7 +101,7 @@ def decode_step(topk, rows, lengths, buffers, host_table, host_planes, pool_plan
     args, keep = step_args(topk, rows, lengths, selected, buffers, host_table, host_planes, pool_planes, slots,
                            output, block_size, -1 if counted else step)
     lib = _native.kernel_library()
-    with torch.cuda.device(device):
+    with _native.on_device(device):
         status = lib.ekv_decode_step(ct.addressof(args), ct.c_void_p(workspace.data_ptr()), workspace.numel(),
                                      _native.stream_handle(device))
     _native.check(lib, status, "decode_step")

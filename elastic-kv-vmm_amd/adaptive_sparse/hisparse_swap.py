@@ -95,7 +95,7 @@ def load_blocks_to_device_buffer_mha(top_k_blocks, device_buffer_tokens, host_ca
                req_pool_indices, seq_lens, lru_slots)
     views = [_native.describe(t, n) for t, n in zip(tensors, names)]
     real = None if num_real_reqs is None else _native.describe(num_real_reqs, "num_real_reqs")
-    with torch.cuda.device(device):
+    with _native.on_device(device):
         status = lib.ekv_hisparse_swap_in(
             *(ct.byref(v) for v in views[:4]), ct.byref(host), ct.byref(dev), *(ct.byref(v) for v in views[4:]),
             int(hot_buffer_size), int(sparse_block_size), None if real is None else ct.byref(real),

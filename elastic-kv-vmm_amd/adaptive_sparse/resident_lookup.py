@@ -66,37 +66,27 @@ def resolve_resident(topk, table, mapping, rows, lengths, selected, output, bloc
         tensors += [misses, miss_count]
     device = _native.device_of(*tensors)
     lib = _native.kernel_library()
-    views = [_native.describe(t, name) for t, name in (
-        (topk, "topk"), (table, "table"), (rows, "rows"), (lengths, "lengths"),
-        (selected, "selected"), (output, "output"))]
-    if resident_bits is not None:
-        entry, mapping_view = lib.ekv_resolve_resident_bits, ct.byref(_native.describe(resident_bits, "bits"))
-    else:
-        entry = lib.ekv_resolve_resident
-        mapping_view = ct.byref(_native.describe(mapping, "mapping")) if mapping is not None else None
-    miss_view = ct.byref(_native.describe(misses, "misses")) if misses is not None else None
-    count_view = ct.byref(_native.describe(miss_count, "miss_count")) if miss_count is not None else None
-    if slot_base is not None:
-        bits_view = ct.byref(_native.describe(resident_bits, "bits")) if resident_bits is not None else None
-        base_view = _native.describe(slot_base, "slot_base")
-        with torch.cuda.device(device):
+    pack = _native.packed   # descriptors as bytes: this call is bound by its host launch cost
+    views = [pack(t, name) for t, name in (
+        (topk, "topk"), (table, "table"), (rows, "rows"), (lengths, "lengths"), (selected, "selected"),
+        (output, "output"))]
+    miss_view = pack(misses, "misses") if misses is not None else None
+    count_view = pack(miss_count, "miss_count") if miss_count is not None else None
+    bits_view = pack(resident_bits, "bits") if resident_bits is not None else None
+    with _native.on_device(device):
+        stream = _native.stream_handle(device)
+        if slot_base is not None:
             status = lib.ekv_resolve_resident_local(
-                ct.byref(views[0]), ct.byref(views[1]), ct.byref(base_view), bits_view, int(bits_shift),
-                ct.byref(views[2]), ct.byref(views[3]), ct.byref(views[4]), ct.byref(views[5]), miss_view,
-                count_view, int(block_size), _native.stream_handle(device))
-        _native.check(lib, status, "resolve_resident")
-        return
-    with torch.cuda.device(device):
-        if resident_bits is not None:
-            status = entry(
-                ct.byref(views[0]), ct.byref(views[1]), mapping_view, int(bits_shift), ct.byref(views[2]),
-                ct.byref(views[3]), ct.byref(views[4]), ct.byref(views[5]), miss_view, count_view,
-                int(block_size), _native.stream_handle(device))
+                views[0], views[1], pack(slot_base, "slot_base"), bits_view, int(bits_shift), *views[2:],
+                miss_view, count_view, int(block_size), stream)
+        elif resident_bits is not None:
+            status = lib.ekv_resolve_resident_bits(
+                views[0], views[1], bits_view, int(bits_shift), *views[2:], miss_view, count_view,
+                int(block_size), stream)
         else:
-            status = entry(
-                ct.byref(views[0]), ct.byref(views[1]), mapping_view, ct.byref(views[2]),
-                ct.byref(views[3]), ct.byref(views[4]), ct.byref(views[5]), miss_view, count_view,
-                int(block_size), _native.stream_handle(device))
+            mapping_view = pack(mapping, "mapping") if mapping is not None else None
+            status = lib.ekv_resolve_resident(
+                views[0], views[1], mapping_view, *views[2:], miss_view, count_view, int(block_size), stream)
     _native.check(lib, status, "resolve_resident")
 
 
@@ -125,7 +115,7 @@ def build_residency_bits(table, out=None, shift=0):
     device = _native.device_of(table, out)
     lib = _native.kernel_library()
     table_view, out_view = _native.describe(table, "table"), _native.describe(out, "resident_bits")
-    with torch.cuda.device(device):
+    with _native.on_device(device):
         status = lib.ekv_residency_bits(ct.byref(table_view), ct.byref(out_view), int(shift),
                                         _native.stream_handle(device))
     _native.check(lib, status, "build_residency_bits")

@@ -61,7 +61,7 @@ def _kv_call(entry, planes, slots, dense, zero_below, name):
     plane_view = _planes_struct(planes)
     slot_view = _native.describe(slots, "slots")
     dense_view = _dense_struct(dense, planes, slots, name)
-    with torch.cuda.device(device):
+    with _native.on_device(device):
         status = getattr(lib, entry)(ct.byref(plane_view), ct.byref(slot_view), ct.byref(dense_view),
                                      int(zero_below), _native.stream_handle(device))
     _native.check(lib, status, entry)

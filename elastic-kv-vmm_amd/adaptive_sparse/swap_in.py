@@ -181,7 +181,7 @@ def swap_in(topk, block_size, rows, selected, slots, misses, miss_count, buffers
     # topk | rows .. table | bits, shift | slot_token .. promote_dst
     head, middle, tail = views[0], views[1:7], views[7:13]
     shift = int(buffers.bits_shift)
-    with torch.cuda.device(device):
+    with _native.on_device(device):
         if counted:
             counter = ct.byref(_native.describe(buffers.step_counter, "step_counter"))
             status = lib.ekv_swap_in_counted(head, int(block_size), *middle, bits_view, shift, *tail, counter,
@@ -205,7 +205,7 @@ def move_kv(src_planes, src_rows, dst_planes, dst_rows, counts, *, zero_below=1)
     lib = _native.kernel_library()
     src_view, dst_view = _planes_struct(src_planes), _planes_struct(dst_planes)
     views = [_native.describe(t, n) for t, n in ((src_rows, "src_rows"), (dst_rows, "dst_rows"), (counts, "counts"))]
-    with torch.cuda.device(device):
+    with _native.on_device(device):
         status = lib.ekv_move_kv(ct.byref(src_view), ct.byref(views[0]), ct.byref(dst_view), ct.byref(views[1]),
                                  ct.byref(views[2]), int(zero_below), _native.stream_handle(device))
     _native.check(lib, status, "move_kv")

@@ -6,6 +6,8 @@ fallback: if the library cannot be loaded, every kernel call raises.
 """
 
 import ctypes as ct
+import os
+import struct
 
 import torch
 
@@ -60,14 +62,17 @@ class EkvKvRows(ct.Structure):
 
 
 _P_TENSOR = ct.POINTER(EkvTensor)
+# The lookup entries take their descriptors as plain pointers, so the wrapper can
+# hand over the bytes of packed() (a ctypes.byref(EkvTensor) is accepted as well).
+_TENSOR_ADDRESS = ct.c_void_p
 _SIGNATURES = {
     "ekv_abi_version": ([], ct.c_int),
     "ekv_source_hash": ([], ct.c_char_p),
-    "ekv_resolve_resident": ([_P_TENSOR] * 9 + [ct.c_int64, ct.c_void_p], ct.c_int),
-    "ekv_resolve_resident_bits": ([_P_TENSOR] * 3 + [ct.c_int64] + [_P_TENSOR] * 6 + [ct.c_int64, ct.c_void_p],
-                                  ct.c_int),
-    "ekv_resolve_resident_local": ([_P_TENSOR] * 4 + [ct.c_int64] + [_P_TENSOR] * 6 + [ct.c_int64, ct.c_void_p],
-                                   ct.c_int),
+    "ekv_resolve_resident": ([_TENSOR_ADDRESS] * 9 + [ct.c_int64, ct.c_void_p], ct.c_int),
+    "ekv_resolve_resident_bits": ([_TENSOR_ADDRESS] * 3 + [ct.c_int64] + [_TENSOR_ADDRESS] * 6
+                                  + [ct.c_int64, ct.c_void_p], ct.c_int),
+    "ekv_resolve_resident_local": ([_TENSOR_ADDRESS] * 4 + [ct.c_int64] + [_TENSOR_ADDRESS] * 6
+                                   + [ct.c_int64, ct.c_void_p], ct.c_int),
     "ekv_residency_bits": ([_P_TENSOR, _P_TENSOR, ct.c_int64, ct.c_void_p], ct.c_int),
     "ekv_gather_rows": ([_P_TENSOR] * 7 + [ct.c_int64, ct.c_int64, ct.c_int, ct.c_void_p], ct.c_int),
     "ekv_gather_kv": ([ct.POINTER(EkvPlanes), _P_TENSOR, ct.POINTER(EkvKvRows), ct.c_int64, ct.c_void_p],
@@ -95,8 +100,19 @@ _SIGNATURES = {
 KERNEL_SYMBOLS = tuple(_SIGNATURES)
 
 
+_TYPED = {}   # argument (or ELASTIC_VMM_LIBRARY, or None for the in-tree build) -> typed library
+
+
 def kernel_library(library=None):
-    """The native library with ekv_* signatures declared (cached per path)."""
+    """The native library with ekv_* signatures declared (cached per path argument).
+
+    The cache is keyed on the path as given, so a call costs one dictionary
+    lookup: resolving the path (file-system calls) happens on first use only.
+    """
+    key = library if library is not None else os.environ.get("ELASTIC_VMM_LIBRARY")
+    lib = _TYPED.get(key)
+    if lib is not None:
+        return lib
     lib = _load_library(library_path(library))
     if not getattr(lib, "_ekv_typed", False):
         for name, (argtypes, restype) in _SIGNATURES.items():
@@ -119,24 +135,43 @@ def kernel_library(library=None):
                 "with `python elastic-kv-vmm_amd/build_native.py`"
             )
         lib._ekv_typed = True
+    _TYPED[key] = lib
     return lib
 
 
 def describe(tensor, name="tensor"):
     """EkvTensor for a torch tensor (any strides, at most 4 dimensions)."""
-    if tensor.dim() > 4:
+    ndim = tensor.dim()
+    if ndim > 4:
         raise ValueError(f"{name} has more than 4 dimensions")
     code = _DTYPE_CODES.get(tensor.dtype)
     if code is None:
         raise TypeError(f"{name} has unsupported dtype {tensor.dtype}")
-    view = EkvTensor()
-    view.data = tensor.data_ptr() if tensor.numel() else None
-    view.dtype = code
-    view.ndim = tensor.dim()
-    for i, (extent, stride) in enumerate(zip(tensor.shape, tensor.stride())):
-        view.shape[i] = extent
-        view.stride[i] = stride
+    view = EkvTensor(tensor.data_ptr() if tensor.numel() else None, code, ndim)
+    # Slice assignment: setting the extents one by one costs more host time per launch.
+    view.shape[:ndim] = tensor.shape
+    view.stride[:ndim] = tensor.stride()
     return view
+
+
+# One struct.Struct per rank: pointer, dtype code, rank, the extents and the
+# element strides, each padded with zero bytes to 4 entries (the EkvTensor layout).
+_PACKERS = tuple(struct.Struct(f"<qii{n}q{8 * (4 - n)}x{n}q{8 * (4 - n)}x") for n in range(5))
+assert all(p.size == ct.sizeof(EkvTensor) for p in _PACKERS)
+
+
+def packed(tensor, name="tensor"):
+    """The bytes of describe(tensor), built in one call: the lookup's launch is bound by host time.
+
+    The data pointer goes over as it is also for an empty tensor (the entry points
+    read no element of one).
+    """
+    shape = tensor.shape
+    ndim = len(shape)
+    code = _DTYPE_CODES.get(tensor.dtype)
+    if code is None or ndim > 4:
+        describe(tensor, name)   # raises the error that names the problem
+    return _PACKERS[ndim].pack(tensor.data_ptr(), code, ndim, *shape, *tensor.stride())
 
 
 def device_of(*tensors):
@@ -150,8 +185,35 @@ def device_of(*tensors):
     return device
 
 
+# torch's raw current-stream query (the one its generated launch code uses) costs a
+# tenth of building a torch.cuda.Stream object; the public call is the fallback.
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device):
+    """The hipStream_t of torch's current stream on `device`, for a launch."""
+    if _RAW_STREAM is not None:
+        return ct.c_void_p(_RAW_STREAM(device.index if device.index is not None else torch.cuda.current_device()))
     return ct.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+class _Current:
+    """A no-op context: the device is already the current one."""
+
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+_CURRENT = _Current()
+
+
+def on_device(device):
+    """Context that makes `device` current for a launch; no switch (and no cost) when it already is."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return _CURRENT if index == torch.cuda.current_device() else torch.cuda.device(index)
 
 
 def check(lib, status, what):

@@ -38,7 +38,7 @@ def gather_rows(raw, positions, request_ids, lengths, request_table, slot_offset
     table_view = ct.byref(_native.describe(request_table, "request_table")) if indirect else None
     offsets_view = ct.byref(_native.describe(slot_offsets, "slot_offsets")) if indirect else None
     out_view = _native.describe(output, "output")
-    with torch.cuda.device(device):
+    with _native.on_device(device):
         status = lib.ekv_gather_rows(
             ct.byref(views[0]), ct.byref(views[1]), ct.byref(views[2]), ct.byref(views[3]),
             table_view, offsets_view, ct.byref(out_view),

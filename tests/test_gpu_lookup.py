@@ -269,3 +269,29 @@ def test_recent_window_parity_with_oracle(gpu, coracle, case):
             c = want_counts[layer, row]
             assert np.array_equal(got_misses[layer, row, :c], want_misses[layer, row, :c])
             assert (got_misses[layer, row, c:] == -5).all()
+
+
+def test_launch_goes_to_the_current_stream(gpu):
+    """The lookup is issued on torch's current stream: a side stream's work is ordered before the host reads it."""
+    from elastic_kv import _native
+
+    batch, context = 4, 8192
+    selected = torch.arange(batch, device=gpu)
+    rows = selected.flip(0)
+    lengths = torch.full((batch,), context, dtype=torch.int32, device=gpu)
+    table = torch.arange(batch * context, device=gpu).reshape(batch, context) + 1
+    mapping = torch.arange(batch * context + 1, device=gpu) * 3 + 5
+    topk = (torch.arange(16, device=gpu) * 4).int().expand(1, batch, 16).contiguous()
+    want = ((rows.view(batch, 1, 1) * context + topk[0].long().view(batch, 16, 1) * 128
+             + torch.arange(128, device=gpu) + 1) * 3 + 5).view(1, batch, 2048).int()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        assert _native.stream_handle(gpu).value == side.cuda_stream
+        out = torch.full((1, batch, 2048), -7, dtype=torch.int32, device=gpu)
+        for _ in range(20):
+            resolve_resident(topk, table, mapping, rows, lengths, selected, out, 128)
+        side.synchronize()
+    # torch's default stream is the null stream: handle 0, which ctypes reads back as None.
+    assert (_native.stream_handle(gpu).value or 0) == torch.cuda.current_stream(gpu).cuda_stream
+    assert torch.equal(out, want)

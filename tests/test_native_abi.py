@@ -137,6 +137,33 @@ def test_kernel_entry_points_validate_before_launch(lib):
     assert typed.ekv_host_device_pointer(None, ct.byref(ct.c_void_p())) == -1
 
 
+def test_packed_descriptors_are_the_struct_bytes(lib):
+    import torch
+
+    from elastic_kv import _native
+
+    typed = _native.kernel_library(str(LIBRARY))
+    cases = [torch.zeros(1, 2, 8, dtype=torch.int32), torch.zeros(3, 4, 5, 6, dtype=torch.bfloat16)[:, 1:3],
+             torch.zeros(2, 9, dtype=torch.int16).t(), torch.tensor(7, dtype=torch.int64),
+             torch.zeros(4, dtype=torch.uint8)[::2]]
+    for t in cases:
+        assert _native.packed(t) == bytes(_native.describe(t)), (t.shape, t.stride())
+    with pytest.raises(ValueError, match="topk has more than 4 dimensions"):
+        _native.packed(torch.zeros(1, 1, 1, 1, 1, dtype=torch.int32), "topk")
+    with pytest.raises(TypeError, match="rows has unsupported dtype"):
+        _native.packed(torch.zeros(2, dtype=torch.float64), "rows")
+
+    # The C side reads the packed bytes: the same validation error as through ctypes.byref.
+    topk = _native.packed(torch.zeros(1, 2, 4, dtype=torch.int32))
+    table = _native.packed(torch.zeros(2, 8, dtype=torch.int64))
+    rows = _native.packed(torch.zeros(2, dtype=torch.int64))
+    lengths = _native.packed(torch.zeros(2, dtype=torch.int32))
+    bad_output = _native.packed(torch.zeros(1, 2, 7, dtype=torch.int32))
+    status = typed.ekv_resolve_resident(topk, table, None, rows, lengths, rows, bad_output, None, None, 2, None)
+    assert status == -1
+    assert b"output dimension 2 is 7, expected 8" in typed.ev_error()
+
+
 FASTDIV_TEST = r"""
 #include "ekv_fastdiv.h"
 #include <cstdio>
@@ -185,6 +212,7 @@ def test_library_built_from_other_sources_is_refused(monkeypatch):
     backing._load_library.cache_clear()
     try:
         monkeypatch.setattr(_native, "source_hash", lambda: "0" * 32)
+        monkeypatch.setattr(_native, "_TYPED", {})   # forget the library typed by earlier tests
         with pytest.raises(RuntimeError, match="built from other sources"):
             _native.kernel_library()
     finally:
