@@ -17,6 +17,12 @@ calling convention that its decode path and swap smoke test use
 (tests/smoke_minimax_swap.py:18-67). tests/test_oracle.py pins all of them
 against the reference's known-answer vectors, closed forms, its smoke
 scenarios and brute-force loops.
+
+Parity unpinned: which free hot slot hisparse_swap gives a particular miss.
+The reference's swap smoke test accepts any free slot and the engine kernel
+that chooses it is not part of the reference; hisparse_swap takes batch-token
+LRU order, empty slots first, and its hits, miss counts, LRU order and bytes
+are pinned as above.
 """
 
 import ctypes as ct
