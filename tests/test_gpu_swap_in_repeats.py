@@ -157,3 +157,46 @@ def test_counted_step_past_the_stamp_range_is_reported(gpu):
     with pytest.raises(RuntimeError, match="overflow"):
         buffers.check_status()
     assert int(buffers.status.item()) == 0
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_swap_in_random_configurations(gpu, seed):
+    """Seeded shapes, block sizes, table forms, summaries, lengths and selections, 2-5 steps each.
+
+    Every step runs lookup + swap-in on the GPU and in the oracle and compares
+    slots, miss counts, the token table, slot tokens, stamps, promotion lists
+    and (per-position summary) the residency bits.
+    """
+    rng = np.random.default_rng(7000 + seed)
+    L, R = int(rng.integers(1, 4)), int(rng.integers(1, 6))
+    B = int(rng.integers(1, R + 1))
+    bs = int(rng.choice([1, 1, 2, 4, 16]))
+    K = int(rng.integers(1, 9))
+    W = K * bs
+    T = int(rng.integers(max(W, 8), 700))
+    C = int(rng.integers(W, W + 64))
+    table_dtype = torch.int16 if rng.random() < 0.5 else torch.int32
+    with_bits = rng.random() < 0.8
+    shift = int(rng.choice([0, 0, 3, 6])) if with_bits else 0
+    buffers = HotBuffers(L, R, T, C, gpu, table_dtype=table_dtype, with_bits=with_bits, bits_shift=shift)
+    host_table = torch.tensor(rng.permutation(R * T), dtype=torch.int32).reshape(R, T)
+    state = {"table": _global(buffers), "slot_token": buffers.slot_token.cpu().numpy(),
+             "stamps": buffers.stamps.cpu().numpy()}
+    rows = rng.permutation(R)[:B]                       # distinct requests: no row is refused
+    lengths = np.where(rng.random(B) < 0.2, rng.integers(1, T + 1, B), rng.integers(T // 2 + 1, T + 1, B))
+    blocks_total = -(-T // bs)
+    row_blocks = -(-lengths // bs)                      # blocks holding a valid position, per batch row
+    span = np.minimum(row_blocks, 2 * K)
+    promoted = 0
+    for step in range(int(rng.integers(2, 6))):
+        selected = np.sort(rng.permutation(B)[:int(rng.integers(1, B + 1))])
+        # a recent-heavy share: the last 2K blocks of each row's own context
+        topk = row_blocks[None, :, None] - 1 - (rng.random((L, B, K)) * span[None, :, None]).astype(np.int64)
+        old = rng.random((L, B, K)) < 0.3
+        topk = np.where(old, rng.integers(0, blocks_total + 3, (L, B, K)), topk)  # some past the length
+        dup = rng.random((L, B, K)) < 0.15
+        topk = np.where(dup, np.take_along_axis(topk, rng.integers(0, K, (L, B, K)), -1), topk)
+        topk[rng.random((L, B, K)) < 0.1] = -1
+        state = _step(gpu, buffers, topk, bs, lengths, state, step, host_table, rows=rows, selected=selected)
+        promoted += int((state["promote_dst"] >= 0).sum())
+    assert promoted > 0
