@@ -1264,10 +1264,15 @@ WORKLOADS = {"decode-read": run_decode_read, "topk-gather": run_topk_gather, "lo
 
 # (key, workload, argument overrides) of the other configurations the default line carries.
 MIGRATION_SPARE_CHUNKS = 700   # > the ~500 chunks a 512-block tick frees and maps
+COMPOSITE_SPARE_CHUNKS = 800   # > the 774 chunks (5 % of the pool) a composite step remaps
 EXTRA_CONFIGS = (("config1_topk_gather", "topk-gather", {}), ("config2_block_gather", "block-gather", {}),
                  ("config4_migration", "migration", {}),
                  ("config4_migration_spare_pool", "migration",
                   {"spare_chunks": MIGRATION_SPARE_CHUNKS, "no_cpu_baseline": True}),
+                 # About one second per step (the remap's VMM calls): 3 timed steps after 1 warm-up.
+                 ("config5_composite", "composite", {"steps": 3, "warmup": 1, "no_cpu_baseline": True}),
+                 ("config5_composite_spare_pool", "composite",
+                  {"steps": 3, "warmup": 1, "spare_chunks": COMPOSITE_SPARE_CHUNKS, "no_cpu_baseline": True}),
                  ("lookup_micro", "lookup-micro", {}))
 
 
@@ -1283,7 +1288,8 @@ def summary(result):
     """The fields of another workload's line that the default line carries for it."""
     keys = ("metric", "value", "unit", "ms_per_step", "roofline", "cpu_baseline", "config", "lookup_us_per_step",
             "hit_rate", "verified_round_trip", "tick_ms", "link_gbs", "pack_gbs", "unpack_gbs", "phase_ms",
-            "higher_is_better", "vs_baseline", "per_batch", "correct")
+            "higher_is_better", "vs_baseline", "per_batch", "correct", "verified_against_host_copy",
+            "step_ms_without_remap", "remap_parts_ms", "promote_gbs_over_pcie", "graph_replay")
     return {key: result[key] for key in keys if key in result}
 
 

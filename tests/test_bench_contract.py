@@ -81,3 +81,17 @@ def test_decode_inputs_reject_shapes_that_cannot_hold_the_picks():
 
     with pytest.raises(ValueError, match="decode inputs need"):
         bench.decode_inputs(torch, torch.device("cpu"), 1, 1, 65536, 2048, 1024, 1024, 0)
+
+
+def test_default_line_extras_name_real_workloads_and_options(monkeypatch):
+    import bench
+
+    monkeypatch.setattr(sys, "argv", ["bench.py"])
+    defaults = vars(bench.parse_args())
+    keys = [key for key, _, _ in bench.EXTRA_CONFIGS]
+    assert len(keys) == len(set(keys))
+    for key, workload, overrides in bench.EXTRA_CONFIGS:
+        assert workload in bench.WORKLOADS, key
+        assert set(overrides) <= set(defaults), (key, set(overrides) - set(defaults))
+    assert {"config1_topk_gather", "config2_block_gather", "config4_migration", "config5_composite",
+            "lookup_micro"} <= set(keys)
