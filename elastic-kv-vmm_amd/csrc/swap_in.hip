@@ -50,6 +50,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kMaxCapacity = 8192;   // slots per hot buffer sortable in LDS
 constexpr int kMaxWidth = 4096;      // lanes per row whose miss tokens are hashed in LDS
+constexpr int kSortPairs = kMaxCapacity / 2 / kThreads;   // compare-exchanges per thread and pass
 constexpr int32_t kStatusStampOverflow = EKV_SWAP_STAMP_OVERFLOW;
 constexpr int32_t kStatusSharedRequest = EKV_SWAP_SHARED_REQUEST;
 
@@ -302,18 +303,31 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
                             : ~uint64_t{0};
         }
         __syncthreads();
-        const int64_t n = a.capacity_pow2;
-        for (int64_t k = 2; k <= n; k <<= 1) {
-            for (int64_t j = k >> 1; j > 0; j >>= 1) {
-                for (int64_t i = threadIdx.x; i < n; i += kThreads) {
-                    const int64_t partner = i ^ j;
-                    if (partner > i) {
-                        const uint64_t x = keys[i], y = keys[partner];
-                        const bool ascending = (i & k) == 0;
-                        if ((x > y) == ascending) {
-                            keys[i] = y;
-                            keys[partner] = x;
-                        }
+        // Bitonic network over the n = pow2(C) keys: in each pass every thread takes the
+        // compare-exchanges p = threadIdx.x + q * kThreads (the pair (i, i + j), i = p with a
+        // zero inserted at bit log2 j), reading all of its pairs before writing any, so the
+        // pass's LDS reads are in flight together instead of one pair at a time.
+        const uint32_t n = static_cast<uint32_t>(a.capacity_pow2);
+        const uint32_t pairs = n >> 1;
+        for (uint32_t k = 2; k <= n; k <<= 1) {
+            for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+                uint64_t first_key[kSortPairs], second_key[kSortPairs];
+#pragma unroll
+                for (int q = 0; q < kSortPairs; ++q) {
+                    const uint32_t p = threadIdx.x + q * kThreads;
+                    const uint32_t i = ((p & ~(j - 1)) << 1) | (p & (j - 1));
+                    if (p < pairs) {
+                        first_key[q] = keys[i];
+                        second_key[q] = keys[i + j];
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < kSortPairs; ++q) {
+                    const uint32_t p = threadIdx.x + q * kThreads;
+                    const uint32_t i = ((p & ~(j - 1)) << 1) | (p & (j - 1));
+                    if (p < pairs && (first_key[q] > second_key[q]) == ((i & k) == 0)) {
+                        keys[i] = second_key[q];
+                        keys[i + j] = first_key[q];
                     }
                 }
                 __syncthreads();
