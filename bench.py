@@ -156,9 +156,13 @@ def cpu_baseline_entry(rates, sample, parity):
             "parity": parity}
 
 
+PROBE_NT_LOAD, PROBE_HALF_TILE = 0x10, 0x20      # include/ekv_kernels.h: EKV_PROBE_NT_LOAD, EKV_PROBE_HALF_TILE
+
+
 def stream_ceilings(torch, device, nbytes=8 << 30, reps=10):
-    """GB/s of this box's own streaming kernels (ekv_stream_probe): read-only, write-only and copy,
-    without a workgroup cap and at 2, 3 and 4 workgroups per CU; plus torch's device copy."""
+    """GB/s of this box's own streaming kernels (ekv_stream_probe): read-only, write-only and copy, each in its
+    variants (32 or 16 KiB tiles; temporal or non-temporal loads) without a workgroup cap and at 2, 3 and 4
+    workgroups per CU; the best of each mode is its ceiling. Plus torch's device copy."""
     from elastic_kv import _native
 
     lib = _native.kernel_library()
@@ -167,16 +171,22 @@ def stream_ceilings(torch, device, nbytes=8 << 30, reps=10):
     src.fill_(1)
     result = {}
     for name, mode, moved in (("read", 0, nbytes), ("write", 1, nbytes), ("copy", 2, 2 * nbytes)):
+        loads = (0,) if name == "write" else (0, PROBE_NT_LOAD)
         per = {}
-        for per_cu in (0, 2, 3, 4):
-            def probe(mode=mode, per_cu=per_cu):
-                status = lib.ekv_stream_probe(mode, src.data_ptr(), dst.data_ptr(), nbytes, per_cu,
-                                              _native.stream_handle(device))
-                _native.check(lib, status, "stream probe")
+        for tile in (0, PROBE_HALF_TILE):
+            for load in loads:
+                label = ("16k" if tile else "32k") + ("_nt_load" if load else "")
+                for per_cu in (0, 2, 3, 4):
+                    def probe(flags=mode | tile | load, per_cu=per_cu):
+                        status = lib.ekv_stream_probe(flags, src.data_ptr(), dst.data_ptr(), nbytes, per_cu,
+                                                      _native.stream_handle(device))
+                        _native.check(lib, status, "stream probe")
 
-            ms = back_to_back_ms(torch, probe, reps)
-            per["max_per_cu" if per_cu == 0 else f"{per_cu}_per_cu"] = round(moved / (ms / 1e3) / 1e9, 1)
-        result[name] = {"best_gbs": max(per.values()), **per}
+                    ms = back_to_back_ms(torch, probe, reps)
+                    cap = "max_per_cu" if per_cu == 0 else f"{per_cu}_per_cu"
+                    per[f"{label}_{cap}"] = round(moved / (ms / 1e3) / 1e9, 1)
+        best = max(per, key=per.get)
+        result[name] = {"best_gbs": per[best], "best_variant": best, **per}
     torch.cuda.synchronize()
     ms = back_to_back_ms(torch, lambda: dst.copy_(src), reps)
     result["torch_copy_gbs"] = round(2 * nbytes / (ms / 1e3) / 1e9, 1)

@@ -405,13 +405,18 @@ int ekv_decode_step_static(const ekv_step_args* args, void* stream);
 #define EKV_PROBE_READ 0   /* read src (fold, no stores)       */
 #define EKV_PROBE_WRITE 1  /* write zeros to dst                */
 #define EKV_PROBE_COPY 2   /* dst = src                         */
+/* Variant flags, OR-ed into the mode. */
+#define EKV_PROBE_NT_LOAD 0x10    /* non-temporal loads                       */
+#define EKV_PROBE_HALF_TILE 0x20  /* 16 KiB tiles, 4 loads in flight per lane */
 
 /*
  * Streaming bandwidth probe over `bytes` of dense device memory (16-byte
  * aligned, a multiple of 16): one launch of the read-only, write-only or
  * copy kernel, with the row-copy engine's access style (16-byte lanes, 8
  * loads in flight per lane, non-temporal stores, 32 KiB tiles dealt to the
- * XCDs in contiguous ranges). workgroups_per_cu > 0 reserves LDS so that at
+ * XCDs in contiguous ranges); EKV_PROBE_NT_LOAD and EKV_PROBE_HALF_TILE
+ * select the variants a ceiling is also taken over (the read and copy modes
+ * take both, the write mode the tile size). workgroups_per_cu > 0 reserves LDS so that at
  * most that many workgroups share a CU; 0 leaves the register limit. dst must
  * hold `bytes` bytes in every mode (the read probe never writes it unless src
  * holds a planted pattern); src may be NULL for EKV_PROBE_WRITE.

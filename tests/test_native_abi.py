@@ -135,6 +135,10 @@ def test_kernel_entry_points_validate_before_launch(lib):
     one_plane = _native.EkvPlanes(4096, 1, 1, 0, 0, 256, 256, 64)
     assert swap(planes=one_plane) == -1 and b"one layer of K and V planes" in typed.ev_error()
     assert typed.ekv_host_device_pointer(None, ct.byref(ct.c_void_p())) == -1
+    assert typed.ekv_stream_probe(2 | 0x40, 4096, 4096, 1 << 20, 0, None) == -1
+    assert b"unknown stream probe flags" in typed.ev_error()
+    assert typed.ekv_stream_probe(3 | 0x10, 4096, 4096, 1 << 20, 0, None) == -1
+    assert b"mode must be" in typed.ev_error()
 
 
 def test_packed_descriptors_are_the_struct_bytes(lib):
