@@ -10,8 +10,6 @@ launch. scatter_kv is the inverse, used to unpack migrated rows.
 import ctypes as ct
 from math import prod
 
-import torch
-
 from elastic_kv import _native
 from experimental.sparse_read import gather_rows  # noqa: F401  (re-export)
 

@@ -7,8 +7,6 @@ row-copy engine of csrc/gather.hip.
 
 import ctypes as ct
 
-import torch
-
 from elastic_kv import _native
 
 
