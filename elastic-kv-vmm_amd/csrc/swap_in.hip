@@ -25,7 +25,8 @@
 // later lanes share that slot and record empty promotions.
 //
 // One 256-thread workgroup per (row, layer): hits are touched in LDS, the
-// (stamp, slot) keys are bitonic-sorted in LDS, then each victim clears its
+// (stamp, slot) keys are bitonic-sorted (held in registers between LDS
+// transposes for hot buffers of 2049-8192 slots, in LDS below), then each victim clears its
 // old token from the token->slot table and residency summary, takes the new
 // token, and writes one promotion (host row -> global slot) record. The
 // lookup's slot output of every miss lane is patched to its new slot, so the
@@ -141,8 +142,100 @@ __device__ __forceinline__ uint32_t token_hash(int32_t token, uint32_t log2_size
     return (static_cast<uint32_t>(token) * 2654435761u) >> (32 - log2_size);
 }
 
+// Register-resident bitonic sort of n = kThreads * R keys (R = 2^LB). Each
+// thread holds R keys whose indices differ only in a window of LB index
+// bits; the network's compare-exchanges along a bit of the window run in
+// registers, and the keys move to another window through LDS (padded by one
+// entry per R, so that a thread's writes at stride R spread over the banks).
+// The windows start at bits 0, LB and log2(n) - LB; for the falling bit of
+// each merge stage the lowest window holding it is taken. On return
+// keys[0 .. n) holds the keys in ascending order.
+template <int R, int LB>
+struct RegisterSort {
+    static constexpr uint32_t kBits = LB + 8;   // log2 n with kThreads = 256 threads
+
+    __device__ __forceinline__ static uint32_t index(uint32_t t, int r, uint32_t s) {
+        return (t & ((1u << s) - 1u)) | (static_cast<uint32_t>(r) << s) | ((t >> s) << (s + LB));
+    }
+    __device__ __forceinline__ static uint32_t padded(uint32_t i) { return i + (i >> LB); }
+    __device__ __forceinline__ static uint32_t window_for(uint32_t bit) {
+        return bit < LB ? 0u : (bit < 2 * LB ? static_cast<uint32_t>(LB) : kBits - LB);
+    }
+
+    template <int Q>
+    __device__ __forceinline__ static void exchange(uint64_t (&v)[R], uint32_t t, uint32_t s, uint32_t k) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if ((r >> Q) & 1) {
+                continue;
+            }
+            const bool up = (index(t, r, s) & k) == 0;
+            const uint64_t x = v[r], y = v[r | (1 << Q)];
+            const bool swap = (x > y) == up;
+            v[r] = swap ? y : x;
+            v[r | (1 << Q)] = swap ? x : y;
+        }
+    }
+
+    // The exchanges along bits top, top - 1, .., s of the window that starts at s, in that
+    // order (the bit of each is fixed at compile time, so the keys stay in registers).
+    template <int Q>
+    __device__ __forceinline__ static void exchange_down(uint64_t (&v)[R], uint32_t t, uint32_t s, uint32_t top,
+                                                         uint32_t k) {
+        if (s + Q <= top) {
+            exchange<Q>(v, t, s, k);
+        }
+        if constexpr (Q > 0) {
+            exchange_down<Q - 1>(v, t, s, top, k);
+        }
+    }
+
+    __device__ __forceinline__ static void relayout(uint64_t (&v)[R], uint64_t* lds, uint32_t t, uint32_t from, uint32_t to) {
+        __syncthreads();   // every thread has read the previous layout
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            lds[padded(index(t, r, from))] = v[r];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            v[r] = lds[padded(index(t, r, to))];
+        }
+    }
+
+    template <typename KeyOf>
+    __device__ __forceinline__ static void sort(uint64_t* lds, KeyOf key_of) {
+        const uint32_t t = threadIdx.x;
+        uint64_t v[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            v[r] = key_of(index(t, r, 0));
+        }
+        uint32_t s = 0;   // start of the window in registers (uniform)
+        for (uint32_t stage = 1; stage <= kBits; ++stage) {
+            const uint32_t k = 1u << stage;
+            // Merge along bits stage - 1 .. 0, one window at a time from the top.
+            for (int32_t top = static_cast<int32_t>(stage) - 1; top >= 0; top = static_cast<int32_t>(s) - 1) {
+                const uint32_t w = window_for(static_cast<uint32_t>(top));
+                if (w != s) {
+                    relayout(v, lds, t, s, w);
+                    s = w;
+                }
+                exchange_down<LB - 1>(v, t, s, static_cast<uint32_t>(top), k);
+            }
+        }
+        __syncthreads();   // every thread has read the last padded layout
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            lds[index(t, r, s)] = v[r];
+        }
+        __syncthreads();
+    }
+};
+
 // Dynamic LDS of one workgroup (C = capacity, W = lanes per row):
-//   region   max(8 * pow2(C), 4 * hash_size) bytes, used three times over:
+//   region   max(8 * pow2(C) (+ 2 KiB of padding for the register sort), 4 * hash_size)
+//            bytes, used three times over:
 //            touch[C] (first hit lane per slot), then the miss-token hash
 //            (miss indices), then the (stamp, slot) sort keys;
 //   stamp    [C] recency stamps;
@@ -297,40 +390,48 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
         }
         // The `unique` victims: the smallest (stamp, slot) keys, empty slots
         // (INT32_MIN) first, then the least recently used.
-        for (int64_t s = threadIdx.x; s < a.capacity_pow2; s += kThreads) {
-            keys[s] = s < C ? (static_cast<uint64_t>(static_cast<uint32_t>(stamp[s]) ^ 0x80000000u) << 32) |
-                                  static_cast<uint64_t>(s)
-                            : ~uint64_t{0};
-        }
-        __syncthreads();
-        // Bitonic network over the n = pow2(C) keys: in each pass every thread takes the
-        // compare-exchanges p = threadIdx.x + q * kThreads (the pair (i, i + j), i = p with a
-        // zero inserted at bit log2 j), reading all of its pairs before writing any, so the
-        // pass's LDS reads are in flight together instead of one pair at a time.
+        const auto key_of = [&](uint32_t s) {
+            return s < C ? (static_cast<uint64_t>(static_cast<uint32_t>(stamp[s]) ^ 0x80000000u) << 32) |
+                               static_cast<uint64_t>(s)
+                         : ~uint64_t{0};
+        };
         const uint32_t n = static_cast<uint32_t>(a.capacity_pow2);
-        const uint32_t pairs = n >> 1;
-        for (uint32_t k = 2; k <= n; k <<= 1) {
-            for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-                uint64_t first_key[kSortPairs], second_key[kSortPairs];
+        if (n == 4096) {
+            RegisterSort<16, 4>::sort(keys, key_of);
+        } else if (n == 8192) {
+            RegisterSort<32, 5>::sort(keys, key_of);
+        } else {
+            for (uint32_t s = threadIdx.x; s < n; s += kThreads) {
+                keys[s] = key_of(s);
+            }
+            __syncthreads();
+            // Bitonic network in LDS: in each pass every thread takes the compare-exchanges
+            // p = threadIdx.x + q * kThreads (the pair (i, i + j), i = p with a zero inserted at
+            // bit log2 j), reading all of its pairs before writing any.
+            const uint32_t pairs = n >> 1;
+            for (uint32_t k = 2; k <= n; k <<= 1) {
+                for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+                    uint64_t first_key[kSortPairs], second_key[kSortPairs];
 #pragma unroll
-                for (int q = 0; q < kSortPairs; ++q) {
-                    const uint32_t p = threadIdx.x + q * kThreads;
-                    const uint32_t i = ((p & ~(j - 1)) << 1) | (p & (j - 1));
-                    if (p < pairs) {
-                        first_key[q] = keys[i];
-                        second_key[q] = keys[i + j];
+                    for (int q = 0; q < kSortPairs; ++q) {
+                        const uint32_t p = threadIdx.x + q * kThreads;
+                        const uint32_t i = ((p & ~(j - 1)) << 1) | (p & (j - 1));
+                        if (p < pairs) {
+                            first_key[q] = keys[i];
+                            second_key[q] = keys[i + j];
+                        }
                     }
-                }
 #pragma unroll
-                for (int q = 0; q < kSortPairs; ++q) {
-                    const uint32_t p = threadIdx.x + q * kThreads;
-                    const uint32_t i = ((p & ~(j - 1)) << 1) | (p & (j - 1));
-                    if (p < pairs && (first_key[q] > second_key[q]) == ((i & k) == 0)) {
-                        keys[i] = second_key[q];
-                        keys[i + j] = first_key[q];
+                    for (int q = 0; q < kSortPairs; ++q) {
+                        const uint32_t p = threadIdx.x + q * kThreads;
+                        const uint32_t i = ((p & ~(j - 1)) << 1) | (p & (j - 1));
+                        if (p < pairs && (first_key[q] > second_key[q]) == ((i & k) == 0)) {
+                            keys[i] = second_key[q];
+                            keys[i + j] = first_key[q];
+                        }
                     }
+                    __syncthreads();
                 }
-                __syncthreads();
             }
         }
         int32_t* bits = a.bits != nullptr ? a.bits + l * a.bt_l + req * a.bt_r : nullptr;
@@ -566,7 +667,10 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
         a.hash_size <<= 1;
         ++a.hash_log2;
     }
-    const size_t region = std::max<size_t>(static_cast<size_t>(a.capacity_pow2) * sizeof(uint64_t),
+    // The register sort of 4096 or 8192 keys moves them through LDS padded by one entry per
+    // 16 or 32 (256 entries more).
+    const int64_t sort_entries = a.capacity_pow2 + (a.capacity_pow2 == 4096 || a.capacity_pow2 == 8192 ? 256 : 0);
+    const size_t region = std::max<size_t>(static_cast<size_t>(sort_entries) * sizeof(uint64_t),
                                            static_cast<size_t>(a.hash_size) * sizeof(int32_t));
     a.region_bytes = static_cast<uint32_t>(region);
     const size_t lds = region + static_cast<size_t>(C) * 4 + static_cast<size_t>(W) * 8;

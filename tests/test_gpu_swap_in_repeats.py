@@ -200,3 +200,28 @@ def test_swap_in_random_configurations(gpu, seed):
         state = _step(gpu, buffers, topk, bs, lengths, state, step, host_table, rows=rows, selected=selected)
         promoted += int((state["promote_dst"] >= 0).sum())
     assert promoted > 0
+
+
+@pytest.mark.parametrize("capacity", [2500, 4096, 5000, 8192])
+def test_large_hot_buffers_evict_in_lru_order(gpu, capacity):
+    """Hot buffers of more than 2048 slots (their 4096 or 8192 sort keys are sorted in registers): nearly full
+    buffers, so every step's misses evict least-recently-used entries; 3 steps against the oracle."""
+    rng = np.random.default_rng(capacity)
+    L, R, K, bs = 2, 2, 64, 4                                    # 256 lanes per row
+    T = capacity + 3000
+    table_dtype = torch.int16 if capacity % 2 else torch.int32
+    buffers = HotBuffers(L, R, T, capacity, gpu, table_dtype=table_dtype)
+    filled = capacity - 5                                        # five empty slots, taken first
+    tokens = np.stack([[rng.choice(T, filled, replace=False) for _ in range(R)] for _ in range(L)])
+    local = np.stack([[rng.permutation(capacity)[:filled] for _ in range(R)] for _ in range(L)])
+    buffers.install(torch.tensor(tokens), torch.tensor(local))
+    host_table = torch.tensor(rng.permutation(R * T), dtype=torch.int32).reshape(R, T)
+    state = {"table": _global(buffers), "slot_token": buffers.slot_token.cpu().numpy(),
+             "stamps": buffers.stamps.cpu().numpy()}
+    evicted = 0
+    for step in range(3):
+        topk = rng.integers(0, T // bs, (L, R, K))
+        before = state["slot_token"].copy()
+        state = _step(gpu, buffers, topk, bs, np.full(R, T), state, step, host_table)
+        evicted += int(((before >= 0) & (state["slot_token"] != before)).sum())
+    assert evicted > 0
