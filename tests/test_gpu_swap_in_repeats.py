@@ -197,6 +197,9 @@ def test_swap_in_random_configurations(gpu, seed):
         dup = rng.random((L, B, K)) < 0.15
         topk = np.where(dup, np.take_along_axis(topk, rng.integers(0, K, (L, B, K)), -1), topk)
         topk[rng.random((L, B, K)) < 0.1] = -1
+        if step == 0:   # every row selected with one valid pick: the first step has misses to promote
+            selected = np.arange(B)
+            topk[:, :, 0] = row_blocks[None, :] - 1
         state = _step(gpu, buffers, topk, bs, lengths, state, step, host_table, rows=rows, selected=selected)
         promoted += int((state["promote_dst"] >= 0).sum())
     assert promoted > 0
