@@ -473,3 +473,37 @@ def test_swap_in_random_configurations(gpu, seed):
                 c = want_counts_full[layer, r]
                 assert np.array_equal(got_src[layer, r, :c], state["promote_src"][layer, r, :c]), (seed, step)
                 assert np.array_equal(got_dst[layer, r, :c], state["promote_dst"][layer, r, :c]), (seed, step)
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_gather_rows_random_configurations(gpu, coracle, seed):
+    """experimental/sparse_read.py's gather_rows on seeded layouts: row widths of 1-300 bf16 elements, direct and
+    indirect addressing, positions, requests, table entries and element offsets in and out of range (odd offsets
+    take the unaligned path), against the C oracle bit for bit."""
+    from types import SimpleNamespace
+
+    from experimental.sparse_read import gather_rows
+
+    rng = np.random.default_rng(9000 + seed)
+    width = int(rng.choice([1, 2, 3, 8, 64, 128, 256, 300]))
+    batch, selected, requests = int(rng.integers(1, 5)), int(rng.integers(1, 200)), int(rng.integers(1, 5))
+    length = int(rng.integers(1, 300))
+    request_stride = length * width + int(rng.integers(0, 3))       # elements per request region
+    sink = int(rng.integers(0, 64))
+    raw_elems = max(1, sink + requests * request_stride + int(rng.integers(-width, 50)))
+    raw = rng.integers(0, 1 << 16, raw_elems, dtype=np.uint16)
+    positions = rng.integers(-3, length + 3, (batch, selected))
+    request_ids = rng.integers(-1, requests + 1, batch)
+    lengths = rng.integers(0, length + 1, batch)
+    table = rng.integers(-2, requests * length + 3, (requests, length))
+    offsets = rng.integers(-5, raw_elems + 5, requests * length + 1)
+    indirect = bool(rng.random() < 0.5)
+    layout = SimpleNamespace(row_elements=width, request_bytes=2 * request_stride, chunk_bytes=2 * sink, itemsize=2)
+    raw_d = torch.tensor(raw.view(np.int16)).view(torch.bfloat16).to(gpu)
+    output = torch.full((batch, selected, width), 7.0, dtype=torch.bfloat16, device=gpu)
+    gather_rows(raw_d, torch.tensor(positions, device=gpu), torch.tensor(request_ids, device=gpu),
+                torch.tensor(lengths, device=gpu), torch.tensor(table, device=gpu), torch.tensor(offsets, device=gpu),
+                output, layout, indirect=indirect)
+    want = coracle.gather_rows(raw, positions, request_ids, lengths, table, offsets, width, request_stride, sink,
+                               indirect)
+    assert np.array_equal(output.view(torch.int16).cpu().numpy().view(np.uint16), want)
