@@ -15,10 +15,11 @@ divided by the measured step time, lookup included.
 
 The default line also carries, as extra keys, the streaming ceilings of this
 box (own read / write / copy kernels), the lookup variants timed in
-alternating arms, and configs 1, 2 and 4 (topk-gather, block-gather,
-migration below), each with its own roofline, parity flags and CPU baseline;
-config 4 also with the VMM spare pool (--spare-chunks: reclaimed chunks'
-memory kept for the next commits).
+alternating arms, configs 1, 2 and 4 (topk-gather, block-gather, migration
+below), each with its own roofline, parity flags and CPU baseline, configs 4
+and 5 also with the VMM spare pool (--spare-chunks: reclaimed chunks' memory
+kept for the next commits), and the reference's two microbenchmarks
+(lookup-micro, virtual-addressing).
 The CPU baseline is the reference's torch CPU path restated
 (oracle/torch_path.py: adaptive_sparse/request_residency.py:819-825, nonzero,
 index_select) at all visible host threads and at one thread.
@@ -46,6 +47,11 @@ Other workloads (same JSON contract):
                 16 Top-K blocks of 128 tokens, two-level int64 lookup, per-call
                 p50/p95 with the host launch included (time-like: lower is
                 better; vs_baseline against the reference's A100 Triton p50)
+  virtual-addressing  the reference's gather microbenchmark
+                (scripts/bench_virtual_addressing.py): gather_rows over a VMM
+                arena of 4 x 65,536 rows of 256 bf16, 2048 positions per
+                request from three support sets, direct and software-table
+                addressing; host-launched p50 per call and HIP-graph GB/s
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -81,7 +87,7 @@ def parse_args():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--workload", default="decode-read",
                         choices=["decode-read", "topk-gather", "block-gather", "migration", "composite",
-                                 "hisparse-swap", "lookup-micro"])
+                                 "hisparse-swap", "lookup-micro", "virtual-addressing"])
     parser.add_argument("--remap-fraction", type=float, default=0.05,
                         help="share of pool chunks unmapped and remapped per composite step")
     parser.add_argument("--capacity", type=int, default=4096, help="hot slots per request (decode-read)")
@@ -1048,6 +1054,130 @@ def run_lookup_micro(torch, args, device):
     return result
 
 
+def reference_support_sets(length, selected, seed=137):
+    """The three position sets of scripts/analyze_virtual_layout.py:11-27: the first `selected` positions, a
+    uniform sample, and runs of selected // 8 positions from random starts (the same generator calls, so the same
+    sets)."""
+    import random
+
+    draw = random.Random(seed)
+    run = max(1, selected // 8)
+    clustered = set()
+    while len(clustered) < selected:
+        start = draw.randrange(length)
+        clustered.update((start + i) % length for i in range(min(run, selected - len(clustered))))
+    return {"contiguous": list(range(selected)), "uniform_random": draw.sample(range(length), selected),
+            "synthetic_clustered": sorted(clustered)}
+
+
+def run_virtual_addressing(torch, args, device):
+    """scripts/bench_virtual_addressing.py of the reference, on this build's gather_rows.
+
+    4 requests x 65,536 positions of 256 bf16 (512 B rows) in a VMM arena, 2048 positions gathered per request
+    from each of the three support sets, direct (layout arithmetic) and software-table (two dependent lookups)
+    addressing over identical payload addresses; every result checked against the closed-form payload
+    (pos * 256 + col + req * 17) % 97, invalid lanes too; then 30 rounds of 20 host-launched calls, the two modes
+    alternating (HIP events, us per call, as the reference measures), and 20 calls replayed from a HIP graph.
+    """
+    from experimental.resident_arena import VmmResidentArena
+    from experimental.sparse_read import gather_rows
+    from experimental.virtual_layout import VirtualKVLayout
+
+    batch, length, selected, width, rounds, calls = 4, 65536, 2048, 256, 30, 20
+    layout = VirtualKVLayout(batch, length, width)
+    arena = VmmResidentArena(layout)
+    results = {}
+    try:
+        for req in range(batch):
+            arena.reserve(req, length)
+            view = arena.row_view(req, length, torch.bfloat16)
+            view.copy_(((torch.arange(length * width, device=device) + req * 17) % 97).reshape(length, width))
+        del view
+        raw = arena.backing.raw.view(torch.bfloat16)
+        request_ids = torch.arange(batch, device=device, dtype=torch.int64).flip(0)
+        lengths = torch.full((batch,), length, device=device, dtype=torch.int64)
+        count = batch * length
+        table = torch.arange(count, 0, -1, device=device, dtype=torch.int64).reshape(batch, length)
+        flat = torch.arange(count, device=device, dtype=torch.int64)
+        offsets = torch.zeros(count + 1, device=device, dtype=torch.int64)
+        offsets[table.flatten()] = (layout.chunk_bytes // layout.itemsize
+                                    + (flat // length) * (layout.request_bytes // layout.itemsize)
+                                    + (flat % length) * width)
+        del flat
+        output = torch.empty((batch, selected, width), device=device, dtype=torch.bfloat16)
+        lanes = batch * selected
+        moved = {False: lanes * (2 * width * 2 + 8),                  # row read + row written + position
+                 True: lanes * (2 * width * 2 + 8 + 8 + 8)}           # + table entry + element offset
+        correct = True
+        for name, support in reference_support_sets(length, selected).items():
+            positions = torch.tensor(support, device=device, dtype=torch.int64).expand(batch, -1).contiguous()
+            columns = torch.arange(width, device=device)
+            expected = ((positions[..., None] * width + columns + request_ids[:, None, None] * 17) % 97).to(
+                torch.bfloat16)
+
+            def call(indirect, read=positions):
+                gather_rows(raw, read, request_ids, lengths, table, offsets, output, layout, indirect=indirect)
+
+            for indirect in (False, True):
+                call(indirect)
+                correct &= bool(torch.equal(output, expected))
+                for invalid in (-1, length):
+                    bad = positions.clone()
+                    bad[:, 0] = invalid
+                    call(indirect, bad)
+                    correct &= bool(torch.equal(output[:, 1:], expected[:, 1:])) and not output[:, 0].any()
+                for _ in range(30):
+                    call(indirect)
+            torch.cuda.synchronize()
+            timings = {False: [], True: []}
+            for repeat in range(rounds):
+                for indirect in ((False, True) if repeat % 2 == 0 else (True, False)):
+                    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    begin.record()
+                    for _ in range(calls):
+                        call(indirect)
+                    end.record()
+                    end.synchronize()
+                    timings[indirect].append(begin.elapsed_time(end) * 1e3 / calls)
+            entry = {}
+            for indirect, label in ((False, "direct"), (True, "software_table")):
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    for _ in range(calls):
+                        call(indirect)
+                graph.replay()
+                torch.cuda.synchronize()
+                correct &= bool(torch.equal(output, expected))
+                replays = []
+                for _ in range(10):
+                    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    begin.record()
+                    graph.replay()
+                    end.record()
+                    end.synchronize()
+                    replays.append(begin.elapsed_time(end) * 1e3 / calls)
+                del graph
+                p50, graph_us = statistics.median(timings[indirect]), statistics.median(replays)
+                entry[label] = {"p50_us": round(p50, 2), "graph_us_per_call": round(graph_us, 2),
+                                "graph_gbs": round(moved[indirect] / (graph_us / 1e6) / 1e9, 1)}
+            results[name] = entry
+            log(f"virtual addressing {name}: {entry}")
+        del raw, output
+        torch.cuda.synchronize()
+    finally:
+        arena.close()
+    value = results["uniform_random"]["direct"]["graph_gbs"]
+    config = {"workload": "virtual-addressing-gather", "batch": batch, "length": length, "selected": selected,
+              "width_bf16": width, "rounds": rounds, "calls_per_round": calls,
+              "support_sets": list(results), "modes": ["direct", "software_table"]}
+    result = envelope(args, value, results["uniform_random"]["direct"]["graph_us_per_call"] / 1e3, config, None,
+                      None, {"per_support_set": results, "correct": bool(correct)},
+                      metric="gather_rows GB/s per call from a HIP graph (uniform-random positions, direct)")
+    result["data"] = "the reference gather benchmark's closed-form payload"
+    result["steps"], result["warmup"] = rounds * calls, 30
+    return result
+
+
 # ------------------------------------------------------------------ composite (config 5)
 
 
@@ -1268,6 +1398,7 @@ def run_composite(torch, args, device):
 
 
 WORKLOADS = {"decode-read": run_decode_read, "topk-gather": run_topk_gather, "lookup-micro": run_lookup_micro,
+             "virtual-addressing": run_virtual_addressing,
              "block-gather": run_block_gather, "migration": run_migration, "composite": run_composite,
              "hisparse-swap": run_hisparse_swap}
 
@@ -1283,7 +1414,8 @@ EXTRA_CONFIGS = (("config1_topk_gather", "topk-gather", {}), ("config2_block_gat
                  ("config5_composite", "composite", {"steps": 3, "warmup": 1, "no_cpu_baseline": True}),
                  ("config5_composite_spare_pool", "composite",
                   {"steps": 3, "warmup": 1, "spare_chunks": COMPOSITE_SPARE_CHUNKS, "no_cpu_baseline": True}),
-                 ("lookup_micro", "lookup-micro", {}))
+                 ("lookup_micro", "lookup-micro", {}),
+                 ("virtual_addressing", "virtual-addressing", {}))
 
 
 def apply_profile_switch(environment, keep):
@@ -1299,7 +1431,7 @@ def summary(result):
     keys = ("metric", "value", "unit", "ms_per_step", "roofline", "cpu_baseline", "config", "lookup_us_per_step",
             "hit_rate", "verified_round_trip", "tick_ms", "link_gbs", "pack_gbs", "unpack_gbs", "phase_ms",
             "higher_is_better", "vs_baseline", "per_batch", "correct", "verified_against_host_copy",
-            "step_ms_without_remap", "remap_parts_ms", "promote_gbs_over_pcie", "graph_replay")
+            "step_ms_without_remap", "remap_parts_ms", "promote_gbs_over_pcie", "graph_replay", "per_support_set")
     return {key: result[key] for key in keys if key in result}
 
 
