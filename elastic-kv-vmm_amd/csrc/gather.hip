@@ -28,6 +28,8 @@
 #include "ekv_vec.h"
 
 #include <algorithm>
+#include <stdexcept>
+#include <atomic>
 #include <cstdlib>
 #include <type_traits>
 
@@ -345,6 +347,32 @@ int64_t env_int(const char* name, int64_t fallback) {
     return std::strtoll(text, nullptr, 10);
 }
 
+// Compute units of the current device (cached per device).
+int64_t device_cus() {
+    static std::atomic<int> cached[64];
+    int device = 0;
+    check_hip(hipGetDevice(&device), "hipGetDevice");
+    if (device < 0 || device >= 64) {
+        throw std::runtime_error("device ordinal out of range");
+    }
+    int cus = cached[device].load(std::memory_order_relaxed);
+    if (cus == 0) {
+        check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
+                  "hipDeviceGetAttribute");
+        cus = std::max(1, cus);
+        cached[device].store(cus, std::memory_order_relaxed);
+    }
+    return cus;
+}
+
+// A small job (a few thousand rows: one layer of a small batch, a short
+// gather) would fill only a fraction of the CUs with full tiles and take one
+// tile's latency on each; below this many workgroups per CU its tiles shrink
+// so that the grid reaches it (a tile keeps at least one row).
+#ifndef EKV_SMALL_JOB_GROUPS_PER_CU
+#define EKV_SMALL_JOB_GROUPS_PER_CU 2
+#endif
+
 template <int M, int VW>
 void launch_engine(EngineArgs a, hipStream_t stream) {
     const int64_t tile_bytes = int64_t{kThreads} * kUnroll * VW;
@@ -354,6 +382,11 @@ void launch_engine(EngineArgs a, hipStream_t stream) {
         a.rows_per_tile = static_cast<uint32_t>(std::min<int64_t>(kThreads, tile_bytes / a.row_bytes));
         a.vec_div = FastDiv(a.vecs_per_row);
         a.tiles = (a.units + a.rows_per_tile - 1) / a.rows_per_tile;
+        const int64_t wanted = EKV_SMALL_JOB_GROUPS_PER_CU * device_cus();
+        if (EKV_SMALL_JOB_GROUPS_PER_CU > 0 && a.tiles < wanted) {
+            a.rows_per_tile = static_cast<uint32_t>(std::max<int64_t>(1, (a.units + wanted - 1) / wanted));
+            a.tiles = (a.units + a.rows_per_tile - 1) / a.rows_per_tile;
+        }
     } else {
         a.seg_bytes = tile_bytes;
         a.segs_per_row = (a.row_bytes + tile_bytes - 1) / tile_bytes;
