@@ -9,9 +9,12 @@ Replaces the third-party host-copy kernels the reference migrates through
   promote: pinned host --hipMemcpyAsync H2D (side stream)--> device staging
                       --unpack (ekv_scatter_kv)--> freshly committed pool pages
 
-Pages are moved in sub-batches so that packing, the two PCIe directions and
-unpacking overlap; events order each sub-batch across the three streams. All
-streams have the default priority.
+The pages are packed in one launch, then copied in sub-batches so that the
+two PCIe directions and the unpacks overlap; events order each sub-batch
+across the three streams. (A pack that shares the GPU with the copy kernels
+that carry the PCIe legs crawls: 64 pages of 2.25 MiB took 2.8-2.9 ms against
+65 us alone, while the whole 512-page pack takes 0.49 ms.) All streams have
+the default priority.
 """
 
 from dataclasses import dataclass
@@ -139,17 +142,23 @@ class MigrationEngine:
 
     def _slots(self, pages):
         layout = self.pool.layout
-        ids = torch.as_tensor(list(pages), dtype=torch.int64).to(self.device, non_blocking=True)
-        return ids.view(1, 1, -1).expand(layout.layers, 1, len(pages))
+        if isinstance(pages, torch.Tensor):
+            ids = pages.to(self.device, torch.int64)
+        else:
+            ids = torch.as_tensor(list(pages), dtype=torch.int64).to(self.device, non_blocking=True)
+        return ids.view(1, 1, -1).expand(layout.layers, 1, len(ids))
 
     def pack(self, pages, staging, start=0):
-        """staging[start + i] = bytes of page pages[i] (on the current stream)."""
-        if pages:
+        """staging[start + i] = bytes of page pages[i] (on the current stream).
+
+        `pages` is a sequence of page ids or an int64 tensor of them (a device
+        tensor saves the copy of the list)."""
+        if len(pages):
             gather_kv(self.pool.planes, self._slots(pages), self._dense(staging, start, len(pages)), zero_below=1)
 
     def unpack(self, pages, staging, start=0):
-        """Bytes of page pages[i] = staging[start + i] (on the current stream)."""
-        if pages:
+        """Bytes of page pages[i] = staging[start + i] (on the current stream); `pages` as for pack()."""
+        if len(pages):
             scatter_kv(self.pool.planes, self._slots(pages), self._dense(staging, start, len(pages)), zero_below=1)
 
     # ------------------------------------------------------------ host rows
@@ -180,7 +189,7 @@ class MigrationEngine:
     def demote(self, pages, host_rows=None):
         """Copy pages to pinned host rows; returns HostPages when the D2H is queued.
 
-        The pack kernels run on the current stream and the D2H copies on a
+        The pack kernel runs on the current stream and the D2H copies on a
         side stream; call wait() (or synchronize) before reading the host rows.
         """
         pages = tuple(int(p) for p in pages)
@@ -189,17 +198,20 @@ class MigrationEngine:
         rows = self.reserve_host(len(pages)) if host_rows is None else host_rows
         compute = torch.cuda.current_stream(self.device)
         self._order_reuse(compute)
+        self.d2h.wait_event(self._pack_all(pages, compute))
         for start in range(0, len(pages), self.sub_batch):
-            chunk = pages[start:start + self.sub_batch]
-            self.pack(chunk, self.out_staging, start)
-            packed = torch.cuda.Event()
-            packed.record(compute)
-            self.d2h.wait_event(packed)
             with torch.cuda.stream(self.d2h):
-                self._copy_rows(rows[start:start + len(chunk)], self.out_staging, start, to_host=True)
+                self._copy_rows(rows[start:start + self.sub_batch], self.out_staging, start, to_host=True)
         self._d2h_done = torch.cuda.Event()
         self._d2h_done.record(self.d2h)
         return HostPages(rows=rows, pages=pages)
+
+    def _pack_all(self, pages, compute):
+        """Pack every page into the device staging in one launch; returns the event after it."""
+        self.pack(pages, self.out_staging)
+        packed = torch.cuda.Event()
+        packed.record(compute)
+        return packed
 
     def _order_reuse(self, compute):
         """Order this call's writes after the previous calls' reads of the same buffers."""
@@ -241,17 +253,14 @@ class MigrationEngine:
         ready = torch.cuda.Event()
         ready.record(compute)
         self.h2d.wait_event(ready)                   # earlier unpacks read the same device staging
-        # Every sub-batch is packed first (each releases its D2H copy at once),
-        # so the source pages are free once the last pack has run; the unpacks
-        # follow on the compute stream, each behind its own H2D copy.
+        # One pack before any copy, so the source pages are free (`packed`)
+        # about half a millisecond in; the unpacks follow on the compute
+        # stream, each behind its own H2D copy.
+        all_packed = self._pack_all(pages, compute)
+        self.d2h.wait_event(all_packed)
         arrivals = []
         for start in range(0, len(pages), self.sub_batch):
-            sources = pages[start:start + self.sub_batch]
-            span = rows[start:start + len(sources)]
-            self.pack(sources, self.out_staging, start)
-            packed = torch.cuda.Event()
-            packed.record(compute)
-            self.d2h.wait_event(packed)
+            span = rows[start:start + self.sub_batch]
             with torch.cuda.stream(self.d2h):
                 self._copy_rows(span, self.out_staging, start, to_host=True)
                 copied = torch.cuda.Event()
@@ -262,8 +271,6 @@ class MigrationEngine:
                 landed = torch.cuda.Event()
                 landed.record(self.h2d)
             arrivals.append((start, landed))
-        all_packed = torch.cuda.Event()
-        all_packed.record(compute)
         for start, landed in arrivals:
             compute.wait_event(landed)
             self.unpack(destinations[start:start + self.sub_batch], self.in_staging, start)

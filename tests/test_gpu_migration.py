@@ -73,10 +73,34 @@ def test_round_trip_is_byte_exact_and_pack_matches_oracle(gpu, coracle, sub_batc
         pool.close()
 
 
+def test_pack_and_unpack_take_a_device_tensor_of_pages(gpu):
+    layout = BlockMajorLayout(blocks=16, **BLOCK)
+    pool = PagedKVPool(layout, device=0)
+    try:
+        pages = [3, 7, 1, 12]
+        pool.allocate(pages + [5, 9])
+        fill(pool, pages, 2)
+        engine = MigrationEngine(pool, max_pages=4)
+        by_list, by_tensor = torch.zeros_like(engine.out_staging), torch.zeros_like(engine.out_staging)
+        engine.pack(pages, by_list)
+        engine.pack(torch.tensor(pages, device=pool.device), by_tensor)
+        torch.cuda.synchronize()
+        assert torch.equal(by_list, by_tensor)
+        for i, page in enumerate(pages):
+            assert torch.equal(by_list[i], pool.page_view(page))
+        engine.unpack(torch.tensor([5, 9], device=pool.device), by_list, start=1)   # staging rows 1, 2: pages 7, 1
+        engine.pack(torch.empty(0, dtype=torch.int64, device=pool.device), by_tensor)   # nothing to do
+        torch.cuda.synchronize()
+        assert torch.equal(pool.page_view(5), pool.page_view(7)) and torch.equal(pool.page_view(9), pool.page_view(1))
+        assert torch.equal(by_list, by_tensor)
+    finally:
+        pool.close()
+
+
 @pytest.mark.parametrize("sub_batch", [3, 64])
 def test_trim_after_packed_event_overlaps_the_copies(gpu, sub_batch):
     # The sources are released and their chunks unmapped once the round trip's
-    # packs have run (host waits on the `packed` event only), while the D2H,
+    # pack has run (host waits on the `packed` event only), while the D2H,
     # H2D and unpacks queued behind them are still in flight; every target
     # page must still receive its source bytes.
     layout = BlockMajorLayout(blocks=64, **BLOCK)
