@@ -22,8 +22,6 @@ kernel reads through its device mapping. There is no CPU fallback.
 import ctypes as ct
 from math import prod
 
-import torch
-
 from elastic_kv import _native
 
 from .profile_ranges import profile_range
