@@ -1370,6 +1370,10 @@ def run_composite(torch, args, device):
     misses_per_step = statistics.mean(promoted[args.warmup:])
     gather_bytes = lanes * 2 * row_bytes * 2 + lanes * 4             # every lane resident after promotion
     promote_bytes = misses_per_step * 2 * row_bytes
+    # Swap-in, per (layer, request): the C int32 stamps read and written back and the K lookup slots read; per miss
+    # its list entry, Top-K id, host row and victim's token read, the patched slot, the victim's token, the two int16
+    # table entries, the two summary words and the two promotion entries written (44 B).
+    swap_bytes = L * R * (8 * C + 4 * K + 4) + misses_per_step * 44
     log(f"step {mean['step_ms']:.1f} ms = remap {mean['remap_ms']:.1f} + lookup {mean['lookup_ms']:.3f} + swap "
         f"{mean['swap_ms']:.3f} + promote {mean['promote_ms']:.2f} + gather {mean['gather_ms']:.2f} ms; "
         f"{misses_per_step / lanes:.3f} of lanes promoted; verified {verified}")
@@ -1382,6 +1386,9 @@ def run_composite(torch, args, device):
     extra = {"verified_against_host_copy": verified, "phase_ms": {k: round(v, 3) for k, v in mean.items()},
              "promoted_rows_per_step": round(misses_per_step), "promoted_fraction": round(misses_per_step / lanes, 4),
              "promote_gbs_over_pcie": round(promote_bytes / (mean["promote_ms"] / 1e3) / 1e9, 2),
+             "swap_in": {"algorithmic_bytes": round(swap_bytes),
+                         "gbs": round(swap_bytes / (mean["swap_ms"] / 1e3) / 1e9, 1),
+                         "frac_of_hbm_peak": round(swap_bytes / (mean["swap_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4)},
              "lookups_per_s": round(lanes / (mean["lookup_ms"] / 1e3), 1),
              "step_ms_without_remap": round(mean["step_ms"] - mean["remap_ms"], 3),
              "remap_parts_ms": {k: round(statistics.mean(v[args.warmup:] or v), 2) if v else 0.0
@@ -1432,7 +1439,8 @@ def summary(result):
     keys = ("metric", "value", "unit", "ms_per_step", "roofline", "cpu_baseline", "config", "lookup_us_per_step",
             "hit_rate", "verified_round_trip", "tick_ms", "link_gbs", "pack_gbs", "unpack_gbs", "phase_ms",
             "higher_is_better", "vs_baseline", "per_batch", "correct", "verified_against_host_copy",
-            "step_ms_without_remap", "remap_parts_ms", "promote_gbs_over_pcie", "graph_replay", "per_support_set")
+            "step_ms_without_remap", "remap_parts_ms", "promote_gbs_over_pcie", "swap_in", "graph_replay",
+            "per_support_set")
     return {key: result[key] for key in keys if key in result}
 
 
