@@ -1656,40 +1656,11 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
     return 0;
 }
 
-// One wave turns 64 consecutive table entries into two bitmap words with a
-// ballot; a grid-stride loop covers every (layer, row, 64-entry group).
-template <typename TableT>
-__global__ __launch_bounds__(kThreads) void residency_bits_kernel(const TableT* __restrict__ table, int64_t t_sl,
-                                                                  int64_t t_sr, int64_t t_sc, int64_t rows,
-                                                                  int64_t cols, int32_t* __restrict__ bits,
-                                                                  int64_t b_sl, int64_t b_sr, int64_t b_sw,
-                                                                  int64_t groups_per_row, int64_t total_groups) {
-    const int lane = threadIdx.x & 63;
-    const int64_t waves = int64_t{gridDim.x} * (kThreads / 64);
-    for (int64_t g = int64_t{blockIdx.x} * (kThreads / 64) + (threadIdx.x >> 6); g < total_groups; g += waves) {
-        const int64_t group = g % groups_per_row;
-        const int64_t row_index = g / groups_per_row;   // layer * rows + row
-        const int64_t layer = row_index / rows;
-        const int64_t row = row_index - layer * rows;
-        const int64_t pos = group * 64 + lane;
-        const bool in_row = pos < cols;
-        const int64_t at = in_row ? pos : 0;
-        const bool set = in_row && table[layer * t_sl + row * t_sr + at * t_sc] != 0;
-        const uint64_t mask = __ballot(set);
-        int32_t* out = bits + layer * b_sl + row * b_sr;
-        const int64_t word = group * 2;
-        if (lane == 0) {
-            out[word * b_sw] = static_cast<int32_t>(static_cast<uint32_t>(mask));
-        } else if (lane == 1 && group * 64 + 32 < cols) {
-            out[(word + 1) * b_sw] = static_cast<int32_t>(static_cast<uint32_t>(mask >> 32));
-        }
-    }
-}
-
-// Summary rows of a shift > 0: one wave per summary word covers the
-// 32 << shift positions of its 32 groups, 64 consecutive entries per
-// iteration (coalesced), each lane OR-ing the bit of its entry's group; the
-// wave's bits are OR-reduced and lane 0 writes the word.
+// Summary rows of any layout (strided entries, rows that do not come in
+// whole 16-byte pieces): one wave per summary word covers the 32 << shift
+// positions of its 32 groups, 64 consecutive entries per iteration, each lane
+// OR-ing the bit of its entry's group; the wave's bits are OR-reduced and
+// lane 0 writes the word (0 for the padding words past the summary).
 template <typename TableT>
 __global__ __launch_bounds__(kThreads) void residency_summary_kernel(
     const TableT* __restrict__ table, int64_t t_sl, int64_t t_sr, int64_t t_sc, int64_t rows, int64_t cols,
@@ -1719,6 +1690,110 @@ __global__ __launch_bounds__(kThreads) void residency_summary_kernel(
     }
 }
 
+// Nonzero entries of one 16-byte piece of a table row: bit k = entry k.
+template <typename TableT>
+__device__ inline uint32_t piece_nonzero(const uint4 v) {
+    if constexpr (sizeof(TableT) == 2) {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        uint32_t bits = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            bits |= static_cast<uint32_t>((w[i] & 0xffffu) != 0) << (2 * i);
+            bits |= static_cast<uint32_t>((w[i] >> 16) != 0) << (2 * i + 1);
+        }
+        return bits;
+    } else if constexpr (sizeof(TableT) == 4) {
+        return static_cast<uint32_t>(v.x != 0) | (static_cast<uint32_t>(v.y != 0) << 1) |
+               (static_cast<uint32_t>(v.z != 0) << 2) | (static_cast<uint32_t>(v.w != 0) << 3);
+    } else {
+        return static_cast<uint32_t>((v.x | v.y) != 0) | (static_cast<uint32_t>((v.z | v.w) != 0) << 1);
+    }
+}
+
+// Group bits of a piece's n entry bits: bit i = any of entries
+// [i << shift, (i + 1) << shift); one bit when a group spans the piece.
+__device__ inline uint32_t fold_groups(uint32_t bits, uint32_t n, uint32_t shift) {
+    if ((1u << shift) >= n) {
+        return bits != 0 ? 1u : 0u;
+    }
+    const uint32_t mask = (1u << (1u << shift)) - 1;   // shift <= 2 here: groups of 1, 2 or 4 entries
+    uint32_t out = 0;
+    for (uint32_t i = 0; i < (n >> shift); ++i) {
+        out |= static_cast<uint32_t>(((bits >> (i << shift)) & mask) != 0) << i;
+    }
+    return out;
+}
+
+// Summary words of contiguous rows that come in whole 16-byte pieces (T a
+// multiple of 16 / sizeof(entry), 16-byte aligned rows). A word's
+// 32 << shift positions are ppw = (32 << shift) / E pieces of E entries; a
+// segment of seg = min(ppw, 64) lanes builds it, each lane loading every
+// seg-th piece with one 16-byte load and OR-ing that piece's group bits into
+// place; shuffles over seg/2, ..., 1 lanes OR the segment and its first lane
+// writes the word. A wave takes kSets groups of 64 / seg consecutive words per
+// iteration (for ppw <= 64: kSets contiguous KiB, one 1 KiB load instruction
+// each, all in flight before any is used) and strides over every word of every
+// (layer, row), padding words included (written 0).
+constexpr int kSummarySets = 4;
+
+template <typename TableT>
+__global__ __launch_bounds__(kThreads) void residency_pieces_kernel(
+    const TableT* __restrict__ table, int64_t t_sl, int64_t t_sr, FastDiv rows_div, int64_t cols,
+    int32_t* __restrict__ bits, int64_t b_sl, int64_t b_sr, int64_t b_sw, FastDiv words_div, uint32_t total_words,
+    uint32_t shift, uint32_t seg_log2, uint32_t per_lane) {
+    constexpr uint32_t kE = 16 / sizeof(TableT);
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t in_seg = lane & ((1u << seg_log2) - 1);
+    const uint32_t words_per_wave = 64u >> seg_log2;
+    const uint32_t wave = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const uint32_t step = gridDim.x * (kThreads / 64) * words_per_wave * kSummarySets;
+    for (uint32_t first = wave * words_per_wave * kSummarySets; first < total_words; first += step) {
+        const TableT* entries[kSummarySets];
+        int64_t word_first[kSummarySets], out_at[kSummarySets];
+        bool live[kSummarySets];
+        uint32_t acc[kSummarySets];
+#pragma unroll
+        for (int k = 0; k < kSummarySets; ++k) {
+            const uint32_t gw = first + k * words_per_wave + (lane >> seg_log2);
+            live[k] = gw < total_words;
+            const uint32_t row_index = words_div.div(live[k] ? gw : 0);   // layer * rows + row
+            const uint32_t word = (live[k] ? gw : 0) - row_index * words_div.divisor;
+            const uint32_t layer = rows_div.div(row_index);
+            const uint32_t row = row_index - layer * rows_div.divisor;
+            entries[k] = table + layer * t_sl + row * t_sr;
+            word_first[k] = static_cast<int64_t>(word) << (5 + shift);
+            out_at[k] = layer * b_sl + row * b_sr + int64_t{word} * b_sw;
+            acc[k] = 0;
+        }
+        for (uint32_t j = 0; j < per_lane; ++j) {
+            const uint32_t piece = in_seg + (j << seg_log2);
+            uint4 v[kSummarySets];
+            bool in[kSummarySets];
+#pragma unroll
+            for (int k = 0; k < kSummarySets; ++k) {
+                const int64_t pos = word_first[k] + int64_t{piece} * kE;
+                in[k] = live[k] && pos < cols;
+                v[k] = in[k] ? *reinterpret_cast<const uint4*>(entries[k] + pos) : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int k = 0; k < kSummarySets; ++k) {
+                if (in[k]) {
+                    acc[k] |= fold_groups(piece_nonzero<TableT>(v[k]), kE, shift) << ((piece * kE) >> shift);
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kSummarySets; ++k) {
+            for (uint32_t offset = (1u << seg_log2) >> 1; offset > 0; offset >>= 1) {
+                acc[k] |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(acc[k]), static_cast<int>(offset)));
+            }
+            if (live[k] && in_seg == 0) {
+                bits[out_at[k]] = static_cast<int32_t>(acc[k]);
+            }
+        }
+    }
+}
+
 template <typename TableT>
 void launch_residency_bits(const ekv_tensor& table, const ekv_tensor& bits, int d, int64_t layers, int64_t rows,
                            int64_t cols, int64_t shift, hipStream_t s) {
@@ -1726,21 +1801,32 @@ void launch_residency_bits(const ekv_tensor& table, const ekv_tensor& bits, int 
     const int64_t t_sl = layered ? table.stride[0] : 0, b_sl = layered ? bits.stride[0] : 0;
     const auto* entries = static_cast<const TableT*>(table.data);
     auto* out = static_cast<int32_t*>(bits.data);
-    if (shift == 0) {
-        const int64_t groups_per_row = (cols + 63) / 64;
-        const int64_t total = layers * rows * groups_per_row;
-        const int64_t blocks = std::min<int64_t>((total + 3) / 4, 65536);
-        residency_bits_kernel<TableT><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, s>>>(
-            entries, t_sl, table.stride[d], table.stride[d + 1], rows, cols, out, b_sl, bits.stride[d],
-            bits.stride[d + 1], groups_per_row, total);
-    } else {
-        const int64_t words_per_row = summary_words(cols, shift);
-        const int64_t total = layers * rows * words_per_row;
-        const int64_t blocks = std::min<int64_t>((total + 3) / 4, 65536);
-        residency_summary_kernel<TableT><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, s>>>(
-            entries, t_sl, table.stride[d], table.stride[d + 1], rows, cols, out, b_sl, bits.stride[d],
-            bits.stride[d + 1], words_per_row, total, static_cast<uint32_t>(shift));
+    const int64_t words_per_row = summary_words(cols, shift);
+    const int64_t total = layers * rows * words_per_row;
+    constexpr int64_t kE = 16 / static_cast<int64_t>(sizeof(TableT));
+    const auto piece_aligned = [](int64_t elements) { return (elements * static_cast<int64_t>(sizeof(TableT))) % 16 == 0; };
+    const bool pieces = table.stride[d + 1] == 1 && cols % kE == 0 &&
+                        (reinterpret_cast<uintptr_t>(table.data) & 15) == 0 && piece_aligned(table.stride[d]) &&
+                        (!layered || piece_aligned(t_sl)) && total < (int64_t{1} << 31);
+    if (pieces) {
+        const int64_t ppw = (int64_t{32} << shift) / kE;   // pieces per summary word (a power of two >= 2)
+        uint32_t seg_log2 = 0;
+        while ((int64_t{1} << seg_log2) < std::min<int64_t>(ppw, 64)) {
+            ++seg_log2;
+        }
+        const int64_t per_lane = ppw >> seg_log2;
+        const int64_t words_per_block = (kThreads / 64) * (64 >> seg_log2) * kSummarySets;
+        const int64_t blocks = std::min<int64_t>((total + words_per_block - 1) / words_per_block, 65536);
+        residency_pieces_kernel<TableT><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, s>>>(
+            entries, t_sl, table.stride[d], FastDiv(static_cast<uint32_t>(rows)), cols, out, b_sl, bits.stride[d],
+            bits.stride[d + 1], FastDiv(static_cast<uint32_t>(words_per_row)), static_cast<uint32_t>(total),
+            static_cast<uint32_t>(shift), seg_log2, static_cast<uint32_t>(per_lane));
+        return;
     }
+    const int64_t blocks = std::min<int64_t>((total + 3) / 4, 65536);
+    residency_summary_kernel<TableT><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, s>>>(
+        entries, t_sl, table.stride[d], table.stride[d + 1], rows, cols, out, b_sl, bits.stride[d],
+        bits.stride[d + 1], words_per_row, total, static_cast<uint32_t>(shift));
 }
 
 int residency_bits(const ekv_tensor* table_p, const ekv_tensor* bits_p, int64_t shift, void* stream) {

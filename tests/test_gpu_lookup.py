@@ -144,6 +144,44 @@ def test_shape_errors_raise(gpu):
                          torch.zeros((1, 2, 8), dtype=torch.int64, device=gpu), 2)
 
 
+@pytest.mark.parametrize("dtype", [torch.int16, torch.int32, torch.int64])
+def test_residency_summary_matches_oracle_on_every_layout(gpu, dtype):
+    # Rows in whole 16-byte pieces take the vectorized kernel; ragged, strided
+    # and misaligned tables the general one. Both must write the oracle's
+    # words over whatever the output held and leave the padding words past
+    # them as they were.
+    from adaptive_sparse.resident_lookup import build_residency_bits, summary_words
+    from oracle import oracle as ref
+
+    rng = np.random.default_rng(300 + dtype.itemsize)
+    per_piece = 16 // dtype.itemsize
+    for case in range(48):
+        shift = int(rng.choice([0, 1, 2, 3, 4, 5, 6, 7, 9, 12, 20]))
+        layered = bool(rng.random() < 0.5)
+        layers, rows = int(rng.integers(1, 4)), int(rng.integers(1, 5))
+        cols = per_piece * int(rng.integers(1, 900)) if rng.random() < 0.7 else int(rng.integers(1, 5000))
+        shape = (layers, rows, cols) if layered else (rows, cols)
+        table = rng.integers(-5, 100, size=shape)
+        table[rng.random(shape) < rng.random()] = 0
+        form = int(rng.integers(0, 4))   # 0, 1: contiguous; 2: strided entries; 3: one entry off the alignment
+        if form == 2:
+            view = strided(table, dtype, gpu)
+        elif form == 3:
+            backing = torch.zeros((*shape[:-1], cols + 1), dtype=dtype, device=gpu)
+            view = backing[..., 1:]
+            view.copy_(torch.tensor(table, dtype=dtype, device=gpu))
+        else:
+            view = torch.tensor(table, dtype=dtype, device=gpu)
+        before = rng.integers(-(1 << 31), 1 << 31, size=(*shape[:-1], summary_words(cols, shift))).astype(np.int32)
+        out = torch.tensor(before, device=gpu)
+        build_residency_bits(view, out=out, shift=shift)
+        want = ref.residency_bits(table, shift)
+        got = out.cpu().numpy()
+        words = want.shape[-1]
+        assert np.array_equal(got[..., :words], want), (case, shape, shift, form)
+        assert np.array_equal(got[..., words:], before[..., words:]), (case, shape, shift, form)
+
+
 @pytest.mark.parametrize("layered", [False, True])
 @pytest.mark.parametrize("bs", [1, 3])
 def test_bitmap_lookup_equals_plain_lookup_and_oracle(gpu, coracle, layered, bs):
