@@ -24,11 +24,12 @@
 // (an LDS hash of the miss tokens names each token's first miss), and its
 // later lanes share that slot and record empty promotions.
 //
-// One 256-thread workgroup per (row, layer): hits are touched in LDS, the
-// (stamp, slot) keys are bitonic-sorted (held in registers between LDS
-// transposes for hot buffers of 2049-8192 slots, in LDS below), then each victim clears its
-// old token from the token->slot table and residency summary, takes the new
-// token, and writes one promotion (host row -> global slot) record. The
+// One 256-thread workgroup per (row, layer): hits are touched in LDS, a
+// radix select over the stamps picks the victims (the smallest (stamp, slot)
+// keys) and a bitonic network in LDS orders just them, then each victim
+// clears its old token from the token->slot table and residency summary,
+// takes the new token, and writes one promotion (host row -> global slot)
+// record. The
 // lookup's slot output of every miss lane is patched to its new slot, so the
 // gather that follows reads the promoted row.
 //
@@ -49,9 +50,9 @@ namespace ekv {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kMaxCapacity = 8192;   // slots per hot buffer sortable in LDS
+constexpr int kMaxCapacity = 8192;   // slots per hot buffer (stamps held in LDS; 16-bit scan fields)
 constexpr int kMaxWidth = 4096;      // lanes per row whose miss tokens are hashed in LDS
-constexpr int kSortPairs = kMaxCapacity / 2 / kThreads;   // compare-exchanges per thread and pass
+constexpr int kSortPairs = kMaxWidth / 2 / kThreads;   // compare-exchanges per thread and pass (victim sort)
 constexpr int32_t kStatusStampOverflow = EKV_SWAP_STAMP_OVERFLOW;
 constexpr int32_t kStatusSharedRequest = EKV_SWAP_SHARED_REQUEST;
 
@@ -85,7 +86,7 @@ struct SwapArgs {
     int64_t ps_l, ps_b, ps_o;
     int32_t* promote_dst;           // [L, B, W] global slot per promotion
     int64_t pd_l, pd_b, pd_o;
-    int64_t batch, table_rows, capacity, capacity_pow2;
+    int64_t batch, table_rows, capacity;
     uint32_t width;
     int64_t step;
     const int64_t* step_counter;    // when set, the step is read from device memory (graph replays)
@@ -142,102 +143,10 @@ __device__ __forceinline__ uint32_t token_hash(int32_t token, uint32_t log2_size
     return (static_cast<uint32_t>(token) * 2654435761u) >> (32 - log2_size);
 }
 
-// Register-resident bitonic sort of n = kThreads * R keys (R = 2^LB). Each
-// thread holds R keys whose indices differ only in a window of LB index
-// bits; the network's compare-exchanges along a bit of the window run in
-// registers, and the keys move to another window through LDS (padded by one
-// entry per R, so that a thread's writes at stride R spread over the banks).
-// The windows start at bits 0, LB and log2(n) - LB; for the falling bit of
-// each merge stage the lowest window holding it is taken. On return
-// keys[0 .. n) holds the keys in ascending order.
-template <int R, int LB>
-struct RegisterSort {
-    static constexpr uint32_t kBits = LB + 8;   // log2 n with kThreads = 256 threads
-
-    __device__ __forceinline__ static uint32_t index(uint32_t t, int r, uint32_t s) {
-        return (t & ((1u << s) - 1u)) | (static_cast<uint32_t>(r) << s) | ((t >> s) << (s + LB));
-    }
-    __device__ __forceinline__ static uint32_t padded(uint32_t i) { return i + (i >> LB); }
-    __device__ __forceinline__ static uint32_t window_for(uint32_t bit) {
-        return bit < LB ? 0u : (bit < 2 * LB ? static_cast<uint32_t>(LB) : kBits - LB);
-    }
-
-    template <int Q>
-    __device__ __forceinline__ static void exchange(uint64_t (&v)[R], uint32_t t, uint32_t s, uint32_t k) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if ((r >> Q) & 1) {
-                continue;
-            }
-            const bool up = (index(t, r, s) & k) == 0;
-            const uint64_t x = v[r], y = v[r | (1 << Q)];
-            const bool swap = (x > y) == up;
-            v[r] = swap ? y : x;
-            v[r | (1 << Q)] = swap ? x : y;
-        }
-    }
-
-    // The exchanges along bits top, top - 1, .., s of the window that starts at s, in that
-    // order (the bit of each is fixed at compile time, so the keys stay in registers).
-    template <int Q>
-    __device__ __forceinline__ static void exchange_down(uint64_t (&v)[R], uint32_t t, uint32_t s, uint32_t top,
-                                                         uint32_t k) {
-        if (s + Q <= top) {
-            exchange<Q>(v, t, s, k);
-        }
-        if constexpr (Q > 0) {
-            exchange_down<Q - 1>(v, t, s, top, k);
-        }
-    }
-
-    __device__ __forceinline__ static void relayout(uint64_t (&v)[R], uint64_t* lds, uint32_t t, uint32_t from, uint32_t to) {
-        __syncthreads();   // every thread has read the previous layout
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            lds[padded(index(t, r, from))] = v[r];
-        }
-        __syncthreads();
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            v[r] = lds[padded(index(t, r, to))];
-        }
-    }
-
-    template <typename KeyOf>
-    __device__ __forceinline__ static void sort(uint64_t* lds, KeyOf key_of) {
-        const uint32_t t = threadIdx.x;
-        uint64_t v[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            v[r] = key_of(index(t, r, 0));
-        }
-        uint32_t s = 0;   // start of the window in registers (uniform)
-        for (uint32_t stage = 1; stage <= kBits; ++stage) {
-            const uint32_t k = 1u << stage;
-            // Merge along bits stage - 1 .. 0, one window at a time from the top.
-            for (int32_t top = static_cast<int32_t>(stage) - 1; top >= 0; top = static_cast<int32_t>(s) - 1) {
-                const uint32_t w = window_for(static_cast<uint32_t>(top));
-                if (w != s) {
-                    relayout(v, lds, t, s, w);
-                    s = w;
-                }
-                exchange_down<LB - 1>(v, t, s, static_cast<uint32_t>(top), k);
-            }
-        }
-        __syncthreads();   // every thread has read the last padded layout
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            lds[index(t, r, s)] = v[r];
-        }
-        __syncthreads();
-    }
-};
-
 // Dynamic LDS of one workgroup (C = capacity, W = lanes per row):
-//   region   max(8 * pow2(C) (+ 2 KiB of padding for the register sort), 4 * hash_size)
-//            bytes, used three times over:
-//            touch[C] (first hit lane per slot), then the miss-token hash
-//            (miss indices), then the (stamp, slot) sort keys;
+//   region   max(4 * C, 4 * hash_size, 8 * pow2(W)) bytes, used three times
+//            over: touch[C] (first hit lane per slot), then the miss-token
+//            hash (miss indices), then the victims' (stamp, slot) keys;
 //   stamp    [C] recency stamps;
 //   info     [W] token of miss i, later the rank of miss i among the owners;
 //   owner    [W] the first miss of the same token (-1: an entry naming no
@@ -245,6 +154,8 @@ struct RegisterSort {
 __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
     extern __shared__ unsigned char shared[];
     __shared__ int32_t wave_totals[kThreads / 64];
+    __shared__ int32_t digit_count[256];   // radix-select histogram of one 8-bit digit
+    __shared__ int32_t chosen[2];          // the digit holding the need-th key, and the keys below it
     uint64_t* keys = reinterpret_cast<uint64_t*>(shared);
     int32_t* touch = reinterpret_cast<int32_t*>(shared);
     int32_t* hash = reinterpret_cast<int32_t*>(shared);
@@ -389,25 +300,72 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
             info[i] = owner[i] == i ? rank++ : -1;
         }
         // The `unique` victims: the smallest (stamp, slot) keys, empty slots
-        // (INT32_MIN) first, then the least recently used.
-        const auto key_of = [&](uint32_t s) {
-            return s < C ? (static_cast<uint64_t>(static_cast<uint32_t>(stamp[s]) ^ 0x80000000u) << 32) |
-                               static_cast<uint64_t>(s)
-                         : ~uint64_t{0};
-        };
-        const uint32_t n = static_cast<uint32_t>(a.capacity_pow2);
-        if (n == 4096) {
-            RegisterSort<16, 4>::sort(keys, key_of);
-        } else if (n == 8192) {
-            RegisterSort<32, 5>::sort(keys, key_of);
-        } else {
-            for (uint32_t s = threadIdx.x; s < n; s += kThreads) {
-                keys[s] = key_of(s);
+        // (INT32_MIN) first, then the least recently used. A radix select
+        // over the order-preserving unsigned form of the stamps (four 8-bit
+        // digits, most significant first) finds the stamp value T of the
+        // unique-th smallest key and how many keys at T it takes; one scan in
+        // slot order then gathers the slots below T and the first of those at
+        // T into the key region, and a bitonic network sorts just them.
+        const auto ordered = [&](uint32_t s) { return static_cast<uint32_t>(stamp[s]) ^ 0x80000000u; };
+        if (unique > 0) {   // uniform: with no victim to choose, the keys are never read
+            uint32_t prefix = 0, prefix_mask = 0;
+            int32_t need = unique;   // keys still to take among those matching the prefix (uniform)
+            for (int shift = 24; shift >= 0; shift -= 8) {
+                digit_count[threadIdx.x] = 0;   // kThreads == 256 digits
+                __syncthreads();
+                for (uint32_t s = threadIdx.x; s < C; s += kThreads) {
+                    const uint32_t v = ordered(s);
+                    if ((v & prefix_mask) == prefix) {
+                        atomicAdd(&digit_count[(v >> shift) & 255u], 1);
+                    }
+                }
+                __syncthreads();
+                const int32_t here = digit_count[threadIdx.x];
+                int32_t matching = 0;
+                const int32_t below = workgroup_exclusive_scan(here, wave_totals, matching);
+                if (below < need && need <= below + here) {   // exactly one digit holds the need-th key
+                    chosen[0] = static_cast<int32_t>(threadIdx.x);
+                    chosen[1] = below;
+                }
+                __syncthreads();
+                prefix |= static_cast<uint32_t>(chosen[0]) << shift;
+                prefix_mask |= 255u << shift;
+                need -= chosen[1];
+            }
+            // Slot s is a victim when v < T, or v == T and fewer than `need`
+            // slots below s hold T. Each thread scans a contiguous run of slots;
+            // the counts of both kinds travel packed in one scan (16 bits each).
+            const uint32_t per_slot_run = (static_cast<uint32_t>(C) + kThreads - 1) / kThreads;
+            const uint32_t slot_begin = min(static_cast<uint32_t>(C), threadIdx.x * per_slot_run);
+            const uint32_t slot_end = min(static_cast<uint32_t>(C), slot_begin + per_slot_run);
+            int32_t packed = 0;
+            for (uint32_t s = slot_begin; s < slot_end; ++s) {
+                const uint32_t v = ordered(s);
+                packed += v < prefix ? (1 << 16) : (v == prefix ? 1 : 0);
+            }
+            int32_t packed_total = 0;
+            const int32_t packed_before = workgroup_exclusive_scan(packed, wave_totals, packed_total);
+            int32_t lower = packed_before >> 16, ties = packed_before & 0xffff;
+            for (uint32_t s = slot_begin; s < slot_end; ++s) {
+                const uint32_t v = ordered(s);
+                if (v < prefix || (v == prefix && ties < need)) {
+                    keys[lower + min(ties, need)] = (static_cast<uint64_t>(v) << 32) | s;
+                }
+                lower += v < prefix ? 1 : 0;
+                ties += v == prefix ? 1 : 0;
+            }
+            uint32_t n = 1;
+            while (n < static_cast<uint32_t>(unique)) {
+                n <<= 1;
+            }
+            for (uint32_t s = unique + threadIdx.x; s < n; s += kThreads) {
+                keys[s] = ~uint64_t{0};
             }
             __syncthreads();
-            // Bitonic network in LDS: in each pass every thread takes the compare-exchanges
-            // p = threadIdx.x + q * kThreads (the pair (i, i + j), i = p with a zero inserted at
-            // bit log2 j), reading all of its pairs before writing any.
+            // Bitonic network in LDS over the n victim keys: in each pass every
+            // thread takes the compare-exchanges p = threadIdx.x + q * kThreads
+            // (the pair (i, i + j), i = p with a zero inserted at bit log2 j),
+            // reading all of its pairs before writing any.
             const uint32_t pairs = n >> 1;
             for (uint32_t k = 2; k <= n; k <<= 1) {
                 for (uint32_t j = k >> 1; j > 0; j >>= 1) {
@@ -650,10 +608,6 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
     a.batch = B;
     a.table_rows = R;
     a.capacity = C;
-    a.capacity_pow2 = 1;
-    while (a.capacity_pow2 < C) {
-        a.capacity_pow2 <<= 1;
-    }
     a.width = static_cast<uint32_t>(W);
     a.step = step;
     a.step_counter = counter;
@@ -667,11 +621,15 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
         a.hash_size <<= 1;
         ++a.hash_log2;
     }
-    // The register sort of 4096 or 8192 keys moves them through LDS padded by one entry per
-    // 16 or 32 (256 entries more).
-    const int64_t sort_entries = a.capacity_pow2 + (a.capacity_pow2 == 4096 || a.capacity_pow2 == 8192 ? 256 : 0);
-    const size_t region = std::max<size_t>(static_cast<size_t>(sort_entries) * sizeof(uint64_t),
-                                           static_cast<size_t>(a.hash_size) * sizeof(int32_t));
+    // The region holds touch[C], then the miss-token hash, then the keys of at most W victims
+    // (padded to a power of two for the sort).
+    int64_t sort_entries = 1;
+    while (sort_entries < W) {
+        sort_entries <<= 1;
+    }
+    const size_t region = std::max({static_cast<size_t>(sort_entries) * sizeof(uint64_t),
+                                    static_cast<size_t>(a.hash_size) * sizeof(int32_t),
+                                    static_cast<size_t>(C) * sizeof(int32_t)});
     a.region_bytes = static_cast<uint32_t>(region);
     const size_t lds = region + static_cast<size_t>(C) * 4 + static_cast<size_t>(W) * 8;
     if (lds > 64 * 1024) {
