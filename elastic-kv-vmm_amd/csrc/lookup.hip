@@ -1656,11 +1656,55 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
     return 0;
 }
 
-// Summary rows of any layout (strided entries, rows that do not come in
-// whole 16-byte pieces): one wave per summary word covers the 32 << shift
+// Per-position bitmaps (shift 0) of any layout: a wave turns 64 consecutive
+// entries of a row into two words with a ballot, four such groups per
+// iteration with their loads in flight together; a wave-stride loop covers
+// every (layer, row, 64-entry group).
+constexpr int kBitmapGroups = 4;
+
+template <typename TableT>
+__global__ __launch_bounds__(kThreads) void residency_bits_kernel(const TableT* __restrict__ table, int64_t t_sl,
+                                                                  int64_t t_sr, int64_t t_sc, int64_t rows,
+                                                                  int64_t cols, int32_t* __restrict__ bits,
+                                                                  int64_t b_sl, int64_t b_sr, int64_t b_sw,
+                                                                  int64_t groups_per_row, int64_t total_groups) {
+    const int lane = threadIdx.x & 63;
+    const int64_t waves = int64_t{gridDim.x} * (kThreads / 64);
+    for (int64_t g0 = (int64_t{blockIdx.x} * (kThreads / 64) + (threadIdx.x >> 6)) * kBitmapGroups;
+         g0 < total_groups; g0 += waves * kBitmapGroups) {
+        bool set[kBitmapGroups];
+        int32_t* out[kBitmapGroups];
+        int64_t group[kBitmapGroups];
+#pragma unroll
+        for (int k = 0; k < kBitmapGroups; ++k) {
+            const int64_t g = g0 + k;   // uniform over the wave
+            const bool live = g < total_groups;
+            group[k] = live ? g % groups_per_row : 0;
+            const int64_t row_index = live ? g / groups_per_row : 0;   // layer * rows + row
+            const int64_t layer = row_index / rows;
+            const int64_t row = row_index - layer * rows;
+            const int64_t pos = group[k] * 64 + lane;
+            set[k] = live && pos < cols && table[layer * t_sl + row * t_sr + pos * t_sc] != 0;
+            out[k] = live ? bits + layer * b_sl + row * b_sr : nullptr;
+        }
+#pragma unroll
+        for (int k = 0; k < kBitmapGroups; ++k) {
+            const uint64_t mask = __ballot(set[k]);
+            const int64_t word = group[k] * 2;
+            if (out[k] != nullptr && lane == 0) {
+                out[k][word * b_sw] = static_cast<int32_t>(static_cast<uint32_t>(mask));
+            } else if (out[k] != nullptr && lane == 1 && group[k] * 64 + 32 < cols) {
+                out[k][(word + 1) * b_sw] = static_cast<int32_t>(static_cast<uint32_t>(mask >> 32));
+            }
+        }
+    }
+}
+
+// Summary rows (shift > 0) of any layout (strided entries, rows that do not
+// come in whole 16-byte pieces): one wave per summary word covers the 32 << shift
 // positions of its 32 groups, 64 consecutive entries per iteration, each lane
 // OR-ing the bit of its entry's group; the wave's bits are OR-reduced and
-// lane 0 writes the word (0 for the padding words past the summary).
+// lane 0 writes the word.
 template <typename TableT>
 __global__ __launch_bounds__(kThreads) void residency_summary_kernel(
     const TableT* __restrict__ table, int64_t t_sl, int64_t t_sr, int64_t t_sc, int64_t rows, int64_t cols,
@@ -1730,10 +1774,10 @@ __device__ inline uint32_t fold_groups(uint32_t bits, uint32_t n, uint32_t shift
 // segment of seg = min(ppw, 64) lanes builds it, each lane loading every
 // seg-th piece with one 16-byte load and OR-ing that piece's group bits into
 // place; shuffles over seg/2, ..., 1 lanes OR the segment and its first lane
-// writes the word. A wave takes kSets groups of 64 / seg consecutive words per
-// iteration (for ppw <= 64: kSets contiguous KiB, one 1 KiB load instruction
-// each, all in flight before any is used) and strides over every word of every
-// (layer, row), padding words included (written 0).
+// writes the word. A wave takes kSummarySets groups of 64 / seg consecutive words per
+// iteration (for ppw <= 64: kSummarySets contiguous KiB, one 1 KiB load instruction
+// each, all in flight before any is used) and strides over every summary word
+// of every (layer, row).
 constexpr int kSummarySets = 4;
 
 template <typename TableT>
@@ -1821,6 +1865,15 @@ void launch_residency_bits(const ekv_tensor& table, const ekv_tensor& bits, int 
             entries, t_sl, table.stride[d], FastDiv(static_cast<uint32_t>(rows)), cols, out, b_sl, bits.stride[d],
             bits.stride[d + 1], FastDiv(static_cast<uint32_t>(words_per_row)), static_cast<uint32_t>(total),
             static_cast<uint32_t>(shift), seg_log2, static_cast<uint32_t>(per_lane));
+        return;
+    }
+    if (shift == 0) {
+        const int64_t groups_per_row = (cols + 63) / 64;
+        const int64_t groups = layers * rows * groups_per_row;
+        const int64_t blocks = std::min<int64_t>((groups + 4 * kBitmapGroups - 1) / (4 * kBitmapGroups), 65536);
+        residency_bits_kernel<TableT><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, s>>>(
+            entries, t_sl, table.stride[d], table.stride[d + 1], rows, cols, out, b_sl, bits.stride[d],
+            bits.stride[d + 1], groups_per_row, groups);
         return;
     }
     const int64_t blocks = std::min<int64_t>((total + 3) / 4, 65536);
