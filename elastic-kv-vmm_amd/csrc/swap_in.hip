@@ -313,11 +313,25 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
             for (int shift = 24; shift >= 0; shift -= 8) {
                 digit_count[threadIdx.x] = 0;   // kThreads == 256 digits
                 __syncthreads();
+                // Runs of one digit in a thread's slots count with one atomic:
+                // recent stamps share their high digits, which would otherwise
+                // serialize thousands of atomics on one counter.
+                uint32_t run_digit = 0;
+                int32_t run = 0;
                 for (uint32_t s = threadIdx.x; s < C; s += kThreads) {
                     const uint32_t v = ordered(s);
                     if ((v & prefix_mask) == prefix) {
-                        atomicAdd(&digit_count[(v >> shift) & 255u], 1);
+                        const uint32_t d = (v >> shift) & 255u;
+                        if (run > 0 && d != run_digit) {
+                            atomicAdd(&digit_count[run_digit], run);
+                            run = 0;
+                        }
+                        run_digit = d;
+                        ++run;
                     }
+                }
+                if (run > 0) {
+                    atomicAdd(&digit_count[run_digit], run);
                 }
                 __syncthreads();
                 const int32_t here = digit_count[threadIdx.x];
