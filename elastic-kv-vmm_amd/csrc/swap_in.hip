@@ -52,7 +52,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kMaxCapacity = 8192;   // slots per hot buffer (stamps held in LDS; 16-bit scan fields)
 constexpr int kMaxWidth = 4096;      // lanes per row whose miss tokens are hashed in LDS
-constexpr int kSortPairs = kMaxWidth / 2 / kThreads;   // compare-exchanges per thread and pass (victim sort)
 constexpr int32_t kStatusStampOverflow = EKV_SWAP_STAMP_OVERFLOW;
 constexpr int32_t kStatusSharedRequest = EKV_SWAP_SHARED_REQUEST;
 
@@ -141,6 +140,40 @@ __device__ __forceinline__ int32_t workgroup_exclusive_scan(int32_t value, int32
 
 __device__ __forceinline__ uint32_t token_hash(int32_t token, uint32_t log2_size) {
     return (static_cast<uint32_t>(token) * 2654435761u) >> (32 - log2_size);
+}
+
+// Ascending bitonic sort of keys[0 .. n) in LDS (n a power of two, at most
+// 2 * Q * kThreads). In each pass every thread takes the compare-exchanges
+// p = threadIdx.x + q * kThreads, q < Q (the pair (i, i + j), i = p with a
+// zero inserted at bit log2 j), reading all of its pairs before writing any.
+// Every thread must call it.
+template <int Q>
+__device__ void sort_victims(uint64_t* keys, uint32_t n) {
+    const uint32_t pairs = n >> 1;
+    for (uint32_t k = 2; k <= n; k <<= 1) {
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            uint64_t first_key[Q], second_key[Q];
+#pragma unroll
+            for (int q = 0; q < Q; ++q) {
+                const uint32_t p = threadIdx.x + q * kThreads;
+                const uint32_t i = ((p & ~(j - 1)) << 1) | (p & (j - 1));
+                if (p < pairs) {
+                    first_key[q] = keys[i];
+                    second_key[q] = keys[i + j];
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < Q; ++q) {
+                const uint32_t p = threadIdx.x + q * kThreads;
+                const uint32_t i = ((p & ~(j - 1)) << 1) | (p & (j - 1));
+                if (p < pairs && (first_key[q] > second_key[q]) == ((i & k) == 0)) {
+                    keys[i] = second_key[q];
+                    keys[i + j] = first_key[q];
+                }
+            }
+            __syncthreads();
+        }
+    }
 }
 
 // Dynamic LDS of one workgroup (C = capacity, W = lanes per row):
@@ -376,34 +409,16 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
                 keys[s] = ~uint64_t{0};
             }
             __syncthreads();
-            // Bitonic network in LDS over the n victim keys: in each pass every
-            // thread takes the compare-exchanges p = threadIdx.x + q * kThreads
-            // (the pair (i, i + j), i = p with a zero inserted at bit log2 j),
-            // reading all of its pairs before writing any.
-            const uint32_t pairs = n >> 1;
-            for (uint32_t k = 2; k <= n; k <<= 1) {
-                for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-                    uint64_t first_key[kSortPairs], second_key[kSortPairs];
-#pragma unroll
-                    for (int q = 0; q < kSortPairs; ++q) {
-                        const uint32_t p = threadIdx.x + q * kThreads;
-                        const uint32_t i = ((p & ~(j - 1)) << 1) | (p & (j - 1));
-                        if (p < pairs) {
-                            first_key[q] = keys[i];
-                            second_key[q] = keys[i + j];
-                        }
-                    }
-#pragma unroll
-                    for (int q = 0; q < kSortPairs; ++q) {
-                        const uint32_t p = threadIdx.x + q * kThreads;
-                        const uint32_t i = ((p & ~(j - 1)) << 1) | (p & (j - 1));
-                        if (p < pairs && (first_key[q] > second_key[q]) == ((i & k) == 0)) {
-                            keys[i] = second_key[q];
-                            keys[i + j] = first_key[q];
-                        }
-                    }
-                    __syncthreads();
-                }
+            // Bitonic network in LDS over the n victim keys, each thread taking
+            // ceil(n / 2 / kThreads) compare-exchanges per pass.
+            if (n <= 2 * kThreads) {
+                sort_victims<1>(keys, n);
+            } else if (n <= 4 * kThreads) {
+                sort_victims<2>(keys, n);
+            } else if (n <= 8 * kThreads) {
+                sort_victims<4>(keys, n);
+            } else {
+                sort_victims<8>(keys, n);
             }
         }
         int32_t* bits = a.bits != nullptr ? a.bits + l * a.bt_l + req * a.bt_r : nullptr;
