@@ -242,6 +242,16 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
         ? static_cast<const void*>(static_cast<const int64_t*>(a.topk) + l * a.topk_sl + b * a.topk_sb)
         : static_cast<const void*>(static_cast<const int32_t*>(a.topk) + l * a.topk_sl + b * a.topk_sb);
 
+    const int32_t* misses = a.misses + l * a.mi_l + b * a.mi_b;
+    // Tokens of the miss entries (-1: the entry names no valid lane), read
+    // while the stamps load: the miss list -> Top-K chain of global reads
+    // overlaps the stamps' instead of following the touch phase.
+    for (int32_t i = threadIdx.x; i < m; i += kThreads) {
+        const int32_t lane = misses[i * a.mi_o];
+        const int64_t token =
+            lane >= 0 && lane < W ? lane_position(a, topk_row, static_cast<uint32_t>(lane)) : int64_t{-1};
+        info[i] = token >= 0 && token < a.table_cols ? static_cast<int32_t>(token) : -1;
+    }
     // Touch hits. A token repeated in the row is one access of its first lane:
     // the slot's stamp takes the lowest lane that hit it.
     for (int64_t s = threadIdx.x; s < C; s += kThreads) {
@@ -264,14 +274,6 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
     }
     __syncthreads();
     if (m > 0) {
-        const int32_t* misses = a.misses + l * a.mi_l + b * a.mi_b;
-        // Tokens of the miss entries (-1: the entry names no valid lane).
-        for (int32_t i = threadIdx.x; i < m; i += kThreads) {
-            const int32_t lane = misses[i * a.mi_o];
-            const int64_t token =
-                lane >= 0 && lane < W ? lane_position(a, topk_row, static_cast<uint32_t>(lane)) : int64_t{-1};
-            info[i] = token >= 0 && token < a.table_cols ? static_cast<int32_t>(token) : -1;
-        }
         for (uint32_t h = threadIdx.x; h < a.hash_size; h += kThreads) {
             hash[h] = -1;
         }
@@ -330,8 +332,11 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
         int32_t unique = 0;
         int32_t rank = workgroup_exclusive_scan(firsts, wave_totals, unique);
         for (int32_t i = run_begin; i < run_end; ++i) {
-            info[i] = owner[i] == i ? rank++ : -1;
+            if (owner[i] == i) {
+                owner[i] = -2 - rank++;   // a first miss: the rank of its victim, encoded below -1
+            }
         }
+        __syncthreads();   // the victim loop reads other threads' entries
         // The `unique` victims: the smallest (stamp, slot) keys, empty slots
         // (INT32_MIN) first, then the least recently used. A radix select
         // over the order-preserving unsigned form of the stamps (four 8-bit
@@ -423,26 +428,32 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
         }
         int32_t* bits = a.bits != nullptr ? a.bits + l * a.bt_l + req * a.bt_r : nullptr;
         for (int32_t i = threadIdx.x; i < m; i += kThreads) {
-            const int32_t first = owner[i];
+            // -1: the entry names no valid lane; <= -2: a first miss, whose
+            // victim has rank -2 - entry; otherwise the index of its first miss.
+            const int32_t entry = owner[i];
             const int32_t lane = misses[i * a.mi_o];
-            if (first < 0) {
+            if (entry == -1) {
                 // Not an entry of a miss list written by the lookup: record an
                 // empty promotion so the move that follows skips it.
                 promote_src[i * a.ps_o] = -1;
                 promote_dst[i * a.pd_o] = -1;
                 continue;
             }
-            const int64_t victim = static_cast<int64_t>(keys[info[first]] & 0xffffffffu);
+            const bool first = entry <= -2;
+            const int32_t rank = -2 - (first ? entry : owner[entry]);
+            const int64_t victim = static_cast<int64_t>(keys[rank] & 0xffffffffu);
             const int32_t global = static_cast<int32_t>(base + victim);
+            const int64_t token = info[i];   // >= 0 for an entry with a valid lane
+            // Independent global reads, issued together (a repeat's are unused).
+            const int32_t old = slot_token[victim * a.st_c];
+            const int32_t host_row = static_cast<int32_t>(a.host_table[req * a.host_sr + token * a.host_st]);
             slots[static_cast<int64_t>(lane) * a.sl_o] = global;
-            if (first != i) {
+            if (!first) {
                 // A repeat of an earlier miss: it shares that miss's slot and promotion.
                 promote_src[i * a.ps_o] = -1;
                 promote_dst[i * a.pd_o] = -1;
                 continue;
             }
-            const int64_t token = lane_position(a, topk_row, static_cast<uint32_t>(lane));
-            const int32_t old = slot_token[victim * a.st_c];
             if (old >= 0 && old < a.table_cols) {
                 set_entry(a, table_row + old * a.tb_t, 0);
                 if (bits != nullptr && a.bits_shift == 0) {
@@ -458,7 +469,7 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
             }
             slot_token[victim * a.st_c] = static_cast<int32_t>(token);
             stamp[victim] = static_cast<int32_t>(stamp_base + W + lane);
-            promote_src[i * a.ps_o] = static_cast<int32_t>(a.host_table[req * a.host_sr + token * a.host_st]);
+            promote_src[i * a.ps_o] = host_row;
             promote_dst[i * a.pd_o] = global;
         }
         __syncthreads();
