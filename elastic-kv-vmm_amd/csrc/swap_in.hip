@@ -181,9 +181,10 @@ __device__ void sort_victims(uint64_t* keys, uint32_t n) {
 //            over: touch[C] (first hit lane per slot), then the miss-token
 //            hash (miss indices), then the victims' (stamp, slot) keys;
 //   stamp    [C] recency stamps;
-//   info     [W] token of miss i, later the rank of miss i among the owners;
+//   info     [W] token of miss i (-1: an entry naming no valid lane);
 //   owner    [W] the first miss of the same token (-1: an entry naming no
-//            valid lane).
+//            valid lane); a first miss's own entry then becomes -2 - the rank
+//            of its victim.
 __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
     extern __shared__ unsigned char shared[];
     __shared__ int32_t wave_totals[kThreads / 64];
