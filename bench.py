@@ -52,6 +52,9 @@ Other workloads (same JSON contract):
                 arena of 4 x 65,536 rows of 256 bf16, 2048 positions per
                 request from three support sets, direct and software-table
                 addressing; host-launched p50 per call and HIP-graph GB/s
+  residency-summary  rebuild of the residency summary (ekv_residency_bits) of
+                the decode-read int16 table (60 x 128 x 65,536) at shifts 6
+                and 0, checked against a torch restatement
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -87,7 +90,8 @@ def parse_args():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--workload", default="decode-read",
                         choices=["decode-read", "topk-gather", "block-gather", "migration", "composite",
-                                 "hisparse-swap", "lookup-micro", "virtual-addressing"])
+                                 "hisparse-swap", "lookup-micro", "virtual-addressing",
+                                 "residency-summary"])
     parser.add_argument("--remap-fraction", type=float, default=0.05,
                         help="share of pool chunks unmapped and remapped per composite step")
     parser.add_argument("--capacity", type=int, default=4096, help="hot slots per request (decode-read)")
@@ -1405,8 +1409,51 @@ def run_composite(torch, args, device):
     return result
 
 
+def run_residency_summary(torch, args, device):
+    """Residency-summary rebuild (ekv_residency_bits) of the config-3 int16 table, shifts 6 and 0."""
+    from adaptive_sparse.resident_lookup import build_residency_bits, summary_words
+
+    L, R, T, C = 60, 128, 65536, 4096
+    gen = torch.Generator(device=device).manual_seed(args.seed)
+    table = torch.zeros((L, R, T), dtype=torch.int16, device=device)
+    table[..., T - C:] = torch.randint(1, C + 1, (L, R, C), dtype=torch.int16, device=device, generator=gen)
+    results, verified = {}, True
+    for shift in (6, 0):
+        out = torch.zeros((L, R, summary_words(T, shift)), dtype=torch.int32, device=device)
+        for _ in range(max(1, args.warmup)):
+            build_residency_bits(table, out=out, shift=shift)
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(args.steps):
+            build_residency_bits(table, out=out, shift=shift)
+        stop.record()
+        stop.synchronize()
+        ms = start.elapsed_time(stop) / args.steps
+        words = -(-(T >> shift) // 32)
+        nbytes = table.numel() * 2 + L * R * words * 4            # table read + summary words written
+        # torch restatement on the first and last layer: bit j of word w = any(table[p] != 0) over its group
+        picked = table[[0, L - 1]]
+        groups = (picked != 0).view(2, R, T >> shift, 1 << shift).any(-1).view(2, R, words, 32).to(torch.int64)
+        want = (groups << torch.arange(32, device=device)).sum(-1)
+        verified &= bool(torch.equal(out[[0, L - 1]][..., :words].to(torch.int64) & 0xffffffff, want))
+        results[shift] = {"ms": ms, "bytes": nbytes, "gbs": nbytes / (ms / 1e3) / 1e9}
+        log(f"residency summary shift {shift}: {ms * 1e3:.1f} us, {nbytes / 1e9:.3f} GB, "
+            f"{results[shift]['gbs']:.0f} GB/s, verified {verified}")
+    main_run = results[6]
+    roof = roofline(main_run["gbs"], "residency_pieces_kernel<int16> (ekv_residency_bits, shift 6)", main_run["bytes"],
+                    main_run["ms"], read_traffic("residency_summary_config3.md"))
+    config = {"workload": "residency-summary-rebuild", "layers": L, "requests": R, "context": T, "hot_capacity": C,
+              "table": "int16 local slots", "bits_shift": 6}
+    extra = {"verified_against_torch": verified,
+             "shift0": {"ms": round(results[0]["ms"], 4), "gbs": round(results[0]["gbs"], 1),
+                        "frac": round(results[0]["gbs"] / HBM_PEAK_GBS, 4), "bytes": results[0]["bytes"]}}
+    return envelope(args, main_run["gbs"], main_run["ms"], config, roof, None, extra,
+                    metric="residency summary rebuild GB/s (int16 table read + summary written), 1 GPU")
+
+
 WORKLOADS = {"decode-read": run_decode_read, "topk-gather": run_topk_gather, "lookup-micro": run_lookup_micro,
-             "virtual-addressing": run_virtual_addressing,
+             "virtual-addressing": run_virtual_addressing, "residency-summary": run_residency_summary,
              "block-gather": run_block_gather, "migration": run_migration, "composite": run_composite,
              "hisparse-swap": run_hisparse_swap}
 
@@ -1423,7 +1470,8 @@ EXTRA_CONFIGS = (("config1_topk_gather", "topk-gather", {}), ("config2_block_gat
                  ("config5_composite_spare_pool", "composite",
                   {"steps": 3, "warmup": 1, "spare_chunks": COMPOSITE_SPARE_CHUNKS, "no_cpu_baseline": True}),
                  ("lookup_micro", "lookup-micro", {}),
-                 ("virtual_addressing", "virtual-addressing", {}))
+                 ("virtual_addressing", "virtual-addressing", {}),
+                 ("residency_summary", "residency-summary", {}))
 
 
 def apply_profile_switch(environment, keep):
@@ -1440,7 +1488,7 @@ def summary(result):
             "hit_rate", "verified_round_trip", "tick_ms", "link_gbs", "pack_gbs", "unpack_gbs", "phase_ms",
             "higher_is_better", "vs_baseline", "per_batch", "correct", "verified_against_host_copy",
             "step_ms_without_remap", "remap_parts_ms", "promote_gbs_over_pcie", "swap_in", "graph_replay",
-            "per_support_set")
+            "per_support_set", "verified_against_torch", "shift0")
     return {key: result[key] for key in keys if key in result}
 
 
