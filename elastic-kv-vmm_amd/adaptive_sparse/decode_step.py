@@ -19,6 +19,7 @@ from elastic_kv import _native
 from .kv_pool import KVPlanes
 from .profile_ranges import profile_range
 from .sparse_read import _dense_struct, _planes_struct
+from .swap_in import STEP_STAMPS
 
 _P_TENSOR = ct.POINTER(_native.EkvTensor)
 
@@ -29,7 +30,7 @@ class StepArgs(ct.Structure):
     _fields_ = [
         ("topk", _P_TENSOR), ("block_size", ct.c_int64), ("rows", _P_TENSOR), ("lengths", _P_TENSOR),
         ("selected", _P_TENSOR), ("table", _P_TENSOR), ("resident_bits", _P_TENSOR), ("bits_shift", ct.c_int64),
-        ("slot_base", _P_TENSOR), ("slot_token", _P_TENSOR), ("stamps", _P_TENSOR), ("step", ct.c_int64),
+        ("resident_counts", _P_TENSOR), ("slot_base", _P_TENSOR), ("slot_token", _P_TENSOR), ("stamps", _P_TENSOR), ("step", ct.c_int64),
         ("step_counter", _P_TENSOR), ("status", _P_TENSOR), ("host_table", _P_TENSOR),
         ("host", ct.POINTER(_native.EkvPlanes)), ("pool", ct.POINTER(_native.EkvPlanes)), ("slots", _P_TENSOR),
         ("out", ct.POINTER(_native.EkvKvRows)),
@@ -64,7 +65,9 @@ def step_args(topk, rows, lengths, selected, buffers, host_table, host_planes, p
         topk=tensor(topk, "topk"), block_size=int(block_size), rows=tensor(rows, "rows"),
         lengths=tensor(lengths, "lengths"), selected=tensor(selected, "selected"),
         table=tensor(buffers.table, "table"), resident_bits=tensor(buffers.bits, "resident_bits"),
-        bits_shift=int(buffers.bits_shift), slot_base=tensor(buffers.slot_base, "slot_base"),
+        bits_shift=int(buffers.bits_shift),
+        resident_counts=tensor(getattr(buffers, "resident_counts", None), "resident_counts"),
+        slot_base=tensor(buffers.slot_base, "slot_base"),
         slot_token=tensor(buffers.slot_token, "slot_token"), stamps=tensor(buffers.stamps, "stamps"),
         step=int(step), step_counter=tensor(buffers.step_counter if step < 0 else None, "step_counter"),
         status=tensor(buffers.status, "status"), host_table=tensor(host_table, "host_table"),
@@ -78,7 +81,8 @@ def decode_step(topk, rows, lengths, buffers, host_table, host_planes, pool_plan
                 block_size=1, selected=None, step=None, workspace=None):
     """Lookup -> swap-in -> promote -> gather for the selected rows of every layer of `topk`.
 
-    topk [L, B, K]; rows, lengths [B]; selected [S] (default: every row);
+    topk [L, B, K]; rows, lengths [B]; selected [S]: batch rows in [0, B)
+    (default: every batch row, 0 .. B - 1);
     buffers: the HotBuffers of the pool; host_table [R, T] and host_planes:
     the pinned host copy (device-mapped); pool_planes: the hot pool; slots
     [L, B, K * block_size] int32 and output [B, L, KV, K * block_size, row]:
@@ -88,10 +92,11 @@ def decode_step(topk, rows, lengths, buffers, host_table, host_planes, pool_plan
     """
     L, B = topk.shape[0], topk.shape[1]
     width = topk.shape[2] * block_size
-    selected = rows if selected is None else selected
+    if selected is None:
+        selected = torch.arange(B, device=topk.device)
     counted = buffers.step_counter is not None and step is None
     if step is None and not counted:
-        if (buffers.step + 1) * 2 * width >= (1 << 31):
+        if (buffers.step + 1) * STEP_STAMPS >= (1 << 31):
             buffers.rebase()
         step = buffers.step
     needed = decode_step_workspace(L, B, width)

@@ -24,6 +24,7 @@ from .profile_ranges import profile_range
 from .sparse_read import _planes_struct
 
 INT32_MIN = -(1 << 31)
+STEP_STAMPS = 8192        # EKV_SWAP_STEP_STAMPS: recency stamps per LRU step, whatever the row width
 SWAP_STAMP_OVERFLOW = 1   # EKV_SWAP_STAMP_OVERFLOW
 SWAP_SHARED_REQUEST = 2   # EKV_SWAP_SHARED_REQUEST
 
@@ -38,14 +39,16 @@ class HotBuffers:
     bits_shift=self.bits_shift); slot_token [L, R, C]: token held by each
     slot (-1 = empty); stamps [L, R, C]: recency stamps; slot_base [R]:
     global slot of each request's local slot 0 (request r owns slots
-    base .. base + C - 1); status [1]: error bits of the swap-ins
+    base .. base + C - 1; every base is at least 1, since global slot 0 is
+    the sink that the lookup reports for a token that is not resident);
+    status [1]: error bits of the swap-ins
     (check_status reads and clears them).
     table is a view into storage whose rows are padded to a multiple of 128
     positions, so every row starts 16-byte aligned and the lookup can stage
     its recent window with 16-byte loads; bits rows are whole 16-byte pieces.
-    With bits_shift > 0 the swap-in sets the bit of every inserted token but
-    keeps the bits of evicted ones (other positions of the group may still be
-    resident), so the summary is a superset; refresh_bits() makes it exact.
+    With bits_shift > 0, resident_counts [L, R, ceil(T / 2**bits_shift)]
+    int32 holds the resident positions under each summary bit; the swap-in
+    keeps it and the summary exact through evictions and insertions.
     """
 
     def __init__(self, layers, requests, context, capacity, device, *, slot_base=None, with_bits=True,
@@ -65,11 +68,16 @@ class HotBuffers:
 
         words = summary_words(context, self.bits_shift)
         self.bits = torch.zeros((layers, requests, words), **kw) if with_bits else None
+        groups = -(-context // (1 << self.bits_shift))
+        self.resident_counts = (torch.zeros((layers, requests, groups), **kw)
+                                if with_bits and self.bits_shift > 0 else None)
         self.status = torch.zeros(1, **kw)
         self.slot_token = torch.full((layers, requests, capacity), -1, **kw)
         self.stamps = torch.full((layers, requests, capacity), INT32_MIN, **kw)
         if slot_base is None:
             slot_base = torch.arange(requests, dtype=torch.int64, device=self.device) * capacity + 1
+        elif slot_base.numel() and int(slot_base.min()) < 1:
+            raise ValueError("slot_base must be >= 1: global slot 0 is the sink that means 'not resident'")
         self.slot_base = slot_base
         self.step = 0
         # With a device step counter the swap-in reads and advances the step on
@@ -96,11 +104,16 @@ class HotBuffers:
         self.refresh_bits()
 
     def refresh_bits(self):
-        """Rebuild the residency summary exactly from the table (drops stale group bits)."""
+        """Rebuild the residency summary (and its group counts) exactly from the table.
+
+        Needed after the table is edited outside the swap-in (install does it).
+        """
         if self.bits is not None:
             from .resident_lookup import build_residency_bits
 
             build_residency_bits(self.table, out=self.bits, shift=self.bits_shift)
+        if self.resident_counts is not None:
+            self.resident_counts.copy_(residency_counts(self.table, self.bits_shift))
 
     def check_status(self):
         """Raise if a swap-in refused a row since the last check (a synchronizing read); clears the flags."""
@@ -129,14 +142,25 @@ class HotBuffers:
         if self.step_counter is not None:
             self.step_counter.zero_()
 
-    def steps_left(self, width):
-        """Swap-in steps of `width` lanes per row before the stamps need a rebase.
+    def steps_left(self):
+        """Swap-in steps left before the stamps need a rebase (any width).
 
         Reads the device counter when there is one (a synchronizing read):
         graph replays advance it without the host seeing them.
         """
         step = int(self.step_counter.item()) if self.step_counter is not None else self.step
-        return max(0, ((1 << 31) - 1) // (2 * width) - 1 - step)
+        # the last step that fits is the largest s with (s + 1) * STEP_STAMPS < 2**31
+        return max(0, ((1 << 31) - 1) // STEP_STAMPS - step)
+
+
+def residency_counts(table, shift):
+    """Resident (non-zero) positions of `table` [.., T] per group of 2**shift positions, int32 [.., groups]."""
+    size = 1 << shift
+    groups = -(-table.shape[-1] // size)
+    resident = table != 0
+    if groups * size != table.shape[-1]:
+        resident = torch.nn.functional.pad(resident, (0, groups * size - table.shape[-1]))
+    return resident.reshape(*table.shape[:-1], groups, size).sum(-1, dtype=torch.int32)
 
 
 def _ranks_from_stamps(stamps):
@@ -157,8 +181,10 @@ def swap_in(topk, block_size, rows, selected, slots, misses, miss_count, buffers
     back after the call (a synchronization) and raises, otherwise call
     buffers.check_status() when convenient.
 
-    Stamps are step * 2W + lane in int32; before they would overflow, the
-    buffers' stamps are renumbered (HotBuffers.rebase) and the step restarts.
+    Stamps are step * 8192 + lane (+ 4096 for a miss) in int32, so a step
+    ranks above every earlier one whatever the width of each call; before
+    they would overflow, the buffers' stamps are renumbered
+    (HotBuffers.rebase) and the step restarts.
     With a device step counter (HotBuffers(step_counter=True)) the kernel
     reads the step from it and advances it, so the call can be captured in a
     HIP graph; graph users check steps_left() and rebase in time.
@@ -166,29 +192,33 @@ def swap_in(topk, block_size, rows, selected, slots, misses, miss_count, buffers
     width = topk.shape[2] * block_size
     counted = buffers.step_counter is not None and step is None
     if step is None:
-        if (buffers.step + 1) * 2 * width >= (1 << 31):
+        if (buffers.step + 1) * STEP_STAMPS >= (1 << 31):
             buffers.rebase()
         step = buffers.step
     tensors = [topk, rows, selected, slots, misses, miss_count, buffers.table, buffers.slot_token,
                buffers.stamps, buffers.slot_base, host_table, promote_src, promote_dst]
     if buffers.bits is not None:
         tensors.append(buffers.bits)
+    if buffers.resident_counts is not None:
+        tensors.append(buffers.resident_counts)
     device = _native.device_of(*tensors)
     lib = _native.kernel_library()
     views = [ct.byref(_native.describe(t, "swap_in tensor")) for t in tensors[:13]]
     bits_view = ct.byref(_native.describe(buffers.bits, "bits")) if buffers.bits is not None else None
+    counts_view = (ct.byref(_native.describe(buffers.resident_counts, "resident_counts"))
+                   if buffers.resident_counts is not None else None)
     status_view = ct.byref(_native.describe(buffers.status, "status"))
-    # topk | rows .. table | bits, shift | slot_token .. promote_dst
+    # topk | rows .. table | bits, shift, group counts | slot_token .. promote_dst
     head, middle, tail = views[0], views[1:7], views[7:13]
     shift = int(buffers.bits_shift)
     with _native.on_device(device):
         if counted:
             counter = ct.byref(_native.describe(buffers.step_counter, "step_counter"))
-            status = lib.ekv_swap_in_counted(head, int(block_size), *middle, bits_view, shift, *tail, counter,
-                                             status_view, _native.stream_handle(device))
+            status = lib.ekv_swap_in_counted(head, int(block_size), *middle, bits_view, shift, counts_view, *tail,
+                                             counter, status_view, _native.stream_handle(device))
         else:
-            status = lib.ekv_swap_in(head, int(block_size), *middle, bits_view, shift, *tail, int(step),
-                                     status_view, _native.stream_handle(device))
+            status = lib.ekv_swap_in(head, int(block_size), *middle, bits_view, shift, counts_view, *tail,
+                                     int(step), status_view, _native.stream_handle(device))
     _native.check(lib, status, "swap_in")
     buffers.step = step + 1
     if check:

@@ -123,13 +123,13 @@ int decode_step(const ekv_step_args& s, void* workspace, uint64_t workspace_byte
     }
     if (s.step_counter != nullptr) {
         check_step(ekv_swap_in_counted(s.topk, s.block_size, s.rows, s.selected, s.slots, &misses, &counts, s.table,
-                                       s.resident_bits, s.bits_shift, s.slot_token, s.stamps, s.slot_base, s.host_table,
-                                       &src, &dst, s.step_counter, s.status, stream),
+                                       s.resident_bits, s.bits_shift, s.resident_counts, s.slot_token, s.stamps,
+                                       s.slot_base, s.host_table, &src, &dst, s.step_counter, s.status, stream),
                    "swap-in");
     } else {
         check_step(ekv_swap_in(s.topk, s.block_size, s.rows, s.selected, s.slots, &misses, &counts, s.table,
-                               s.resident_bits, s.bits_shift, s.slot_token, s.stamps, s.slot_base, s.host_table, &src,
-                               &dst, s.step, s.status, stream),
+                               s.resident_bits, s.bits_shift, s.resident_counts, s.slot_token, s.stamps, s.slot_base,
+                               s.host_table, &src, &dst, s.step, s.status, stream),
                    "swap-in");
     }
     check_step(ekv_move_kv(s.host, &src, s.pool, &dst, &counts, 1, stream), "promote");

@@ -6,10 +6,12 @@
 // then the misses are inserted in selection order. Here the hot buffer of a
 // (layer, request) row is `capacity` slots; the reference's ordered dict is
 // represented by one recency stamp per slot:
-//   touched hit of lane o at step s: stamp = s * 2W + o
-//   inserted miss of lane o:         stamp = s * 2W + W + o      (W = lanes per row)
+//   touched hit of lane o at step s: stamp = s * 8192 + o
+//   inserted miss of lane o:         stamp = s * 8192 + 4096 + o
 //   empty slot:                      stamp = INT32_MIN
-// so sorting slots by (stamp, slot) reproduces the dict's order, and the m
+// (a row has at most 4096 lanes, so every step's stamps lie above all of the
+// steps before it whatever the width of each call), so sorting slots by
+// (stamp, slot) reproduces the dict's order, and the m
 // victims of a step (m = misses) are the m smallest keys: empty slots first,
 // then the least recently used entries. The i-th miss (in lane order) takes
 // the i-th victim.
@@ -29,9 +31,17 @@
 // keys) and a bitonic network in LDS orders just them, then each victim
 // clears its old token from the token->slot table and residency summary,
 // takes the new token, and writes one promotion (host row -> global slot)
-// record. The
-// lookup's slot output of every miss lane is patched to its new slot, so the
-// gather that follows reads the promoted row.
+// record. The lookup's slot output of every miss lane is patched to its new
+// slot, so the gather that follows reads the promoted row.
+//
+// Residency summary. At bits_shift 0 a bit is one position: an evicted
+// token clears it, an inserted token sets it. A coarser bit covers 2^shift
+// positions; with per-bit resident counts the summary stays exact: every
+// eviction decrements its group's count and clears the bit when it reaches
+// zero, then (after a workgroup barrier, so no clear can follow a set) every
+// insertion increments its group's count and sets the bit from zero.
+// Without counts a coarse bit is only ever set, and the summary is a
+// superset of the table.
 //
 // Refused rows. Two selected rows naming one request would race on its hot
 // buffer, and a step whose stamps would overflow int32 cannot be ordered:
@@ -52,6 +62,11 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kMaxCapacity = 8192;   // slots per hot buffer (stamps held in LDS; 16-bit scan fields)
 constexpr int kMaxWidth = 4096;      // lanes per row whose miss tokens are hashed in LDS
+// Stamps per LRU step: hits take step * kStepStamps + lane, misses
+// step * kStepStamps + kMaxWidth + lane, so a call with fewer lanes than the
+// one before still stamps above it.
+constexpr int64_t kStepStamps = EKV_SWAP_STEP_STAMPS;
+static_assert(kStepStamps == 2 * kMaxWidth, "hit and miss stamps of one step take 2 * kMaxWidth values");
 constexpr int32_t kStatusStampOverflow = EKV_SWAP_STAMP_OVERFLOW;
 constexpr int32_t kStatusSharedRequest = EKV_SWAP_SHARED_REQUEST;
 
@@ -75,6 +90,8 @@ struct SwapArgs {
     int32_t* bits;                  // [L, R, words] residency summary (may be null)
     int64_t bt_l, bt_r, bt_w;
     uint32_t bits_shift;            // bit q covers positions [q << shift, (q + 1) << shift)
+    int32_t* line_counts;           // [L, R, groups] resident positions per summary bit (bits_shift > 0; may be null)
+    int64_t lc_l, lc_r, lc_q;
     int32_t* slot_token;            // [L, R, C] token held by each slot (-1 = empty)
     int64_t st_l, st_r, st_c;
     int32_t* stamps;                // [L, R, C] recency stamps
@@ -220,7 +237,7 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
     }
     shared_request = __syncthreads_or(shared_request);
     const int64_t step = a.step_counter != nullptr ? *a.step_counter : a.step;  // uniform
-    const bool overflow = step < 0 || (step + 1) * 2 * W >= (int64_t{1} << 31);
+    const bool overflow = step < 0 || (step + 1) * kStepStamps >= (int64_t{1} << 31);
     if (shared_request || overflow) {
         // Change nothing, record empty promotions (the move that follows
         // copies nothing; the missed lanes keep slot 0) and flag the error.
@@ -234,7 +251,7 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
         return;
     }
     const int64_t base = a.slot_base[req];
-    const int64_t stamp_base = step * 2 * W;
+    const int64_t stamp_base = step * kStepStamps;
     int32_t* slots = a.slots + l * a.sl_l + b * a.sl_b;
     const int64_t table_row = l * a.tb_l + req * a.tb_r;   // element offset of this (layer, request) row
     int32_t* slot_token = a.slot_token + l * a.st_l + req * a.st_r;
@@ -428,6 +445,10 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
             }
         }
         int32_t* bits = a.bits != nullptr ? a.bits + l * a.bt_l + req * a.bt_r : nullptr;
+        // Group counts keep a coarse summary exact: decrements here, increments after the barrier.
+        int32_t* line_counts = bits != nullptr && a.bits_shift > 0 && a.line_counts != nullptr
+                                   ? a.line_counts + l * a.lc_l + req * a.lc_r
+                                   : nullptr;
         for (int32_t i = threadIdx.x; i < m; i += kThreads) {
             // -1: the entry names no valid lane; <= -2: a first miss, whose
             // victim has rank -2 - entry; otherwise the index of its first miss.
@@ -458,22 +479,40 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
             if (old >= 0 && old < a.table_cols) {
                 set_entry(a, table_row + old * a.tb_t, 0);
                 if (bits != nullptr && a.bits_shift == 0) {
-                    // A coarser summary keeps the bit of the group (other
-                    // positions of it may still be resident); it stays a superset.
                     atomicAnd(reinterpret_cast<unsigned int*>(bits + (old >> 5) * a.bt_w), ~(1u << (old & 31)));
+                } else if (line_counts != nullptr) {
+                    // The group's last resident position leaves: clear its bit.
+                    const int64_t q = old >> a.bits_shift;
+                    if (atomicSub(line_counts + q * a.lc_q, 1) == 1) {
+                        atomicAnd(reinterpret_cast<unsigned int*>(bits + (q >> 5) * a.bt_w), ~(1u << (q & 31)));
+                    }
                 }
+                // Without counts a coarse bit stays set (other positions of
+                // its group may still be resident): a superset.
             }
             set_entry(a, table_row + token * a.tb_t, a.table16 ? static_cast<int32_t>(victim + 1) : global);
-            if (bits != nullptr) {
+            if (bits != nullptr && line_counts == nullptr) {
                 const int64_t q = token >> a.bits_shift;
                 atomicOr(reinterpret_cast<unsigned int*>(bits + (q >> 5) * a.bt_w), 1u << (q & 31));
             }
             slot_token[victim * a.st_c] = static_cast<int32_t>(token);
-            stamp[victim] = static_cast<int32_t>(stamp_base + W + lane);
+            stamp[victim] = static_cast<int32_t>(stamp_base + kMaxWidth + lane);
             promote_src[i * a.ps_o] = host_row;
             promote_dst[i * a.pd_o] = global;
         }
         __syncthreads();
+        if (line_counts != nullptr) {   // uniform
+            // Insertions: after every eviction's clear above, so a group that
+            // both loses and gains positions ends with its bit set.
+            for (int32_t i = threadIdx.x; i < m; i += kThreads) {
+                if (owner[i] <= -2) {   // a first miss: info[i] is its valid token
+                    const int64_t q = static_cast<int64_t>(info[i]) >> a.bits_shift;
+                    if (atomicAdd(line_counts + q * a.lc_q, 1) == 0) {
+                        atomicOr(reinterpret_cast<unsigned int*>(bits + (q >> 5) * a.bt_w), 1u << (q & 31));
+                    }
+                }
+            }
+        }
     }
     for (int64_t s = threadIdx.x; s < C; s += kThreads) {
         stamps[s * a.sp_c] = stamp[s];
@@ -495,7 +534,8 @@ void need_i32(const ekv_tensor& t, const char* name) {
 
 int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows_p, const ekv_tensor* selected_p,
             const ekv_tensor* slots_p, const ekv_tensor* misses_p, const ekv_tensor* counts_p,
-            const ekv_tensor* table_p, const ekv_tensor* bits_p, int64_t bits_shift, const ekv_tensor* slot_token_p,
+            const ekv_tensor* table_p, const ekv_tensor* bits_p, int64_t bits_shift, const ekv_tensor* counts_q_p,
+            const ekv_tensor* slot_token_p,
             const ekv_tensor* stamps_p, const ekv_tensor* slot_base_p, const ekv_tensor* host_table_p,
             const ekv_tensor* promote_src_p, const ekv_tensor* promote_dst_p, int64_t step,
             const ekv_tensor* step_counter_p, const ekv_tensor* status_p, void* stream) {
@@ -551,7 +591,7 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
     if (W > kMaxWidth) {
         throw std::invalid_argument("at most " + std::to_string(kMaxWidth) + " lanes per row");
     }
-    if (T >= (int64_t{1} << 31) || step < 0 || (step + 1) * 2 * W >= (int64_t{1} << 31)) {
+    if (T >= (int64_t{1} << 31) || step < 0 || (step + 1) * kStepStamps >= (int64_t{1} << 31)) {
         throw std::invalid_argument("token count or step outside the 32-bit stamp range");
     }
     int32_t* status = nullptr;
@@ -595,6 +635,20 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
         if (bits.shape[2] < (summary_bits + 31) / 32) {
             throw std::invalid_argument("resident_bits needs ceil(ceil(T / 2^bits_shift) / 32) words per row");
         }
+        if (counts_q_p != nullptr) {
+            const ekv_tensor& groups = need(counts_q_p, "resident_counts");
+            if (bits_shift == 0) {
+                throw std::invalid_argument("resident_counts serve a summary with bits_shift > 0");
+            }
+            need_ndim(groups, 3, "resident_counts");
+            need_i32(groups, "resident_counts");
+            need_dim(groups, 0, L, "resident_counts");
+            need_dim(groups, 1, R, "resident_counts");
+            need_dim(groups, 2, summary_bits, "resident_counts");
+            need_data(groups, "resident_counts");
+        }
+    } else if (counts_q_p != nullptr) {
+        throw std::invalid_argument("resident_counts need resident_bits");
     }
     const int64_t count = selected.shape[0];
     if (count == 0 || L == 0 || W == 0) {
@@ -631,6 +685,10 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
         a.bits = static_cast<int32_t*>(bits_p->data);
         a.bt_l = bits_p->stride[0], a.bt_r = bits_p->stride[1], a.bt_w = bits_p->stride[2];
         a.bits_shift = static_cast<uint32_t>(bits_shift);
+        if (counts_q_p != nullptr) {
+            a.line_counts = static_cast<int32_t*>(counts_q_p->data);
+            a.lc_l = counts_q_p->stride[0], a.lc_r = counts_q_p->stride[1], a.lc_q = counts_q_p->stride[2];
+        }
     }
     a.selected_count = count;
     a.status = status;
@@ -695,13 +753,14 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
 extern "C" int ekv_swap_in(const ekv_tensor* topk, int64_t block_size, const ekv_tensor* rows,
                            const ekv_tensor* selected, const ekv_tensor* slots, const ekv_tensor* misses,
                            const ekv_tensor* miss_count, const ekv_tensor* table, const ekv_tensor* resident_bits,
-                           int64_t bits_shift, const ekv_tensor* slot_token, const ekv_tensor* stamps,
+                           int64_t bits_shift, const ekv_tensor* resident_counts, const ekv_tensor* slot_token,
+                           const ekv_tensor* stamps,
                            const ekv_tensor* slot_base, const ekv_tensor* host_table, const ekv_tensor* promote_src,
                            const ekv_tensor* promote_dst, int64_t step, const ekv_tensor* status, void* stream) {
     return ekv::guarded(-1, [&] {
         return ekv::swap_in(topk, block_size, rows, selected, slots, misses, miss_count, table, resident_bits,
-                            bits_shift, slot_token, stamps, slot_base, host_table, promote_src, promote_dst, step,
-                            nullptr, status, stream);
+                            bits_shift, resident_counts, slot_token, stamps, slot_base, host_table, promote_src,
+                            promote_dst, step, nullptr, status, stream);
     });
 }
 
@@ -709,7 +768,8 @@ extern "C" int ekv_swap_in_counted(const ekv_tensor* topk, int64_t block_size, c
                                    const ekv_tensor* selected, const ekv_tensor* slots, const ekv_tensor* misses,
                                    const ekv_tensor* miss_count, const ekv_tensor* table,
                                    const ekv_tensor* resident_bits, int64_t bits_shift,
-                                   const ekv_tensor* slot_token, const ekv_tensor* stamps,
+                                   const ekv_tensor* resident_counts, const ekv_tensor* slot_token,
+                                   const ekv_tensor* stamps,
                                    const ekv_tensor* slot_base, const ekv_tensor* host_table,
                                    const ekv_tensor* promote_src, const ekv_tensor* promote_dst,
                                    const ekv_tensor* step_counter, const ekv_tensor* status, void* stream) {
@@ -718,7 +778,7 @@ extern "C" int ekv_swap_in_counted(const ekv_tensor* topk, int64_t block_size, c
             throw std::invalid_argument("step_counter is required");
         }
         return ekv::swap_in(topk, block_size, rows, selected, slots, misses, miss_count, table, resident_bits,
-                            bits_shift, slot_token, stamps, slot_base, host_table, promote_src, promote_dst, 0,
-                            step_counter, status, stream);
+                            bits_shift, resident_counts, slot_token, stamps, slot_base, host_table, promote_src,
+                            promote_dst, 0, step_counter, status, stream);
     });
 }

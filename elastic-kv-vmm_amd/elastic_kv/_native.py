@@ -14,7 +14,7 @@ import torch
 from ._source_hash import source_hash
 from .backing import _load_library, library_path
 
-EKV_ABI_VERSION = 2
+EKV_ABI_VERSION = 3
 
 _DTYPE_CODES = {
     torch.int32: 1,
@@ -79,9 +79,9 @@ _SIGNATURES = {
                       ct.c_int),
     "ekv_scatter_kv": ([ct.POINTER(EkvPlanes), _P_TENSOR, ct.POINTER(EkvKvRows), ct.c_int64, ct.c_void_p],
                        ct.c_int),
-    "ekv_swap_in": ([_P_TENSOR, ct.c_int64] + [_P_TENSOR] * 7 + [ct.c_int64] + [_P_TENSOR] * 6
+    "ekv_swap_in": ([_P_TENSOR, ct.c_int64] + [_P_TENSOR] * 7 + [ct.c_int64] + [_P_TENSOR] * 7
                     + [ct.c_int64, _P_TENSOR, ct.c_void_p], ct.c_int),
-    "ekv_swap_in_counted": ([_P_TENSOR, ct.c_int64] + [_P_TENSOR] * 7 + [ct.c_int64] + [_P_TENSOR] * 8
+    "ekv_swap_in_counted": ([_P_TENSOR, ct.c_int64] + [_P_TENSOR] * 7 + [ct.c_int64] + [_P_TENSOR] * 9
                             + [ct.c_void_p], ct.c_int),
     "ekv_move_kv": ([ct.POINTER(EkvPlanes), _P_TENSOR, ct.POINTER(EkvPlanes), _P_TENSOR, _P_TENSOR, ct.c_int64,
                      ct.c_void_p], ct.c_int),

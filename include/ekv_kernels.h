@@ -62,7 +62,7 @@ typedef struct ekv_kv_rows {
 } ekv_kv_rows;
 
 /* ABI revision of this header; bumped on any incompatible change. */
-#define EKV_ABI_VERSION 2
+#define EKV_ABI_VERSION 3
 int ekv_abi_version(void);
 
 /* Fingerprint (32 hex digits) of the sources the library was built from; the
@@ -200,9 +200,14 @@ int ekv_gather_kv(const ekv_planes* planes, const ekv_tensor* slots,
 int ekv_scatter_kv(const ekv_planes* planes, const ekv_tensor* slots,
                    const ekv_kv_rows* src, int64_t zero_below, void* stream);
 
+/* Recency stamps one LRU step spans: hits take step * 8192 + lane, misses
+ * step * 8192 + 4096 + lane (a row has at most 4096 lanes), so every step's
+ * stamps exceed all earlier steps' whatever the width of each call. */
+#define EKV_SWAP_STEP_STAMPS 8192
+
 /* Error bits a swap-in ORs into its status word (a row so refused changes
  * nothing and records empty promotions). */
-#define EKV_SWAP_STAMP_OVERFLOW 1  /* (step + 1) * 2W would reach 2^31 */
+#define EKV_SWAP_STAMP_OVERFLOW 1  /* (step + 1) * EKV_SWAP_STEP_STAMPS would reach 2^31 */
 #define EKV_SWAP_SHARED_REQUEST 2  /* two selected rows name one request */
 
 /*
@@ -219,16 +224,25 @@ int ekv_scatter_kv(const ekv_planes* planes, const ekv_tensor* slots,
  *   token -> local slot + 1 (the form of ekv_resolve_resident_local), updated
  *   resident_bits [L, R, words] int32 or NULL: a residency summary of the
  *   table with bits_shift as in ekv_resolve_resident_bits; inserted tokens
- *   set their bit, evicted tokens clear theirs only at bits_shift 0 (a
- *   coarser summary stays a superset; ekv_residency_bits makes it exact)
+ *   set their bit, and at bits_shift 0 evicted tokens clear theirs
+ *   resident_counts NULL, or with resident_bits at bits_shift > 0:
+ *   [L, R, ceil(T / 2^bits_shift)] int32, the resident positions under each
+ *   summary bit (as the table holds them on entry), kept up to date; a bit
+ *   is cleared when its count reaches zero, so the summary stays exact.
+ *   Without them a coarse summary only gains bits and becomes a superset
+ *   (ekv_residency_bits makes it exact again)
  *   slot_token [L, R, C] int32 (-1 = empty), stamps [L, R, C] int32: LRU state
  *   slot_base [R]: global slot of local slot 0 of each request's hot buffer
+ *   (at least 1: global slot 0 is the sink that means "not resident", so a
+ *   hot buffer starting there could never report its slot 0 as a hit)
  *   host_table [R, T]: token -> host row of the pinned host copy
  *   promote_src / promote_dst [L, B, W] int32: i < miss_count[l, b] get the
  *   host row and the global slot of the i-th promotion (feed to ekv_move_kv)
  *   status NULL or [1] int32 in device memory: EKV_SWAP_* bits are OR-ed in
- * Stamps are step * 2W + lane; `step` must grow by one per call and keep
- * (step + 1) * 2W below 2^31. W <= min(C, 4096), C <= 8192.
+ * Stamps are step * EKV_SWAP_STEP_STAMPS + lane (+ 4096 for a miss);
+ * `step` must grow by one per call (the width W may change from call to
+ * call) and keep (step + 1) * EKV_SWAP_STEP_STAMPS below 2^31, i.e.
+ * step < 262143. W <= min(C, 4096), C <= 8192.
  * A token repeated within a row is one access by its first lane (the
  * replay's rule applied to the selection with later repeats dropped): its
  * later miss entries share the first one's slot and get empty promotions.
@@ -240,7 +254,7 @@ int ekv_swap_in(const ekv_tensor* topk, int64_t block_size, const ekv_tensor* ro
                 const ekv_tensor* selected, const ekv_tensor* slots,
                 const ekv_tensor* misses, const ekv_tensor* miss_count,
                 const ekv_tensor* table, const ekv_tensor* resident_bits, int64_t bits_shift,
-                const ekv_tensor* slot_token, const ekv_tensor* stamps,
+                const ekv_tensor* resident_counts, const ekv_tensor* slot_token, const ekv_tensor* stamps,
                 const ekv_tensor* slot_base, const ekv_tensor* host_table,
                 const ekv_tensor* promote_src, const ekv_tensor* promote_dst,
                 int64_t step, const ekv_tensor* status, void* stream);
@@ -249,7 +263,7 @@ int ekv_swap_in(const ekv_tensor* topk, int64_t block_size, const ekv_tensor* ro
  * ekv_swap_in with the step read from device memory: step_counter [1] int64
  * holds the step of this call and is incremented after the swap-in (a second
  * launch on the same stream), so a captured HIP graph replays consecutive
- * steps. The caller keeps (step + 1) * 2W below 2^31 (rebasing the stamps
+ * steps. The caller keeps (step + 1) * EKV_SWAP_STEP_STAMPS below 2^31 (rebasing the stamps
  * and the counter in time); a call past that limit changes nothing, records
  * empty promotions and sets EKV_SWAP_STAMP_OVERFLOW in `status`.
  * No reference counterpart: the graph-replayable form of ekv_swap_in.
@@ -258,8 +272,8 @@ int ekv_swap_in_counted(const ekv_tensor* topk, int64_t block_size, const ekv_te
                         const ekv_tensor* selected, const ekv_tensor* slots,
                         const ekv_tensor* misses, const ekv_tensor* miss_count,
                         const ekv_tensor* table, const ekv_tensor* resident_bits, int64_t bits_shift,
-                        const ekv_tensor* slot_token, const ekv_tensor* stamps,
-                        const ekv_tensor* slot_base, const ekv_tensor* host_table,
+                        const ekv_tensor* resident_counts, const ekv_tensor* slot_token,
+                        const ekv_tensor* stamps, const ekv_tensor* slot_base, const ekv_tensor* host_table,
                         const ekv_tensor* promote_src, const ekv_tensor* promote_dst,
                         const ekv_tensor* step_counter, const ekv_tensor* status, void* stream);
 
@@ -346,6 +360,7 @@ typedef struct ekv_step_args {
     const ekv_tensor* table;          /* [L, R, T]: int16 local slot + 1, or int32 global slot; 0 = not resident */
     const ekv_tensor* resident_bits;  /* NULL or its residency summary ... */
     int64_t bits_shift;               /* ... one bit per 2^bits_shift positions */
+    const ekv_tensor* resident_counts; /* NULL or [L, R, groups] int32 resident positions per bit (shift > 0) */
     const ekv_tensor* slot_base;      /* [R] global slot of each request's local slot 0 */
     const ekv_tensor* slot_token;     /* [L, R, C] LRU state, as ekv_swap_in */
     const ekv_tensor* stamps;         /* [L, R, C] */

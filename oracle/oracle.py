@@ -151,22 +151,28 @@ def lru_misses(steps, capacity):
     return result
 
 
+SWAP_STEP_STAMPS = 8192   # recency stamps per LRU step: 2 x the 4096 lanes a row may have
+
+
 def swap_in(step, block_size, topk, rows, selected, slots, misses, counts, table, slot_token, stamps, slot_base,
             host_table):
     """Batch-token LRU swap-in after a lookup, on numpy arrays (copies are returned).
 
     Per selected row b (request r = rows[b]) of every layer: hits touch their
-    slot (stamp = step*2W + the lowest lane that hit it), the first miss
+    slot (stamp = step*8192 + the lowest lane that hit it), the first miss
     entry of every distinct token (in miss-list order) takes the next of the
     slots with the smallest (stamp, slot) - empty slots (-2^31) first; a
     victim's old token leaves the table, the new token enters it, its stamp
-    becomes step*2W + W + lane, and promotion i records
+    becomes step*8192 + 4096 + lane, and promotion i records
     (host_table[r, token], global slot). A later miss entry of the same token
     gets that slot and an empty promotion (-1, -1), as does an entry naming
     no valid lane. This is benchmarks/hisparse_locality_replay.py:90-99
     applied to the selection with repeated tokens reduced to their first
-    lane. Selected rows that share a request with another selected row, and
-    every row when (step + 1) * 2W reaches 2^31, change nothing and record
+    lane. A step spans 8192 stamps whatever the row width W (at most 4096),
+    so the stamps of a call with a smaller W than the call before still
+    rank above the earlier ones. Selected rows that share a request with
+    another selected row, and every row when (step + 1) * 8192 reaches 2^31,
+    change nothing and record
     empty promotions; "status" returns the error bits (1 = stamp overflow,
     2 = shared request). Returns a dict of the new arrays.
     """
@@ -184,7 +190,7 @@ def swap_in(step, block_size, topk, rows, selected, slots, misses, counts, table
     live = [int(b) for b in selected if 0 <= int(b) < B and 0 <= int(rows[int(b)]) < R]
     named = [int(rows[b]) for b in live]
     status = 0
-    overflow = step < 0 or (step + 1) * 2 * W >= 1 << 31
+    overflow = step < 0 or (step + 1) * SWAP_STEP_STAMPS >= 1 << 31
     for layer in range(L):
         for b in live:
             r = int(rows[b])
@@ -199,7 +205,7 @@ def swap_in(step, block_size, topk, rows, selected, slots, misses, counts, table
                 if slot > 0 and 0 <= slot - base < C:
                     first_hit.setdefault(slot - base, lane)
             for local, lane in first_hit.items():
-                stamp[local] = step * 2 * W + lane
+                stamp[local] = step * SWAP_STEP_STAMPS + lane
             order = sorted(range(C), key=lambda v: (stamp[v], v))
             taken = {}
             m = max(0, min(int(counts[layer, b]), W))
@@ -220,7 +226,7 @@ def swap_in(step, block_size, topk, rows, selected, slots, misses, counts, table
                     table[layer, r, old] = 0
                 table[layer, r, token] = base + victim
                 slot_token[layer, r, victim] = token
-                stamp[victim] = step * 2 * W + W + lane
+                stamp[victim] = step * SWAP_STEP_STAMPS + SWAP_STEP_STAMPS // 2 + lane
                 src[layer, b, i] = host_table[r, token]
                 dst[layer, b, i] = base + victim
                 slots[layer, b, lane] = base + victim

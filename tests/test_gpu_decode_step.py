@@ -45,7 +45,8 @@ class Side:
 
     def state(self):
         b = self.buffers
-        return [b.table.cpu(), b.bits.cpu(), b.slot_token.cpu(), b.stamps.cpu(), self.pool.cpu()]
+        counts = [b.resident_counts.cpu()] if b.resident_counts is not None else []
+        return [b.table.cpu(), b.bits.cpu(), b.slot_token.cpu(), b.stamps.cpu(), self.pool.cpu()] + counts
 
 
 def _topk(rng):
@@ -116,6 +117,48 @@ def test_decode_step_equals_its_stages(gpu, host, table_dtype, shift):
         decode_step(topk, rows, lengths, fused.buffers, host_table, host_planes, fused.planes,
                     torch.empty((L, R, K), dtype=torch.int32, device=gpu),
                     torch.empty((R, L, 2, K, ROW), dtype=torch.uint8, device=gpu), workspace=workspace[:-256])
+
+
+def test_decode_step_without_selected_serves_every_batch_row(gpu, host):
+    # A batch of 3 rows naming requests 4, 2 and 3 (ids outside 0 .. B - 1 and
+    # permuted) with no `selected`: every batch row must be looked up, swapped
+    # in and gathered, as the staged path does with selected = 0 .. B - 1.
+    host_planes, host_table, host_rows = host
+    staged, fused = Side(gpu, host, torch.int16, 6, False, 7), Side(gpu, host, torch.int16, 6, False, 7)
+    rows = torch.tensor([4, 2, 3], device=gpu)
+    B = rows.numel()
+    lengths = torch.full((B,), T, dtype=torch.int32, device=gpu)
+    rng = np.random.default_rng(13)
+    for step in range(2):
+        topk = _topk(rng)[:, :B].contiguous().to(gpu)
+        outputs = []
+        for side in (staged, fused):
+            slots = torch.full((L, B, K), -9, dtype=torch.int32, device=gpu)
+            out = torch.empty((B, L, 2, K, ROW), dtype=torch.uint8, device=gpu)
+            b = side.buffers
+            if side is staged:
+                every = torch.arange(B, device=gpu)
+                misses = torch.empty((L, B, K), dtype=torch.int32, device=gpu)
+                counts = torch.zeros((L, B), dtype=torch.int32, device=gpu)
+                resolve_resident(topk, b.table, None, rows, lengths, every, slots, 1, misses=misses,
+                                 miss_count=counts, resident_bits=b.bits, bits_shift=b.bits_shift,
+                                 slot_base=b.slot_base)
+                src, dst = torch.empty_like(slots), torch.empty_like(slots)
+                swap_in(topk, 1, rows, every, slots, misses, counts, b, host_table, src, dst)
+                move_kv(host_planes, src, side.planes, dst, counts)
+                gather_kv(side.planes, slots, out)
+            else:
+                decode_step(topk, rows, lengths, b, host_table, host_planes, side.planes, slots, out)
+            outputs.append([slots.cpu(), out.cpu()] + side.state())
+        torch.cuda.synchronize()
+        for a, b in zip(*outputs):
+            assert torch.equal(a, b), step
+        assert int((outputs[1][0] > 0).sum()) == L * B * K          # no batch row left unserved
+        got, tokens = outputs[1][1].numpy(), topk.cpu().numpy()
+        for layer in range(L):
+            for i, r in enumerate(rows.tolist()):
+                want = host_rows[layer, :, host_table[r].cpu().numpy()[tokens[layer, i]]]
+                assert np.array_equal(got[i, layer], np.swapaxes(want, 0, 1)), (step, layer, i)
 
 
 def test_decode_step_replays_from_a_graph(gpu, host):

@@ -4,7 +4,8 @@ The summary builder must equal the oracle's, and every lookup kernel that
 reads a summary (the prefetching int16 kernel, the contiguous-pieces kernel,
 the strided int16 and int32 kernels) must give the oracle's plain lookup -
 slots, miss lists and counts - for exact summaries and for supersets of
-them (stale group bits), which the swap-in leaves behind at shift > 0.
+them (stale group bits). The swap-in keeps a coarse summary exact through
+its group counts; without them it leaves a superset behind.
 """
 
 import numpy as np
@@ -120,45 +121,78 @@ def test_summary_rejects_a_short_row_and_bad_shift(gpu):
                          resident_bits=torch.zeros((2, 4), dtype=torch.int32, device=gpu), bits_shift=21)
 
 
-@pytest.mark.parametrize("table_dtype", [torch.int32, torch.int16])
-def test_swap_in_keeps_a_superset_summary(gpu, table_dtype):
-    # A stream through lookup + swap-in with a line summary (shift 6): after every
-    # step the maintained summary covers the exact one (inserted tokens set their
-    # group bit, evictions keep it), the lookup through it equals the oracle's
-    # plain lookup, and refresh_bits() makes it exact again.
+def _stream_step(rng, buffers, L, R, T, K, recent):
+    """One lookup + swap-in step of a locality stream; returns the oracle's lookup of the table before it."""
+    topk = np.stack([rng.permutation(np.concatenate([
+        rng.choice(np.arange(T - recent, T), K - K // 4, replace=False),
+        rng.choice(np.arange(0, T - recent), K // 4, replace=False)])) for _ in range(L * R)]).reshape(L, R, K)
+    topk_d = torch.tensor(topk, dtype=torch.int32, device=buffers.device)
+    table_before = _global(buffers)
+    rows = torch.arange(R, device=buffers.device)
+    lengths = torch.full((R,), T, dtype=torch.int32, device=buffers.device)
+    slots = torch.empty((L, R, K), dtype=torch.int32, device=buffers.device)
+    misses = torch.full((L, R, K), -1, dtype=torch.int32, device=buffers.device)
+    counts = torch.empty((L, R), dtype=torch.int32, device=buffers.device)
+    resolve_resident(topk_d, buffers.table, None, rows, lengths, rows, slots, 1, misses=misses,
+                     miss_count=counts, resident_bits=buffers.bits, bits_shift=buffers.bits_shift,
+                     slot_base=buffers.slot_base if buffers.table.dtype == torch.int16 else None)
+    want, _, want_counts = ref.resolve_resident(topk, table_before, None, np.arange(R), np.full(R, T), np.arange(R),
+                                                1, np.zeros((L, R, K), np.int32), with_misses=True)
+    got_slots, got_counts = slots.cpu().numpy(), counts.cpu().numpy()
+    host_table = torch.arange(R * T, dtype=torch.int32, device=buffers.device).reshape(R, T)
+    src = torch.full((L, R, K), -9, dtype=torch.int32, device=buffers.device)
+    dst = torch.full((L, R, K), -9, dtype=torch.int32, device=buffers.device)
+    swap_in(topk_d, 1, rows, rows, slots, misses, counts, buffers, host_table, src, dst, check=True)
+    return np.array_equal(got_slots, want) and np.array_equal(got_counts, want_counts)
+
+
+def _group_counts(table, shift):
+    """Resident positions per group of 2**shift positions (the last group ragged)."""
+    T = table.shape[-1]
+    groups = -(-T // (1 << shift))
+    padded = np.zeros((*table.shape[:-1], groups << shift), bool)
+    padded[..., :T] = table != 0
+    return padded.reshape(*table.shape[:-1], groups, 1 << shift).sum(-1)
+
+
+@pytest.mark.parametrize("table_dtype,shift", [(torch.int16, 6), (torch.int32, 6), (torch.int16, 3)])
+def test_swap_in_keeps_the_coarse_summary_exact(gpu, table_dtype, shift):
+    # A stream through lookup + swap-in with a coarse summary: after every step
+    # the summary the swap-in maintains equals a fresh build_residency_bits of
+    # the table (and the oracle's), its group counts equal the table's, and the
+    # lookup through it equals the oracle's plain lookup. Old groups fill and
+    # empty as uniform picks come and go, so bits are cleared as well as set.
+    L, R, T, C, K = 2, 3, 3001, 256, 128
+    rng = np.random.default_rng(5 + shift)
+    buffers = HotBuffers(L, R, T, C, gpu, table_dtype=table_dtype, bits_shift=shift)
+    ever = np.zeros(ref.residency_bits(_global(buffers), shift).shape, np.uint32)
+    for step in range(12):
+        assert _stream_step(rng, buffers, L, R, T, K, 400), step
+        table = _global(buffers)
+        exact = ref.residency_bits(table, shift)
+        words = exact.shape[-1]
+        kept = buffers.bits.cpu().numpy()
+        assert np.array_equal(kept[..., :words], exact), step
+        assert not kept[..., words:].any()
+        assert torch.equal(buffers.bits, build_residency_bits(buffers.table, shift=shift)), step
+        assert np.array_equal(buffers.resident_counts.cpu().numpy(), _group_counts(table, shift)), step
+        ever |= exact.view(np.uint32)
+    assert (ever != exact.view(np.uint32)).any()       # groups emptied: bits were cleared, not only set
+
+
+def test_swap_in_without_group_counts_keeps_a_superset(gpu):
+    # The ABI's count-less form: a coarse summary only gains bits (a superset
+    # that lookups still read correctly); refresh_bits() makes it exact again.
     L, R, T, C, K = 2, 3, 3000, 256, 128
     rng = np.random.default_rng(5)
-    buffers = HotBuffers(L, R, T, C, gpu, table_dtype=table_dtype, bits_shift=6)
-    local = buffers.slot_base if table_dtype == torch.int16 else None
-    rows = torch.arange(R, device=gpu)
-    lengths = torch.full((R,), T, dtype=torch.int32, device=gpu)
-    host_table = torch.arange(R * T, dtype=torch.int32, device=gpu).reshape(R, T)
-    state = None
+    buffers = HotBuffers(L, R, T, C, gpu, table_dtype=torch.int16, bits_shift=6)
+    buffers.resident_counts = None
     for step in range(8):
-        topk = np.stack([rng.permutation(np.concatenate([
-            rng.choice(np.arange(T - 400, T), 96, replace=False), rng.choice(np.arange(0, T - 400), 32, replace=False)]))
-            for _ in range(L * R)]).reshape(L, R, K)
-        topk_d = torch.tensor(topk, dtype=torch.int32, device=gpu)
-        table_before = _global(buffers)
-        slots = torch.empty((L, R, K), dtype=torch.int32, device=gpu)
-        misses = torch.full((L, R, K), -1, dtype=torch.int32, device=gpu)
-        counts = torch.empty((L, R), dtype=torch.int32, device=gpu)
-        resolve_resident(topk_d, buffers.table, None, rows, lengths, rows, slots, 1, misses=misses,
-                         miss_count=counts, resident_bits=buffers.bits, bits_shift=buffers.bits_shift,
-                         slot_base=local)
-        want, want_misses, want_counts = ref.resolve_resident(topk, table_before, None, np.arange(R),
-                                                              np.full(R, T), np.arange(R), 1,
-                                                              np.zeros((L, R, K), np.int32), with_misses=True)
-        assert np.array_equal(slots.cpu().numpy(), want), step
-        assert np.array_equal(counts.cpu().numpy(), want_counts), step
-        src = torch.full((L, R, K), -9, dtype=torch.int32, device=gpu)
-        dst = torch.full((L, R, K), -9, dtype=torch.int32, device=gpu)
-        swap_in(topk_d, 1, rows, rows, slots, misses, counts, buffers, host_table, src, dst, check=True)
+        assert _stream_step(rng, buffers, L, R, T, K, 400), step
         exact = ref.residency_bits(_global(buffers), 6).view(np.uint32)
         kept = buffers.bits.cpu().numpy()[..., :exact.shape[-1]].view(np.uint32)
-        assert np.array_equal(kept & exact, exact), step             # a superset
-        state = kept
-    assert (state != ref.residency_bits(_global(buffers), 6).view(np.uint32)).any()   # evictions left stale bits
+        assert np.array_equal(kept & exact, exact), step
+    assert (kept != exact).any()                       # evictions left stale bits
     buffers.refresh_bits()
     exact = ref.residency_bits(_global(buffers), 6)
     assert np.array_equal(buffers.bits.cpu().numpy()[..., :exact.shape[-1]], exact)

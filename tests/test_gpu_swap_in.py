@@ -111,6 +111,58 @@ def test_lookup_swap_promote_gather_cycle(gpu, capacity):
         arena.close()
 
 
+def test_width_changes_between_calls_keep_the_lru_order(gpu):
+    # Every call has its own row width (1 .. 16 lanes). The LRU state must equal
+    # the oracle's after each call, and each (layer, request) stream's promotion
+    # count must equal the reference's dict replay (lru_misses) over the same
+    # selections: a narrower call never evicts a slot that one of its hits reads.
+    L, R, T, C = 2, 3, 120, 16
+    rng = np.random.default_rng(41)
+    buffers = HotBuffers(L, R, T, C, gpu)
+    host_table = torch.arange(R * T, dtype=torch.int32).reshape(R, T)
+    rows = torch.arange(R, device=gpu)
+    lengths = torch.full((R,), T, dtype=torch.int32, device=gpu)
+    state = {"table": buffers.table.cpu().numpy(), "slot_token": buffers.slot_token.cpu().numpy(),
+             "stamps": buffers.stamps.cpu().numpy()}
+    streams = {(layer, r): [] for layer in range(L) for r in range(R)}
+    promoted = {key: [] for key in streams}
+    widths = [16, 2, 9, 1, 16, 5, 3, 12, 1, 7, 16, 4, 2, 10, 6, 1, 13, 8]
+    for step, K in enumerate(widths):
+        topk = np.stack([rng.choice(np.arange(T - 40, T), K, replace=False) for _ in range(L * R)]).reshape(L, R, K)
+        topk_d = torch.tensor(topk, dtype=torch.int32, device=gpu)
+        slots = torch.empty((L, R, K), dtype=torch.int32, device=gpu)
+        misses = torch.full((L, R, K), -1, dtype=torch.int32, device=gpu)
+        counts = torch.empty((L, R), dtype=torch.int32, device=gpu)
+        resolve_resident(topk_d, buffers.table, None, rows, lengths, rows, slots, 1, misses=misses,
+                         miss_count=counts, resident_bits=buffers.bits)
+        want_slots, want_misses, want_counts = ref.resolve_resident(
+            topk, state["table"], None, np.arange(R), np.full(R, T), np.arange(R), 1,
+            np.zeros((L, R, K), np.int32), with_misses=True)
+        miss_np = np.full((L, R, K), -1, np.int32)
+        for (layer, r), lanes in want_misses.items():
+            miss_np[layer, r, :len(lanes)] = lanes
+        src = torch.full((L, R, K), -9, dtype=torch.int32, device=gpu)
+        dst = torch.full((L, R, K), -9, dtype=torch.int32, device=gpu)
+        swap_in(topk_d, 1, rows, rows, slots, misses, counts, buffers, host_table.to(gpu), src, dst, check=True)
+        state = ref.swap_in(step, 1, topk, np.arange(R), np.arange(R), want_slots, miss_np, want_counts,
+                            state["table"], state["slot_token"], state["stamps"], buffers.slot_base.cpu().numpy(),
+                            host_table.numpy())
+        got_slots = slots.cpu().numpy()
+        assert np.array_equal(got_slots, state["slots"]), (step, K)
+        assert np.array_equal(buffers.table.cpu().numpy(), state["table"]), (step, K)
+        assert np.array_equal(buffers.slot_token.cpu().numpy(), state["slot_token"]), (step, K)
+        assert np.array_equal(buffers.stamps.cpu().numpy(), state["stamps"]), (step, K)
+        for (layer, r), stream in streams.items():
+            stream.append(topk[layer, r].tolist())
+            promoted[(layer, r)].append(int(want_counts[layer, r]))
+            # every lane reads its own token's slot after the call
+            held = buffers.slot_token.cpu().numpy()[layer, r]
+            local = got_slots[layer, r] - int(buffers.slot_base[r])
+            assert held[local].tolist() == topk[layer, r].tolist(), (step, layer, r)
+    for key, stream in streams.items():
+        assert promoted[key] == ref.lru_misses(stream, C), key
+
+
 def test_miss_entries_without_a_lane_record_empty_promotions(gpu):
     # A miss list the lookup did not write (lane -1, lane past the row) must not
     # leave stale promotion records behind for the move that follows.

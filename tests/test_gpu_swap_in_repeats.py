@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from adaptive_sparse.resident_lookup import resolve_resident
-from adaptive_sparse.swap_in import SWAP_SHARED_REQUEST, SWAP_STAMP_OVERFLOW, HotBuffers, swap_in
+from adaptive_sparse.swap_in import STEP_STAMPS, SWAP_SHARED_REQUEST, SWAP_STAMP_OVERFLOW, HotBuffers, swap_in
 from oracle import oracle as ref
 
 pytestmark = pytest.mark.gpu
@@ -140,7 +140,7 @@ def test_counted_step_past_the_stamp_range_is_reported(gpu):
     # swap-in must change nothing, record empty promotions and report the overflow.
     L, R, T, C, K = 1, 2, 64, 8, 4
     buffers = HotBuffers(L, R, T, C, gpu, step_counter=True)
-    buffers.step_counter.fill_((1 << 31) // (2 * K))
+    buffers.step_counter.fill_((1 << 31) // STEP_STAMPS - 1)     # the first step whose stamps leave int32
     topk = torch.tensor([[[1, 2, 3, 4], [5, 6, 7, 8]]], dtype=torch.int32, device=gpu)
     rows = torch.arange(R, device=gpu)
     slots = torch.zeros((L, R, K), dtype=torch.int32, device=gpu)

@@ -650,8 +650,9 @@ def test_hot_buffer_rebase_keeps_the_lru_order():
         return [sorted(range(8), key=lambda s: (int(row[s]), s)) for row in values.reshape(-1, 8)]
 
     before = lru_order(stamps)
+    assert buffers.steps_left() == (1 << 31) // 8192 - 1 - 123
     buffers.rebase()
-    assert buffers.step == 0
+    assert buffers.step == 0 and buffers.steps_left() == (1 << 31) // 8192 - 1
     assert lru_order(buffers.stamps) == before
     kept = buffers.stamps[buffers.stamps != INT32_MIN]
     assert int(kept.min()) >= -8 and int(kept.max()) < 0
@@ -751,3 +752,13 @@ def test_plane_projection_commits_each_logical_chunk_in_every_plane():
     views = projection.views(torch.int16, (2, 5))
     assert [v.shape for v in views] == [(2, 5)] * 3
     assert [v.view(torch.uint8)[0, :2].tolist() for v in views] == [[0, 1], [24, 25], [48, 49]]
+
+
+def test_hot_buffers_refuse_a_slot_base_on_the_sink():
+    import torch
+
+    from adaptive_sparse.swap_in import HotBuffers
+
+    with pytest.raises(ValueError, match="slot_base must be >= 1"):
+        HotBuffers(1, 2, 16, 4, "cpu", slot_base=torch.tensor([0, 4]))
+    assert HotBuffers(1, 2, 16, 4, "cpu", slot_base=torch.tensor([1, 5])).slot_base.tolist() == [1, 5]

@@ -353,13 +353,14 @@ def test_residency_summary_groups_the_bitmap():
                     assert bool((got[layer, row, group // 32] >> (group % 32)) & 1) == want
 
 
-def _lookup_swap_steps(step_tokens, capacity, context, block_size=1):
+def _lookup_swap_steps(step_tokens, capacity, context, block_size=1, fixed_width=True):
     """Drive lookup + swap-in for one (layer, request) stream; returns per-step promotion counts.
 
     Checks after every step that the hot buffer holds exactly the tokens of
     an OrderedDict run of the reference policy (hisparse_locality_replay.py
     :90-99) over the selections with repeated tokens reduced to their first
-    occurrence, in the same recency order.
+    occurrence, in the same recency order. With fixed_width=False every step
+    is a call whose row width is that step's selection size.
     """
     from collections import OrderedDict
 
@@ -369,8 +370,9 @@ def _lookup_swap_steps(step_tokens, capacity, context, block_size=1):
     host_table = np.arange(context)[None] + 1000
     model = OrderedDict()
     promoted_per_step = []
-    K = max(len(t) for t in step_tokens)
+    widest = max(len(t) for t in step_tokens)
     for step, tokens in enumerate(step_tokens):
+        K = widest if fixed_width else len(tokens)
         topk = np.full((1, 1, K), -1, np.int64)
         topk[0, 0, :len(tokens)] = tokens
         out, miss_lists, counts = ref.resolve_resident(topk, table[0], None, [0], [context], [0], block_size,
@@ -419,6 +421,37 @@ def test_swap_in_matches_lru_replay_on_random_streams():
     for capacity, context, k in ((8, 40, 6), (16, 100, 16), (5, 12, 5)):
         steps = [rng.sample(range(context), rng.randint(1, k)) for _ in range(40)]
         assert _lookup_swap_steps(steps, capacity, context) == ref.lru_misses(steps, capacity)
+
+
+def test_swap_in_order_survives_a_narrower_call():
+    """Step 0 fills 8 slots with 8 lanes; step 1 has 2 lanes: token 10 hits, token 40 misses.
+
+    The miss must evict the least recent token of step 0 (token 0), never the
+    slot of the hit it sits beside, whatever the two calls' widths."""
+    context, capacity = 64, 8
+    table = np.zeros((1, 1, context), np.int32)
+    slot_token = np.full((1, 1, capacity), -1, np.int32)
+    stamps = np.full((1, 1, capacity), -(1 << 31), np.int32)
+    host = np.arange(context)[None] + 1000
+    for step, tokens in enumerate(([0, 10, 20, 30, 1, 2, 3, 4], [10, 40])):
+        topk = np.array([[tokens]], np.int64)
+        out, miss_lists, counts = ref.resolve_resident(topk, table[0], None, [0], [context], [0], 1,
+                                                       np.zeros((1, 1, len(tokens)), np.int32), with_misses=True)
+        miss = np.zeros((1, 1, len(tokens)), np.int32)
+        miss[0, 0, :len(miss_lists[(0, 0)])] = miss_lists[(0, 0)]
+        state = ref.swap_in(step, 1, topk, [0], [0], out, miss, counts, table, slot_token, stamps, [1], host)
+        table, slot_token, stamps = state["table"], state["slot_token"], state["stamps"]
+    assert state["slots"][0, 0].tolist() == [2, 1]          # token 10 keeps slot 2, token 40 takes token 0's slot 1
+    assert table[0, 0, 10] == 2 and table[0, 0, 40] == 1 and table[0, 0, 0] == 0
+    assert sorted(slot_token[0, 0].tolist()) == sorted([40, 10, 20, 30, 1, 2, 3, 4])
+
+
+def test_swap_in_matches_lru_replay_when_the_width_changes_every_call():
+    rng = random.Random(37)
+    for capacity, context, k in ((8, 40, 8), (16, 100, 16), (6, 20, 6)):
+        steps = [rng.sample(range(context), rng.randint(1, k)) for _ in range(60)]
+        assert len({len(s) for s in steps}) > 2
+        assert _lookup_swap_steps(steps, capacity, context, fixed_width=False) == ref.lru_misses(steps, capacity)
 
 
 def test_swap_in_repeated_tokens_follow_the_deduplicated_replay():

@@ -45,6 +45,7 @@ def _side(gpu, host_planes, host_table, seed):
 def _first_layers(buffers, n):
     """The hot-buffer state of the first n layers (views), as step_args reads it."""
     return SimpleNamespace(table=buffers.table[:n], bits=buffers.bits[:n], bits_shift=buffers.bits_shift,
+                           resident_counts=buffers.resident_counts[:n],
                            slot_base=buffers.slot_base, slot_token=buffers.slot_token[:n],
                            stamps=buffers.stamps[:n], step_counter=None, status=buffers.status)
 
@@ -61,9 +62,10 @@ def test_static_step_equals_the_workspace_step_on_two_calls(gpu):
         lib = _native.kernel_library()
         stream = _native.stream_handle(gpu)
         rng = np.random.default_rng(12)
-        # call 1: every layer and row, 512 lanes, LRU step 0 (stamps below 2 * 512);
-        # call 2: 2 layers x 4 rows, 128 lanes, step 4 (stamps from 4 * 2 * 128 = 1024 on, still the newest)
-        for call, (layers, batch, K, step) in enumerate(((L, R, 512, 0), (2, 4, 128, 4))):
+        # call 1: every layer and row, 512 lanes, LRU step 0; call 2: 2 layers x 4 rows,
+        # 128 lanes, step 1 (a step spans 8192 stamps whatever its width, so the
+        # narrower call's stamps are still the newest)
+        for call, (layers, batch, K, step) in enumerate(((L, R, 512, 0), (2, 4, 128, 1))):
             topk = torch.tensor(np.stack([rng.permutation(np.concatenate([
                 rng.choice(np.arange(T - 900, T), K - K // 8, replace=False),
                 rng.choice(np.arange(0, T - 900), K // 8, replace=False)])) for _ in range(layers * batch)])
@@ -87,7 +89,8 @@ def test_static_step_equals_the_workspace_step_on_two_calls(gpu):
                 torch.cuda.synchronize()
                 del keep
                 results.append([slots.cpu(), out.cpu(), pool.cpu(), buffers.table.cpu(), buffers.bits.cpu(),
-                                buffers.slot_token.cpu(), buffers.stamps.cpu(), buffers.status.cpu()])
+                                buffers.resident_counts.cpu(), buffers.slot_token.cpu(), buffers.stamps.cpu(),
+                                buffers.status.cpu()])
             print(f"[no-alloc] call {call}: {layers} layers x {batch} rows x {K} lanes", flush=True)
             for a, b in zip(*results):
                 assert torch.equal(a, b), call
