@@ -24,34 +24,32 @@ import torch
 from elastic_kv.backing import Backing
 from elastic_kv.slots import FreeSlots
 
-from .kv_pool import BlockMajorLayout
+from .kv_pool import BlockMajorLayout, PlanePoolLayout
 from .minimax_vmm import PhysicalPages
 from .sparse_read import gather_kv, scatter_kv
 
 
-class PagedKVPool:
-    """Block-major paged KV pool over one VMM Backing with refcounted chunks.
+class _PagedPool:
+    """Page ownership over one VMM Backing: allocate / release / trim / close."""
 
-    Page p holds layers x kv plane rows of row_bytes contiguously; page 0 is
-    the permanent sink. `pages` tracks ownership (PhysicalPages with one
-    plane of block_bytes rows), `free` hands out page ids.
-    """
-
-    def __init__(self, layout, device=0, backing_factory=Backing):
-        if not isinstance(layout, BlockMajorLayout):
-            raise TypeError("layout must be a BlockMajorLayout")
+    def _own(self, layout, device, backing_factory, page_size, page_count, planes):
         self.layout = layout
         self.device = torch.device("cuda", device) if isinstance(device, int) else torch.device(device)
         index = self.device.index or 0
         self.backing = backing_factory(layout.capacity_bytes, layout.chunk_bytes, index)
-        self.pages = PhysicalPages(self.backing, 1, layout.blocks - 1, [(0, layout.block_bytes)],
+        self.pages = PhysicalPages(self.backing, page_size, page_count, planes,
                                    lambda: torch.cuda.synchronize(self.device), chunk_bytes=layout.chunk_bytes)
-        self.free = FreeSlots(layout.blocks - 1)
+        self.free = FreeSlots(page_count)
         self.planes = layout.kv_planes(self.backing.base, index, owner=self.backing)
 
-    def page_view(self, page):
-        """uint8 view of one page's bytes (its chunks must be mapped)."""
-        return self.backing.raw.narrow(0, page * self.layout.block_bytes, self.layout.block_bytes)
+    def take(self, count):
+        """Allocate the `count` lowest free page ids (committing their chunks); None when too few are free."""
+        ranges = self.free.peek(count)
+        if ranges is None:
+            return None
+        pages = [p for a, b in ranges for p in range(a, b)]
+        self.allocate(pages)
+        return pages
 
     def allocate(self, pages):
         """Take specific free page ids and commit their chunks (map + zero)."""
@@ -99,6 +97,54 @@ class PagedKVPool:
     def close(self):
         torch.cuda.synchronize(self.device)
         self.backing.close()
+
+
+class PagedKVPool(_PagedPool):
+    """Block-major paged KV pool over one VMM Backing with refcounted chunks.
+
+    Page p holds layers x kv plane rows of row_bytes contiguously; page 0 is
+    the permanent sink. `pages` tracks ownership (PhysicalPages with one
+    plane of block_bytes rows), `free` hands out page ids.
+    """
+
+    def __init__(self, layout, device=0, backing_factory=Backing):
+        if not isinstance(layout, BlockMajorLayout):
+            raise TypeError("layout must be a BlockMajorLayout")
+        self._own(layout, device, backing_factory, 1, layout.blocks - 1, [(0, layout.block_bytes)])
+
+    def page_view(self, page):
+        """uint8 view of one page's bytes (its chunks must be mapped)."""
+        return self.backing.raw.narrow(0, page * self.layout.block_bytes, self.layout.block_bytes)
+
+
+class PlanePagedPool(_PagedPool):
+    """Plane-major paged KV pool: the layout of the reference's MiniMax main pool.
+
+    One plane per (layer, K|V), each padded to whole chunks
+    (adaptive_sparse/minimax_vmm.py:220-243); page p holds token slots
+    [p * page_size, (p + 1) * page_size) of every plane, slot s of a plane at
+    s * row_bytes. Page 0 (and so slot 0) is the permanent sink. Ownership is
+    PhysicalPages over the planes (adaptive_sparse/minimax_vmm.py:40-98).
+    """
+
+    def __init__(self, layers, kv, page_count, page_size, row_bytes, device=0, chunk_bytes=2 << 20,
+                 backing_factory=Backing):
+        layout = PlanePoolLayout(layers, kv, (page_count + 1) * page_size, row_bytes, chunk_bytes)
+        planes = [(plane * layout.plane_chunks, row_bytes) for plane in range(layout.planes)]
+        self.page_size = page_size
+        self._own(layout, device, backing_factory, page_size, page_count, planes)
+
+    def slots(self, pages):
+        """int64 token slots of `pages`, page after page, on the pool's device."""
+        pages = torch.as_tensor(list(pages), dtype=torch.int64).to(self.device)
+        offsets = torch.arange(self.page_size, dtype=torch.int64, device=self.device)
+        return (pages.view(-1, 1) * self.page_size + offsets).flatten()
+
+    def plane_rows(self, layer, kv):
+        """uint8 [slots, row_bytes] view of one plane (read only rows whose chunks are mapped)."""
+        layout = self.layout
+        return self.backing.raw.narrow(0, layout.plane_offset(layer, kv), layout.plane_bytes).view(
+            layout.rows, layout.row_bytes)
 
 
 @dataclass

@@ -3,19 +3,25 @@
 The round trip is self-pinning: destination pages must hold exactly the
 bytes the source pages held before demotion (the reference's bitwise
 migration check, adaptive_sparse/logical_shadow.py:88-123, compares the same
-way through int16 views). Packing is also checked against the oracle.
+way through int16 views). Packing is also checked against the oracle. The
+transactions run a request through demote -> host-backed decode (the
+SGLang-convention swap-in, against the oracle) -> promote, and every token's
+bytes must survive, the newest taken from its reserved device slot.
 """
 
 import numpy as np
 import pytest
 import torch
 
+from adaptive_sparse.host_arena import HostKVCache
 from adaptive_sparse.kv_pool import BlockMajorLayout
 from adaptive_sparse.migration import (
-    MigrationCoordinator, MigrationRequest, abort_demote, abort_promote, commit_demote, commit_promote,
+    HiSparseCoordinator, MigrationRequest, abort_demote, abort_promote, commit_demote, commit_promote,
     prepare_demote, prepare_promote,
 )
-from adaptive_sparse.migration_engine import MigrationEngine, PagedKVPool
+from adaptive_sparse.migration_budget import MigrationBandwidthEstimator
+from adaptive_sparse.migration_engine import MigrationEngine, PagedKVPool, PlanePagedPool
+from oracle import oracle as ref
 
 pytestmark = pytest.mark.gpu
 
@@ -142,53 +148,165 @@ def test_trim_after_packed_event_overlaps_the_copies(gpu, sub_batch):
         pool.close()
 
 
-def test_transactions_demote_promote_cycle(gpu):
-    layout = BlockMajorLayout(blocks=64, **BLOCK)
-    pool = PagedKVPool(layout, device=0)
+class _Truth:
+    """The bytes every token of one request must read back: truth[token] = [L, KV, row] uint8."""
+
+    def __init__(self, pool):
+        self.pool, self.rows = pool, {}
+
+    def write(self, token, slot, gen):
+        layout = self.pool.layout
+        value = torch.randint(0, 256, (layout.layers, layout.kv, layout.row_bytes), dtype=torch.uint8,
+                              device=self.pool.device, generator=gen)
+        for layer in range(layout.layers):
+            for kv in range(layout.kv):
+                self.pool.plane_rows(layer, kv)[slot].copy_(value[layer, kv])
+        self.rows[token] = value.cpu()
+
+    def check_slots(self, slots, tokens, what):
+        layout = self.pool.layout
+        idx = torch.as_tensor(slots, dtype=torch.int64, device=self.pool.device)
+        got = torch.stack([torch.stack([self.pool.plane_rows(layer, kv)[idx] for kv in range(layout.kv)])
+                           for layer in range(layout.layers)]).cpu()                   # [L, KV, n, row]
+        want = torch.stack([self.rows[int(t)] for t in tokens], dim=2)
+        assert torch.equal(got, want), what
+
+
+def _resident_request(gpu, coordinator, truth, row, length, pages, first_logical, gen):
+    """Publish a resident request of `length` tokens over `pages`, with random K/V bytes."""
+    pool = coordinator.pool
+    pool.allocate(pages)
+    slots = pool.slots(pages)[:length]
+    logical = torch.arange(first_logical, first_logical + length, device=gpu)
+    coordinator.req_to_token[row, :length] = logical
+    coordinator.mapping[logical] = slots
+    for token in range(length):
+        truth.write(token, int(slots[token]), gen)
+    return MigrationRequest(row=row, length=length)
+
+
+def _host_backed_step(coordinator, truth, request, rng, gen, layers, block_size):
+    """One host-backed decode step of `request` through ekv_hisparse_swap_in, checked against the oracle."""
+    gpu = coordinator.pool.device
+    row, length = request.row, request.length
+    coordinator.backup_previous_token(row, length)
+    truth.write(length, coordinator.newest_slot(row), gen)              # the model writes the new token's K/V
+    request.length = length = length + 1
+    coordinator.req_to_token[row, length - 1] = 5000 + length - 1
+    hot = coordinator.device_buffer_size
+    K = hot // block_size
+    newest_block = (length - 1) // block_size
+    held = coordinator.req_to_device_buffer[row]             # the hot buffer's slots: rows of owned pages
+    for layer in range(layers):
+        # most blocks recent, some old, one repeated, one padding
+        recent = rng.choice(np.arange(newest_block - 23, newest_block + 1), K // 2, replace=False)
+        old = rng.choice(newest_block + 1, K - len(recent), replace=False)
+        blocks = rng.permutation(np.concatenate([recent, old]))
+        blocks[1] = blocks[0]
+        blocks[-1] = -1
+        top = torch.tensor(blocks[None], dtype=torch.int64, device=gpu)
+        planes = [coordinator.pool.plane_rows(layer, kv) for kv in range(2)]
+        host_k, host_v = coordinator.host.layer(layer)
+        # The oracle's device rows: only the hot buffer's rows are read or written by the swap, so only
+        # they are copied (the rest of a plane may lie in unmapped chunks and stays zero here).
+        device_rows = []
+        for kv in range(2):
+            rows = np.zeros(tuple(planes[kv].shape), np.uint8)
+            rows[held.cpu().numpy()] = planes[kv][held].cpu().numpy()
+            device_rows.append(rows)
+        want = ref.hisparse_swap(
+            blocks[None], coordinator.req_device_buffer_tokens[layer].cpu().numpy(),
+            coordinator.req_to_host_pool.cpu().numpy(), coordinator.req_to_device_buffer.cpu().numpy(),
+            host_k.numpy(), host_v.numpy(), device_rows[0], device_rows[1], [row], [length],
+            coordinator.lru_slots[layer].cpu().numpy(), hot, block_size)
+        out = torch.full((1, K * block_size), -7, dtype=torch.int32, device=gpu)
+        coordinator.swap_in(layer, torch.tensor([row], device=gpu), torch.tensor([length], dtype=torch.int32,
+                            device=gpu), top, out, block_size)
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), want[0]), layer
+        assert np.array_equal(coordinator.req_device_buffer_tokens[layer].cpu().numpy(), want[1]), layer
+        assert np.array_equal(coordinator.lru_slots[layer].cpu().numpy().astype(np.int64), want[2]), layer
+        held_np = held.cpu().numpy()
+        for kv in range(2):
+            assert np.array_equal(planes[kv][held].cpu().numpy(), want[3 + kv][held_np]), (layer, kv)
+        # every selected token reads its own bytes (the newest one from the reserved slot)
+        tokens = [b * block_size + j for b in blocks if b >= 0 for j in range(block_size) if b * block_size + j < length]
+        locs = out[0, :len(tokens)].cpu()
+        assert (locs > 0).all() and (out[0, len(tokens):] == -1).all()
+        for kv in range(2):
+            got = planes[kv][locs.to(gpu).long()].cpu()
+            assert torch.equal(got, torch.stack([truth.rows[t][layer, kv] for t in tokens])), (layer, kv)
+
+
+@pytest.mark.parametrize("decode_steps", [0, 4])
+def test_demote_host_backed_decode_promote(gpu, decode_steps, monkeypatch):
+    # A resident request of 300 tokens (19 pages of 16) is demoted: its host
+    # rows hold every token, 5 pages stay as its hot buffer (64 slots + the
+    # reserved newest-token slot), the rest are released. `decode_steps` host-
+    # backed decode steps follow, each writing a new token into the reserved
+    # slot and swapping every layer's Top-K in through ekv_hisparse_swap_in
+    # (checked against the oracle). The promotion then restores every token
+    # into fresh pages: from host, and - after decode - the newest one from
+    # the reserved slot (host_len = length - 1).
+    monkeypatch.delenv("EKV_CHUNK_AWARE_RETENTION", raising=False)
+    L, ROW, PAGE, HOT, BS = 3, 2048, 16, 64, 2
+    rng = np.random.default_rng(11 + decode_steps)
+    gen = torch.Generator(device=gpu).manual_seed(3 + decode_steps)
+    pool = PlanePagedPool(L, 2, 255, PAGE, ROW, device=0)
+    host = HostKVCache(L, 2, 1024, ROW)
     try:
-        engine = MigrationEngine(pool, max_pages=32, sub_batch=4)
-        mapping = torch.zeros(100, dtype=torch.int64, device=gpu)
-        pages = list(range(3, 3 + 20))
-        pool.allocate(pages)
-        fill(pool, pages, 7)
-        logical = torch.arange(40, 60, device=gpu)
-        mapping[logical] = torch.tensor(pages, device=gpu)
-        original = {i: pool.page_view(p).clone() for i, p in enumerate(pages)}
-        coordinator = MigrationCoordinator(pool, engine, mapping, keep_pages=6)
-        request = MigrationRequest(row=2, logical=logical)
-        published = []
+        estimator = MigrationBandwidthEstimator(1 << 30, 0.5)
+        coordinator = HiSparseCoordinator(pool, host, rows=4, max_len=512, logical_size=8192, hot_capacity=HOT,
+                                          bandwidth=estimator)
+        assert coordinator.padded_buffer_size == 80
+        truth = _Truth(pool)
+        # A chunk holds 64 pages of a plane: the 5 retained pages (the first ones) lie in chunk 0's range,
+        # the 14 released ones in chunk 2's, which the demotion must unmap in all 6 planes.
+        pages = (rng.choice(np.arange(1, 64), 5, replace=False).tolist()
+                 + rng.choice(np.arange(128, 192), 14, replace=False).tolist())
+        request = _resident_request(gpu, coordinator, truth, 2, 300, pages, 1000, gen)
+        logical = coordinator.req_to_token[2, :300].clone()
         sync = torch.cuda.synchronize
+        published = []
 
         prepared = prepare_demote(coordinator, request, sync)
-        assert len(prepared.retained_rows) == 6 and len(prepared.released_rows) == 14
         abort_demote(prepared)
-        with pytest.raises(RuntimeError):
-            abort_demote(prepared)
-        assert engine.host_free.count == 32
-
+        assert host.free_rows == 1024 and coordinator.req_to_host_pool_allocated_len[2] == 0
         prepared = prepare_demote(coordinator, request, sync)
+        host_rows = coordinator.req_to_host_pool[2, :300].cpu()
+        want = torch.stack([truth.rows[t] for t in range(300)], dim=2)              # [L, KV, 300, row]
+        assert torch.equal(host.view[:, :, host_rows], want)
         backed = pool.backing.backed_bytes
         released = commit_demote(prepared, published.append, sync, trim_quiescent=pool.trim)
-        assert published == [2] and prepared.status == "committed"
-        assert (mapping[logical] == 0).all()
-        assert released > 0 and pool.backing.backed_bytes == backed - released
-        assert coordinator.hot[2] == tuple(pages[i] for i in prepared.retained_rows)
-        with pytest.raises(RuntimeError):
-            commit_demote(prepared, published.append, sync)
+        assert published == [2] and (coordinator.mapping[logical] == 0).all()
+        assert released == 6 * pool.layout.chunk_bytes and pool.backing.backed_bytes == backed - released
+        retained = coordinator.req_to_device_buffer[2].cpu()
+        assert retained.tolist() == pool.slots(pages[:5]).tolist()
+        assert coordinator.hot_pages[2] == tuple(pages[:5]) and coordinator.skip_first_backup[2]
+        assert estimator.samples("demotion") == 1
+
+        for _ in range(decode_steps):
+            _host_backed_step(coordinator, truth, request, rng, gen, L, BS)
+        length = request.length
+        assert length == 300 + decode_steps
+        assert coordinator.skip_first_backup[2] == (decode_steps == 0)
 
         promotion = prepare_promote(coordinator, request, sync)
         abort_promote(promotion)
-        promotion = prepare_promote(coordinator, request, sync, destinations=list(range(40, 60)))
+        promotion = prepare_promote(coordinator, request, sync)
+        destination = promotion.destination
+        assert len(destination) == -(-length // PAGE) * PAGE
         grown = commit_promote(promotion, published.append, sync)
-        assert published == [2, 2] and promotion.status == "committed"
-        assert mapping[logical].tolist() == list(range(40, 60))
-        assert grown >= 0 and 2 not in coordinator.host_backed and 2 not in coordinator.hot
-        for i in range(20):
-            assert torch.equal(pool.page_view(40 + i), original[i]), i
-        assert engine.host_free.count == 32
-        with pytest.raises(RuntimeError, match="missing committed host KV"):
+        assert published == [2, 2] and grown >= 0
+        logical = coordinator.req_to_token[2, :length]
+        assert torch.equal(coordinator.mapping[logical], destination[:length])
+        truth.check_slots(destination[:length], range(length), "promoted tokens")
+        assert host.free_rows == 1024 and 2 not in coordinator.hot_pages
+        assert estimator.samples("promotion") == 1 and estimator.bandwidth("promotion") > 0
+        with pytest.raises(RuntimeError, match="hot-buffer capacity"):
             prepare_promote(coordinator, request, sync)
     finally:
+        torch.cuda.synchronize()
         pool.close()
 
 
@@ -245,8 +363,8 @@ def test_full_tick_of_512_blocks_round_trips_byte_exact(gpu):
             sources = rng.choice(live, size=move, replace=False).tolist()
             free = sorted(set(range(1, blocks)) - set(live))
             targets = rng.choice(free, size=move, replace=False).tolist()
-            snapshot = torch.empty((move, layout.block_bytes), dtype=torch.uint8, device=gpu)
-            engine.pack(sources, snapshot)
+            # the expected bytes come from plain copies of the source pages, not from the pack kernel
+            snapshot = torch.stack([pool.page_view(p).clone() for p in sources])
             torch.cuda.synchronize()
             pool.allocate(targets)
             host = engine.round_trip(sources, targets)

@@ -318,73 +318,115 @@ def test_chunk_aware_plan_keeps_pages_sharing_chunks():
 
 # ------------------------------------------------------------------ transactions
 #
-# The order of side effects in the prepare / commit / abort split
-# (reference adaptive_sparse/migration.py:67-288): a demotion unpublishes the
-# mapping before any page is released and trims before it publishes the
-# request as host-backed; a promotion frees the host copy and the hot pages,
-# publishes the new mapping, trims, then publishes the request as resident.
-# A failed byte move gives back whatever the prepare took.
+# The prepare / commit / abort split of the reference's
+# adaptive_sparse/migration.py:67-288 over HiSparseCoordinator, with a fake
+# pool, host cache and row mover on the CPU: the order of side effects (a
+# demotion unpublishes the mapping before any page is released and trims
+# before it publishes the request as host-backed; a promotion frees the host
+# rows and the hot pages, publishes the new mapping, trims, then publishes the
+# request as resident), the hot-buffer state a demotion leaves, the host_len
+# rule of a promotion, and the clean-up of failed moves.
+
+PAGE, HOT = 4, 6            # padded hot buffer: ceil((6 + 1) / 4) * 4 = 8 slots = 2 pages
 
 
 class _FakePool:
     def __init__(self, log, backed=1000):
         self.log = log
+        self.page_size = PAGE
+        self.device = "cpu"
+        self.layout = SimpleNamespace(layers=3, kv=2, row_bytes=16)
         self.pages = None
         self.backing = SimpleNamespace(backed_bytes=backed)
-        self.free = SimpleNamespace(peek=lambda n: [(50, 50 + n)])
 
-    def release(self, pages):
-        self.log.append(("release", tuple(pages)))
+    def take(self, count):
+        pages = list(range(50, 50 + count))
+        self.allocate(pages)
+        return pages
 
     def allocate(self, pages):
         self.log.append(("allocate", tuple(pages)))
         self.backing.backed_bytes += 10 * len(pages)
+
+    def release(self, pages):
+        self.log.append(("release", tuple(pages)))
+
+    def slots(self, pages):
+        import torch
+
+        return (torch.tensor(pages).view(-1, 1) * PAGE + torch.arange(PAGE)).flatten()
 
     def trim(self):
         self.log.append(("trim",))
         return 0
 
 
-class _FakeEngine:
+class _FakeHost:
+    def __init__(self, log, rows=64):
+        self.log, self.next, self.rows = log, 200, rows
+
+    def alloc(self, count):
+        import torch
+
+        if count > self.rows:
+            return None
+        self.rows -= count
+        self.next += count
+        return torch.arange(self.next - count, self.next)
+
+    def free(self, rows):
+        self.log.append(("free_host", tuple(rows)))
+        self.rows += len(rows)
+
+
+class _FakeMover:
     def __init__(self, log, fail=None):
         self.log, self.fail = log, fail
 
-    def demote(self, pages):
-        if self.fail == "demote":
+    def _log(self, kind, src, dst):
+        from adaptive_sparse.migration import Transfer
+
+        if self.fail == kind:
             raise OSError("copy failed")
-        self.log.append(("demote", tuple(pages)))
-        return SimpleNamespace(pages=list(pages))
+        self.log.append((kind, tuple(src.tolist()), tuple(dst.tolist())))
+        return Transfer(len(src) * 96)
 
-    def promote(self, host, destinations):
-        if self.fail == "promote":
-            raise OSError("copy failed")
-        self.log.append(("promote", tuple(destinations)))
+    def pool_to_host(self, slots, rows):
+        return self._log("d2h", slots, rows)
 
-    def release_host(self, host):
-        self.log.append(("release_host", tuple(host.pages)))
+    def host_to_pool(self, rows, slots):
+        return self._log("h2d", rows, slots)
+
+    def pool_to_pool(self, src, dst):
+        return self._log("d2d", src, dst)
 
 
-def _coordinator(log, fail=None, keep=2):
+PAGES = [7, 3, 9, 12, 5]    # the request's pages, in logical order
+
+
+def _coordinator(log, fail=None, length=20):
     import torch
 
-    from adaptive_sparse.migration import MigrationCoordinator
+    from adaptive_sparse.migration import HiSparseCoordinator, MigrationRequest
 
-    mapping = torch.zeros(16, dtype=torch.int64)
-    mapping[4:9] = torch.tensor([11, 12, 13, 14, 15])
-    return MigrationCoordinator(_FakePool(log), _FakeEngine(log, fail), mapping, keep_pages=keep)
+    coordinator = HiSparseCoordinator(_FakePool(log), _FakeHost(log), rows=4, max_len=64, logical_size=256,
+                                      hot_capacity=HOT, mover=_FakeMover(log, fail))
+    logical = torch.arange(100, 100 + length)
+    coordinator.req_to_token[1, :length] = logical
+    coordinator.mapping[logical] = (torch.tensor(PAGES).view(-1, 1) * PAGE + torch.arange(PAGE)).flatten()[:length]
+    return coordinator, MigrationRequest(row=1, length=length), logical
 
 
-def test_transactions_order_side_effects_and_clean_up_failures(monkeypatch):
-    import torch
+def _slots(pages):
+    return tuple(p * PAGE + i for p in pages for i in range(PAGE))
 
-    from adaptive_sparse.migration import (MigrationRequest, abort_promote, commit_demote, commit_promote,
-                                           prepare_demote, prepare_promote)
+
+def test_demotion_leaves_the_hisparse_hot_buffer_state(monkeypatch):
+    from adaptive_sparse.migration import commit_demote, prepare_demote
 
     monkeypatch.delenv("EKV_CHUNK_AWARE_RETENTION", raising=False)
     log = []
-    coordinator = _coordinator(log)
-    logical = torch.arange(4, 9)
-    request = MigrationRequest(row=3, logical=logical)
+    coordinator, request, logical = _coordinator(log)
     sync = lambda: log.append(("sync",))
 
     def publish(kind):
@@ -392,32 +434,89 @@ def test_transactions_order_side_effects_and_clean_up_failures(monkeypatch):
         return lambda row: log.append((kind, row, tuple(coordinator.mapping[logical].tolist())))
 
     prepared = prepare_demote(coordinator, request, sync)
-    assert log == [("sync",), ("demote", (11, 12, 13, 14, 15)), ("sync",)]
+    assert coordinator.padded_buffer_size == 8
+    assert log == [("sync",), ("d2h", _slots(PAGES), tuple(range(200, 220))), ("sync",)]
     assert prepared.retained_rows == (0, 1) and prepared.released_rows == (2, 3, 4)
-    assert coordinator.mapping[logical].tolist() == [11, 12, 13, 14, 15]   # ownership unchanged by prepare
+    assert coordinator.mapping[logical].tolist() == list(_slots(PAGES))         # ownership unchanged by prepare
+    assert coordinator.req_to_host_pool[1, :20].tolist() == list(range(200, 220))
     log.clear()
     assert commit_demote(prepared, publish("host"), sync, trim_quiescent=lambda: log.append(("trim",)) or 30) == 30
-    assert log == [("sync",), ("release", (13, 14, 15)), ("sync",), ("trim",), ("host", 3, (0, 0, 0, 0, 0))]
-    assert coordinator.hot[3] == (11, 12) and coordinator.host_backed[3].pages == [11, 12, 13, 14, 15]
+    assert log == [("sync",), ("release", (9, 12, 5)), ("sync",), ("trim",), ("host", 1, (0,) * 20)]
+    # the hot buffer: the retained pages' token slots, index HOT the reserved newest-token slot
+    assert coordinator.req_to_device_buffer[1].tolist() == list(_slots([7, 3]))
+    assert coordinator.newest_slot(1) == _slots([7, 3])[HOT]
+    assert coordinator.req_device_buffer_size[1] == 8 and coordinator.hot_pages[1] == (7, 3)
+    assert (coordinator.req_device_buffer_tokens[:, 1] == -1).all()
+    assert (coordinator.lru_slots[:, 1] == coordinator._lru_init).all()
+    assert coordinator.skip_first_backup[1]                                      # the host image is authoritative
+    with pytest.raises(RuntimeError, match="already been resolved"):
+        commit_demote(prepared, publish("host"), sync)
+    with pytest.raises(RuntimeError, match="unexpectedly owns"):
+        prepare_demote(coordinator, request, sync)
 
+
+def _demoted(log, length=20):
+    from adaptive_sparse.migration import commit_demote, prepare_demote
+
+    coordinator, request, logical = _coordinator(log, length=length)
+    commit_demote(prepare_demote(coordinator, request, lambda: None), lambda row: None, lambda: None)
     log.clear()
+    return coordinator, request, logical
+
+
+def test_promotion_of_an_authoritative_host_image_copies_every_token_from_host(monkeypatch):
+    from adaptive_sparse.migration import abort_promote, commit_promote, prepare_promote
+
+    monkeypatch.delenv("EKV_CHUNK_AWARE_RETENTION", raising=False)
+    log = []
+    coordinator, request, logical = _demoted(log)
+    sync = lambda: log.append(("sync",))
     promotion = prepare_promote(coordinator, request, sync)
-    assert log == [("allocate", (50, 51, 52, 53, 54)), ("promote", (50, 51, 52, 53, 54)), ("sync",)]
-    assert coordinator.mapping[logical].tolist() == [0] * 5              # unpublished until commit
+    # host_len == length: 20 host rows into the 5 new pages, nothing from the reserved slot
+    assert log == [("sync",), ("allocate", (50, 51, 52, 53, 54)),
+                   ("h2d", tuple(range(200, 220)), _slots(range(50, 55))), ("sync",)]
+    assert coordinator.mapping[logical].tolist() == [0] * 20                      # unpublished until commit
     log.clear()
     abort_promote(promotion)
     assert log == [("release", (50, 51, 52, 53, 54)), ("trim",)] and promotion.status == "aborted"
     with pytest.raises(RuntimeError, match="prepared promotion"):
         abort_promote(promotion)
-
-    promotion = prepare_promote(coordinator, request, sync, destinations=[7, 6, 5, 4, 3])
+    promotion = prepare_promote(coordinator, request, lambda: None, destinations=[9, 8, 7, 6, 5])
     log.clear()
-    assert commit_promote(promotion, publish("gpu"), sync) == 50            # growth since this prepare: 5 pages
-    assert log == [("release_host", (11, 12, 13, 14, 15)), ("release", (11, 12)), ("sync",), ("trim",),
-                   ("gpu", 3, (7, 6, 5, 4, 3))]
-    assert 3 not in coordinator.hot and 3 not in coordinator.host_backed
+    published = []
+    assert commit_promote(promotion, lambda row: published.append(
+        (row, tuple(coordinator.mapping[logical].tolist()))), sync) == 50          # growth: 5 pages
+    assert log == [("free_host", tuple(range(200, 220))), ("release", (7, 3)), ("sync",), ("trim",)]
+    assert published == [(1, _slots([9, 8, 7, 6, 5]))]
+    assert 1 not in coordinator.hot_pages and coordinator.req_device_buffer_size[1] == 0
+    assert coordinator.req_to_host_pool_allocated_len[1] == 0 and (coordinator.req_to_host_pool[1] == -1).all()
     with pytest.raises(RuntimeError, match="already been resolved"):
-        commit_promote(promotion, publish("gpu"), sync)
+        commit_promote(promotion, lambda row: None, sync)
+
+
+def test_promotion_after_decode_takes_the_newest_token_from_the_reserved_slot(monkeypatch):
+    from adaptive_sparse.migration import prepare_promote
+
+    monkeypatch.delenv("EKV_CHUNK_AWARE_RETENTION", raising=False)
+    log = []
+    coordinator, request, logical = _demoted(log, length=20)
+    reserved = coordinator.newest_slot(1)
+    # decode step 1 (length 20 -> 21): the host already holds token 19, nothing to back up
+    assert coordinator.backup_previous_token(1, 20) is None and log == []
+    assert not coordinator.skip_first_backup[1]
+    # decode step 2 (21 -> 22): token 20, in the reserved slot, goes to a new host row
+    coordinator.backup_previous_token(1, 21)
+    assert log == [("d2h", (reserved,), (220,))]
+    assert coordinator.req_to_host_pool[1, 20] == 220 and coordinator.req_to_host_pool_allocated_len[1] == 21
+    log.clear()
+    request.length = 22
+    extended = list(range(100, 122))
+    coordinator.req_to_token[1, :22] = __import__("torch").tensor(extended)
+    prepare_promote(coordinator, request, lambda: None, destinations=[30, 31, 32, 33, 34, 35])
+    # host_len == length - 1 == 21: tokens 0..20 from host, token 21 from the reserved slot
+    destination = _slots(range(30, 36))
+    assert log == [("allocate", tuple(range(30, 36))), ("h2d", tuple(range(200, 221)), destination[:21]),
+                   ("d2d", (reserved,), destination[21:22])]
 
 
 def test_transactions_reject_bad_state_and_undo_failed_moves(monkeypatch):
@@ -428,28 +527,71 @@ def test_transactions_reject_bad_state_and_undo_failed_moves(monkeypatch):
     monkeypatch.delenv("EKV_CHUNK_AWARE_RETENTION", raising=False)
     sync = lambda: None
     log = []
-    coordinator = _coordinator(log)
+    coordinator, request, logical = _coordinator(log)
+    with pytest.raises(ValueError, match="fully committed long resident"):
+        prepare_demote(coordinator, MigrationRequest(row=1, length=7), sync)
+    coordinator.mapping[logical[5]] = 0
     with pytest.raises(RuntimeError, match="missing physical locations"):
-        prepare_demote(coordinator, MigrationRequest(row=0, logical=torch.arange(3, 6)), sync)
-    coordinator.mapping[5] = 11
+        prepare_demote(coordinator, request, sync)
+    coordinator.mapping[logical[5]] = 3 * PAGE + 1
+    coordinator.mapping[logical[4]] = 3 * PAGE + 1
+    with pytest.raises(RuntimeError, match="misaligned"):
+        prepare_demote(coordinator, request, sync)
+    coordinator.mapping[logical[4:8]] = torch.arange(4) + 7 * PAGE               # page 7 twice
     with pytest.raises(RuntimeError, match="reuses a physical page"):
-        prepare_demote(coordinator, MigrationRequest(row=0, logical=torch.arange(4, 9)), sync)
+        prepare_demote(coordinator, request, sync)
+    with pytest.raises(RuntimeError, match="hot-buffer capacity"):
+        prepare_promote(coordinator, request, sync)
+
+    log = []
+    coordinator, request, logical = _coordinator(log, fail="d2h")
+    with pytest.raises(OSError):
+        prepare_demote(coordinator, request, sync)
+    assert log == [("free_host", tuple(range(200, 220)))]                       # the host rows come back
+    assert coordinator.req_to_host_pool_allocated_len[1] == 0 and coordinator.mapping[logical].min() > 0
+
+    log = []
+    coordinator, request, logical = _demoted(log)
+    coordinator.req_to_host_pool[1, 7] = -1
     with pytest.raises(RuntimeError, match="missing committed host KV"):
-        prepare_promote(coordinator, MigrationRequest(row=0, logical=torch.arange(4, 9)), sync)
-
-    log = []
-    coordinator = _coordinator(log, fail="demote")
+        prepare_promote(coordinator, request, sync)
+    coordinator.req_to_host_pool[1, 7] = 207
+    coordinator.skip_first_backup[1] = False                                   # a decode step happened ...
+    coordinator.req_to_device_buffer[1, HOT] = 0                               # ... but no newest token is held
+    with pytest.raises(RuntimeError, match="latest device token"):
+        prepare_promote(coordinator, request, sync)
+    coordinator.skip_first_backup[1] = True
+    coordinator.mover.fail = "h2d"
     with pytest.raises(OSError):
-        prepare_demote(coordinator, MigrationRequest(row=1, logical=torch.arange(4, 9)), sync)
-    assert log == [] and coordinator.mapping[4:9].tolist() == [11, 12, 13, 14, 15]
+        prepare_promote(coordinator, request, sync)
+    assert log == [("allocate", (50, 51, 52, 53, 54)), ("release", (50, 51, 52, 53, 54)), ("trim",)]
+    assert coordinator.req_to_host_pool_allocated_len[1] == 20                 # the host copy survives
+    with pytest.raises(ValueError, match="needs 5 destination pages"):
+        prepare_promote(coordinator, request, sync, destinations=[1, 2])
 
+
+def test_transactions_feed_the_bandwidth_estimator(monkeypatch):
+    from adaptive_sparse.migration import (abort_promote, commit_demote, commit_promote, prepare_demote,
+                                           prepare_promote)
+    from adaptive_sparse.migration_budget import MigrationBandwidthEstimator
+
+    monkeypatch.delenv("EKV_CHUNK_AWARE_RETENTION", raising=False)
     log = []
-    coordinator = _coordinator(log, fail="promote")
-    coordinator.host_backed[2] = SimpleNamespace(pages=[1, 2])
-    with pytest.raises(OSError):
-        prepare_promote(coordinator, MigrationRequest(row=2, logical=torch.arange(0, 2)), sync)
-    assert log == [("allocate", (50, 51)), ("release", (50, 51)), ("trim",)]
-    assert 2 in coordinator.host_backed                                     # the host copy survives
+    coordinator, request, _ = _coordinator(log)
+    coordinator.bandwidth = MigrationBandwidthEstimator(1 << 30, 0.5)
+    seconds = iter([0.002, 0.004])                                 # the committed demotion, then promotion
+    from adaptive_sparse import migration
+
+    monkeypatch.setattr(migration.Transfer, "seconds", lambda self: next(seconds))
+    prepared = prepare_demote(coordinator, request, lambda: None)
+    assert coordinator.bandwidth.samples("demotion") == 0          # only committed migrations count
+    commit_demote(prepared, lambda row: None, lambda: None)
+    assert coordinator.bandwidth.bandwidth("demotion") == 20 * 96 / 0.002
+    abort_promote(prepare_promote(coordinator, request, lambda: None))
+    assert coordinator.bandwidth.samples("promotion") == 0
+    commit_promote(prepare_promote(coordinator, request, lambda: None), lambda row: None, lambda: None)
+    assert coordinator.bandwidth.samples("promotion") == 1
+    assert coordinator.bandwidth.bandwidth("promotion") == 20 * 96 / 0.004
 
 
 # ------------------------------------------------------------------ estimator
