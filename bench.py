@@ -97,6 +97,8 @@ def parse_args():
     parser.add_argument("--capacity", type=int, default=4096, help="hot slots per request (decode-read)")
     parser.add_argument("--spare-chunks", type=int, default=0,
                         help="VMM spare pool of the migration and composite pools (0: release at once)")
+    parser.add_argument("--serial-remap", action="store_true",
+                        help="composite: remap with the GPU idle before the step's kernels (no overlap)")
     parser.add_argument("--seed", type=int, default=2024)
     parser.add_argument("--cpu-seconds", type=float, default=8.0,
                         help="bound of each CPU baseline sample (per thread count)")
@@ -733,25 +735,32 @@ def run_migration(torch, args, device):
     gen = torch.Generator(device=device).manual_seed(args.seed)
     for page in live:
         pool.page_view(page).view(torch.bfloat16).normal_(generator=gen)
+    # The tick runs on a non-blocking stream: a HIP VMM unmap waits for the work queued on the legacy
+    # null stream, not for other streams', so the sources' unmaps then overlap the PCIe legs and unpacks
+    # (which never touch the unmapped chunks) instead of waiting for them.
+    stream = torch.cuda.Stream(device)
+    torch.cuda.set_stream(stream)
     engine = MigrationEngine(pool, max_pages=MOVE, sub_batch=64)
     snapshot = torch.empty((MOVE, layout.block_bytes), dtype=torch.uint8, device=device)
     moved = 2 * MOVE * layout.block_bytes
     ticks, verified = [], True
-    phases = {"map_s": [], "move_s": [], "trim_s": []}
+    phases = {"map_s": [], "move_s": [], "trim_s": [], "mapped": [], "unmapped": []}
     for tick in range(args.warmup + args.steps):
         sources = rng.choice(live, size=MOVE, replace=False).tolist()
         free = sorted(set(range(1, BLOCKS)) - set(live))
         targets = rng.choice(free, size=MOVE, replace=False).tolist()
         engine.pack(sources, snapshot)                  # reference copy, outside the timed tick
         torch.cuda.synchronize()
+        backed_before = len(pool.backing.mapped_chunks)
         t0 = time.perf_counter()
         pool.allocate(targets)                          # hipMemMap-commit + zero the destination chunks
         t1 = time.perf_counter()
+        mapped_now = len(pool.backing.mapped_chunks)
         host = engine.round_trip(sources, targets)      # pack -> D2H -> H2D -> unpack, pipelined
         pool.release(sources)
-        pool.trim(after=host.packed, pages=sources)     # unmap chunks only the sources used, once packed,
-        t2 = time.perf_counter()                        # while the PCIe legs and unpacks still run
-        torch.cuda.synchronize()
+        unmapped = pool.trim(after=host.packed, pages=sources) // layout.chunk_bytes
+        t2 = time.perf_counter()                        # unmap chunks only the sources used, once packed,
+        torch.cuda.synchronize()                        # while the PCIe legs and unpacks still run
         t3 = time.perf_counter()
         engine.release_host(host)
         check = torch.empty_like(snapshot)
@@ -764,7 +773,20 @@ def run_migration(torch, args, device):
             phases["map_s"].append(t1 - t0)
             phases["move_s"].append(t3 - t1)            # round trip, with the unmap overlapped
             phases["trim_s"].append(t2 - t1)            # issue + wait for the packs + release and unmap
+            phases["mapped"].append(mapped_now - backed_before)
+            phases["unmapped"].append(unmapped)
     tick_s = statistics.mean(ticks)
+    map_chunks, unmap_chunks = statistics.mean(phases["mapped"]), statistics.mean(phases["unmapped"])
+    # GPU-only time of one pipelined round trip (no VMM call beside it), to set against the tick.
+    sources = rng.choice(live, size=MOVE, replace=False).tolist()
+    ev_rt = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    torch.cuda.synchronize()
+    ev_rt[0].record()
+    host = engine.round_trip(sources, sources)          # back into the same pages: the bytes do not change
+    ev_rt[1].record()
+    torch.cuda.synchronize()
+    engine.release_host(host)
+    gpu_round_trip_ms = ev_rt[0].elapsed_time(ev_rt[1])
     # Phase breakdown of one non-pipelined move (events per stream).
     sources = torch.tensor(rng.choice(live, size=MOVE, replace=False).tolist(), device=device)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
@@ -818,12 +840,19 @@ def run_migration(torch, args, device):
                           "release_and_unmap_overlapped": round(statistics.mean(phases["trim_s"]) * 1e3, 3),
                           "pack": round(pack_ms, 3), "d2h": round(d2h_ms, 3), "h2d": round(h2d_ms, 3),
                           "unpack": round(unpack_ms, 3)},
+             "gpu_round_trip_ms": round(gpu_round_trip_ms, 3),
+             "vmm_chunks_per_tick": {"mapped": round(map_chunks, 1), "unmapped": round(unmap_chunks, 1)},
+             "vmm_us_per_chunk": {
+                 "map_and_zero": round(statistics.mean(phases["map_s"]) * 1e6 / max(map_chunks, 1), 1),
+                 "release_and_unmap": round(statistics.mean(phases["trim_s"]) * 1e6 / max(unmap_chunks, 1), 1)},
              "link_gbs": {"d2h": round(one_way / (d2h_ms / 1e3) / 1e9, 2),
                           "h2d": round(one_way / (h2d_ms / 1e3) / 1e9, 2), "peak_per_direction": PCIE_PEAK_GBS},
              "pack_gbs": round(pack_bytes / (pack_ms / 1e3) / 1e9, 1),
              "unpack_gbs": round(pack_bytes / (unpack_ms / 1e3) / 1e9, 1)}
     result = envelope(args, moved / tick_s / 1e9, tick_s * 1e3, config, roof, baseline, extra,
                       metric="migrated GB/s (D2H + H2D bytes per tick / tick time), 1 GPU")
+    torch.cuda.synchronize()
+    torch.cuda.set_stream(torch.cuda.default_stream(device))
     pool.close()
     return result
 
@@ -1264,9 +1293,12 @@ def run_composite(torch, args, device):
 
     remap_parts = {"invalidate_ms": [], "unmap_ms": [], "map_ms": []}
 
-    def remap():
-        """Unmap + remap `remap_count` random chunks (never chunk 0); their hot slots become empty."""
-        r0 = time.perf_counter()
+    def invalidate():
+        """Choose `remap_count` random chunks (never chunk 0) and empty their hot slots (queued, no wait).
+
+        Returns the chunk ids and the [L, R] mask of the (layer, request) items whose slots they hold: a
+        2 MiB chunk of a plane is 4096 rows of 512 B, so it holds (most of) one request's hot buffer.
+        """
         chosen = rng.choice(np.arange(1, backing.chunk_count), size=remap_count, replace=False)
         ids = torch.tensor(chosen, device=device)
         plane, within = ids // layout.plane_chunks, ids % layout.plane_chunks
@@ -1281,13 +1313,26 @@ def run_composite(torch, args, device):
         buffers.slot_token[layer, req, loc] = -1
         buffers.stamps[layer, req, loc] = INT32_MIN
         build_residency_bits(buffers.table, out=buffers.bits)
+        touched = torch.zeros((L, R), dtype=torch.bool, device=device)
+        touched[layer, req] = True
+        return chosen.tolist(), touched
+
+    def remap_chunks(chosen):
+        r1 = time.perf_counter()
+        backing.reclaim(chosen, synchronize=False)   # hipMemUnmap + release (or keep); no kernel uses them
+        r2 = time.perf_counter()
+        backing.ensure(chosen)                       # hipMemCreate + map + access + zero fill
+        r3 = time.perf_counter()
+        return r2 - r1, r3 - r2
+
+    def remap():
+        """Unmap + remap the chosen chunks with the GPU idle (the form the graph replays below use)."""
+        r0 = time.perf_counter()
+        chosen, _ = invalidate()
         torch.cuda.synchronize()
         r1 = time.perf_counter()
-        backing.reclaim(chosen.tolist())          # synchronizes, then hipMemUnmap + release (or keep)
-        r2 = time.perf_counter()
-        backing.ensure(chosen.tolist())           # hipMemCreate + map + access + zero fill
-        r3 = time.perf_counter()
-        for key, value in zip(remap_parts, (r1 - r0, r2 - r1, r3 - r2)):
+        unmap_s, map_s = remap_chunks(chosen)
+        for key, value in zip(remap_parts, (r1 - r0, unmap_s, map_s)):
             remap_parts[key].append(value * 1e3)
 
     topk = torch.zeros((L, R, K), dtype=torch.int32, device=device)   # refilled in place every step
@@ -1305,7 +1350,8 @@ def run_composite(torch, args, device):
     def gather():
         gather_kv(planes, slots, output)
 
-    phases = {name: [] for name in ("remap_ms", "lookup_ms", "swap_ms", "promote_ms", "gather_ms", "step_ms")}
+    phases = {name: [] for name in ("remap_ms", "lookup_ms", "swap_ms", "promote_ms", "gather_ms", "step_ms",
+                                    "gpu_beside_remap_ms", "after_remap_ms")}
     promoted, verified = [], True
     def verify():
         # every lane is resident after the step: its gathered rows must be its token's host rows
@@ -1319,33 +1365,64 @@ def run_composite(torch, args, device):
                 ok &= bool(torch.equal(got, expect))
         return ok
 
+    # The step runs on a non-blocking stream. A HIP VMM unmap waits for the work queued on the legacy null
+    # stream but not for other streams' (measured: 50 unmaps took 55.6 ms behind a 42 ms kernel on the null
+    # stream, 12.4 ms behind one on a side stream, 13.2 ms idle), so the remap's driver calls run on the
+    # host while the kernels that never touch the remapped chunks run on the GPU:
+    #   queue: invalidate the chosen chunks' slots -> lookup -> swap-in -> promote of the items whose
+    #          hot buffers the chunks do not hold
+    #   host:  unmap (+ release) and re-commit (map + zero fill, waited for) the chosen chunks
+    #   queue: promote of the items whose hot buffers they hold (into the fresh chunks) -> gather
+    # The chunks' last readers are the previous step's kernels, which the step boundary has drained.
+    stream = torch.cuda.Stream(device)
+    torch.cuda.set_stream(stream)
+    counts_beside = torch.empty_like(counts)
+    counts_after = torch.empty_like(counts)
+    step_remap = {"queue_ms": [], "unmap_ms": [], "map_ms": []}
     for step in range(args.warmup + args.steps):
         topk.copy_(composite_topk(torch, device, L, R, K, lengths, gen))
         torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(7)]
         t0 = time.perf_counter()
-        if remap_count:
-            remap()
-        t1 = time.perf_counter()
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+        chosen, touched = invalidate() if remap_count else ([], torch.zeros((L, R), dtype=torch.bool, device=device))
         ev[0].record()
         lookup()
         ev[1].record()
         swap()
         ev[2].record()
-        promote()
+        torch.where(touched, torch.zeros_like(counts), counts, out=counts_beside)
+        torch.where(touched, counts, torch.zeros_like(counts), out=counts_after)
+        move_kv(host_planes, promote_src, planes, promote_dst, counts_beside)
         ev[3].record()
-        gather()
-        ev[4].record()
-        torch.cuda.synchronize()
+        if args.serial_remap:
+            torch.cuda.synchronize()            # the comparison form: the driver calls with the GPU idle
+        t1 = time.perf_counter()
+        unmap_s, map_s = remap_chunks(chosen) if chosen else (0.0, 0.0)
         t2 = time.perf_counter()
+        ev[6].record()                          # the stream restarts here (it may have gone idle meanwhile)
+        move_kv(host_planes, promote_src, planes, promote_dst, counts_after)
+        ev[4].record()
+        gather()
+        ev[5].record()
+        torch.cuda.synchronize()
+        t3 = time.perf_counter()
         promoted.append(int(counts.sum().item()))
         if step == args.warmup + args.steps - 1 or step == 0:
             verified &= verify()
         if step >= args.warmup:
-            phases["remap_ms"].append((t1 - t0) * 1e3)
-            for i, name in enumerate(("lookup_ms", "swap_ms", "promote_ms", "gather_ms")):
-                phases[name].append(ev[i].elapsed_time(ev[i + 1]))
-            phases["step_ms"].append((t2 - t0) * 1e3)
+            phases["remap_ms"].append((t2 - t1) * 1e3)
+            step_remap["queue_ms"].append((t1 - t0) * 1e3)
+            step_remap["unmap_ms"].append(unmap_s * 1e3)
+            step_remap["map_ms"].append(map_s * 1e3)
+            phases["lookup_ms"].append(ev[0].elapsed_time(ev[1]))
+            phases["swap_ms"].append(ev[1].elapsed_time(ev[2]))
+            phases["promote_ms"].append(ev[2].elapsed_time(ev[3]) + ev[6].elapsed_time(ev[4]))
+            phases["gather_ms"].append(ev[4].elapsed_time(ev[5]))
+            phases["gpu_beside_remap_ms"].append(ev[0].elapsed_time(ev[3]))
+            phases["after_remap_ms"].append((t3 - t2) * 1e3)
+            phases["step_ms"].append((t3 - t0) * 1e3)
+    torch.cuda.synchronize()
+    torch.cuda.set_stream(torch.cuda.default_stream(device))
     # The same step replayed from one HIP graph (the swap-in reads its LRU step from
     # the device counter), with the chunk remap between replays.
     graph = torch.cuda.CUDAGraph()
@@ -1378,9 +1455,13 @@ def run_composite(torch, args, device):
     # its list entry, Top-K id, host row and victim's token read, the patched slot, the victim's token, the two int16
     # table entries, the two summary words and the two promotion entries written (44 B).
     swap_bytes = L * R * (8 * C + 4 * K + 4) + misses_per_step * 44
-    log(f"step {mean['step_ms']:.1f} ms = remap {mean['remap_ms']:.1f} + lookup {mean['lookup_ms']:.3f} + swap "
-        f"{mean['swap_ms']:.3f} + promote {mean['promote_ms']:.2f} + gather {mean['gather_ms']:.2f} ms; "
-        f"{misses_per_step / lanes:.3f} of lanes promoted; verified {verified}")
+    serial_gpu = mean["lookup_ms"] + mean["swap_ms"] + mean["promote_ms"] + mean["gather_ms"]
+    log(f"step {mean['step_ms']:.1f} ms: remap {mean['remap_ms']:.1f} ms (unmap "
+        f"{statistics.mean(step_remap['unmap_ms'] or [0]):.1f} + map {statistics.mean(step_remap['map_ms'] or [0]):.1f})"
+        f" beside {mean['gpu_beside_remap_ms']:.1f} ms of GPU work, then {mean['after_remap_ms']:.1f} ms; GPU work "
+        f"lookup {mean['lookup_ms']:.3f} + swap {mean['swap_ms']:.3f} + promote {mean['promote_ms']:.2f} + gather "
+        f"{mean['gather_ms']:.2f} = {serial_gpu:.1f} ms; {misses_per_step / lanes:.3f} of lanes promoted; "
+        f"verified {verified}")
     config = {"workload": "composite-elastic-decode", "requests": R, "context": "uniform [4096, 32768]", "layers": L,
               "kv_heads": 2, "head_dim": 128, "topk": K, "hot_capacity": C, "remap_fraction": args.remap_fraction,
               "spare_chunks": args.spare_chunks,
@@ -1394,9 +1475,16 @@ def run_composite(torch, args, device):
                          "gbs": round(swap_bytes / (mean["swap_ms"] / 1e3) / 1e9, 1),
                          "frac_of_hbm_peak": round(swap_bytes / (mean["swap_ms"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4)},
              "lookups_per_s": round(lanes / (mean["lookup_ms"] / 1e3), 1),
-             "step_ms_without_remap": round(mean["step_ms"] - mean["remap_ms"], 3),
-             "remap_parts_ms": {k: round(statistics.mean(v[args.warmup:] or v), 2) if v else 0.0
-                                for k, v in remap_parts.items()},
+             "gpu_work_ms": round(serial_gpu, 3), "serial_remap": bool(args.serial_remap),
+             "overlap": "the remap's unmap + map run on the host beside the lookup, swap-in and the promote of the "
+                        "items whose hot buffers the remapped chunks do not hold (a non-blocking stream); the other "
+                        "items' promote and the gather follow",
+             "remap_parts_ms": {k: round(statistics.mean(v), 2) if v else 0.0 for k, v in step_remap.items()},
+             "vmm_us_per_chunk": {
+                 "unmap_and_release" if not args.spare_chunks else "unmap":
+                     round(statistics.mean(step_remap["unmap_ms"]) * 1e3 / remap_count, 1) if remap_count else None,
+                 "map_and_zero": round(statistics.mean(step_remap["map_ms"]) * 1e3 / remap_count, 1)
+                 if remap_count else None},
              "remapped_chunks_per_step": remap_count, "pool_commit_s": round(commit_s, 3),
              "graph_replay": {"replays": len(graph_ms), "gpu_ms_per_step": round(statistics.mean(graph_ms), 3),
                               "verified_against_host_copy": graph_verified}}
@@ -1487,7 +1575,8 @@ def summary(result):
     keys = ("metric", "value", "unit", "ms_per_step", "roofline", "cpu_baseline", "config", "lookup_us_per_step",
             "hit_rate", "verified_round_trip", "tick_ms", "link_gbs", "pack_gbs", "unpack_gbs", "phase_ms",
             "higher_is_better", "vs_baseline", "per_batch", "correct", "verified_against_host_copy",
-            "step_ms_without_remap", "remap_parts_ms", "promote_gbs_over_pcie", "swap_in", "graph_replay",
+            "gpu_work_ms", "overlap", "remap_parts_ms", "vmm_us_per_chunk", "vmm_chunks_per_tick",
+            "gpu_round_trip_ms", "promote_gbs_over_pcie", "swap_in", "graph_replay",
             "per_support_set", "verified_against_torch", "shift0")
     return {key: result[key] for key in keys if key in result}
 

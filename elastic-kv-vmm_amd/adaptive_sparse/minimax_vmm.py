@@ -106,7 +106,10 @@ class PhysicalPages:
         return set(self.backing.mapped_chunks).difference(self.refs)
 
     def stats(self):
-        return {"backed_bytes": self.backing.backed_bytes,
+        """backed (mapped) bytes, spare bytes (unmapped chunks the backing's spare pool still
+        holds: a trim into the pool releases no device memory), reclaimable bytes, owned pages."""
+        spare = getattr(self.backing, "spare_bytes", 0)
+        return {"backed_bytes": self.backing.backed_bytes, "spare_bytes": spare,
                 "reclaimable_bytes": len(self.reclaimable_chunks()) * self.chunk_bytes,
                 "owned_pages": len(self.pages) - 1, "trim_sync_ns": self.trim_sync_ns}
 

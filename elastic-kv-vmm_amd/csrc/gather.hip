@@ -30,28 +30,20 @@
 #include <algorithm>
 #include <stdexcept>
 #include <atomic>
-#include <cstdlib>
 #include <type_traits>
 
 namespace ekv {
 namespace {
 
-#ifndef EKV_COPY_UNROLL
-#define EKV_COPY_UNROLL 8
-#endif
-
 constexpr int kThreads = 256;
-constexpr int kUnroll = EKV_COPY_UNROLL;  // independent VW-byte loads in flight per lane
+constexpr int kUnroll = 8;  // independent VW-byte loads in flight per lane
 // KV gathers of small rows reserve LDS they do not use, so that at most 3 of
 // their workgroups share a CU (160 KiB of LDS per CU on MI355X; 4 KiB static
 // + 48 KiB reserved per workgroup). Fewer gathers in flight per CU measured
 // faster on the decode shapes: 5 per CU (the register limit) 5.08 ms, 4 per
 // CU 5.01 ms, 3 per CU 4.91 ms, 2 per CU 5.06 ms for 31.5 M rows of 512 B.
 // (Large rows, and the lookup kernels, measured no gain from fewer groups.)
-#ifndef EKV_GATHER_LDS_RESERVE
-#define EKV_GATHER_LDS_RESERVE 49152
-#endif
-constexpr size_t kGatherLdsReserve = EKV_GATHER_LDS_RESERVE;
+constexpr size_t kGatherLdsReserve = 49152;
 // MI355X has 8 XCDs; workgroups are dispatched to them round robin. Dealing
 // each XCD one contiguous range of tiles keeps neighbouring rows (same
 // request region of a plane, adjacent slot reads) on one XCD's L2 and TLBs:
@@ -201,22 +193,14 @@ __device__ __forceinline__ void locate(const EngineArgs& a, int64_t u, int64_t& 
     }
 }
 
-#ifndef EKV_COPY_NT_LOAD
-#define EKV_COPY_NT_LOAD 0
-#endif
-#ifndef EKV_COPY_NT_STORE
-#define EKV_COPY_NT_STORE 1
-#endif
-
+// Loads are plain (cached) and stores non-temporal: the copied rows are not
+// read again by this kernel, and streaming them past the caches keeps the
+// L2 for the row offsets and the source rows.
 template <int VW>
 __device__ __forceinline__ typename Vec<VW>::type load_vec(const char* p, bool aligned) {
     using V = typename Vec<VW>::type;
     if (aligned) {
-#if EKV_COPY_NT_LOAD
-        return __builtin_nontemporal_load(reinterpret_cast<const V*>(p));
-#else
         return *reinterpret_cast<const V*>(p);
-#endif
     }
     V v;
     __builtin_memcpy(&v, p, VW);
@@ -226,11 +210,7 @@ __device__ __forceinline__ typename Vec<VW>::type load_vec(const char* p, bool a
 template <int VW>
 __device__ __forceinline__ void store_vec(char* p, typename Vec<VW>::type v) {
     using V = typename Vec<VW>::type;
-#if EKV_COPY_NT_STORE
     __builtin_nontemporal_store(v, reinterpret_cast<V*>(p));
-#else
-    *reinterpret_cast<V*>(p) = v;
-#endif
 }
 
 __device__ __forceinline__ int64_t tile_of(const EngineArgs& a, int64_t iteration_tile) {
@@ -339,14 +319,6 @@ __global__ __launch_bounds__(kThreads) void copy_large_rows(const EngineArgs a) 
     }
 }
 
-int64_t env_int(const char* name, int64_t fallback) {
-    const char* text = std::getenv(name);
-    if (text == nullptr || *text == '\0') {
-        return fallback;
-    }
-    return std::strtoll(text, nullptr, 10);
-}
-
 // Compute units of the current device (cached per device).
 int64_t device_cus() {
     static std::atomic<int> cached[64];
@@ -369,9 +341,7 @@ int64_t device_cus() {
 // gather) would fill only a fraction of the CUs with full tiles and take one
 // tile's latency on each; below this many workgroups per CU its tiles shrink
 // so that the grid reaches it (a tile keeps at least one row).
-#ifndef EKV_SMALL_JOB_GROUPS_PER_CU
-#define EKV_SMALL_JOB_GROUPS_PER_CU 2
-#endif
+constexpr int64_t kSmallJobGroupsPerCu = 2;
 
 template <int M, int VW>
 void launch_engine(EngineArgs a, hipStream_t stream) {
@@ -382,8 +352,8 @@ void launch_engine(EngineArgs a, hipStream_t stream) {
         a.rows_per_tile = static_cast<uint32_t>(std::min<int64_t>(kThreads, tile_bytes / a.row_bytes));
         a.vec_div = FastDiv(a.vecs_per_row);
         a.tiles = (a.units + a.rows_per_tile - 1) / a.rows_per_tile;
-        const int64_t wanted = EKV_SMALL_JOB_GROUPS_PER_CU * device_cus();
-        if (EKV_SMALL_JOB_GROUPS_PER_CU > 0 && a.tiles < wanted) {
+        const int64_t wanted = kSmallJobGroupsPerCu * device_cus();
+        if (a.tiles < wanted) {
             a.rows_per_tile = static_cast<uint32_t>(std::max<int64_t>(1, (a.units + wanted - 1) / wanted));
             a.tiles = (a.units + a.rows_per_tile - 1) / a.rows_per_tile;
         }
@@ -392,16 +362,9 @@ void launch_engine(EngineArgs a, hipStream_t stream) {
         a.segs_per_row = (a.row_bytes + tile_bytes - 1) / tile_bytes;
         a.tiles = a.units * a.segs_per_row;
     }
-    // Launch-shape knobs (defaults: one workgroup per tile, tiles dealt in
-    // XCD-contiguous ranges); the environment overrides them for sweeps.
-    const int64_t max_groups = env_int("EKV_COPY_MAX_WORKGROUPS", 0);
-    const int64_t xcd_groups = env_int("EKV_COPY_XCD_GROUPS", kXcdCount);
-    a.xcd_groups = small ? static_cast<uint32_t>(std::max<int64_t>(0, xcd_groups)) : 0u;
-    int64_t grid = a.tiles;
-    if (max_groups > 0) {
-        grid = std::min(grid, max_groups);
-    }
-    grid = std::min<int64_t>(grid, 0x7fffffff);
+    // One workgroup per tile; small-row tiles are dealt to the XCDs in contiguous ranges.
+    a.xcd_groups = small ? static_cast<uint32_t>(kXcdCount) : 0u;
+    const int64_t grid = std::min<int64_t>(a.tiles, 0x7fffffff);
     if (grid <= 0) {
         return;
     }

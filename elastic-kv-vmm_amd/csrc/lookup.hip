@@ -53,51 +53,22 @@
 namespace ekv {
 namespace {
 
-// Tuning knobs (compile-time; the defaults measured best on the 60-layer
-// decode shapes, 128 requests x 2048 lanes x 65,536-token tables):
-//   EKV_LOOKUP_THREADS / EKV_LOOKUP_ITERS  workgroup size and 64-lane
-//       iterations per wave (a row chunk is THREADS * ITERS lanes);
-//   EKV_LOOKUP_WINDOW        table entries of the recent window staged in LDS
-//       (a multiple of 128; 0 = off);
-//   EKV_LOOKUP_STAGE_BITS    stage bitmap rows of up to
-//       EKV_LOOKUP_STAGED_BIT_WORDS words in LDS (else lanes read their word);
-//   EKV_LOOKUP_DENSE         32-bit byte-offset addressing for unit-stride rows;
-//   EKV_LOOKUP_STREAMING     non-temporal Top-K loads and slot stores (read or
-//       written once): 3-5 % faster on the 60-layer shapes, and only with
-//       both (table lines, which lanes of a row share, keep the cache).
-#ifndef EKV_LOOKUP_THREADS
-#define EKV_LOOKUP_THREADS 256
-#endif
-#ifndef EKV_LOOKUP_ITERS
-#define EKV_LOOKUP_ITERS 8
-#endif
-#ifndef EKV_LOOKUP_WINDOW
-#define EKV_LOOKUP_WINDOW 1024
-#endif
-#ifndef EKV_LOOKUP_STAGE_BITS
-#define EKV_LOOKUP_STAGE_BITS 1
-#endif
-#ifndef EKV_LOOKUP_STAGED_BIT_WORDS
-#define EKV_LOOKUP_STAGED_BIT_WORDS 4096
-#endif
-#ifndef EKV_LOOKUP_DENSE
-#define EKV_LOOKUP_DENSE 1
-#endif
-#ifndef EKV_LOOKUP_STREAMING
-#define EKV_LOOKUP_STREAMING 1
-#endif
-//   EKV_LOOKUP_RUNS          int16 local-slot lookups with block size 1 and
-//       16-byte aligned rows give each thread two contiguous 4-lane pieces
-//       (resolve_local_runs) instead of 8 strided 64-lane iterations.
-#ifndef EKV_LOOKUP_RUNS
-#define EKV_LOOKUP_RUNS 1
-#endif
-constexpr int kThreads = EKV_LOOKUP_THREADS;
-constexpr int kIters = EKV_LOOKUP_ITERS;        // 64-lane iterations per wave per chunk
+// Launch shape (measured best on the 60-layer decode shapes, 128 requests x
+// 2048 lanes x 65,536-token tables): 256-thread workgroups walking a row in
+// chunks of 8 64-lane iterations per wave; a recent window of 1024 table
+// entries staged in LDS for the strided int32 form; summary rows of up to
+// 4096 words staged in LDS (else lanes read their word); 32-bit byte-offset
+// addressing for unit-stride rows; non-temporal Top-K loads and slot stores
+// (read or written once: 3-5 % faster, and only with both, since the table
+// lines that lanes of a row share keep the cache). int16 local-slot lookups
+// with block size 1 and 16-byte aligned rows give each thread two contiguous
+// 4-lane pieces (resolve_local_runs) instead of 8 strided 64-lane iterations.
+constexpr int kThreads = 256;
+constexpr int kIters = 8;                       // 64-lane iterations per wave per chunk
 constexpr int kWaveSpan = 64 * kIters;          // 512 lanes per wave per chunk
 constexpr int kChunkLanes = kThreads * kIters;  // 2048 lanes per chunk
-constexpr int kStagedBitWords = EKV_LOOKUP_STAGED_BIT_WORDS;  // 4096 words: T <= 131072 tokens
-constexpr int kWindow = EKV_LOOKUP_WINDOW;
+constexpr int kStagedBitWords = 4096;           // 4096 words: T <= 131072 tokens
+constexpr int kWindow = 1024;
 static_assert(kWindow % 128 == 0, "the window must keep 16-byte alignment of the staged bitmap");
 static_assert(kThreads % 64 == 0 && kThreads <= 1024, "whole waves per workgroup");
 
@@ -144,23 +115,15 @@ inline int64_t summary_words(int64_t cols, int64_t shift) {
 }
 
 // Loads and stores of data touched once per launch (Top-K indices, slots),
-// with the non-temporal hint when EKV_LOOKUP_STREAMING is set.
+// with the non-temporal hint.
 template <typename T>
 __device__ __forceinline__ T stream_load(const T* p) {
-#if EKV_LOOKUP_STREAMING
     return __builtin_nontemporal_load(p);
-#else
-    return *p;
-#endif
 }
 
 template <typename T>
 __device__ __forceinline__ void stream_store(T value, T* p) {
-#if EKV_LOOKUP_STREAMING
     __builtin_nontemporal_store(value, p);
-#else
-    *p = value;
-#endif
 }
 
 // Element `index` of a row at `base` with element stride `stride`. The dense
@@ -480,13 +443,10 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 // half, a thread's miss count (0..4) is ranked inside its wave by three
 // bit-plane ballots and across waves by one LDS exchange of wave totals; a
 // thread puts its misses in lane order from its rank on, so the list is the
-// same ascending list as the strided form's. With EKV_LOOKUP_MISS_LDS (the
-// default) the chunk's list is assembled in LDS and then written out by
-// consecutive threads, so its stores are coalesced instead of one scattered
-// 4-byte store per miss: 11-13 % faster on the 60-layer decode shapes.
-#ifndef EKV_LOOKUP_MISS_LDS
-#define EKV_LOOKUP_MISS_LDS 1
-#endif
+// same ascending list as the strided form's. The chunk's list is assembled
+// in LDS and then written out by consecutive threads, so its stores are
+// coalesced instead of one scattered 4-byte store per miss: 11-13 % faster
+// on the 60-layer decode shapes.
 template <bool kCompact>
 __device__ __forceinline__ void resolve_local_runs(const LookupArgs& a) {
     static_assert(kIters == 8, "two 4-lane pieces per thread");
@@ -495,9 +455,7 @@ __device__ __forceinline__ void resolve_local_runs(const LookupArgs& a) {
     constexpr int kWaves = kThreads / 64;
     extern __shared__ __align__(16) uint32_t lds[];   // the staged bitmap row
     __shared__ int32_t wave_totals[2 * kWaves];       // [half][wave]
-#if EKV_LOOKUP_MISS_LDS
     __shared__ int32_t chunk_misses[kChunkLanes];
-#endif
     const int64_t row = a.selected.fetch(blockIdx.x);
     if (row < 0 || row >= a.batch) {
         return;  // uniform over the workgroup
@@ -612,21 +570,14 @@ __device__ __forceinline__ void resolve_local_runs(const LookupArgs& a) {
             for (int j = 0; j < kIters; ++j) {
                 if ((miss >> j) & 1u) {
                     const int32_t lane_id = static_cast<int32_t>(first[j / kPiece] + j % kPiece);
-#if EKV_LOOKUP_MISS_LDS
                     chunk_misses[rank[j / kPiece]] = lane_id;
-#else
-                    // Cached, as in the strided form: list ends fall mid-line.
-                    *element<true>(misses, 1, static_cast<uint32_t>(running + rank[j / kPiece])) = lane_id;
-#endif
                     ++rank[j / kPiece];
                 }
             }
-#if EKV_LOOKUP_MISS_LDS
             __syncthreads();
             for (int32_t i = threadIdx.x; i < chunk_total; i += kThreads) {
                 *element<true>(misses, 1, static_cast<uint32_t>(running + i)) = chunk_misses[i];
             }
-#endif
             __syncthreads();  // wave_totals (and the staged list) are rewritten by the next chunk
             running += chunk_total;
         }
@@ -660,12 +611,6 @@ void resolve_runs_kernel(const LookupArgs a) {
 // cannot sink a load into the branch that consumes it and serialize the
 // staging; the last iteration's loads for a next item that does not exist read
 // one line of each row. Results equal the contiguous-pieces kernel's.
-#ifndef EKV_LOOKUP_PIPE
-#define EKV_LOOKUP_PIPE 1
-#endif
-#ifndef EKV_LOOKUP_PIPE_GRID
-#define EKV_LOOKUP_PIPE_GRID 1   // 1: persistent grid (resident workgroups); 0: one item per workgroup
-#endif
 constexpr uint32_t kPipeBitPieces = 2 * kThreads;   // 16-byte bitmap pieces per item at most: 2048 words
 constexpr uint32_t kPipeMaxItems = 16;              // items per workgroup
 constexpr uint32_t kNoRow = 0xffffffffu;
@@ -985,9 +930,6 @@ __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupAr
 // of the workgroup's index metadata: one dependent memory level fewer before
 // the first table reads (0.5-0.7 us of a 60-layer launch inside a decode
 // step, 2 us of a 30-layer one).
-#ifndef EKV_LOOKUP_PIPE2
-#define EKV_LOOKUP_PIPE2 1
-#endif
 
 // One item between its two stages: its table entries in flight and its lanes'
 // classification.
@@ -1303,25 +1245,19 @@ void launch_runs_pipe_loads(const LookupArgs& a, dim3 grid, hipStream_t stream) 
     const uint32_t count = grid.x;
     const uint32_t items = grid.x * grid.y;   // below 2^31 (checked by the host)
     // Resident workgroups, or more when they would take over kPipeMaxItems items each.
-    const uint32_t groups =
-        EKV_LOOKUP_PIPE_GRID
-            ? std::min(items, std::max(runs_pipe_resident<kCompact, TableT, kBitLoads>(),
-                                       (items + kPipeMaxItems - 1) / kPipeMaxItems))
-            : items;
+    const uint32_t groups = std::min(items, std::max(runs_pipe_resident<kCompact, TableT, kBitLoads>(),
+                                                     (items + kPipeMaxItems - 1) / kPipeMaxItems));
     resolve_runs_pipe_kernel<kCompact, TableT, kBitLoads><<<dim3(groups), dim3(kThreads), 0, stream>>>(
         a, items, count, FastDiv(count));
 }
 
-// One 16-byte bitmap piece per thread when the row has at most kThreads of
-// them, else two.
+// Summary rows of at most kThreads 16-byte pieces take the two-stage kernel;
+// longer ones (up to 2 * kThreads pieces) the one-stage kernel with two
+// pieces per thread.
 template <bool kCompact, typename TableT>
 void launch_runs_pipe(const LookupArgs& a, dim3 grid, hipStream_t stream) {
     if ((a.bits_words + 3) / 4 <= kThreads) {
-        if (EKV_LOOKUP_PIPE2 && EKV_LOOKUP_PIPE_GRID) {
-            launch_runs_pipe2<kCompact, TableT>(a, grid, stream);
-            return;
-        }
-        launch_runs_pipe_loads<kCompact, TableT, 1>(a, grid, stream);
+        launch_runs_pipe2<kCompact, TableT>(a, grid, stream);
     } else {
         launch_runs_pipe_loads<kCompact, TableT, 2>(a, grid, stream);
     }
@@ -1606,7 +1542,7 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
     // measured faster on the 60-layer decode shapes than staging them.
     a.window = kWindow > 0 && width >= kWindow / 4 && table.dtype != EKV_INT16 &&
                        (mapping == nullptr || table.dtype == EKV_INT32) ? 1 : 0;
-    a.bits_staged = EKV_LOOKUP_STAGE_BITS && bits_p != nullptr && a.bits_words <= kStagedBitWords ? 1 : 0;
+    a.bits_staged = bits_p != nullptr && a.bits_words <= kStagedBitWords ? 1 : 0;
 
     const dim3 grid(static_cast<uint32_t>(count), static_cast<uint32_t>(layers));
     const auto s = static_cast<hipStream_t>(stream);
@@ -1614,7 +1550,7 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
     // Dense rows (unit inner strides, every row extent below 4 GiB) take the
     // 32-bit byte-offset addressing of element<true>.
     constexpr int64_t kFourGiB = int64_t{1} << 32;
-    const bool dense = EKV_LOOKUP_DENSE && a.topk_sk == 1 && a.table_sc == 1 && a.out_so == 1 && (!compact || a.miss_so == 1) &&
+    const bool dense = a.topk_sk == 1 && a.table_sc == 1 && a.out_so == 1 && (!compact || a.miss_so == 1) &&
                        (a.bits == nullptr || a.bits_sw == 1) && k * itemsize(topk.dtype) < kFourGiB &&
                        a.table_cols * itemsize(table.dtype) < kFourGiB && width * 4 < kFourGiB &&
                        a.bits_words * 4 < kFourGiB;
@@ -1626,7 +1562,7 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
     const bool pieces_layout = bits_p != nullptr && topk.dtype == EKV_INT32 && block_size == 1 &&
                                width % kIters == 0 && rows_aligned(topk.data, a.topk_sl, layers, a.topk_sb, batch) &&
                                rows_aligned(output.data, a.out_sl, layers, a.out_sb, batch);
-    a.runs = EKV_LOOKUP_RUNS && local && pieces_layout ? 1 : 0;
+    a.runs = local && pieces_layout ? 1 : 0;
     // The prefetching form: rows of one chunk, a non-empty batch and table
     // (stray selections and requests read batch row 0 and table entry 0 of
     // row 0, and discard them), fewer than 2^31 items, and bitmap rows of at
@@ -1641,7 +1577,7 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
     // Batch and table rows are kept as 32-bit indices (all ones = none).
     // Tables: int16 local slots, or int32 global slots in the single-level form.
     const bool pipe_table = local || (mapping == nullptr && table.dtype == EKV_INT32);
-    a.pipe = EKV_LOOKUP_PIPE && pipe_table && pieces_layout && dense && a.bits_staged && bits_pieces &&
+    a.pipe = pipe_table && pieces_layout && dense && a.bits_staged && bits_pieces &&
                      width <= kChunkLanes &&
                      batch > 0 && batch < (int64_t{1} << 31) && a.table_rows > 0 &&
                      a.table_rows < (int64_t{1} << 31) && a.table_cols > 0 && count * layers < (int64_t{1} << 31)

@@ -5,8 +5,9 @@ precommits (maps and zero-fills asynchronously) the chunks just past newly
 admitted ranges. Semantics follow the reference's Residency admission math
 without its serving-engine coupling:
 - fully backed chunks: elastic_kv/adapter.py:562-570;
-- chunk budget from free device memory, prefill headroom and an optional
-  broker snapshot: :572-647;
+- chunk budget from free device memory and prefill headroom: :572-647
+  (the reference also caps it by its cross-process capacity broker, which
+  is not part of this path);
 - the admission walk over free slot ranges: :671-756;
 - the request-affine preflight: :649-669;
 - the lookahead precommit after admitted ranges: :806-831.
@@ -14,9 +15,6 @@ without its serving-engine coupling:
 An arena is any object with `mapped_chunks` (a set of chunk ids), `planes`
 (chunks committed per chunk id; default 1) and `precommit(ids)` returning
 the number newly committed. This build's Backing and PhysicalPages have them.
-An arena's optional `backing` may report `broker_available_bytes` and
-`broker_snapshot()`. This build has no cross-process broker (Backing reports
-None), but a snapshot supplied by the caller is honoured, as the reference does.
 """
 
 import time
@@ -31,38 +29,6 @@ def fully_backed_chunks(arenas, precommitted=()):
     if arenas:
         backed.update(set.intersection(*(set(arena.mapped_chunks) for arena in arenas)))
     return backed
-
-
-def _broker_limit(arenas, usable, counters):
-    available, snapshots = [], []
-    for arena in arenas:
-        backing = getattr(arena, "backing", None)
-        snapshot = getattr(backing, "broker_snapshot", None)
-        if callable(snapshot):
-            snapshot = snapshot()
-        if isinstance(snapshot, dict):
-            snapshots.append(snapshot)
-            value = snapshot.get("available_bytes")
-        else:
-            value = getattr(backing, "broker_available_bytes", None)
-        if value is not None:
-            available.append(value)
-    if available:
-        shared = min(available)
-        counters["physical_global_broker_available_bytes"] = shared
-        if shared < usable:
-            counters["physical_global_broker_limited_calls"] = (
-                counters.get("physical_global_broker_limited_calls", 0) + 1)
-        usable = min(usable, shared)
-    # Under enforced fairness a tenant over its share may not grow at all.
-    fair = [0 for s in snapshots if s.get("fair_mode") == "enforce" and s.get("fairness_pressure")]
-    if fair:
-        counters["physical_global_broker_fair_available_bytes"] = 0
-        if 0 < usable:
-            counters["physical_global_broker_fair_limited_calls"] = (
-                counters.get("physical_global_broker_fair_limited_calls", 0) + 1)
-        usable = 0
-    return usable
 
 
 def chunk_budget(arenas, chunk_bytes, free_bytes, prefill_headroom, counters=None, reclaim=None):
@@ -88,7 +54,7 @@ def chunk_budget(arenas, chunk_bytes, free_bytes, prefill_headroom, counters=Non
         counters["physical_empty_cache_ns"] = (
             counters.get("physical_empty_cache_ns", 0) + time.perf_counter_ns() - started)
         free = after
-    usable = _broker_limit(arenas, max(0, free - prefill_headroom), counters)
+    usable = max(0, free - prefill_headroom)
     return usable // cost, cost, prefill_headroom
 
 

@@ -218,7 +218,11 @@ class Backing:
 
     @property
     def metrics(self):
-        return {**self._metrics, "backed_bytes": self.backed_bytes, "reserved_bytes": self.reserved_bytes}
+        """Counters plus the memory picture: backed (mapped) bytes, the spare pool's bytes
+        (unmapped but still held), their sum held_bytes, and the reservation."""
+        backed, spare = self.backed_bytes, self.spare_bytes
+        return {**self._metrics, "backed_bytes": backed, "spare_bytes": spare, "held_bytes": backed + spare,
+                "reserved_bytes": self.reserved_bytes}
 
     def set_spare_chunks(self, count):
         """Keep up to `count` reclaimed chunks' physical memory for the next commits (0: release at once).

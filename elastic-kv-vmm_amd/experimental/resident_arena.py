@@ -85,9 +85,11 @@ class VmmResidentArena:
         self._usable()
         self.layout.prefix_chunks(req, length)       # validates req and length
         if length > self._lengths[req]:
-            raise ValueError("requested view exceeds the committed prefix")
+            raise ValueError(f"a view of {length} rows is longer than the {self._lengths[req]} rows "
+                             f"request {req} has committed")
         if dtype.itemsize != self.layout.itemsize:
-            raise ValueError("dtype item size does not match the layout")
+            raise ValueError(f"{dtype} has {dtype.itemsize}-byte elements; the layout's hold "
+                             f"{self.layout.itemsize} bytes")
         window = self.backing.raw.narrow(0, self.layout.request_offset(req), length * self.layout.row_bytes)
         return window.view(dtype).reshape(length, self.layout.row_elements)
 

@@ -42,42 +42,6 @@ def test_headroom_is_reserved_before_the_token_budget():
     assert ctrl.counters["physical_limited_calls"] == 1
 
 
-def test_capped_by_broker_remaining_bytes():
-    # :726-752
-    arena = SimpleNamespace(planes=1, mapped_chunks={0}, backing=SimpleNamespace(broker_available_bytes=1_000))
-    ctrl, _ = admission([arena], 10_000)
-    assert ctrl.physical_available_tokens(30, [(1, 31)]) == 19
-    assert ctrl.counters["physical_global_broker_available_bytes"] == 1_000
-    assert ctrl.counters["physical_global_broker_limited_calls"] == 1
-
-
-def broker_snapshot(available, pressure):
-    return {"capacity_bytes": 10_000, "outstanding_bytes": 10_000 - available, "available_bytes": available,
-            "fair_mode": "enforce", "fair_target_bytes": 2_500, "tenant_usage_bytes": 2_000,
-            "fairness_pressure": pressure}
-
-
-def test_enforced_fair_pressure_stops_growth():
-    # :754-789
-    arena = SimpleNamespace(planes=1, mapped_chunks={0},
-                            backing=SimpleNamespace(broker_available_bytes=10_000,
-                                                    broker_snapshot=broker_snapshot(8_000, True)))
-    ctrl, _ = admission([arena], 10_000)
-    assert ctrl.physical_available_tokens(30, [(1, 31)]) == 9
-    assert ctrl.counters["physical_global_broker_fair_available_bytes"] == 0
-    assert ctrl.counters["physical_global_broker_fair_limited_calls"] == 1
-
-
-def test_fair_mode_without_pressure_allows_borrowing():
-    # :791-826
-    arena = SimpleNamespace(planes=1, mapped_chunks={0},
-                            backing=SimpleNamespace(broker_available_bytes=1_000,
-                                                    broker_snapshot=lambda: broker_snapshot(1_000, False)))
-    ctrl, _ = admission([arena], 10_000)
-    assert ctrl.physical_available_tokens(30, [(1, 31)]) == 19
-    assert "physical_global_broker_fair_limited_calls" not in ctrl.counters
-
-
 def test_logical_policy_does_not_query_memory():
     # :828-833
     def fail():

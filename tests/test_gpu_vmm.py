@@ -33,6 +33,7 @@ def test_spare_pool_recycles_reclaimed_chunks_zeroed(gpu):
             raw[i * chunk:(i + 1) * chunk].fill_(i + 1)
         assert backing.reclaim([2, 3, 4, 5]) == 4
         assert backing.spare_bytes == 3 * chunk and backing.backed_bytes == 2 * chunk
+        assert backing.metrics["held_bytes"] == 5 * chunk and backing.metrics["spare_bytes"] == 3 * chunk
         assert backing.ensure([6, 7, 3]) == 3                     # all three from the pool
         assert backing.spare_bytes == 0 and backing.backed_bytes == 5 * chunk
         for i in (3, 6, 7):

@@ -158,6 +158,8 @@ def test_spare_pool_through_the_python_backing(fake_library):
     assert backing.reclaim([0, 1, 2], synchronize=False) == 3
     assert backing.spare_bytes == 2 * CHUNK and backing.backed_bytes == 0
     assert lib.fake_calls(OPS["release"]) == 1 and lib.fake_live_handles() == 2
+    metrics = backing.metrics                    # the kept chunks are still held, not released
+    assert (metrics["spare_bytes"], metrics["backed_bytes"], metrics["held_bytes"]) == (2 * CHUNK, 0, 2 * CHUNK)
     assert backing.ensure([3, 2]) == 2 and lib.fake_calls(OPS["create"]) == 3     # both recycled
     assert backing.spare_bytes == 0 and backing.mapped_chunks == {2, 3}
     with pytest.raises(ValueError, match="spare_chunks"):
