@@ -11,10 +11,9 @@
 //   empty slot:                      stamp = INT32_MIN
 // (a row has at most 4096 lanes, so every step's stamps lie above all of the
 // steps before it whatever the width of each call), so sorting slots by
-// (stamp, slot) reproduces the dict's order, and the m
-// victims of a step (m = misses) are the m smallest keys: empty slots first,
-// then the least recently used entries. The i-th miss (in lane order) takes
-// the i-th victim.
+// (stamp, slot) reproduces the dict's order, and the m victims of a step
+// (m = distinct missed tokens) are the slots of the m smallest keys: empty
+// slots first, then the least recently used entries.
 //
 // Repeated tokens. The reference's replay refuses a selection that repeats a
 // token (hisparse_locality_replay.py:55-56), but Top-K blocks expand to
@@ -27,12 +26,15 @@
 // later lanes share that slot and record empty promotions.
 //
 // One 256-thread workgroup per (row, layer): hits are touched in LDS, a
-// radix select over the stamps picks the victims (the smallest (stamp, slot)
-// keys) and a bitonic network in LDS orders just them, then each victim
-// clears its old token from the token->slot table and residency summary,
-// takes the new token, and writes one promotion (host row -> global slot)
-// record. The lookup's slot output of every miss lane is patched to its new
-// slot, so the gather that follows reads the promoted row.
+// radix select over the stamps finds the victims (the slots of the smallest
+// (stamp, slot) keys), which one scan lists in slot order; the i-th distinct
+// miss (in miss-list order) takes the i-th of them. (Which victim slot a
+// miss takes is this kernel's own convention: the reference's LRU is an
+// ordered dict of tokens, whose contents and order do not depend on it.)
+// Each victim clears its old token from the token->slot table and residency
+// summary, takes the new token, and writes one promotion (host row -> global
+// slot) record. The lookup's slot output of every miss lane is patched to its
+// new slot, so the gather that follows reads the promoted row.
 //
 // Residency summary. At bits_shift 0 a bit is one position: an evicted
 // token clears it, an inserted token sets it. A coarser bit covers 2^shift
@@ -62,6 +64,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kMaxCapacity = 8192;   // slots per hot buffer (stamps held in LDS; 16-bit scan fields)
 constexpr int kMaxWidth = 4096;      // lanes per row whose miss tokens are hashed in LDS
+static_assert(kMaxWidth <= 16 * kThreads && kMaxCapacity <= 32 * kThreads,
+              "the kernel's register batches hold at most 16 lanes and 32 stamps per thread");
 // Stamps per LRU step: hits take step * kStepStamps + lane, misses
 // step * kStepStamps + kMaxWidth + lane, so a call with fewer lanes than the
 // one before still stamps above it.
@@ -107,17 +111,11 @@ struct SwapArgs {
     int64_t step;
     const int64_t* step_counter;    // when set, the step is read from device memory (graph replays)
     int32_t* status;                // EKV_SWAP_* error bits, OR-ed in (may be null)
-    uint32_t region_bytes;          // LDS bytes of the touch / hash / sort-key region
-    uint32_t hash_size, hash_log2;  // miss-token hash buckets: a power of two >= 2W
+    uint32_t touched_words;         // ceil(C / 32): words of the touched-slot bits
+    uint32_t hash_size, hash_log2;  // miss-token hash buckets: a power of two >= 2W (and >= 2)
+    uint32_t token_bitmap;          // 1: T <= 16 * hash_size, the region first serves as a token bitmap
+    uint32_t bitmap_words;          // ceil(T / 32)
 };
-
-__device__ __forceinline__ int64_t lane_position(const SwapArgs& a, const void* topk_row, uint32_t lane) {
-    const uint32_t b = a.block_size == 1 ? lane : a.block_div.div(lane);
-    const int64_t block = a.topk64 ? static_cast<const int64_t*>(topk_row)[b * a.topk_sk]
-                                   : static_cast<int64_t>(static_cast<const int32_t*>(topk_row)[b * a.topk_sk]);
-    const uint32_t offset = a.block_size == 1 ? 0u : lane - b * a.block_size;
-    return block * a.block_size + offset;
-}
 
 // Writes a token -> slot table entry (int32 global slot or int16 local slot + 1).
 __device__ __forceinline__ void set_entry(const SwapArgs& a, int64_t offset, int32_t value) {
@@ -155,64 +153,154 @@ __device__ __forceinline__ int32_t workgroup_exclusive_scan(int32_t value, int32
     return before + inclusive - value;
 }
 
+// A workgroup barrier that orders LDS only: waves wait for their own LDS
+// accesses, not for their outstanding global stores (which a full
+// __syncthreads would also wait for).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Lanes of this wave below the calling lane whose bit is set in `mask`.
+__device__ __forceinline__ int32_t lanes_below(uint64_t mask) {
+    return static_cast<int32_t>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u)));
+}
+
+// Sum, minimum and maximum of one value per thread over the workgroup
+// (wave shuffles, then one LDS exchange of the wave results). Every thread
+// must call it; `partial` holds 3 * (kThreads / 64) words.
+__device__ __forceinline__ void workgroup_sum_min_max(uint32_t& sum, uint32_t& lo, uint32_t& hi, uint32_t* partial) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        sum += __shfl_xor(sum, offset);
+        lo = min(lo, static_cast<uint32_t>(__shfl_xor(lo, offset)));
+        hi = max(hi, static_cast<uint32_t>(__shfl_xor(hi, offset)));
+    }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        partial[3 * wave] = sum;
+        partial[3 * wave + 1] = lo;
+        partial[3 * wave + 2] = hi;
+    }
+    lds_barrier();
+    sum = 0;
+    lo = 0xffffffffu;
+    hi = 0;
+#pragma unroll
+    for (int w = 0; w < kThreads / 64; ++w) {
+        sum += partial[3 * w];
+        lo = min(lo, partial[3 * w + 1]);
+        hi = max(hi, partial[3 * w + 2]);
+    }
+}
+
 __device__ __forceinline__ uint32_t token_hash(int32_t token, uint32_t log2_size) {
     return (static_cast<uint32_t>(token) * 2654435761u) >> (32 - log2_size);
 }
 
-// Ascending bitonic sort of keys[0 .. n) in LDS (n a power of two, at most
-// 2 * Q * kThreads). In each pass every thread takes the compare-exchanges
-// p = threadIdx.x + q * kThreads, q < Q (the pair (i, i + j), i = p with a
-// zero inserted at bit log2 j), reading all of its pairs before writing any.
-// Every thread must call it.
-template <int Q>
-__device__ void sort_victims(uint64_t* keys, uint32_t n) {
-    const uint32_t pairs = n >> 1;
-    for (uint32_t k = 2; k <= n; k <<= 1) {
-        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-            uint64_t first_key[Q], second_key[Q];
-#pragma unroll
-            for (int q = 0; q < Q; ++q) {
-                const uint32_t p = threadIdx.x + q * kThreads;
-                const uint32_t i = ((p & ~(j - 1)) << 1) | (p & (j - 1));
-                if (p < pairs) {
-                    first_key[q] = keys[i];
-                    second_key[q] = keys[i + j];
-                }
+// Packed 16-bit buckets of the miss-token hash: bucket h is the half
+// (h & 1) of word h >> 1; 0xffff marks an empty bucket, otherwise the bucket
+// holds a miss index (< 4096).
+constexpr uint32_t kEmptyBucket = 0xffffu;
+
+__device__ __forceinline__ uint32_t bucket_of(const uint32_t* words, uint32_t h) {
+    return (words[h >> 1] >> ((h & 1u) * 16u)) & 0xffffu;
+}
+
+// Writes `value` into bucket h when the bucket holds `expected`; the other
+// half of the word is preserved (retried while another lane changes it).
+// Returns the bucket's value before the write, or its current value when it
+// no longer held `expected`.
+__device__ __forceinline__ uint32_t bucket_cas(uint32_t* words, uint32_t h, uint32_t expected, uint32_t value) {
+    const uint32_t shift = (h & 1u) * 16u;
+    uint32_t* word = words + (h >> 1);
+    uint32_t seen = *word;
+    while (true) {
+        const uint32_t held = (seen >> shift) & 0xffffu;
+        if (held != expected) {
+            return held;
+        }
+        const uint32_t desired = (seen & ~(0xffffu << shift)) | (value << shift);
+        const uint32_t previous = atomicCAS(word, seen, desired);
+        if (previous == seen) {
+            return expected;
+        }
+        seen = previous;   // the word changed (this bucket or its neighbour): look again
+    }
+}
+
+// Lowers bucket h to `value` when that is smaller (a 16-bit atomicMin).
+__device__ __forceinline__ void bucket_min(uint32_t* words, uint32_t h, uint32_t value) {
+    uint32_t held = bucket_of(words, h);
+    while (value < held) {
+        const uint32_t seen = bucket_cas(words, h, held, value);
+        if (seen == held) {
+            return;
+        }
+        held = seen;
+    }
+}
+
+// Open-addressing hash of the miss tokens: every token ends up in one bucket
+// holding its lowest miss index. The table holds at least 2m buckets, so
+// every probe meets its token or an empty bucket. Every thread must call it.
+__device__ __forceinline__ void hash_miss_tokens(uint32_t* hash, const int32_t* info, int32_t m, uint32_t log2_size) {
+    const uint32_t mask = (1u << log2_size) - 1u;
+    for (int32_t i = threadIdx.x; i < m; i += kThreads) {
+        const int32_t token = info[i];
+        if (token < 0) {
+            continue;
+        }
+        uint32_t h = token_hash(token, log2_size);
+        while (true) {
+            const uint32_t held = bucket_cas(hash, h, kEmptyBucket, static_cast<uint32_t>(i));
+            if (held == kEmptyBucket) {
+                break;   // claimed
             }
-#pragma unroll
-            for (int q = 0; q < Q; ++q) {
-                const uint32_t p = threadIdx.x + q * kThreads;
-                const uint32_t i = ((p & ~(j - 1)) << 1) | (p & (j - 1));
-                if (p < pairs && (first_key[q] > second_key[q]) == ((i & k) == 0)) {
-                    keys[i] = second_key[q];
-                    keys[i + j] = first_key[q];
-                }
+            if (info[held] == token) {
+                bucket_min(hash, h, static_cast<uint32_t>(i));
+                break;
             }
-            __syncthreads();
+            h = (h + 1) & mask;
         }
     }
 }
 
 // Dynamic LDS of one workgroup (C = capacity, W = lanes per row):
-//   region   max(4 * C, 4 * hash_size, 8 * pow2(W)) bytes, used three times
-//            over: touch[C] (first hit lane per slot), then the miss-token
-//            hash (miss indices), then the victims' (stamp, slot) keys;
-//   stamp    [C] recency stamps;
-//   info     [W] token of miss i (-1: an entry naming no valid lane);
-//   owner    [W] the first miss of the same token (-1: an entry naming no
-//            valid lane); a first miss's own entry then becomes -2 - the rank
-//            of its victim.
+//   stamp    int32 [C]  recency stamps;
+//   info     int32 [W]  token of miss i (-1: an entry naming no valid lane);
+//   touched  uint32 [ceil(C / 32)]  one bit per slot a hit touches;
+//   region   hash_size 16-bit buckets (the miss-token hash), then the int16
+//            list of the victims' slots in slot order;
+//   owner    int16 [W]  the first miss of the same token (-1: an entry naming
+//            no valid lane); a first miss's own entry then becomes -2 - the
+//            rank of its victim.
+// 36.5 KiB at C = 4096, W = 2048, so 4 workgroups share a CU.
+//
+// Global reads come in three batches, each issued as a fixed number of
+// unrolled loads from clamped, in-bounds addresses and waited for once: the
+// stamps, lookup slots and miss list (with the request checks); the Top-K
+// ids of the miss entries; the victims' old tokens and host rows. (A loop
+// with a run-time trip count waits for each load before issuing the next: a
+// workgroup then spends most of its life on a chain of HBM round trips.)
+// kSlotRegs >= C / kThreads stamps and kLaneRegs >= W / kThreads lanes per
+// thread are held in registers.
+template <int kSlotRegs, int kLaneRegs>
 __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
-    extern __shared__ unsigned char shared[];
+    extern __shared__ __align__(16) unsigned char shared[];
     __shared__ int32_t wave_totals[kThreads / 64];
-    __shared__ int32_t digit_count[256];   // radix-select histogram of one 8-bit digit
+    __shared__ int32_t digit_count[2][256];   // radix-select histograms of one 8-bit digit (two passes)
     __shared__ int32_t chosen[2];          // the digit holding the need-th key, and the keys below it
-    uint64_t* keys = reinterpret_cast<uint64_t*>(shared);
-    int32_t* touch = reinterpret_cast<int32_t*>(shared);
-    int32_t* hash = reinterpret_cast<int32_t*>(shared);
-    int32_t* stamp = reinterpret_cast<int32_t*>(shared + a.region_bytes);
+    __shared__ uint32_t key_range[3 * (kThreads / 64)];   // empties, smallest and largest other key per wave
+    __shared__ int32_t row_counts[2][kSlotRegs][kThreads / 64];   // keys below T / at T per (row, wave)
+    int32_t* stamp = reinterpret_cast<int32_t*>(shared);
     int32_t* info = stamp + a.capacity;
-    int32_t* owner = info + a.width;
+    uint32_t* touched = reinterpret_cast<uint32_t*>(info + a.width);
+    uint32_t* hash = touched + a.touched_words;
+    int16_t* victims = reinterpret_cast<int16_t*>(hash);
+    int16_t* owner = reinterpret_cast<int16_t*>(hash + a.hash_size / 2);
     const int64_t b = a.selected[blockIdx.x];
     if (b < 0 || b >= a.batch) {
         return;
@@ -225,9 +313,34 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
     const int64_t C = a.capacity;
     const int64_t W = a.width;
     const int32_t counted = a.counts[l * a.ct_l + b * a.ct_b];
-    const int32_t m = counted < 0 ? 0 : (counted > W ? static_cast<int32_t>(W) : counted);
+    const int64_t base = a.slot_base[req];
+    const int64_t step = a.step_counter != nullptr ? *a.step_counter : a.step;  // uniform
     int32_t* promote_src = a.promote_src + l * a.ps_l + b * a.ps_b;
     int32_t* promote_dst = a.promote_dst + l * a.pd_l + b * a.pd_b;
+    int32_t* slots = a.slots + l * a.sl_l + b * a.sl_b;
+    const int64_t table_row = l * a.tb_l + req * a.tb_r;   // element offset of this (layer, request) row
+    int32_t* slot_token = a.slot_token + l * a.st_l + req * a.st_r;
+    int32_t* stamps = a.stamps + l * a.sp_l + req * a.sp_r;
+    const int32_t* misses = a.misses + l * a.mi_l + b * a.mi_b;
+    const void* topk_row = a.topk64
+        ? static_cast<const void*>(static_cast<const int64_t*>(a.topk) + l * a.topk_sl + b * a.topk_sb)
+        : static_cast<const void*>(static_cast<const int32_t*>(a.topk) + l * a.topk_sl + b * a.topk_sb);
+
+    // Batch 1: stamps, the lookup slots of this thread's lanes, its miss-list entries.
+    int32_t held_stamp[kSlotRegs];
+#pragma unroll
+    for (int k = 0; k < kSlotRegs; ++k) {
+        const int64_t s = min(static_cast<int64_t>(threadIdx.x) + int64_t{k} * kThreads, C - 1);
+        held_stamp[k] = stamps[s * a.sp_c];
+    }
+    int32_t lane_slot[kLaneRegs];
+    int32_t miss_lane[kLaneRegs];
+#pragma unroll
+    for (int k = 0; k < kLaneRegs; ++k) {
+        const int64_t o = min(static_cast<int64_t>(threadIdx.x) + int64_t{k} * kThreads, W - 1);
+        lane_slot[k] = slots[o * a.sl_o];
+        miss_lane[k] = misses[o * a.mi_o];   // entries at or past the count are read but not used
+    }
     // One workgroup owns each (layer, request) hot buffer: a second selected
     // row naming the same request would race on it, so both rows are refused.
     bool shared_request = false;
@@ -235,8 +348,17 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
         const int64_t other = a.selected[j];
         shared_request |= j != blockIdx.x && other >= 0 && other < a.batch && a.rows[other] == req;
     }
+    // Batch 2: the Top-K ids of the miss entries.
+    int64_t miss_block[kLaneRegs];
+#pragma unroll
+    for (int k = 0; k < kLaneRegs; ++k) {
+        const uint32_t lane = static_cast<uint32_t>(min(max(miss_lane[k], 0), static_cast<int32_t>(W - 1)));
+        const uint32_t blk = a.block_size == 1 ? lane : a.block_div.div(lane);
+        miss_block[k] = a.topk64 ? static_cast<const int64_t*>(topk_row)[blk * a.topk_sk]
+                                 : static_cast<int64_t>(static_cast<const int32_t*>(topk_row)[blk * a.topk_sk]);
+    }
+    const int32_t m = counted < 0 ? 0 : (counted > W ? static_cast<int32_t>(W) : counted);
     shared_request = __syncthreads_or(shared_request);
-    const int64_t step = a.step_counter != nullptr ? *a.step_counter : a.step;  // uniform
     const bool overflow = step < 0 || (step + 1) * kStepStamps >= (int64_t{1} << 31);
     if (shared_request || overflow) {
         // Change nothing, record empty promotions (the move that follows
@@ -250,96 +372,121 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
         }
         return;
     }
-    const int64_t base = a.slot_base[req];
     const int64_t stamp_base = step * kStepStamps;
-    int32_t* slots = a.slots + l * a.sl_l + b * a.sl_b;
-    const int64_t table_row = l * a.tb_l + req * a.tb_r;   // element offset of this (layer, request) row
-    int32_t* slot_token = a.slot_token + l * a.st_l + req * a.st_r;
-    int32_t* stamps = a.stamps + l * a.sp_l + req * a.sp_r;
-    const void* topk_row = a.topk64
-        ? static_cast<const void*>(static_cast<const int64_t*>(a.topk) + l * a.topk_sl + b * a.topk_sb)
-        : static_cast<const void*>(static_cast<const int32_t*>(a.topk) + l * a.topk_sl + b * a.topk_sb);
-
-    const int32_t* misses = a.misses + l * a.mi_l + b * a.mi_b;
-    // Tokens of the miss entries (-1: the entry names no valid lane), read
-    // while the stamps load: the miss list -> Top-K chain of global reads
-    // overlaps the stamps' instead of following the touch phase.
-    for (int32_t i = threadIdx.x; i < m; i += kThreads) {
-        const int32_t lane = misses[i * a.mi_o];
-        const int64_t token =
-            lane >= 0 && lane < W ? lane_position(a, topk_row, static_cast<uint32_t>(lane)) : int64_t{-1};
-        info[i] = token >= 0 && token < a.table_cols ? static_cast<int32_t>(token) : -1;
+#pragma unroll
+    for (int k = 0; k < kSlotRegs; ++k) {
+        const int64_t s = threadIdx.x + int64_t{k} * kThreads;
+        if (s < C) {
+            stamp[s] = held_stamp[k];
+        }
     }
+    int32_t hit_local[kLaneRegs];   // local slot a lane hits, or -1
+#pragma unroll
+    for (int k = 0; k < kLaneRegs; ++k) {
+        const int64_t o = threadIdx.x + int64_t{k} * kThreads;
+        const int64_t offset = static_cast<int64_t>(lane_slot[k]) - base;
+        hit_local[k] = o < W && lane_slot[k] > 0 && offset >= 0 && offset < C ? static_cast<int32_t>(offset) : -1;
+        const int64_t i = o;   // this thread's k-th miss-list entry
+        if (i < m) {
+            const int32_t lane = miss_lane[k];
+            const int64_t offset_in_block =
+                a.block_size == 1 ? 0 : static_cast<int64_t>(lane) - int64_t{a.block_div.div(static_cast<uint32_t>(lane))} *
+                                                                          a.block_size;
+            const int64_t token = lane >= 0 && lane < W ? miss_block[k] * a.block_size + offset_in_block : int64_t{-1};
+            info[i] = token >= 0 && token < a.table_cols ? static_cast<int32_t>(token) : -1;
+        }
+    }
+    for (uint32_t w = threadIdx.x; w < a.touched_words; w += kThreads) {
+        touched[w] = 0;
+    }
+    // The region starts as a token bitmap (all clear) when the tokens fit it,
+    // else as the empty hash.
+    const uint32_t region_words = a.token_bitmap ? a.bitmap_words : a.hash_size / 2;
+    const uint32_t region_fill = a.token_bitmap ? 0u : 0xffffffffu;
+    for (uint32_t w = threadIdx.x; w < region_words; w += kThreads) {
+        hash[w] = region_fill;
+    }
+    __syncthreads();
     // Touch hits. A token repeated in the row is one access of its first lane:
-    // the slot's stamp takes the lowest lane that hit it.
-    for (int64_t s = threadIdx.x; s < C; s += kThreads) {
-        stamp[s] = stamps[s * a.sp_c];
-        touch[s] = INT32_MAX;
-    }
-    __syncthreads();
-    for (int64_t o = threadIdx.x; o < W; o += kThreads) {
-        const int32_t slot = slots[o * a.sl_o];
-        const int64_t local = static_cast<int64_t>(slot) - base;
-        if (slot > 0 && local >= 0 && local < C) {
-            atomicMin(&touch[local], static_cast<int32_t>(o));
+    // a touched slot's stamp becomes stamp_base + the lowest lane that hit it
+    // (marked, raised to INT32_MAX, then lowered by every hitting lane).
+#pragma unroll
+    for (int k = 0; k < kLaneRegs; ++k) {
+        if (hit_local[k] >= 0) {
+            atomicOr(&touched[hit_local[k] >> 5], 1u << (hit_local[k] & 31));
         }
     }
-    __syncthreads();
-    for (int64_t s = threadIdx.x; s < C; s += kThreads) {
-        if (touch[s] != INT32_MAX) {
-            stamp[s] = static_cast<int32_t>(stamp_base + touch[s]);
+    // Repeated miss tokens. With the token bitmap, each valid entry sets its
+    // token's bit; a bit found set means some token repeats, and only then is
+    // the exact hash built (each token's lowest miss index). Without repeats
+    // every valid entry is its token's first miss.
+    bool repeated = false;
+    if (a.token_bitmap) {   // uniform
+#pragma unroll
+        for (int k = 0; k < kLaneRegs; ++k) {
+            const int32_t i = static_cast<int32_t>(threadIdx.x) + k * kThreads;
+            const int32_t token = i < m ? info[i] : -1;
+            if (token >= 0) {
+                const uint32_t bit = 1u << (token & 31);
+                repeated |= (atomicOr(&hash[token >> 5], bit) & bit) != 0u;
+            }
         }
+    } else {
+        hash_miss_tokens(hash, info, m, a.hash_log2);
     }
-    __syncthreads();
-    if (m > 0) {
-        for (uint32_t h = threadIdx.x; h < a.hash_size; h += kThreads) {
-            hash[h] = -1;
+    const bool exact_hash = !a.token_bitmap || __syncthreads_or(repeated);   // uniform
+    if (a.token_bitmap && exact_hash) {
+        for (uint32_t w = threadIdx.x; w < a.hash_size / 2; w += kThreads) {
+            hash[w] = 0xffffffffu;
         }
         __syncthreads();
-        // Open-addressing hash of the miss tokens: every token ends up in one
-        // bucket holding its lowest miss index. The table holds at least 2m
-        // buckets, so every probe meets its token or an empty bucket.
-        const uint32_t mask = a.hash_size - 1;
-        for (int32_t i = threadIdx.x; i < m; i += kThreads) {
-            const int32_t token = info[i];
-            if (token < 0) {
-                continue;
-            }
+        hash_miss_tokens(hash, info, m, a.hash_log2);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kSlotRegs; ++k) {
+        const uint32_t s = threadIdx.x + k * kThreads;
+        if (s < C && ((touched[s >> 5] >> (s & 31)) & 1u)) {
+            stamp[s] = INT32_MAX;
+        }
+    }
+    const uint32_t mask = a.hash_size - 1;
+#pragma unroll
+    for (int k = 0; k < kLaneRegs; ++k) {
+        const int32_t i = static_cast<int32_t>(threadIdx.x) + k * kThreads;
+        if (i >= m) {
+            continue;
+        }
+        const int32_t token = info[i];
+        int32_t first = -1;
+        if (token >= 0 && !exact_hash) {
+            first = i;
+        } else if (token >= 0) {
             for (uint32_t h = token_hash(token, a.hash_log2);; h = (h + 1) & mask) {
-                int32_t held = hash[h];
-                if (held < 0) {
-                    held = atomicCAS(&hash[h], -1, i);
-                    if (held < 0) {
-                        break;   // claimed
-                    }
+                const uint32_t held = bucket_of(hash, h);
+                if (held == kEmptyBucket) {
+                    break;   // not reached: every inserted token lies on its probe path
                 }
                 if (info[held] == token) {
-                    atomicMin(&hash[h], i);
+                    first = static_cast<int32_t>(held);
                     break;
                 }
             }
         }
-        __syncthreads();
-        for (int32_t i = threadIdx.x; i < m; i += kThreads) {
-            const int32_t token = info[i];
-            int32_t first = -1;
-            if (token >= 0) {
-                for (uint32_t h = token_hash(token, a.hash_log2);; h = (h + 1) & mask) {
-                    const int32_t held = hash[h];
-                    if (held < 0) {
-                        break;   // not reached: every inserted token lies on its probe path
-                    }
-                    if (info[held] == token) {
-                        first = held;
-                        break;
-                    }
-                }
-            }
-            owner[i] = first;
+        owner[i] = static_cast<int16_t>(first);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kLaneRegs; ++k) {
+        if (hit_local[k] >= 0) {
+            atomicMin(&stamp[hit_local[k]],
+                      static_cast<int32_t>(stamp_base + threadIdx.x + static_cast<int64_t>(k) * kThreads));
         }
-        __syncthreads();
+    }
+    if (m > 0) {
         // Rank of each first miss among the first misses, in miss-list order:
-        // every thread counts a contiguous run of entries, one scan.
+        // every thread counts a contiguous run of entries, one scan. (The
+        // scan's barriers also order the touches above before the select.)
         const int32_t per_thread = (m + kThreads - 1) / kThreads;
         const int32_t run_begin = min(m, static_cast<int32_t>(threadIdx.x) * per_thread);
         const int32_t run_end = min(m, run_begin + per_thread);
@@ -351,35 +498,66 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
         int32_t rank = workgroup_exclusive_scan(firsts, wave_totals, unique);
         for (int32_t i = run_begin; i < run_end; ++i) {
             if (owner[i] == i) {
-                owner[i] = -2 - rank++;   // a first miss: the rank of its victim, encoded below -1
+                owner[i] = static_cast<int16_t>(-2 - rank++);   // a first miss: its victim's rank, below -1
             }
         }
-        __syncthreads();   // the victim loop reads other threads' entries
-        // The `unique` victims: the smallest (stamp, slot) keys, empty slots
-        // (INT32_MIN) first, then the least recently used. A radix select
-        // over the order-preserving unsigned form of the stamps (four 8-bit
-        // digits, most significant first) finds the stamp value T of the
-        // unique-th smallest key and how many keys at T it takes; one scan in
-        // slot order then gathers the slots below T and the first of those at
-        // T into the key region, and a bitonic network sorts just them.
-        const auto ordered = [&](uint32_t s) { return static_cast<uint32_t>(stamp[s]) ^ 0x80000000u; };
-        if (unique > 0) {   // uniform: with no victim to choose, the keys are never read
-            uint32_t prefix = 0, prefix_mask = 0;
-            int32_t need = unique;   // keys still to take among those matching the prefix (uniform)
-            for (int shift = 24; shift >= 0; shift -= 8) {
-                digit_count[threadIdx.x] = 0;   // kThreads == 256 digits
-                __syncthreads();
+        // The `unique` victims: the slots of the smallest (stamp, slot) keys,
+        // empty slots (INT32_MIN) first, then the least recently used. In
+        // the order-preserving unsigned form of the stamps an empty slot is
+        // key 0. When the empties do not cover the victims, a radix select
+        // over the other keys (8-bit digits, most significant first) finds
+        // the key T of the (unique - empties)-th smallest of them and how
+        // many keys at T it takes; it starts at the highest digit where the
+        // smallest and largest of those keys differ (the stamps of a buffer
+        // span a few steps: two digits). The victims are then listed in slot
+        // order, and the i-th first miss takes the i-th of them.
+        if (unique > 0) {   // uniform
+            // This thread's keys, slots t + 256 k, read once (the touches
+            // landed before the rank scan's barriers); 0xffffffff past C.
+            uint32_t key[kSlotRegs];
+#pragma unroll
+            for (int k = 0; k < kSlotRegs; ++k) {
+                const uint32_t s = threadIdx.x + k * kThreads;
+                key[k] = s < C ? static_cast<uint32_t>(stamp[s]) ^ 0x80000000u : 0xffffffffu;
+            }
+            digit_count[0][threadIdx.x] = 0;   // the first pass's histogram; the reduction's barrier follows
+            uint32_t empties = 0, lo = 0xffffffffu, hi = 0;
+#pragma unroll
+            for (int k = 0; k < kSlotRegs; ++k) {
+                const uint32_t v = key[k];
+                const bool other = v != 0 && threadIdx.x + k * kThreads < C;
+                empties += v == 0 ? 1u : 0u;
+                lo = other ? min(lo, v) : lo;
+                hi = other ? max(hi, v) : hi;
+            }
+            workgroup_sum_min_max(empties, lo, hi, key_range);
+            uint32_t prefix = 0, prefix_mask = 0xffffffffu;
+            int32_t need = unique;   // keys still to take at the prefix (uniform)
+            int first_shift = -8;    // no select: the empties alone, or every other key equal
+            if (static_cast<uint32_t>(unique) > empties) {
+                need = unique - static_cast<int32_t>(empties);
+                const uint32_t differ = lo ^ hi;
+                prefix = lo;
+                if (differ != 0) {
+                    first_shift = ((31 - __clz(differ)) / 8) * 8;
+                    prefix_mask = first_shift == 24 ? 0u : ~((1u << (first_shift + 8)) - 1u);
+                    prefix = lo & prefix_mask;
+                }
+            }
+            for (int shift = first_shift, pass = 0; shift >= 0; shift -= 8, ++pass) {
+                int32_t* count = digit_count[pass & 1];
                 // Runs of one digit in a thread's slots count with one atomic:
                 // recent stamps share their high digits, which would otherwise
                 // serialize thousands of atomics on one counter.
                 uint32_t run_digit = 0;
                 int32_t run = 0;
-                for (uint32_t s = threadIdx.x; s < C; s += kThreads) {
-                    const uint32_t v = ordered(s);
-                    if ((v & prefix_mask) == prefix) {
+#pragma unroll
+                for (int k = 0; k < kSlotRegs; ++k) {
+                    const uint32_t v = key[k];
+                    if (v != 0 && (v & prefix_mask) == prefix && threadIdx.x + k * kThreads < C) {
                         const uint32_t d = (v >> shift) & 255u;
                         if (run > 0 && d != run_digit) {
-                            atomicAdd(&digit_count[run_digit], run);
+                            atomicAdd(&count[run_digit], run);
                             run = 0;
                         }
                         run_digit = d;
@@ -387,73 +565,140 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
                     }
                 }
                 if (run > 0) {
-                    atomicAdd(&digit_count[run_digit], run);
+                    atomicAdd(&count[run_digit], run);
                 }
-                __syncthreads();
-                const int32_t here = digit_count[threadIdx.x];
-                int32_t matching = 0;
-                const int32_t below = workgroup_exclusive_scan(here, wave_totals, matching);
-                if (below < need && need <= below + here) {   // exactly one digit holds the need-th key
-                    chosen[0] = static_cast<int32_t>(threadIdx.x);
-                    chosen[1] = below;
+                lds_barrier();
+                // Wave 0 scans the 256 counts (4 digits per lane) and names the
+                // digit holding the need-th key; the others clear the next
+                // pass's histogram meanwhile.
+                if (threadIdx.x < 64) {
+                    int32_t c[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        c[j] = count[4 * threadIdx.x + j];
+                    }
+                    const int32_t mine = c[0] + c[1] + c[2] + c[3];
+                    int32_t inclusive = mine;
+#pragma unroll
+                    for (int offset = 1; offset < 64; offset <<= 1) {
+                        const int32_t lower = __shfl_up(inclusive, offset);
+                        inclusive += threadIdx.x >= static_cast<uint32_t>(offset) ? lower : 0;
+                    }
+                    int32_t below = inclusive - mine;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        if (below < need && need <= below + c[j]) {   // exactly one digit holds the need-th key
+                            chosen[0] = static_cast<int32_t>(4 * threadIdx.x + j);
+                            chosen[1] = below;
+                        }
+                        below += c[j];
+                    }
                 }
-                __syncthreads();
+                for (uint32_t d = threadIdx.x; d < 256; d += kThreads) {
+                    digit_count[(pass + 1) & 1][d] = 0;
+                }
+                lds_barrier();
                 prefix |= static_cast<uint32_t>(chosen[0]) << shift;
                 prefix_mask |= 255u << shift;
                 need -= chosen[1];
             }
-            // Slot s is a victim when v < T, or v == T and fewer than `need`
-            // slots below s hold T. Each thread scans a contiguous run of slots;
-            // the counts of both kinds travel packed in one scan (16 bits each).
-            const uint32_t per_slot_run = (static_cast<uint32_t>(C) + kThreads - 1) / kThreads;
-            const uint32_t slot_begin = min(static_cast<uint32_t>(C), threadIdx.x * per_slot_run);
-            const uint32_t slot_end = min(static_cast<uint32_t>(C), slot_begin + per_slot_run);
-            int32_t packed = 0;
-            for (uint32_t s = slot_begin; s < slot_end; ++s) {
-                const uint32_t v = ordered(s);
-                packed += v < prefix ? (1 << 16) : (v == prefix ? 1 : 0);
-            }
-            int32_t packed_total = 0;
-            const int32_t packed_before = workgroup_exclusive_scan(packed, wave_totals, packed_total);
-            int32_t lower = packed_before >> 16, ties = packed_before & 0xffff;
-            for (uint32_t s = slot_begin; s < slot_end; ++s) {
-                const uint32_t v = ordered(s);
-                if (v < prefix || (v == prefix && ties < need)) {
-                    keys[lower + min(ties, need)] = (static_cast<uint64_t>(v) << 32) | s;
+            // T = prefix. Slot s is a victim when its key is below T (every
+            // empty slot, when the empties do not cover the victims), or at T
+            // and fewer than `need` slots below s hold T; its place in the list
+            // is the number of victims below it. Thread t takes slots
+            // t + 256 k (conflict-free LDS reads); the slot-order counts of
+            // both kinds come from per-wave ballots over each row of 256 slots.
+            const int wave = threadIdx.x >> 6;
+            uint32_t my_lower = 0, my_tie = 0;
+#pragma unroll
+            for (int k = 0; k < kSlotRegs; ++k) {
+                const uint32_t s = threadIdx.x + k * kThreads;
+                const uint32_t v = key[k];
+                const bool lower = s < C && v < prefix;
+                const bool tie = s < C && v == prefix;
+                const uint64_t lower_lanes = __ballot(lower);
+                const uint64_t tie_lanes = __ballot(tie);
+                my_lower |= lower ? 1u << k : 0u;
+                my_tie |= tie ? 1u << k : 0u;
+                if ((threadIdx.x & 63) == 0) {
+                    row_counts[0][k][wave] = __popcll(lower_lanes);
+                    row_counts[1][k][wave] = __popcll(tie_lanes);
                 }
-                lower += v < prefix ? 1 : 0;
-                ties += v == prefix ? 1 : 0;
             }
-            uint32_t n = 1;
-            while (n < static_cast<uint32_t>(unique)) {
-                n <<= 1;
+            lds_barrier();
+            // Lane j < kSlotRegs of each wave takes row j: its keys of each kind
+            // in all waves and in the waves below this one; a shuffle scan over
+            // the lanes adds the rows below j, and the row loop reads row k's
+            // base from lane k.
+            const int lane = threadIdx.x & 63;
+            int32_t row_lower = 0, row_tie = 0, wave_lower = 0, wave_tie = 0;
+            if (lane < kSlotRegs) {
+#pragma unroll
+                for (int w = 0; w < kThreads / 64; ++w) {
+                    const int32_t lower_here = row_counts[0][lane][w];
+                    const int32_t tie_here = row_counts[1][lane][w];
+                    row_lower += lower_here;
+                    row_tie += tie_here;
+                    wave_lower += w < wave ? lower_here : 0;
+                    wave_tie += w < wave ? tie_here : 0;
+                }
             }
-            for (uint32_t s = unique + threadIdx.x; s < n; s += kThreads) {
-                keys[s] = ~uint64_t{0};
+            int32_t lower_scan = row_lower, tie_scan = row_tie;
+#pragma unroll
+            for (int offset = 1; offset < kSlotRegs; offset <<= 1) {
+                const int32_t lower_up = __shfl_up(lower_scan, offset);
+                const int32_t tie_up = __shfl_up(tie_scan, offset);
+                lower_scan += lane >= offset ? lower_up : 0;
+                tie_scan += lane >= offset ? tie_up : 0;
             }
-            __syncthreads();
-            // Bitonic network in LDS over the n victim keys, each thread taking
-            // ceil(n / 2 / kThreads) compare-exchanges per pass.
-            if (n <= 2 * kThreads) {
-                sort_victims<1>(keys, n);
-            } else if (n <= 4 * kThreads) {
-                sort_victims<2>(keys, n);
-            } else if (n <= 8 * kThreads) {
-                sort_victims<4>(keys, n);
-            } else {
-                sort_victims<8>(keys, n);
+            const int32_t lower_base = lower_scan - row_lower + wave_lower;   // row `lane`'s base for this wave
+            const int32_t tie_base = tie_scan - row_tie + wave_tie;
+#pragma unroll
+            for (int k = 0; k < kSlotRegs; ++k) {
+                const bool lower = (my_lower >> k) & 1u;
+                const bool tie = (my_tie >> k) & 1u;
+                const int32_t lower_before = __builtin_amdgcn_readlane(lower_base, k) + lanes_below(__ballot(lower));
+                const int32_t ties_before = __builtin_amdgcn_readlane(tie_base, k) + lanes_below(__ballot(tie));
+                if (lower || (tie && ties_before < need)) {
+                    victims[lower_before + min(ties_before, need)] = static_cast<int16_t>(threadIdx.x + k * kThreads);
+                }
             }
+            lds_barrier();
         }
         int32_t* bits = a.bits != nullptr ? a.bits + l * a.bt_l + req * a.bt_r : nullptr;
         // Group counts keep a coarse summary exact: decrements here, increments after the barrier.
         int32_t* line_counts = bits != nullptr && a.bits_shift > 0 && a.line_counts != nullptr
                                    ? a.line_counts + l * a.lc_l + req * a.lc_r
                                    : nullptr;
-        for (int32_t i = threadIdx.x; i < m; i += kThreads) {
-            // -1: the entry names no valid lane; <= -2: a first miss, whose
-            // victim has rank -2 - entry; otherwise the index of its first miss.
-            const int32_t entry = owner[i];
-            const int32_t lane = misses[i * a.mi_o];
+        // Batch 3: each entry's victim (from LDS), then the victims' old
+        // tokens and the promoted tokens' host rows, all loads issued before
+        // any is used. Entry encoding: -1 names no valid lane; <= -2 is a
+        // first miss, whose victim has rank -2 - entry; otherwise the index
+        // of its first miss.
+        int32_t entry_of[kLaneRegs];
+        int32_t victim_of[kLaneRegs];
+        int32_t old_of[kLaneRegs];
+        int32_t host_row_of[kLaneRegs];
+#pragma unroll
+        for (int k = 0; k < kLaneRegs; ++k) {
+            const int32_t i = static_cast<int32_t>(threadIdx.x) + k * kThreads;
+            const int32_t entry = i < m ? static_cast<int32_t>(owner[i]) : -1;
+            const int32_t rank = entry == -1 ? 0 : -2 - (entry <= -2 ? entry : static_cast<int32_t>(owner[entry]));
+            const int32_t victim = entry == -1 ? 0 : static_cast<int32_t>(static_cast<uint16_t>(victims[rank]));
+            const int64_t token = entry == -1 ? 0 : info[i];   // >= 0 for an entry with a valid lane
+            entry_of[k] = entry;
+            victim_of[k] = victim;
+            old_of[k] = slot_token[static_cast<int64_t>(victim) * a.st_c];
+            host_row_of[k] = static_cast<int32_t>(a.host_table[req * a.host_sr + token * a.host_st]);
+        }
+#pragma unroll
+        for (int k = 0; k < kLaneRegs; ++k) {
+            const int32_t i = static_cast<int32_t>(threadIdx.x) + k * kThreads;
+            if (i >= m) {
+                continue;
+            }
+            const int32_t entry = entry_of[k];
+            const int32_t lane = miss_lane[k];
             if (entry == -1) {
                 // Not an entry of a miss list written by the lookup: record an
                 // empty promotion so the move that follows skips it.
@@ -462,13 +707,11 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
                 continue;
             }
             const bool first = entry <= -2;
-            const int32_t rank = -2 - (first ? entry : owner[entry]);
-            const int64_t victim = static_cast<int64_t>(keys[rank] & 0xffffffffu);
+            const int64_t victim = victim_of[k];
             const int32_t global = static_cast<int32_t>(base + victim);
-            const int64_t token = info[i];   // >= 0 for an entry with a valid lane
-            // Independent global reads, issued together (a repeat's are unused).
-            const int32_t old = slot_token[victim * a.st_c];
-            const int32_t host_row = static_cast<int32_t>(a.host_table[req * a.host_sr + token * a.host_st]);
+            const int64_t token = info[i];
+            const int32_t old = old_of[k];
+            const int32_t host_row = host_row_of[k];
             slots[static_cast<int64_t>(lane) * a.sl_o] = global;
             if (!first) {
                 // A repeat of an earlier miss: it shares that miss's slot and promotion.
@@ -500,8 +743,8 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
             promote_src[i * a.ps_o] = host_row;
             promote_dst[i * a.pd_o] = global;
         }
-        __syncthreads();
         if (line_counts != nullptr) {   // uniform
+            __syncthreads();   // the evictions' count decrements (global atomics) precede the increments
             // Insertions: after every eviction's clear above, so a group that
             // both loses and gains positions ends with its bit set.
             for (int32_t i = threadIdx.x; i < m; i += kThreads) {
@@ -512,7 +755,11 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
                     }
                 }
             }
+        } else {
+            lds_barrier();     // the victims' stamps land in LDS before the write-back
         }
+    } else {
+        __syncthreads();   // the touches above land before the stamps are written back
     }
     for (int64_t s = threadIdx.x; s < C; s += kThreads) {
         stamps[s * a.sp_c] = stamp[s];
@@ -720,25 +967,28 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
         a.hash_size <<= 1;
         ++a.hash_log2;
     }
-    // The region holds touch[C], then the miss-token hash, then the keys of at most W victims
-    // (padded to a power of two for the sort).
-    int64_t sort_entries = 1;
-    while (sort_entries < W) {
-        sort_entries <<= 1;
-    }
-    const size_t region = std::max({static_cast<size_t>(sort_entries) * sizeof(uint64_t),
-                                    static_cast<size_t>(a.hash_size) * sizeof(int32_t),
-                                    static_cast<size_t>(C) * sizeof(int32_t)});
-    a.region_bytes = static_cast<uint32_t>(region);
-    const size_t lds = region + static_cast<size_t>(C) * 4 + static_cast<size_t>(W) * 8;
+    a.touched_words = static_cast<uint32_t>((C + 31) / 32);
+    // The hash region holds 16 * hash_size bits: a bitmap of the tokens when they fit.
+    a.token_bitmap = T <= int64_t{16} * a.hash_size ? 1u : 0u;
+    a.bitmap_words = static_cast<uint32_t>(a.token_bitmap ? (T + 31) / 32 : 0);
+    // stamps, miss tokens, touched bits, the 16-bit hash buckets (then the
+    // victim list, 2 bytes per victim: at most W <= hash_size / 2), the owners
+    static_assert(kMaxWidth <= 0x7fff && kMaxCapacity <= 0x7fff, "miss indices and slots fit 16 bits");
+    const size_t lds = static_cast<size_t>(C) * 4 + static_cast<size_t>(W) * 4 +
+                       static_cast<size_t>(a.touched_words) * 4 + static_cast<size_t>(a.hash_size) * 2 +
+                       static_cast<size_t>(W) * 2;
+    const dim3 grid(static_cast<uint32_t>(count), static_cast<uint32_t>(L));
+    const auto s = static_cast<hipStream_t>(stream);
+    // Registers per thread: 16 stamps up to C = 4096 (else 32), 8 lanes up to W = 2048 (else 16).
+    const bool wide_slots = C > 16 * kThreads, wide_lanes = W > 8 * kThreads;
+    auto* kernel = wide_slots ? (wide_lanes ? swap_in_kernel<32, 16> : swap_in_kernel<32, 8>)
+                              : (wide_lanes ? swap_in_kernel<16, 16> : swap_in_kernel<16, 8>);
     if (lds > 64 * 1024) {
-        check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(swap_in_kernel),
+        check_hip(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)),
                   "raise the swap-in LDS limit");
     }
-    const dim3 grid(static_cast<uint32_t>(count), static_cast<uint32_t>(L));
-    const auto s = static_cast<hipStream_t>(stream);
-    swap_in_kernel<<<grid, dim3(kThreads), lds, s>>>(a);
+    kernel<<<grid, dim3(kThreads), lds, s>>>(a);
     check_hip(hipGetLastError(), "launch swap-in");
     if (counter != nullptr) {
         advance_step_kernel<<<dim3(1), dim3(64), 0, s>>>(counter);

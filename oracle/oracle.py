@@ -159,10 +159,11 @@ def swap_in(step, block_size, topk, rows, selected, slots, misses, counts, table
     """Batch-token LRU swap-in after a lookup, on numpy arrays (copies are returned).
 
     Per selected row b (request r = rows[b]) of every layer: hits touch their
-    slot (stamp = step*8192 + the lowest lane that hit it), the first miss
-    entry of every distinct token (in miss-list order) takes the next of the
-    slots with the smallest (stamp, slot) - empty slots (-2^31) first; a
-    victim's old token leaves the table, the new token enters it, its stamp
+    slot (stamp = step*8192 + the lowest lane that hit it); with u distinct
+    missed tokens, the victims are the slots of the u smallest (stamp, slot)
+    keys - empty slots (-2^31) first - and the first miss entry of the i-th
+    distinct token (in miss-list order) takes the i-th victim in slot order;
+    a victim's old token leaves the table, the new token enters it, its stamp
     becomes step*8192 + 4096 + lane, and promotion i records
     (host_table[r, token], global slot). A later miss entry of the same token
     gets that slot and an empty promotion (-1, -1), as does an entry naming
@@ -207,8 +208,18 @@ def swap_in(step, block_size, topk, rows, selected, slots, misses, counts, table
             for local, lane in first_hit.items():
                 stamp[local] = step * SWAP_STEP_STAMPS + lane
             order = sorted(range(C), key=lambda v: (stamp[v], v))
-            taken = {}
             m = max(0, min(int(counts[layer, b]), W))
+            # The victims are the slots of the u smallest keys (u = distinct valid missed tokens), handed
+            # out in slot order.
+            distinct = set()
+            for i in range(m):
+                lane = int(misses[layer, b, i])
+                if 0 <= lane < W:
+                    token = int(topk[layer, b, lane // block_size]) * block_size + lane % block_size
+                    if 0 <= token < T:
+                        distinct.add(token)
+            victims = sorted(order[:len(distinct)])
+            taken = {}
             for i in range(m):
                 lane = int(misses[layer, b, i])
                 if not 0 <= lane < W:
@@ -219,7 +230,7 @@ def swap_in(step, block_size, topk, rows, selected, slots, misses, counts, table
                 if token in taken:
                     slots[layer, b, lane] = base + taken[token]
                     continue
-                victim = order[len(taken)]
+                victim = victims[len(taken)]
                 taken[token] = victim
                 old = int(slot_token[layer, r, victim])
                 if old >= 0:
