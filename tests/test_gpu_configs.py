@@ -15,6 +15,12 @@
   (adaptive_sparse/request_residency.py:805-832 with the batch-token LRU of
   benchmarks/hisparse_locality_replay.py:90-99), and every gathered row equals
   its token's host row.
+- Config 5 at full size (128 requests x 60 layers), two steps, each with
+  its 5 % chunk remap: every gathered K/V row equals its token's host row,
+  the hot-buffer state stays a bijection between tokens and slots, every
+  selected lane is resident in the slot it read, and the residency summary
+  equals a fresh build (size-independent checks; the oracle itself runs at
+  the reduced size above).
 - The prefetching lookup with more items than 16 per resident workgroup, the
   launch shape where the host raises the grid above the resident count.
 """
@@ -216,6 +222,116 @@ def test_config5_composite_steps_match_the_oracle(gpu):
                     host_rows = host_table[r, topk[layer, r]]
                     for kv in range(2):
                         assert np.array_equal(got[r, layer, kv], host[layer, kv, host_rows]), (step, layer, r, kv)
+    finally:
+        torch.cuda.synchronize()
+        backing.close()
+        if arena is not None:
+            arena.close()
+
+
+def _composite_topk_gpu(gen, L, R, K, lengths, window=4096):
+    """Per (layer, request) on the device: K distinct tokens, 80 % from the last `window`, the rest uniform older."""
+    device = lengths.device
+    T = int(lengths.max())
+    far_want = K - (K * 4) // 5
+    older = (lengths - window).clamp_min(0)
+    far = torch.minimum(older, torch.full_like(older, far_want))
+    near_count = K - far
+    near = torch.rand((L, R, window), generator=gen, device=device).argsort(-1)[..., :K] + older.view(1, R, 1)
+    keys = torch.rand((L, R, T), generator=gen, device=device)
+    keys.masked_fill_(torch.arange(T, device=device).view(1, 1, T) >= older.view(1, R, 1), 2.0)
+    old = keys.topk(far_want, dim=-1, largest=False).indices
+    del keys
+    lane = torch.arange(K, device=device).view(1, 1, K)
+    pick = torch.where(lane < near_count.view(1, R, 1), near,
+                       torch.gather(old, -1, (lane - near_count.view(1, R, 1)).clamp(0, far_want - 1)))
+    order = torch.rand((L, R, K), generator=gen, device=device).argsort(-1)
+    return torch.gather(pick, -1, order).to(torch.int32).contiguous()
+
+
+def test_config5_full_size_steps_keep_rows_and_lru_invariants(gpu):
+    L, R, K, C, HOST_ROWS, row_bytes = 60, 128, 2048, 4096, 65536, 512
+    gen = torch.Generator(device=gpu).manual_seed(505)
+    rng = np.random.default_rng(505)
+    lengths = torch.randint(4096, 32769, (R,), generator=gen, device=gpu)
+    T = int(lengths.max())
+    layout = PlanePoolLayout(layers=L, kv=2, rows=1 + R * C, row_bytes=row_bytes)
+    backing = Backing(layout.capacity_bytes, layout.chunk_bytes, device=0)
+    arena = None
+    try:
+        backing.ensure(range(backing.chunk_count))
+        planes = layout.kv_planes(backing.base, 0, owner=backing)
+        host_plane = HOST_ROWS * row_bytes
+        arena = HostArena(2 * L * host_plane)
+        host_gpu = torch.randint(0, 256, (L, 2, HOST_ROWS, row_bytes), dtype=torch.uint8, device=gpu,
+                                 generator=gen)
+        arena.host.copy_(host_gpu.view(-1).cpu())
+        host_planes = KVPlanes(base=arena.device_ptr, device=0, layers=L, kv=2, layer_stride=2 * host_plane,
+                               kv_stride=host_plane, row_stride=row_bytes, row_bytes=row_bytes, rows=HOST_ROWS,
+                               owner=arena)
+        host_table = ((torch.arange(R, device=gpu).view(R, 1) * T + torch.arange(T, device=gpu).view(1, T))
+                      % HOST_ROWS).to(torch.int32)
+        buffers = HotBuffers(L, R, T, C, gpu, table_dtype=torch.int16)
+        recent = (lengths.view(1, R, 1) - C + torch.arange(C, device=gpu).view(1, 1, C)).expand(L, R, C)
+        local = torch.rand((L, R, C), generator=gen, device=gpu).argsort(-1)
+        buffers.install(recent, local)
+        rows = torch.arange(R, device=gpu)
+        move_kv(host_planes, host_table[rows.view(1, R, 1), recent].contiguous(), planes,
+                (local + buffers.slot_base.view(1, R, 1)).to(torch.int32).contiguous(),
+                torch.full((L, R), C, dtype=torch.int32, device=gpu))
+        lengths32 = lengths.to(torch.int32)
+        slots = torch.empty((L, R, K), dtype=torch.int32, device=gpu)
+        misses = torch.empty_like(slots)
+        counts = torch.empty((L, R), dtype=torch.int32, device=gpu)
+        src, dst = torch.empty_like(slots), torch.empty_like(slots)
+        output = torch.empty((R, L, 2, K, row_bytes), dtype=torch.uint8, device=gpu)
+        chunk_rows = layout.chunk_bytes // row_bytes
+        remap_count = round(0.05 * backing.chunk_count)
+        torch.cuda.synchronize()
+        print(f"[config 5 full] ready: {backing.chunk_count} chunks, remap {remap_count} per step", flush=True)
+        for step in range(2):
+            # remap: empty the chosen chunks' hot slots, unmap them and commit them again (zero-filled)
+            chosen = rng.choice(np.arange(1, backing.chunk_count), size=remap_count, replace=False)
+            ids = torch.tensor(chosen, device=gpu)
+            plane, within = ids // layout.plane_chunks, ids % layout.plane_chunks
+            slot = within.view(-1, 1) * chunk_rows + torch.arange(chunk_rows, device=gpu).view(1, -1)
+            layer = (plane // 2).view(-1, 1).expand_as(slot)
+            keep = (slot >= 1) & (slot < layout.rows)
+            slot, layer = slot[keep], layer[keep]
+            req, loc = (slot - 1) // C, (slot - 1) % C
+            token = buffers.slot_token[layer, req, loc].long()
+            held = token >= 0
+            buffers.table[layer[held], req[held], token[held]] = 0
+            buffers.slot_token[layer, req, loc] = -1
+            buffers.stamps[layer, req, loc] = INT32_MIN
+            buffers.refresh_bits()
+            backing.reclaim(chosen.tolist())
+            backing.ensure(chosen.tolist())
+            topk = _composite_topk_gpu(gen, L, R, K, lengths)
+            resolve_resident(topk, buffers.table, None, rows, lengths32, rows, slots, 1, misses=misses,
+                             miss_count=counts, resident_bits=buffers.bits, slot_base=buffers.slot_base)
+            swap_in(topk, 1, rows, rows, slots, misses, counts, buffers, host_table, src, dst, check=True)
+            move_kv(host_planes, src, planes, dst, counts)
+            gather_kv(planes, slots, output)
+            torch.cuda.synchronize()
+            print(f"[config 5 full] step {step}: {int(counts.sum())} of {L * R * K} lanes promoted", flush=True)
+            # every gathered row is its token's host row
+            for layer_index in range(L):
+                host_rows = torch.gather(host_table, 1, topk[layer_index].long()).long()          # [R, K]
+                for kv in range(2):
+                    want = host_gpu[layer_index, kv][host_rows]                                    # [R, K, row]
+                    assert torch.equal(output[:, layer_index, kv], want), (step, layer_index, kv)
+            # every selected lane is resident in the slot it read
+            local_slot = slots.long() - buffers.slot_base.view(1, R, 1)
+            assert bool(((local_slot >= 0) & (local_slot < C)).all()), step
+            assert torch.equal(torch.gather(buffers.slot_token, 2, local_slot).long(), topk.long()), step
+            # the token <-> slot state is a bijection, and the summary is exact
+            slot_token = buffers.slot_token.long()
+            held = slot_token >= 0
+            entry = torch.gather(buffers.table.long(), 2, slot_token.clamp_min(0))              # [L, R, C]
+            assert torch.equal(entry[held], (torch.arange(C, device=gpu).expand(L, R, C) + 1)[held]), step
+            assert int((buffers.table != 0).sum()) == int(held.sum()), step
+            assert torch.equal(buffers.bits, build_residency_bits(buffers.table)), step
     finally:
         torch.cuda.synchronize()
         backing.close()
