@@ -18,7 +18,8 @@ box (own read / write / copy kernels), the lookup variants timed in
 alternating arms, configs 1, 2 and 4 (topk-gather, block-gather, migration
 below), each with its own roofline, parity flags and CPU baseline, configs 4
 and 5 also with the VMM spare pool (--spare-chunks: reclaimed chunks' memory
-kept for the next commits), and the reference's two microbenchmarks
+kept for the next commits), the decode read at hot capacity 8192 (81 % hits,
+the lookup's longest default case), and the reference's two microbenchmarks
 (lookup-micro, virtual-addressing).
 The CPU baseline is the reference's torch CPU path restated
 (oracle/torch_path.py: adaptive_sparse/request_residency.py:819-825, nonzero,
@@ -534,7 +535,9 @@ def run_decode_read(torch, args, device):
     config = {"workload": "hisparse-topk-decode-read", "requests": R, "context": T, "layers": L, "kv_heads": 2,
               "head_dim": 128, "topk": K, "hot_capacity": C, "pool_bytes": layout.capacity_bytes,
               "chunk_bytes": layout.chunk_bytes}
-    lookup_traffic = read_traffic("resolve_resident_hisparse_decode.md")
+    # The committed counter summaries were taken at hot capacity 4096; other capacities move other bytes.
+    profiled = C == 4096
+    lookup_traffic = read_traffic("resolve_resident_hisparse_decode.md") if profiled else None
     extra = {"lookups_per_s": round(lanes / (phase["lookup"] / 1e3), 1),
              "lookup_us_per_step": round(phase["lookup"] * 1e3, 2),
              "lookup_us_per_layer": round(phase["lookup"] * 1e3 / L, 2),
@@ -553,7 +556,7 @@ def run_decode_read(torch, args, device):
              "event_spread": step_spread,
              "hit_rate": round(hits / lanes, 4), "pool_commit_s": round(commit_s, 3)}
     roof = roofline(achieved, "copy_small_rows<KvGather,16> (ekv_gather_kv)", gather_bytes, phase["gather"],
-                    read_traffic("gather_kv_hisparse_decode.md"))
+                    read_traffic("gather_kv_hisparse_decode.md") if profiled else None)
     result = envelope(args, gather_bytes / (step_ms / 1e3) / 1e9, step_ms, config, roof, baseline, extra)
     del raw, output
     torch.cuda.synchronize()
@@ -1557,6 +1560,8 @@ EXTRA_CONFIGS = (("config1_topk_gather", "topk-gather", {}), ("config2_block_gat
                  ("config5_composite", "composite", {"steps": 3, "warmup": 1, "no_cpu_baseline": True}),
                  ("config5_composite_spare_pool", "composite",
                   {"steps": 3, "warmup": 1, "spare_chunks": COMPOSITE_SPARE_CHUNKS, "no_cpu_baseline": True}),
+                 # The decode read at twice the hot capacity (81 % hits): the lookup's longest default case.
+                 ("config3_capacity_8192", "decode-read", {"capacity": 8192, "no_cpu_baseline": True}),
                  ("lookup_micro", "lookup-micro", {}),
                  ("virtual_addressing", "virtual-addressing", {}),
                  ("residency_summary", "residency-summary", {}))
@@ -1577,7 +1582,8 @@ def summary(result):
             "higher_is_better", "vs_baseline", "per_batch", "correct", "verified_against_host_copy",
             "gpu_work_ms", "overlap", "remap_parts_ms", "vmm_us_per_chunk", "vmm_chunks_per_tick",
             "gpu_round_trip_ms", "promote_gbs_over_pcie", "swap_in", "graph_replay",
-            "per_support_set", "verified_against_torch", "shift0")
+            "per_support_set", "verified_against_torch", "shift0", "lookup_roofline", "event_spread",
+            "lookup_arms_back_to_back", "lookup_variants_identical")
     return {key: result[key] for key in keys if key in result}
 
 

@@ -1067,17 +1067,23 @@ void resolve_runs_pipe2_kernel(const LookupArgs a, uint32_t items, uint32_t coun
     runs_issue_ids(a, layer_next, nxt, n <= 1, next_loads);
     meta_request(a, cur);
     meta_request(a, nxt);
-    meta_request(a, mine);
     runs_issue_bits(a, layer, cur, false, first_loads);
     runs_issue_bits(a, layer_next, nxt, n <= 1, next_loads);
+    // Items 0 and 1 read their metadata with scalar loads; item t's (per
+    // thread) are vector loads, and vector loads complete in issue order. Its
+    // request row is therefore read after the summary rows are issued (its
+    // wait then covers loads the first stage waits for anyway, not the Top-K
+    // ids alone), and its slot base is written to LDS only after the first
+    // stage has issued its table reads.
+    meta_request(a, mine);
     meta_base<TableT>(a, cur);
     meta_base<TableT>(a, nxt);
     meta_base<TableT>(a, mine);
-    if (threadIdx.x < n) {
-        meta[threadIdx.x] = uint4{mine.row, mine.req, mine.base, static_cast<uint32_t>(mine.bound)};
-    }
     RunsPending pend;
     runs_begin<TableT>(a, layer, cur, first_loads, staged_bits[0], last_piece, live_piece, pend);
+    if (threadIdx.x < n) {   // read from the second item on, after the next first stage's barrier
+        meta[threadIdx.x] = uint4{mine.row, mine.req, mine.base, static_cast<uint32_t>(mine.bound)};
+    }
     for (uint32_t k = 0;; ++k) {
         // Item k's slots from its table entries.
         int32_t slot[kIters];

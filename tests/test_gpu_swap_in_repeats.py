@@ -228,3 +228,31 @@ def test_large_hot_buffers_evict_in_lru_order(gpu, capacity):
         state = _step(gpu, buffers, topk, bs, np.full(R, T), state, step, host_table)
         evicted += int(((before >= 0) & (state["slot_token"] != before)).sum())
     assert evicted > 0
+
+
+@pytest.mark.parametrize("capacity", [4096, 8192])
+@pytest.mark.parametrize("K,bs", [(2049, 1), (1000, 3), (1024, 4)])
+def test_rows_wider_than_2048_lanes_evict_in_lru_order(gpu, capacity, K, bs):
+    """Rows of 2049 to 4096 lanes (their lane state is held 16 lanes per thread) over hot buffers of 4096 and
+    8192 slots, nearly full, with repeated blocks: 3 steps against the oracle."""
+    rng = np.random.default_rng(K * 7 + capacity)
+    L, R = 1, 2
+    W = K * bs
+    T = capacity + 2 * W
+    buffers = HotBuffers(L, R, T, capacity, gpu, table_dtype=torch.int16 if bs == 3 else torch.int32)
+    filled = capacity - 3
+    tokens = np.stack([[rng.choice(T, filled, replace=False) for _ in range(R)] for _ in range(L)])
+    local = np.stack([[rng.permutation(capacity)[:filled] for _ in range(R)] for _ in range(L)])
+    buffers.install(torch.tensor(tokens), torch.tensor(local))
+    host_table = torch.tensor(rng.permutation(R * T), dtype=torch.int32).reshape(R, T)
+    state = {"table": _global(buffers), "slot_token": buffers.slot_token.cpu().numpy(),
+             "stamps": buffers.stamps.cpu().numpy()}
+    evicted = 0
+    for step in range(3):
+        topk = rng.integers(0, T // bs, (L, R, K))
+        topk[..., 1::97] = topk[..., 0:1]                        # repeated blocks
+        topk[..., 5::211] = -1
+        before = state["slot_token"].copy()
+        state = _step(gpu, buffers, topk, bs, np.array([T, T - 5]), state, step, host_table)
+        evicted += int(((before >= 0) & (state["slot_token"] != before)).sum())
+    assert evicted > 0
