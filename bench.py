@@ -1295,6 +1295,12 @@ def run_composite(torch, args, device):
     log(f"composite ready: T={T}, host arena {arena.nbytes / 1e9:.1f} GB, remap {remap_count} chunks/step")
 
     remap_parts = {"invalidate_ms": [], "unmap_ms": [], "map_ms": []}
+    # Device-resident fill values: a Python scalar in an indexed assignment is copied from pageable host
+    # memory, a copy that blocks the host until the stream's queued work (the summary rebuild) has run.
+    fill = {"table": torch.zeros((), dtype=buffers.table.dtype, device=device),
+            "slot_token": torch.full((), -1, dtype=torch.int32, device=device),
+            "stamps": torch.full((), INT32_MIN, dtype=torch.int32, device=device),
+            "touched": torch.ones((), dtype=torch.bool, device=device)}
 
     def invalidate():
         """Choose `remap_count` random chunks (never chunk 0) and empty their hot slots (queued, no wait).
@@ -1312,12 +1318,12 @@ def run_composite(torch, args, device):
         req, loc = (slot - 1) // C, (slot - 1) % C
         token = buffers.slot_token[layer, req, loc].long()
         held = token >= 0
-        buffers.table[layer[held], req[held], token[held]] = 0
-        buffers.slot_token[layer, req, loc] = -1
-        buffers.stamps[layer, req, loc] = INT32_MIN
+        buffers.table[layer[held], req[held], token[held]] = fill["table"]
+        buffers.slot_token[layer, req, loc] = fill["slot_token"]
+        buffers.stamps[layer, req, loc] = fill["stamps"]
         build_residency_bits(buffers.table, out=buffers.bits)
         touched = torch.zeros((L, R), dtype=torch.bool, device=device)
-        touched[layer, req] = True
+        touched[layer, req] = fill["touched"]
         return chosen.tolist(), touched
 
     def remap_chunks(chosen):
