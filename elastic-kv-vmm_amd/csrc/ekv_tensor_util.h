@@ -98,6 +98,13 @@ struct IndexRef {
         return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
                                     static_cast<uint32_t>(lo));
     }
+
+    // The element's low 32 bits (its value truncated to int32), one load and
+    // no branch: for batches of independent loads that must all be in flight
+    // before any is waited for.
+    __device__ __forceinline__ int32_t low(int64_t i) const {
+        return *reinterpret_cast<const int32_t*>(static_cast<const char*>(data) + i * stride * (is64 ? 8 : 4));
+    }
 #endif
 };
 

@@ -117,6 +117,18 @@ struct SwapArgs {
     uint32_t bitmap_words;          // ceil(T / 32)
 };
 
+// A Top-K id (int32 or int64 elements) without a branch on the element type:
+// the low word, then the high word (for int32 ids the low word again,
+// replaced by its sign). A branch per id would make the compiler wait for
+// each load before issuing the next.
+__device__ __forceinline__ int64_t load_id(const void* row, int32_t is64, int64_t index) {
+    const char* at = static_cast<const char*>(row) + index * (is64 ? 8 : 4);
+    const int32_t lo = *reinterpret_cast<const int32_t*>(at);
+    const int32_t high = *reinterpret_cast<const int32_t*>(at + (is64 ? 4 : 0));
+    return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(is64 ? high : lo >> 31)) << 32) |
+                                static_cast<uint32_t>(lo));
+}
+
 // Writes a token -> slot table entry (int32 global slot or int16 local slot + 1).
 __device__ __forceinline__ void set_entry(const SwapArgs& a, int64_t offset, int32_t value) {
     if (a.table16) {
@@ -326,6 +338,15 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
         ? static_cast<const void*>(static_cast<const int64_t*>(a.topk) + l * a.topk_sl + b * a.topk_sb)
         : static_cast<const void*>(static_cast<const int32_t*>(a.topk) + l * a.topk_sl + b * a.topk_sb);
 
+    // One workgroup owns each (layer, request) hot buffer: a second selected
+    // row naming the same request would race on it, so both rows are refused.
+    // Thread t checks selection entry t (and t + kThreads, ... for longer
+    // selections). Vector loads complete in issue order, so entry t is read
+    // before batch 1 and its request row right after batch 1 is issued: batch 2
+    // then waits for batch 1 alone, not for two dependent reads behind it.
+    const int64_t selected_count = a.selected_count;   // at least 1
+    const int64_t first_j = threadIdx.x;
+    const int64_t first_other = a.selected.fetch(first_j < selected_count ? first_j : selected_count - 1);
     // Batch 1: stamps, the lookup slots of this thread's lanes, its miss-list entries.
     int32_t held_stamp[kSlotRegs];
 #pragma unroll
@@ -341,10 +362,11 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
         lane_slot[k] = slots[o * a.sl_o];
         miss_lane[k] = misses[o * a.mi_o];   // entries at or past the count are read but not used
     }
-    // One workgroup owns each (layer, request) hot buffer: a second selected
-    // row naming the same request would race on it, so both rows are refused.
-    bool shared_request = false;
-    for (int64_t j = threadIdx.x; j < a.selected_count; j += kThreads) {
+    const bool first_in_range =
+        first_j < selected_count && first_j != blockIdx.x && first_other >= 0 && first_other < a.batch;
+    const int64_t first_req = a.rows.fetch(first_in_range ? first_other : b);   // b is a valid batch row
+    bool shared_request = first_in_range && first_req == req;
+    for (int64_t j = first_j + kThreads; j < selected_count; j += kThreads) {
         const int64_t other = a.selected[j];
         shared_request |= j != blockIdx.x && other >= 0 && other < a.batch && a.rows[other] == req;
     }
@@ -354,8 +376,7 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
     for (int k = 0; k < kLaneRegs; ++k) {
         const uint32_t lane = static_cast<uint32_t>(min(max(miss_lane[k], 0), static_cast<int32_t>(W - 1)));
         const uint32_t blk = a.block_size == 1 ? lane : a.block_div.div(lane);
-        miss_block[k] = a.topk64 ? static_cast<const int64_t*>(topk_row)[blk * a.topk_sk]
-                                 : static_cast<int64_t>(static_cast<const int32_t*>(topk_row)[blk * a.topk_sk]);
+        miss_block[k] = load_id(topk_row, a.topk64, blk * a.topk_sk);
     }
     const int32_t m = counted < 0 ? 0 : (counted > W ? static_cast<int32_t>(W) : counted);
     shared_request = __syncthreads_or(shared_request);
@@ -689,7 +710,7 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
             entry_of[k] = entry;
             victim_of[k] = victim;
             old_of[k] = slot_token[static_cast<int64_t>(victim) * a.st_c];
-            host_row_of[k] = static_cast<int32_t>(a.host_table[req * a.host_sr + token * a.host_st]);
+            host_row_of[k] = a.host_table.low(req * a.host_sr + token * a.host_st);
         }
 #pragma unroll
         for (int k = 0; k < kLaneRegs; ++k) {
