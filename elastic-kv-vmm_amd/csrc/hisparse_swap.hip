@@ -366,16 +366,20 @@ __global__ __launch_bounds__(kThreads) void hisparse_swap_kernel(const HsArgs a)
             kinds[k] = kind;
             auxes[k] = aux;
         }
+        // One unconditional load per lane, its address chosen by selects (a
+        // branch per kind made the compiler wait for each load before the
+        // next): a hit's device row, a miss's host row, otherwise the
+        // request's first device row, read and not used.
         int64_t rows[kLanesPerThread];
 #pragma unroll
         for (int k = 0; k < kLanesPerThread; ++k) {
             const int64_t o = threadIdx.x + k * kThreads;
-            rows[k] = -1;
-            if (kinds[k] == kHit) {
-                rows[k] = load_index(a.dev_locs, a.dev_locs64, r * a.dl_sr + int64_t{auxes[k]} * a.dl_ss);
-            } else if (kinds[k] == kMiss) {
-                rows[k] = load_index(a.host_locs, a.host_locs64, r * a.hl_sr + int64_t{s.lane_tok[o]} * a.hl_st);
-            }
+            const bool hit = kinds[k] == kHit, miss = kinds[k] == kMiss;
+            const int64_t token = s.lane_tok[miss ? o : 0];
+            const void* base = miss ? a.host_locs : a.dev_locs;
+            const int64_t at = miss ? r * a.hl_sr + token * a.hl_st : r * a.dl_sr + (hit ? int64_t{auxes[k]} : 0) * a.dl_ss;
+            const int64_t row = load_index(base, miss ? a.host_locs64 : a.dev_locs64, at);
+            rows[k] = hit || miss ? row : -1;
         }
 #pragma unroll
         for (int k = 0; k < kLanesPerThread; ++k) {
@@ -511,7 +515,8 @@ __global__ __launch_bounds__(kThreads) void hisparse_swap_kernel(const HsArgs a)
             for (int k = 0; k < kLanesPerThread; ++k) {
                 const int64_t m = threadIdx.x + k * kThreads;
                 const int32_t slot = m < misses ? s.victim[m] : -1;
-                loc[k] = slot >= 0 ? device_row(a, r, slot) : -1;
+                const int64_t row = device_row(a, r, slot >= 0 ? slot : 0);   // unconditional: loads in flight together
+                loc[k] = slot >= 0 ? row : -1;
             }
 #pragma unroll
             for (int k = 0; k < kLanesPerThread; ++k) {
