@@ -102,38 +102,50 @@ int decode_step(const ekv_step_args& s, void* workspace, uint64_t workspace_byte
     const ekv_tensor src = int32_view(base + list, layers, batch, width, 3);
     const ekv_tensor dst = int32_view(base + 2 * list, layers, batch, width, 3);
     const ekv_tensor counts = int32_view(base + 3 * list, layers, batch, 1, 2);
+    const ekv_tensor& table = need(s.table, "table");
+    // The four stages, queued in order. Every stage is checked first without
+    // launching (CheckOnly), so an argument a later stage refuses fails the
+    // call before the lookup has written its slots.
+    const auto stages = [&] {
+        if (table.dtype == EKV_INT16) {
+            check_step(ekv_resolve_resident_local(s.topk, s.table, s.slot_base, s.resident_bits, s.bits_shift,
+                                                  s.rows, s.lengths, s.selected, s.slots, &misses, &counts,
+                                                  s.block_size, stream),
+                       "lookup");
+        } else if (s.resident_bits != nullptr) {
+            check_step(ekv_resolve_resident_bits(s.topk, s.table, s.resident_bits, s.bits_shift, s.rows, s.lengths,
+                                                 s.selected, s.slots, &misses, &counts, s.block_size, stream),
+                       "lookup");
+        } else {
+            check_step(ekv_resolve_resident(s.topk, s.table, nullptr, s.rows, s.lengths, s.selected, s.slots,
+                                            &misses, &counts, s.block_size, stream),
+                       "lookup");
+        }
+        if (s.step_counter != nullptr) {
+            check_step(ekv_swap_in_counted(s.topk, s.block_size, s.rows, s.selected, s.slots, &misses, &counts,
+                                           s.table, s.resident_bits, s.bits_shift, s.resident_counts, s.slot_token,
+                                           s.stamps, s.slot_base, s.host_table, &src, &dst, s.step_counter,
+                                           s.status, stream),
+                       "swap-in");
+        } else {
+            check_step(ekv_swap_in(s.topk, s.block_size, s.rows, s.selected, s.slots, &misses, &counts, s.table,
+                                   s.resident_bits, s.bits_shift, s.resident_counts, s.slot_token, s.stamps,
+                                   s.slot_base, s.host_table, &src, &dst, s.step, s.status, stream),
+                       "swap-in");
+        }
+        check_step(ekv_move_kv(s.host, &src, s.pool, &dst, &counts, 1, stream), "promote");
+        check_step(ekv_gather_kv(s.pool, s.slots, s.out, 1, stream), "gather");
+    };
+    {
+        CheckOnly checking;
+        stages();
+    }
     const uint64_t rows_total = static_cast<uint64_t>(layers * batch);
     const uint32_t zero_blocks = static_cast<uint32_t>(std::min<uint64_t>((rows_total + 255) / 256, 1024));
     zero_words_kernel<<<dim3(zero_blocks), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(
         static_cast<int32_t*>(counts.data), rows_total);
     check_hip(hipGetLastError(), "launch count reset");
-    const ekv_tensor& table = need(s.table, "table");
-    if (table.dtype == EKV_INT16) {
-        check_step(ekv_resolve_resident_local(s.topk, s.table, s.slot_base, s.resident_bits, s.bits_shift, s.rows,
-                                              s.lengths, s.selected, s.slots, &misses, &counts, s.block_size, stream),
-                   "lookup");
-    } else if (s.resident_bits != nullptr) {
-        check_step(ekv_resolve_resident_bits(s.topk, s.table, s.resident_bits, s.bits_shift, s.rows, s.lengths,
-                                             s.selected, s.slots, &misses, &counts, s.block_size, stream),
-                   "lookup");
-    } else {
-        check_step(ekv_resolve_resident(s.topk, s.table, nullptr, s.rows, s.lengths, s.selected, s.slots, &misses,
-                                        &counts, s.block_size, stream),
-                   "lookup");
-    }
-    if (s.step_counter != nullptr) {
-        check_step(ekv_swap_in_counted(s.topk, s.block_size, s.rows, s.selected, s.slots, &misses, &counts, s.table,
-                                       s.resident_bits, s.bits_shift, s.resident_counts, s.slot_token, s.stamps,
-                                       s.slot_base, s.host_table, &src, &dst, s.step_counter, s.status, stream),
-                   "swap-in");
-    } else {
-        check_step(ekv_swap_in(s.topk, s.block_size, s.rows, s.selected, s.slots, &misses, &counts, s.table,
-                               s.resident_bits, s.bits_shift, s.resident_counts, s.slot_token, s.stamps, s.slot_base,
-                               s.host_table, &src, &dst, s.step, s.status, stream),
-                   "swap-in");
-    }
-    check_step(ekv_move_kv(s.host, &src, s.pool, &dst, &counts, 1, stream), "promote");
-    check_step(ekv_gather_kv(s.pool, s.slots, s.out, 1, stream), "gather");
+    stages();
     return 0;
 }
 

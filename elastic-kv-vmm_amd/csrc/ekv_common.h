@@ -23,6 +23,30 @@ inline void check_hip(hipError_t status, const char* what) {
     }
 }
 
+// Checking without launching: while a CheckOnly guard lives on this thread,
+// the kernel entry points run all of their argument checks and return before
+// their first launch. ekv_decode_step checks its four stages this way before
+// it queues any of them, so a bad argument to a later stage fails the call
+// with nothing queued instead of after the earlier stages have written their
+// outputs.
+inline bool& check_only_flag() {
+    static thread_local bool flag = false;
+    return flag;
+}
+
+inline bool check_only() { return check_only_flag(); }
+
+class CheckOnly {
+public:
+    CheckOnly() : previous_(check_only_flag()) { check_only_flag() = true; }
+    ~CheckOnly() { check_only_flag() = previous_; }
+    CheckOnly(const CheckOnly&) = delete;
+    CheckOnly& operator=(const CheckOnly&) = delete;
+
+private:
+    bool previous_;
+};
+
 // Makes `device` current for the lifetime of the guard and restores the
 // caller's current device afterwards (HIP's current device is per thread).
 class DeviceGuard {

@@ -718,13 +718,13 @@ void resolve_runs_pipe_kernel(const LookupArgs a, uint32_t items, uint32_t count
         RunsLoads<kBitLoads> next_loads;
         if (cur.row != kNoRow) {  // uniform
             const bool table_ok = cur.req != kNoRow;
-            if (table_ok) {
+            // Staged unconditionally (an item without a table row read summary
+            // row 0, and none of its lanes is valid), so the loads are not
+            // moved into a branch that waits for every load in flight.
 #pragma unroll
-                for (int h = 0; h < kBitLoads; ++h) {
-                    const uint32_t piece = h * kThreads + threadIdx.x;
-                    *reinterpret_cast<i32x4*>(&staged_bits[4 * (piece < last_piece ? piece : last_piece)]) =
-                        loads.bits[h];
-                }
+            for (int h = 0; h < kBitLoads; ++h) {
+                const uint32_t piece = h * kThreads + threadIdx.x;
+                *reinterpret_cast<i32x4*>(&staged_bits[4 * (piece < last_piece ? piece : last_piece)]) = loads.bits[h];
             }
             __syncthreads();
             const int32_t block[kIters] = {loads.ids[0].x, loads.ids[0].y, loads.ids[0].z, loads.ids[0].w,
@@ -924,12 +924,13 @@ __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupAr
 // k's compaction barriers, which the one-stage kernel runs with only the next
 // item's Top-K in flight. The summary row is staged in two LDS buffers used
 // alternately: item k + 1 writes the buffer item k - 1 read, and item k - 1's
-// compaction barriers separate the two. The prologue issues the first two
-// items' loads as soon as their addresses are known (Top-K ids after the
-// batch row, the summary row after the request row) instead of after all
-// of the workgroup's index metadata: one dependent memory level fewer before
-// the first table reads (0.5-0.7 us of a 60-layer launch inside a decode
-// step, 2 us of a 30-layer one).
+// compaction barriers separate the two. The prologue reaches the first
+// item's table reads in three memory levels: the index metadata and Top-K ids
+// of the first two items (guessing the identity selection), their summary
+// rows, then the table entries. Its index reads are vector loads from
+// clamped indices with no per-lane branch; as scalar loads and branchy reads
+// they had been a chain of six or more dependent round trips (one layer per
+// launch: 5.9 against 6.3 us).
 
 // One item between its two stages: its table entries in flight and its lanes'
 // classification.
@@ -946,10 +947,11 @@ __device__ __forceinline__ void runs_begin(const LookupArgs& a, uint32_t layer, 
                                            const RunsLoads<1>& loads, uint32_t* staged, uint32_t last_piece,
                                            const bool (&live_piece)[2], RunsPending& p) {
     const bool table_ok = m.row != kNoRow && m.req != kNoRow;   // uniform
-    if (table_ok) {
-        *reinterpret_cast<i32x4*>(&staged[4 * (threadIdx.x < last_piece ? threadIdx.x : last_piece)]) =
-            loads.bits[0];
-    }
+    // Staged unconditionally: an item without a table row read summary row 0
+    // and no lane reads it (every lane is invalid). A store under the test let
+    // the compiler move the summary row's load into the branch and wait there
+    // for every load in flight.
+    *reinterpret_cast<i32x4*>(&staged[4 * (threadIdx.x < last_piece ? threadIdx.x : last_piece)]) = loads.bits[0];
     __syncthreads();
     const int32_t block[kIters] = {loads.ids[0].x, loads.ids[0].y, loads.ids[0].z, loads.ids[0].w,
                                    loads.ids[1].x, loads.ids[1].y, loads.ids[1].z, loads.ids[1].w};
@@ -1008,6 +1010,58 @@ __device__ __forceinline__ void meta_base(const LookupArgs& a, RunsMeta& m) {
     }
 }
 
+// Workgroup-uniform index reads for the prologue, as vector loads. The
+// compiler makes a uniform read a scalar load, and it waits for every
+// outstanding scalar load before the first use of any of them, so the
+// prologue's independent index reads (and the kernel-argument reloads between
+// them) became a chain of memory round trips. Vector loads complete in issue
+// order: a batch of them is waited for once, and scalar waits do not wait for
+// them. An opaque per-lane zero in the address keeps them vector loads;
+// index_value reads the value back as a uniform (scalar) one.
+struct PendingIndex {
+    int32_t lo, hi;
+};
+
+__device__ __forceinline__ uint32_t opaque_zero() {
+    uint32_t zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    return zero;
+}
+
+// Element i of `r`: its low word and, for int64 arrays, its high word (for
+// int32 arrays the element again); no branch on the element type.
+__device__ __forceinline__ PendingIndex issue_index(const IndexRef& r, int64_t i, uint32_t zero) {
+    const char* at = static_cast<const char*>(r.data) + i * r.stride * (r.is64 ? 8 : 4) + zero;
+    return PendingIndex{*reinterpret_cast<const int32_t*>(at), *reinterpret_cast<const int32_t*>(at + (r.is64 ? 4 : 0))};
+}
+
+__device__ __forceinline__ int64_t index_value(const IndexRef& r, const PendingIndex& p) {
+    // Both words are read back unconditionally: a read under the element-type
+    // test let the compiler move the high word's load into that branch and
+    // wait there for every load in flight.
+    const int32_t lo = __builtin_amdgcn_readfirstlane(p.lo);
+    const int32_t high = __builtin_amdgcn_readfirstlane(p.hi);
+    const int32_t hi = r.is64 ? high : (lo >> 31);
+    return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo));
+}
+
+// The same element read by a per-thread load (any value per lane).
+__device__ __forceinline__ int64_t lane_value(const IndexRef& r, const PendingIndex& p) {
+    const int32_t hi = r.is64 ? p.hi : (p.lo >> 31);
+    return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                static_cast<uint32_t>(p.lo));
+}
+
+// The request row and bound of item metadata whose batch row is known.
+__device__ __forceinline__ void meta_apply(const LookupArgs& a, RunsMeta& m, int64_t req, int64_t length) {
+    if (m.row != kNoRow) {
+        const bool table_ok = req >= 0 && req < a.table_rows && a.table_cols > 0;
+        const int64_t bound = length < a.table_cols ? length : a.table_cols;
+        m.req = table_ok ? static_cast<uint32_t>(req) : kNoRow;
+        m.bound = bound > 0 ? static_cast<int32_t>(bound) : 0;
+    }
+}
+
 // runs_issue in two parts: the Top-K ids need only the batch row, the
 // summary row needs the request.
 __device__ __forceinline__ void runs_issue_ids(const LookupArgs& a, uint32_t layer, const RunsMeta& m,
@@ -1020,6 +1074,19 @@ __device__ __forceinline__ void runs_issue_ids(const LookupArgs& a, uint32_t lay
         const uint32_t first = h * kHalf + threadIdx.x * 4;
         const uint32_t at = first_only ? 0u : (first < a.width ? first : a.width - 4);
         l.ids[h] = stream_load(reinterpret_cast<const i32x4*>(element<true>(topk, 1, at)));
+    }
+}
+
+// Keeps a guessed item's metadata and Top-K loads when its selection entry
+// names the guessed row; otherwise re-reads them for the row the entry names
+// (none for an entry outside the batch: every lane of the item is invalid).
+__device__ __forceinline__ void settle_guess(const LookupArgs& a, uint32_t layer, int64_t entry, bool first_only,
+                                             RunsMeta& m, RunsLoads<1>& l) {
+    const uint32_t row = entry >= 0 && entry < a.batch ? static_cast<uint32_t>(entry) : kNoRow;
+    if (row != m.row) {   // uniform
+        m = RunsMeta{row, kNoRow, 0u, 0};
+        meta_request(a, m);
+        runs_issue_ids(a, layer, m, first_only, l);
     }
 }
 
@@ -1049,38 +1116,65 @@ void resolve_runs_pipe2_kernel(const LookupArgs a, uint32_t items, uint32_t coun
     const uint32_t last_piece = static_cast<uint32_t>((a.bits_words + 3) >> 2) - 1;
     const uint32_t n = (items - blockIdx.x + gridDim.x - 1) / gridDim.x;  // this workgroup's items, <= kPipeMaxItems
 
-    // Prologue, one memory level at a time: the batch rows of items 0 and 1
-    // (every thread) and of item t (thread t < n); then items 0 and 1's Top-K
-    // ids beside the request rows and lengths; then their summary rows beside
-    // the slot bases. Item t's metadata goes to LDS for the later iterations,
-    // published by the first stage's barrier.
+    // Prologue. Items 0 and 1 guess the identity selection (entry j names
+    // batch row j: every batch row, the decode default), so their selection
+    // entries, the guessed rows' request rows and lengths and their Top-K ids
+    // are requested at once; settle_guess re-reads them for the row an entry
+    // actually names when it differs. Then their summary rows and slot bases.
+    // Thread t reads item t's selection entry beside them, its request row and
+    // length beside the summary rows, and its slot base after the first
+    // item's table reads are issued (vector loads complete in issue order, so
+    // waiting for it then waits for nothing the first item does not need
+    // next); item t's metadata goes to LDS for the later iterations, published
+    // by the next first stage's barrier. Every per-thread read is
+    // unconditional, from a clamped index: a read under a per-lane condition
+    // let the compiler wait for all loads in flight inside that branch.
     const uint32_t k_next = n > 1 ? 1u : 0u;
     const uint32_t k_mine = threadIdx.x < n ? threadIdx.x : 0u;
     uint32_t layer = count_div.div(blockIdx.x);
     uint32_t layer_next = count_div.div(blockIdx.x + k_next * gridDim.x);
-    RunsMeta cur = meta_row(a, blockIdx.x, count, count_div);
-    RunsMeta nxt = meta_row(a, blockIdx.x + k_next * gridDim.x, count, count_div);
-    RunsMeta mine = meta_row(a, blockIdx.x + k_mine * gridDim.x, count, count_div);
+    const uint32_t zero = opaque_zero();
+    const uint32_t item_next = blockIdx.x + k_next * gridDim.x;
+    const uint32_t item_mine = blockIdx.x + k_mine * gridDim.x;
+    const uint32_t j_cur = blockIdx.x - layer * count, j_next = item_next - layer_next * count;
+    const uint32_t j_mine = item_mine - count_div.div(item_mine) * count;
+    RunsMeta cur{j_cur < a.batch ? j_cur : kNoRow, kNoRow, 0u, 0};
+    RunsMeta nxt{j_next < a.batch ? j_next : kNoRow, kNoRow, 0u, 0};
+    const PendingIndex entry_cur = issue_index(a.selected, j_cur, zero);
+    const PendingIndex entry_next = issue_index(a.selected, j_next, zero);
+    const PendingIndex req_cur = issue_index(a.rows, cur.row != kNoRow ? cur.row : 0u, zero);
+    const PendingIndex len_cur = issue_index(a.lengths, cur.row != kNoRow ? cur.row : 0u, zero);
+    const PendingIndex req_next = issue_index(a.rows, nxt.row != kNoRow ? nxt.row : 0u, zero);
+    const PendingIndex len_next = issue_index(a.lengths, nxt.row != kNoRow ? nxt.row : 0u, zero);
+    const PendingIndex entry_mine = issue_index(a.selected, j_mine, zero);
     RunsLoads<1> first_loads;
     RunsLoads<1> next_loads;
     runs_issue_ids(a, layer, cur, false, first_loads);
     runs_issue_ids(a, layer_next, nxt, n <= 1, next_loads);
-    meta_request(a, cur);
-    meta_request(a, nxt);
+    meta_apply(a, cur, index_value(a.rows, req_cur), index_value(a.lengths, len_cur));
+    meta_apply(a, nxt, index_value(a.rows, req_next), index_value(a.lengths, len_next));
+    settle_guess(a, layer, index_value(a.selected, entry_cur), false, cur, first_loads);
+    settle_guess(a, layer_next, index_value(a.selected, entry_next), n <= 1, nxt, next_loads);
     runs_issue_bits(a, layer, cur, false, first_loads);
     runs_issue_bits(a, layer_next, nxt, n <= 1, next_loads);
-    // Items 0 and 1 read their metadata with scalar loads; item t's (per
-    // thread) are vector loads, and vector loads complete in issue order. Its
-    // request row is therefore read after the summary rows are issued (its
-    // wait then covers loads the first stage waits for anyway, not the Top-K
-    // ids alone), and its slot base is written to LDS only after the first
-    // stage has issued its table reads.
-    meta_request(a, mine);
-    meta_base<TableT>(a, cur);
-    meta_base<TableT>(a, nxt);
-    meta_base<TableT>(a, mine);
+    PendingIndex base_cur{0, 0}, base_next{0, 0};
+    if constexpr (std::is_same_v<TableT, int16_t>) {
+        base_cur = issue_index(a.slot_base, cur.req != kNoRow ? cur.req : 0u, zero);
+        base_next = issue_index(a.slot_base, nxt.req != kNoRow ? nxt.req : 0u, zero);
+    }
+    const int64_t row_mine = lane_value(a.selected, entry_mine);
+    RunsMeta mine{row_mine >= 0 && row_mine < a.batch ? static_cast<uint32_t>(row_mine) : kNoRow, kNoRow, 0u, 0};
+    const PendingIndex req_mine = issue_index(a.rows, mine.row != kNoRow ? mine.row : 0u, zero);
+    const PendingIndex len_mine = issue_index(a.lengths, mine.row != kNoRow ? mine.row : 0u, zero);
     RunsPending pend;
     runs_begin<TableT>(a, layer, cur, first_loads, staged_bits[0], last_piece, live_piece, pend);
+    meta_apply(a, mine, lane_value(a.rows, req_mine), lane_value(a.lengths, len_mine));
+    if constexpr (std::is_same_v<TableT, int16_t>) {
+        const PendingIndex base_mine = issue_index(a.slot_base, mine.req != kNoRow ? mine.req : 0u, zero);
+        cur.base = cur.req != kNoRow ? static_cast<uint32_t>(index_value(a.slot_base, base_cur)) : 0u;
+        nxt.base = nxt.req != kNoRow ? static_cast<uint32_t>(index_value(a.slot_base, base_next)) : 0u;
+        mine.base = mine.req != kNoRow ? static_cast<uint32_t>(lane_value(a.slot_base, base_mine)) : 0u;
+    }
     if (threadIdx.x < n) {   // read from the second item on, after the next first stage's barrier
         meta[threadIdx.x] = uint4{mine.row, mine.req, mine.base, static_cast<uint32_t>(mine.bound)};
     }
@@ -1589,6 +1683,9 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
                      a.table_rows < (int64_t{1} << 31) && a.table_cols > 0 && count * layers < (int64_t{1} << 31)
                  ? 1
                  : 0;
+    if (check_only()) {
+        return 0;
+    }
     if (topk.dtype == EKV_INT64) {
         launch_table<int64_t>(a, table.dtype, map_dtype, compact, dense, grid, s);
     } else {

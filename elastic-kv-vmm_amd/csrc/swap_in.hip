@@ -919,15 +919,24 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
         throw std::invalid_argument("resident_counts need resident_bits");
     }
     const int64_t count = selected.shape[0];
+    if (L > 65535 || count > 0x7fffffff) {
+        throw std::invalid_argument("too many layers or rows for one launch");
+    }
+    if (count > 0 && L > 0 && W > 0) {
+        for (const auto* t : {&topk, &rows, &selected, &slots, &misses, &counts, &table, &slot_token, &stamps,
+                              &slot_base, &host_table, &promote_src, &promote_dst}) {
+            need_data(*t, "tensor");
+        }
+    }
+    if (check_only()) {
+        return 0;
+    }
     if (count == 0 || L == 0 || W == 0) {
         if (counter != nullptr) {
             advance_step_kernel<<<dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream)>>>(counter);
             check_hip(hipGetLastError(), "launch step advance");
         }
         return 0;
-    }
-    if (L > 65535 || count > 0x7fffffff) {
-        throw std::invalid_argument("too many layers or rows for one launch");
     }
     SwapArgs a{};
     a.topk = topk.data;
@@ -978,10 +987,6 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
     a.width = static_cast<uint32_t>(W);
     a.step = step;
     a.step_counter = counter;
-    for (const auto* t : {&topk, &rows, &selected, &slots, &misses, &counts, &table, &slot_token, &stamps,
-                          &slot_base, &host_table, &promote_src, &promote_dst}) {
-        need_data(*t, "tensor");
-    }
     a.hash_size = 2;
     a.hash_log2 = 1;
     while (a.hash_size < 2 * W) {

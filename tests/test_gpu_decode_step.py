@@ -194,3 +194,34 @@ def test_decode_step_replays_from_a_graph(gpu, host):
         for a, b in zip(eager.state(), graphed.state()):
             assert torch.equal(a, b), step
     del graph
+
+
+def test_a_stage_that_refuses_its_arguments_leaves_nothing_queued(gpu, host):
+    """The step checks all four stages before it launches any: a refusal by the swap-in or the
+    promote leaves the slots, the hot buffers, the pool and the output as they were."""
+    host_planes, host_table, _ = host
+    side = Side(gpu, host, torch.int16, 6, False, 5)
+    rows = torch.arange(R, device=gpu)
+    lengths = torch.full((R,), T, dtype=torch.int32, device=gpu)
+    rng = np.random.default_rng(11)
+    narrow_host = KVPlanes(base=host_planes.base, device=0, layers=L, kv=2, layer_stride=host_planes.layer_stride,
+                           kv_stride=host_planes.kv_stride, row_stride=ROW, row_bytes=ROW // 2, rows=host_planes.rows,
+                           owner=host_planes.owner)
+    wide = C + 8                                    # more lanes per row than a hot buffer holds
+    cases = [
+        (torch.tensor(rng.integers(0, T, (L, R, wide)), dtype=torch.int32, device=gpu), host_planes, "swap-in"),
+        (_topk(rng).to(gpu), narrow_host, "promote"),
+    ]
+    for topk, planes, stage in cases:
+        width = topk.shape[2]
+        before = side.state()
+        slots = torch.full((L, R, width), -9, dtype=torch.int32, device=gpu)
+        out = torch.full((R, L, 2, width, ROW), 0x5a, dtype=torch.uint8, device=gpu)
+        with pytest.raises(RuntimeError, match=stage):
+            decode_step(topk, rows, lengths, side.buffers, host_table, planes, side.planes, slots, out)
+        torch.cuda.synchronize()
+        assert bool((slots == -9).all()), stage
+        assert bool((out == 0x5a).all()), stage
+        for a, b in zip(before, side.state()):
+            assert torch.equal(a, b), stage
+        assert side.buffers.step == 0
