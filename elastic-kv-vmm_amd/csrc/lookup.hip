@@ -932,6 +932,11 @@ __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupAr
 // they had been a chain of six or more dependent round trips (one layer per
 // launch: 5.9 against 6.3 us).
 
+// Where the two-stage kernel's threads store slot pieces that no output row
+// takes (past a row's width, or of an item with no batch row): written by
+// every such store, read by nothing.
+__device__ i32x4 discarded_pieces[kThreads];
+
 // One item between its two stages: its table entries in flight and its lanes'
 // classification.
 struct RunsPending {
@@ -940,18 +945,22 @@ struct RunsPending {
     uint32_t invalid;   // bit j: lane j is padding or out of range (slot -1)
 };
 
-// First stage of an item: stage its summary row in `staged` (after a barrier
-// every thread passes), classify its lanes and issue its table reads.
+// An item's summary row into `staged` (its first stage's barrier publishes
+// it). Staged unconditionally: an item without a table row read summary row
+// 0 and no lane reads it (every lane is invalid); a store under the test let
+// the compiler move the summary row's load into the branch and wait there for
+// every load in flight.
+__device__ __forceinline__ void runs_stage(const RunsLoads<1>& loads, uint32_t* staged, uint32_t last_piece) {
+    *reinterpret_cast<i32x4*>(&staged[4 * (threadIdx.x < last_piece ? threadIdx.x : last_piece)]) = loads.bits[0];
+}
+
+// First stage of an item whose summary row runs_stage has written: after a
+// barrier every thread passes, classify its lanes and issue its table reads.
 template <typename TableT>
 __device__ __forceinline__ void runs_begin(const LookupArgs& a, uint32_t layer, const RunsMeta& m,
-                                           const RunsLoads<1>& loads, uint32_t* staged, uint32_t last_piece,
+                                           const RunsLoads<1>& loads, uint32_t* staged,
                                            const bool (&live_piece)[2], RunsPending& p) {
     const bool table_ok = m.row != kNoRow && m.req != kNoRow;   // uniform
-    // Staged unconditionally: an item without a table row read summary row 0
-    // and no lane reads it (every lane is invalid). A store under the test let
-    // the compiler move the summary row's load into the branch and wait there
-    // for every load in flight.
-    *reinterpret_cast<i32x4*>(&staged[4 * (threadIdx.x < last_piece ? threadIdx.x : last_piece)]) = loads.bits[0];
     __syncthreads();
     const int32_t block[kIters] = {loads.ids[0].x, loads.ids[0].y, loads.ids[0].z, loads.ids[0].w,
                                    loads.ids[1].x, loads.ids[1].y, loads.ids[1].z, loads.ids[1].w};
@@ -1167,7 +1176,8 @@ void resolve_runs_pipe2_kernel(const LookupArgs a, uint32_t items, uint32_t coun
     const PendingIndex req_mine = issue_index(a.rows, mine.row != kNoRow ? mine.row : 0u, zero);
     const PendingIndex len_mine = issue_index(a.lengths, mine.row != kNoRow ? mine.row : 0u, zero);
     RunsPending pend;
-    runs_begin<TableT>(a, layer, cur, first_loads, staged_bits[0], last_piece, live_piece, pend);
+    runs_stage(first_loads, staged_bits[0], last_piece);
+    runs_begin<TableT>(a, layer, cur, first_loads, staged_bits[0], live_piece, pend);
     meta_apply(a, mine, lane_value(a.rows, req_mine), lane_value(a.lengths, len_mine));
     if constexpr (std::is_same_v<TableT, int16_t>) {
         const PendingIndex base_mine = issue_index(a.slot_base, mine.req != kNoRow ? mine.req : 0u, zero);
@@ -1190,15 +1200,25 @@ void resolve_runs_pipe2_kernel(const LookupArgs a, uint32_t items, uint32_t coun
             }
             slot[j] = (pend.need >> j) & 1u ? value : ((pend.invalid >> j) & 1u ? -1 : 0);
         }
+        // The next item's summary row is staged before this item's slots are
+        // stored, so waiting for it does not wait for those stores too; with
+        // no next item the loads of the last iteration (one piece of row 0)
+        // go to the buffer no later item reads.
+        const bool more = k + 1 < n;   // uniform
+        runs_stage(next_loads, staged_bits[(k + 1) & 1], last_piece);
         const bool live = cur.row != kNoRow;   // uniform
-        if (live) {
-            int32_t* out = a.out + layer * a.out_sl + cur.row * a.out_sb;
+        {
+            // Two stores on every path: a piece past the row or of an item
+            // with no batch row goes to a scratch word block nobody reads. With
+            // conditional stores the compiler could not count the stores in
+            // flight and waited for all of them (their acknowledgements)
+            // before staging the next item's summary row.
+            int32_t* out = a.out + layer * a.out_sl + (live ? cur.row : 0u) * a.out_sb;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                if (live_piece[h]) {
-                    stream_store(i32x4{slot[4 * h], slot[4 * h + 1], slot[4 * h + 2], slot[4 * h + 3]},
-                                 reinterpret_cast<i32x4*>(element<true>(out, 1, first[h])));
-                }
+                i32x4* to = live && live_piece[h] ? reinterpret_cast<i32x4*>(element<true>(out, 1, first[h]))
+                                                  : &discarded_pieces[threadIdx.x];
+                stream_store(i32x4{slot[4 * h], slot[4 * h + 1], slot[4 * h + 2], slot[4 * h + 3]}, to);
             }
         }
         uint32_t miss = 0;  // bit j: lane j is a miss
@@ -1209,13 +1229,11 @@ void resolve_runs_pipe2_kernel(const LookupArgs a, uint32_t items, uint32_t coun
             }
         }
         // Stage one of item k + 1 and the loads of item k + 2, ahead of item k's compaction.
-        const bool more = k + 1 < n;   // uniform
         RunsMeta after = nxt;
         uint32_t layer_after = layer_next;
         RunsLoads<1> after_loads = next_loads;
         if (more) {
-            runs_begin<TableT>(a, layer_next, nxt, next_loads, staged_bits[(k + 1) & 1], last_piece, live_piece,
-                               pend);
+            runs_begin<TableT>(a, layer_next, nxt, next_loads, staged_bits[(k + 1) & 1], live_piece, pend);
             const uint32_t k_after = k + 2 < n ? k + 2 : k + 1;
             after = runs_meta(meta, k_after);
             layer_after = count_div.div(blockIdx.x + k_after * gridDim.x);
