@@ -193,12 +193,6 @@ __device__ __forceinline__ void locate(const EngineArgs& a, int64_t u, int64_t& 
     }
 }
 
-// The source of a gathered zero row's loads in a branch-free tile: its 16
-// bytes per lane are all zero, stay cached, and take no HBM traffic.
-// (Device global memory, not constant memory: a pointer that may point into
-// either is a flat address, whose loads also count as LDS operations.)
-__device__ __align__(16) uint32_t zero_block[4] = {0u, 0u, 0u, 0u};
-
 // Loads are plain (cached) and stores non-temporal: the copied rows are not
 // read again by this kernel, and streaming them past the caches keeps the
 // L2 for the row offsets and the source rows.
@@ -235,8 +229,6 @@ template <int M, int VW>
 __global__ __launch_bounds__(kThreads) void copy_small_rows(const EngineArgs a) {
     using V = typename Vec<VW>::type;
     constexpr bool kCheckAlign = (M == RowsIndirect) && VW > 1;
-    // Modes whose every row has a destination (the gathers).
-    constexpr bool kEveryRowWritten = is_gather_mode(M) || M == RowsDirect || M == RowsIndirect;
     __shared__ int64_t src_off[kThreads];
     __shared__ int64_t dst_off[kThreads];
     const int64_t grid_tiles = (a.xcd_groups == 0) ? a.tiles
@@ -257,60 +249,32 @@ __global__ __launch_bounds__(kThreads) void copy_small_rows(const EngineArgs a) 
         }
         __syncthreads();
         const uint32_t tile_vecs = rows_here * a.vecs_per_row;
-        if (kEveryRowWritten && tile_vecs == kThreads * kUnroll) {   // uniform
-            // A whole tile in one pass, with no per-lane branch: every lane
-            // loads (a zero row reads the zero block instead) and stores.
-            // Behind per-lane branches the compiler waited for every earlier
-            // load and store before each store, one acknowledgement after
-            // another.
-            int64_t s[kUnroll], d[kUnroll];
-#pragma unroll
-            for (int i = 0; i < kUnroll; ++i) {
-                const uint32_t idx = threadIdx.x + i * kThreads;
-                const uint32_t r = a.vec_div.div(idx);
-                const int64_t c = static_cast<int64_t>(idx - r * a.vecs_per_row) * VW;
-                s[i] = src_off[r];
-                d[i] = dst_off[r] + c;
-                s[i] = s[i] >= 0 ? s[i] + c : -1;
-            }
+        for (uint32_t base = threadIdx.x; base < tile_vecs; base += kThreads * kUnroll) {
             V v[kUnroll];
+            int64_t d[kUnroll];
 #pragma unroll
             for (int i = 0; i < kUnroll; ++i) {
-                const char* from = s[i] >= 0 ? a.src_base + s[i] : reinterpret_cast<const char*>(zero_block);
-                v[i] = load_vec<VW>(from, !kCheckAlign || (reinterpret_cast<uintptr_t>(from) % VW) == 0);
-            }
-#pragma unroll
-            for (int i = 0; i < kUnroll; ++i) {
-                store_vec<VW>(a.dst_base + d[i], v[i]);
-            }
-        } else {
-            for (uint32_t base = threadIdx.x; base < tile_vecs; base += kThreads * kUnroll) {
-                V v[kUnroll];
-                int64_t d[kUnroll];
-#pragma unroll
-                for (int i = 0; i < kUnroll; ++i) {
-                    const uint32_t idx = base + i * kThreads;
-                    d[i] = -1;
-                    v[i] = V{};
-                    if (idx < tile_vecs) {
-                        const uint32_t r = a.vec_div.div(idx);
-                        const uint32_t c = idx - r * a.vecs_per_row;
-                        const int64_t s = src_off[r];
-                        const int64_t t = dst_off[r];
-                        if (t >= 0) {
-                            d[i] = t + static_cast<int64_t>(c) * VW;
-                            if (s >= 0) {
-                                const bool aligned = !kCheckAlign || (s % VW) == 0;
-                                v[i] = load_vec<VW>(a.src_base + s + static_cast<int64_t>(c) * VW, aligned);
-                            }
+                const uint32_t idx = base + i * kThreads;
+                d[i] = -1;
+                v[i] = V{};
+                if (idx < tile_vecs) {
+                    const uint32_t r = a.vec_div.div(idx);
+                    const uint32_t c = idx - r * a.vecs_per_row;
+                    const int64_t s = src_off[r];
+                    const int64_t t = dst_off[r];
+                    if (t >= 0) {
+                        d[i] = t + static_cast<int64_t>(c) * VW;
+                        if (s >= 0) {
+                            const bool aligned = !kCheckAlign || (s % VW) == 0;
+                            v[i] = load_vec<VW>(a.src_base + s + static_cast<int64_t>(c) * VW, aligned);
                         }
                     }
                 }
+            }
 #pragma unroll
-                for (int i = 0; i < kUnroll; ++i) {
-                    if (d[i] >= 0) {
-                        store_vec<VW>(a.dst_base + d[i], v[i]);
-                    }
+            for (int i = 0; i < kUnroll; ++i) {
+                if (d[i] >= 0) {
+                    store_vec<VW>(a.dst_base + d[i], v[i]);
                 }
             }
         }
