@@ -535,9 +535,10 @@ def run_decode_read(torch, args, device):
     config = {"workload": "hisparse-topk-decode-read", "requests": R, "context": T, "layers": L, "kv_heads": 2,
               "head_dim": 128, "topk": K, "hot_capacity": C, "pool_bytes": layout.capacity_bytes,
               "chunk_bytes": layout.chunk_bytes}
-    # The committed counter summaries were taken at hot capacity 4096; other capacities move other bytes.
-    profiled = C == 4096
-    lookup_traffic = read_traffic("resolve_resident_hisparse_decode.md") if profiled else None
+    # Committed counter summaries exist for hot capacities 4096 and 8192; other capacities move other bytes.
+    suffix = {4096: "", 8192: "_capacity8192"}.get(C)
+    profiled = suffix is not None
+    lookup_traffic = read_traffic(f"resolve_resident_hisparse_decode{suffix}.md") if profiled else None
     extra = {"lookups_per_s": round(lanes / (phase["lookup"] / 1e3), 1),
              "lookup_us_per_step": round(phase["lookup"] * 1e3, 2),
              "lookup_us_per_layer": round(phase["lookup"] * 1e3 / L, 2),
@@ -556,7 +557,7 @@ def run_decode_read(torch, args, device):
              "event_spread": step_spread,
              "hit_rate": round(hits / lanes, 4), "pool_commit_s": round(commit_s, 3)}
     roof = roofline(achieved, "copy_small_rows<KvGather,16> (ekv_gather_kv)", gather_bytes, phase["gather"],
-                    read_traffic("gather_kv_hisparse_decode.md") if profiled else None)
+                    read_traffic(f"gather_kv_hisparse_decode{suffix}.md") if profiled else None)
     result = envelope(args, gather_bytes / (step_ms / 1e3) / 1e9, step_ms, config, roof, baseline, extra)
     del raw, output
     torch.cuda.synchronize()
