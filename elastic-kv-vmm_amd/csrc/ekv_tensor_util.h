@@ -108,6 +108,51 @@ struct IndexRef {
 #endif
 };
 
+#if defined(__HIPCC__)
+// Index reads for a kernel's prologue, as vector loads. The compiler makes a
+// workgroup-uniform read a scalar load, and it waits for every outstanding
+// scalar load before the first use of any of them, so a prologue's
+// independent index reads (and the kernel-argument reloads between them)
+// become a chain of memory round trips. Vector loads complete in issue order:
+// a batch of them is waited for once, and scalar waits do not wait for them.
+// An opaque per-lane zero in the address keeps them vector loads; index_value
+// reads a uniform value back as a scalar, lane_value a per-lane one.
+struct PendingIndex {
+    int32_t lo, hi;
+};
+
+__device__ __forceinline__ uint32_t opaque_zero() {
+    uint32_t zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+    return zero;
+}
+
+// Element i of `r`: its low word and, for int64 arrays, its high word (for
+// int32 arrays the element again); no branch on the element type.
+__device__ __forceinline__ PendingIndex issue_index(const IndexRef& r, int64_t i, uint32_t zero) {
+    const char* at = static_cast<const char*>(r.data) + i * r.stride * (r.is64 ? 8 : 4) + zero;
+    return PendingIndex{*reinterpret_cast<const int32_t*>(at), *reinterpret_cast<const int32_t*>(at + (r.is64 ? 4 : 0))};
+}
+
+__device__ __forceinline__ int64_t index_value(const IndexRef& r, const PendingIndex& p) {
+    // Both words are read back unconditionally: a read under the element-type
+    // test let the compiler move the high word's load into that branch and
+    // wait there for every load in flight.
+    const int32_t lo = __builtin_amdgcn_readfirstlane(p.lo);
+    const int32_t high = __builtin_amdgcn_readfirstlane(p.hi);
+    const int32_t hi = r.is64 ? high : (lo >> 31);
+    return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo));
+}
+
+// The same element read by a per-thread load (any value per lane).
+__device__ __forceinline__ int64_t lane_value(const IndexRef& r, const PendingIndex& p) {
+    const int32_t hi = r.is64 ? p.hi : (p.lo >> 31);
+    return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                                static_cast<uint32_t>(p.lo));
+}
+
+#endif
+
 inline IndexRef index_ref(const ekv_tensor& t, int dim) {
     IndexRef r;
     r.data = t.data;

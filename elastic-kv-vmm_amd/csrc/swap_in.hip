@@ -313,20 +313,48 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
     uint32_t* hash = touched + a.touched_words;
     int16_t* victims = reinterpret_cast<int16_t*>(hash);
     int16_t* owner = reinterpret_cast<int16_t*>(hash + a.hash_size / 2);
-    const int64_t b = a.selected[blockIdx.x];
-    if (b < 0 || b >= a.batch) {
-        return;
-    }
+    // The prologue's reads are vector loads issued together: as scalar loads
+    // (uniform reads) the compiler waited for each before the next one, and
+    // the selection entry, request row, miss count, step and slot base were a
+    // chain of round trips. The request row and miss count are read on the
+    // guess that the selection is the identity (entry j names batch row j:
+    // every batch row, the decode default); a different entry re-reads them
+    // for its row. The slot base is read beside batch 1, with whose results
+    // it is first needed.
+    const uint32_t zero = opaque_zero();
     const int64_t l = blockIdx.y;
-    const int64_t req = a.rows[b];
-    if (req < 0 || req >= a.table_rows) {
-        return;  // uniform: a row outside the tables has nothing resident
+    const int64_t guess = blockIdx.x < a.batch ? blockIdx.x : 0;
+    const PendingIndex entry_read = issue_index(a.selected, blockIdx.x, zero);
+    const PendingIndex req_read = issue_index(a.rows, guess, zero);
+    const int32_t counted_read = a.counts[l * a.ct_l + guess * a.ct_b + zero];
+    // The device step of a graph replay; without one, a word of the counts
+    // stands in and is not used.
+    const bool device_step = a.step_counter != nullptr;   // uniform
+    const int32_t* step_words = device_step ? reinterpret_cast<const int32_t*>(a.step_counter) : a.counts;
+    const int32_t step_lo = step_words[zero];
+    const int32_t step_hi = step_words[(device_step ? 1u : 0u) + zero];
+    // Every value is read back before the first early return, so the loads
+    // stay together (the compiler moves a load whose uses all lie past a
+    // return below it, where it waits for it alone).
+    const int64_t b = index_value(a.selected, entry_read);
+    int64_t req = index_value(a.rows, req_read);
+    int32_t counted = __builtin_amdgcn_readfirstlane(counted_read);
+    const int64_t step =
+        device_step ? static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(
+                                                __builtin_amdgcn_readfirstlane(step_hi))) << 32) |
+                                           static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(step_lo)))
+                    : a.step;   // uniform
+    const bool live = b >= 0 && b < a.batch;   // uniform
+    if (live && b != guess) {   // uniform: the selection is not the identity here
+        req = a.rows.fetch(b);
+        counted = a.counts[l * a.ct_l + b * a.ct_b];
+    }
+    if (!live || req < 0 || req >= a.table_rows) {
+        return;  // uniform: a stray selection, or a row outside the tables (nothing resident)
     }
     const int64_t C = a.capacity;
     const int64_t W = a.width;
-    const int32_t counted = a.counts[l * a.ct_l + b * a.ct_b];
-    const int64_t base = a.slot_base[req];
-    const int64_t step = a.step_counter != nullptr ? *a.step_counter : a.step;  // uniform
+    const PendingIndex base_read = issue_index(a.slot_base, req, zero);
     int32_t* promote_src = a.promote_src + l * a.ps_l + b * a.ps_b;
     int32_t* promote_dst = a.promote_dst + l * a.pd_l + b * a.pd_b;
     int32_t* slots = a.slots + l * a.sl_l + b * a.sl_b;
@@ -401,6 +429,7 @@ __global__ __launch_bounds__(kThreads) void swap_in_kernel(const SwapArgs a) {
             stamp[s] = held_stamp[k];
         }
     }
+    const int64_t base = index_value(a.slot_base, base_read);
     int32_t hit_local[kLaneRegs];   // local slot a lane hits, or -1
 #pragma unroll
     for (int k = 0; k < kLaneRegs; ++k) {
