@@ -19,8 +19,9 @@
   its 5 % chunk remap: every gathered K/V row equals its token's host row,
   the hot-buffer state stays a bijection between tokens and slots, every
   selected lane is resident in the slot it read, and the residency summary
-  equals a fresh build (size-independent checks; the oracle itself runs at
-  the reduced size above).
+  kept by the swap-ins equals a fresh build, per position and per 64
+  positions with its group counts (size-independent checks; the oracle
+  itself runs at the reduced size above).
 - The prefetching lookup with more items than 16 per resident workgroup, the
   launch shape where the host raises the grid above the resident count.
 """
@@ -33,7 +34,7 @@ from adaptive_sparse.host_arena import HostArena
 from adaptive_sparse.kv_pool import KVPlanes, PlanePoolLayout
 from adaptive_sparse.resident_lookup import build_residency_bits, resolve_resident
 from adaptive_sparse.sparse_read import gather_kv
-from adaptive_sparse.swap_in import INT32_MIN, HotBuffers, move_kv, swap_in
+from adaptive_sparse.swap_in import INT32_MIN, HotBuffers, move_kv, residency_counts, swap_in
 from elastic_kv.backing import Backing
 from oracle import oracle as ref
 
@@ -249,7 +250,10 @@ def _composite_topk_gpu(gen, L, R, K, lengths, window=4096):
     return torch.gather(pick, -1, order).to(torch.int32).contiguous()
 
 
-def test_config5_full_size_steps_keep_rows_and_lru_invariants(gpu):
+@pytest.mark.parametrize("shift", [0, 6])
+def test_config5_full_size_steps_keep_rows_and_lru_invariants(gpu, shift):
+    # shift 0: the per-position summary that the composite workload of bench.py runs; shift 6: the line summary
+    # with the group counts that the swap-in keeps.
     L, R, K, C, HOST_ROWS, row_bytes = 60, 128, 2048, 4096, 65536, 512
     gen = torch.Generator(device=gpu).manual_seed(505)
     rng = np.random.default_rng(505)
@@ -271,7 +275,7 @@ def test_config5_full_size_steps_keep_rows_and_lru_invariants(gpu):
                                owner=arena)
         host_table = ((torch.arange(R, device=gpu).view(R, 1) * T + torch.arange(T, device=gpu).view(1, T))
                       % HOST_ROWS).to(torch.int32)
-        buffers = HotBuffers(L, R, T, C, gpu, table_dtype=torch.int16)
+        buffers = HotBuffers(L, R, T, C, gpu, table_dtype=torch.int16, bits_shift=shift)
         recent = (lengths.view(1, R, 1) - C + torch.arange(C, device=gpu).view(1, 1, C)).expand(L, R, C)
         local = torch.rand((L, R, C), generator=gen, device=gpu).argsort(-1)
         buffers.install(recent, local)
@@ -288,7 +292,8 @@ def test_config5_full_size_steps_keep_rows_and_lru_invariants(gpu):
         chunk_rows = layout.chunk_bytes // row_bytes
         remap_count = round(0.05 * backing.chunk_count)
         torch.cuda.synchronize()
-        print(f"[config 5 full] ready: {backing.chunk_count} chunks, remap {remap_count} per step", flush=True)
+        print(f"[config 5 full, shift {shift}] ready: {backing.chunk_count} chunks, remap {remap_count} per step",
+              flush=True)
         for step in range(2):
             # remap: empty the chosen chunks' hot slots, unmap them and commit them again (zero-filled)
             chosen = rng.choice(np.arange(1, backing.chunk_count), size=remap_count, replace=False)
@@ -309,12 +314,14 @@ def test_config5_full_size_steps_keep_rows_and_lru_invariants(gpu):
             backing.ensure(chosen.tolist())
             topk = _composite_topk_gpu(gen, L, R, K, lengths)
             resolve_resident(topk, buffers.table, None, rows, lengths32, rows, slots, 1, misses=misses,
-                             miss_count=counts, resident_bits=buffers.bits, slot_base=buffers.slot_base)
+                             miss_count=counts, resident_bits=buffers.bits, bits_shift=buffers.bits_shift,
+                             slot_base=buffers.slot_base)
             swap_in(topk, 1, rows, rows, slots, misses, counts, buffers, host_table, src, dst, check=True)
             move_kv(host_planes, src, planes, dst, counts)
             gather_kv(planes, slots, output)
             torch.cuda.synchronize()
-            print(f"[config 5 full] step {step}: {int(counts.sum())} of {L * R * K} lanes promoted", flush=True)
+            print(f"[config 5 full, shift {shift}] step {step}: {int(counts.sum())} of {L * R * K} lanes promoted",
+                  flush=True)
             # every gathered row is its token's host row
             for layer_index in range(L):
                 host_rows = torch.gather(host_table, 1, topk[layer_index].long()).long()          # [R, K]
@@ -325,13 +332,15 @@ def test_config5_full_size_steps_keep_rows_and_lru_invariants(gpu):
             local_slot = slots.long() - buffers.slot_base.view(1, R, 1)
             assert bool(((local_slot >= 0) & (local_slot < C)).all()), step
             assert torch.equal(torch.gather(buffers.slot_token, 2, local_slot).long(), topk.long()), step
-            # the token <-> slot state is a bijection, and the summary is exact
+            # the token <-> slot state is a bijection, and the summary (and its group counts) are exact
             slot_token = buffers.slot_token.long()
             held = slot_token >= 0
             entry = torch.gather(buffers.table.long(), 2, slot_token.clamp_min(0))              # [L, R, C]
             assert torch.equal(entry[held], (torch.arange(C, device=gpu).expand(L, R, C) + 1)[held]), step
             assert int((buffers.table != 0).sum()) == int(held.sum()), step
-            assert torch.equal(buffers.bits, build_residency_bits(buffers.table)), step
+            assert torch.equal(buffers.bits, build_residency_bits(buffers.table, shift=shift)), step
+            if shift:
+                assert torch.equal(buffers.resident_counts, residency_counts(buffers.table, shift)), step
     finally:
         torch.cuda.synchronize()
         backing.close()
