@@ -960,7 +960,9 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
     if (check_only()) {
         return 0;
     }
-    if (count == 0 || L == 0 || W == 0) {
+    // An empty batch leaves every selection entry stray: nothing to do (the
+    // kernel's first reads assume batch row 0 exists).
+    if (count == 0 || L == 0 || W == 0 || B == 0) {
         if (counter != nullptr) {
             advance_step_kernel<<<dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream)>>>(counter);
             check_hip(hipGetLastError(), "launch step advance");

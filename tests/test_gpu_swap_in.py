@@ -186,6 +186,29 @@ def test_miss_entries_without_a_lane_record_empty_promotions(gpu):
     assert table[5] == dst[0] and table[7] == dst[3] and int((table != 0).sum()) == 2
 
 
+@pytest.mark.parametrize("counted", [False, True])
+def test_an_empty_batch_leaves_the_hot_buffers_alone(gpu, counted):
+    # topk [L, 0, K]: the selection's entries name batch rows that do not exist, so nothing is resident, evicted
+    # or promoted; the call is still one step.
+    L, R, T, C, K = 2, 3, 64, 8, 4
+    buffers = HotBuffers(L, R, T, C, gpu, step_counter=counted)
+    tokens = torch.arange(C, device=gpu).view(1, 1, C).expand(L, R, C)
+    buffers.install(tokens, torch.arange(C, device=gpu).flip(0).view(1, 1, C).expand(L, R, C))
+    before = [t.clone() for t in (buffers.table, buffers.bits, buffers.slot_token, buffers.stamps)]
+    empty = torch.zeros((L, 0, K), dtype=torch.int32, device=gpu)
+    selected = torch.tensor([0, 1], device=gpu)
+    host_table = torch.arange(R * T, dtype=torch.int32, device=gpu).reshape(R, T)
+    swap_in(empty, 1, torch.zeros(0, dtype=torch.int64, device=gpu), selected, empty.clone(), empty.clone(),
+            torch.zeros((L, 0), dtype=torch.int32, device=gpu), buffers, host_table, empty.clone(), empty.clone(),
+            check=True)
+    torch.cuda.synchronize()
+    for got, want in zip((buffers.table, buffers.bits, buffers.slot_token, buffers.stamps), before):
+        assert torch.equal(got, want)
+    assert buffers.step == 1
+    if counted:
+        assert int(buffers.step_counter.item()) == 1
+
+
 @pytest.mark.parametrize("bs", [2, 3])
 def test_paged_blocks_lookup_and_swap_in_match_oracle(gpu, bs):
     # Top-K over blocks of bs tokens, -1 padding and rows shorter than the
