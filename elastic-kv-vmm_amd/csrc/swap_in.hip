@@ -951,18 +951,22 @@ int swap_in(const ekv_tensor* topk_p, int64_t block_size, const ekv_tensor* rows
     if (L > 65535 || count > 0x7fffffff) {
         throw std::invalid_argument("too many layers or rows for one launch");
     }
-    if (count > 0 && L > 0 && W > 0) {
+    // An empty batch leaves every selection entry stray: nothing to launch
+    // (the kernel's first reads assume batch row 0 exists).
+    const bool launches = count > 0 && L > 0 && W > 0 && B > 0;
+    if (launches) {
         for (const auto* t : {&topk, &rows, &selected, &slots, &misses, &counts, &table, &slot_token, &stamps,
                               &slot_base, &host_table, &promote_src, &promote_dst}) {
             need_data(*t, "tensor");
+        }
+        if (T == 0) {
+            throw std::invalid_argument("the token table has no positions");   // host rows are read at position 0
         }
     }
     if (check_only()) {
         return 0;
     }
-    // An empty batch leaves every selection entry stray: nothing to do (the
-    // kernel's first reads assume batch row 0 exists).
-    if (count == 0 || L == 0 || W == 0 || B == 0) {
+    if (!launches) {
         if (counter != nullptr) {
             advance_step_kernel<<<dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream)>>>(counter);
             check_hip(hipGetLastError(), "launch step advance");

@@ -209,6 +209,22 @@ def test_an_empty_batch_leaves_the_hot_buffers_alone(gpu, counted):
         assert int(buffers.step_counter.item()) == 1
 
 
+def test_a_table_without_positions_is_refused(gpu):
+    # With no token positions no miss can be inserted, and the promotions' host rows are read at position 0:
+    # refused before anything is queued.
+    L, R, C, K = 1, 2, 8, 4
+    buffers = HotBuffers(L, R, 0, C, gpu)
+    topk = torch.zeros((L, R, K), dtype=torch.int32, device=gpu)
+    rows = torch.arange(R, device=gpu)
+    lists = [torch.full((L, R, K), -7, dtype=torch.int32, device=gpu) for _ in range(4)]
+    counts = torch.full((L, R), K, dtype=torch.int32, device=gpu)
+    with pytest.raises(RuntimeError, match="no positions"):
+        swap_in(topk, 1, rows, rows, lists[0], lists[1], counts, buffers,
+                torch.zeros((R, 0), dtype=torch.int32, device=gpu), lists[2], lists[3])
+    torch.cuda.synchronize()
+    assert all(bool((t == -7).all()) for t in lists)
+
+
 @pytest.mark.parametrize("bs", [2, 3])
 def test_paged_blocks_lookup_and_swap_in_match_oracle(gpu, bs):
     # Top-K over blocks of bs tokens, -1 padding and rows shorter than the
