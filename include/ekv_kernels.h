@@ -248,7 +248,9 @@ int ekv_scatter_kv(const ekv_planes* planes, const ekv_tensor* slots,
  * later miss entries share the first one's slot and get empty promotions.
  * Selected rows naming the same request are refused (status
  * EKV_SWAP_SHARED_REQUEST). Miss-list entries that name no valid lane get
- * promote_src = promote_dst = -1, which ekv_move_kv skips.
+ * promote_src = promote_dst = -1, which ekv_move_kv skips. An empty batch
+ * (B = 0) or selection launches nothing; a table without positions (T = 0)
+ * is refused when there is work.
  */
 int ekv_swap_in(const ekv_tensor* topk, int64_t block_size, const ekv_tensor* rows,
                 const ekv_tensor* selected, const ekv_tensor* slots,
