@@ -55,39 +55,20 @@ def resolve_resident(topk, table, mapping, rows, lengths, selected, output, bloc
         raise ValueError("an int16 table holds local slots and needs slot_base (and only it)")
     if slot_base is not None and mapping is not None:
         raise ValueError("slot_base needs the single-level form (mapping=None)")
-    tensors = [topk, table, rows, lengths, selected, output]
+    # The call is bound by its host launch cost: the launch helper describes the
+    # tensors in C++ (device checks, descriptors, torch's current stream) and
+    # calls the entry point by address.
+    helper, entries = _native.launch_helper()
     if slot_base is not None:
-        tensors.append(slot_base)
-    if resident_bits is not None:
-        tensors.append(resident_bits)
-    if mapping is not None:
-        tensors.append(mapping)
-    if misses is not None:
-        tensors += [misses, miss_count]
-    device = _native.device_of(*tensors)
-    lib = _native.kernel_library()
-    pack = _native.packed   # descriptors as bytes: this call is bound by its host launch cost
-    views = [pack(t, name) for t, name in (
-        (topk, "topk"), (table, "table"), (rows, "rows"), (lengths, "lengths"), (selected, "selected"),
-        (output, "output"))]
-    miss_view = pack(misses, "misses") if misses is not None else None
-    count_view = pack(miss_count, "miss_count") if miss_count is not None else None
-    bits_view = pack(resident_bits, "bits") if resident_bits is not None else None
-    with _native.on_device(device):
-        stream = _native.stream_handle(device)
-        if slot_base is not None:
-            status = lib.ekv_resolve_resident_local(
-                views[0], views[1], pack(slot_base, "slot_base"), bits_view, int(bits_shift), *views[2:],
-                miss_view, count_view, int(block_size), stream)
-        elif resident_bits is not None:
-            status = lib.ekv_resolve_resident_bits(
-                views[0], views[1], bits_view, int(bits_shift), *views[2:], miss_view, count_view,
-                int(block_size), stream)
-        else:
-            mapping_view = pack(mapping, "mapping") if mapping is not None else None
-            status = lib.ekv_resolve_resident(
-                views[0], views[1], mapping_view, *views[2:], miss_view, count_view, int(block_size), stream)
-    _native.check(lib, status, "resolve_resident")
+        form, entry = 2, entries["ekv_resolve_resident_local"]
+    elif resident_bits is not None:
+        form, entry = 1, entries["ekv_resolve_resident_bits"]
+    else:
+        form, entry = 0, entries["ekv_resolve_resident"]
+    status = helper.resolve(form, entry, topk, table, mapping, slot_base, resident_bits, int(bits_shift), rows,
+                            lengths, selected, output, misses, miss_count, int(block_size))
+    if status:
+        _native.check(_native.kernel_library(), status, "resolve_resident")
 
 
 def summary_words(context, shift=0):

@@ -1,0 +1,250 @@
+// Python-facing launch helpers for the two launch-bound entry points of the
+// library: the resident lookup (ekv_resolve_resident*) and the row gather
+// (ekv_gather_rows). Their GPU work is a few microseconds, so describing the
+// tensors for the C ABI from Python (attribute reads and struct packing,
+// about 1 us per tensor) set the call rate. Here the descriptors are read
+// straight from the tensors, the device and stream come from torch's current
+// HIP stream, and the entry point, passed in by address from the loaded
+// libelastic_vmm.so, is called with the GIL released. Validation of shapes and
+// types stays in the entry points; this file only builds descriptors, with the
+// same device and dtype errors as the ctypes path (elastic_kv/_native.py).
+#include <Python.h>
+
+#include <c10/hip/HIPFunctions.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/csrc/autograd/python_variable.h>
+
+#include "../../include/ekv_kernels.h"
+
+#include <set>
+#include <string>
+
+#ifndef EKV_SOURCE_HASH
+#define EKV_SOURCE_HASH unknown
+#endif
+#define EKV_STRINGIFY_(x) #x
+#define EKV_STRINGIFY(x) EKV_STRINGIFY_(x)
+
+namespace {
+
+int dtype_code(c10::ScalarType type) {
+    switch (type) {
+        case c10::ScalarType::Int: return EKV_INT32;
+        case c10::ScalarType::Long: return EKV_INT64;
+        case c10::ScalarType::Byte: return EKV_UINT8;
+        case c10::ScalarType::Char: return EKV_INT8;
+        case c10::ScalarType::Short: return EKV_INT16;
+        case c10::ScalarType::BFloat16: return EKV_BFLOAT16;
+        case c10::ScalarType::Half: return EKV_FLOAT16;
+        case c10::ScalarType::Float: return EKV_FLOAT32;
+        default: return 0;
+    }
+}
+
+// One optional tensor argument: its Python object, name and descriptor.
+struct Arg {
+    PyObject* object;
+    const char* name;
+    ekv_tensor view{};
+    const ekv_tensor* pointer() const { return object == Py_None ? nullptr : &view; }
+};
+
+// Fills every present argument's descriptor; returns the device index, or -1
+// with a Python exception set. The device checks run over all arguments
+// before any descriptor is built, as elastic_kv._native.device_of does.
+template <size_t N>
+int describe_all(Arg (&args)[N]) {
+    const at::Tensor* tensors[N] = {};
+    for (size_t i = 0; i < N; ++i) {
+        if (args[i].object == Py_None) {
+            continue;
+        }
+        if (!THPVariable_Check(args[i].object)) {
+            PyErr_Format(PyExc_TypeError, "%s must be a tensor", args[i].name);
+            return -1;
+        }
+        tensors[i] = &THPVariable_Unpack(args[i].object);
+    }
+    std::set<std::string> devices;
+    c10::Device device(c10::DeviceType::CPU);
+    for (size_t i = 0; i < N; ++i) {
+        if (tensors[i] != nullptr) {
+            device = tensors[i]->device();
+            devices.insert(device.str());
+        }
+    }
+    if (devices.size() != 1) {
+        std::string listed = "[";
+        for (const std::string& one : devices) {
+            listed += (listed.size() > 1 ? ", '" : "'") + one + "'";
+        }
+        PyErr_Format(PyExc_ValueError, "tensors must share one device, got %s]", listed.c_str());
+        return -1;
+    }
+    if (!device.is_cuda()) {
+        PyErr_SetString(PyExc_ValueError, "hot-path kernels need GPU tensors (no CPU fallback exists)");
+        return -1;
+    }
+    for (size_t i = 0; i < N; ++i) {
+        const at::Tensor* t = tensors[i];
+        if (t == nullptr) {
+            continue;
+        }
+        const int64_t ndim = t->dim();
+        if (ndim > 4) {
+            PyErr_Format(PyExc_ValueError, "%s has more than 4 dimensions", args[i].name);
+            return -1;
+        }
+        const int code = dtype_code(t->scalar_type());
+        if (code == 0) {
+            PyErr_Format(PyExc_TypeError, "%s has unsupported dtype %s", args[i].name,
+                         c10::toString(t->scalar_type()));
+            return -1;
+        }
+        ekv_tensor& view = args[i].view;
+        view.data = t->data_ptr();
+        view.dtype = code;
+        view.ndim = static_cast<int32_t>(ndim);
+        for (int64_t d = 0; d < ndim; ++d) {
+            view.shape[d] = t->size(d);
+            view.stride[d] = t->stride(d);
+        }
+    }
+    return device.has_index() ? device.index() : c10::hip::current_device();
+}
+
+// Makes `device` current for the call and restores the caller's device.
+class CurrentDevice {
+public:
+    explicit CurrentDevice(int device) : previous_(c10::hip::current_device()) {
+        if (previous_ != device) {
+            c10::hip::set_device(static_cast<c10::DeviceIndex>(device));
+        }
+        device_ = device;
+    }
+    ~CurrentDevice() {
+        if (previous_ != device_) {
+            c10::hip::set_device(previous_);
+        }
+    }
+
+private:
+    c10::DeviceIndex previous_;
+    int device_ = 0;
+};
+
+bool read_int(PyObject* object, const char* name, int64_t& value) {
+    value = PyLong_AsLongLong(object);
+    if (value == -1 && PyErr_Occurred()) {
+        PyErr_Format(PyExc_TypeError, "%s must be an int", name);
+        return false;
+    }
+    return true;
+}
+
+// resolve(form, entry, topk, table, mapping, slot_base, resident_bits,
+//         bits_shift, rows, lengths, selected, output, misses, miss_count,
+//         block_size) -> status of the entry point
+// form 0: ekv_resolve_resident (mapping may be None)
+// form 1: ekv_resolve_resident_bits
+// form 2: ekv_resolve_resident_local
+PyObject* resolve(PyObject*, PyObject* const* argv, Py_ssize_t argc) {
+    if (argc != 15) {
+        PyErr_SetString(PyExc_TypeError, "resolve takes 15 arguments");
+        return nullptr;
+    }
+    int64_t form = 0, entry = 0, bits_shift = 0, block_size = 0;
+    if (!read_int(argv[0], "form", form) || !read_int(argv[1], "entry", entry) ||
+        !read_int(argv[7], "bits_shift", bits_shift) || !read_int(argv[14], "block_size", block_size)) {
+        return nullptr;
+    }
+    Arg args[] = {{argv[2], "topk"},      {argv[3], "table"},       {argv[4], "mapping"},
+                  {argv[5], "slot_base"}, {argv[6], "bits"},        {argv[8], "rows"},
+                  {argv[9], "lengths"},   {argv[10], "selected"},   {argv[11], "output"},
+                  {argv[12], "misses"},   {argv[13], "miss_count"}};
+    try {
+        const int device = describe_all(args);
+        if (device < 0) {
+            return nullptr;
+        }
+        CurrentDevice current(device);
+        void* stream = c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(device)).stream();
+        const ekv_tensor* t[11];
+        for (int i = 0; i < 11; ++i) {
+            t[i] = args[i].pointer();
+        }
+        int status = 0;
+        Py_BEGIN_ALLOW_THREADS
+        if (form == 2) {
+            status = reinterpret_cast<decltype(&ekv_resolve_resident_local)>(entry)(
+                t[0], t[1], t[3], t[4], bits_shift, t[5], t[6], t[7], t[8], t[9], t[10], block_size, stream);
+        } else if (form == 1) {
+            status = reinterpret_cast<decltype(&ekv_resolve_resident_bits)>(entry)(
+                t[0], t[1], t[4], bits_shift, t[5], t[6], t[7], t[8], t[9], t[10], block_size, stream);
+        } else {
+            status = reinterpret_cast<decltype(&ekv_resolve_resident)>(entry)(
+                t[0], t[1], t[2], t[5], t[6], t[7], t[8], t[9], t[10], block_size, stream);
+        }
+        Py_END_ALLOW_THREADS
+        return PyLong_FromLong(status);
+    } catch (const std::exception& error) {
+        PyErr_SetString(PyExc_RuntimeError, error.what());
+        return nullptr;
+    }
+}
+
+// gather_rows(entry, raw, positions, request_ids, lengths, request_table,
+//             slot_offsets, output, request_stride, sink_elements, indirect)
+// -> status of ekv_gather_rows
+PyObject* gather_rows(PyObject*, PyObject* const* argv, Py_ssize_t argc) {
+    if (argc != 11) {
+        PyErr_SetString(PyExc_TypeError, "gather_rows takes 11 arguments");
+        return nullptr;
+    }
+    int64_t entry = 0, request_stride = 0, sink_elements = 0, indirect = 0;
+    if (!read_int(argv[0], "entry", entry) || !read_int(argv[8], "request_stride", request_stride) ||
+        !read_int(argv[9], "sink_elements", sink_elements) || !read_int(argv[10], "indirect", indirect)) {
+        return nullptr;
+    }
+    Arg args[] = {{argv[1], "raw"},           {argv[2], "positions"},    {argv[3], "request_ids"},
+                  {argv[4], "lengths"},       {argv[5], "request_table"}, {argv[6], "slot_offsets"},
+                  {argv[7], "output"}};
+    try {
+        const int device = describe_all(args);
+        if (device < 0) {
+            return nullptr;
+        }
+        CurrentDevice current(device);
+        void* stream = c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(device)).stream();
+        int status = 0;
+        Py_BEGIN_ALLOW_THREADS
+        status = reinterpret_cast<decltype(&ekv_gather_rows)>(entry)(
+            args[0].pointer(), args[1].pointer(), args[2].pointer(), args[3].pointer(), args[4].pointer(),
+            args[5].pointer(), args[6].pointer(), request_stride, sink_elements, indirect ? 1 : 0, stream);
+        Py_END_ALLOW_THREADS
+        return PyLong_FromLong(status);
+    } catch (const std::exception& error) {
+        PyErr_SetString(PyExc_RuntimeError, error.what());
+        return nullptr;
+    }
+}
+
+PyObject* abi_version(PyObject*, PyObject*) { return PyLong_FromLong(EKV_ABI_VERSION); }
+
+PyObject* source_hash(PyObject*, PyObject*) { return PyUnicode_FromString(EKV_STRINGIFY(EKV_SOURCE_HASH)); }
+
+PyMethodDef methods[] = {
+    {"resolve", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(resolve)), METH_FASTCALL,
+     "Describe the lookup's tensors and call an ekv_resolve_resident* entry point."},
+    {"gather_rows", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(gather_rows)), METH_FASTCALL,
+     "Describe the row gather's tensors and call ekv_gather_rows."},
+    {"abi_version", abi_version, METH_NOARGS, "EKV_ABI_VERSION this module was built against."},
+    {"source_hash", source_hash, METH_NOARGS, "Fingerprint of the native sources this module was built from."},
+    {nullptr, nullptr, 0, nullptr}};
+
+PyModuleDef module = {PyModuleDef_HEAD_INIT, "_ekv_launch", "Launch helpers for the launch-bound entry points.",
+                      -1, methods};
+
+}  // namespace
+
+PyMODINIT_FUNC PyInit__ekv_launch(void) { return PyModule_Create(&module); }

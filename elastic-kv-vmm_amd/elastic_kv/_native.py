@@ -1,13 +1,19 @@
 """ctypes binding of the ekv_* kernel entry points of libelastic_vmm.so.
 
 torch tensors are described to the C ABI as (pointer, dtype code, shape,
-element strides); nothing but plain values crosses the boundary. There is no
-fallback: if the library cannot be loaded, every kernel call raises.
+element strides); nothing but plain values crosses the boundary. The two
+launch-bound entry points (the lookup and the row gather) are called through
+a small compiled launch helper (launch_helper) that builds the same
+descriptors in C++. There is no fallback: if the library or the helper
+cannot be loaded, every kernel call raises.
 """
 
 import ctypes as ct
+import importlib.util
 import os
 import struct
+import sysconfig
+from pathlib import Path
 
 import torch
 
@@ -137,6 +143,46 @@ def kernel_library(library=None):
         lib._ekv_typed = True
     _TYPED[key] = lib
     return lib
+
+
+LAUNCHER_PATH = (Path(__file__).resolve().parents[1] / "lib"
+                 / ("_ekv_launch" + sysconfig.get_config_var("EXT_SUFFIX")))
+_LAUNCH = {}   # ELASTIC_VMM_LIBRARY key -> (launch helper module, {entry name: address})
+
+
+def launch_helper(library=None):
+    """(module, entry addresses) for the launch-bound entry points (cached like kernel_library).
+
+    The module (lib/_ekv_launch*.so, built from csrc/py_launch.cpp by
+    build_native.py) reads the tensors' descriptors in C++ and calls the
+    entry point of kernel_library(library) whose address it is given: the
+    lookup and the row gather take a few microseconds on the GPU, and
+    describing their tensors from Python took longer than that. It is
+    refused when missing or built from other sources, like the library.
+    """
+    key = library if library is not None else os.environ.get("ELASTIC_VMM_LIBRARY")
+    found = _LAUNCH.get(key)
+    if found is not None:
+        return found
+    lib = kernel_library(library)
+    if not LAUNCHER_PATH.exists():
+        raise RuntimeError(f"the launch helper {LAUNCHER_PATH.name} is missing; build it with "
+                           "`python elastic-kv-vmm_amd/build_native.py`")
+    spec = importlib.util.spec_from_file_location("_ekv_launch", LAUNCHER_PATH)
+    module = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(module)
+    if module.abi_version() != EKV_ABI_VERSION:
+        raise RuntimeError(f"{LAUNCHER_PATH.name} was built for kernel ABI {module.abi_version()}, "
+                           f"not {EKV_ABI_VERSION}; rebuild it")
+    tree = source_hash()
+    if tree is not None and module.source_hash() != tree:
+        raise RuntimeError(f"{LAUNCHER_PATH.name} was built from other sources (module {module.source_hash()}, "
+                           f"tree {tree}); rebuild it with `python elastic-kv-vmm_amd/build_native.py`")
+    entries = {name: ct.cast(getattr(lib, name), ct.c_void_p).value
+               for name in ("ekv_resolve_resident", "ekv_resolve_resident_bits", "ekv_resolve_resident_local",
+                            "ekv_gather_rows")}
+    found = _LAUNCH[key] = (module, entries)
+    return found
 
 
 def describe(tensor, name="tensor"):

@@ -1,8 +1,9 @@
 """Fingerprint of the native sources.
 
 build_native.py compiles it into libelastic_vmm.so (ekv_source_hash) and the
-loader compares it with the sources next to the library, so a library built
-from older sources is refused instead of running stale kernels.
+launch helper module (source_hash()), and the loader compares it with the
+sources next to them, so a build from older sources is refused instead of
+running stale kernels.
 """
 
 import hashlib
@@ -13,8 +14,8 @@ HEADER_DIR = PACKAGE_ROOT.parent / "include"
 
 
 def native_sources():
-    """The HIP sources and headers the library is built from, in a fixed order."""
-    sources = sorted(path for path in (PACKAGE_ROOT / "csrc").glob("*") if path.suffix in (".hip", ".h"))
+    """The HIP and C++ sources and headers the library and launch helper are built from, in a fixed order."""
+    sources = sorted(path for path in (PACKAGE_ROOT / "csrc").glob("*") if path.suffix in (".hip", ".cpp", ".h"))
     return sources + sorted(HEADER_DIR.glob("*.h"))
 
 

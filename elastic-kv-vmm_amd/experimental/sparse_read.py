@@ -5,8 +5,6 @@ Triton kernel): same arguments and checks; the rows are copied by the HIP
 row-copy engine of csrc/gather.hip.
 """
 
-import ctypes as ct
-
 from elastic_kv import _native
 
 
@@ -25,21 +23,12 @@ def gather_rows(raw, positions, request_ids, lengths, request_table, slot_offset
         raise ValueError("output shape does not match positions and row width")
     if not batch or not selected:
         return
-    tensors = [raw, positions, request_ids, lengths, output]
-    if indirect:
-        tensors += [request_table, slot_offsets]
-    device = _native.device_of(*tensors)
-    lib = _native.kernel_library()
-    views = [_native.describe(t, n) for t, n in (
-        (raw, "raw"), (positions, "positions"), (request_ids, "request_ids"),
-        (lengths, "lengths"))]
-    table_view = ct.byref(_native.describe(request_table, "request_table")) if indirect else None
-    offsets_view = ct.byref(_native.describe(slot_offsets, "slot_offsets")) if indirect else None
-    out_view = _native.describe(output, "output")
-    with _native.on_device(device):
-        status = lib.ekv_gather_rows(
-            ct.byref(views[0]), ct.byref(views[1]), ct.byref(views[2]), ct.byref(views[3]),
-            table_view, offsets_view, ct.byref(out_view),
-            layout.request_bytes // layout.itemsize, layout.chunk_bytes // layout.itemsize,
-            1 if indirect else 0, _native.stream_handle(device))
-    _native.check(lib, status, "gather_rows")
+    # Launch-bound (a few microseconds of GPU work): the launch helper describes
+    # the tensors in C++ and calls ekv_gather_rows by address.
+    helper, entries = _native.launch_helper()
+    status = helper.gather_rows(entries["ekv_gather_rows"], raw, positions, request_ids, lengths,
+                                request_table if indirect else None, slot_offsets if indirect else None, output,
+                                layout.request_bytes // layout.itemsize, layout.chunk_bytes // layout.itemsize,
+                                1 if indirect else 0)
+    if status:
+        _native.check(_native.kernel_library(), status, "gather_rows")

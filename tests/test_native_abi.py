@@ -221,3 +221,40 @@ def test_library_built_from_other_sources_is_refused(monkeypatch):
             _native.kernel_library()
     finally:
         backing._load_library.cache_clear()
+
+
+def test_launch_helper_loads_and_matches_the_library(lib):
+    import torch
+
+    from elastic_kv import _native
+    from elastic_kv._source_hash import source_hash
+
+    helper, entries = _native.launch_helper()
+    assert helper.abi_version() == _native.EKV_ABI_VERSION
+    assert helper.source_hash() == source_hash()
+    typed = _native.kernel_library()
+    for name, address in entries.items():
+        assert address == ct.cast(getattr(typed, name), ct.c_void_p).value, name
+    # Host tensors are refused before any HIP call, with the ctypes path's messages.
+    i32 = lambda *shape: torch.zeros(shape, dtype=torch.int32)  # noqa: E731
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        helper.resolve(0, entries["ekv_resolve_resident"], i32(1, 2, 4), i32(2, 8), None, None, None, 0,
+                       torch.arange(2), i32(2), torch.arange(2), i32(1, 2, 4), None, None, 1)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        helper.gather_rows(entries["ekv_gather_rows"], i32(64), i32(1, 2), i32(1), i32(1), None, None,
+                           i32(1, 2, 8), 8, 0, 0)
+    with pytest.raises(TypeError, match="rows must be a tensor"):
+        helper.resolve(0, entries["ekv_resolve_resident"], i32(1, 2, 4), i32(2, 8), None, None, None, 0,
+                       [0, 1], i32(2), torch.arange(2), i32(1, 2, 4), None, None, 1)
+    with pytest.raises(TypeError, match="resolve takes 15 arguments"):
+        helper.resolve(0)
+
+
+def test_launch_helper_built_from_other_sources_is_refused(monkeypatch):
+    from elastic_kv import _native
+
+    monkeypatch.setattr(_native, "source_hash", lambda: "0" * 32)
+    monkeypatch.setattr(_native, "_LAUNCH", {})
+    monkeypatch.setattr(_native, "kernel_library", lambda library=None: None)
+    with pytest.raises(RuntimeError, match="launch helper|built from other sources"):
+        _native.launch_helper()
