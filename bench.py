@@ -61,6 +61,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
 
 import argparse
+import dataclasses
 import json
 import os
 import platform
@@ -100,6 +101,9 @@ def parse_args():
                         help="VMM spare pool of the migration and composite pools (0: release at once)")
     parser.add_argument("--serial-remap", action="store_true",
                         help="composite: remap with the GPU idle before the step's kernels (no overlap)")
+    parser.add_argument("--remap-groups", type=int, default=2,
+                        help="composite: remap the chunks in this many groups, each followed by the promote of "
+                             "the items whose hot buffers it completes (1: promote after the whole remap)")
     parser.add_argument("--seed", type=int, default=2024)
     parser.add_argument("--cpu-seconds", type=float, default=8.0,
                         help="bound of each CPU baseline sample (per thread count)")
@@ -1301,21 +1305,24 @@ def run_composite(torch, args, device):
     fill = {"table": torch.zeros((), dtype=buffers.table.dtype, device=device),
             "slot_token": torch.full((), -1, dtype=torch.int32, device=device),
             "stamps": torch.full((), INT32_MIN, dtype=torch.int32, device=device),
-            "touched": torch.ones((), dtype=torch.bool, device=device)}
+            "zero_counts": torch.zeros_like(counts)}
 
-    def invalidate():
+    def invalidate(groups=1):
         """Choose `remap_count` random chunks (never chunk 0) and empty their hot slots (queued, no wait).
 
-        Returns the chunk ids and the [L, R] mask of the (layer, request) items whose slots they hold: a
-        2 MiB chunk of a plane is 4096 rows of 512 B, so it holds (most of) one request's hot buffer.
+        Returns the chunk ids, split in `groups` consecutive groups, and the [L, R] group of the (layer,
+        request) items whose slots they hold (the last group holding any of its slots; -1: none): a 2 MiB
+        chunk of a plane is 4096 rows of 512 B, so it holds (most of) one request's hot buffer.
         """
         chosen = rng.choice(np.arange(1, backing.chunk_count), size=remap_count, replace=False)
         ids = torch.tensor(chosen, device=device)
         plane, within = ids // layout.plane_chunks, ids % layout.plane_chunks
         slot = (within.view(-1, 1) * chunk_rows + torch.arange(chunk_rows, device=device).view(1, -1))
         layer = (plane // 2).view(-1, 1).expand_as(slot)
+        assignment = np.arange(len(chosen)) * groups // len(chosen)     # the group of each chosen chunk
+        group = torch.tensor(assignment, device=device).view(-1, 1).expand_as(slot)
         keep = (slot >= 1) & (slot < layout.rows)
-        slot, layer = slot[keep], layer[keep]
+        slot, layer, group = slot[keep], layer[keep], group[keep]
         req, loc = (slot - 1) // C, (slot - 1) % C
         token = buffers.slot_token[layer, req, loc].long()
         held = token >= 0
@@ -1323,9 +1330,9 @@ def run_composite(torch, args, device):
         buffers.slot_token[layer, req, loc] = fill["slot_token"]
         buffers.stamps[layer, req, loc] = fill["stamps"]
         build_residency_bits(buffers.table, out=buffers.bits)
-        touched = torch.zeros((L, R), dtype=torch.bool, device=device)
-        touched[layer, req] = fill["touched"]
-        return chosen.tolist(), touched
+        item_group = torch.full((L * R,), -1, dtype=torch.int64, device=device)
+        item_group.scatter_reduce_(0, layer * R + req, group, reduce="amax")
+        return [chosen[assignment == g].tolist() for g in range(groups)], item_group.view(L, R)
 
     def remap_chunks(chosen):
         r1 = time.perf_counter()
@@ -1338,7 +1345,7 @@ def run_composite(torch, args, device):
     def remap():
         """Unmap + remap the chosen chunks with the GPU idle (the form the graph replays below use)."""
         r0 = time.perf_counter()
-        chosen, _ = invalidate()
+        (chosen,), _ = invalidate()
         torch.cuda.synchronize()
         r1 = time.perf_counter()
         unmap_s, map_s = remap_chunks(chosen)
@@ -1363,54 +1370,73 @@ def run_composite(torch, args, device):
     phases = {name: [] for name in ("remap_ms", "lookup_ms", "swap_ms", "promote_ms", "gather_ms", "step_ms",
                                     "gpu_beside_remap_ms", "after_remap_ms")}
     promoted, verified = [], True
+
     def verify():
-        # every lane is resident after the step: its gathered rows must be its token's host rows
+        """Every lane is resident after the step: its gathered rows must be its token's host rows.
+
+        Checked in every layer on the GPU: the expected rows are gathered from the pinned host copy
+        (device-mapped) by the token's host row, ten layers at a time, and compared bit for bit.
+        """
+        host_rows = torch.gather(host_table.expand(L, R, T), 2, topk.long())               # [L, R, K]
         ok = True
-        for layer in (0, L - 1):
-            host_rows = torch.gather(host_table, 1, topk[layer].long()).long()        # [R, K]
-            for kv in range(2):
-                base = (layer * 2 + kv) * host_plane
-                expect = arena.host.narrow(0, base, host_plane).view(HOST_ROWS, row_bytes)[host_rows.cpu()]
-                got = output[:, layer, kv].contiguous().view(torch.uint8).view(R, K, row_bytes).cpu()
-                ok &= bool(torch.equal(got, expect))
+        for first in range(0, L, 10):
+            last = min(L, first + 10)
+            part = dataclasses.replace(host_planes, base=host_planes.base + first * host_planes.layer_stride,
+                                       layers=L - first)
+            expect = torch.empty((R, last - first, 2, K, 256), dtype=torch.bfloat16, device=device)
+            gather_kv(part, host_rows[first:last].contiguous(), expect, zero_below=0)
+            ok &= bool(torch.equal(output[:, first:last].view(torch.int16), expect.view(torch.int16)))
         return ok
 
     # The step runs on a non-blocking stream. A HIP VMM unmap waits for the work queued on the legacy null
     # stream but not for other streams' (measured: 50 unmaps took 55.6 ms behind a 42 ms kernel on the null
     # stream, 12.4 ms behind one on a side stream, 13.2 ms idle), so the remap's driver calls run on the
-    # host while the kernels that never touch the remapped chunks run on the GPU:
+    # host while kernels that never touch the chunks being remapped run on the GPU:
     #   queue: invalidate the chosen chunks' slots -> lookup -> swap-in -> promote of the items whose
     #          hot buffers the chunks do not hold
-    #   host:  unmap (+ release) and re-commit (map + zero fill, waited for) the chosen chunks
-    #   queue: promote of the items whose hot buffers they hold (into the fresh chunks) -> gather
+    #   host:  per group of the chosen chunks, unmap (+ release) and re-commit (map + zero fill, waited
+    #          for) them, then queue the promote of the items whose hot buffers that group completes (into
+    #          the fresh chunks): an item's group is the last one holding any of its slots, so no queued
+    #          promote touches a chunk of a later group, and those promotes run while the later groups'
+    #          driver calls do
+    #   queue: gather
     # The chunks' last readers are the previous step's kernels, which the step boundary has drained.
+    groups = 1 if args.serial_remap else max(1, args.remap_groups)
     stream = torch.cuda.Stream(device)
     torch.cuda.set_stream(stream)
-    counts_beside = torch.empty_like(counts)
-    counts_after = torch.empty_like(counts)
+    counts_part = torch.empty_like(counts)      # rewritten and read in stream order
+    no_items = torch.full((L, R), -1, dtype=torch.int64, device=device)
     step_remap = {"queue_ms": [], "unmap_ms": [], "map_ms": []}
     for step in range(args.warmup + args.steps):
         topk.copy_(composite_topk(torch, device, L, R, K, lengths, gen))
         torch.cuda.synchronize()
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(7)]
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(6)]
         t0 = time.perf_counter()
-        chosen, touched = invalidate() if remap_count else ([], torch.zeros((L, R), dtype=torch.bool, device=device))
+        chunk_groups, item_group = invalidate(groups) if remap_count else ([[]] * groups, no_items)
         ev[0].record()
         lookup()
         ev[1].record()
         swap()
         ev[2].record()
-        torch.where(touched, torch.zeros_like(counts), counts, out=counts_beside)
-        torch.where(touched, counts, torch.zeros_like(counts), out=counts_after)
-        move_kv(host_planes, promote_src, planes, promote_dst, counts_beside)
+        torch.where(item_group < 0, counts, fill["zero_counts"], out=counts_part)
+        move_kv(host_planes, promote_src, planes, promote_dst, counts_part)
         ev[3].record()
         if args.serial_remap:
             torch.cuda.synchronize()            # the comparison form: the driver calls with the GPU idle
         t1 = time.perf_counter()
-        unmap_s, map_s = remap_chunks(chosen) if chosen else (0.0, 0.0)
+        unmap_s = map_s = 0.0
+        group_events = []
+        for group, chunks in enumerate(chunk_groups):
+            if chunks:
+                unmap_g, map_g = remap_chunks(chunks)
+                unmap_s, map_s = unmap_s + unmap_g, map_s + map_g
+            pair = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            pair[0].record()
+            torch.where(item_group == group, counts, fill["zero_counts"], out=counts_part)
+            move_kv(host_planes, promote_src, planes, promote_dst, counts_part)
+            pair[1].record()
+            group_events.append(pair)
         t2 = time.perf_counter()
-        ev[6].record()                          # the stream restarts here (it may have gone idle meanwhile)
-        move_kv(host_planes, promote_src, planes, promote_dst, counts_after)
         ev[4].record()
         gather()
         ev[5].record()
@@ -1426,7 +1452,7 @@ def run_composite(torch, args, device):
             step_remap["map_ms"].append(map_s * 1e3)
             phases["lookup_ms"].append(ev[0].elapsed_time(ev[1]))
             phases["swap_ms"].append(ev[1].elapsed_time(ev[2]))
-            phases["promote_ms"].append(ev[2].elapsed_time(ev[3]) + ev[6].elapsed_time(ev[4]))
+            phases["promote_ms"].append(ev[2].elapsed_time(ev[3]) + sum(a.elapsed_time(b) for a, b in group_events))
             phases["gather_ms"].append(ev[4].elapsed_time(ev[5]))
             phases["gpu_beside_remap_ms"].append(ev[0].elapsed_time(ev[3]))
             phases["after_remap_ms"].append((t3 - t2) * 1e3)
@@ -1487,8 +1513,10 @@ def run_composite(torch, args, device):
              "lookups_per_s": round(lanes / (mean["lookup_ms"] / 1e3), 1),
              "gpu_work_ms": round(serial_gpu, 3), "serial_remap": bool(args.serial_remap),
              "overlap": "the remap's unmap + map run on the host beside the lookup, swap-in and the promote of the "
-                        "items whose hot buffers the remapped chunks do not hold (a non-blocking stream); the other "
-                        "items' promote and the gather follow",
+                        "items whose hot buffers the remapped chunks do not hold (a non-blocking stream); the chunks "
+                        "are remapped in groups, each followed by the promote of the items it completes, which "
+                        "runs beside the later groups' driver calls; the gather follows",
+             "remap_groups": groups,
              "remap_parts_ms": {k: round(statistics.mean(v), 2) if v else 0.0 for k, v in step_remap.items()},
              "vmm_us_per_chunk": {
                  "unmap_and_release" if not args.spare_chunks else "unmap":
