@@ -124,7 +124,11 @@ public:
     }
     ~CurrentDevice() {
         if (previous_ != device_) {
-            c10::hip::set_device(previous_);
+            try {
+                c10::hip::set_device(previous_);
+            } catch (...) {
+                // A destructor must not throw; the launch's own status is what the caller needs.
+            }
         }
     }
 
