@@ -918,10 +918,13 @@ def run_hisparse_swap(torch, args, device):
     saved = tuple(t.clone() for t in live)
     marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
+    host_us = []   # host time of each call (it returns once queued: the per-layer launch cost of a serving loop)
     wall0 = time.perf_counter()
     marks[0].record()
     for i in range(args.steps):
+        h0 = time.perf_counter()
         call(args.warmup + i, live)
+        host_us.append((time.perf_counter() - h0) * 1e6)
         marks[i + 1].record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - wall0) * 1e3 / args.steps
@@ -983,7 +986,8 @@ def run_hisparse_swap(torch, args, device):
             "kernel": "hisparse_swap_kernel<16> (ekv_hisparse_swap_in)",
             "algorithmic_bytes_per_launch": round(statistics.mean(promoted)), "avg_launch_ms": round(mean_ms, 4)}
     extra = {"call_ms": spread(call_ms), "misses_per_call": round(statistics.mean(misses), 1),
-             "hit_rate": round(hit_rate, 4), "tokens_per_s": round(R * W / (mean_ms / 1e3), 1)}
+             "hit_rate": round(hit_rate, 4), "tokens_per_s": round(R * W / (mean_ms / 1e3), 1),
+             "host_us_per_call": round(statistics.median(host_us), 2)}
     result = envelope(args, achieved, wall_ms, config, roof, baseline, extra,
                       metric="HiSparse swap-in promoted GB/s (host rows copied per call / call time), 1 GPU")
     return result

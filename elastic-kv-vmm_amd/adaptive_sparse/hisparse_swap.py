@@ -72,30 +72,13 @@ def load_blocks_to_device_buffer_mha(top_k_blocks, device_buffer_tokens, host_ca
     [host rows, ...]; device_buffer_k/v: GPU tensors [device rows, ...]; both
     with rows of item_size_bytes. Updates the hot state in place; returns None.
     """
-    device_tensors = [top_k_blocks, device_buffer_tokens, host_cache_locs, device_buffer_locs, device_buffer_k,
-                      device_buffer_v, top_k_device_locs, req_pool_indices, seq_lens, lru_slots]
-    if num_real_reqs is not None:
-        device_tensors.append(num_real_reqs)
-    device = _native.device_of(*device_tensors)
-    host_row_bytes, host_stride, host_kv, host_rows = _row_layout(host_cache_k, host_cache_v, "host cache")
-    dev_row_bytes, dev_stride, dev_kv, dev_rows = _row_layout(device_buffer_k, device_buffer_v, "device buffer")
-    if not host_row_bytes == dev_row_bytes == int(item_size_bytes):
-        raise ValueError(f"rows hold {host_row_bytes} (host) and {dev_row_bytes} (device) bytes, "
-                         f"item_size_bytes is {item_size_bytes}")
-    host_base = host_device_pointer(host_cache_k)
-    host_v_base = host_device_pointer(host_cache_v)
-    host = _native.EkvPlanes(host_base, 1, 2, 0, host_v_base - host_base, host_stride, host_row_bytes, host_rows)
-    dev = _native.EkvPlanes(device_buffer_k.data_ptr(), 1, 2, 0, dev_kv, dev_stride, dev_row_bytes, dev_rows)
-    lib = _native.kernel_library()
-    names = ("top_k_blocks", "device_buffer_tokens", "host_cache_locs", "device_buffer_locs", "top_k_device_locs",
-             "req_pool_indices", "seq_lens", "lru_slots")
-    tensors = (top_k_blocks, device_buffer_tokens, host_cache_locs, device_buffer_locs, top_k_device_locs,
-               req_pool_indices, seq_lens, lru_slots)
-    views = [_native.describe(t, n) for t, n in zip(tensors, names)]
-    real = None if num_real_reqs is None else _native.describe(num_real_reqs, "num_real_reqs")
-    with _native.on_device(device):
-        status = lib.ekv_hisparse_swap_in(
-            *(ct.byref(v) for v in views[:4]), ct.byref(host), ct.byref(dev), *(ct.byref(v) for v in views[4:]),
-            int(hot_buffer_size), int(sparse_block_size), None if real is None else ct.byref(real),
-            _native.stream_handle(device))
-    _native.check(lib, status, "load_blocks_to_device_buffer_mha")
+    # Called once per layer and step: the launch helper runs these checks (those of _row_layout and
+    # host_device_pointer, in this order) and builds the descriptors in C++.
+    helper, entries = _native.launch_helper()
+    status = helper.hisparse(entries["ekv_hisparse_swap_in"], entries["ekv_host_device_pointer"], top_k_blocks,
+                             device_buffer_tokens, host_cache_locs, device_buffer_locs, host_cache_k, host_cache_v,
+                             device_buffer_k, device_buffer_v, top_k_device_locs, req_pool_indices, seq_lens,
+                             lru_slots, int(item_size_bytes), int(hot_buffer_size), int(sparse_block_size),
+                             num_real_reqs)
+    if status:
+        _native.check(_native.kernel_library(), status, "load_blocks_to_device_buffer_mha")

@@ -1,13 +1,15 @@
-// Python-facing launch helpers for the two launch-bound entry points of the
-// library: the resident lookup (ekv_resolve_resident*) and the row gather
-// (ekv_gather_rows). Their GPU work is a few microseconds, so describing the
-// tensors for the C ABI from Python (attribute reads and struct packing,
-// about 1 us per tensor) set the call rate. Here the descriptors are read
-// straight from the tensors, the device and stream come from torch's current
-// HIP stream, and the entry point, passed in by address from the loaded
-// libelastic_vmm.so, is called with the GIL released. Validation of shapes and
-// types stays in the entry points; this file only builds descriptors, with the
-// same device and dtype errors as the ctypes path (elastic_kv/_native.py).
+// Python-facing launch helpers for the launch-bound entry points of the
+// library: the resident lookup (ekv_resolve_resident*), the row gather
+// (ekv_gather_rows) and the per-layer SGLang-convention swap-in
+// (ekv_hisparse_swap_in). Their GPU work can be a few microseconds, so
+// describing the tensors for the C ABI from Python (attribute reads and
+// struct packing, about 1 us per tensor) set the call rate. Here the
+// descriptors are read straight from the tensors, the device and stream come
+// from torch's current HIP stream, and the entry point, passed in by address
+// from the loaded libelastic_vmm.so, is called with the GIL released.
+// Validation of shapes and types stays in the entry points; this file only
+// builds descriptors, with the same device and dtype errors as the ctypes
+// path (elastic_kv/_native.py).
 #include <Python.h>
 
 #include <c10/hip/HIPFunctions.h>
@@ -45,7 +47,9 @@ int dtype_code(c10::ScalarType type) {
 struct Arg {
     PyObject* object;
     const char* name;
+    bool described = true;   // false: only its device is checked (a K/V row buffer of any dtype)
     ekv_tensor view{};
+    const at::Tensor* tensor = nullptr;
     const ekv_tensor* pointer() const { return object == Py_None ? nullptr : &view; }
 };
 
@@ -63,7 +67,7 @@ int describe_all(Arg (&args)[N]) {
             PyErr_Format(PyExc_TypeError, "%s must be a tensor", args[i].name);
             return -1;
         }
-        tensors[i] = &THPVariable_Unpack(args[i].object);
+        tensors[i] = args[i].tensor = &THPVariable_Unpack(args[i].object);
     }
     std::set<std::string> devices;
     c10::Device device(c10::DeviceType::CPU);
@@ -87,7 +91,7 @@ int describe_all(Arg (&args)[N]) {
     }
     for (size_t i = 0; i < N; ++i) {
         const at::Tensor* t = tensors[i];
-        if (t == nullptr) {
+        if (t == nullptr || !args[i].described) {
             continue;
         }
         const int64_t ndim = t->dim();
@@ -233,6 +237,127 @@ PyObject* gather_rows(PyObject*, PyObject* const* argv, Py_ssize_t argc) {
     }
 }
 
+// Row layout of a K/V tensor pair (adaptive_sparse.hisparse_swap._row_layout):
+// row bytes, row stride and K -> V offset in bytes, rows. False with a Python
+// exception set.
+bool row_layout(const at::Tensor& first, const at::Tensor& second, const char* name, ekv_planes& planes) {
+    if (first.sizes() != second.sizes() || first.scalar_type() != second.scalar_type() ||
+        first.strides() != second.strides()) {
+        PyErr_Format(PyExc_ValueError, "%s K and V must share shape, dtype and strides", name);
+        return false;
+    }
+    if (first.dim() < 1 || first.size(0) == 0) {
+        PyErr_Format(PyExc_ValueError, "%s needs at least one row", name);
+        return false;
+    }
+    const int64_t item = static_cast<int64_t>(first.element_size());
+    int64_t expect = 1;
+    for (int64_t d = first.dim() - 1; d >= 1; --d) {
+        if (first.size(d) > 1 && first.stride(d) != expect) {
+            PyErr_Format(PyExc_ValueError, "%s rows must be contiguous", name);
+            return false;
+        }
+        expect *= first.size(d);
+    }
+    planes.layers = 1;
+    planes.kv = 2;
+    planes.layer_stride = 0;
+    planes.kv_stride = static_cast<int64_t>(reinterpret_cast<uintptr_t>(second.data_ptr()) -
+                                            reinterpret_cast<uintptr_t>(first.data_ptr()));
+    planes.row_stride = first.stride(0) * item;
+    planes.row_bytes = expect * item;
+    planes.rows = first.size(0);
+    return true;
+}
+
+// hisparse(entry, pointer_entry, top_k_blocks, device_buffer_tokens,
+//          host_cache_locs, device_buffer_locs, host_cache_k, host_cache_v,
+//          device_buffer_k, device_buffer_v, top_k_device_locs,
+//          req_pool_indices, seq_lens, lru_slots, item_size_bytes,
+//          hot_buffer_size, sparse_block_size, num_real_reqs)
+// -> status of ekv_hisparse_swap_in (or of ekv_host_device_pointer)
+// The checks and their order are those of
+// adaptive_sparse.hisparse_swap.load_blocks_to_device_buffer_mha.
+PyObject* hisparse(PyObject*, PyObject* const* argv, Py_ssize_t argc) {
+    if (argc != 18) {
+        PyErr_SetString(PyExc_TypeError, "hisparse takes 18 arguments");
+        return nullptr;
+    }
+    int64_t entry = 0, pointer_entry = 0, item_size = 0, hot = 0, block_size = 0;
+    if (!read_int(argv[0], "entry", entry) || !read_int(argv[1], "pointer_entry", pointer_entry) ||
+        !read_int(argv[14], "item_size_bytes", item_size) || !read_int(argv[15], "hot_buffer_size", hot) ||
+        !read_int(argv[16], "sparse_block_size", block_size)) {
+        return nullptr;
+    }
+    Arg args[] = {{argv[2], "top_k_blocks"},        {argv[3], "device_buffer_tokens"},
+                  {argv[4], "host_cache_locs"},     {argv[5], "device_buffer_locs"},
+                  {argv[10], "top_k_device_locs"},  {argv[11], "req_pool_indices"},
+                  {argv[12], "seq_lens"},           {argv[13], "lru_slots"},
+                  {argv[17], "num_real_reqs"},      {argv[8], "device_buffer_k", false},
+                  {argv[9], "device_buffer_v", false}};
+    if (argv[8] == Py_None || argv[9] == Py_None) {
+        PyErr_SetString(PyExc_TypeError, "device_buffer_k and device_buffer_v are required");
+        return nullptr;
+    }
+    for (PyObject* host : {argv[6], argv[7]}) {
+        if (!THPVariable_Check(host)) {
+            PyErr_SetString(PyExc_TypeError, "host_cache_k and host_cache_v must be tensors");
+            return nullptr;
+        }
+    }
+    try {
+        const int device = describe_all(args);
+        if (device < 0) {
+            return nullptr;
+        }
+        const at::Tensor& host_k = THPVariable_Unpack(argv[6]);
+        const at::Tensor& host_v = THPVariable_Unpack(argv[7]);
+        ekv_planes host{}, dev{};
+        if (!row_layout(host_k, host_v, "host cache", host) ||
+            !row_layout(*args[9].tensor, *args[10].tensor, "device buffer", dev)) {
+            return nullptr;
+        }
+        if (host.row_bytes != dev.row_bytes || host.row_bytes != item_size) {
+            PyErr_Format(PyExc_ValueError, "rows hold %lld (host) and %lld (device) bytes, item_size_bytes is %lld",
+                         static_cast<long long>(host.row_bytes), static_cast<long long>(dev.row_bytes),
+                         static_cast<long long>(item_size));
+            return nullptr;
+        }
+        for (const at::Tensor* t : {&host_k, &host_v}) {
+            if (!t->device().is_cpu() || !t->is_pinned()) {
+                PyErr_SetString(PyExc_ValueError, "the host cache must be pinned CPU memory (pin_memory)");
+                return nullptr;
+            }
+        }
+        const auto device_pointer = reinterpret_cast<decltype(&ekv_host_device_pointer)>(pointer_entry);
+        void* host_k_device = nullptr;
+        void* host_v_device = nullptr;
+        int status = device_pointer(host_k.data_ptr(), &host_k_device);
+        if (status == 0) {
+            status = device_pointer(host_v.data_ptr(), &host_v_device);
+        }
+        if (status != 0) {
+            return PyLong_FromLong(status);
+        }
+        host.base = host_k_device;
+        host.kv_stride = static_cast<int64_t>(reinterpret_cast<uintptr_t>(host_v_device) -
+                                              reinterpret_cast<uintptr_t>(host_k_device));
+        dev.base = args[9].tensor->data_ptr();
+        CurrentDevice current(device);
+        void* stream = c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(device)).stream();
+        Py_BEGIN_ALLOW_THREADS
+        status = reinterpret_cast<decltype(&ekv_hisparse_swap_in)>(entry)(
+            args[0].pointer(), args[1].pointer(), args[2].pointer(), args[3].pointer(), &host, &dev,
+            args[4].pointer(), args[5].pointer(), args[6].pointer(), args[7].pointer(), hot, block_size,
+            args[8].pointer(), stream);
+        Py_END_ALLOW_THREADS
+        return PyLong_FromLong(status);
+    } catch (const std::exception& error) {
+        PyErr_SetString(PyExc_RuntimeError, error.what());
+        return nullptr;
+    }
+}
+
 PyObject* abi_version(PyObject*, PyObject*) { return PyLong_FromLong(EKV_ABI_VERSION); }
 
 PyObject* source_hash(PyObject*, PyObject*) { return PyUnicode_FromString(EKV_STRINGIFY(EKV_SOURCE_HASH)); }
@@ -242,6 +367,8 @@ PyMethodDef methods[] = {
      "Describe the lookup's tensors and call an ekv_resolve_resident* entry point."},
     {"gather_rows", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(gather_rows)), METH_FASTCALL,
      "Describe the row gather's tensors and call ekv_gather_rows."},
+    {"hisparse", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(hisparse)), METH_FASTCALL,
+     "Check and describe the SGLang-convention swap-in's arguments and call ekv_hisparse_swap_in."},
     {"abi_version", abi_version, METH_NOARGS, "EKV_ABI_VERSION this module was built against."},
     {"source_hash", source_hash, METH_NOARGS, "Fingerprint of the native sources this module was built from."},
     {nullptr, nullptr, 0, nullptr}};

@@ -1,10 +1,10 @@
 """ctypes binding of the ekv_* kernel entry points of libelastic_vmm.so.
 
 torch tensors are described to the C ABI as (pointer, dtype code, shape,
-element strides); nothing but plain values crosses the boundary. The two
-launch-bound entry points (the lookup and the row gather) are called through
-a small compiled launch helper (launch_helper) that builds the same
-descriptors in C++. There is no fallback: if the library or the helper
+element strides); nothing but plain values crosses the boundary. The
+launch-bound entry points (the lookup, the row gather and the SGLang-convention
+swap-in) are called through a small compiled launch helper (launch_helper)
+that builds the same descriptors in C++. There is no fallback: if the library or the helper
 cannot be loaded, every kernel call raises.
 """
 
@@ -156,8 +156,9 @@ def launch_helper(library=None):
     The module (lib/_ekv_launch*.so, built from csrc/py_launch.cpp by
     build_native.py) reads the tensors' descriptors in C++ and calls the
     entry point of kernel_library(library) whose address it is given: the
-    lookup and the row gather take a few microseconds on the GPU, and
-    describing their tensors from Python took longer than that. It is
+    lookup, the row gather and the per-layer SGLang-convention swap-in can
+    take a few microseconds on the GPU, and describing their tensors from
+    Python took longer than that. It is
     refused when missing or built from other sources, like the library.
     """
     key = library if library is not None else os.environ.get("ELASTIC_VMM_LIBRARY")
@@ -180,7 +181,7 @@ def launch_helper(library=None):
                            f"tree {tree}); rebuild it with `python elastic-kv-vmm_amd/build_native.py`")
     entries = {name: ct.cast(getattr(lib, name), ct.c_void_p).value
                for name in ("ekv_resolve_resident", "ekv_resolve_resident_bits", "ekv_resolve_resident_local",
-                            "ekv_gather_rows")}
+                            "ekv_gather_rows", "ekv_hisparse_swap_in", "ekv_host_device_pointer")}
     found = _LAUNCH[key] = (module, entries)
     return found
 

@@ -151,3 +151,42 @@ def test_argument_errors_name_the_argument(gpu):
         resolve_resident(i32(1, 2, 4), i32(2, 8), None, rows.cpu(), i32(2), rows, i32(1, 2, 4), 1)
     with pytest.raises(RuntimeError, match="resolve_resident"):   # the entry point's own shape check
         resolve_resident(i32(1, 2, 4), i32(2, 8), None, rows, i32(2), rows, i32(1, 2, 5), 1)
+
+
+def test_hisparse_argument_errors_match_the_python_checks(gpu):
+    from adaptive_sparse.hisparse_swap import load_blocks_to_device_buffer_mha
+
+    H, W, ROWS, WIDTH = 8, 4, 16, 64
+    dev_k = torch.zeros((ROWS, WIDTH), dtype=torch.bfloat16, device=gpu)
+    host_k = torch.zeros((ROWS, WIDTH), dtype=torch.bfloat16).pin_memory()
+    args = dict(top_k_blocks=torch.zeros((1, W), dtype=torch.int32, device=gpu),
+                device_buffer_tokens=torch.full((1, H + 1), -1, dtype=torch.int32, device=gpu),
+                host_cache_locs=torch.zeros((1, ROWS), dtype=torch.int64, device=gpu),
+                device_buffer_locs=torch.arange(1, H + 2, device=gpu).view(1, -1),
+                host_cache_k=host_k, host_cache_v=torch.zeros_like(host_k).pin_memory(),
+                device_buffer_k=dev_k, device_buffer_v=torch.zeros_like(dev_k),
+                top_k_device_locs=torch.full((1, W), -7, dtype=torch.int32, device=gpu),
+                req_pool_indices=torch.zeros(1, dtype=torch.int64, device=gpu),
+                seq_lens=torch.ones(1, dtype=torch.int32, device=gpu),
+                lru_slots=torch.arange(H, dtype=torch.int16, device=gpu).view(1, -1),
+                item_size_bytes=WIDTH * 2, hot_buffer_size=H, sparse_block_size=1)
+    cases = [
+        (dict(host_cache_k=torch.zeros((ROWS, WIDTH), dtype=torch.bfloat16),
+              host_cache_v=torch.zeros((ROWS, WIDTH), dtype=torch.bfloat16)), ValueError, "pinned CPU memory"),
+        (dict(host_cache_v=torch.zeros((ROWS, WIDTH // 2), dtype=torch.bfloat16).pin_memory()), ValueError,
+         "host cache K and V must share shape"),
+        (dict(device_buffer_k=dev_k[:, ::2], device_buffer_v=torch.zeros_like(dev_k)[:, ::2]), ValueError,
+         "device buffer rows must be contiguous"),
+        (dict(item_size_bytes=WIDTH * 4), ValueError, "item_size_bytes is 256"),
+        (dict(seq_lens=torch.ones(1, dtype=torch.int32)), ValueError, "share one device"),
+        (dict(top_k_blocks=torch.zeros((1, W), dtype=torch.float64, device=gpu)), TypeError,
+         "top_k_blocks has unsupported dtype"),
+    ]
+    for change, error, message in cases:
+        with pytest.raises(error, match=message):
+            load_blocks_to_device_buffer_mha(**{**args, **change})
+    torch.cuda.synchronize()
+    assert bool((args["top_k_device_locs"] == -7).all())   # nothing ran
+    load_blocks_to_device_buffer_mha(**args)                 # and the unchanged arguments are accepted
+    torch.cuda.synchronize()
+    assert args["top_k_device_locs"][0, 0].item() == args["device_buffer_locs"][0, H].item()   # the newest token
