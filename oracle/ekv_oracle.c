@@ -1,9 +1,9 @@
 /*
  * ekv_oracle.c - CPU restatement of the sparse-KV residency hot path.
  *
- * TEST INFRASTRUCTURE ONLY. This file is the checker: tests/, the smoke entry
- * point and the bench's CPU-baseline leg call it to verify (and, for the
- * baseline, to time) the HIP kernels. No product code path may call it.
+ * TEST INFRASTRUCTURE ONLY: tests/, the smoke entry point and the bench's
+ * CPU-baseline leg call it to verify (and, for the baseline, to time) the
+ * HIP kernels. No product code path may call it.
  *
  * Plain scalar C, one element at a time, written to follow the reference's
  * semantics literally rather than to be fast. All index arrays are dense

@@ -1,7 +1,7 @@
 """CPU oracle of the sparse-KV residency hot path.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
-CPU-baseline leg of bench.py, as the checker of the HIP kernels. Product code
+CPU-baseline leg of bench.py, to verify the HIP kernels' results. Product code
 never imports it.
 
 Two independent restatements of the reference semantics live here:
