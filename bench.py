@@ -1001,7 +1001,7 @@ REFERENCE_LOOKUP_MICRO_US = {"triton_p50": {1: 30.54, 2: 30.00, 4: 30.08}, "torc
 
 
 def run_lookup_micro(torch, args, device):
-    """tests/bench_resident_lookup.py of the reference, on this build's resolve_resident.
+    """tests/bench_resident_lookup.py of the reference, on this library's resolve_resident.
 
     Per batch of 1, 2 and 4 requests: a two-level lookup (int64 table -> int64
     mapping) of 16 Top-K blocks of 128 tokens (2048 lanes per row) over
@@ -1117,7 +1117,7 @@ def reference_support_sets(length, selected, seed=137):
 
 
 def run_virtual_addressing(torch, args, device):
-    """scripts/bench_virtual_addressing.py of the reference, on this build's gather_rows.
+    """scripts/bench_virtual_addressing.py of the reference, on this library's gather_rows.
 
     4 requests x 65,536 positions of 256 bf16 (512 B rows) in a VMM arena, 2048 positions gathered per request
     from each of the three support sets, direct (layout arithmetic) and software-table (two dependent lookups)
@@ -1630,7 +1630,7 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: this path has no "
-              "cross-GPU step in this build (each GPU runs its own shard independently)", file=sys.stderr)
+              "cross-GPU step here (each GPU runs its own shard independently)", file=sys.stderr)
         return 2
     apply_profile_switch(os.environ, args.profile_ranges)
     import torch

@@ -12,7 +12,7 @@ mapping (0 = not resident), the host token rows of host-backed requests, and
 their hot buffers (device slots, the token each slot holds per layer, the LRU
 order, the reserved slot of the newest token). Demotion leaves a request in
 exactly the state ekv_hisparse_swap_in serves host-backed decode from, and
-promotion restores it from there. The byte movement is this build's own:
+promotion restores it from there. The byte movement is this library's own:
 ekv_move_kv copies scattered token rows of every plane between the pool and
 device-mapped pinned host memory in one launch per direction.
 """
@@ -112,7 +112,7 @@ class Transfer:
 
 
 class HiSparseCoordinator:
-    """The HiSparse state the migration transactions act on (SGLang's names, this build's pool).
+    """The HiSparse state the migration transactions act on (SGLang's names, this library's pool).
 
     pool: a PlanePagedPool (page_size token slots per page, slot 0 the sink);
     host: a HostKVCache; mover: the row copies (RowMover over both by

@@ -2,7 +2,7 @@
 
 Replaces the third-party host-copy kernels the reference migrates through
 (adaptive_sparse/migration.py:109-111 backup_from_device_all_layer and
-:232-237 load_to_device_per_layer) with this build's own path:
+:232-237 load_to_device_per_layer) with this library's own path:
 
   demote:  pool pages --pack (ekv_gather_kv)--> device staging
                       --hipMemcpyAsync D2H (side stream)--> pinned host

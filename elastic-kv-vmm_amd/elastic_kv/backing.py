@@ -18,7 +18,7 @@ How this module is organised:
   * teardown is a weakref finalizer over the _NativeObject, not the Backing,
     so an unreferenced Backing still releases its reservation.
 
-The reference's cross-process capacity broker is not part of this build:
+The reference's cross-process capacity broker is not part of this library:
 asking for it through the environment raises, and the broker queries answer
 "no broker".
 """
@@ -41,8 +41,8 @@ _INVALID = (1 << 64) - 1
 _PACKAGE_ROOT = Path(__file__).resolve().parents[1]
 DEFAULT_LIBRARY = _PACKAGE_ROOT / "lib" / "libelastic_vmm.so"
 BUILD_HINT = (
-    "Build it with `python elastic-kv-vmm_amd/build_native.py` (the elastic-kv-build-vmm "
-    "step of this build) or set ELASTIC_VMM_LIBRARY"
+    "Build it with `python elastic-kv-vmm_amd/build_native.py` (the counterpart of the reference's "
+    "elastic-kv-build-vmm) or set ELASTIC_VMM_LIBRARY"
 )
 _BROKER_VARIABLES = ("EKV_GLOBAL_BROKER_PATH", "EKV_GLOBAL_BROKER_MIB", "EKV_GLOBAL_BROKER_FAIR_MODE")
 
@@ -65,7 +65,7 @@ _QUERY_SYMBOLS = {
     "ev_granularity": ([ct.c_void_p], _U64),
     "ev_poisoned": ([ct.c_void_p], ct.c_int),
 }
-# The spare pool (this build's extension of the ABI); a library without it
+# The spare pool (this library's extension of the ABI); a library without it
 # serves Backings whose spare limit stays 0.
 _SPARE_SYMBOLS = {
     "ev_set_spare": ([ct.c_void_p, _U64], ct.c_int),
@@ -178,7 +178,7 @@ class Backing:
             raise ValueError("VMM backing requires a GPU device")
         asked = [name for name in _BROKER_VARIABLES if os.environ.get(name) not in (None, "", "0", "off")]
         if asked:
-            raise ValueError("the cross-process VMM capacity broker is not part of this build; unset "
+            raise ValueError("the cross-process VMM capacity broker is not part of this library; unset "
                              + ", ".join(asked))
         self.device = torch.cuda.current_device() if target.index is None else target.index
         self._native = _NativeObject(_load_library(library_path(library)), self.device, self.capacity_bytes,
@@ -355,7 +355,7 @@ class Backing:
         self._finalizer.detach()
         self._chunks.clear()
 
-    # ---------------------------------------------------------------- no broker in this build
+    # ---------------------------------------------------------------- no broker in this library
     # The reference's broker queries and claims (elastic_kv/backing.py); callers written
     # against them see a backing without a broker.
 

@@ -23,7 +23,7 @@
  *   block = topk[l, row, o / bs]; pos = block * bs + o % bs
  *   valid = block >= 0 && pos < lengths[row]
  *   out   = valid ? int32(mapping[table[rows[row], pos]]) : -1
- * Extensions of this build: layer dimension L (table / mapping optionally
+ * Extensions beyond the reference: layer dimension L (table / mapping optionally
  * per layer), mapping == NULL (single level), bounds-guarded lanes -> -1
  * (where the reference would read out of bounds), and the miss list: lanes
  * with valid && out == 0 in ascending order (== torch.nonzero row-major),

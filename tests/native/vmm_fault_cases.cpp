@@ -7,7 +7,7 @@
 //   :97-153  a failed batch rolls back the chunks it created, after the zero
 //            fills it started have finished; a rollback that fails poisons;
 //   :166-184 a decommit that fails part-way poisons;
-//   :186-215 close releases everything (this build keeps the object alive
+//   :186-215 close releases everything (this library keeps the object alive
 //            when that fails, so the close can be retried);
 //   :235-256 ids outside the reservation and NULL id arrays fail before any
 //            driver call; duplicates are ignored.

@@ -26,7 +26,7 @@ BLOCK, HOT, WIDTH = 128, 256, 128
 
 
 def smoke_check(planes, gpu):
-    """tests/smoke_minimax_swap.py:18-67 through this build's swap-in; returns the locations."""
+    """tests/smoke_minimax_swap.py:18-67 through this library's swap-in; returns the locations."""
     results = []
     for layer in range(2):
         device_k, device_v = planes[layer], planes[layer + 2]

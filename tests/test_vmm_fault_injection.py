@@ -10,7 +10,7 @@ Two builds with g++ (no GPU, no HIP):
   * the driver alone as a shared library, loaded by the Python Backing
     (library=...), so its rollback / poison handling runs over the real native
     code - the cases of the reference's tests/test_backing.py:205-265 without
-    the broker, which is not part of this build.
+    the broker, which is not part of this library.
 """
 
 import ctypes as ct
