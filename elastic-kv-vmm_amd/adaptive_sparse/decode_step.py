@@ -30,7 +30,8 @@ class StepArgs(ct.Structure):
     _fields_ = [
         ("topk", _P_TENSOR), ("block_size", ct.c_int64), ("rows", _P_TENSOR), ("lengths", _P_TENSOR),
         ("selected", _P_TENSOR), ("table", _P_TENSOR), ("resident_bits", _P_TENSOR), ("bits_shift", ct.c_int64),
-        ("resident_counts", _P_TENSOR), ("slot_base", _P_TENSOR), ("slot_token", _P_TENSOR), ("stamps", _P_TENSOR), ("step", ct.c_int64),
+        ("resident_counts", _P_TENSOR), ("slot_base", _P_TENSOR), ("slot_token", _P_TENSOR), ("stamps", _P_TENSOR),
+        ("step", ct.c_int64),
         ("step_counter", _P_TENSOR), ("status", _P_TENSOR), ("host_table", _P_TENSOR),
         ("host", ct.POINTER(_native.EkvPlanes)), ("pool", ct.POINTER(_native.EkvPlanes)), ("slots", _P_TENSOR),
         ("out", ct.POINTER(_native.EkvKvRows)),
@@ -99,17 +100,20 @@ def decode_step(topk, rows, lengths, buffers, host_table, host_planes, pool_plan
         if (buffers.step + 1) * STEP_STAMPS >= (1 << 31):
             buffers.rebase()
         step = buffers.step
-    needed = decode_step_workspace(L, B, width)
-    device = _native.device_of(topk, rows, lengths, selected, buffers.table, host_table, slots, output)
+    for planes in (host_planes, pool_planes):
+        if not isinstance(planes, KVPlanes):
+            raise TypeError("host_planes and pool_planes must be KVPlanes")
     if workspace is None:
-        workspace = torch.empty(needed, dtype=torch.uint8, device=device)
-    args, keep = step_args(topk, rows, lengths, selected, buffers, host_table, host_planes, pool_planes, slots,
-                           output, block_size, -1 if counted else step)
-    lib = _native.kernel_library()
-    with _native.on_device(device):
-        status = lib.ekv_decode_step(ct.addressof(args), ct.c_void_p(workspace.data_ptr()), workspace.numel(),
-                                     _native.stream_handle(device))
-    _native.check(lib, status, "decode_step")
-    del keep
+        workspace = torch.empty(decode_step_workspace(L, B, width), dtype=torch.uint8, device=topk.device)
+    # The launch helper checks the devices, builds the step's descriptors (those of step_args) in C++ and
+    # calls ekv_decode_step: at small shapes the step's GPU work is shorter than building them in Python.
+    helper, entries = _native.launch_helper()
+    status = helper.decode_step(
+        entries["ekv_decode_step"], topk, rows, lengths, selected, buffers.table, buffers.bits,
+        int(buffers.bits_shift), getattr(buffers, "resident_counts", None), buffers.slot_base, buffers.slot_token,
+        buffers.stamps, -1 if counted else int(step), buffers.step_counter if counted else None, buffers.status,
+        host_table, host_planes, pool_planes, slots, output, int(block_size), workspace)
+    if status:
+        _native.check(_native.kernel_library(), status, "decode_step")
     if not counted:
         buffers.step = step + 1

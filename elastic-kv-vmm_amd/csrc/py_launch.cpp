@@ -1,7 +1,8 @@
 // Python-facing launch helpers for the launch-bound entry points of the
 // library: the resident lookup (ekv_resolve_resident*), the row gather
-// (ekv_gather_rows) and the per-layer SGLang-convention swap-in
-// (ekv_hisparse_swap_in). Their GPU work can be a few microseconds, so
+// (ekv_gather_rows), the per-layer SGLang-convention swap-in
+// (ekv_hisparse_swap_in) and the one-call decode step (ekv_decode_step).
+// Their GPU work can be a few microseconds at small shapes, so
 // describing the tensors for the C ABI from Python (attribute reads and
 // struct packing, about 1 us per tensor) set the call rate. Here the
 // descriptors are read straight from the tensors, the device and stream come
@@ -358,6 +359,161 @@ PyObject* hisparse(PyObject*, PyObject* const* argv, Py_ssize_t argc) {
     }
 }
 
+// The fields of a KVPlanes object (adaptive_sparse.kv_pool.KVPlanes). False
+// with a Python exception set.
+bool read_planes(PyObject* object, ekv_planes& planes) {
+    static const char* const names[] = {"base", "layers", "kv", "layer_stride", "kv_stride", "row_stride",
+                                        "row_bytes", "rows"};
+    int64_t values[8];
+    for (int i = 0; i < 8; ++i) {
+        PyObject* value = PyObject_GetAttrString(object, names[i]);
+        if (value == nullptr) {
+            return false;
+        }
+        values[i] = PyLong_AsLongLong(value);
+        Py_DECREF(value);
+        if (values[i] == -1 && PyErr_Occurred()) {
+            return false;
+        }
+    }
+    planes.base = reinterpret_cast<void*>(static_cast<uintptr_t>(values[0]));
+    planes.layers = values[1];
+    planes.kv = values[2];
+    planes.layer_stride = values[3];
+    planes.kv_stride = values[4];
+    planes.row_stride = values[5];
+    planes.row_bytes = values[6];
+    planes.rows = values[7];
+    return true;
+}
+
+// The dense (B, L, KV, K, *row) rows of `tensor` for slots [L, B, K] of
+// `planes` (adaptive_sparse.sparse_read._dense_struct). False with a Python
+// exception set.
+bool dense_rows(const at::Tensor& tensor, const ekv_planes& planes, const at::Tensor& slots, const char* name,
+                ekv_kv_rows& rows) {
+    if (tensor.dim() < 4) {
+        PyErr_Format(PyExc_ValueError, "%s must be shaped (B, L, KV, K, ...)", name);
+        return false;
+    }
+    if (slots.dim() != 3) {
+        PyErr_SetString(PyExc_ValueError, "slots must be shaped [L, B, K]");
+        return false;
+    }
+    const int64_t expected[4] = {slots.size(1), slots.size(0), planes.kv, slots.size(2)};
+    for (int d = 0; d < 4; ++d) {
+        if (tensor.size(d) != expected[d]) {
+            PyErr_Format(PyExc_ValueError, "%s leading shape (%lld, %lld, %lld, %lld) != (%lld, %lld, %lld, %lld)",
+                         name, static_cast<long long>(tensor.size(0)), static_cast<long long>(tensor.size(1)),
+                         static_cast<long long>(tensor.size(2)), static_cast<long long>(tensor.size(3)),
+                         static_cast<long long>(expected[0]), static_cast<long long>(expected[1]),
+                         static_cast<long long>(expected[2]), static_cast<long long>(expected[3]));
+            return false;
+        }
+    }
+    const int64_t item = static_cast<int64_t>(tensor.element_size());
+    int64_t expect = 1;
+    for (int64_t d = tensor.dim() - 1; d >= 4; --d) {
+        expect *= tensor.size(d);
+    }
+    if (expect * item != planes.row_bytes) {
+        PyErr_Format(PyExc_ValueError, "%s rows hold %lld bytes, pool rows %lld", name,
+                     static_cast<long long>(expect * item), static_cast<long long>(planes.row_bytes));
+        return false;
+    }
+    expect = 1;
+    for (int64_t d = tensor.dim() - 1; d >= 4; --d) {
+        if (tensor.size(d) > 1 && tensor.stride(d) != expect) {
+            PyErr_Format(PyExc_ValueError, "%s rows must be contiguous", name);
+            return false;
+        }
+        expect *= tensor.size(d);
+    }
+    rows.data = tensor.data_ptr();
+    rows.layer_stride = tensor.stride(1) * item;
+    rows.batch_stride = tensor.stride(0) * item;
+    rows.kv_stride = tensor.stride(2) * item;
+    rows.lane_stride = tensor.stride(3) * item;
+    return true;
+}
+
+// decode_step(entry, topk, rows, lengths, selected, table, resident_bits,
+//             bits_shift, resident_counts, slot_base, slot_token, stamps,
+//             step, step_counter, status, host_table, host_planes,
+//             pool_planes, slots, output, block_size, workspace)
+// -> status of ekv_decode_step (the planes are KVPlanes objects; the
+// workspace is a device tensor of at least ekv_decode_step_workspace_bytes)
+PyObject* decode_step(PyObject*, PyObject* const* argv, Py_ssize_t argc) {
+    if (argc != 22) {
+        PyErr_SetString(PyExc_TypeError, "decode_step takes 22 arguments");
+        return nullptr;
+    }
+    int64_t entry = 0, bits_shift = 0, step = 0, block_size = 0;
+    if (!read_int(argv[0], "entry", entry) || !read_int(argv[7], "bits_shift", bits_shift) ||
+        !read_int(argv[12], "step", step) || !read_int(argv[20], "block_size", block_size)) {
+        return nullptr;
+    }
+    Arg args[] = {{argv[1], "topk"},         {argv[2], "rows"},           {argv[3], "lengths"},
+                  {argv[4], "selected"},     {argv[5], "table"},          {argv[6], "resident_bits"},
+                  {argv[8], "resident_counts"}, {argv[9], "slot_base"},   {argv[10], "slot_token"},
+                  {argv[11], "stamps"},      {argv[13], "step_counter"},  {argv[14], "status"},
+                  {argv[15], "host_table"},  {argv[18], "slots"},         {argv[19], "output", false},
+                  {argv[21], "workspace", false}};
+    for (const int required : {1, 2, 3, 4, 5, 9, 10, 11, 15, 18, 19, 21}) {
+        if (argv[required] == Py_None) {
+            PyErr_SetString(PyExc_TypeError, "decode_step: a required tensor is None");
+            return nullptr;
+        }
+    }
+    try {
+        const int device = describe_all(args);
+        if (device < 0) {
+            return nullptr;
+        }
+        ekv_planes host{}, pool{};
+        ekv_kv_rows out{};
+        if (!read_planes(argv[16], host) || !read_planes(argv[17], pool) ||
+            !dense_rows(*args[14].tensor, pool, *args[13].tensor, "output", out)) {
+            return nullptr;
+        }
+        const at::Tensor& workspace = *args[15].tensor;
+        ekv_step_args step_args{};
+        step_args.topk = args[0].pointer();
+        step_args.block_size = block_size;
+        step_args.rows = args[1].pointer();
+        step_args.lengths = args[2].pointer();
+        step_args.selected = args[3].pointer();
+        step_args.table = args[4].pointer();
+        step_args.resident_bits = args[5].pointer();
+        step_args.bits_shift = bits_shift;
+        step_args.resident_counts = args[6].pointer();
+        step_args.slot_base = args[7].pointer();
+        step_args.slot_token = args[8].pointer();
+        step_args.stamps = args[9].pointer();
+        step_args.step = step;
+        step_args.step_counter = args[10].pointer();
+        step_args.status = args[11].pointer();
+        step_args.host_table = args[12].pointer();
+        step_args.host = &host;
+        step_args.pool = &pool;
+        step_args.slots = args[13].pointer();
+        step_args.out = &out;
+        void* workspace_data = workspace.data_ptr();
+        const uint64_t workspace_bytes = static_cast<uint64_t>(workspace.numel()) * workspace.element_size();
+        CurrentDevice current(device);
+        void* stream = c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(device)).stream();
+        int status = 0;
+        Py_BEGIN_ALLOW_THREADS
+        status = reinterpret_cast<decltype(&ekv_decode_step)>(entry)(&step_args, workspace_data, workspace_bytes,
+                                                                     stream);
+        Py_END_ALLOW_THREADS
+        return PyLong_FromLong(status);
+    } catch (const std::exception& error) {
+        PyErr_SetString(PyExc_RuntimeError, error.what());
+        return nullptr;
+    }
+}
+
 PyObject* abi_version(PyObject*, PyObject*) { return PyLong_FromLong(EKV_ABI_VERSION); }
 
 PyObject* source_hash(PyObject*, PyObject*) { return PyUnicode_FromString(EKV_STRINGIFY(EKV_SOURCE_HASH)); }
@@ -369,6 +525,8 @@ PyMethodDef methods[] = {
      "Describe the row gather's tensors and call ekv_gather_rows."},
     {"hisparse", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(hisparse)), METH_FASTCALL,
      "Check and describe the SGLang-convention swap-in's arguments and call ekv_hisparse_swap_in."},
+    {"decode_step", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(decode_step)), METH_FASTCALL,
+     "Describe a decode step's tensors, planes and output rows and call ekv_decode_step."},
     {"abi_version", abi_version, METH_NOARGS, "EKV_ABI_VERSION this module was built against."},
     {"source_hash", source_hash, METH_NOARGS, "Fingerprint of the native sources this module was built from."},
     {nullptr, nullptr, 0, nullptr}};

@@ -2,10 +2,11 @@
 
 torch tensors are described to the C ABI as (pointer, dtype code, shape,
 element strides); nothing but plain values crosses the boundary. The
-launch-bound entry points (the lookup, the row gather and the SGLang-convention
-swap-in) are called through a small compiled launch helper (launch_helper)
-that builds the same descriptors in C++. There is no fallback: if the library or the helper
-cannot be loaded, every kernel call raises.
+launch-bound entry points (the lookup, the row gather, the SGLang-convention
+swap-in and the one-call decode step) are called through a small compiled
+launch helper (launch_helper) that builds the same descriptors in C++. There
+is no fallback: if the library or the helper cannot be loaded, every kernel
+call raises.
 """
 
 import ctypes as ct
@@ -148,6 +149,9 @@ def kernel_library(library=None):
 LAUNCHER_PATH = (Path(__file__).resolve().parents[1] / "lib"
                  / ("_ekv_launch" + sysconfig.get_config_var("EXT_SUFFIX")))
 _LAUNCH = {}   # ELASTIC_VMM_LIBRARY key -> (launch helper module, {entry name: address})
+# The entry points the launch helper calls (by address).
+_LAUNCH_ENTRIES = ("ekv_resolve_resident", "ekv_resolve_resident_bits", "ekv_resolve_resident_local",
+                   "ekv_gather_rows", "ekv_hisparse_swap_in", "ekv_host_device_pointer", "ekv_decode_step")
 
 
 def launch_helper(library=None):
@@ -156,9 +160,9 @@ def launch_helper(library=None):
     The module (lib/_ekv_launch*.so, built from csrc/py_launch.cpp by
     build_native.py) reads the tensors' descriptors in C++ and calls the
     entry point of kernel_library(library) whose address it is given: the
-    lookup, the row gather and the per-layer SGLang-convention swap-in can
-    take a few microseconds on the GPU, and describing their tensors from
-    Python took longer than that. It is
+    lookup, the row gather, the per-layer SGLang-convention swap-in and a
+    small decode step can take a few microseconds on the GPU, and describing
+    their tensors from Python took longer than that. It is
     refused when missing or built from other sources, like the library.
     """
     key = library if library is not None else os.environ.get("ELASTIC_VMM_LIBRARY")
@@ -179,9 +183,7 @@ def launch_helper(library=None):
     if tree is not None and module.source_hash() != tree:
         raise RuntimeError(f"{LAUNCHER_PATH.name} was built from other sources (module {module.source_hash()}, "
                            f"tree {tree}); rebuild it with `python elastic-kv-vmm_amd/build_native.py`")
-    entries = {name: ct.cast(getattr(lib, name), ct.c_void_p).value
-               for name in ("ekv_resolve_resident", "ekv_resolve_resident_bits", "ekv_resolve_resident_local",
-                            "ekv_gather_rows", "ekv_hisparse_swap_in", "ekv_host_device_pointer")}
+    entries = {name: ct.cast(getattr(lib, name), ct.c_void_p).value for name in _LAUNCH_ENTRIES}
     found = _LAUNCH[key] = (module, entries)
     return found
 

@@ -225,3 +225,32 @@ def test_a_stage_that_refuses_its_arguments_leaves_nothing_queued(gpu, host):
         for a, b in zip(before, side.state()):
             assert torch.equal(a, b), stage
         assert side.buffers.step == 0
+
+
+def test_argument_errors_name_the_argument(gpu, host):
+    """The launch helper's own checks of the step's planes and output rows (before the entry point's)."""
+    host_planes, host_table, _ = host
+    side = Side(gpu, host, torch.int16, 6, False, 6)
+    rows = torch.arange(R, device=gpu)
+    lengths = torch.full((R,), T, dtype=torch.int32, device=gpu)
+    topk = _topk(np.random.default_rng(12)).to(gpu)
+    slots = torch.full((L, R, K), -9, dtype=torch.int32, device=gpu)
+    out = torch.full((R, L, 2, K, ROW), 0x5a, dtype=torch.uint8, device=gpu)
+    cases = [
+        (dict(out=out[:, :, :1]), ValueError, r"output leading shape \(5, 3, 1, 256\) != \(5, 3, 2, 256\)"),
+        (dict(out=out[..., :ROW // 2]), ValueError, "output rows hold 32 bytes, pool rows 64"),
+        (dict(out=out[..., ::2]), ValueError, "output rows hold 32 bytes"),
+        (dict(out=torch.zeros((R, L, 2, K, 2 * ROW), dtype=torch.uint8, device=gpu)[..., ::2]), ValueError,
+         "output rows must be contiguous"),
+        (dict(host_planes=(host_planes,)), TypeError, "must be KVPlanes"),
+        (dict(lengths=lengths.cpu()), ValueError, "share one device"),
+    ]
+    for change, error, message in cases:
+        arguments = dict(topk=topk, rows=rows, lengths=lengths, buffers=side.buffers, host_table=host_table,
+                         host_planes=host_planes, pool_planes=side.planes, slots=slots, output=out)
+        arguments.update({("output" if k == "out" else k): v for k, v in change.items()})
+        with pytest.raises(error, match=message):
+            decode_step(**arguments)
+    torch.cuda.synchronize()
+    assert bool((slots == -9).all()) and bool((out == 0x5a).all())
+    assert side.buffers.step == 0
