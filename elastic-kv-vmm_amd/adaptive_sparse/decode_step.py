@@ -83,7 +83,8 @@ def decode_step(topk, rows, lengths, buffers, host_table, host_planes, pool_plan
     """Lookup -> swap-in -> promote -> gather for the selected rows of every layer of `topk`.
 
     topk [L, B, K]; rows, lengths [B]; selected [S]: batch rows in [0, B)
-    (default: every batch row, 0 .. B - 1);
+    (default: every batch row, 0 .. B - 1, built on each call: a serving
+    loop passes one it keeps);
     buffers: the HotBuffers of the pool; host_table [R, T] and host_planes:
     the pinned host copy (device-mapped); pool_planes: the hot pool; slots
     [L, B, K * block_size] int32 and output [B, L, KV, K * block_size, row]:
