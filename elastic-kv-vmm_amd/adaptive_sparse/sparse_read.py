@@ -7,7 +7,6 @@ resolve_resident - are read from the K and V planes of every layer in one
 launch. scatter_kv is the inverse, used to unpack migrated rows.
 """
 
-import ctypes as ct
 from math import prod
 
 from elastic_kv import _native
@@ -46,23 +45,22 @@ def _dense_struct(tensor, planes, slots, name):
 
 
 def _kv_call(entry, planes, slots, dense, zero_below, name):
+    if not isinstance(planes, KVPlanes):
+        raise TypeError("planes must be a KVPlanes")
     if slots.dim() != 3:
         raise ValueError("slots must be shaped [L, B, K]")
     if slots.shape[0] > planes.layers:
         raise ValueError("slots name more layers than the pool holds")
-    device = _native.device_of(slots, dense)
-    if device.index != planes.device:
-        raise ValueError("slots and pool live on different devices")
     if not slots.numel():
+        if _native.device_of(slots, dense).index != planes.device:
+            raise ValueError("slots and pool live on different devices")
         return
-    lib = _native.kernel_library()
-    plane_view = _planes_struct(planes)
-    slot_view = _native.describe(slots, "slots")
-    dense_view = _dense_struct(dense, planes, slots, name)
-    with _native.on_device(device):
-        status = getattr(lib, entry)(ct.byref(plane_view), ct.byref(slot_view), ct.byref(dense_view),
-                                     int(zero_below), _native.stream_handle(device))
-    _native.check(lib, status, entry)
+    # The launch helper checks the devices and the dense rows (those of _dense_struct) and builds the
+    # descriptors in C++.
+    helper, entries = _native.launch_helper()
+    status = helper.kv(entries[entry], planes, slots, dense, int(zero_below), name)
+    if status:
+        _native.check(_native.kernel_library(), status, entry)
 
 
 @profile_range("native/gather")

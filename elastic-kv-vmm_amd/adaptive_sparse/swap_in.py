@@ -13,15 +13,12 @@ repeated within a row (a Top-K block listed twice) is one access by its first
 lane: the replay's rule applied to the selection with later repeats dropped.
 """
 
-import ctypes as ct
-
 import torch
 
 from elastic_kv import _native
 
 from .kv_pool import KVPlanes
 from .profile_ranges import profile_range
-from .sparse_read import _planes_struct
 
 INT32_MIN = -(1 << 31)
 STEP_STAMPS = 8192        # EKV_SWAP_STEP_STAMPS: recency stamps per LRU step, whatever the row width
@@ -195,31 +192,14 @@ def swap_in(topk, block_size, rows, selected, slots, misses, miss_count, buffers
         if (buffers.step + 1) * STEP_STAMPS >= (1 << 31):
             buffers.rebase()
         step = buffers.step
-    tensors = [topk, rows, selected, slots, misses, miss_count, buffers.table, buffers.slot_token,
-               buffers.stamps, buffers.slot_base, host_table, promote_src, promote_dst]
-    if buffers.bits is not None:
-        tensors.append(buffers.bits)
-    if buffers.resident_counts is not None:
-        tensors.append(buffers.resident_counts)
-    device = _native.device_of(*tensors)
-    lib = _native.kernel_library()
-    views = [ct.byref(_native.describe(t, "swap_in tensor")) for t in tensors[:13]]
-    bits_view = ct.byref(_native.describe(buffers.bits, "bits")) if buffers.bits is not None else None
-    counts_view = (ct.byref(_native.describe(buffers.resident_counts, "resident_counts"))
-                   if buffers.resident_counts is not None else None)
-    status_view = ct.byref(_native.describe(buffers.status, "status"))
-    # topk | rows .. table | bits, shift, group counts | slot_token .. promote_dst
-    head, middle, tail = views[0], views[1:7], views[7:13]
-    shift = int(buffers.bits_shift)
-    with _native.on_device(device):
-        if counted:
-            counter = ct.byref(_native.describe(buffers.step_counter, "step_counter"))
-            status = lib.ekv_swap_in_counted(head, int(block_size), *middle, bits_view, shift, counts_view, *tail,
-                                             counter, status_view, _native.stream_handle(device))
-        else:
-            status = lib.ekv_swap_in(head, int(block_size), *middle, bits_view, shift, counts_view, *tail,
-                                     int(step), status_view, _native.stream_handle(device))
-    _native.check(lib, status, "swap_in")
+    helper, entries = _native.launch_helper()
+    status = helper.swap_in(
+        entries["ekv_swap_in_counted" if counted else "ekv_swap_in"], int(counted), topk, int(block_size), rows,
+        selected, slots, misses, miss_count, buffers.table, buffers.bits, int(buffers.bits_shift),
+        buffers.resident_counts, buffers.slot_token, buffers.stamps, buffers.slot_base, host_table, promote_src,
+        promote_dst, int(step), buffers.step_counter if counted else None, buffers.status)
+    if status:
+        _native.check(_native.kernel_library(), status, "swap_in")
     buffers.step = step + 1
     if check:
         buffers.check_status()
@@ -231,11 +211,7 @@ def move_kv(src_planes, src_rows, dst_planes, dst_rows, counts, *, zero_below=1)
     for planes in (src_planes, dst_planes):
         if not isinstance(planes, KVPlanes):
             raise TypeError("planes must be KVPlanes")
-    device = _native.device_of(src_rows, dst_rows, counts)
-    lib = _native.kernel_library()
-    src_view, dst_view = _planes_struct(src_planes), _planes_struct(dst_planes)
-    views = [_native.describe(t, n) for t, n in ((src_rows, "src_rows"), (dst_rows, "dst_rows"), (counts, "counts"))]
-    with _native.on_device(device):
-        status = lib.ekv_move_kv(ct.byref(src_view), ct.byref(views[0]), ct.byref(dst_view), ct.byref(views[1]),
-                                 ct.byref(views[2]), int(zero_below), _native.stream_handle(device))
-    _native.check(lib, status, "move_kv")
+    helper, entries = _native.launch_helper()
+    status = helper.move(entries["ekv_move_kv"], src_planes, src_rows, dst_planes, dst_rows, counts, int(zero_below))
+    if status:
+        _native.check(_native.kernel_library(), status, "move_kv")

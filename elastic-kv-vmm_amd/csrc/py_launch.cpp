@@ -1,8 +1,10 @@
-// Python-facing launch helpers for the launch-bound entry points of the
-// library: the resident lookup (ekv_resolve_resident*), the row gather
-// (ekv_gather_rows), the per-layer SGLang-convention swap-in
-// (ekv_hisparse_swap_in) and the one-call decode step (ekv_decode_step).
-// Their GPU work can be a few microseconds at small shapes, so
+// Python-facing launch helpers for the kernel entry points of the library:
+// the resident lookup (ekv_resolve_resident*), the row gather
+// (ekv_gather_rows), the plane gather / scatter / move (ekv_gather_kv,
+// ekv_scatter_kv, ekv_move_kv), the batch-token swap-in (ekv_swap_in*), the
+// per-layer SGLang-convention swap-in (ekv_hisparse_swap_in) and the one-call
+// decode step (ekv_decode_step). Their GPU work can be a few microseconds at
+// small shapes, so
 // describing the tensors for the C ABI from Python (attribute reads and
 // struct packing, about 1 us per tensor) set the call rate. Here the
 // descriptors are read straight from the tensors, the device and stream come
@@ -514,6 +516,161 @@ PyObject* decode_step(PyObject*, PyObject* const* argv, Py_ssize_t argc) {
     }
 }
 
+// kv(entry, planes, slots, dense, zero_below, dense_name)
+// -> status of ekv_gather_kv or ekv_scatter_kv (same signature): slots
+// [L, B, K] of `planes` (a KVPlanes object on the slots' device) and the
+// dense (B, L, KV, K, *row) rows `dense`.
+PyObject* kv(PyObject*, PyObject* const* argv, Py_ssize_t argc) {
+    if (argc != 6) {
+        PyErr_SetString(PyExc_TypeError, "kv takes 6 arguments");
+        return nullptr;
+    }
+    int64_t entry = 0, zero_below = 0;
+    if (!read_int(argv[0], "entry", entry) || !read_int(argv[4], "zero_below", zero_below)) {
+        return nullptr;
+    }
+    const char* name = PyUnicode_AsUTF8(argv[5]);
+    if (name == nullptr) {
+        return nullptr;
+    }
+    if (argv[2] == Py_None || argv[3] == Py_None) {
+        PyErr_SetString(PyExc_TypeError, "slots and the dense rows are required");
+        return nullptr;
+    }
+    Arg args[] = {{argv[2], "slots"}, {argv[3], name, false}};
+    try {
+        const int device = describe_all(args);
+        if (device < 0) {
+            return nullptr;
+        }
+        ekv_planes planes{};
+        if (!read_planes(argv[1], planes)) {
+            return nullptr;
+        }
+        PyObject* planes_device = PyObject_GetAttrString(argv[1], "device");
+        if (planes_device == nullptr) {
+            return nullptr;
+        }
+        const long long pool_device = PyLong_AsLongLong(planes_device);
+        Py_DECREF(planes_device);
+        if (pool_device == -1 && PyErr_Occurred()) {
+            return nullptr;
+        }
+        if (pool_device != device) {
+            PyErr_SetString(PyExc_ValueError, "slots and pool live on different devices");
+            return nullptr;
+        }
+        ekv_kv_rows rows{};
+        if (!dense_rows(*args[1].tensor, planes, *args[0].tensor, name, rows)) {
+            return nullptr;
+        }
+        CurrentDevice current(device);
+        void* stream = c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(device)).stream();
+        int status = 0;
+        Py_BEGIN_ALLOW_THREADS
+        status = reinterpret_cast<decltype(&ekv_gather_kv)>(entry)(&planes, args[0].pointer(), &rows, zero_below,
+                                                                   stream);
+        Py_END_ALLOW_THREADS
+        return PyLong_FromLong(status);
+    } catch (const std::exception& error) {
+        PyErr_SetString(PyExc_RuntimeError, error.what());
+        return nullptr;
+    }
+}
+
+// move(entry, src_planes, src_rows, dst_planes, dst_rows, counts, zero_below)
+// -> status of ekv_move_kv (the planes are KVPlanes objects).
+PyObject* move(PyObject*, PyObject* const* argv, Py_ssize_t argc) {
+    if (argc != 7) {
+        PyErr_SetString(PyExc_TypeError, "move takes 7 arguments");
+        return nullptr;
+    }
+    int64_t entry = 0, zero_below = 0;
+    if (!read_int(argv[0], "entry", entry) || !read_int(argv[6], "zero_below", zero_below)) {
+        return nullptr;
+    }
+    for (const int required : {2, 4, 5}) {
+        if (argv[required] == Py_None) {
+            PyErr_SetString(PyExc_TypeError, "move: the row lists and counts are required");
+            return nullptr;
+        }
+    }
+    Arg args[] = {{argv[2], "src_rows"}, {argv[4], "dst_rows"}, {argv[5], "counts"}};
+    try {
+        const int device = describe_all(args);
+        if (device < 0) {
+            return nullptr;
+        }
+        ekv_planes src{}, dst{};
+        if (!read_planes(argv[1], src) || !read_planes(argv[3], dst)) {
+            return nullptr;
+        }
+        CurrentDevice current(device);
+        void* stream = c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(device)).stream();
+        int status = 0;
+        Py_BEGIN_ALLOW_THREADS
+        status = reinterpret_cast<decltype(&ekv_move_kv)>(entry)(&src, args[0].pointer(), &dst, args[1].pointer(),
+                                                                 args[2].pointer(), zero_below, stream);
+        Py_END_ALLOW_THREADS
+        return PyLong_FromLong(status);
+    } catch (const std::exception& error) {
+        PyErr_SetString(PyExc_RuntimeError, error.what());
+        return nullptr;
+    }
+}
+
+// swap_in(entry, counted, topk, block_size, rows, selected, slots, misses,
+//         miss_count, table, resident_bits, bits_shift, resident_counts,
+//         slot_token, stamps, slot_base, host_table, promote_src,
+//         promote_dst, step, step_counter, status)
+// -> status of ekv_swap_in (counted = 0) or ekv_swap_in_counted (1)
+PyObject* swap_in(PyObject*, PyObject* const* argv, Py_ssize_t argc) {
+    if (argc != 22) {
+        PyErr_SetString(PyExc_TypeError, "swap_in takes 22 arguments");
+        return nullptr;
+    }
+    int64_t entry = 0, counted = 0, block_size = 0, bits_shift = 0, step = 0;
+    if (!read_int(argv[0], "entry", entry) || !read_int(argv[1], "counted", counted) ||
+        !read_int(argv[3], "block_size", block_size) || !read_int(argv[11], "bits_shift", bits_shift) ||
+        !read_int(argv[19], "step", step)) {
+        return nullptr;
+    }
+    Arg args[] = {{argv[2], "topk"},          {argv[4], "rows"},          {argv[5], "selected"},
+                  {argv[6], "slots"},         {argv[7], "misses"},        {argv[8], "miss_count"},
+                  {argv[9], "table"},         {argv[10], "resident_bits"}, {argv[12], "resident_counts"},
+                  {argv[13], "slot_token"},   {argv[14], "stamps"},       {argv[15], "slot_base"},
+                  {argv[16], "host_table"},   {argv[17], "promote_src"},  {argv[18], "promote_dst"},
+                  {argv[20], "step_counter"}, {argv[21], "status"}};
+    try {
+        const int device = describe_all(args);
+        if (device < 0) {
+            return nullptr;
+        }
+        const ekv_tensor* t[17];
+        for (int i = 0; i < 17; ++i) {
+            t[i] = args[i].pointer();
+        }
+        CurrentDevice current(device);
+        void* stream = c10::hip::getCurrentHIPStream(static_cast<c10::DeviceIndex>(device)).stream();
+        int status = 0;
+        Py_BEGIN_ALLOW_THREADS
+        if (counted) {
+            status = reinterpret_cast<decltype(&ekv_swap_in_counted)>(entry)(
+                t[0], block_size, t[1], t[2], t[3], t[4], t[5], t[6], t[7], bits_shift, t[8], t[9], t[10], t[11],
+                t[12], t[13], t[14], t[15], t[16], stream);
+        } else {
+            status = reinterpret_cast<decltype(&ekv_swap_in)>(entry)(
+                t[0], block_size, t[1], t[2], t[3], t[4], t[5], t[6], t[7], bits_shift, t[8], t[9], t[10], t[11],
+                t[12], t[13], t[14], step, t[16], stream);
+        }
+        Py_END_ALLOW_THREADS
+        return PyLong_FromLong(status);
+    } catch (const std::exception& error) {
+        PyErr_SetString(PyExc_RuntimeError, error.what());
+        return nullptr;
+    }
+}
+
 PyObject* abi_version(PyObject*, PyObject*) { return PyLong_FromLong(EKV_ABI_VERSION); }
 
 PyObject* source_hash(PyObject*, PyObject*) { return PyUnicode_FromString(EKV_STRINGIFY(EKV_SOURCE_HASH)); }
@@ -527,6 +684,12 @@ PyMethodDef methods[] = {
      "Check and describe the SGLang-convention swap-in's arguments and call ekv_hisparse_swap_in."},
     {"decode_step", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(decode_step)), METH_FASTCALL,
      "Describe a decode step's tensors, planes and output rows and call ekv_decode_step."},
+    {"kv", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(kv)), METH_FASTCALL,
+     "Describe a plane gather or scatter and call ekv_gather_kv / ekv_scatter_kv."},
+    {"move", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(move)), METH_FASTCALL,
+     "Describe a row move between two plane sets and call ekv_move_kv."},
+    {"swap_in", reinterpret_cast<PyCFunction>(reinterpret_cast<void (*)(void)>(swap_in)), METH_FASTCALL,
+     "Describe the batch-token LRU swap-in's tensors and call ekv_swap_in / ekv_swap_in_counted."},
     {"abi_version", abi_version, METH_NOARGS, "EKV_ABI_VERSION this module was built against."},
     {"source_hash", source_hash, METH_NOARGS, "Fingerprint of the native sources this module was built from."},
     {nullptr, nullptr, 0, nullptr}};

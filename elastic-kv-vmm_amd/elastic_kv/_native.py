@@ -151,7 +151,8 @@ LAUNCHER_PATH = (Path(__file__).resolve().parents[1] / "lib"
 _LAUNCH = {}   # ELASTIC_VMM_LIBRARY key -> (launch helper module, {entry name: address})
 # The entry points the launch helper calls (by address).
 _LAUNCH_ENTRIES = ("ekv_resolve_resident", "ekv_resolve_resident_bits", "ekv_resolve_resident_local",
-                   "ekv_gather_rows", "ekv_hisparse_swap_in", "ekv_host_device_pointer", "ekv_decode_step")
+                   "ekv_gather_rows", "ekv_gather_kv", "ekv_scatter_kv", "ekv_move_kv", "ekv_swap_in",
+                   "ekv_swap_in_counted", "ekv_hisparse_swap_in", "ekv_host_device_pointer", "ekv_decode_step")
 
 
 def launch_helper(library=None):
