@@ -114,7 +114,6 @@ def decode_step(topk, rows, lengths, buffers, host_table, host_planes, pool_plan
         int(buffers.bits_shift), getattr(buffers, "resident_counts", None), buffers.slot_base, buffers.slot_token,
         buffers.stamps, -1 if counted else int(step), buffers.step_counter if counted else None, buffers.status,
         host_table, host_planes, pool_planes, slots, output, int(block_size), workspace)
-    if status:
-        _native.check(_native.kernel_library(), status, "decode_step")
+    _native.launch_check(status, "decode_step")
     if not counted:
         buffers.step = step + 1

@@ -80,5 +80,4 @@ def load_blocks_to_device_buffer_mha(top_k_blocks, device_buffer_tokens, host_ca
                              device_buffer_k, device_buffer_v, top_k_device_locs, req_pool_indices, seq_lens,
                              lru_slots, int(item_size_bytes), int(hot_buffer_size), int(sparse_block_size),
                              num_real_reqs)
-    if status:
-        _native.check(_native.kernel_library(), status, "load_blocks_to_device_buffer_mha")
+    _native.launch_check(status, "load_blocks_to_device_buffer_mha")

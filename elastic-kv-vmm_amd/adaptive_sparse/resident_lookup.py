@@ -67,8 +67,7 @@ def resolve_resident(topk, table, mapping, rows, lengths, selected, output, bloc
         form, entry = 0, entries["ekv_resolve_resident"]
     status = helper.resolve(form, entry, topk, table, mapping, slot_base, resident_bits, int(bits_shift), rows,
                             lengths, selected, output, misses, miss_count, int(block_size))
-    if status:
-        _native.check(_native.kernel_library(), status, "resolve_resident")
+    _native.launch_check(status, "resolve_resident")
 
 
 def summary_words(context, shift=0):

@@ -59,8 +59,7 @@ def _kv_call(entry, planes, slots, dense, zero_below, name):
     # descriptors in C++.
     helper, entries = _native.launch_helper()
     status = helper.kv(entries[entry], planes, slots, dense, int(zero_below), name)
-    if status:
-        _native.check(_native.kernel_library(), status, entry)
+    _native.launch_check(status, entry)
 
 
 @profile_range("native/gather")

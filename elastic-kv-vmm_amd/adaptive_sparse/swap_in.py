@@ -198,8 +198,7 @@ def swap_in(topk, block_size, rows, selected, slots, misses, miss_count, buffers
         selected, slots, misses, miss_count, buffers.table, buffers.bits, int(buffers.bits_shift),
         buffers.resident_counts, buffers.slot_token, buffers.stamps, buffers.slot_base, host_table, promote_src,
         promote_dst, int(step), buffers.step_counter if counted else None, buffers.status)
-    if status:
-        _native.check(_native.kernel_library(), status, "swap_in")
+    _native.launch_check(status, "swap_in")
     buffers.step = step + 1
     if check:
         buffers.check_status()
@@ -213,5 +212,4 @@ def move_kv(src_planes, src_rows, dst_planes, dst_rows, counts, *, zero_below=1)
             raise TypeError("planes must be KVPlanes")
     helper, entries = _native.launch_helper()
     status = helper.move(entries["ekv_move_kv"], src_planes, src_rows, dst_planes, dst_rows, counts, int(zero_below))
-    if status:
-        _native.check(_native.kernel_library(), status, "move_kv")
+    _native.launch_check(status, "move_kv")

@@ -155,8 +155,17 @@ _LAUNCH_ENTRIES = ("ekv_resolve_resident", "ekv_resolve_resident_bits", "ekv_res
                    "ekv_swap_in_counted", "ekv_hisparse_swap_in", "ekv_host_device_pointer", "ekv_decode_step")
 
 
+_DEFAULT = object()   # _LAUNCH key of the helper bound on the first call without a library argument
+_BOUND = {}           # _LAUNCH key -> the typed library whose entry points that helper calls
+
+
 def launch_helper(library=None):
     """(module, entry addresses) for the launch-bound entry points (cached like kernel_library).
+
+    Without a library argument the first call binds the helper to the
+    library that ELASTIC_VMM_LIBRARY (or the in-tree default) names then, and
+    later calls reuse it without reading the environment again: reading it
+    cost about a microsecond, a sixth of a small lookup's launch.
 
     The module (lib/_ekv_launch*.so, built from csrc/py_launch.cpp by
     build_native.py) reads the tensors' descriptors in C++ and calls the
@@ -166,9 +175,15 @@ def launch_helper(library=None):
     their tensors from Python took longer than that. It is
     refused when missing or built from other sources, like the library.
     """
+    if library is None:
+        found = _LAUNCH.get(_DEFAULT)
+        if found is not None:
+            return found
     key = library if library is not None else os.environ.get("ELASTIC_VMM_LIBRARY")
     found = _LAUNCH.get(key)
     if found is not None:
+        if library is None:
+            _LAUNCH[_DEFAULT], _BOUND[_DEFAULT] = found, _BOUND.get(key)
         return found
     lib = kernel_library(library)
     if not LAUNCHER_PATH.exists():
@@ -186,7 +201,16 @@ def launch_helper(library=None):
                            f"tree {tree}); rebuild it with `python elastic-kv-vmm_amd/build_native.py`")
     entries = {name: ct.cast(getattr(lib, name), ct.c_void_p).value for name in _LAUNCH_ENTRIES}
     found = _LAUNCH[key] = (module, entries)
+    _BOUND[key] = lib
+    if library is None:
+        _LAUNCH[_DEFAULT], _BOUND[_DEFAULT] = found, lib
     return found
+
+
+def launch_check(status, what):
+    """Raise for a failed call through the default launch helper, with the message of the library it called."""
+    if status:
+        check(_BOUND.get(_DEFAULT) or kernel_library(), status, what)
 
 
 def describe(tensor, name="tensor"):

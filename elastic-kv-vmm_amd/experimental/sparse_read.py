@@ -30,5 +30,4 @@ def gather_rows(raw, positions, request_ids, lengths, request_table, slot_offset
                                 request_table if indirect else None, slot_offsets if indirect else None, output,
                                 layout.request_bytes // layout.itemsize, layout.chunk_bytes // layout.itemsize,
                                 1 if indirect else 0)
-    if status:
-        _native.check(_native.kernel_library(), status, "gather_rows")
+    _native.launch_check(status, "gather_rows")
