@@ -844,19 +844,43 @@ __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupAr
     // tables only, so a staged id is the table value itself).
     extern __shared__ __align__(16) uint32_t lds[];
     __shared__ int32_t wave_totals[kThreads / 64];
-    const int64_t row = a.selected.fetch(blockIdx.x);
-    if (row < 0 || row >= a.batch) {
-        return;  // uniform over the workgroup
-    }
     const int64_t layer = blockIdx.y;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const TopkT* topk = static_cast<const TopkT*>(a.topk) + layer * a.topk_sl + row * a.topk_sb;
-    // First chunk's Top-K ids before the request's metadata, as above.
+    // The selection entry, and the request row, length and first chunk's
+    // Top-K ids of the row it names on the guess that the selection is the
+    // identity (entry j names batch row j), are requested together, so the
+    // table reads come after one memory level instead of two; a different
+    // entry re-reads them for its row. The batch is not empty (the host
+    // launches nothing for an empty one). A stray entry runs no chunk and
+    // writes nothing: there is no early return, which would let the
+    // compiler move the guessed loads past it and wait for them there.
+    const uint32_t zero = opaque_zero();
+    const int64_t guess = blockIdx.x < a.batch ? blockIdx.x : 0;
+    PendingIndex entry_read = issue_index(a.selected, blockIdx.x, zero);
+    PendingIndex req_read = issue_index(a.rows, guess, zero);
+    PendingIndex length_read = issue_index(a.lengths, guess, zero);
+    const TopkT* topk_rows = static_cast<const TopkT*>(a.topk) + layer * a.topk_sl;
     TopkT block[kIters];
-    load_blocks<false>(a, topk, wave * kWaveSpan + lane, block);
-    const int64_t req = a.rows.fetch(row);
-    const int64_t length = a.lengths.fetch(row);
+    load_blocks<false>(a, topk_rows + guess * a.topk_sb, wave * kWaveSpan + lane, block);
+    // One wait for all six index words: passed through one asm statement,
+    // they are read back (made uniform) only after every load is issued.
+    // Without it the compiler read each word back right after its load and
+    // waited for it there, six round trips in a row.
+    asm volatile("" : "+v"(entry_read.lo), "+v"(entry_read.hi), "+v"(req_read.lo), "+v"(req_read.hi),
+                 "+v"(length_read.lo), "+v"(length_read.hi));
+    const int64_t entry = index_value(a.selected, entry_read);
+    const bool live = entry >= 0 && entry < a.batch;  // uniform
+    const int64_t row = live ? entry : guess;
+    int64_t req = index_value(a.rows, req_read);
+    int64_t length = index_value(a.lengths, length_read);
+    const TopkT* topk = topk_rows + row * a.topk_sb;
+    if (row != guess) {  // uniform: the selection is not the identity here
+        req = a.rows.fetch(row);
+        length = a.lengths.fetch(row);
+        load_blocks<false>(a, topk, wave * kWaveSpan + lane, block);
+    }
+    const uint32_t width = live ? a.width : 0u;  // a stray entry runs no chunk
     const bool table_ok = req >= 0 && req < a.table_rows && a.table_cols > 0;  // uniform
     const int64_t bound = length < a.table_cols ? length : a.table_cols;
     const TableT* table =
@@ -868,7 +892,7 @@ __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupAr
     int32_t* misses = kCompact ? a.misses + layer * a.miss_sl + row * a.miss_sb : nullptr;
     int32_t running = 0;
 
-    for (uint32_t chunk = 0; chunk < a.width; chunk += kChunkLanes) {
+    for (uint32_t chunk = 0; chunk < width; chunk += kChunkLanes) {
         const uint32_t first = chunk + wave * kWaveSpan + lane;
         if (chunk != 0) {
             load_blocks<false>(a, topk, first, block);
@@ -911,7 +935,7 @@ __global__ __launch_bounds__(kThreads) void resolve_mapped_kernel(const LookupAr
         running = emit<kCompact>(a, out, misses, first, slot, running, wave_totals, lane, wave);
     }
     if constexpr (kCompact) {
-        if (threadIdx.x == 0) {
+        if (threadIdx.x == 0 && live) {
             a.counts[layer * a.count_sl + row * a.count_sb] = running;
         }
     }
@@ -1537,6 +1561,9 @@ int resolve_resident(const ekv_tensor* topk_p, const ekv_tensor* table_p, const 
     const int64_t count = selected.shape[0];
     if (count == 0 || width == 0 || layers == 0) {
         return 0;  // the reference returns without launching
+    }
+    if (batch == 0) {
+        return 0;  // every selection entry is stray: nothing is written (the kernels read batch row 0 first)
     }
     if (width >= (int64_t{1} << 31) - kChunkLanes) {
         throw std::invalid_argument("K * block_size must be below 2^31");
