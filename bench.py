@@ -1630,7 +1630,7 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported: this path has no "
-              "cross-GPU step here (each GPU runs its own shard independently)", file=sys.stderr)
+              "cross-GPU step (each GPU runs its own shard independently)", file=sys.stderr)
         return 2
     apply_profile_switch(os.environ, args.profile_ranges)
     import torch
